@@ -1,0 +1,1116 @@
+// Runtime behind include/akasha_hip.h: backend, tensors, graphs, the
+// per-shader launchers, ModelWeights and the batched InferenceSession.
+//
+// Reference interfaces mirrored here (paths relative to akasha-core's root):
+//   InferenceSession      src/nn/inference.rs:13-326
+//   DecodeScratch / Cache src/nn/inference_graphs.rs:13-196, 511-543
+//   ModelWeights          src/nn/weights.rs:32-47, 158-171
+//   AkashaError           src/lib.rs:10-37
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "akasha_hip.h"
+#include "kernels.h"
+
+using namespace akh;
+
+namespace {
+
+thread_local std::string g_err;
+
+akh_status fail(akh_status st, const std::string& msg) {
+  g_err = msg;
+  return st;
+}
+
+#define HIP_TRY(expr)                                                    \
+  do {                                                                   \
+    hipError_t e_ = (expr);                                              \
+    if (e_ != hipSuccess)                                                \
+      return fail(AKH_E_HIP, std::string(#expr) + ": " +                 \
+                                 hipGetErrorString(e_));                 \
+  } while (0)
+
+#define CHECK_ARG(cond, msg)                                   \
+  do {                                                         \
+    if (!(cond)) return fail(AKH_E_INVALID, std::string(msg)); \
+  } while (0)
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Backend
+// ---------------------------------------------------------------------------
+
+struct akh_backend {
+  int device = 0;
+  int num_cus = 256;
+  hipStream_t stream = nullptr;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  bool capturing = false;
+  // Split-K workspace of the per-shader matmul launchers.
+  float* ws = nullptr;
+  size_t ws_floats = 0;
+  unsigned* cnt = nullptr;
+  size_t cnt_n = 0;
+};
+
+struct akh_graph {
+  akh_backend* be = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+extern "C" const char* akh_last_error(void) { return g_err.c_str(); }
+extern "C" int akh_abi_version(void) { return AKH_ABI_VERSION; }
+
+extern "C" akh_status akh_backend_new(int device, akh_backend** out) {
+  CHECK_ARG(out, "akh_backend_new: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  CHECK_ARG(device >= 0 && device < n, "akh_backend_new: no such device");
+  HIP_TRY(hipSetDevice(device));
+  akh_backend* be = new akh_backend();
+  be->device = device;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess &&
+      prop.multiProcessorCount > 0)
+    be->num_cus = prop.multiProcessorCount;
+  hipError_t e = hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreate(&be->t0);
+  if (e == hipSuccess) e = hipEventCreate(&be->t1);
+  be->ws_floats = (size_t)4 << 20;  // 16 MiB
+  be->cnt_n = (size_t)1 << 16;
+  if (e == hipSuccess) e = hipMalloc(&be->ws, be->ws_floats * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&be->cnt, be->cnt_n * sizeof(unsigned));
+  if (e == hipSuccess) e = hipMemset(be->cnt, 0, be->cnt_n * sizeof(unsigned));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    akh_backend_free(be);
+    return fail(AKH_E_HIP, std::string("akh_backend_new: ") + hipGetErrorString(e));
+  }
+  *out = be;
+  return AKH_OK;
+}
+
+extern "C" void akh_backend_free(akh_backend* be) {
+  if (!be) return;
+  hipSetDevice(be->device);
+  if (be->stream) hipStreamSynchronize(be->stream);
+  if (be->ws) hipFree(be->ws);
+  if (be->cnt) hipFree(be->cnt);
+  if (be->t0) hipEventDestroy(be->t0);
+  if (be->t1) hipEventDestroy(be->t1);
+  if (be->stream) hipStreamDestroy(be->stream);
+  delete be;
+}
+
+extern "C" akh_status akh_synchronize(akh_backend* be) {
+  CHECK_ARG(be, "akh_synchronize: backend is NULL");
+  CHECK_ARG(!be->capturing, "akh_synchronize: graph capture in progress");
+  HIP_TRY(hipStreamSynchronize(be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_tensor_alloc(akh_backend* be, size_t bytes,
+                                       void** dev) {
+  CHECK_ARG(be && dev, "akh_tensor_alloc: NULL argument");
+  CHECK_ARG(!be->capturing, "akh_tensor_alloc: graph capture in progress");
+  *dev = nullptr;
+  void* p = nullptr;
+  HIP_TRY(hipMalloc(&p, bytes ? bytes : 4));
+  hipError_t e = hipMemsetAsync(p, 0, bytes ? bytes : 4, be->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
+  if (e != hipSuccess) {
+    hipFree(p);
+    return fail(AKH_E_HIP, std::string("akh_tensor_alloc: ") + hipGetErrorString(e));
+  }
+  *dev = p;
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_tensor_free(akh_backend* be, void* dev) {
+  CHECK_ARG(be, "akh_tensor_free: backend is NULL");
+  CHECK_ARG(!be->capturing, "akh_tensor_free: graph capture in progress");
+  if (!dev) return AKH_OK;
+  HIP_TRY(hipStreamSynchronize(be->stream));
+  HIP_TRY(hipFree(dev));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_tensor_upload(akh_backend* be, void* dev,
+                                        const void* host, size_t bytes) {
+  CHECK_ARG(be && (dev || !bytes) && (host || !bytes),
+            "akh_tensor_upload: NULL argument");
+  CHECK_ARG(!be->capturing, "akh_tensor_upload: graph capture in progress");
+  if (!bytes) return AKH_OK;
+  HIP_TRY(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, be->stream));
+  HIP_TRY(hipStreamSynchronize(be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_tensor_download(akh_backend* be, void* host,
+                                          const void* dev, size_t bytes) {
+  CHECK_ARG(be && (dev || !bytes) && (host || !bytes),
+            "akh_tensor_download: NULL argument");
+  CHECK_ARG(!be->capturing, "akh_tensor_download: graph capture in progress");
+  if (!bytes) return AKH_OK;
+  HIP_TRY(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, be->stream));
+  HIP_TRY(hipStreamSynchronize(be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_graph_begin(akh_backend* be) {
+  CHECK_ARG(be, "akh_graph_begin: backend is NULL");
+  CHECK_ARG(!be->capturing, "akh_graph_begin: capture already in progress");
+  HIP_TRY(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal));
+  be->capturing = true;
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_graph_end(akh_backend* be, akh_graph** out) {
+  CHECK_ARG(be && out, "akh_graph_end: NULL argument");
+  CHECK_ARG(be->capturing, "akh_graph_end: no capture in progress");
+  *out = nullptr;
+  be->capturing = false;
+  akh_graph* g = new akh_graph();
+  g->be = be;
+  hipError_t e = hipStreamEndCapture(be->stream, &g->graph);
+  if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    akh_graph_free(g);
+    return fail(AKH_E_HIP, std::string("akh_graph_end: ") + hipGetErrorString(e));
+  }
+  *out = g;
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_graph_execute(akh_graph* g) {
+  CHECK_ARG(g && g->exec, "akh_graph_execute: invalid graph");
+  CHECK_ARG(!g->be->capturing, "akh_graph_execute: capture in progress");
+  HIP_TRY(hipGraphLaunch(g->exec, g->be->stream));
+  return AKH_OK;
+}
+
+extern "C" void akh_graph_free(akh_graph* g) {
+  if (!g) return;
+  if (g->exec) hipGraphExecDestroy(g->exec);
+  if (g->graph) hipGraphDestroy(g->graph);
+  delete g;
+}
+
+extern "C" akh_status akh_timer_start(akh_backend* be) {
+  CHECK_ARG(be && !be->capturing, "akh_timer_start: invalid backend state");
+  HIP_TRY(hipEventRecord(be->t0, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_timer_stop(akh_backend* be, float* ms) {
+  CHECK_ARG(be && ms && !be->capturing, "akh_timer_stop: invalid argument");
+  HIP_TRY(hipEventRecord(be->t1, be->stream));
+  HIP_TRY(hipEventSynchronize(be->t1));
+  HIP_TRY(hipEventElapsedTime(ms, be->t0, be->t1));
+  return AKH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Launch planning
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// K chunks of the skinny GEMM: aim for ~2 blocks per CU over the N tiles,
+// chunk a multiple of 64 rows.  Returns the effective number of chunks.
+int skinny_ksplit(int N, int K, int num_cus) {
+  const int ntiles = (N + 31) / 32;
+  int ks = (2 * num_cus + ntiles / 2) / ntiles;
+  ks = std::max(1, std::min(ks, std::max(1, K / 64)));
+  const int kc = (((K + ks - 1) / ks) + 63) & ~63;
+  return (K + kc - 1) / kc;
+}
+
+size_t skinny_ws_floats(int N, int ks) {
+  const int ntiles = (N + 31) / 32;
+  return ks > 1 ? (size_t)ntiles * ks * 32 * 32 : 0;
+}
+
+bool supported_head_dim(uint32_t hd) {
+  return hd == 2 || hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64 ||
+         hd == 128;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Per-shader launchers
+// ---------------------------------------------------------------------------
+
+#define BE_CHECK(be) CHECK_ARG(be, "backend is NULL")
+
+extern "C" akh_status akh_embedding(akh_backend* be, const uint32_t* tokens,
+                                    const float* table, float* out,
+                                    akh_embedding_meta shape,
+                                    const akh_embedding_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(tokens && table && out && meta, "akh_embedding: NULL buffer");
+  HIP_TRY(shader_embedding(tokens, table, out, shape, meta, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_rmsnorm(akh_backend* be, const float* input,
+                                  const float* weight, float* output,
+                                  akh_norm_meta shape,
+                                  const akh_norm_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(input && weight && output && meta, "akh_rmsnorm: NULL buffer");
+  HIP_TRY(shader_rmsnorm(input, weight, output, shape, meta, be->stream));
+  return AKH_OK;
+}
+
+static akh_status matmul_common(akh_backend* be, const float* a,
+                                const float* b, float* c,
+                                akh_matmul_meta shape,
+                                const akh_matmul_meta* meta, int epi) {
+  BE_CHECK(be);
+  CHECK_ARG(a && b && c && meta, "akh_matmul: NULL buffer");
+  if (shape.m == 0 || shape.n == 0) return AKH_OK;
+  if (shape.m <= (uint32_t)kMaxBatch) {
+    SkinnyParams p{};
+    p.x = a;
+    p.w = b;
+    p.y = c;
+    p.M = shape.m;
+    p.N = shape.n;
+    p.K = shape.k;
+    p.meta = meta;
+    int ks = skinny_ksplit(shape.n, shape.k, be->num_cus);
+    while (ks > 1 && skinny_ws_floats(shape.n, ks) > be->ws_floats) --ks;
+    const int ntiles = (shape.n + 31) / 32;
+    CHECK_ARG(ks == 1 || (size_t)ntiles <= be->cnt_n, "akh_matmul: n too large");
+    p.ksplit = ks;
+    p.ws = be->ws;
+    p.cnt = be->cnt;
+    HIP_TRY(launch_skinny(p, epi, false, ntiles, be->stream));
+  } else {
+    GemmParams p{};
+    p.a = a;
+    p.b = b;
+    p.c = c;
+    p.M = shape.m;
+    p.N = shape.n;
+    p.K = shape.k;
+    p.meta = meta;
+    HIP_TRY(launch_gemm(p, epi, (shape.n + 127) / 128, (shape.m + 127) / 128,
+                        be->stream));
+  }
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_matmul(akh_backend* be, const float* a,
+                                 const float* b, float* c,
+                                 akh_matmul_meta shape,
+                                 const akh_matmul_meta* meta) {
+  return matmul_common(be, a, b, c, shape, meta, EPI_STORE);
+}
+
+extern "C" akh_status akh_matmul_add(akh_backend* be, const float* a,
+                                     const float* b, float* c,
+                                     akh_matmul_meta shape,
+                                     const akh_matmul_meta* meta) {
+  return matmul_common(be, a, b, c, shape, meta, EPI_ADD);
+}
+
+extern "C" akh_status akh_head_gather(akh_backend* be, const float* src,
+                                      float* dst, akh_head_move_meta shape,
+                                      const akh_head_move_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(src && dst && meta, "akh_head_gather: NULL buffer");
+  HIP_TRY(shader_head_gather(src, dst, shape, meta, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_rope(akh_backend* be, float* buf,
+                               akh_rope_meta shape,
+                               const akh_rope_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(buf && meta, "akh_rope: NULL buffer");
+  CHECK_ARG(shape.head_dim && shape.dim % shape.head_dim == 0 &&
+                shape.head_dim % 2 == 0,
+            "akh_rope: head_dim must be even and divide dim");
+  HIP_TRY(shader_rope(buf, shape.seq_len, shape.dim,
+                      reinterpret_cast<const uint32_t*>(meta), 0, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_rope_offset(akh_backend* be, float* buf,
+                                      akh_rope_offset_meta shape,
+                                      const akh_rope_offset_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(buf && meta, "akh_rope_offset: NULL buffer");
+  CHECK_ARG(shape.head_dim && shape.dim % shape.head_dim == 0 &&
+                shape.head_dim % 2 == 0,
+            "akh_rope_offset: head_dim must be even and divide dim");
+  HIP_TRY(shader_rope(buf, shape.seq_len, shape.dim,
+                      reinterpret_cast<const uint32_t*>(meta), 1, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_cache_write(akh_backend* be, const float* src,
+                                      float* cache,
+                                      akh_cache_write_meta shape,
+                                      const akh_cache_write_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(src && cache && meta, "akh_cache_write: NULL buffer");
+  HIP_TRY(shader_cache_write(src, cache, shape, meta, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_flash_attention(akh_backend* be, const float* q,
+                                          const float* k, const float* v,
+                                          float* out, float* l_cache,
+                                          akh_flash_attn_meta shape,
+                                          const akh_flash_attn_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(q && k && v && out && meta, "akh_flash_attention: NULL buffer");
+  // emit.rs:564-572: head_dim <= 128 and dim % head_dim == 0.
+  CHECK_ARG(shape.head_dim > 0 && shape.head_dim <= 128,
+            "flash_attention: head_dim must be <= 128");
+  CHECK_ARG(shape.dim % shape.head_dim == 0,
+            "flash_attention: dim must be divisible by head_dim");
+  CHECK_ARG(supported_head_dim(shape.head_dim),
+            "flash_attention: head_dim must be a power of two");
+  if (shape.seq_len == 0) return AKH_OK;
+  FlashParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = out;
+  p.lse = l_cache;
+  p.S = shape.seq_len;
+  p.d = shape.dim;
+  p.hd = shape.head_dim;
+  p.H = shape.dim / shape.head_dim;
+  p.scale = shape.scale;
+  p.meta = meta;
+  HIP_TRY(launch_flash(p, 1, shape.seq_len, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_attn_qk_cached(akh_backend* be, const float* q,
+                                         const float* k_cache, float* scores,
+                                         uint32_t num_heads,
+                                         uint32_t max_attn_len,
+                                         const akh_attn_cached_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(q && k_cache && scores && meta, "akh_attn_qk_cached: NULL buffer");
+  if (!num_heads || !max_attn_len) return AKH_OK;
+  HIP_TRY(shader_attn_qk_cached(q, k_cache, scores, num_heads, max_attn_len,
+                                meta, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_softmax_rect(akh_backend* be, float* scores,
+                                       akh_softmax_rect_meta shape,
+                                       const akh_softmax_rect_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(scores && meta, "akh_softmax_rect: NULL buffer");
+  HIP_TRY(shader_softmax_rect(scores, shape, meta, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_attn_av_cached(akh_backend* be, const float* scores,
+                                         const float* v_cache, float* out,
+                                         uint32_t dim,
+                                         const akh_attn_cached_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(scores && v_cache && out && meta, "akh_attn_av_cached: NULL buffer");
+  if (!dim) return AKH_OK;
+  HIP_TRY(shader_attn_av_cached(scores, v_cache, out, dim, meta, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_silu(akh_backend* be, float* buf, uint32_t len) {
+  BE_CHECK(be);
+  CHECK_ARG(buf || !len, "akh_silu: NULL buffer");
+  HIP_TRY(shader_silu(buf, len, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_argmax_rows(akh_backend* be, const float* logits,
+                                      uint32_t rows, uint32_t n,
+                                      uint32_t* out) {
+  BE_CHECK(be);
+  CHECK_ARG(logits && out, "akh_argmax_rows: NULL buffer");
+  CHECK_ARG(n > 0, "akh_argmax_rows: empty rows");
+  HIP_TRY(shader_argmax_rows(logits, rows, n, out, be->stream));
+  return AKH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Model weights
+// ---------------------------------------------------------------------------
+
+struct akh_model {
+  akh_backend* be = nullptr;
+  akh_model_config cfg{};
+  std::vector<float*> params;   // ModelWeights::params() order
+  std::vector<size_t> counts;
+
+  float* embedding() const { return params[0]; }
+  float* layer(uint32_t l, int which) const { return params[1 + 6 * l + which]; }
+  float* final_norm() const { return params[1 + 6 * cfg.num_layers]; }
+  float* lm_head() const { return params[2 + 6 * cfg.num_layers]; }
+};
+
+enum { W_NORM1 = 0, W_QKV = 1, W_OUT = 2, W_NORM2 = 3, W_UP = 4, W_DOWN = 5 };
+
+extern "C" void akh_model_free(akh_model* m) {
+  if (!m) return;
+  hipSetDevice(m->be->device);
+  hipStreamSynchronize(m->be->stream);
+  for (float* p : m->params)
+    if (p) hipFree(p);
+  delete m;
+}
+
+extern "C" akh_status akh_model_new(akh_backend* be,
+                                    const akh_model_config* cfg,
+                                    akh_model** out) {
+  CHECK_ARG(be && cfg && out, "akh_model_new: NULL argument");
+  *out = nullptr;
+  const akh_model_config c = *cfg;
+  // config.rs:15-17: at least one layer, dim divisible by heads.
+  CHECK_ARG(c.num_layers >= 1, "At least one layer is required!");
+  CHECK_ARG(c.num_heads > 0 && c.dim % c.num_heads == 0,
+            "dim must be divisible by num_heads");
+  CHECK_ARG(c.vocab_size > 0 && c.ffn_hidden > 0, "empty vocab or ffn");
+  akh_model* m = new akh_model();
+  m->be = be;
+  m->cfg = c;
+  const size_t d = c.dim, V = c.vocab_size, F = c.ffn_hidden;
+  m->counts.push_back(V * d);
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    m->counts.push_back(d);
+    m->counts.push_back(d * 3 * d);
+    m->counts.push_back(d * d);
+    m->counts.push_back(d);
+    m->counts.push_back(d * F);
+    m->counts.push_back(F * d);
+  }
+  m->counts.push_back(d);
+  m->counts.push_back(d * V);
+  for (size_t n : m->counts) {
+    void* p = nullptr;
+    akh_status st = akh_tensor_alloc(be, n * sizeof(float), &p);
+    if (st != AKH_OK) {
+      akh_model_free(m);
+      return st;
+    }
+    m->params.push_back(static_cast<float*>(p));
+  }
+  *out = m;
+  return AKH_OK;
+}
+
+extern "C" uint32_t akh_model_num_params(const akh_model* m) {
+  return m ? (uint32_t)m->params.size() : 0u;
+}
+
+extern "C" akh_status akh_model_param(akh_model* m, uint32_t index,
+                                      float** dev, size_t* count) {
+  CHECK_ARG(m && index < m->params.size(), "akh_model_param: bad index");
+  if (dev) *dev = m->params[index];
+  if (count) *count = m->counts[index];
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_model_upload_param(akh_model* m, uint32_t index,
+                                             const float* host, size_t count) {
+  CHECK_ARG(m && index < m->params.size(), "akh_model_upload_param: bad index");
+  CHECK_ARG(count == m->counts[index], "akh_model_upload_param: size mismatch");
+  return akh_tensor_upload(m->be, m->params[index], host, count * sizeof(float));
+}
+
+// ---------------------------------------------------------------------------
+// Batched session
+// ---------------------------------------------------------------------------
+
+struct akh_session {
+  akh_model* m = nullptr;
+  akh_backend* be = nullptr;
+  uint32_t max_ctx = 0, B = 0;
+  std::vector<uint32_t> cur_len;
+
+  // Cache: per layer, K then V, each [B, max_ctx, dim]; sequence b's slice
+  // is exactly the reference's per-session Cache tensor [max_ctx, dim].
+  float* kv = nullptr;
+  float2* rope = nullptr;  // [max_ctx, head_dim / 2] (cos, sin)
+
+  // Decode-step buffers (32 rows: the MFMA tile height).
+  float *x = nullptr, *q = nullptr, *attn = nullptr, *ffn = nullptr;
+  float *logits = nullptr, *ss1 = nullptr, *ss2 = nullptr;
+  uint2* amax = nullptr;
+  uint32_t* tok = nullptr;
+  int* pos = nullptr;
+  uint32_t* hist = nullptr;  // [B, max_ctx + 1] greedy tokens by position
+  float* ws = nullptr;
+  unsigned* cnt = nullptr;
+
+  // Launch plan.
+  int ks_qkv = 1, ks_out = 1, ks_up = 1, ks_down = 1, ks_lm = 1;
+  int attn_split = 1;
+
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+
+  // Prefill buffers, grown on demand to B * prompt_len rows.
+  size_t prows = 0;
+  float *px = nullptr, *pxn = nullptr, *pq = nullptr, *pattn = nullptr,
+        *pffn = nullptr;
+  uint32_t* ptok = nullptr;
+
+  size_t layer_stride() const { return (size_t)2 * B * max_ctx * m->cfg.dim; }
+  float* kcache(uint32_t l) { return kv + l * layer_stride(); }
+  float* vcache(uint32_t l) {
+    return kv + l * layer_stride() + (size_t)B * max_ctx * m->cfg.dim;
+  }
+  long seq_stride() const { return (long)max_ctx * m->cfg.dim; }
+};
+
+namespace {
+
+void free_prefill(akh_session* s) {
+  for (float* p : {s->px, s->pxn, s->pq, s->pattn, s->pffn})
+    if (p) hipFree(p);
+  if (s->ptok) hipFree(s->ptok);
+  s->px = s->pxn = s->pq = s->pattn = s->pffn = nullptr;
+  s->ptok = nullptr;
+  s->prows = 0;
+}
+
+akh_status ensure_prefill(akh_session* s, size_t rows) {
+  if (rows <= s->prows) return AKH_OK;
+  free_prefill(s);
+  const size_t d = s->m->cfg.dim, F = s->m->cfg.ffn_hidden;
+  HIP_TRY(hipMalloc(&s->px, rows * d * 4));
+  HIP_TRY(hipMalloc(&s->pxn, rows * d * 4));
+  HIP_TRY(hipMalloc(&s->pq, rows * d * 4));
+  HIP_TRY(hipMalloc(&s->pattn, rows * d * 4));
+  HIP_TRY(hipMalloc(&s->pffn, rows * F * 4));
+  HIP_TRY(hipMalloc(&s->ptok, rows * 4));
+  s->prows = rows;
+  return AKH_OK;
+}
+
+akh_status upload_positions(akh_session* s) {
+  std::vector<int> p(kMaxBatch, 0);
+  for (uint32_t b = 0; b < s->B; ++b) p[b] = (int)s->cur_len[b];
+  HIP_TRY(hipMemcpyAsync(s->pos, p.data(), kMaxBatch * sizeof(int),
+                         hipMemcpyHostToDevice, s->be->stream));
+  HIP_TRY(hipStreamSynchronize(s->be->stream));
+  return AKH_OK;
+}
+
+SkinnyParams skinny_base(akh_session* s) {
+  SkinnyParams p{};
+  p.M = (int)s->B;
+  p.ws = s->ws;
+  p.cnt = s->cnt;
+  p.eps = s->m->cfg.norm_eps;
+  p.ss_slots = (int)(s->m->cfg.dim / kSlotW);
+  return p;
+}
+
+// One decode-step kernel, addressed by `which` (see enqueue_decode).
+hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
+  const akh_model_config& c = s->m->cfg;
+  SkinnyParams p = skinny_base(s);
+  p.x = s->x;
+  p.w = s->m->layer(l, W_QKV);
+  p.N = 3 * c.dim;
+  p.K = c.dim;
+  p.ksplit = s->ks_qkv;
+  p.ss_in = s->ss1;
+  p.gain = s->m->layer(l, W_NORM1);
+  p.q_out = s->q;
+  p.kcache = s->kcache(l);
+  p.vcache = s->vcache(l);
+  p.seq_stride = s->seq_stride();
+  p.pos = s->pos;
+  p.rope = s->rope;
+  p.dim = c.dim;
+  p.head_dim = c.dim / c.num_heads;
+  return launch_skinny(p, EPI_QKV, true, (p.N + 31) / 32, s->be->stream);
+}
+
+hipError_t enqueue_attn(akh_session* s, uint32_t l) {
+  const akh_model_config& c = s->m->cfg;
+  DecodeAttnParams p{};
+  p.q = s->q;
+  p.kc = s->kcache(l);
+  p.vc = s->vcache(l);
+  p.out = s->attn;
+  p.pos = s->pos;
+  p.ws = s->ws;
+  p.cnt = s->cnt;
+  p.seq_stride = s->seq_stride();
+  p.B = (int)s->B;
+  p.H = (int)c.num_heads;
+  p.d = (int)c.dim;
+  p.nsplit = s->attn_split;
+  const uint32_t hd = c.dim / c.num_heads;
+  p.scale = 1.0f / sqrtf((float)hd);
+  return launch_decode_attn(p, (int)hd, s->be->stream);
+}
+
+hipError_t enqueue_out(akh_session* s, uint32_t l) {
+  const akh_model_config& c = s->m->cfg;
+  SkinnyParams p = skinny_base(s);
+  p.x = s->attn;
+  p.w = s->m->layer(l, W_OUT);
+  p.y = s->x;
+  p.N = c.dim;
+  p.K = c.dim;
+  p.ksplit = s->ks_out;
+  p.ss_out = s->ss2;
+  return launch_skinny(p, EPI_ADD, false, (p.N + 31) / 32, s->be->stream);
+}
+
+hipError_t enqueue_up(akh_session* s, uint32_t l) {
+  const akh_model_config& c = s->m->cfg;
+  SkinnyParams p = skinny_base(s);
+  p.x = s->x;
+  p.w = s->m->layer(l, W_UP);
+  p.y = s->ffn;
+  p.N = c.ffn_hidden;
+  p.K = c.dim;
+  p.ksplit = s->ks_up;
+  p.ss_in = s->ss2;
+  p.gain = s->m->layer(l, W_NORM2);
+  return launch_skinny(p, EPI_SILU, true, (p.N + 31) / 32, s->be->stream);
+}
+
+hipError_t enqueue_down(akh_session* s, uint32_t l) {
+  const akh_model_config& c = s->m->cfg;
+  SkinnyParams p = skinny_base(s);
+  p.x = s->ffn;
+  p.w = s->m->layer(l, W_DOWN);
+  p.y = s->x;
+  p.N = c.dim;
+  p.K = c.ffn_hidden;
+  p.ksplit = s->ks_down;
+  p.ss_out = s->ss1;
+  return launch_skinny(p, EPI_ADD, false, (p.N + 31) / 32, s->be->stream);
+}
+
+hipError_t enqueue_lm_head(akh_session* s) {
+  const akh_model_config& c = s->m->cfg;
+  SkinnyParams p = skinny_base(s);
+  p.x = s->x;
+  p.w = s->m->lm_head();
+  p.y = s->logits;
+  p.N = c.vocab_size;
+  p.K = c.dim;
+  p.ksplit = s->ks_lm;
+  p.ss_in = s->ss1;
+  p.gain = s->m->final_norm();
+  p.amax = s->amax;
+  return launch_skinny(p, EPI_LOGITS, true, (p.N + 31) / 32, s->be->stream);
+}
+
+// The decode step of build_decode_layer (inference_graphs.rs:339-509) for
+// all sequences: 5 kernels per layer.  RMSNorm runs inside the consumer
+// GEMM (statistics carried as slot partials), RoPE + cache append inside
+// the QKV GEMM epilogue, SiLU inside ffn_up's, the residual adds inside
+// out_proj's and ffn_down's; lm_head emits argmax partials and the last
+// kernel picks the greedy token and advances every position.
+hipError_t enqueue_decode(akh_session* s) {
+  const akh_model_config& c = s->m->cfg;
+  hipStream_t st = s->be->stream;
+  hipError_t e = launch_gather_rows(s->m->embedding(), s->tok, c.vocab_size,
+                                    nullptr, 0, 0, s->x, (int)s->B,
+                                    (int)c.dim, s->ss1, st);
+  for (uint32_t l = 0; l < c.num_layers && e == hipSuccess; ++l) {
+    e = enqueue_qkv(s, l);
+    if (e == hipSuccess) e = enqueue_attn(s, l);
+    if (e == hipSuccess) e = enqueue_out(s, l);
+    if (e == hipSuccess) e = enqueue_up(s, l);
+    if (e == hipSuccess) e = enqueue_down(s, l);
+  }
+  if (e == hipSuccess) e = enqueue_lm_head(s);
+  if (e == hipSuccess)
+    e = launch_argmax_final(s->amax, (int)((c.vocab_size + 31) / 32),
+                            (int)s->B, s->tok, s->pos, s->hist,
+                            (int)s->max_ctx + 1, st);
+  return e;
+}
+
+akh_status ensure_decode_graph(akh_session* s) {
+  if (s->gexec) return AKH_OK;
+  hipStream_t st = s->be->stream;
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  hipError_t e = enqueue_decode(s);
+  hipGraph_t g = nullptr;
+  hipError_t e2 = hipStreamEndCapture(st, &g);
+  if (e != hipSuccess || e2 != hipSuccess) {
+    if (g) hipGraphDestroy(g);
+    return fail(AKH_E_HIP, std::string("decode graph capture: ") +
+                               hipGetErrorString(e != hipSuccess ? e : e2));
+  }
+  hipGraphExec_t ex = nullptr;
+  e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    hipGraphDestroy(g);
+    return fail(AKH_E_HIP, std::string("decode graph instantiate: ") +
+                               hipGetErrorString(e));
+  }
+  s->graph = g;
+  s->gexec = ex;
+  return AKH_OK;
+}
+
+akh_status download_outputs(akh_session* s, float* logits, uint32_t* next) {
+  const akh_model_config& c = s->m->cfg;
+  hipStream_t st = s->be->stream;
+  if (logits)
+    HIP_TRY(hipMemcpyAsync(logits, s->logits,
+                           (size_t)s->B * c.vocab_size * sizeof(float),
+                           hipMemcpyDeviceToHost, st));
+  if (next)
+    HIP_TRY(hipMemcpyAsync(next, s->tok, (size_t)s->B * sizeof(uint32_t),
+                           hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return AKH_OK;
+}
+
+}  // namespace
+
+extern "C" void akh_session_free(akh_session* s) {
+  if (!s) return;
+  hipSetDevice(s->be->device);
+  hipStreamSynchronize(s->be->stream);
+  if (s->gexec) hipGraphExecDestroy(s->gexec);
+  if (s->graph) hipGraphDestroy(s->graph);
+  free_prefill(s);
+  void* bufs[] = {s->kv,   s->rope, s->x,   s->q,    s->attn, s->ffn,
+                  s->logits, s->ss1, s->ss2, s->amax, s->tok,  s->pos,
+                  s->hist, s->ws,   s->cnt};
+  for (void* p : bufs)
+    if (p) hipFree(p);
+  delete s;
+}
+
+extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
+                                      uint32_t batch, akh_session** out) {
+  CHECK_ARG(m && out, "akh_session_new: NULL argument");
+  *out = nullptr;
+  const akh_model_config& c = m->cfg;
+  CHECK_ARG(batch >= 1 && batch <= (uint32_t)kMaxBatch,
+            "akh_session_new: batch must be in 1..32");
+  CHECK_ARG(max_context_len >= 1, "akh_session_new: max_context_len is 0");
+  const uint32_t hd = c.dim / c.num_heads;
+  CHECK_ARG(supported_head_dim(hd) && hd >= 4,
+            "akh_session_new: head_dim must be a power of two in 4..128");
+  CHECK_ARG(c.dim % kSlotW == 0, "akh_session_new: dim must be a multiple of 32");
+  CHECK_ARG(c.ffn_hidden % 4 == 0, "akh_session_new: ffn_hidden % 4 != 0");
+
+  akh_session* s = new akh_session();
+  s->m = m;
+  s->be = m->be;
+  s->max_ctx = max_context_len;
+  s->B = batch;
+  s->cur_len.assign(batch, 0);
+  const int cus = s->be->num_cus;
+  s->ks_qkv = skinny_ksplit(3 * c.dim, c.dim, cus);
+  s->ks_out = skinny_ksplit(c.dim, c.dim, cus);
+  s->ks_up = skinny_ksplit(c.ffn_hidden, c.dim, cus);
+  s->ks_down = skinny_ksplit(c.dim, c.ffn_hidden, cus);
+  s->ks_lm = skinny_ksplit(c.vocab_size, c.dim, cus);
+  // Attention: ~6 blocks per CU, chunks of at most 1024 rows.
+  {
+    const int bh = (int)(batch * c.num_heads);
+    int ns = (6 * cus + bh - 1) / bh;
+    ns = std::min(ns, std::max(1, (int)(max_context_len / 32)));
+    ns = std::max(ns, (int)((max_context_len + 1023) / 1024));
+    s->attn_split = std::max(1, ns);
+  }
+  size_t ws = 0;
+  ws = std::max(ws, skinny_ws_floats(3 * c.dim, s->ks_qkv));
+  ws = std::max(ws, skinny_ws_floats(c.dim, s->ks_out));
+  ws = std::max(ws, skinny_ws_floats(c.ffn_hidden, s->ks_up));
+  ws = std::max(ws, skinny_ws_floats(c.dim, s->ks_down));
+  ws = std::max(ws, skinny_ws_floats(c.vocab_size, s->ks_lm));
+  ws = std::max(ws, (size_t)batch * c.num_heads * s->attn_split * (hd + 4));
+  size_t ncnt = std::max<size_t>((c.vocab_size + 31) / 32,
+                                 (size_t)batch * c.num_heads);
+  ncnt = std::max<size_t>(ncnt, (3 * c.dim + 31) / 32);
+  ncnt = std::max<size_t>(ncnt, (c.ffn_hidden + 31) / 32);
+
+  const size_t d = c.dim, V = c.vocab_size, F = c.ffn_hidden, R = kMaxBatch;
+  const size_t ntl = (V + 31) / 32;
+  hipError_t e = hipSetDevice(s->be->device);
+  auto alloc = [&](void** p, size_t bytes) {
+    if (e == hipSuccess) e = hipMalloc(p, bytes);
+    if (e == hipSuccess) e = hipMemset(*p, 0, bytes);
+  };
+  alloc((void**)&s->kv, (size_t)c.num_layers * 2 * batch * max_context_len * d * 4);
+  alloc((void**)&s->rope, (size_t)max_context_len * (hd / 2) * sizeof(float2));
+  alloc((void**)&s->x, R * d * 4);
+  alloc((void**)&s->q, R * d * 4);
+  alloc((void**)&s->attn, R * d * 4);
+  alloc((void**)&s->ffn, R * F * 4);
+  alloc((void**)&s->logits, R * V * 4);
+  alloc((void**)&s->ss1, R * (d / kSlotW) * 4);
+  alloc((void**)&s->ss2, R * (d / kSlotW) * 4);
+  alloc((void**)&s->amax, R * ntl * sizeof(uint2));
+  alloc((void**)&s->tok, R * 4);
+  alloc((void**)&s->pos, R * 4);
+  alloc((void**)&s->hist, (size_t)batch * (max_context_len + 1) * 4);
+  alloc((void**)&s->ws, std::max<size_t>(ws, 1) * 4);
+  alloc((void**)&s->cnt, ncnt * 4);
+  if (e == hipSuccess) {
+    // RoPE table in f32 exactly as src/shaders/cpu.rs:98-100 forms it:
+    // freq = 1 / 10000^(2i / head_dim), angle = pos * freq, then sin/cos.
+    std::vector<float2> tab((size_t)max_context_len * (hd / 2));
+    for (uint32_t t = 0; t < max_context_len; ++t)
+      for (uint32_t i = 0; i < hd / 2; ++i) {
+        const float freq = 1.0f / powf(10000.0f, (float)(2 * i) / (float)hd);
+        const float angle = (float)t * freq;
+        tab[(size_t)t * (hd / 2) + i] = make_float2(cosf(angle), sinf(angle));
+      }
+    e = hipMemcpy(s->rope, tab.data(), tab.size() * sizeof(float2),
+                  hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    akh_session_free(s);
+    return fail(AKH_E_HIP, std::string("akh_session_new: ") + hipGetErrorString(e));
+  }
+  *out = s;
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_session_reset(akh_session* s) {
+  CHECK_ARG(s, "akh_session_reset: NULL session");
+  std::fill(s->cur_len.begin(), s->cur_len.end(), 0u);
+  return upload_positions(s);
+}
+
+extern "C" akh_status akh_session_cur_len(const akh_session* s, uint32_t* out) {
+  CHECK_ARG(s && out, "akh_session_cur_len: NULL argument");
+  std::copy(s->cur_len.begin(), s->cur_len.end(), out);
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_session_truncate(akh_session* s, uint32_t len) {
+  CHECK_ARG(s, "akh_session_truncate: NULL session");
+  for (uint32_t b = 0; b < s->B; ++b)
+    CHECK_ARG(len <= s->cur_len[b], "akh_session_truncate: len > cur_len");
+  std::fill(s->cur_len.begin(), s->cur_len.end(), len);
+  return upload_positions(s);
+}
+
+// InferenceSession::prefill (inference.rs:61-176) for all sequences, with
+// build_prefill_layer's node order (inference_graphs.rs:198-337): 7 kernels
+// per layer (RMSNorm, QKV GEMM + RoPE + cache append, flash attention,
+// out_proj + residual, RMSNorm, ffn_up + SiLU, ffn_down + residual).
+extern "C" akh_status akh_session_prefill(akh_session* s,
+                                          const uint32_t* tokens,
+                                          uint32_t prompt_len, float* logits,
+                                          uint32_t* next) {
+  CHECK_ARG(s && (tokens || !prompt_len), "akh_session_prefill: NULL argument");
+  if (prompt_len == 0) return fail(AKH_E_EMPTY_PROMPT, "prompt is empty");
+  if (prompt_len > s->max_ctx)
+    return fail(AKH_E_PROMPT_TOO_LONG,
+                "prompt is " + std::to_string(prompt_len) +
+                    " tokens, context window is " + std::to_string(s->max_ctx));
+  for (uint32_t b = 0; b < s->B; ++b)
+    if (s->cur_len[b] != 0)
+      return fail(AKH_E_CACHE_NOT_EMPTY,
+                  "prefill needs an empty cache, this one holds " +
+                      std::to_string(s->cur_len[b]) + " tokens");
+  const akh_model_config& c = s->m->cfg;
+  const uint32_t S = prompt_len, d = c.dim, hd = d / c.num_heads;
+  const size_t rows = (size_t)s->B * S;
+  akh_status st0 = ensure_prefill(s, rows);
+  if (st0 != AKH_OK) return st0;
+  hipStream_t st = s->be->stream;
+  HIP_TRY(hipMemcpyAsync(s->ptok, tokens, rows * 4, hipMemcpyHostToDevice, st));
+
+  HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
+                                (int)d, c.vocab_size, st));
+  const int gm = (int)((rows + 127) / 128);
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    HIP_TRY(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM1), s->pxn,
+                                (int)rows, (int)d, c.norm_eps, st));
+    GemmParams g{};
+    g.a = s->pxn;
+    g.b = s->m->layer(l, W_QKV);
+    g.M = (int)rows;
+    g.N = 3 * d;
+    g.K = d;
+    g.q_out = s->pq;
+    g.kcache = s->kcache(l);
+    g.vcache = s->vcache(l);
+    g.seq_stride = s->seq_stride();
+    g.S = (int)S;
+    g.rope = s->rope;
+    g.dim = d;
+    g.head_dim = hd;
+    HIP_TRY(launch_gemm(g, EPI_QKV, (g.N + 127) / 128, gm, st));
+
+    FlashParams f{};
+    f.q = s->pq;
+    f.k = s->kcache(l);
+    f.v = s->vcache(l);
+    f.o = s->pattn;
+    f.q_bs = (long)S * d;
+    f.kv_bs = s->seq_stride();
+    f.o_bs = (long)S * d;
+    f.S = (int)S;
+    f.d = (int)d;
+    f.hd = (int)hd;
+    f.H = (int)c.num_heads;
+    f.scale = 1.0f / sqrtf((float)hd);
+    HIP_TRY(launch_flash(f, (int)s->B, (int)S, st));
+
+    GemmParams o{};
+    o.a = s->pattn;
+    o.b = s->m->layer(l, W_OUT);
+    o.c = s->px;
+    o.M = (int)rows;
+    o.N = d;
+    o.K = d;
+    HIP_TRY(launch_gemm(o, EPI_ADD, (d + 127) / 128, gm, st));
+
+    HIP_TRY(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM2), s->pxn,
+                                (int)rows, (int)d, c.norm_eps, st));
+    GemmParams u{};
+    u.a = s->pxn;
+    u.b = s->m->layer(l, W_UP);
+    u.c = s->pffn;
+    u.M = (int)rows;
+    u.N = c.ffn_hidden;
+    u.K = d;
+    HIP_TRY(launch_gemm(u, EPI_SILU, (u.N + 127) / 128, gm, st));
+
+    GemmParams w{};
+    w.a = s->pffn;
+    w.b = s->m->layer(l, W_DOWN);
+    w.c = s->px;
+    w.M = (int)rows;
+    w.N = d;
+    w.K = c.ffn_hidden;
+    HIP_TRY(launch_gemm(w, EPI_ADD, (d + 127) / 128, gm, st));
+  }
+  // Last row of every sequence -> final RMSNorm (in the lm_head prologue)
+  // -> lm_head -> greedy token (inference.rs:120-168).
+  HIP_TRY(launch_gather_rows(nullptr, nullptr, 0, s->px, (long)S - 1, (long)S,
+                             s->x, (int)s->B, (int)d, s->ss1, st));
+  HIP_TRY(enqueue_lm_head(s));
+  HIP_TRY(launch_argmax_final(s->amax, (int)((c.vocab_size + 31) / 32),
+                              (int)s->B, s->tok, nullptr, nullptr, 0, st));
+  std::fill(s->cur_len.begin(), s->cur_len.end(), S);
+  akh_status ps = upload_positions(s);
+  if (ps != AKH_OK) return ps;
+  return download_outputs(s, logits, next);
+}
+
+extern "C" akh_status akh_session_decode_step(akh_session* s,
+                                              const uint32_t* tokens,
+                                              float* logits, uint32_t* next) {
+  CHECK_ARG(s, "akh_session_decode_step: NULL session");
+  for (uint32_t b = 0; b < s->B; ++b)
+    if (s->cur_len[b] >= s->max_ctx)
+      return fail(AKH_E_CONTEXT_FULL, "context window is full (" +
+                                          std::to_string(s->max_ctx) +
+                                          " tokens)");
+  akh_status st0 = ensure_decode_graph(s);
+  if (st0 != AKH_OK) return st0;
+  hipStream_t st = s->be->stream;
+  if (tokens)
+    HIP_TRY(hipMemcpyAsync(s->tok, tokens, (size_t)s->B * 4,
+                           hipMemcpyHostToDevice, st));
+  HIP_TRY(hipGraphLaunch(s->gexec, st));
+  for (uint32_t b = 0; b < s->B; ++b) s->cur_len[b] += 1;
+  return download_outputs(s, logits, next);
+}
+
+extern "C" akh_status akh_session_decode_greedy(akh_session* s,
+                                                uint32_t steps,
+                                                uint32_t* out_tokens) {
+  CHECK_ARG(s, "akh_session_decode_greedy: NULL session");
+  for (uint32_t b = 0; b < s->B; ++b)
+    if (s->cur_len[b] + steps > s->max_ctx)
+      return fail(AKH_E_CONTEXT_FULL, "context window is full (" +
+                                          std::to_string(s->max_ctx) +
+                                          " tokens)");
+  if (steps == 0) return AKH_OK;
+  akh_status st0 = ensure_decode_graph(s);
+  if (st0 != AKH_OK) return st0;
+  hipStream_t st = s->be->stream;
+  std::vector<uint32_t> start(s->cur_len);
+  for (uint32_t i = 0; i < steps; ++i) HIP_TRY(hipGraphLaunch(s->gexec, st));
+  for (uint32_t b = 0; b < s->B; ++b) s->cur_len[b] += steps;
+  if (out_tokens) {
+    std::vector<uint32_t> h((size_t)s->B * (s->max_ctx + 1));
+    HIP_TRY(hipMemcpyAsync(h.data(), s->hist, h.size() * 4,
+                           hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    for (uint32_t i = 0; i < steps; ++i)
+      for (uint32_t b = 0; b < s->B; ++b)
+        out_tokens[(size_t)i * s->B + b] =
+            h[(size_t)b * (s->max_ctx + 1) + start[b] + 1 + i];
+  }
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_session_download_cache(akh_session* s,
+                                                 uint32_t layer, uint32_t seq,
+                                                 int which, float* host) {
+  CHECK_ARG(s && host && layer < s->m->cfg.num_layers && seq < s->B &&
+                (which == 0 || which == 1),
+            "akh_session_download_cache: bad argument");
+  const float* src = (which == 0 ? s->kcache(layer) : s->vcache(layer)) +
+                     (size_t)seq * s->seq_stride();
+  return akh_tensor_download(s->be, host, src,
+                             (size_t)s->seq_stride() * sizeof(float));
+}
+
+extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,
+                                                     int kernel,
+                                                     uint32_t reps,
+                                                     float* avg_ms) {
+  CHECK_ARG(s && avg_ms && reps > 0, "akh_session_time_decode_kernel: bad argument");
+  CHECK_ARG(kernel >= 0 && kernel <= 5, "akh_session_time_decode_kernel: bad kernel");
+  for (uint32_t b = 0; b < s->B; ++b)
+    CHECK_ARG(s->cur_len[b] >= 1 && s->cur_len[b] < s->max_ctx,
+              "akh_session_time_decode_kernel: needs 1 <= cur_len < max_ctx");
+  akh_backend* be = s->be;
+  auto one = [&]() -> hipError_t {
+    switch (kernel) {
+      case 0: return enqueue_attn(s, 0);
+      case 1: return enqueue_qkv(s, 0);
+      case 2: return enqueue_out(s, 0);
+      case 3: return enqueue_up(s, 0);
+      case 4: return enqueue_down(s, 0);
+      default: return enqueue_lm_head(s);
+    }
+  };
+  HIP_TRY(one());  // warm
+  HIP_TRY(hipEventRecord(be->t0, be->stream));
+  for (uint32_t i = 0; i < reps; ++i) HIP_TRY(one());
+  HIP_TRY(hipEventRecord(be->t1, be->stream));
+  HIP_TRY(hipEventSynchronize(be->t1));
+  float ms = 0.f;
+  HIP_TRY(hipEventElapsedTime(&ms, be->t0, be->t1));
+  *avg_ms = ms / (float)reps;
+  return AKH_OK;
+}

@@ -1,0 +1,249 @@
+/*
+ * akasha_hip.h -- C ABI of libakasha_hip.so, the MI355X (gfx950) backend for
+ * akasha-core's inference path.
+ *
+ * This is the surface a Rust `hip` feature of akasha-core / wilupgu binds
+ * through a thin FFI crate (see INTEGRATION.md for the binding).  It has
+ * three layers, each replacing a reference interface:
+ *
+ *   1. Backend, tensors and graphs: wilupgu's Backend / Tensor / ComputeGraph
+ *      (reference call sites: src/nn/inference.rs:83,170,189,257,261;
+ *      src/nn/ops/meta.rs:4-16; src/main.rs:366).
+ *   2. One launcher per reference Shader or matmul builtin on the inference
+ *      path, with buffers in binding-slot order and the meta structs of
+ *      src/nn/ops/meta.rs byte for byte.  Each launcher mirrors an `*_with`
+ *      emitter of src/nn/ops/emit.rs: `shape` is the build-time meta (it
+ *      sizes the launch, as the emitter's grid does) and `meta` is the device
+ *      meta tensor the kernel reads when it executes, so a captured graph
+ *      follows metas rewritten between executions.
+ *   3. A batched InferenceSession (src/nn/inference.rs:13-326): B independent
+ *      sequences, each with its own KV cache, sharing one read of the
+ *      weights per step.
+ *
+ * Conventions: all pointers named dev/device are device pointers from
+ * akh_tensor_alloc; everything else is host memory.  Calls on one backend
+ * are not re-entrant (the reference's devices are single-threaded too:
+ * README.md:55-57).  No exception crosses this ABI: every entry returns an
+ * akh_status, and akh_last_error() describes the last failure.
+ */
+#ifndef AKASHA_HIP_H
+#define AKASHA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AKH_ABI_VERSION 1
+
+/* Status codes.  1..5 are AkashaError's variants (src/lib.rs:10-17). */
+typedef enum {
+  AKH_OK = 0,
+  AKH_E_EMPTY_PROMPT = 1,      /* AkashaError::EmptyPrompt */
+  AKH_E_PROMPT_TOO_LONG = 2,   /* AkashaError::PromptTooLong { len, max } */
+  AKH_E_CONTEXT_FULL = 3,      /* AkashaError::ContextFull { max } */
+  AKH_E_NO_CACHE = 4,          /* AkashaError::NoCache */
+  AKH_E_CACHE_NOT_EMPTY = 5,   /* AkashaError::CacheNotEmpty { cur_len } */
+  AKH_E_INVALID = 6,           /* a precondition the reference assert!s */
+  AKH_E_HIP = 7                /* HIP runtime error */
+} akh_status;
+
+/* ---- metas: src/nn/ops/meta.rs, #[repr(C)] u32/f32 --------------------- */
+typedef struct { uint32_t m, n, k; } akh_matmul_meta;                 /* :19-25 */
+typedef struct { uint32_t seq_len, size; float eps; } akh_norm_meta;  /* :29-35 */
+typedef struct {
+  uint32_t seq_len, full_dim, head_dim, head_offset;
+} akh_head_move_meta;                                                  /* :40-47 */
+typedef struct { uint32_t attn_len, dim, head_dim; } akh_attn_cached_meta; /* :62-68 */
+typedef struct { uint32_t num_rows, width; float scale; } akh_softmax_rect_meta; /* :72-78 */
+typedef struct { uint32_t seq_len, dim, head_dim, row_offset; } akh_rope_meta; /* :82-89 */
+typedef struct { uint32_t seq_len, dim, head_dim, pos; } akh_rope_offset_meta; /* :93-100 */
+typedef struct { uint32_t row_count, width, dst_row_offset; } akh_cache_write_meta; /* :104-110 */
+typedef struct { uint32_t vocab_size, dim, seq_len; } akh_embedding_meta; /* :114-120 */
+typedef struct {
+  uint32_t seq_len, dim, head_dim;
+  float scale;
+  uint32_t row_offset;
+} akh_flash_attn_meta;                                                 /* :156-164 */
+
+/* ---- 1. backend, tensors, graphs ----------------------------------------- */
+
+typedef struct akh_backend akh_backend;
+typedef struct akh_graph akh_graph;
+
+/* HipBackend::new(device), the counterpart of CudaBackend::new(0)
+ * (src/main.rs:366).  Creates one stream at default priority. */
+akh_status akh_backend_new(int device, akh_backend** out);
+void akh_backend_free(akh_backend* be);
+/* Backend::synchronize (src/nn/ops/emit.rs:1052). */
+akh_status akh_synchronize(akh_backend* be);
+/* Text of the last failure on this thread ("" if none). */
+const char* akh_last_error(void);
+int akh_abi_version(void);
+
+/* Tensor::init_from_cpu / copy_from_cpu / to_cpu (inference.rs:83,189,261).
+ * akh_tensor_alloc returns zeroed device memory. */
+akh_status akh_tensor_alloc(akh_backend* be, size_t bytes, void** dev);
+akh_status akh_tensor_free(akh_backend* be, void* dev);
+akh_status akh_tensor_upload(akh_backend* be, void* dev, const void* host,
+                             size_t bytes);
+akh_status akh_tensor_download(akh_backend* be, void* host, const void* dev,
+                               size_t bytes);
+
+/* ComputeGraph::new / add_node / execute (src/nn/ops/emit.rs:36-45,
+ * inference.rs:170,257).  Launchers called between begin and end are
+ * recorded into a hipGraph instead of running; akh_graph_execute replays it
+ * on the backend's stream.  Metas are read from device memory at replay. */
+akh_status akh_graph_begin(akh_backend* be);
+akh_status akh_graph_end(akh_backend* be, akh_graph** out);
+akh_status akh_graph_execute(akh_graph* g);
+void akh_graph_free(akh_graph* g);
+
+/* ---- 2. launchers (one per Shader / builtin; src/shaders/mod.rs) --------- */
+
+/* EMBEDDING, ops::embedding_with (emit.rs:228-244; cpu.rs:25-41). */
+akh_status akh_embedding(akh_backend* be, const uint32_t* tokens,
+                         const float* table, float* out,
+                         akh_embedding_meta shape,
+                         const akh_embedding_meta* meta);
+/* RMSNORM, ops::rmsnorm_with (emit.rs:151-168; cpu.rs:205-222). */
+akh_status akh_rmsnorm(akh_backend* be, const float* input,
+                       const float* weight, float* output,
+                       akh_norm_meta shape, const akh_norm_meta* meta);
+/* MATMUL / GEMV builtins, ops::matmul_with (emit.rs:19-45):
+ * C[m,n] = A[m,k] B[k,n], row-major, B stored [in, out].  Output binding:
+ * every element of C[0..m, 0..n] is written. */
+akh_status akh_matmul(akh_backend* be, const float* a, const float* b,
+                      float* c, akh_matmul_meta shape,
+                      const akh_matmul_meta* meta);
+/* MATMUL_ADD / GEMV_ADD builtins, ops::matmul_add_with (emit.rs:91-114):
+ * C += A B (Accumulate binding). */
+akh_status akh_matmul_add(akh_backend* be, const float* a, const float* b,
+                          float* c, akh_matmul_meta shape,
+                          const akh_matmul_meta* meta);
+/* HEAD_GATHER, ops::head_gather_with (emit.rs:405-413; cpu.rs:238-255). */
+akh_status akh_head_gather(akh_backend* be, const float* src, float* dst,
+                           akh_head_move_meta shape,
+                           const akh_head_move_meta* meta);
+/* ROPE, ops::rope (emit.rs:306-313; cpu.rs:84-109): in place, position =
+ * row index. */
+akh_status akh_rope(akh_backend* be, float* buf, akh_rope_meta shape,
+                    const akh_rope_meta* meta);
+/* ROPE_OFFSET, ops::rope_offset_with (emit.rs:325-342; cpu.rs:111-142). */
+akh_status akh_rope_offset(akh_backend* be, float* buf,
+                           akh_rope_offset_meta shape,
+                           const akh_rope_offset_meta* meta);
+/* CACHE_WRITE, ops::cache_write_with (emit.rs:649-666; cpu.rs:224-236). */
+akh_status akh_cache_write(akh_backend* be, const float* src, float* cache,
+                           akh_cache_write_meta shape,
+                           const akh_cache_write_meta* meta);
+/* FLASH_ATTENTION, ops::flash_attention (emit.rs:556-597): causal
+ * softmax(scale Q K^T) V for one sequence of rows [row_offset,
+ * row_offset+seq_len) of [*, dim] buffers; l_cache[row*H + h] receives
+ * max + ln(sum).  head_dim <= 128 (emit.rs:564-567). */
+akh_status akh_flash_attention(akh_backend* be, const float* q,
+                               const float* k, const float* v, float* out,
+                               float* l_cache, akh_flash_attn_meta shape,
+                               const akh_flash_attn_meta* meta);
+/* ATTN_QK_CACHED, ops::attn_qk_cached_with (emit.rs:485-504). */
+akh_status akh_attn_qk_cached(akh_backend* be, const float* q,
+                              const float* k_cache, float* scores,
+                              uint32_t num_heads, uint32_t max_attn_len,
+                              const akh_attn_cached_meta* meta);
+/* SOFTMAX_RECT, ops::softmax_rect_with (emit.rs:528-542). */
+akh_status akh_softmax_rect(akh_backend* be, float* scores,
+                            akh_softmax_rect_meta shape,
+                            const akh_softmax_rect_meta* meta);
+/* ATTN_AV_CACHED, ops::attn_av_cached_with (emit.rs:507-525). */
+akh_status akh_attn_av_cached(akh_backend* be, const float* scores,
+                              const float* v_cache, float* out, uint32_t dim,
+                              const akh_attn_cached_meta* meta);
+/* SILU, ops::silu (emit.rs:686-696): in place x / (1 + e^-x). */
+akh_status akh_silu(akh_backend* be, float* buf, uint32_t len);
+/* Greedy token choice, sample_token with temperature <= 0 and no
+ * repetition penalty (src/nn/sampling.rs:30-32, 83-91): out[r] = first
+ * index of the maximum of logits[r, 0..n]. */
+akh_status akh_argmax_rows(akh_backend* be, const float* logits,
+                           uint32_t rows, uint32_t n, uint32_t* out);
+
+/* ---- 3. model weights and the batched session ---------------------------- */
+
+/* ModelConfig (src/config.rs:1-30). */
+typedef struct {
+  uint32_t vocab_size, dim, num_heads, num_layers, ffn_hidden;
+  float norm_eps;
+  uint32_t eos_token;
+} akh_model_config;
+
+typedef struct akh_model akh_model;
+typedef struct akh_session akh_session;
+
+/* ModelWeights::zeros (src/nn/weights.rs:125-156) on the device. */
+akh_status akh_model_new(akh_backend* be, const akh_model_config* cfg,
+                         akh_model** out);
+void akh_model_free(akh_model* m);
+/* Number of tensors in ModelWeights::params() order (weights.rs:158-171):
+ * embedding, then per layer norm_1, qkv_proj, out_proj, norm_2, ffn_up,
+ * ffn_down, then final_norm, lm_head. */
+uint32_t akh_model_num_params(const akh_model* m);
+/* Device pointer and element count of parameter `index`. */
+akh_status akh_model_param(akh_model* m, uint32_t index, float** dev,
+                           size_t* count);
+/* Copy `count` floats from host into parameter `index` (count must match). */
+akh_status akh_model_upload_param(akh_model* m, uint32_t index,
+                                  const float* host, size_t count);
+
+/* InferenceSession::new + replace_cache(Cache::new(...)) for `batch`
+ * independent sequences (inference.rs:25-54; inference_graphs.rs:520-538).
+ * batch <= 32. */
+akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
+                           uint32_t batch, akh_session** out);
+void akh_session_free(akh_session* s);
+/* Cache::reset for every sequence (inference_graphs.rs:540-542). */
+akh_status akh_session_reset(akh_session* s);
+/* cur_len of every sequence (host copy). */
+akh_status akh_session_cur_len(const akh_session* s, uint32_t* out);
+/* InferenceSession::prefill (inference.rs:61-176) on all sequences at once:
+ * tokens is [batch, prompt_len].  logits ([batch, vocab], last row of each
+ * sequence) and next ([batch], greedy argmax) may be NULL. */
+akh_status akh_session_prefill(akh_session* s, const uint32_t* tokens,
+                               uint32_t prompt_len, float* logits,
+                               uint32_t* next);
+/* InferenceSession::decode_step (inference.rs:178-262) for every sequence:
+ * tokens is [batch] (NULL = feed each sequence its previous greedy token,
+ * kept on the device).  logits / next may be NULL. */
+akh_status akh_session_decode_step(akh_session* s, const uint32_t* tokens,
+                                   float* logits, uint32_t* next);
+/* `steps` greedy decode steps back to back, each feeding the previous
+ * step's argmax, with no host synchronisation in between (the hot loop of
+ * InferenceSession::generate at temperature 0, inference.rs:303-323).
+ * out_tokens ([steps, batch]) may be NULL. */
+akh_status akh_session_decode_greedy(akh_session* s, uint32_t steps,
+                                     uint32_t* out_tokens);
+/* Shorten every sequence to `len` cached tokens (len <= min cur_len); the
+ * rows below `len` are kept.  Used to replay a timed decode window. */
+akh_status akh_session_truncate(akh_session* s, uint32_t len);
+/* Copy sequence `seq`'s K or V cache of layer `layer` ([max_ctx, dim]) to
+ * host (which: 0 = K, 1 = V). */
+akh_status akh_session_download_cache(akh_session* s, uint32_t layer,
+                                      uint32_t seq, int which, float* host);
+
+/* ---- timing (HIP events on the backend's stream) ------------------------- */
+
+/* Start / stop an event pair around whatever is enqueued in between; stop
+ * waits for completion and returns the elapsed milliseconds. */
+akh_status akh_timer_start(akh_backend* be);
+akh_status akh_timer_stop(akh_backend* be, float* ms);
+/* Replay one kernel of the decode step `reps` times alone between events
+ * and report its mean duration.  kernel: 0 = attention of layer 0,
+ * 1 = qkv projection, 2 = out projection, 3 = ffn up, 4 = ffn down,
+ * 5 = lm_head. */
+akh_status akh_session_time_decode_kernel(akh_session* s, int kernel,
+                                          uint32_t reps, float* avg_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,150 @@
+/*
+ * akasha_oracle.h -- CPU restatement of the akasha-core inference path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * backend and the "port" CPU baseline timed by bench.py.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the
+ * product library (libakasha_hip.so) never links or calls it.
+ *
+ * Every function restates one reference function (file:line under the
+ * akasha-core source tree, paths relative to its root) with the same loop
+ * order and the same f32 left-fold summations, so results are bit-faithful to
+ * the reference CPU backend wherever the reference defines the order.  Build
+ * with -ffp-contract=off (no fused multiply-add: Rust never contracts).
+ *
+ * Parity pinning (what checks each function beyond retyping it) is listed per
+ * function in tests/test_oracle.py.  One row is tolerance-pinned only: the
+ * GEMM/GEMV summation order of the absent wilupgu builtins (assumed textbook,
+ * k ascending).
+ */
+#ifndef AKASHA_ORACLE_H
+#define AKASHA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- deterministic generators ------------------------------------------ */
+
+/* src/nn/ops/emit.rs:910-921 (rand_vec): LCG, 24 high bits -> [-1, 1]. */
+void ora_rand_vec(float* out, size_t n, uint64_t seed);
+/* src/nn/train.rs:818-828 (rand_tokens): same LCG, (state >> 33) % vocab. */
+void ora_rand_tokens(uint32_t* out, size_t n, uint32_t vocab, uint64_t seed);
+
+/* ---- kernels (src/shaders/cpu.rs and the wilupgu builtins) ------------- */
+
+/* cpu.rs:25-41 */
+void ora_embedding(const uint32_t* tokens, const float* table, float* out,
+                   uint32_t vocab_size, uint32_t dim, uint32_t seq_len);
+/* cpu.rs:205-222 */
+void ora_rmsnorm(const float* x, const float* w, float* out, uint32_t rows,
+                 uint32_t size, float eps);
+/* wilupgu MATMUL / GEMV (emit.rs:19-57; layout pinned by emit.rs:1449-1455):
+ * C[m,n] = sum_k A[m,k] * B[k,n], k ascending left fold from 0. */
+void ora_matmul(const float* a, const float* b, float* c, uint32_t m,
+                uint32_t n, uint32_t k);
+/* wilupgu MATMUL_ADD / GEMV_ADD (emit.rs:91-126): C[m,n] += (sum_k ...). */
+void ora_matmul_add(const float* a, const float* b, float* c, uint32_t m,
+                    uint32_t n, uint32_t k);
+/* cpu.rs:238-255 */
+void ora_head_gather(const float* src, float* dst, uint32_t seq_len,
+                     uint32_t full_dim, uint32_t head_dim,
+                     uint32_t head_offset);
+/* cpu.rs:84-109 (position = row index) */
+void ora_rope(float* x, uint32_t seq_len, uint32_t dim, uint32_t head_dim);
+/* cpu.rs:111-142 (position = pos_offset + row index) */
+void ora_rope_offset(float* x, uint32_t seq_len, uint32_t dim,
+                     uint32_t head_dim, uint32_t pos_offset);
+/* cpu.rs:224-236 */
+void ora_cache_write(const float* src, float* dst, uint32_t row_count,
+                     uint32_t width, uint32_t dst_row_offset);
+/* cpu.rs:144-162: scores[h*attn_len + j] = q_h . K[j, h] (unscaled) */
+void ora_attn_qk_cached(const float* q, const float* k_cache, float* scores,
+                        uint32_t attn_len, uint32_t dim, uint32_t head_dim);
+/* cpu.rs:180-203 */
+void ora_softmax_rect(float* x, uint32_t num_rows, uint32_t width,
+                      float scale);
+/* cpu.rs:164-178 */
+void ora_attn_av_cached(const float* scores, const float* v_cache, float* out,
+                        uint32_t attn_len, uint32_t dim, uint32_t head_dim);
+/* cpu.rs:63-69 */
+void ora_silu(float* x, size_t n);
+/* src/nn/ops/emit.rs:931-999 (cpu_attention, forward half): causal
+ * softmax(scale * Q K^T) V per head, scale = 1/sqrt(head_dim); rows are
+ * [seq_len, dim] with head h at columns h*head_dim. */
+void ora_causal_attention(const float* q, const float* k, const float* v,
+                          float* out, uint32_t seq_len, uint32_t dim,
+                          uint32_t head_dim);
+/* src/nn/sampling.rs:83-91: first index of the maximum (strict >). */
+uint32_t ora_argmax(const float* logits, uint32_t n);
+
+/* ---- model + session (src/nn/inference.rs, inference_graphs.rs) -------- */
+
+/* src/config.rs:1-30 (ModelConfig; ffn_hidden = 4*dim, eps = 1e-5). */
+typedef struct {
+  uint32_t vocab_size;
+  uint32_t dim;
+  uint32_t num_heads;
+  uint32_t num_layers;
+  uint32_t ffn_hidden;
+  float norm_eps;
+  uint32_t eos_token;
+} ora_config;
+
+/* src/nn/weights.rs:32-47; one pointer per tensor, laid out exactly as the
+ * reference's ModelWeights ([in, out] row-major matrices, qkv rows
+ * interleaved [Q_row | K_row | V_row] per weights.rs:49-58).  Per-layer
+ * arrays have num_layers entries. */
+typedef struct {
+  const float* embedding;      /* [vocab, dim] */
+  const float* const* norm_1;  /* [dim] each */
+  const float* const* qkv_proj; /* [dim, 3*dim] */
+  const float* const* out_proj; /* [dim, dim] */
+  const float* const* norm_2;   /* [dim] */
+  const float* const* ffn_up;   /* [dim, ffn] */
+  const float* const* ffn_down; /* [ffn, dim] */
+  const float* final_norm;      /* [dim] */
+  const float* lm_head;         /* [dim, vocab] */
+} ora_weights;
+
+typedef struct ora_session ora_session;
+
+/* Error codes follow src/lib.rs:10-17 (AkashaError). */
+enum {
+  ORA_OK = 0,
+  ORA_E_EMPTY_PROMPT = 1,
+  ORA_E_PROMPT_TOO_LONG = 2,
+  ORA_E_CONTEXT_FULL = 3,
+  ORA_E_NO_CACHE = 4,
+  ORA_E_CACHE_NOT_EMPTY = 5
+};
+
+/* InferenceSession::new + replace_cache(Cache::new) (inference.rs:25-54,
+ * inference_graphs.rs:511-538).  The weights are borrowed, not copied. */
+ora_session* ora_session_new(const ora_config* cfg, const ora_weights* w,
+                             uint32_t max_context_len);
+void ora_session_free(ora_session* s);
+/* Cache::reset (inference_graphs.rs:540-542). */
+void ora_session_reset(ora_session* s);
+uint32_t ora_session_cur_len(const ora_session* s);
+/* InferenceSession::prefill (inference.rs:61-176): logits of the last row. */
+int ora_session_prefill(ora_session* s, const uint32_t* tokens, uint32_t n,
+                        float* logits);
+/* InferenceSession::decode_step (inference.rs:178-262). */
+int ora_session_decode_step(ora_session* s, uint32_t token, float* logits);
+/* Pointers into the session's cache (per layer [max_ctx, dim]). */
+const float* ora_session_k_cache(const ora_session* s, uint32_t layer);
+const float* ora_session_v_cache(const ora_session* s, uint32_t layer);
+
+/* Host-thread count used by ora_matmul / ora_matmul_add (OpenMP over
+ * output columns; every output element keeps its own k-ascending fold, so
+ * results are identical for any count).  Default 1. */
+void ora_set_threads(int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

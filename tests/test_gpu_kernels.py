@@ -1,0 +1,258 @@
+"""Per-shader launchers of libakasha_hip.so against the CPU oracle.
+
+Shapes, seeds and tolerances follow the reference's own kernel tests
+(src/nn/ops/emit.rs:1001-1503) where they exist.  Every call goes through
+the C ABI on the GPU.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _meta(be, m):
+    return be.meta(m)
+
+
+def test_embedding(backend, pkg, ora):
+    h = pkg.hip
+    vocab, dim = 11, 300
+    table = ora.rand_vec(vocab * dim, 3)
+    toks = np.array([0, 10, 11, 5, 4294967295, 3], np.uint32)
+    out = backend.zeros(len(toks) * dim)
+    shape = h.EmbeddingMeta(vocab, dim, len(toks))
+    backend.embedding(backend.tensor(toks), backend.tensor(table), out, shape, _meta(backend, shape))
+    got = out.download()
+    assert np.array_equal(got, ora.embedding(toks, table, vocab, dim, len(toks)))
+
+
+@pytest.mark.parametrize("rows,size", [(5, 96), (3, 768), (1, 32)])
+def test_rmsnorm(backend, pkg, ora, rows, size):
+    h = pkg.hip
+    x = ora.rand_vec(rows * size, 9) * 3
+    w = 1 + ora.rand_vec(size, 10) * 0.1
+    out = backend.zeros(rows * size)
+    shape = h.NormMeta(rows, size, 1e-5)
+    backend.rmsnorm(backend.tensor(x), backend.tensor(w), out, shape, _meta(backend, shape))
+    np.testing.assert_allclose(out.download(), ora.rmsnorm(x, w, rows, size, 1e-5),
+                               rtol=1e-5, atol=1e-6)
+
+
+def test_gemv_routing(backend, pkg, ora):
+    # gemv_routing_matches_cpu_reference (emit.rs:1424-1465): n=301, k=19.
+    h = pkg.hip
+    n, k = 301, 19
+    a, b, c0 = ora.rand_vec(k, 10), ora.rand_vec(k * n, 20), ora.rand_vec(n, 30)
+    shape = h.MatMulMeta(1, n, k)
+    meta = _meta(backend, shape)
+    c = backend.zeros(n)
+    cadd = backend.tensor(c0)
+    ta, tb = backend.tensor(a), backend.tensor(b)
+    backend.matmul(ta, tb, c, shape, meta)
+    backend.matmul_add(ta, tb, cadd, shape, meta)
+    assert np.abs(c.download() - ora.matmul(a, b, 1, n, k)).max() < 1e-4
+    assert np.abs(cadd.download() - ora.matmul_add(a, b, c0, 1, n, k)).max() < 1e-4
+
+
+@pytest.mark.parametrize("m,n,k", [(37, 301, 19), (2, 50257, 768), (32, 768, 3072),
+                                   (128, 128, 64), (200, 2304, 768), (513, 130, 37)])
+def test_matmul_and_add(backend, pkg, ora, m, n, k):
+    h = pkg.hip
+    a, b = ora.rand_vec(m * k, 1), ora.rand_vec(k * n, 2)
+    c0 = ora.rand_vec(m * n, 3)
+    shape = h.MatMulMeta(m, n, k)
+    meta = _meta(backend, shape)
+    ta, tb = backend.tensor(a), backend.tensor(b)
+    c, cadd = backend.zeros(m * n), backend.tensor(c0)
+    backend.matmul(ta, tb, c, shape, meta)
+    backend.matmul_add(ta, tb, cadd, shape, meta)
+    ref = ora.matmul(a, b, m, n, k)
+    tol = 1e-4 * max(1.0, np.sqrt(k / 19.0))
+    assert np.abs(c.download() - ref).max() < tol
+    assert np.abs(cadd.download() - ora.matmul_add(a, b, c0, m, n, k)).max() < tol
+
+
+def test_matmul_live_meta_bounds_work(backend, pkg, ora):
+    # Grid sized for the build-time shape; the live meta shrinks m and n.
+    h = pkg.hip
+    M, N, K = 64, 256, 32
+    a, b = ora.rand_vec(M * K, 4), ora.rand_vec(K * N, 5)
+    sentinel = np.full(M * N, 7.0, np.float32)
+    for m, n in ((40, 200), (1, 100)):
+        c = backend.tensor(sentinel)
+        live = h.MatMulMeta(m, n, K)
+        backend.matmul(backend.tensor(a), backend.tensor(b[: K * n].copy()), c,
+                       h.MatMulMeta(M, N, K), _meta(backend, live))
+        got = c.download()
+        ref = ora.matmul(a[: m * K], b[: K * n], m, n, K)
+        assert np.abs(got[: m * n] - ref).max() < 1e-4
+        assert np.all(got[m * n:] == 7.0)
+
+
+@pytest.mark.parametrize("seq,dim", [(8, 4), (37, 12), (65, 48)])
+def test_head_gather_qkv_slices(backend, pkg, ora, seq, dim):
+    # qkv_split_matches_three_head_gathers shapes (emit.rs:1227-1231).
+    h = pkg.hip
+    src = ora.rand_vec(seq * 3 * dim, 50)
+    t = backend.tensor(src)
+    for role in range(3):
+        out = backend.zeros(seq * dim)
+        shape = h.HeadMoveMeta(seq, 3 * dim, dim, role * dim)
+        backend.head_gather(t, out, shape, _meta(backend, shape))
+        assert np.array_equal(out.download(), ora.head_gather(src, seq, 3 * dim, dim, role * dim))
+
+
+@pytest.mark.parametrize("seq,dim,hd", [(8, 8, 4), (37, 12, 4), (65, 48, 16)])
+def test_rope_and_offset(backend, pkg, ora, seq, dim, hd):
+    h = pkg.hip
+    x = ora.rand_vec(seq * dim, 10)
+    buf = backend.tensor(x)
+    shape = h.RopeMeta(seq, dim, hd, 0)
+    backend.rope(buf, shape, _meta(backend, shape))
+    assert np.abs(buf.download() - ora.rope(x, seq, dim, hd)).max() < 1e-4
+    for pos in (0, 5, 511):
+        row = x[:dim].copy()
+        rb = backend.tensor(row)
+        s2 = h.RopeOffsetMeta(1, dim, hd, pos)
+        backend.rope_offset(rb, s2, _meta(backend, s2))
+        assert np.abs(rb.download() - ora.rope_offset(row, 1, dim, hd, pos)).max() < 1e-4
+
+
+def test_cache_write(backend, pkg, ora):
+    h = pkg.hip
+    src, dst = ora.rand_vec(3 * 64, 1), ora.rand_vec(10 * 64, 2)
+    t = backend.tensor(dst)
+    shape = h.CacheWriteMeta(3, 64, 4)
+    backend.cache_write(backend.tensor(src), t, shape, _meta(backend, shape))
+    assert np.array_equal(t.download(), ora.cache_write(src, dst, 3, 64, 4))
+
+
+def _flash(backend, h, q, k, v, seq, dim, hd, row_offset=0, total_rows=None):
+    total_rows = total_rows or seq
+    out = backend.zeros(total_rows * dim)
+    lse = backend.zeros(seq * (dim // hd))
+    shape = h.FlashAttnMeta(seq, dim, hd, np.float32(1.0) / np.sqrt(np.float32(hd)), row_offset)
+    backend.flash_attention(backend.tensor(q), backend.tensor(k), backend.tensor(v), out, lse,
+                            shape, _meta(backend, shape))
+    return out.download(), lse.download()
+
+
+@pytest.mark.parametrize("seq,heads,hd", [(8, 2, 4), (37, 3, 16), (65, 12, 64), (200, 2, 64),
+                                          (130, 1, 128)])
+def test_flash_attention(backend, pkg, ora, seq, heads, hd):
+    # flash_attention_matches_cpu_reference (emit.rs:1001-1098), tol 1e-3.
+    h = pkg.hip
+    dim = heads * hd
+    n = seq * dim
+    q, k, v = ora.rand_vec(n, 1), ora.rand_vec(n, 2), ora.rand_vec(n, 3)
+    got, lse = _flash(backend, h, q, k, v, seq, dim, hd)
+    ref = ora.causal_attention(q, k, v, seq, dim, hd)
+    assert np.abs(got - ref).max() < 1e-3
+    # l_cache = max + ln(sum) of the scaled scores (cuda.rs:680-682).
+    Q, K = q.reshape(seq, dim).astype(np.float64), k.reshape(seq, dim).astype(np.float64)
+    for hh in range(heads):
+        sl = slice(hh * hd, (hh + 1) * hd)
+        s = Q[:, sl] @ K[:, sl].T / np.sqrt(hd)
+        s[np.triu_indices(seq, 1)] = -np.inf
+        ref_l = np.log(np.exp(s - s.max(1, keepdims=True)).sum(1)) + s.max(1)
+        assert np.abs(lse.reshape(seq, heads)[:, hh] - ref_l).max() < 1e-3
+
+
+def test_flash_attention_c2_config(backend, pkg, ora):
+    # batch 8, 12 heads, seq 512, head_dim 64, N(0,1)
+    # from seed 2, scale 1/8; sequences are row_offset slices of [8*512, 768].
+    h = pkg.hip
+    B, S, H, hd = 8, 512, 12, 64
+    d = H * hd
+    rng = np.random.default_rng(2)
+    q, k, v = (rng.standard_normal(B * S * d, dtype=np.float32) for _ in range(3))
+    tq, tk, tv = backend.tensor(q), backend.tensor(k), backend.tensor(v)
+    out = backend.zeros(B * S * d)
+    lse = backend.zeros(S * H)
+    for b in range(B):
+        shape = h.FlashAttnMeta(S, d, hd, 0.125, b * S)
+        backend.flash_attention(tq, tk, tv, out, lse, shape, _meta(backend, shape))
+    got = out.download().reshape(B, S * d)
+    for b in (0, 5, 7):
+        sl = slice(b * S * d, (b + 1) * S * d)
+        ref = ora.causal_attention(q[sl], k[sl], v[sl], S, d, hd)
+        assert np.abs(got[b] - ref).max() < 1e-3
+
+
+@pytest.mark.parametrize("attn_len,heads,hd", [(1, 2, 4), (5, 3, 16), (33, 12, 64)])
+def test_cached_attention_three_dispatch(backend, pkg, ora, attn_len, heads, hd):
+    # cached_attention_matches_cpu_reference (emit.rs:1332-1420): grid sized
+    # for max_ctx 64, meta bounds the live work; tol 1e-4.
+    h = pkg.hip
+    dim, max_ctx = heads * hd, 64
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    q = ora.rand_vec(dim, 1)
+    kc, vc = ora.rand_vec(max_ctx * dim, 2), ora.rand_vec(max_ctx * dim, 3)
+    scores = backend.zeros(heads * max_ctx)
+    out = backend.zeros(dim)
+    am = _meta(backend, h.AttnCachedMeta(attn_len, dim, hd))
+    sm_shape = h.SoftmaxRectMeta(heads, attn_len, scale)
+    tk, tv = backend.tensor(kc), backend.tensor(vc)
+    backend.attn_qk_cached(backend.tensor(q), tk, scores, heads, max_ctx, am)
+    backend.softmax_rect(scores, sm_shape, _meta(backend, sm_shape))
+    backend.attn_av_cached(scores, tv, out, dim, am)
+    s = ora.attn_qk_cached(q, kc, attn_len, dim, hd)
+    p = ora.softmax_rect(s, heads, attn_len, scale)
+    ref = ora.attn_av_cached(p, vc, attn_len, dim, hd)
+    assert np.abs(out.download() - ref).max() < 1e-4
+
+
+def test_silu_past_1d_grid_limit(backend, pkg):
+    # elementwise_ops_past_1d_grid_limit (emit.rs:1473-1503).
+    n = 17_000_003
+    boundary = 65535 * 256
+    i = np.arange(n)
+    data = (((i % 1000) - 500) / 250.0).astype(np.float32)
+    t = backend.tensor(data)
+    backend.silu(t, n)
+    out = t.download()
+    for idx in (0, boundary - 1, boundary, 16_900_000, n - 1):
+        v = np.float64(data[idx])
+        assert abs(out[idx] - v / (1 + np.exp(-v))) < 1e-5
+
+
+def test_argmax_rows(backend, pkg, ora):
+    rows = np.array([[1, 4, 2, 8, 3], [1, 8, 2, 8, 3], [-np.inf] * 5], np.float32)
+    out = backend.zeros(3, np.uint32)
+    backend.argmax_rows(backend.tensor(rows), 3, 5, out)
+    assert list(out.download(np.uint32)) == [3, 1, 0]
+    big = np.random.default_rng(1).standard_normal((4, 50257)).astype(np.float32)
+    big[2, 777] = big[2, 50000] = 99.0
+    o2 = backend.zeros(4, np.uint32)
+    backend.argmax_rows(backend.tensor(big), 4, 50257, o2)
+    assert list(o2.download(np.uint32)) == [ora.argmax(r) for r in big]
+
+
+def test_shader_decode_graph_replays_with_live_metas(backend, pkg, ora):
+    # build_decode_layer + decode_step through the per-shader ABI, captured
+    # once into a hipGraph and replayed every step after the dynamic metas
+    # are rewritten (inference.rs:178-262).
+    from shader_graph import ShaderDecoder
+    cfg = pkg.ModelConfig.new(97, 64, 4, 2, 16)
+    w = pkg.synthetic_weights(cfg, seed=42)
+    dec = ShaderDecoder(pkg.hip, backend, cfg, w, 16)
+    ref = ora.OracleSession(cfg, w, 16)
+    toks = [3, 41, 7, 96, 0, 25, 11, 12, 13, 50]
+    for t in toks:
+        got = dec.decode_step(t)
+        exp = ref.decode_step(t)
+        assert np.abs(got - exp).max() < 1e-3
+        assert int(np.argmax(got)) == ora.argmax(exp)
+
+
+def test_shader_prefill_graph(backend, pkg, ora):
+    from shader_graph import shader_prefill
+    cfg = pkg.ModelConfig.new(97, 128, 2, 2, 48)  # head_dim 64 -> MFMA flash
+    w = pkg.synthetic_weights(cfg, seed=8)
+    toks = ora.rand_tokens(37, 97, 4)
+    logits, kc = shader_prefill(pkg.hip, backend, cfg, w, toks, 48)
+    ref = ora.OracleSession(cfg, w, 48)
+    exp = ref.prefill(toks)
+    assert np.abs(logits - exp).max() < 1e-3
+    np.testing.assert_allclose(kc[1], ref.k_cache(1), atol=1e-4)
