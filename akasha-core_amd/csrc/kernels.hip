@@ -402,7 +402,11 @@ __global__ __launch_bounds__(256) void k_skinny(SkinnyParams p) {
 
   // K chunk of this block (multiple of 64 so each half-wave gets a
   // multiple of 8 rows), then this wave's quarter and this half's rows.
-  const int kc = (((K + p.ksplit - 1) / p.ksplit) + 63) & ~63;
+  // Derived from the launched grid, so the number of chunks never exceeds
+  // what the host sized the workspace for, whatever the live meta says.
+  const int kc = max(64, (((K + (int)gridDim.y - 1) / (int)gridDim.y) + 63) & ~63);
+  const int nks = max(1, (K + kc - 1) / kc);
+  if (ks >= nks) return;
   const int kb = ks * kc;
   const int ke = min(K, kb + kc);
   const int hl = kc / 8;  // rows per half-wave
@@ -478,7 +482,6 @@ __global__ __launch_bounds__(256) void k_skinny(SkinnyParams p) {
              red[3][m][col + 1];
   }
 
-  const int nks = (K + kc - 1) / kc;
   if (nks > 1) {
     // Publish this block's partial tile; the last block sums all of them.
     float* mine = p.ws + ((size_t)tile * nks + ks) * 32 * NT;

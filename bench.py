@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Benchmark of the akasha-core inference hot path on one MI355X.
+
+Headline (BASELINE.json metric, config 4): akasha-hall 1.0 fp32 greedy
+decode at batch 32 -- every sequence prefilled with 448 random tokens
+(seed 4), then decode steps at positions 448..511 so the KV cache reaches
+512 tokens.  A "step" is one decode step of all 32 sequences (embedding ->
+12 layers -> lm_head -> argmax, graph-replayed, tokens fed back on the
+device).  ``value`` = 32 * steps / time (tok/s), inputs resident in HBM.
+Windows of up to 64 steps are replayed from position 448 (the cache is
+truncated back to 448 between windows).
+
+Also reported: the roofline of the dominant decode kernel (single-query
+attention over the cache, timed alone with HIP events), the whole-step HBM
+roofline, per-kernel times, config-3 prefill (16 x 512) throughput against
+the fp32 MFMA peak, and the CPU baseline: the oracle's decode step (a C
+restatement of the reference CPU backend) on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import __graft_entry__ as entry  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_step_bytes(cfg, B, T):
+    """Algorithmic bytes of one decode step whose attention reads T rows:
+    weights once, KV rows read, KV append, embedding rows, logits written."""
+    d, L, V = cfg.dim, cfg.num_layers, cfg.vocab_size
+    weights = 4 * (sum(int(np.prod(s)) for s in cfg.param_shapes()) - V * d)
+    kv_read = 2 * L * B * T * d * 4
+    kv_append = 2 * L * B * d * 4
+    return weights + kv_read + kv_append + B * d * 4 + B * V * 4
+
+
+def prefill_flops(cfg, B, S):
+    d, F, L, H, hd, V = cfg.dim, cfg.ffn_hidden, cfg.num_layers, cfg.num_heads, cfg.head_dim, cfg.vocab_size
+    gemm = 2 * B * S * L * (d * 3 * d + d * d + d * F + F * d)
+    attn = 2 * hd * S * (S + 1) * B * H * L
+    lm = 2 * B * d * V
+    return gemm + attn + lm
+
+
+def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=1):
+    ora = entry.load_oracle()
+    ora.set_threads(threads)
+    s = ora.OracleSession(cfg, weights, cfg.seq_len)
+    s.set_len(prompt_len)
+    tok = 1
+    t0 = time.perf_counter()
+    n = 0
+    while n < max_steps and time.perf_counter() - t0 < budget_s:
+        logits = s.decode_step(tok)
+        tok = ora.argmax(logits)
+        n += 1
+    dt = time.perf_counter() - t0
+    s.close()
+    ora.set_threads(1)
+    return n / dt, n, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "sequences shard by data parallelism with no exchange, so N GPUs would "
+              "run N independent copies of this benchmark.", file=sys.stderr)
+        sys.exit(2)
+
+    pkg = entry.load_package()
+    hip = pkg.hip
+    cfg = pkg.ModelConfig.akasha_hall_1()
+    B, P, CTX = 32, 448, 512
+    log("bench: generating hall-1.0 weights (seed 0)")
+    w = pkg.synthetic_weights(cfg, seed=0)
+    be = hip.Backend(0)
+    model = hip.Model(be, cfg)
+    model.upload(w)
+    sess = hip.Session(model, CTX, B)
+    prompt = pkg.synthetic_tokens(B * P, cfg.vocab_size, seed=4).reshape(B, P)
+    log("bench: prefill 32 x 448")
+    sess.prefill(prompt, want_logits=False)
+    window = CTX - P
+
+    def run_steps(n):
+        done, total_ms = 0, 0.0
+        while done < n:
+            k = min(window, n - done)
+            sess.truncate(P)
+            be.synchronize()
+            be.timer_start()
+            sess.decode_greedy(k, want_tokens=False)
+            total_ms += be.timer_stop()
+            done += k
+        return total_ms
+
+    log(f"bench: warmup {args.warmup} decode steps")
+    if args.warmup:
+        run_steps(args.warmup)
+    log(f"bench: timing {args.steps} decode steps")
+    ms = run_steps(args.steps)
+    ms_per_step = ms / args.steps
+    tok_s = B * args.steps / (ms / 1e3)
+
+    # Whole-step HBM roofline over the same position schedule.
+    total_bytes, done = 0, 0
+    while done < args.steps:
+        k = min(window, args.steps - done)
+        total_bytes += sum(decode_step_bytes(cfg, B, P + i + 1) for i in range(k))
+        done += k
+    step_gbs = total_bytes / (ms / 1e3) / 1e9
+
+    # Dominant kernel: decode attention of layer 0 at T = 481 (pos 480).
+    sess.truncate(P)
+    sess.decode_greedy(32, want_tokens=False)
+    T = P + 32 + 1
+    names = ["decode_attn", "qkv_rope_append", "out_proj_residual", "ffn_up_silu",
+             "ffn_down_residual", "lm_head_argmax"]
+    kms = {n: sess.time_decode_kernel(i, args.kernel_reps) for i, n in enumerate(names)}
+    d, L, V, F = cfg.dim, cfg.num_layers, cfg.vocab_size, cfg.ffn_hidden
+    attn_bytes = 2 * B * T * d * 4 + 2 * B * d * 4
+    attn_gbs = attn_bytes / (kms["decode_attn"] / 1e3) / 1e9
+    kbytes = {
+        "decode_attn": attn_bytes,
+        "qkv_rope_append": d * 3 * d * 4 + d * 4 + B * 3 * d * 4,
+        "out_proj_residual": d * d * 4 + 3 * B * d * 4,
+        "ffn_up_silu": d * F * 4 + d * 4 + B * (d + F) * 4,
+        "ffn_down_residual": F * d * 4 + B * (F + 2 * d) * 4,
+        "lm_head_argmax": d * V * 4 + d * 4 + B * V * 4,
+    }
+    kernels = {n: {"ms": round(kms[n], 5), "bytes": kbytes[n],
+                   "GB/s": round(kbytes[n] / (kms[n] / 1e3) / 1e9, 1)} for n in names}
+
+    prefill = None
+    if not args.no_prefill:
+        Bp, Sp = 16, 512
+        ps = hip.Session(model, CTX, Bp)
+        ptoks = pkg.synthetic_tokens(Bp * Sp, cfg.vocab_size, seed=3).reshape(Bp, Sp)
+        ps.prefill(ptoks, want_logits=False)  # warm
+        times = []
+        for _ in range(3):
+            ps.reset()
+            be.synchronize()
+            be.timer_start()
+            ps.prefill(ptoks, want_logits=False)
+            times.append(be.timer_stop())
+        pms = min(times)
+        fl = prefill_flops(cfg, Bp, Sp)
+        prefill = {"workload": "config 3: hall-1.0 fp32 prefill 16 x 512 (seed 3), last-row logits",
+                   "ms": round(pms, 3), "tok_s": round(Bp * Sp / (pms / 1e3), 1),
+                   "tflops": round(fl / (pms / 1e3) / 1e12, 2),
+                   "mfma_frac": round(fl / (pms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+                   "flop": fl}
+        ps.close()
+
+    cpu = None
+    if not args.no_cpu:
+        log("bench: CPU baseline (oracle decode step, 1 thread)")
+        v1, n1, t1 = cpu_baseline(cfg, w, P, threads=1)
+        cpu = {"value": round(v1, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"oracle decode of 1 sequence, {n1} steps at positions 448.. "
+                         f"({t1:.1f} s), zero KV prefix; the reference CPU backend runs "
+                         f"one sequence per session"}
+        nt = min(16, os.cpu_count() or 1)
+        vN, nN, tN = cpu_baseline(cfg, w, P, budget_s=6.0, threads=nt)
+        cpu_omp = {"value": round(vN, 3), "cores": nt, "steps": nN, "seconds": round(tN, 2)}
+    else:
+        cpu_omp = None
+
+    sess.close()
+    model.close()
+    be.close()
+
+    out = {
+        "metric": "decode tok/s @ batch 32 ctx 512 (%HBM roofline)",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "config 4: akasha-hall 1.0 greedy decode, batch 32, "
+                               "prefill 448 (seed 4), positions 448..511 (KV 449..512)",
+                   "model": "akasha-hall-1.0 (162M)", "global_batch": B, "seq_len": CTX,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"kernel": "decode_attn (layer 0, T=481)", "bound": "hbm",
+                     "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "step_roofline": {"achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                          "bytes_per_step_mean": int(total_bytes / args.steps)},
+        "kernels": kernels,
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+        "cpu_baseline_omp": cpu_omp,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -298,6 +298,9 @@ void ora_session_free(ora_session* s) {
 }
 
 void ora_session_reset(ora_session* s) { s->cur_len = 0; }
+void ora_session_set_len(ora_session* s, uint32_t len) {
+  s->cur_len = len < s->max_ctx ? len : s->max_ctx;
+}
 uint32_t ora_session_cur_len(const ora_session* s) { return s->cur_len; }
 const float* ora_session_k_cache(const ora_session* s, uint32_t l) {
   return s->k_cache[l];

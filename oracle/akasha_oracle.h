@@ -139,6 +139,11 @@ int ora_session_decode_step(ora_session* s, uint32_t token, float* logits);
 const float* ora_session_k_cache(const ora_session* s, uint32_t layer);
 const float* ora_session_v_cache(const ora_session* s, uint32_t layer);
 
+/* Benchmark hook: pretend `len` tokens are cached (their rows keep whatever
+ * the cache holds, zeros for a fresh session), so a decode step at
+ * position `len` can be timed without a long CPU prefill first. */
+void ora_session_set_len(ora_session* s, uint32_t len);
+
 /* Host-thread count used by ora_matmul / ora_matmul_add (OpenMP over
  * output columns; every output element keeps its own k-ascending fold, so
  * results are identical for any count).  Default 1. */

@@ -71,6 +71,7 @@ def load():
         "ora_session_k_cache": (FP, [C.c_void_p, u32]),
         "ora_session_v_cache": (FP, [C.c_void_p, u32]),
         "ora_set_threads": (None, [C.c_int]),
+        "ora_session_set_len": (None, [C.c_void_p, u32]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -226,6 +227,10 @@ class OracleSession:
 
     def reset(self):
         _lib.ora_session_reset(self.h)
+
+    def set_len(self, n: int):
+        """Benchmark hook: treat n tokens as cached (see akasha_oracle.h)."""
+        _lib.ora_session_set_len(self.h, n)
 
     def k_cache(self, layer: int) -> np.ndarray:
         p = _lib.ora_session_k_cache(self.h, layer)
