@@ -112,9 +112,12 @@ hipError_t launch_gather_rows(const float* table, const uint32_t* ids,
                               uint32_t vocab, const float* src, long src_row0,
                               long src_row_stride, float* dst, int M, int d,
                               float* ss, hipStream_t s);
+// Greedy token per row from the lm_head partials; with `pos` it also does
+// the decode step's bookkeeping (token history, position advance), without
+// it records the token at `next_pos` of the history (prefill).
 hipError_t launch_argmax_final(const uint2* part, int ntiles, int M,
                                uint32_t* tok, int* pos, uint32_t* hist,
-                               int hist_stride, hipStream_t s);
+                               int hist_stride, int next_pos, hipStream_t s);
 hipError_t launch_rows_rmsnorm(const float* x, const float* w, float* out,
                                int rows, int size, float eps, hipStream_t s);
 hipError_t launch_embedding_rows(const uint32_t* tokens, const float* table,

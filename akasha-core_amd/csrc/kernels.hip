@@ -565,11 +565,14 @@ __global__ __launch_bounds__(256) void k_skinny(SkinnyParams p) {
   }
 }
 
-// Final argmax over the lm_head tiles' partials; advances each row's
-// position and records the token (decode step bookkeeping on the device).
+// Final argmax over the lm_head tiles' partials, plus the step's
+// bookkeeping on the device.  hist[m, p] is the token at position p of
+// sequence m.  Decode (pos set): record the consumed token at pos[m], the
+// chosen one at pos[m] + 1, advance pos[m].  Prefill (pos null): record the
+// chosen token at position `next_pos`.
 __global__ __launch_bounds__(256) void k_argmax_final(
     const uint2* part, int ntiles, uint32_t* tok, int* pos, uint32_t* hist,
-    int hist_stride) {
+    int hist_stride, int next_pos) {
   const int m = blockIdx.x;
   float bv = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
@@ -580,12 +583,18 @@ __global__ __launch_bounds__(256) void k_argmax_final(
   block_amax256(bv, bi);
   if (threadIdx.x == 0) {
     const uint32_t id = bi == 0xFFFFFFFFu ? 0u : bi;
-    tok[m] = id;
+    uint32_t* hrow = hist ? hist + (size_t)m * hist_stride : nullptr;
     if (pos) {
-      const int p1 = pos[m] + 1;
-      if (hist) hist[(size_t)m * hist_stride + p1] = id;
-      pos[m] = p1;
+      const int p = pos[m];
+      if (hrow) {
+        hrow[p] = tok[m];
+        hrow[p + 1] = id;
+      }
+      pos[m] = p + 1;
+    } else if (hrow) {
+      hrow[next_pos] = id;
     }
+    tok[m] = id;
   }
 }
 
@@ -1184,9 +1193,9 @@ hipError_t launch_gather_rows(const float* table, const uint32_t* ids,
 
 hipError_t launch_argmax_final(const uint2* part, int ntiles, int M,
                                uint32_t* tok, int* pos, uint32_t* hist,
-                               int hist_stride, hipStream_t s) {
+                               int hist_stride, int next_pos, hipStream_t s) {
   hipLaunchKernelGGL(k_argmax_final, dim3(M), dim3(256), 0, s, part, ntiles,
-                     tok, pos, hist, hist_stride);
+                     tok, pos, hist, hist_stride, next_pos);
   return hipGetLastError();
 }
 

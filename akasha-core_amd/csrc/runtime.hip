@@ -748,7 +748,7 @@ hipError_t enqueue_decode(akh_session* s) {
   if (e == hipSuccess)
     e = launch_argmax_final(s->amax, (int)((c.vocab_size + 31) / 32),
                             (int)s->B, s->tok, s->pos, s->hist,
-                            (int)s->max_ctx + 1, st);
+                            (int)s->max_ctx + 1, 0, st);
   return e;
 }
 
@@ -913,6 +913,11 @@ extern "C" akh_status akh_session_truncate(akh_session* s, uint32_t len) {
   CHECK_ARG(s, "akh_session_truncate: NULL session");
   for (uint32_t b = 0; b < s->B; ++b)
     CHECK_ARG(len <= s->cur_len[b], "akh_session_truncate: len > cur_len");
+  // The next step feeds the token that occupied position `len`.
+  HIP_TRY(hipMemcpy2DAsync(s->tok, sizeof(uint32_t), s->hist + len,
+                           (size_t)(s->max_ctx + 1) * sizeof(uint32_t),
+                           sizeof(uint32_t), s->B, hipMemcpyDeviceToDevice,
+                           s->be->stream));
   std::fill(s->cur_len.begin(), s->cur_len.end(), len);
   return upload_positions(s);
 }
@@ -943,6 +948,10 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
   if (st0 != AKH_OK) return st0;
   hipStream_t st = s->be->stream;
   HIP_TRY(hipMemcpyAsync(s->ptok, tokens, rows * 4, hipMemcpyHostToDevice, st));
+  // Token history: the prompt occupies positions 0..S-1 of every sequence.
+  HIP_TRY(hipMemcpy2DAsync(s->hist, (size_t)(s->max_ctx + 1) * 4, s->ptok,
+                           (size_t)S * 4, (size_t)S * 4, s->B,
+                           hipMemcpyDeviceToDevice, st));
 
   HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
                                 (int)d, c.vocab_size, st));
@@ -1016,7 +1025,8 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
                              s->x, (int)s->B, (int)d, s->ss1, st));
   HIP_TRY(enqueue_lm_head(s));
   HIP_TRY(launch_argmax_final(s->amax, (int)((c.vocab_size + 31) / 32),
-                              (int)s->B, s->tok, nullptr, nullptr, 0, st));
+                              (int)s->B, s->tok, nullptr, s->hist,
+                              (int)s->max_ctx + 1, (int)S, st));
   std::fill(s->cur_len.begin(), s->cur_len.end(), S);
   akh_status ps = upload_positions(s);
   if (ps != AKH_OK) return ps;
