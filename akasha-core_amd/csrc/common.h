@@ -1,0 +1,112 @@
+// Device helpers shared by the kernel files (CDNA4 / gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+namespace akh {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// v_mfma_f32_32x32x2f32.  Operand layout: lane l supplies A[l % 32][l / 32]
+// and B[l / 32][l % 32]; accumulator register r of lane l holds
+// D[acc_row(r, l / 32)][l % 32].
+__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ int acc_row(int r, int h) {
+  return (r >> 2) * 8 + h * 4 + (r & 3);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Reductions over a 256-thread block; every thread gets the result.  The
+// order is fixed (butterfly in waves, then waves 0..3), so results are
+// reproducible run to run.
+__device__ __forceinline__ float block_sum256(float v, float* red4) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red4[w] = v;
+  __syncthreads();
+  return ((red4[0] + red4[1]) + red4[2]) + red4[3];
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red4) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red4[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+}
+
+// (x0*c - x1*s, x0*s + x1*c) with every product rounded separately, as the
+// reference's CPU RoPE computes it (src/shaders/cpu.rs:102-103).
+__device__ __forceinline__ void rope_pair(float& x0, float& x1, float c,
+                                          float s) {
+  const float a = __fmul_rn(x0, c), b = __fmul_rn(x1, s);
+  const float e = __fmul_rn(x0, s), f = __fmul_rn(x1, c);
+  x0 = __fsub_rn(a, b);
+  x1 = __fadd_rn(e, f);
+}
+
+// Greedy-argmax merge (src/nn/sampling.rs:83-91 picks the first index of
+// the maximum): larger value wins, equal values keep the lower index, which
+// equals the sequential strict-> scan for any split of the row.
+__device__ __forceinline__ void amax_merge(float& bv, uint32_t& bi, float v,
+                                           uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__device__ __forceinline__ void block_amax256(float& bv, uint32_t& bi) {
+  __shared__ float sv[4];
+  __shared__ uint32_t si[4];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const uint32_t oi = __shfl_xor(bi, o, 64);
+    amax_merge(bv, bi, ov, oi);
+  }
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    sv[w] = bv;
+    si[w] = bi;
+  }
+  __syncthreads();
+  bv = sv[0];
+  bi = si[0];
+  for (int k = 1; k < 4; ++k) amax_merge(bv, bi, sv[k], si[k]);
+}
+
+// Index of element (row m, column k) of a 32-row activation tile stored in
+// the k-quad layout [K/4][32][4]: a half-wave reading four consecutive k of
+// its 32 rows touches 512 contiguous bytes.
+__device__ __forceinline__ size_t kq_index(int m, int k) {
+  return ((size_t)(k >> 2) * 32 + m) * 4 + (k & 3);
+}
+
+}  // namespace akh

@@ -1,0 +1,441 @@
+// Prefill kernels: the LDS-tiled fp32 MFMA GEMM (every prefill matmul and
+// the per-shader MATMUL for m > 32), causal flash attention, row RMSNorm and
+// the embedding gather.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace akh {
+
+// Host-sized embedding gather for the batched prefill (cpu.rs:25-41).
+__global__ void k_embedding_rows(const uint32_t* tokens, const float* table,
+                                 float* out, int d, uint32_t vocab) {
+  const int t = blockIdx.x;
+  const uint32_t id = tokens[t];
+  const float4* src = reinterpret_cast<const float4*>(table + (size_t)id * d);
+  float4* dst = reinterpret_cast<float4*>(out + (size_t)t * d);
+  for (int c = threadIdx.x; c < d / 4; c += blockDim.x)
+    dst[c] = id < vocab ? src[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// RMSNorm of every row (cpu.rs:205-222), one 256-thread block per row.
+__global__ __launch_bounds__(256) void k_rows_rmsnorm(const float* x,
+                                                      const float* w,
+                                                      float* out, int size,
+                                                      float eps) {
+  __shared__ float red4[4];
+  const float* xr = x + (size_t)blockIdx.x * size;
+  float* o = out + (size_t)blockIdx.x * size;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < size; c += 256) ss += xr[c] * xr[c];
+  ss = block_sum256(ss, red4);
+  const float rs = 1.0f / sqrtf(ss / (float)size + eps);
+  for (int c = threadIdx.x; c < size; c += 256)
+    o[c] = __fmul_rn(__fmul_rn(xr[c], rs), w[c]);
+}
+
+// Epilogue on the adjacent column pair (n, n + 1), n even, of row m.
+template <int EPI>
+__device__ __forceinline__ void epi_pair_gemm(const GemmParams& p, int M,
+                                              int N, int m, int n, float v0,
+                                              float v1) {
+  if (m >= M || n >= N) return;
+  const bool has1 = n + 1 < N;
+  if (EPI == GEMM_STORE) {
+    float* y = p.c + (size_t)m * N + n;
+    y[0] = v0;
+    if (has1) y[1] = v1;
+  } else if (EPI == GEMM_ADD) {
+    float* y = p.c + (size_t)m * N + n;
+    y[0] = y[0] + v0;
+    if (has1) y[1] = y[1] + v1;
+  } else if (EPI == GEMM_SILU) {
+    float* y = p.c + (size_t)m * N + n;
+    y[0] = v0 / (1.0f + expf(-v0));
+    if (has1) y[1] = v1 / (1.0f + expf(-v1));
+  } else if (EPI == GEMM_QKV) {
+    // Columns [0, d) are Q, [d, 2d) K, [2d, 3d) V (weights.rs:49-58).
+    const int dim = p.dim;
+    const int region = n / dim, c = n - region * dim;
+    const int seq = m / p.S, t = m - seq * p.S;
+    if (region < 2) {
+      const int i = (c % p.head_dim) >> 1;
+      const float2 cs = p.rope[(size_t)t * (p.head_dim >> 1) + i];
+      rope_pair(v0, v1, cs.x, cs.y);
+    }
+    float* dst;
+    if (region == 0)
+      dst = p.q_out + (size_t)m * dim + c;
+    else
+      dst = (region == 1 ? p.kcache : p.vcache) + (size_t)seq * p.seq_stride +
+            (size_t)t * dim + c;
+    dst[0] = v0;
+    dst[1] = v1;
+  }
+}
+
+// C[M,N] = A[M,K] B[K,N], 128x128 block tile, BK = 16, 4 waves in 2x2,
+// each wave a 64x64 sub-tile as 2x2 MFMA 32x32 tiles.  A is staged
+// transposed in LDS so MFMA A-operand reads are contiguous; within a wave's
+// 64 columns, lane j of N tile t owns column 2j + t so each lane holds
+// adjacent column pairs (float2 B reads, paired epilogue for RoPE).  The
+// next K tile is fetched into registers while the current one is consumed.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
+  constexpr int BM = 128, BN = 128, BK = 16;
+  constexpr int APAD = 4;
+  __shared__ float As[BK][BM + APAD];
+  __shared__ float Bs[BK][BN];
+
+  int M = p.M, N = p.N, K = p.K;
+  if (p.meta) {
+    M = (int)p.meta->m;
+    N = (int)p.meta->n;
+    K = (int)p.meta->k;
+  }
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  if (m0 >= M || n0 >= N) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // A: 128 rows x 16 k -> thread loads row tid/2, k 8*(tid&1) .. +7.
+  // B: 16 rows x 128 cols -> rows tid/32 and tid/32 + 8, cols 4*(tid&31).
+  const int a_row = tid >> 1, a_k = (tid & 1) * 8;
+  const int b_row = tid >> 5, b_col = (tid & 31) * 4;
+  const bool a_vec = (K & 3) == 0;
+  const bool b_vec = (N & 3) == 0;
+
+  float ra[8], rb[8];
+  auto load_tile = [&](int k0) {
+    const int gm = m0 + a_row;
+    const float* ap = p.a + (size_t)(gm < M ? gm : 0) * K;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int gk = k0 + a_k + 4 * q;
+      if (gm < M && a_vec && gk + 3 < K) {
+        const float4 t = *reinterpret_cast<const float4*>(ap + gk);
+        ra[4 * q] = t.x; ra[4 * q + 1] = t.y; ra[4 * q + 2] = t.z; ra[4 * q + 3] = t.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          ra[4 * q + e] = (gm < M && gk + e < K) ? ap[gk + e] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int gk = k0 + b_row + 8 * q;
+      const int gn = n0 + b_col;
+      const float* bp = p.b + (size_t)(gk < K ? gk : 0) * N + gn;
+      if (gk < K && b_vec && gn + 3 < N) {
+        const float4 t = *reinterpret_cast<const float4*>(bp);
+        rb[4 * q] = t.x; rb[4 * q + 1] = t.y; rb[4 * q + 2] = t.z; rb[4 * q + 3] = t.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rb[4 * q + e] = (gk < K && gn + e < N) ? bp[e] : 0.f;
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) As[a_k + e][a_row] = ra[e];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      *reinterpret_cast<float4*>(&Bs[b_row + 8 * q][b_col]) =
+          make_float4(rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[a][t] = zero16();
+
+  const int nk = (K + BK - 1) / BK;
+  load_tile(0);
+  store_tile();
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) load_tile((kt + 1) * BK);
+#pragma unroll
+    for (int s = 0; s < BK / 2; ++s) {
+      const int kk = 2 * s + h;
+      const float a0 = As[kk][wm * 64 + j];
+      const float a1 = As[kk][wm * 64 + 32 + j];
+      const float2 bb = *reinterpret_cast<const float2*>(&Bs[kk][wn * 64 + 2 * j]);
+      acc[0][0] = mfma32(a0, bb.x, acc[0][0]);
+      acc[0][1] = mfma32(a0, bb.y, acc[0][1]);
+      acc[1][0] = mfma32(a1, bb.x, acc[1][0]);
+      acc[1][1] = mfma32(a1, bb.y, acc[1][1]);
+    }
+    __syncthreads();
+    if (kt + 1 < nk) {
+      store_tile();
+      __syncthreads();
+    }
+  }
+
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 64 + a * 32 + acc_row(r, h);
+      const int n = n0 + wn * 64 + 2 * j;
+      epi_pair_gemm<EPI>(p, M, N, m, n, acc[a][0][r], acc[a][1][r]);
+    }
+}
+
+// Causal flash attention, head_dim 64, on MFMA.  Block = 4 waves x 32
+// queries of one (sequence, head); keys stream through LDS in blocks of 32.
+// Each wave computes S^T = K Q^T so every lane owns one query (column) and
+// 16 keys, making the online-softmax row statistics lane-local (plus one
+// exchange between the two half-waves); P^T then feeds O^T += V^T P^T
+// straight from the accumulator registers.
+__global__ __launch_bounds__(256) void k_flash64(FlashParams p) {
+  constexpr int HD = 64, QB = 128, KB = 32;
+  __shared__ float Ks[KB][HD + 1];
+  __shared__ float Vs[KB][HD];
+  __shared__ float Os[4][32][HD + 1];
+
+  int S = p.S, d = p.d;
+  float scale = p.scale;
+  long roff = 0;
+  if (p.meta) {
+    S = (int)p.meta->seq_len;
+    d = (int)p.meta->dim;
+    scale = p.meta->scale;
+    roff = (long)p.meta->row_offset * d;
+  }
+  const int H = d / HD;
+  const int qblk = blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int q0 = qblk * QB;
+  if (q0 >= S) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+
+  const float* qp = p.q + roff + (size_t)b * p.q_bs + hh * HD;
+  const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
+  const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
+
+  // This lane's query row and its 32 dims (half h).
+  const int qi = q0 + wave * 32 + j;
+  float qreg[32];
+  {
+    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 32 * h;
+#pragma unroll
+    for (int s = 0; s < 32; s += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(qr + s);
+      qreg[s] = t.x; qreg[s + 1] = t.y; qreg[s + 2] = t.z; qreg[s + 3] = t.w;
+    }
+  }
+  f32x16 o0 = zero16(), o1 = zero16();
+  float mrow = -INFINITY, lrow = 0.f;
+
+  const int wave_qmax = q0 + wave * 32 + 31;
+  const int kend = min(S, q0 + QB);  // keys needed by the block
+  const int nkb = (kend + KB - 1) / KB;
+
+  // Cooperative K/V block load: thread t loads rows t/16 and t/16 + 16,
+  // float4 column t%16, of both tensors.
+  const int lr = tid >> 4, lc = (tid & 15) * 4;
+  float4 kr[2], vr[2];
+  auto load_kv = [&](int kb) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int key = kb * KB + lr + 16 * q;
+      const size_t off = (size_t)(key < S ? key : 0) * d + lc;
+      kr[q] = *reinterpret_cast<const float4*>(kp + off);
+      vr[q] = *reinterpret_cast<const float4*>(vp + off);
+    }
+  };
+  load_kv(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int r = lr + 16 * q;
+      Ks[r][lc] = kr[q].x; Ks[r][lc + 1] = kr[q].y;
+      Ks[r][lc + 2] = kr[q].z; Ks[r][lc + 3] = kr[q].w;
+      *reinterpret_cast<float4*>(&Vs[r][lc]) = vr[q];
+    }
+    __syncthreads();
+    if (kb + 1 < nkb) load_kv(kb + 1);
+    const int j0 = kb * KB;
+    if (j0 > wave_qmax) continue;  // block entirely above this wave's rows
+
+    f32x16 st = zero16();
+#pragma unroll
+    for (int s = 0; s < 32; ++s) st = mfma32(Ks[j][32 * h + s], qreg[s], st);
+
+    float pm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = j0 + acc_row(r, h);
+      float v = st[r] * scale;
+      if (key > qi || key >= S) v = -INFINITY;
+      st[r] = v;
+      pm = fmaxf(pm, v);
+    }
+    pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+    const float mnew = fmaxf(mrow, pm);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = st[r] == -INFINITY ? 0.f : expf(st[r] - mnew);
+      st[r] = e;
+      ps += e;
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    const float corr = mrow == -INFINITY ? 0.f : expf(mrow - mnew);
+    lrow = lrow * corr + ps;
+    mrow = mnew;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      o0[r] *= corr;
+      o1[r] *= corr;
+    }
+    // O^T += V^T P^T: step s uses key acc_row(s, h) on both operands.
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int key = acc_row(s, h);
+      o0 = mfma32(Vs[key][j], st[s], o0);
+      o1 = mfma32(Vs[key][32 + j], st[s], o1);
+    }
+  }
+
+  // O^T (rows = dims) -> LDS -> coalesced row writes.
+  const float inv = 1.0f / lrow;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    Os[wave][j][acc_row(r, h)] = o0[r] * inv;
+    Os[wave][j][32 + acc_row(r, h)] = o1[r] * inv;
+  }
+  __syncthreads();
+  float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD;
+  for (int e = lane; e < 32 * HD; e += 64) {
+    const int r = e / HD, c = e % HD;
+    const int qrow = q0 + wave * 32 + r;
+    if (qrow < S) op[(size_t)qrow * d + c] = Os[wave][r][c];
+  }
+  if (p.lse && h == 0 && qi < S) p.lse[(size_t)qi * H + hh] = mrow + logf(lrow);
+}
+
+// Causal flash attention for other head sizes (up to 128, as the reference
+// asserts, emit.rs:564-567): one thread per query row with an HD-float
+// accumulator, keys staged through LDS in blocks of 64 shared by the
+// block's 64 queries.
+template <int HD>
+__global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
+  constexpr int KB = 64;
+  __shared__ float Ks[KB][HD];
+  __shared__ float Vs[KB][HD];
+  int S = p.S, d = p.d;
+  float scale = p.scale;
+  long roff = 0;
+  if (p.meta) {
+    S = (int)p.meta->seq_len;
+    d = (int)p.meta->dim;
+    scale = p.meta->scale;
+    roff = (long)p.meta->row_offset * d;
+  }
+  const int H = d / HD;
+  const int hh = blockIdx.y, b = blockIdx.z;
+  const int q0 = blockIdx.x * 64;
+  if (q0 >= S) return;
+  const int i = q0 + threadIdx.x;
+  const float* qp = p.q + roff + (size_t)b * p.q_bs + hh * HD;
+  const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
+  const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
+  float q[HD], acc[HD];
+#pragma unroll
+  for (int c = 0; c < HD; ++c) {
+    q[c] = i < S ? qp[(size_t)i * d + c] : 0.f;
+    acc[c] = 0.f;
+  }
+  float mrow = -INFINITY, lrow = 0.f;
+  const int kend = min(S, q0 + 64);
+  for (int k0 = 0; k0 < kend; k0 += KB) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < KB * HD; e += 64) {
+      const int r = e / HD, c = e % HD;
+      const int key = k0 + r;
+      Ks[r][c] = key < S ? kp[(size_t)key * d + c] : 0.f;
+      Vs[r][c] = key < S ? vp[(size_t)key * d + c] : 0.f;
+    }
+    __syncthreads();
+    const int lim = min(KB, (i < S ? i : -1) - k0 + 1);
+    for (int r = 0; r < lim; ++r) {
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < HD; ++c) s += q[c] * Ks[r][c];
+      s *= scale;
+      const float mnew = fmaxf(mrow, s);
+      const float corr = mrow == -INFINITY ? 0.f : expf(mrow - mnew);
+      const float e = expf(s - mnew);
+      lrow = lrow * corr + e;
+#pragma unroll
+      for (int c = 0; c < HD; ++c) acc[c] = acc[c] * corr + e * Vs[r][c];
+      mrow = mnew;
+    }
+  }
+  if (i >= S) return;
+  float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD + (size_t)i * d;
+#pragma unroll
+  for (int c = 0; c < HD; ++c) op[c] = acc[c] / lrow;
+  if (p.lse) p.lse[(size_t)i * H + hh] = mrow + logf(lrow);
+}
+
+// ---------------------------------------------------------------------------
+
+hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
+  dim3 g((p.N + 127) / 128, (p.M + 127) / 128), b(256);
+  switch (epi) {
+    case GEMM_STORE: hipLaunchKernelGGL(k_gemm<GEMM_STORE>, g, b, 0, s, p); break;
+    case GEMM_ADD: hipLaunchKernelGGL(k_gemm<GEMM_ADD>, g, b, 0, s, p); break;
+    case GEMM_SILU: hipLaunchKernelGGL(k_gemm<GEMM_SILU>, g, b, 0, s, p); break;
+    case GEMM_QKV: hipLaunchKernelGGL(k_gemm<GEMM_QKV>, g, b, 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
+                        hipStream_t s) {
+  const int H = p.d / p.hd;
+  if (p.hd == 64) {
+    hipLaunchKernelGGL(k_flash64, dim3((max_rows + 127) / 128, H, batch),
+                       dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
+  dim3 g((max_rows + 63) / 64, H, batch), b(64);
+  switch (p.hd) {
+    case 2: hipLaunchKernelGGL(k_flash_generic<2>, g, b, 0, s, p); break;
+    case 4: hipLaunchKernelGGL(k_flash_generic<4>, g, b, 0, s, p); break;
+    case 8: hipLaunchKernelGGL(k_flash_generic<8>, g, b, 0, s, p); break;
+    case 16: hipLaunchKernelGGL(k_flash_generic<16>, g, b, 0, s, p); break;
+    case 32: hipLaunchKernelGGL(k_flash_generic<32>, g, b, 0, s, p); break;
+    case 128: hipLaunchKernelGGL(k_flash_generic<128>, g, b, 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_rows_rmsnorm(const float* x, const float* w, float* out,
+                               int rows, int size, float eps, hipStream_t s) {
+  hipLaunchKernelGGL(k_rows_rmsnorm, dim3(rows), dim3(256), 0, s, x, w, out,
+                     size, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_embedding_rows(const uint32_t* tokens, const float* table,
+                                 float* out, int rows, int d, uint32_t vocab,
+                                 hipStream_t s) {
+  hipLaunchKernelGGL(k_embedding_rows, dim3(rows), dim3(256), 0, s, tokens,
+                     table, out, d, vocab);
+  return hipGetLastError();
+}
+
+}  // namespace akh

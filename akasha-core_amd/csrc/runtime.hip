@@ -42,6 +42,11 @@ akh_status fail(akh_status st, const std::string& msg) {
     if (!(cond)) return fail(AKH_E_INVALID, std::string(msg)); \
   } while (0)
 
+bool supported_head_dim(uint32_t hd) {
+  return hd == 2 || hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64 ||
+         hd == 128;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -54,11 +59,6 @@ struct akh_backend {
   hipStream_t stream = nullptr;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   bool capturing = false;
-  // Split-K workspace of the per-shader matmul launchers.
-  float* ws = nullptr;
-  size_t ws_floats = 0;
-  unsigned* cnt = nullptr;
-  size_t cnt_n = 0;
 };
 
 struct akh_graph {
@@ -86,12 +86,6 @@ extern "C" akh_status akh_backend_new(int device, akh_backend** out) {
   hipError_t e = hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreate(&be->t0);
   if (e == hipSuccess) e = hipEventCreate(&be->t1);
-  be->ws_floats = (size_t)4 << 20;  // 16 MiB
-  be->cnt_n = (size_t)1 << 16;
-  if (e == hipSuccess) e = hipMalloc(&be->ws, be->ws_floats * sizeof(float));
-  if (e == hipSuccess) e = hipMalloc(&be->cnt, be->cnt_n * sizeof(unsigned));
-  if (e == hipSuccess) e = hipMemset(be->cnt, 0, be->cnt_n * sizeof(unsigned));
-  if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     akh_backend_free(be);
     return fail(AKH_E_HIP, std::string("akh_backend_new: ") + hipGetErrorString(e));
@@ -104,8 +98,6 @@ extern "C" void akh_backend_free(akh_backend* be) {
   if (!be) return;
   hipSetDevice(be->device);
   if (be->stream) hipStreamSynchronize(be->stream);
-  if (be->ws) hipFree(be->ws);
-  if (be->cnt) hipFree(be->cnt);
   if (be->t0) hipEventDestroy(be->t0);
   if (be->t1) hipEventDestroy(be->t1);
   if (be->stream) hipStreamDestroy(be->stream);
@@ -221,34 +213,6 @@ extern "C" akh_status akh_timer_stop(akh_backend* be, float* ms) {
 }
 
 // ---------------------------------------------------------------------------
-// Launch planning
-// ---------------------------------------------------------------------------
-
-namespace {
-
-// K chunks of the skinny GEMM: aim for ~2 blocks per CU over the N tiles,
-// chunk a multiple of 64 rows.  Returns the effective number of chunks.
-int skinny_ksplit(int N, int K, int num_cus) {
-  const int ntiles = (N + 31) / 32;
-  int ks = (2 * num_cus + ntiles / 2) / ntiles;
-  ks = std::max(1, std::min(ks, std::max(1, K / 64)));
-  const int kc = (((K + ks - 1) / ks) + 63) & ~63;
-  return (K + kc - 1) / kc;
-}
-
-size_t skinny_ws_floats(int N, int ks) {
-  const int ntiles = (N + 31) / 32;
-  return ks > 1 ? (size_t)ntiles * ks * 32 * 32 : 0;
-}
-
-bool supported_head_dim(uint32_t hd) {
-  return hd == 2 || hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64 ||
-         hd == 128;
-}
-
-}  // namespace
-
-// ---------------------------------------------------------------------------
 // Per-shader launchers
 // ---------------------------------------------------------------------------
 
@@ -274,57 +238,24 @@ extern "C" akh_status akh_rmsnorm(akh_backend* be, const float* input,
   return AKH_OK;
 }
 
-static akh_status matmul_common(akh_backend* be, const float* a,
-                                const float* b, float* c,
-                                akh_matmul_meta shape,
-                                const akh_matmul_meta* meta, int epi) {
-  BE_CHECK(be);
-  CHECK_ARG(a && b && c && meta, "akh_matmul: NULL buffer");
-  if (shape.m == 0 || shape.n == 0) return AKH_OK;
-  if (shape.m <= (uint32_t)kMaxBatch) {
-    SkinnyParams p{};
-    p.x = a;
-    p.w = b;
-    p.y = c;
-    p.M = shape.m;
-    p.N = shape.n;
-    p.K = shape.k;
-    p.meta = meta;
-    int ks = skinny_ksplit(shape.n, shape.k, be->num_cus);
-    while (ks > 1 && skinny_ws_floats(shape.n, ks) > be->ws_floats) --ks;
-    const int ntiles = (shape.n + 31) / 32;
-    CHECK_ARG(ks == 1 || (size_t)ntiles <= be->cnt_n, "akh_matmul: n too large");
-    p.ksplit = ks;
-    p.ws = be->ws;
-    p.cnt = be->cnt;
-    HIP_TRY(launch_skinny(p, epi, false, ntiles, be->stream));
-  } else {
-    GemmParams p{};
-    p.a = a;
-    p.b = b;
-    p.c = c;
-    p.M = shape.m;
-    p.N = shape.n;
-    p.K = shape.k;
-    p.meta = meta;
-    HIP_TRY(launch_gemm(p, epi, (shape.n + 127) / 128, (shape.m + 127) / 128,
-                        be->stream));
-  }
-  return AKH_OK;
-}
-
 extern "C" akh_status akh_matmul(akh_backend* be, const float* a,
                                  const float* b, float* c,
                                  akh_matmul_meta shape,
                                  const akh_matmul_meta* meta) {
-  return matmul_common(be, a, b, c, shape, meta, EPI_STORE);
+  BE_CHECK(be);
+  CHECK_ARG(a && b && c && meta, "akh_matmul: NULL buffer");
+  HIP_TRY(shader_matmul(a, b, c, shape, meta, 0, be->stream));
+  return AKH_OK;
 }
 
 extern "C" akh_status akh_matmul_add(akh_backend* be, const float* a,
                                      const float* b, float* c,
                                      akh_matmul_meta shape,
                                      const akh_matmul_meta* meta) {
-  return matmul_common(be, a, b, c, shape, meta, EPI_ADD);
+  BE_CHECK(be);
+  CHECK_ARG(a && b && c && meta, "akh_matmul_add: NULL buffer");
+  HIP_TRY(shader_matmul(a, b, c, shape, meta, 1, be->stream));
+  return AKH_OK;
 }
 
 extern "C" akh_status akh_head_gather(akh_backend* be, const float* src,
@@ -386,20 +317,7 @@ extern "C" akh_status akh_flash_attention(akh_backend* be, const float* q,
             "flash_attention: dim must be divisible by head_dim");
   CHECK_ARG(supported_head_dim(shape.head_dim),
             "flash_attention: head_dim must be a power of two");
-  if (shape.seq_len == 0) return AKH_OK;
-  FlashParams p{};
-  p.q = q;
-  p.k = k;
-  p.v = v;
-  p.o = out;
-  p.lse = l_cache;
-  p.S = shape.seq_len;
-  p.d = shape.dim;
-  p.hd = shape.head_dim;
-  p.H = shape.dim / shape.head_dim;
-  p.scale = shape.scale;
-  p.meta = meta;
-  HIP_TRY(launch_flash(p, 1, shape.seq_len, be->stream));
+  HIP_TRY(shader_flash_attention(q, k, v, out, l_cache, shape, meta, be->stream));
   return AKH_OK;
 }
 
@@ -460,7 +378,7 @@ extern "C" akh_status akh_argmax_rows(akh_backend* be, const float* logits,
 struct akh_model {
   akh_backend* be = nullptr;
   akh_model_config cfg{};
-  std::vector<float*> params;   // ModelWeights::params() order
+  std::vector<float*> params;  // ModelWeights::params() order
   std::vector<size_t> counts;
 
   float* embedding() const { return params[0]; }
@@ -553,19 +471,19 @@ struct akh_session {
   float* kv = nullptr;
   float2* rope = nullptr;  // [max_ctx, head_dim / 2] (cos, sin)
 
-  // Decode-step buffers (32 rows: the MFMA tile height).
-  float *x = nullptr, *q = nullptr, *attn = nullptr, *ffn = nullptr;
-  float *logits = nullptr, *ss1 = nullptr, *ss2 = nullptr;
-  uint2* amax = nullptr;
-  uint32_t* tok = nullptr;
-  int* pos = nullptr;
-  uint32_t* hist = nullptr;  // [B, max_ctx + 1] greedy tokens by position
-  float* ws = nullptr;
-  unsigned* cnt = nullptr;
+  // Decode-step state, 32 rows (the MFMA tile height).  *_t buffers are in
+  // the k-quad layout [K/4][32][4].
+  float* xt = nullptr;      // residual stream
+  float* q = nullptr;       // [32, dim] post-RoPE queries
+  float* attn_t = nullptr;  // attention output
+  float* ffn_t = nullptr;   // silu(ffn_up)
+  float* logits = nullptr;  // [32, vocab]
+  uint2* amax = nullptr;    // [32, vocab / 32] argmax partials
+  uint32_t* tok = nullptr;  // tokens fed to the next step
+  int* pos = nullptr;       // per-sequence position of the next token
+  uint32_t* hist = nullptr; // [B, max_ctx + 1] token at each position
 
-  // Launch plan.
-  int ks_qkv = 1, ks_out = 1, ks_up = 1, ks_down = 1, ks_lm = 1;
-  int attn_split = 1;
+  int ks_out = 1, ks_down = 1;  // K split of the residual GEMMs
 
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -585,6 +503,16 @@ struct akh_session {
 };
 
 namespace {
+
+// K split of a residual decode GEMM: about two blocks per CU over the N
+// tiles, chunks a multiple of 64 rows (16 per wave of the 4-wave kernel).
+int residual_ksplit(int N, int K, int num_cus) {
+  const int ntiles = (N + 31) / 32;
+  int ks = (2 * num_cus + ntiles / 2) / ntiles;
+  ks = std::max(1, std::min(ks, std::max(1, K / 64)));
+  const int kc = (((K + ks - 1) / ks) + 63) / 64 * 64;
+  return (K + kc - 1) / kc;
+}
 
 void free_prefill(akh_session* s) {
   for (float* p : {s->px, s->pxn, s->pq, s->pattn, s->pffn})
@@ -618,26 +546,22 @@ akh_status upload_positions(akh_session* s) {
   return AKH_OK;
 }
 
-SkinnyParams skinny_base(akh_session* s) {
-  SkinnyParams p{};
+DecGemmParams dec_base(akh_session* s) {
+  DecGemmParams p{};
   p.M = (int)s->B;
-  p.ws = s->ws;
-  p.cnt = s->cnt;
   p.eps = s->m->cfg.norm_eps;
-  p.ss_slots = (int)(s->m->cfg.dim / kSlotW);
   return p;
 }
 
-// One decode-step kernel, addressed by `which` (see enqueue_decode).
+// norm_1 + fused QKV projection + RoPE + KV append (inference_graphs.rs:
+// 363-426): one kernel.
 hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
-  SkinnyParams p = skinny_base(s);
-  p.x = s->x;
+  DecGemmParams p = dec_base(s);
+  p.xt = s->xt;
   p.w = s->m->layer(l, W_QKV);
   p.N = 3 * c.dim;
   p.K = c.dim;
-  p.ksplit = s->ks_qkv;
-  p.ss_in = s->ss1;
   p.gain = s->m->layer(l, W_NORM1);
   p.q_out = s->q;
   p.kcache = s->kcache(l);
@@ -647,96 +571,88 @@ hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
   p.rope = s->rope;
   p.dim = c.dim;
   p.head_dim = c.dim / c.num_heads;
-  return launch_skinny(p, EPI_QKV, true, (p.N + 31) / 32, s->be->stream);
+  return launch_dec_gemm(p, DEC_QKV, true, 1, s->be->stream);
 }
 
+// attn_qk_cached + softmax_rect + attn_av_cached (inference_graphs.rs:
+// 428-456): one kernel.
 hipError_t enqueue_attn(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
-  DecodeAttnParams p{};
+  DecAttnParams p{};
   p.q = s->q;
   p.kc = s->kcache(l);
   p.vc = s->vcache(l);
-  p.out = s->attn;
+  p.out_t = s->attn_t;
   p.pos = s->pos;
-  p.ws = s->ws;
-  p.cnt = s->cnt;
   p.seq_stride = s->seq_stride();
-  p.B = (int)s->B;
   p.H = (int)c.num_heads;
   p.d = (int)c.dim;
-  p.nsplit = s->attn_split;
   const uint32_t hd = c.dim / c.num_heads;
   p.scale = 1.0f / sqrtf((float)hd);
-  return launch_decode_attn(p, (int)hd, s->be->stream);
+  return launch_dec_attn(p, (int)s->B, (int)hd, s->be->stream);
 }
 
+// out_proj + residual (inference_graphs.rs:458-470).
 hipError_t enqueue_out(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
-  SkinnyParams p = skinny_base(s);
-  p.x = s->attn;
+  DecGemmParams p = dec_base(s);
+  p.xt = s->attn_t;
   p.w = s->m->layer(l, W_OUT);
-  p.y = s->x;
+  p.yt = s->xt;
   p.N = c.dim;
   p.K = c.dim;
-  p.ksplit = s->ks_out;
-  p.ss_out = s->ss2;
-  return launch_skinny(p, EPI_ADD, false, (p.N + 31) / 32, s->be->stream);
+  return launch_dec_gemm(p, DEC_RESID, false, s->ks_out, s->be->stream);
 }
 
+// norm_2 + ffn_up + SiLU (inference_graphs.rs:472-495).
 hipError_t enqueue_up(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
-  SkinnyParams p = skinny_base(s);
-  p.x = s->x;
+  DecGemmParams p = dec_base(s);
+  p.xt = s->xt;
   p.w = s->m->layer(l, W_UP);
-  p.y = s->ffn;
+  p.yt = s->ffn_t;
   p.N = c.ffn_hidden;
   p.K = c.dim;
-  p.ksplit = s->ks_up;
-  p.ss_in = s->ss2;
   p.gain = s->m->layer(l, W_NORM2);
-  return launch_skinny(p, EPI_SILU, true, (p.N + 31) / 32, s->be->stream);
+  return launch_dec_gemm(p, DEC_SILU_T, true, 1, s->be->stream);
 }
 
+// ffn_down + residual (inference_graphs.rs:497-508).
 hipError_t enqueue_down(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
-  SkinnyParams p = skinny_base(s);
-  p.x = s->ffn;
+  DecGemmParams p = dec_base(s);
+  p.xt = s->ffn_t;
   p.w = s->m->layer(l, W_DOWN);
-  p.y = s->x;
+  p.yt = s->xt;
   p.N = c.dim;
   p.K = c.ffn_hidden;
-  p.ksplit = s->ks_down;
-  p.ss_out = s->ss1;
-  return launch_skinny(p, EPI_ADD, false, (p.N + 31) / 32, s->be->stream);
+  return launch_dec_gemm(p, DEC_RESID, false, s->ks_down, s->be->stream);
 }
 
+// final_norm + lm_head + per-tile argmax (inference.rs:228-252).
 hipError_t enqueue_lm_head(akh_session* s) {
   const akh_model_config& c = s->m->cfg;
-  SkinnyParams p = skinny_base(s);
-  p.x = s->x;
+  DecGemmParams p = dec_base(s);
+  p.xt = s->xt;
   p.w = s->m->lm_head();
   p.y = s->logits;
+  p.amax = s->amax;
   p.N = c.vocab_size;
   p.K = c.dim;
-  p.ksplit = s->ks_lm;
-  p.ss_in = s->ss1;
   p.gain = s->m->final_norm();
-  p.amax = s->amax;
-  return launch_skinny(p, EPI_LOGITS, true, (p.N + 31) / 32, s->be->stream);
+  return launch_dec_gemm(p, DEC_LOGITS, true, 1, s->be->stream);
 }
 
-// The decode step of build_decode_layer (inference_graphs.rs:339-509) for
-// all sequences: 5 kernels per layer.  RMSNorm runs inside the consumer
-// GEMM (statistics carried as slot partials), RoPE + cache append inside
-// the QKV GEMM epilogue, SiLU inside ffn_up's, the residual adds inside
-// out_proj's and ffn_down's; lm_head emits argmax partials and the last
-// kernel picks the greedy token and advances every position.
+// One decode step of build_decode_layer (inference_graphs.rs:339-509) for
+// every sequence: embedding, 5 kernels per layer, lm_head, greedy argmax +
+// position advance.  Reads tok/pos from the device, so it can be replayed
+// step after step with no host work.
 hipError_t enqueue_decode(akh_session* s) {
   const akh_model_config& c = s->m->cfg;
   hipStream_t st = s->be->stream;
-  hipError_t e = launch_gather_rows(s->m->embedding(), s->tok, c.vocab_size,
-                                    nullptr, 0, 0, s->x, (int)s->B,
-                                    (int)c.dim, s->ss1, st);
+  hipError_t e = launch_rows_to_kq(s->m->embedding(), s->tok, c.vocab_size,
+                                   nullptr, 0, 0, s->xt, (int)s->B,
+                                   (int)c.dim, st);
   for (uint32_t l = 0; l < c.num_layers && e == hipSuccess; ++l) {
     e = enqueue_qkv(s, l);
     if (e == hipSuccess) e = enqueue_attn(s, l);
@@ -799,9 +715,8 @@ extern "C" void akh_session_free(akh_session* s) {
   if (s->gexec) hipGraphExecDestroy(s->gexec);
   if (s->graph) hipGraphDestroy(s->graph);
   free_prefill(s);
-  void* bufs[] = {s->kv,   s->rope, s->x,   s->q,    s->attn, s->ffn,
-                  s->logits, s->ss1, s->ss2, s->amax, s->tok,  s->pos,
-                  s->hist, s->ws,   s->cnt};
+  void* bufs[] = {s->kv,     s->rope, s->xt,  s->q,   s->attn_t, s->ffn_t,
+                  s->logits, s->amax, s->tok, s->pos, s->hist};
   for (void* p : bufs)
     if (p) hipFree(p);
   delete s;
@@ -818,8 +733,9 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   const uint32_t hd = c.dim / c.num_heads;
   CHECK_ARG(supported_head_dim(hd) && hd >= 4,
             "akh_session_new: head_dim must be a power of two in 4..128");
-  CHECK_ARG(c.dim % kSlotW == 0, "akh_session_new: dim must be a multiple of 32");
-  CHECK_ARG(c.ffn_hidden % 4 == 0, "akh_session_new: ffn_hidden % 4 != 0");
+  CHECK_ARG(c.dim % 32 == 0, "akh_session_new: dim must be a multiple of 32");
+  CHECK_ARG(c.ffn_hidden % 32 == 0,
+            "akh_session_new: ffn_hidden must be a multiple of 32");
 
   akh_session* s = new akh_session();
   s->m = m;
@@ -828,30 +744,8 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   s->B = batch;
   s->cur_len.assign(batch, 0);
   const int cus = s->be->num_cus;
-  s->ks_qkv = skinny_ksplit(3 * c.dim, c.dim, cus);
-  s->ks_out = skinny_ksplit(c.dim, c.dim, cus);
-  s->ks_up = skinny_ksplit(c.ffn_hidden, c.dim, cus);
-  s->ks_down = skinny_ksplit(c.dim, c.ffn_hidden, cus);
-  s->ks_lm = skinny_ksplit(c.vocab_size, c.dim, cus);
-  // Attention: ~6 blocks per CU, chunks of at most 1024 rows.
-  {
-    const int bh = (int)(batch * c.num_heads);
-    int ns = (6 * cus + bh - 1) / bh;
-    ns = std::min(ns, std::max(1, (int)(max_context_len / 32)));
-    ns = std::max(ns, (int)((max_context_len + 1023) / 1024));
-    s->attn_split = std::max(1, ns);
-  }
-  size_t ws = 0;
-  ws = std::max(ws, skinny_ws_floats(3 * c.dim, s->ks_qkv));
-  ws = std::max(ws, skinny_ws_floats(c.dim, s->ks_out));
-  ws = std::max(ws, skinny_ws_floats(c.ffn_hidden, s->ks_up));
-  ws = std::max(ws, skinny_ws_floats(c.dim, s->ks_down));
-  ws = std::max(ws, skinny_ws_floats(c.vocab_size, s->ks_lm));
-  ws = std::max(ws, (size_t)batch * c.num_heads * s->attn_split * (hd + 4));
-  size_t ncnt = std::max<size_t>((c.vocab_size + 31) / 32,
-                                 (size_t)batch * c.num_heads);
-  ncnt = std::max<size_t>(ncnt, (3 * c.dim + 31) / 32);
-  ncnt = std::max<size_t>(ncnt, (c.ffn_hidden + 31) / 32);
+  s->ks_out = residual_ksplit(c.dim, c.dim, cus);
+  s->ks_down = residual_ksplit(c.dim, c.ffn_hidden, cus);
 
   const size_t d = c.dim, V = c.vocab_size, F = c.ffn_hidden, R = kMaxBatch;
   const size_t ntl = (V + 31) / 32;
@@ -862,19 +756,15 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   };
   alloc((void**)&s->kv, (size_t)c.num_layers * 2 * batch * max_context_len * d * 4);
   alloc((void**)&s->rope, (size_t)max_context_len * (hd / 2) * sizeof(float2));
-  alloc((void**)&s->x, R * d * 4);
+  alloc((void**)&s->xt, R * d * 4);
   alloc((void**)&s->q, R * d * 4);
-  alloc((void**)&s->attn, R * d * 4);
-  alloc((void**)&s->ffn, R * F * 4);
+  alloc((void**)&s->attn_t, R * d * 4);
+  alloc((void**)&s->ffn_t, R * F * 4);
   alloc((void**)&s->logits, R * V * 4);
-  alloc((void**)&s->ss1, R * (d / kSlotW) * 4);
-  alloc((void**)&s->ss2, R * (d / kSlotW) * 4);
   alloc((void**)&s->amax, R * ntl * sizeof(uint2));
   alloc((void**)&s->tok, R * 4);
   alloc((void**)&s->pos, R * 4);
   alloc((void**)&s->hist, (size_t)batch * (max_context_len + 1) * 4);
-  alloc((void**)&s->ws, std::max<size_t>(ws, 1) * 4);
-  alloc((void**)&s->cnt, ncnt * 4);
   if (e == hipSuccess) {
     // RoPE table in f32 exactly as src/shaders/cpu.rs:98-100 forms it:
     // freq = 1 / 10000^(2i / head_dim), angle = pos * freq, then sin/cos.
@@ -955,7 +845,6 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
 
   HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
                                 (int)d, c.vocab_size, st));
-  const int gm = (int)((rows + 127) / 128);
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     HIP_TRY(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM1), s->pxn,
                                 (int)rows, (int)d, c.norm_eps, st));
@@ -973,7 +862,7 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     g.rope = s->rope;
     g.dim = d;
     g.head_dim = hd;
-    HIP_TRY(launch_gemm(g, EPI_QKV, (g.N + 127) / 128, gm, st));
+    HIP_TRY(launch_gemm(g, GEMM_QKV, st));
 
     FlashParams f{};
     f.q = s->pq;
@@ -986,7 +875,6 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     f.S = (int)S;
     f.d = (int)d;
     f.hd = (int)hd;
-    f.H = (int)c.num_heads;
     f.scale = 1.0f / sqrtf((float)hd);
     HIP_TRY(launch_flash(f, (int)s->B, (int)S, st));
 
@@ -997,7 +885,7 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     o.M = (int)rows;
     o.N = d;
     o.K = d;
-    HIP_TRY(launch_gemm(o, EPI_ADD, (d + 127) / 128, gm, st));
+    HIP_TRY(launch_gemm(o, GEMM_ADD, st));
 
     HIP_TRY(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM2), s->pxn,
                                 (int)rows, (int)d, c.norm_eps, st));
@@ -1008,7 +896,7 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     u.M = (int)rows;
     u.N = c.ffn_hidden;
     u.K = d;
-    HIP_TRY(launch_gemm(u, EPI_SILU, (u.N + 127) / 128, gm, st));
+    HIP_TRY(launch_gemm(u, GEMM_SILU, st));
 
     GemmParams w{};
     w.a = s->pffn;
@@ -1017,12 +905,12 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     w.M = (int)rows;
     w.N = d;
     w.K = c.ffn_hidden;
-    HIP_TRY(launch_gemm(w, EPI_ADD, (d + 127) / 128, gm, st));
+    HIP_TRY(launch_gemm(w, GEMM_ADD, st));
   }
-  // Last row of every sequence -> final RMSNorm (in the lm_head prologue)
-  // -> lm_head -> greedy token (inference.rs:120-168).
-  HIP_TRY(launch_gather_rows(nullptr, nullptr, 0, s->px, (long)S - 1, (long)S,
-                             s->x, (int)s->B, (int)d, s->ss1, st));
+  // Last row of every sequence -> final RMSNorm (folded into lm_head) ->
+  // lm_head -> greedy token (inference.rs:120-168).
+  HIP_TRY(launch_rows_to_kq(nullptr, nullptr, 0, s->px, (long)S - 1, (long)S,
+                            s->xt, (int)s->B, (int)d, st));
   HIP_TRY(enqueue_lm_head(s));
   HIP_TRY(launch_argmax_final(s->amax, (int)((c.vocab_size + 31) / 32),
                               (int)s->B, s->tok, nullptr, s->hist,

@@ -1,0 +1,391 @@
+// Per-shader kernels: one per reference Shader / matmul builtin on the
+// inference path (src/shaders/mod.rs), with the reference's semantics and
+// the meta read from device memory when the kernel runs, so a captured graph
+// follows metas rewritten between replays.  The launch is sized from the
+// build-time shape and the live meta bounds the work, as in the reference
+// (ARCHITECTURE.md "live metas").
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace akh {
+
+namespace {
+
+unsigned grid1d(size_t n, unsigned block) {
+  size_t g = (n + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > 65535u * 16u) g = 65535u * 16u;
+  return (unsigned)g;
+}
+
+}  // namespace
+
+// EMBEDDING (src/shaders/cpu.rs:25-41): ids >= vocab give a zero row.
+__global__ void k_embedding(const uint32_t* tokens, const float* table,
+                            float* out, const akh_embedding_meta* meta) {
+  const uint32_t vocab = meta->vocab_size, dim = meta->dim;
+  const uint32_t t = blockIdx.y;
+  if (t >= meta->seq_len) return;
+  const uint32_t id = tokens[t];
+  for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c < dim;
+       c += gridDim.x * blockDim.x)
+    out[(size_t)t * dim + c] = id < vocab ? table[(size_t)id * dim + c] : 0.f;
+}
+
+// RMSNORM (src/shaders/cpu.rs:205-222), one 256-thread block per row:
+// y = x * (1 / sqrt(sum(x^2) / size + eps)) * w.
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* x,
+                                                 const float* w, float* out,
+                                                 const akh_norm_meta* meta) {
+  __shared__ float red4[4];
+  const uint32_t r = blockIdx.x;
+  if (r >= meta->seq_len) return;
+  const uint32_t size = meta->size;
+  const float* xr = x + (size_t)r * size;
+  float ss = 0.f;
+  for (uint32_t c = threadIdx.x; c < size; c += 256) ss += xr[c] * xr[c];
+  ss = block_sum256(ss, red4);
+  const float rs = 1.0f / sqrtf(ss / (float)size + meta->eps);
+  for (uint32_t c = threadIdx.x; c < size; c += 256)
+    out[(size_t)r * size + c] = __fmul_rn(__fmul_rn(xr[c], rs), w[c]);
+}
+
+// MATMUL / GEMV and MATMUL_ADD / GEMV_ADD for m <= 32 (the reference routes
+// m == 1 to GEMV, emit.rs:31-33): C[m, n] (+)= A[m, k] B[k, n].
+//
+// One 256-thread block per 32-column tile of C, whole K.  Row-major A is
+// staged through LDS 256 k at a time in the k-quad layout, so every MFMA
+// A operand is one conflict-free LDS read per four k; the four waves split
+// each staged piece and their partial tiles are reduced in LDS.
+__global__ __launch_bounds__(256) void k_shader_skinny(
+    const float* a, const float* b, float* c, const akh_matmul_meta* meta,
+    int accumulate) {
+  constexpr int KP = 256;  // k per staged piece
+  __shared__ float4 xs[KP / 4][32];
+  __shared__ float red[2][32][33];
+  const int M = (int)meta->m, N = (int)meta->n, K = (int)meta->k;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * 32;
+  if (n0 >= N || M <= 0) return;
+  const int ncol = n0 + j;
+  const bool col_ok = ncol < N;
+  const bool a_vec = (K & 3) == 0;
+  f32x16 acc = zero16();
+
+  for (int kp0 = 0; kp0 < K; kp0 += KP) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 32 * (KP / 4); idx += 256) {
+      const int m = idx / (KP / 4), q = idx % (KP / 4);
+      const int k = kp0 + 4 * q;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (m < M) {
+        const float* ar = a + (size_t)m * K;
+        if (a_vec && k + 3 < K) {
+          v = *reinterpret_cast<const float4*>(ar + k);
+        } else {
+          if (k < K) v.x = ar[k];
+          if (k + 1 < K) v.y = ar[k + 1];
+          if (k + 2 < K) v.z = ar[k + 2];
+          if (k + 3 < K) v.w = ar[k + 3];
+        }
+      }
+      xs[q][m] = v;
+    }
+    __syncthreads();
+    // Wave w takes k-quads [16w, 16w + 16) of the piece; half h the first
+    // or second 8 of them.
+    const int qb = wave * 16 + h * 8;
+#pragma unroll
+    for (int g = 0; g < 8; g += 2) {
+      float wv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = kp0 + 4 * (qb + g) + u;
+        wv[u] = (k < K && col_ok) ? b[(size_t)k * N + ncol] : 0.f;
+      }
+      const float4 x0 = xs[qb + g][j], x1 = xs[qb + g + 1][j];
+      acc = mfma32(x0.x, wv[0], acc);
+      acc = mfma32(x0.y, wv[1], acc);
+      acc = mfma32(x0.z, wv[2], acc);
+      acc = mfma32(x0.w, wv[3], acc);
+      acc = mfma32(x1.x, wv[4], acc);
+      acc = mfma32(x1.y, wv[5], acc);
+      acc = mfma32(x1.z, wv[6], acc);
+      acc = mfma32(x1.w, wv[7], acc);
+    }
+  }
+  // Tree reduction of the four waves' tiles: (2,3) -> (0,1), then 1 -> 0.
+  for (int half = 2; half >= 1; half >>= 1) {
+    __syncthreads();
+    if (wave >= half && wave < 2 * half)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[wave - half][acc_row(r, h)][j] = acc[r];
+    __syncthreads();
+    if (wave < half)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += red[wave][acc_row(r, h)][j];
+  }
+  if (wave != 0 || !col_ok) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = acc_row(r, h);
+    if (m < M) {
+      float* y = c + (size_t)m * N + ncol;
+      *y = accumulate ? *y + acc[r] : acc[r];
+    }
+  }
+}
+
+// HEAD_GATHER (src/shaders/cpu.rs:238-255).
+__global__ void k_head_gather(const float* src, float* dst,
+                              const akh_head_move_meta* meta) {
+  const uint32_t rows = meta->seq_len, full = meta->full_dim,
+                 hd = meta->head_dim, off = meta->head_offset;
+  const size_t total = (size_t)rows * hd;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = i / hd, c = i % hd;
+    dst[i] = src[r * full + off + c];
+  }
+}
+
+// ROPE / ROPE_OFFSET (src/shaders/cpu.rs:84-142): in place, pairs
+// (2i, 2i+1) of each head rotated by pos * 10000^(-2i/head_dim), position =
+// row (+ meta pos for ROPE_OFFSET).
+__global__ void k_rope(float* x, const uint32_t* meta, int with_offset) {
+  const uint32_t rows = meta[0], dim = meta[1], hd = meta[2];
+  const uint32_t pos0 = with_offset ? meta[3] : 0u;
+  const size_t pairs = (size_t)rows * (dim / 2);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < pairs;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t t = (uint32_t)(i / (dim / 2));
+    const uint32_t c = (uint32_t)(i % (dim / 2)) * 2u;
+    const uint32_t di = c % hd;
+    const float freq = 1.0f / powf(10000.0f, (float)di / (float)hd);
+    const float angle = (float)(t + pos0) * freq;
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    float* p = x + (size_t)t * dim + c;
+    float x0 = p[0], x1 = p[1];
+    rope_pair(x0, x1, cs, sn);
+    p[0] = x0;
+    p[1] = x1;
+  }
+}
+
+// CACHE_WRITE (src/shaders/cpu.rs:224-236).
+__global__ void k_cache_write(const float* src, float* dst,
+                              const akh_cache_write_meta* meta) {
+  const uint32_t rows = meta->row_count, width = meta->width,
+                 off = meta->dst_row_offset;
+  const size_t total = (size_t)rows * width;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[(size_t)off * width + i] = src[i];
+}
+
+// ATTN_QK_CACHED (src/shaders/cpu.rs:144-162): one thread per (row, head).
+__global__ void k_attn_qk_cached(const float* q, const float* kc,
+                                 float* scores,
+                                 const akh_attn_cached_meta* meta) {
+  const uint32_t len = meta->attn_len, dim = meta->dim, hd = meta->head_dim;
+  const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x, h = blockIdx.y;
+  if (j >= len || h >= dim / hd) return;
+  const float* qh = q + h * hd;
+  const float* kr = kc + (size_t)j * dim + h * hd;
+  float s = 0.f;
+  for (uint32_t c = 0; c < hd; ++c) s += qh[c] * kr[c];
+  scores[(size_t)h * len + j] = s;
+}
+
+// SOFTMAX_RECT (src/shaders/cpu.rs:180-203), one block per row.
+__global__ __launch_bounds__(256) void k_softmax_rect(
+    float* x, const akh_softmax_rect_meta* meta) {
+  __shared__ float red4[4];
+  const uint32_t r = blockIdx.x;
+  if (r >= meta->num_rows) return;
+  const uint32_t width = meta->width;
+  const float scale = meta->scale;
+  float* row = x + (size_t)r * width;
+  float mx = -INFINITY;
+  for (uint32_t i = threadIdx.x; i < width; i += 256)
+    mx = fmaxf(mx, row[i] * scale);
+  mx = block_max256(mx, red4);
+  float sum = 0.f;
+  for (uint32_t i = threadIdx.x; i < width; i += 256) {
+    const float e = expf(row[i] * scale - mx);
+    row[i] = e;
+    sum += e;
+  }
+  sum = block_sum256(sum, red4);
+  for (uint32_t i = threadIdx.x; i < width; i += 256) row[i] = row[i] / sum;
+}
+
+// ATTN_AV_CACHED (src/shaders/cpu.rs:164-178): one thread per channel.
+__global__ void k_attn_av_cached(const float* p, const float* vc, float* out,
+                                 const akh_attn_cached_meta* meta) {
+  const uint32_t len = meta->attn_len, dim = meta->dim, hd = meta->head_dim;
+  const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= dim) return;
+  const float* ph = p + (size_t)(d / hd) * len;
+  float s = 0.f;
+  for (uint32_t j = 0; j < len; ++j) s += ph[j] * vc[(size_t)j * dim + d];
+  out[d] = s;
+}
+
+// SILU (src/shaders/cpu.rs:63-69).
+__global__ void k_silu(float* x, uint32_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const float v = x[i];
+    x[i] = v / (1.0f + expf(-v));
+  }
+}
+
+// Greedy argmax of each row (sampling.rs:83-91).
+__global__ __launch_bounds__(256) void k_argmax_rows(const float* logits,
+                                                     uint32_t n,
+                                                     uint32_t* out) {
+  const float* row = logits + (size_t)blockIdx.x * n;
+  float bv = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  for (uint32_t i = threadIdx.x; i < n; i += 256) amax_merge(bv, bi, row[i], i);
+  block_amax256(bv, bi);
+  if (threadIdx.x == 0) out[blockIdx.x] = bi == 0xFFFFFFFFu ? 0u : bi;
+}
+
+// ---------------------------------------------------------------------------
+
+hipError_t shader_embedding(const uint32_t* tokens, const float* table,
+                            float* out, akh_embedding_meta shape,
+                            const akh_embedding_meta* meta, hipStream_t s) {
+  if (shape.seq_len == 0 || shape.dim == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_embedding, dim3((shape.dim + 255) / 256, shape.seq_len),
+                     dim3(256), 0, s, tokens, table, out, meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_rmsnorm(const float* x, const float* w, float* out,
+                          akh_norm_meta shape, const akh_norm_meta* meta,
+                          hipStream_t s) {
+  if (shape.seq_len == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rmsnorm, dim3(shape.seq_len), dim3(256), 0, s, x, w,
+                     out, meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_matmul(const float* a, const float* b, float* c,
+                         akh_matmul_meta shape, const akh_matmul_meta* meta,
+                         int accumulate, hipStream_t s) {
+  if (shape.m == 0 || shape.n == 0) return hipSuccess;
+  if (shape.m <= (uint32_t)kMaxBatch) {
+    hipLaunchKernelGGL(k_shader_skinny, dim3((shape.n + 31) / 32), dim3(256),
+                       0, s, a, b, c, meta, accumulate);
+    return hipGetLastError();
+  }
+  GemmParams p{};
+  p.a = a;
+  p.b = b;
+  p.c = c;
+  p.M = shape.m;
+  p.N = shape.n;
+  p.K = shape.k;
+  p.meta = meta;
+  return launch_gemm(p, accumulate ? GEMM_ADD : GEMM_STORE, s);
+}
+
+hipError_t shader_head_gather(const float* src, float* dst,
+                              akh_head_move_meta shape,
+                              const akh_head_move_meta* meta, hipStream_t s) {
+  hipLaunchKernelGGL(k_head_gather,
+                     dim3(grid1d((size_t)shape.seq_len * shape.head_dim, 256)),
+                     dim3(256), 0, s, src, dst, meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_rope(float* buf, uint32_t seq_len, uint32_t dim,
+                       const uint32_t* meta_u32, int with_offset,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(k_rope, dim3(grid1d((size_t)seq_len * (dim / 2), 256)),
+                     dim3(256), 0, s, buf, meta_u32, with_offset);
+  return hipGetLastError();
+}
+
+hipError_t shader_cache_write(const float* src, float* cache,
+                              akh_cache_write_meta shape,
+                              const akh_cache_write_meta* meta,
+                              hipStream_t s) {
+  hipLaunchKernelGGL(k_cache_write,
+                     dim3(grid1d((size_t)shape.row_count * shape.width, 256)),
+                     dim3(256), 0, s, src, cache, meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_flash_attention(const float* q, const float* k,
+                                  const float* v, float* out, float* lse,
+                                  akh_flash_attn_meta shape,
+                                  const akh_flash_attn_meta* meta,
+                                  hipStream_t s) {
+  if (shape.seq_len == 0) return hipSuccess;
+  FlashParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.o = out;
+  p.lse = lse;
+  p.S = shape.seq_len;
+  p.d = shape.dim;
+  p.hd = shape.head_dim;
+  p.scale = shape.scale;
+  p.meta = meta;
+  return launch_flash(p, 1, shape.seq_len, s);
+}
+
+hipError_t shader_attn_qk_cached(const float* q, const float* kc,
+                                 float* scores, uint32_t num_heads,
+                                 uint32_t max_attn_len,
+                                 const akh_attn_cached_meta* meta,
+                                 hipStream_t s) {
+  hipLaunchKernelGGL(k_attn_qk_cached,
+                     dim3((max_attn_len + 255) / 256, num_heads), dim3(256), 0,
+                     s, q, kc, scores, meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_softmax_rect(float* x, akh_softmax_rect_meta shape,
+                               const akh_softmax_rect_meta* meta,
+                               hipStream_t s) {
+  if (shape.num_rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_softmax_rect, dim3(shape.num_rows), dim3(256), 0, s, x,
+                     meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_attn_av_cached(const float* scores, const float* vc,
+                                 float* out, uint32_t dim,
+                                 const akh_attn_cached_meta* meta,
+                                 hipStream_t s) {
+  hipLaunchKernelGGL(k_attn_av_cached, dim3((dim + 255) / 256), dim3(256), 0,
+                     s, scores, vc, out, meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_silu(float* buf, uint32_t len, hipStream_t s) {
+  if (len == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_silu, dim3(grid1d(len, 256)), dim3(256), 0, s, buf,
+                     len);
+  return hipGetLastError();
+}
+
+hipError_t shader_argmax_rows(const float* logits, uint32_t rows, uint32_t n,
+                              uint32_t* out, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_argmax_rows, dim3(rows), dim3(256), 0, s, logits, n,
+                     out);
+  return hipGetLastError();
+}
+
+}  // namespace akh
