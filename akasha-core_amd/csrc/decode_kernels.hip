@@ -20,43 +20,72 @@ namespace akh {
 
 // Y[M, N] (epilogue) A[M, K] . W[K, N] for M <= 32.
 //
-// Grid (N / 32 tiles, ksplit), W waves per block.  The block's K chunk is
-// split over its waves, and within a wave half h of the lanes walks rows
-// kbase_h + s: lane (j, h) supplies A[j][k] (a float4 of the k-quad tile
-// covers four steps) and W[k][n0 + j] (a wave load covers two 128-byte row
-// segments), and v_mfma_f32_32x32x2f32 accumulates the 32x32 output tile.
-// The waves' tiles are reduced in LDS as a binary tree (fixed order) and
-// wave 0 runs the epilogue.
-template <int W, int EPI, bool NORM>
+// Grid (N tiles of NT = 32*C columns, ksplit), W waves per block.  A pass of
+// the block covers KC = 2*W*HL rows of K: wave w takes 2*HL of them and half
+// h of its lanes HL, lane (j, h) supplying A[j][k] (a float4 of the k-quad
+// tile covers four k) and W[k][n0 + C*j + c] for MFMA tile c, so a wave load
+// covers two row segments of 128*C contiguous bytes.  All of a pass's loads
+// are issued before its first MFMA, so each wave keeps HL weight rows in
+// flight.  The waves' tiles are reduced in LDS as a binary tree (fixed
+// order) and wave 0 runs the epilogue.
+template <int C, int W, int HL, int EPI, bool NORM>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
-  constexpr int U = 8;
+  constexpr int NT = 32 * C;
   constexpr int RH = W > 1 ? W / 2 : 1;
-  __shared__ float red[RH][32][33];
+  constexpr int KC = 2 * W * HL;
+  static_assert(HL % 4 == 0, "HL must cover whole k-quads");
+  __shared__ float red[RH][32][NT + 1];
   __shared__ float ssw[W][32];
   __shared__ float rs_s[32];
 
   const int M = p.M, N = p.N, K = p.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, h = lane >> 5;
-  const int tile = blockIdx.x, n0 = tile * 32;
-  constexpr int STEP = 16 * W;  // chunk granularity: 8 k per half-wave
-  const int kc = ((K + (int)gridDim.y - 1) / (int)gridDim.y + STEP - 1) / STEP * STEP;
-  const int kb = blockIdx.y * kc;
+  const int tile = blockIdx.x, n0 = tile * NT;
+  const int per = (K + (int)gridDim.y - 1) / (int)gridDim.y;
+  const int rows = (per + KC - 1) / KC * KC;  // whole passes per block
+  const int kb = blockIdx.y * rows;
   if (kb >= K) return;
-  const int ke = min(K, kb + kc);
-  const int kw = kc / W, hl = kw / 2;
-  const int kbase = kb + wave * kw + h * hl;
-  const int ncol = n0 + j;
-  const bool col_ok = ncol < N;
-
-  f32x16 acc = zero16();
-  float ss = 0.f;
-  for (int s0 = 0; s0 < hl; s0 += U) {
-    const int k0 = kbase + s0;
-    float a[U], wv[U];
+  const int ke = min(K, kb + rows);
+  const int ncol = n0 + C * j;
+  bool cok[C];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int kq = (k0 >> 2) + q;
+  for (int c = 0; c < C; ++c) cok[c] = ncol + c < N;
+  const bool vec = C > 1 && (N % C) == 0 && ncol + C <= N;
+
+  f32x16 acc[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) acc[c] = zero16();
+  float ss = 0.f;
+  for (int k0 = kb; k0 < ke; k0 += KC) {
+    const int kr = k0 + wave * 2 * HL + h * HL;  // first row of this half
+    float a[HL];
+    float wv[HL][C];
+#pragma unroll
+    for (int u = 0; u < HL; ++u) {
+      const int k = kr + u;
+      const bool ok = k < ke;
+      const float* wr = p.w + (size_t)(ok ? k : kb) * N + ncol;
+      if (C == 4 && vec) {
+        const float4 t = ok ? *reinterpret_cast<const float4*>(wr)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[u][0] = t.x;
+        wv[u][C > 1 ? 1 : 0] = t.y;
+        wv[u][C > 2 ? 2 : 0] = t.z;
+        wv[u][C > 3 ? 3 : 0] = t.w;
+      } else if (C == 2 && vec) {
+        const float2 t = ok ? *reinterpret_cast<const float2*>(wr)
+                            : make_float2(0.f, 0.f);
+        wv[u][0] = t.x;
+        wv[u][C > 1 ? 1 : 0] = t.y;
+      } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c) wv[u][c] = (ok && cok[c]) ? wr[c] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < HL / 4; ++q) {
+      const int kq = (kr >> 2) + q;
       float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
       if (4 * kq < ke)
         t = *reinterpret_cast<const float4*>(p.xt + ((size_t)kq * 32 + j) * 4);
@@ -65,16 +94,11 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
       a[4 * q + 2] = t.z;
       a[4 * q + 3] = t.w;
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = k0 + u;
-      wv[u] = (k < ke && col_ok) ? p.w[(size_t)k * N + ncol] : 0.f;
-    }
     if (NORM) {
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
+      for (int q = 0; q < HL / 4; ++q) {
         float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (k0 + 4 * q < ke) g = *reinterpret_cast<const float4*>(p.gain + k0 + 4 * q);
+        if (kr + 4 * q < ke) g = *reinterpret_cast<const float4*>(p.gain + kr + 4 * q);
         const float gg[4] = {g.x, g.y, g.z, g.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -85,7 +109,9 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc = mfma32(a[u], wv[u], acc);
+    for (int u = 0; u < HL; ++u)
+#pragma unroll
+      for (int c = 0; c < C; ++c) acc[c] = mfma32(a[u], wv[u][c], acc[c]);
   }
 
   if (W > 1) {
@@ -93,11 +119,17 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
       __syncthreads();
       if (wave >= half && wave < 2 * half)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[wave - half][acc_row(r, h)][j] = acc[r];
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            red[wave - half][acc_row(r, h)][C * j + c] = acc[c][r];
       __syncthreads();
       if (wave < half)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += red[wave][acc_row(r, h)][j];
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            acc[c][r] += red[wave][acc_row(r, h)][C * j + c];
     }
   }
   if (NORM) {
@@ -118,46 +150,58 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int m = acc_row(r, h);
-    float v = acc[r];
-    if (NORM) v = __fmul_rn(v, rs_s[m]);
+    float v[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) v[c] = NORM ? __fmul_rn(acc[c][r], rs_s[m]) : acc[c][r];
     if (EPI == DEC_RESID) {
-      if (m < M && col_ok) {
-        float* y = p.yt + kq_index(m, ncol);
-        if (gridDim.y > 1)
-          atomicAdd(y, v);
-        else
-          *y = *y + v;
-      }
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        if (m < M && cok[c]) {
+          float* y = p.yt + kq_index(m, ncol + c);
+          if (gridDim.y > 1)
+            atomicAdd(y, v[c]);
+          else
+            *y = *y + v[c];
+        }
     } else if (EPI == DEC_SILU_T) {
-      if (m < M && col_ok) p.yt[kq_index(m, ncol)] = v / (1.0f + expf(-v));
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        if (m < M && cok[c]) p.yt[kq_index(m, ncol + c)] = v[c] / (1.0f + expf(-v[c]));
     } else if (EPI == DEC_QKV) {
+      static_assert(EPI != DEC_QKV || C == 1, "QKV epilogue pairs lanes");
       // RoPE pairs (2i, 2i+1) sit in lanes j and j^1 of the same half.
-      const float partner = __shfl_xor(v, 1, 64);
-      if (m < M && col_ok) {
+      const float partner = __shfl_xor(v[0], 1, 64);
+      if (m < M && cok[0]) {
         const int dim = p.dim;
-        const int region = ncol / dim, c = ncol - region * dim;
+        const int region = ncol / dim, cc = ncol - region * dim;
         const int pos = p.pos[m];
-        float out = v;
+        float out = v[0];
         if (region < 2) {
-          const int i = (c % p.head_dim) >> 1;
+          const int i = (cc % p.head_dim) >> 1;
           const float2 cs = p.rope[(size_t)pos * (p.head_dim >> 1) + i];
           const bool odd = ncol & 1;
-          float x0 = odd ? partner : v, x1 = odd ? v : partner;
+          float x0 = odd ? partner : v[0], x1 = odd ? v[0] : partner;
           rope_pair(x0, x1, cs.x, cs.y);
           out = odd ? x1 : x0;
         }
         if (region == 0)
-          p.q_out[(size_t)m * dim + c] = out;
+          p.q_out[(size_t)m * dim + cc] = out;
         else
           (region == 1 ? p.kcache : p.vcache)[(size_t)m * p.seq_stride +
-                                              (size_t)pos * dim + c] = out;
+                                              (size_t)pos * dim + cc] = out;
       }
     } else if (EPI == DEC_LOGITS) {
-      const bool ok = m < M && col_ok;
-      if (ok) p.y[(size_t)m * N + ncol] = v;
-      // First maximum of the row over this tile's 32 columns.
-      float bv = ok ? v : -INFINITY;
+      // Logits, and the first maximum of the row over this tile's columns.
+      float bv = -INFINITY;
       uint32_t bi = (uint32_t)ncol;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const bool ok = m < M && cok[c];
+        if (ok) {
+          p.y[(size_t)m * N + ncol + c] = v[c];
+          amax_merge(bv, bi, v[c], (uint32_t)(ncol + c));
+        }
+      }
 #pragma unroll
       for (int o = 16; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);
@@ -165,7 +209,7 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
         amax_merge(bv, bi, ov, oi);
       }
       if (j == 0 && m < M) {
-        const int ntiles = (N + 31) / 32;
+        const int ntiles = (N + NT - 1) / NT;
         p.amax[(size_t)m * ntiles + tile] = make_uint2(__float_as_uint(bv), bi);
       }
     }
@@ -328,29 +372,38 @@ __global__ __launch_bounds__(256) void k_argmax_final(
 
 // ---------------------------------------------------------------------------
 
-template <int W, int EPI, bool NORM>
+template <int C, int W, int HL, int EPI, bool NORM>
 static hipError_t dec_go(const DecGemmParams& p, int ksplit, hipStream_t s) {
-  hipLaunchKernelGGL((k_dec_gemm<W, EPI, NORM>), dim3((p.N + 31) / 32, ksplit),
-                     dim3(64 * W), 0, s, p);
+  hipLaunchKernelGGL((k_dec_gemm<C, W, HL, EPI, NORM>),
+                     dim3((p.N + 32 * C - 1) / (32 * C), ksplit), dim3(64 * W), 0,
+                     s, p);
   return hipGetLastError();
 }
 
-hipError_t launch_dec_gemm(const DecGemmParams& p, int epi, bool norm,
-                           int ksplit, hipStream_t s) {
-  if (ksplit < 1 || (ksplit > 1 && (epi != DEC_RESID || norm)))
-    return hipErrorInvalidValue;
-  switch (epi) {
-    case DEC_RESID:
-      return norm ? hipErrorInvalidValue : dec_go<4, DEC_RESID, false>(p, ksplit, s);
-    case DEC_SILU_T:
-      return norm ? dec_go<8, DEC_SILU_T, true>(p, 1, s)
-                  : dec_go<8, DEC_SILU_T, false>(p, 1, s);
-    case DEC_QKV:
-      return norm ? dec_go<8, DEC_QKV, true>(p, 1, s)
-                  : dec_go<8, DEC_QKV, false>(p, 1, s);
-    case DEC_LOGITS:
-      return norm ? dec_go<4, DEC_LOGITS, true>(p, 1, s)
-                  : dec_go<4, DEC_LOGITS, false>(p, 1, s);
+// Launch shapes per role (N tile, waves, rows in flight per half-wave):
+//   QKV, UP    32 cols, 16 waves, 24 rows: one block per N tile owns the
+//              whole K = dim (needed by the folded RMSNorm);
+//   OUT, DOWN  32 cols,  4 waves, 16 rows: K split in chunks of 128 rows,
+//              partial tiles added atomically into the residual stream;
+//   LM         64 cols,  8 waves, 24 rows: whole K in two passes.
+int dec_gemm_rows_per_block(int cfg) {
+  switch (cfg) {
+    case DEC_CFG_QKV:
+    case DEC_CFG_UP: return 2 * 16 * 24;
+    case DEC_CFG_OUT:
+    case DEC_CFG_DOWN: return 2 * 4 * 16;
+    default: return 2 * 8 * 24;
+  }
+}
+
+hipError_t launch_dec_gemm(const DecGemmParams& p, int cfg, int ksplit,
+                           hipStream_t s) {
+  switch (cfg) {
+    case DEC_CFG_QKV: return dec_go<1, 16, 24, DEC_QKV, true>(p, 1, s);
+    case DEC_CFG_UP: return dec_go<1, 16, 24, DEC_SILU_T, true>(p, 1, s);
+    case DEC_CFG_OUT:
+    case DEC_CFG_DOWN: return dec_go<1, 4, 16, DEC_RESID, false>(p, ksplit, s);
+    case DEC_CFG_LM: return dec_go<2, 8, 24, DEC_LOGITS, true>(p, 1, s);
   }
   return hipErrorInvalidValue;
 }

@@ -148,9 +148,22 @@ struct DecAttnParams {
   float scale;
 };
 
-// ksplit > 1 only for DEC_RESID (partial tiles are added atomically).
-hipError_t launch_dec_gemm(const DecGemmParams& p, int epi, bool norm,
-                           int ksplit, hipStream_t s);
+// Roles of the decode GEMMs; each has its own launch shape.
+enum DecCfg : int {
+  DEC_CFG_QKV = 0,   // norm_1 + qkv_proj + RoPE + KV append (DEC_QKV)
+  DEC_CFG_OUT = 1,   // out_proj + residual (DEC_RESID, K split)
+  DEC_CFG_UP = 2,    // norm_2 + ffn_up + SiLU (DEC_SILU_T)
+  DEC_CFG_DOWN = 3,  // ffn_down + residual (DEC_RESID, K split)
+  DEC_CFG_LM = 4,    // final norm + lm_head + argmax partials (DEC_LOGITS)
+};
+// Columns of one lm_head tile (the argmax partials are per tile).
+constexpr int kLmTileCols = 64;
+// Rows of K one block of the role covers per pass; the residual roles split
+// K into ceil(K / rows) blocks.
+int dec_gemm_rows_per_block(int cfg);
+// ksplit > 1 only for the residual roles (partial tiles added atomically).
+hipError_t launch_dec_gemm(const DecGemmParams& p, int cfg, int ksplit,
+                           hipStream_t s);
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
                            hipStream_t s);
 // xt[:, m] = table[ids[m]] (zero row if ids[m] >= vocab), or, with ids null,

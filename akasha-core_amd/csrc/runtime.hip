@@ -504,14 +504,14 @@ struct akh_session {
 
 namespace {
 
-// K split of a residual decode GEMM: about two blocks per CU over the N
-// tiles, chunks a multiple of 64 rows (16 per wave of the 4-wave kernel).
-int residual_ksplit(int N, int K, int num_cus) {
-  const int ntiles = (N + 31) / 32;
-  int ks = (2 * num_cus + ntiles / 2) / ntiles;
-  ks = std::max(1, std::min(ks, std::max(1, K / 64)));
-  const int kc = (((K + ks - 1) / ks) + 63) / 64 * 64;
-  return (K + kc - 1) / kc;
+// K split of a residual decode GEMM: one block per pass of its role.
+int residual_ksplit(int cfg, int K) {
+  const int rows = dec_gemm_rows_per_block(cfg);
+  return std::max(1, (K + rows - 1) / rows);
+}
+
+int lm_tiles(const akh_model_config& c) {
+  return (int)((c.vocab_size + kLmTileCols - 1) / kLmTileCols);
 }
 
 void free_prefill(akh_session* s) {
@@ -571,7 +571,7 @@ hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
   p.rope = s->rope;
   p.dim = c.dim;
   p.head_dim = c.dim / c.num_heads;
-  return launch_dec_gemm(p, DEC_QKV, true, 1, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_QKV, 1, s->be->stream);
 }
 
 // attn_qk_cached + softmax_rect + attn_av_cached (inference_graphs.rs:
@@ -601,7 +601,7 @@ hipError_t enqueue_out(akh_session* s, uint32_t l) {
   p.yt = s->xt;
   p.N = c.dim;
   p.K = c.dim;
-  return launch_dec_gemm(p, DEC_RESID, false, s->ks_out, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_OUT, s->ks_out, s->be->stream);
 }
 
 // norm_2 + ffn_up + SiLU (inference_graphs.rs:472-495).
@@ -614,7 +614,7 @@ hipError_t enqueue_up(akh_session* s, uint32_t l) {
   p.N = c.ffn_hidden;
   p.K = c.dim;
   p.gain = s->m->layer(l, W_NORM2);
-  return launch_dec_gemm(p, DEC_SILU_T, true, 1, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_UP, 1, s->be->stream);
 }
 
 // ffn_down + residual (inference_graphs.rs:497-508).
@@ -626,7 +626,7 @@ hipError_t enqueue_down(akh_session* s, uint32_t l) {
   p.yt = s->xt;
   p.N = c.dim;
   p.K = c.ffn_hidden;
-  return launch_dec_gemm(p, DEC_RESID, false, s->ks_down, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_DOWN, s->ks_down, s->be->stream);
 }
 
 // final_norm + lm_head + per-tile argmax (inference.rs:228-252).
@@ -640,7 +640,7 @@ hipError_t enqueue_lm_head(akh_session* s) {
   p.N = c.vocab_size;
   p.K = c.dim;
   p.gain = s->m->final_norm();
-  return launch_dec_gemm(p, DEC_LOGITS, true, 1, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_LM, 1, s->be->stream);
 }
 
 // One decode step of build_decode_layer (inference_graphs.rs:339-509) for
@@ -662,7 +662,7 @@ hipError_t enqueue_decode(akh_session* s) {
   }
   if (e == hipSuccess) e = enqueue_lm_head(s);
   if (e == hipSuccess)
-    e = launch_argmax_final(s->amax, (int)((c.vocab_size + 31) / 32),
+    e = launch_argmax_final(s->amax, lm_tiles(c),
                             (int)s->B, s->tok, s->pos, s->hist,
                             (int)s->max_ctx + 1, 0, st);
   return e;
@@ -743,9 +743,8 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   s->max_ctx = max_context_len;
   s->B = batch;
   s->cur_len.assign(batch, 0);
-  const int cus = s->be->num_cus;
-  s->ks_out = residual_ksplit(c.dim, c.dim, cus);
-  s->ks_down = residual_ksplit(c.dim, c.ffn_hidden, cus);
+  s->ks_out = residual_ksplit(DEC_CFG_OUT, c.dim);
+  s->ks_down = residual_ksplit(DEC_CFG_DOWN, c.ffn_hidden);
 
   const size_t d = c.dim, V = c.vocab_size, F = c.ffn_hidden, R = kMaxBatch;
   const size_t ntl = (V + 31) / 32;
@@ -912,7 +911,7 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
   HIP_TRY(launch_rows_to_kq(nullptr, nullptr, 0, s->px, (long)S - 1, (long)S,
                             s->xt, (int)s->B, (int)d, st));
   HIP_TRY(enqueue_lm_head(s));
-  HIP_TRY(launch_argmax_final(s->amax, (int)((c.vocab_size + 31) / 32),
+  HIP_TRY(launch_argmax_final(s->amax, lm_tiles(c),
                               (int)s->B, s->tok, nullptr, s->hist,
                               (int)s->max_ctx + 1, (int)S, st));
   std::fill(s->cur_len.begin(), s->cur_len.end(), S);
