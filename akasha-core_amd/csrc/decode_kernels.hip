@@ -1,16 +1,20 @@
 // Batched decode kernels: every sequence of a step is one row of a 32-row
 // MFMA tile, so each weight byte is read once per step for the whole batch.
 //
-// Activations that feed a GEMM (the residual stream, the attention output
-// and the SiLU'd ffn hidden state) live in the k-quad layout [K/4][32][4]:
-// the MFMA A operand of a half-wave is one contiguous 512-byte float4 load
-// per four k.  RMSNorm is folded into its consumer GEMM: the gain is applied
-// to the A operand, the sum of squares of the same operand is accumulated
-// in the main loop, and 1/rms scales the output rows (the norm is a per-row
-// scale, so it commutes with the contraction).  Nothing synchronises across
-// work-groups inside a kernel; the residual GEMMs split K across
-// work-groups and add their partial tiles into the residual stream with
-// device-scope atomics.
+// Dataflow of one layer (B <= 32 rows):
+//
+//   xn_t --qkv GEMM--> P_qkv --attention (sum, RoPE, KV append)--> attn_t
+//   attn_t --out GEMM--> P_out --rows_norm (x += sum, RMSNorm)--> x_t, xn_t
+//   xn_t --up GEMM--> P_up_t --down GEMM (A = silu(sum))--> P_down
+//   P_down --rows_norm (x += sum, next RMSNorm)--> x_t, xn_t
+//
+// Activations that feed a GEMM live in the k-quad layout [K/4][32][4]: the
+// MFMA A operand of a half-wave is one contiguous 512-byte float4 load per
+// four k.  A decode GEMM moves only a few MB, so the kernels split K over
+// many small blocks (the whole GPU works on each GEMM) and store partial
+// tiles; the consumer of each GEMM sums the partials in a fixed order.
+// Nothing synchronises across work-groups inside a kernel and no atomics
+// are used, so results are deterministic.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -18,25 +22,29 @@
 
 namespace akh {
 
-// Y[M, N] (epilogue) A[M, K] . W[K, N] for M <= 32.
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// Y (epilogue) A[M, K] . W[K, N] for M <= 32.
 //
-// Grid (N tiles of NT = 32*C columns, ksplit), W waves per block.  A pass of
-// the block covers KC = 2*W*HL rows of K: wave w takes 2*HL of them and half
-// h of its lanes HL, lane (j, h) supplying A[j][k] (a float4 of the k-quad
-// tile covers four k) and W[k][n0 + C*j + c] for MFMA tile c, so a wave load
-// covers two row segments of 128*C contiguous bytes.  All of a pass's loads
-// are issued before its first MFMA, so each wave keeps HL weight rows in
-// flight.  The waves' tiles are reduced in LDS as a binary tree (fixed
-// order) and wave 0 runs the epilogue.
-template <int C, int W, int HL, int EPI, bool NORM>
+// Grid (N tiles of NT = 32*C columns, K chunks), W waves per block.  A block
+// tile is C sub-tiles of 32 consecutive columns; lane (j, h) owns column
+// n0 + 32c + j of sub-tile c, so every weight load of a half-wave is one
+// 128-byte row segment.  A pass covers KC = 2*W*HL rows of K: wave w takes
+// 2*HL of them and half h of its lanes HL, each lane supplying A[j][k] (a
+// float4 of the k-quad tile covers four k) to all C sub-tiles.  All loads of
+// a pass are issued before its first MFMA.  A block runs one pass when K is
+// split over the grid, and loops over all of K otherwise.  The waves' tiles
+// are reduced in LDS as a binary tree (fixed order); wave 0 runs the
+// epilogue.
+//
+// PRO_SILU_SUM: A = silu(sum of p.nparts k-quad partial tiles at p.xt).
+template <int C, int W, int HL, int EPI, int PRO>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   constexpr int NT = 32 * C;
   constexpr int RH = W > 1 ? W / 2 : 1;
   constexpr int KC = 2 * W * HL;
   static_assert(HL % 4 == 0, "HL must cover whole k-quads");
   __shared__ float red[RH][32][NT + 1];
-  __shared__ float ssw[W][32];
-  __shared__ float rs_s[32];
 
   const int M = p.M, N = p.N, K = p.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -47,16 +55,17 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   const int kb = blockIdx.y * rows;
   if (kb >= K) return;
   const int ke = min(K, kb + rows);
-  const int ncol = n0 + C * j;
+  int col[C];
   bool cok[C];
 #pragma unroll
-  for (int c = 0; c < C; ++c) cok[c] = ncol + c < N;
-  const bool vec = C > 1 && (N % C) == 0 && ncol + C <= N;
+  for (int c = 0; c < C; ++c) {
+    col[c] = n0 + 32 * c + j;
+    cok[c] = col[c] < N;
+  }
 
   f32x16 acc[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) acc[c] = zero16();
-  float ss = 0.f;
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kr = k0 + wave * 2 * HL + h * HL;  // first row of this half
     float a[HL];
@@ -65,48 +74,34 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
     for (int u = 0; u < HL; ++u) {
       const int k = kr + u;
       const bool ok = k < ke;
-      const float* wr = p.w + (size_t)(ok ? k : kb) * N + ncol;
-      if (C == 4 && vec) {
-        const float4 t = ok ? *reinterpret_cast<const float4*>(wr)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-        wv[u][0] = t.x;
-        wv[u][C > 1 ? 1 : 0] = t.y;
-        wv[u][C > 2 ? 2 : 0] = t.z;
-        wv[u][C > 3 ? 3 : 0] = t.w;
-      } else if (C == 2 && vec) {
-        const float2 t = ok ? *reinterpret_cast<const float2*>(wr)
-                            : make_float2(0.f, 0.f);
-        wv[u][0] = t.x;
-        wv[u][C > 1 ? 1 : 0] = t.y;
-      } else {
+      const float* wr = p.w + (size_t)(ok ? k : kb) * N;
 #pragma unroll
-        for (int c = 0; c < C; ++c) wv[u][c] = (ok && cok[c]) ? wr[c] : 0.f;
-      }
+      for (int c = 0; c < C; ++c) wv[u][c] = (ok && cok[c]) ? wr[col[c]] : 0.f;
     }
 #pragma unroll
     for (int q = 0; q < HL / 4; ++q) {
       const int kq = (kr >> 2) + q;
       float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (4 * kq < ke)
-        t = *reinterpret_cast<const float4*>(p.xt + ((size_t)kq * 32 + j) * 4);
+      if (4 * kq < ke) {
+        const size_t off = ((size_t)kq * 32 + j) * 4;
+        if (PRO == PRO_SILU_SUM) {
+          for (int s = 0; s < p.nparts; ++s) {
+            const float4 v =
+                *reinterpret_cast<const float4*>(p.xt + (size_t)s * 32 * K + off);
+            t.x += v.x;
+            t.y += v.y;
+            t.z += v.z;
+            t.w += v.w;
+          }
+          t = make_float4(silu(t.x), silu(t.y), silu(t.z), silu(t.w));
+        } else {
+          t = *reinterpret_cast<const float4*>(p.xt + off);
+        }
+      }
       a[4 * q] = t.x;
       a[4 * q + 1] = t.y;
       a[4 * q + 2] = t.z;
       a[4 * q + 3] = t.w;
-    }
-    if (NORM) {
-#pragma unroll
-      for (int q = 0; q < HL / 4; ++q) {
-        float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (kr + 4 * q < ke) g = *reinterpret_cast<const float4*>(p.gain + kr + 4 * q);
-        const float gg[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x = a[4 * q + e];
-          ss += x * x;
-          a[4 * q + e] = __fmul_rn(x, gg[e]);
-        }
-      }
     }
 #pragma unroll
     for (int u = 0; u < HL; ++u)
@@ -122,84 +117,40 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
         for (int c = 0; c < C; ++c)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            red[wave - half][acc_row(r, h)][C * j + c] = acc[c][r];
+            red[wave - half][acc_row(r, h)][32 * c + j] = acc[c][r];
       __syncthreads();
       if (wave < half)
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            acc[c][r] += red[wave][acc_row(r, h)][C * j + c];
+            acc[c][r] += red[wave][acc_row(r, h)][32 * c + j];
     }
-  }
-  if (NORM) {
-    // Whole rows are in this block (the host never splits K of a
-    // normalising GEMM): finish sum(x^2) and turn it into 1/rms.
-    ss += __shfl_xor(ss, 32, 64);
-    if (h == 0) ssw[wave][j] = ss;
-    __syncthreads();
-    if (threadIdx.x < 32) {
-      float t = 0.f;
-      for (int w = 0; w < W; ++w) t += ssw[w][threadIdx.x];
-      rs_s[threadIdx.x] = 1.0f / sqrtf(t / (float)K + p.eps);
-    }
-    __syncthreads();
   }
   if (wave != 0) return;
 
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int m = acc_row(r, h);
-    float v[C];
-#pragma unroll
-    for (int c = 0; c < C; ++c) v[c] = NORM ? __fmul_rn(acc[c][r], rs_s[m]) : acc[c][r];
-    if (EPI == DEC_RESID) {
+    if (EPI == DEC_PART) {
+      float* y = p.y + ((size_t)blockIdx.y * 32 + m) * N;
 #pragma unroll
       for (int c = 0; c < C; ++c)
-        if (m < M && cok[c]) {
-          float* y = p.yt + kq_index(m, ncol + c);
-          if (gridDim.y > 1)
-            atomicAdd(y, v[c]);
-          else
-            *y = *y + v[c];
-        }
-    } else if (EPI == DEC_SILU_T) {
+        if (cok[c]) y[col[c]] = acc[c][r];
+    } else if (EPI == DEC_PART_T) {
+      float* y = p.y + (size_t)blockIdx.y * 32 * N;
 #pragma unroll
       for (int c = 0; c < C; ++c)
-        if (m < M && cok[c]) p.yt[kq_index(m, ncol + c)] = v[c] / (1.0f + expf(-v[c]));
-    } else if (EPI == DEC_QKV) {
-      static_assert(EPI != DEC_QKV || C == 1, "QKV epilogue pairs lanes");
-      // RoPE pairs (2i, 2i+1) sit in lanes j and j^1 of the same half.
-      const float partner = __shfl_xor(v[0], 1, 64);
-      if (m < M && cok[0]) {
-        const int dim = p.dim;
-        const int region = ncol / dim, cc = ncol - region * dim;
-        const int pos = p.pos[m];
-        float out = v[0];
-        if (region < 2) {
-          const int i = (cc % p.head_dim) >> 1;
-          const float2 cs = p.rope[(size_t)pos * (p.head_dim >> 1) + i];
-          const bool odd = ncol & 1;
-          float x0 = odd ? partner : v[0], x1 = odd ? v[0] : partner;
-          rope_pair(x0, x1, cs.x, cs.y);
-          out = odd ? x1 : x0;
-        }
-        if (region == 0)
-          p.q_out[(size_t)m * dim + cc] = out;
-        else
-          (region == 1 ? p.kcache : p.vcache)[(size_t)m * p.seq_stride +
-                                              (size_t)pos * dim + cc] = out;
-      }
+        if (cok[c]) y[kq_index(m, col[c])] = acc[c][r];
     } else if (EPI == DEC_LOGITS) {
       // Logits, and the first maximum of the row over this tile's columns.
       float bv = -INFINITY;
-      uint32_t bi = (uint32_t)ncol;
+      uint32_t bi = (uint32_t)col[0];
 #pragma unroll
       for (int c = 0; c < C; ++c) {
-        const bool ok = m < M && cok[c];
-        if (ok) {
-          p.y[(size_t)m * N + ncol + c] = v[c];
-          amax_merge(bv, bi, v[c], (uint32_t)(ncol + c));
+        if (m < M && cok[c]) {
+          p.y[(size_t)m * N + col[c]] = acc[c][r];
+          amax_merge(bv, bi, acc[c][r], (uint32_t)col[c]);
         }
       }
 #pragma unroll
@@ -217,10 +168,17 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
 }
 
 // Single-query attention over the KV cache for one (sequence, head) per
-// block: AW waves split the live rows 0..pos, each streams its rows with
-// HD/4 lanes per row (a float4 each) and RB row groups of K and V in flight,
-// keeps an online softmax, and the waves' (max, sum, o) are merged in LDS.
-// The output row is written in the k-quad layout for the out_proj GEMM.
+// block, with the fused head of the layer's attention:
+//   q, k, v of the new token = the sum of the QKV GEMM's partial tiles, with
+//   RoPE on q and k at position pos; k and v appended to the cache at row
+//   pos (inference_graphs.rs:398-426);
+//   softmax(scale * q . K[0..pos]) . V[0..pos] (attn_qk_cached + softmax_rect
+//   + attn_av_cached, inference_graphs.rs:428-456).
+// AW waves split the cached rows 0..pos-1; each streams its rows with HD/4
+// lanes per row (a float4 each) and RB row groups of K and V in flight,
+// keeping an online softmax; wave 0 also folds in the new row.  The waves'
+// (max, sum, o) are merged in LDS and the output row is written in the
+// k-quad layout for the out_proj GEMM.
 template <int HD, int AW>
 __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   constexpr int LPR = HD / 4;    // lanes per row
@@ -232,17 +190,55 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   const int bh = blockIdx.x, b = bh / p.H, hh = bh - b * p.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane % LPR, rl = lane / LPR;
-  const int T = p.pos[b] + 1;
+  const int pos = p.pos[b];
+  const int d = p.d;
+
+  // The new token's q, k, v (columns hh*HD + 4g .. +3 of each role).
+  float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), kn = q4, vn = q4;
+  {
+    const size_t cq = (size_t)hh * HD + 4 * g;
+    for (int s = 0; s < p.nparts; ++s) {
+      const float* row = p.qkv + ((size_t)s * 32 + b) * 3 * d;
+      const float4 a = *reinterpret_cast<const float4*>(row + cq);
+      const float4 k = *reinterpret_cast<const float4*>(row + d + cq);
+      const float4 v = *reinterpret_cast<const float4*>(row + 2 * d + cq);
+      q4.x += a.x; q4.y += a.y; q4.z += a.z; q4.w += a.w;
+      kn.x += k.x; kn.y += k.y; kn.z += k.z; kn.w += k.w;
+      vn.x += v.x; vn.y += v.y; vn.z += v.z; vn.w += v.w;
+    }
+    // Pairs (4g, 4g+1) and (4g+2, 4g+3) of the head: rope entries 2g, 2g+1.
+    const float2 c0 = p.rope[(size_t)pos * (HD / 2) + 2 * g];
+    const float2 c1 = p.rope[(size_t)pos * (HD / 2) + 2 * g + 1];
+    rope_pair(q4.x, q4.y, c0.x, c0.y);
+    rope_pair(q4.z, q4.w, c1.x, c1.y);
+    rope_pair(kn.x, kn.y, c0.x, c0.y);
+    rope_pair(kn.z, kn.w, c1.x, c1.y);
+  }
+  const size_t hoff = (size_t)b * p.seq_stride + hh * HD + 4 * g;
+  if (wave == 0 && rl == 0) {
+    *reinterpret_cast<float4*>(p.kc + hoff + (size_t)pos * d) = kn;
+    *reinterpret_cast<float4*>(p.vc + hoff + (size_t)pos * d) = vn;
+  }
+
+  // Cached rows 0..pos-1, split over the waves.
+  const int T = pos;
   const int ch = ((T + AW - 1) / AW + RPW - 1) / RPW * RPW;
   const int r0 = wave * ch, r1 = min(T, r0 + ch);
-
-  const float4 q4 =
-      *reinterpret_cast<const float4*>(p.q + (size_t)b * p.d + hh * HD + 4 * g);
-  const float* kbase = p.kc + (size_t)b * p.seq_stride + hh * HD + 4 * g;
-  const float* vbase = p.vc + (size_t)b * p.seq_stride + hh * HD + 4 * g;
+  const float* kbase = p.kc + hoff;
+  const float* vbase = p.vc + hoff;
 
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (wave == 0) {
+    // The new row; every lane of a row group holds its full score, and only
+    // row slot 0 adds it so the slot sum below counts it once.
+    float s = q4.x * kn.x + q4.y * kn.y + q4.z * kn.z + q4.w * kn.w;
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    m = s * p.scale;
+    l = rl == 0 ? 1.f : 0.f;
+    acc = rl == 0 ? vn : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   for (int base = r0; base < r1; base += RPW * RB) {
     float4 kv[RB], vv[RB];
     bool ok[RB];
@@ -250,7 +246,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     for (int i = 0; i < RB; ++i) {
       const int r = base + i * RPW + rl;
       ok[i] = r < r1;
-      const size_t off = (size_t)(ok[i] ? r : r0) * p.d;
+      const size_t off = (size_t)(ok[i] ? r : r0) * d;
       kv[i] = *reinterpret_cast<const float4*>(kbase + off);
       vv[i] = *reinterpret_cast<const float4*>(vbase + off);
     }
@@ -280,8 +276,6 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
       pv.z += e * vv[i].z;
       pv.w += e * vv[i].w;
     }
-#pragma unroll
-    for (int o = LPR; o < 64; o <<= 1) ps += __shfl_xor(ps, o, 64);
     l = l * corr + ps;
     acc.x = acc.x * corr + pv.x;
     acc.y = acc.y * corr + pv.y;
@@ -289,8 +283,10 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     acc.w = acc.w * corr + pv.w;
     m = mn;
   }
+  // Sum the wave's row slots (they share the running max m).
 #pragma unroll
   for (int o = LPR; o < 64; o <<= 1) {
+    l += __shfl_xor(l, o, 64);
     acc.x += __shfl_xor(acc.x, o, 64);
     acc.y += __shfl_xor(acc.y, o, 64);
     acc.z += __shfl_xor(acc.z, o, 64);
@@ -322,23 +318,60 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   }
 }
 
-// Rows into the k-quad layout: an embedding lookup (EMBEDDING semantics,
-// cpu.rs:25-41) or the last row of every prefilled sequence.
-__global__ void k_rows_to_kq(const float* table, const uint32_t* ids,
-                             uint32_t vocab, const float* src, long row0,
-                             long row_stride, float* xt, int d) {
-  const int m = blockIdx.x;
-  const float* row;
-  if (ids) {
-    const uint32_t id = ids[m];
-    row = id < vocab ? table + (size_t)id * d : nullptr;
-  } else {
-    row = src + (size_t)(row0 + (long)m * row_stride) * d;
+// One block per row m: the row's new residual value (an embedding lookup,
+// a gathered row, or x + the sum of a GEMM's partial tiles) is stored in the
+// k-quad residual stream, and its RMSNorm with `gain` (cpu.rs:205-222:
+// x * (1 / sqrt(sum(x^2)/d + eps)) * w) as the next GEMM's input.
+template <int QPT>
+__global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
+  __shared__ float red4[4];
+  const int m = blockIdx.x, d = p.d, nq = d / 4;
+  const float* row = nullptr;
+  if (p.ids) {
+    const uint32_t id = p.ids[m];
+    row = id < p.vocab ? p.table + (size_t)id * d : nullptr;
+  } else if (p.src) {
+    row = p.src + (size_t)(p.row0 + (long)m * p.row_stride) * d;
   }
-  for (int q = threadIdx.x; q < d / 4; q += blockDim.x) {
-    const float4 v = row ? *reinterpret_cast<const float4*>(row + 4 * q)
-                         : make_float4(0.f, 0.f, 0.f, 0.f);
-    *reinterpret_cast<float4*>(xt + ((size_t)q * 32 + m) * 4) = v;
+  const bool gather = p.ids || p.src;
+  float4 x[QPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < QPT; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < nq) {
+      float* xq = p.xt + ((size_t)q * 32 + m) * 4;
+      if (gather) {
+        if (row) v = *reinterpret_cast<const float4*>(row + 4 * q);
+      } else {
+        v = *reinterpret_cast<const float4*>(xq);
+        for (int s = 0; s < p.nparts; ++s) {
+          const float4 t =
+              *reinterpret_cast<const float4*>(p.parts + ((size_t)s * 32 + m) * d + 4 * q);
+          v.x += t.x;
+          v.y += t.y;
+          v.z += t.z;
+          v.w += t.w;
+        }
+      }
+      *reinterpret_cast<float4*>(xq) = v;
+      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    x[i] = v;
+  }
+  ss = block_sum256(ss, red4);
+  const float rs = 1.0f / sqrtf(ss / (float)d + p.eps);
+#pragma unroll
+  for (int i = 0; i < QPT; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    if (q < nq) {
+      const float4 g = *reinterpret_cast<const float4*>(p.gain + 4 * q);
+      const float4 v = x[i];
+      *reinterpret_cast<float4*>(p.xnt + ((size_t)q * 32 + m) * 4) = make_float4(
+          __fmul_rn(__fmul_rn(v.x, rs), g.x), __fmul_rn(__fmul_rn(v.y, rs), g.y),
+          __fmul_rn(__fmul_rn(v.z, rs), g.z), __fmul_rn(__fmul_rn(v.w, rs), g.w));
+    }
   }
 }
 
@@ -372,38 +405,56 @@ __global__ __launch_bounds__(256) void k_argmax_final(
 
 // ---------------------------------------------------------------------------
 
-template <int C, int W, int HL, int EPI, bool NORM>
-static hipError_t dec_go(const DecGemmParams& p, int ksplit, hipStream_t s) {
-  hipLaunchKernelGGL((k_dec_gemm<C, W, HL, EPI, NORM>),
-                     dim3((p.N + 32 * C - 1) / (32 * C), ksplit), dim3(64 * W), 0,
-                     s, p);
+namespace {
+
+// Launch shapes per role (C sub-tiles, W waves, HL rows per half-wave),
+// chosen by a sweep on MI355X.  The four layer GEMMs split K into many
+// small blocks; lm_head runs whole-K blocks of 128 columns.
+template <int ROLE>
+struct RoleShape;
+template <> struct RoleShape<DEC_CFG_QKV> { static constexpr int C = 1, W = 2, HL = 16; };
+template <> struct RoleShape<DEC_CFG_OUT> { static constexpr int C = 1, W = 2, HL = 8; };
+template <> struct RoleShape<DEC_CFG_UP> { static constexpr int C = 1, W = 2, HL = 16; };
+template <> struct RoleShape<DEC_CFG_DOWN> { static constexpr int C = 1, W = 2, HL = 16; };
+template <> struct RoleShape<DEC_CFG_LM> { static constexpr int C = 4, W = 4, HL = 16; };
+
+template <int ROLE>
+int role_splits(int K) {
+  if (ROLE == DEC_CFG_LM) return 1;
+  constexpr int KC = 2 * RoleShape<ROLE>::W * RoleShape<ROLE>::HL;
+  return (K + KC - 1) / KC;
+}
+
+template <int ROLE, int EPI, int PRO>
+hipError_t dec_go(const DecGemmParams& p, hipStream_t s) {
+  using S = RoleShape<ROLE>;
+  hipLaunchKernelGGL((k_dec_gemm<S::C, S::W, S::HL, EPI, PRO>),
+                     dim3((p.N + 32 * S::C - 1) / (32 * S::C), role_splits<ROLE>(p.K)),
+                     dim3(64 * S::W), 0, s, p);
   return hipGetLastError();
 }
 
-// Launch shapes per role (N tile, waves, rows in flight per half-wave):
-//   QKV, UP    32 cols, 16 waves, 24 rows: one block per N tile owns the
-//              whole K = dim (needed by the folded RMSNorm);
-//   OUT, DOWN  32 cols,  4 waves, 16 rows: K split in chunks of 128 rows,
-//              partial tiles added atomically into the residual stream;
-//   LM         64 cols,  8 waves, 24 rows: whole K in two passes.
-int dec_gemm_rows_per_block(int cfg) {
-  switch (cfg) {
-    case DEC_CFG_QKV:
-    case DEC_CFG_UP: return 2 * 16 * 24;
-    case DEC_CFG_OUT:
-    case DEC_CFG_DOWN: return 2 * 4 * 16;
-    default: return 2 * 8 * 24;
+}  // namespace
+
+int dec_gemm_splits(int role, int K) {
+  switch (role) {
+    case DEC_CFG_QKV: return role_splits<DEC_CFG_QKV>(K);
+    case DEC_CFG_OUT: return role_splits<DEC_CFG_OUT>(K);
+    case DEC_CFG_UP: return role_splits<DEC_CFG_UP>(K);
+    case DEC_CFG_DOWN: return role_splits<DEC_CFG_DOWN>(K);
+    default: return 1;
   }
 }
 
-hipError_t launch_dec_gemm(const DecGemmParams& p, int cfg, int ksplit,
-                           hipStream_t s) {
-  switch (cfg) {
-    case DEC_CFG_QKV: return dec_go<1, 16, 24, DEC_QKV, true>(p, 1, s);
-    case DEC_CFG_UP: return dec_go<1, 16, 24, DEC_SILU_T, true>(p, 1, s);
-    case DEC_CFG_OUT:
-    case DEC_CFG_DOWN: return dec_go<1, 4, 16, DEC_RESID, false>(p, ksplit, s);
-    case DEC_CFG_LM: return dec_go<2, 8, 24, DEC_LOGITS, true>(p, 1, s);
+int dec_lm_tile_cols() { return 32 * RoleShape<DEC_CFG_LM>::C; }
+
+hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
+  switch (role) {
+    case DEC_CFG_QKV: return dec_go<DEC_CFG_QKV, DEC_PART, PRO_NONE>(p, s);
+    case DEC_CFG_OUT: return dec_go<DEC_CFG_OUT, DEC_PART, PRO_NONE>(p, s);
+    case DEC_CFG_UP: return dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NONE>(p, s);
+    case DEC_CFG_DOWN: return dec_go<DEC_CFG_DOWN, DEC_PART, PRO_SILU_SUM>(p, s);
+    case DEC_CFG_LM: return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -424,12 +475,16 @@ hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
   return hipGetLastError();
 }
 
-hipError_t launch_rows_to_kq(const float* table, const uint32_t* ids,
-                             uint32_t vocab, const float* src, long row0,
-                             long row_stride, float* xt, int M, int d,
-                             hipStream_t s) {
-  hipLaunchKernelGGL(k_rows_to_kq, dim3(M), dim3(256), 0, s, table, ids,
-                     vocab, src, row0, row_stride, xt, d);
+hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s) {
+  const int nq = p.d / 4;
+  if (nq <= 256)
+    hipLaunchKernelGGL(k_rows_norm<1>, dim3(M), dim3(256), 0, s, p);
+  else if (nq <= 512)
+    hipLaunchKernelGGL(k_rows_norm<2>, dim3(M), dim3(256), 0, s, p);
+  else if (nq <= 1024)
+    hipLaunchKernelGGL(k_rows_norm<4>, dim3(M), dim3(256), 0, s, p);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -113,65 +113,77 @@ hipError_t launch_embedding_rows(const uint32_t* tokens, const float* table,
 // ---------------------------------------------------------------------------
 
 enum DecEpi : int {
-  DEC_RESID = 0,   // yt += acc (k-quad; atomic when K is split)
-  DEC_SILU_T = 1,  // yt = silu(acc) (k-quad)
-  DEC_QKV = 2,     // RoPE(Q) -> q_out [32, dim]; RoPE(K), V -> cache row pos
-  DEC_LOGITS = 3,  // y = acc [32, N] + per-tile argmax partials
+  DEC_PART = 0,    // y[split, m, n] = partial tile of K chunk `split`
+  DEC_PART_T = 1,  // the same, each partial tile in the k-quad layout
+  DEC_LOGITS = 2,  // y[m, n] = whole-K result + per-tile argmax partials
+};
+
+enum DecPro : int {
+  PRO_NONE = 0,      // A = xt
+  PRO_SILU_SUM = 1,  // A = silu(sum of nparts k-quad partial tiles at xt)
+};
+
+// Roles of the decode GEMMs; each has its own launch shape.
+enum DecCfg : int {
+  DEC_CFG_QKV = 0,   // qkv_proj  -> partials (summed by attention)
+  DEC_CFG_OUT = 1,   // out_proj  -> partials (summed by rows_norm)
+  DEC_CFG_UP = 2,    // ffn_up    -> k-quad partials (summed by down)
+  DEC_CFG_DOWN = 3,  // ffn_down on silu(sum) -> partials (rows_norm)
+  DEC_CFG_LM = 4,    // lm_head   -> logits + argmax partials
 };
 
 struct DecGemmParams {
-  const float* xt;  // A operand, k-quad [K/4][32][4]
+  const float* xt;  // A operand (k-quad), or nparts k-quad partial tiles
+  int nparts;
   const float* w;   // [K, N] row-major
   int M, N, K;
-  const float* gain;  // RMSNorm gain when the GEMM normalises its input
-  float eps;
-  float* yt;     // DEC_RESID / DEC_SILU_T output (k-quad [N/4][32][4])
-  float* y;      // DEC_LOGITS output [32, N]
-  uint2* amax;   // DEC_LOGITS: [32, ntiles] (value bits, index)
-  float* q_out;  // DEC_QKV
-  float* kcache;
-  float* vcache;
-  long seq_stride;
-  const int* pos;
-  const float2* rope;
-  int dim, head_dim;
+  float* y;         // partial tiles or logits
+  uint2* amax;      // DEC_LOGITS: [32, ntiles] (value bits, index)
 };
 
+// Number of K chunks (partial tiles) a role's GEMM produces for contraction
+// length K, and the column count of one lm_head tile.
+int dec_gemm_splits(int role, int K);
+int dec_lm_tile_cols();
+hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s);
+
 struct DecAttnParams {
-  const float* q;   // [32, d] row-major
-  const float* kc;  // sequence b at kc + b * seq_stride, rows of d
-  const float* vc;
-  float* out_t;     // k-quad [d/4][32][4]
-  const int* pos;   // attends to rows 0..pos[b]
+  const float* qkv;  // nparts partial tiles [nparts][32][3*d]
+  int nparts;
+  const float2* rope;  // [max_ctx, head_dim / 2] (cos, sin)
+  float* kc;         // sequence b at kc + b * seq_stride, rows of d
+  float* vc;
+  float* out_t;      // k-quad [d/4][32][4]
+  const int* pos;    // position of the new token of each sequence
   long seq_stride;
   int H, d;
   float scale;
 };
 
-// Roles of the decode GEMMs; each has its own launch shape.
-enum DecCfg : int {
-  DEC_CFG_QKV = 0,   // norm_1 + qkv_proj + RoPE + KV append (DEC_QKV)
-  DEC_CFG_OUT = 1,   // out_proj + residual (DEC_RESID, K split)
-  DEC_CFG_UP = 2,    // norm_2 + ffn_up + SiLU (DEC_SILU_T)
-  DEC_CFG_DOWN = 3,  // ffn_down + residual (DEC_RESID, K split)
-  DEC_CFG_LM = 4,    // final norm + lm_head + argmax partials (DEC_LOGITS)
-};
-// Columns of one lm_head tile (the argmax partials are per tile).
-constexpr int kLmTileCols = 64;
-// Rows of K one block of the role covers per pass; the residual roles split
-// K into ceil(K / rows) blocks.
-int dec_gemm_rows_per_block(int cfg);
-// ksplit > 1 only for the residual roles (partial tiles added atomically).
-hipError_t launch_dec_gemm(const DecGemmParams& p, int cfg, int ksplit,
-                           hipStream_t s);
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
                            hipStream_t s);
-// xt[:, m] = table[ids[m]] (zero row if ids[m] >= vocab), or, with ids null,
-// src row (row0 + m * row_stride), for m < M.
-hipError_t launch_rows_to_kq(const float* table, const uint32_t* ids,
-                             uint32_t vocab, const float* src, long row0,
-                             long row_stride, float* xt, int M, int d,
-                             hipStream_t s);
+
+// Per-row residual update + RMSNorm: x = table[ids[m]] (zero row if the id
+// is out of vocab), or src row (row0 + m * row_stride), or xt + the sum of
+// nparts row-major partial tiles [nparts][32][d]; xt <- x (k-quad) and
+// xnt <- x * rsqrt(mean(x^2) + eps) * gain (k-quad).
+struct RowsNormParams {
+  const float* table;
+  const uint32_t* ids;
+  uint32_t vocab;
+  const float* src;
+  long row0, row_stride;
+  const float* parts;
+  int nparts;
+  float* xt;
+  const float* gain;
+  float eps;
+  float* xnt;
+  int d;
+};
+
+hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s);
+
 // Greedy token per row from the lm_head partials.  With `pos`, also the
 // decode step's bookkeeping on the device: hist[m, pos] = consumed token,
 // hist[m, pos + 1] = chosen token, pos[m] += 1.  Without it (prefill) the

@@ -472,18 +472,21 @@ struct akh_session {
   float2* rope = nullptr;  // [max_ctx, head_dim / 2] (cos, sin)
 
   // Decode-step state, 32 rows (the MFMA tile height).  *_t buffers are in
-  // the k-quad layout [K/4][32][4].
+  // the k-quad layout [K/4][32][4]; p_* hold a GEMM's partial tiles.
   float* xt = nullptr;      // residual stream
-  float* q = nullptr;       // [32, dim] post-RoPE queries
+  float* xnt = nullptr;     // RMSNorm of the residual stream (GEMM input)
   float* attn_t = nullptr;  // attention output
-  float* ffn_t = nullptr;   // silu(ffn_up)
+  float* p_qkv = nullptr;   // [ks_qkv][32][3*dim]
+  float* p_out = nullptr;   // [ks_out][32][dim]
+  float* p_up = nullptr;    // [ks_up] k-quad tiles of [32, ffn]
+  float* p_down = nullptr;  // [ks_down][32][dim]
   float* logits = nullptr;  // [32, vocab]
-  uint2* amax = nullptr;    // [32, vocab / 32] argmax partials
+  uint2* amax = nullptr;    // [32, lm tiles] argmax partials
   uint32_t* tok = nullptr;  // tokens fed to the next step
   int* pos = nullptr;       // per-sequence position of the next token
   uint32_t* hist = nullptr; // [B, max_ctx + 1] token at each position
 
-  int ks_out = 1, ks_down = 1;  // K split of the residual GEMMs
+  int ks_qkv = 1, ks_out = 1, ks_up = 1, ks_down = 1;
 
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -504,14 +507,9 @@ struct akh_session {
 
 namespace {
 
-// K split of a residual decode GEMM: one block per pass of its role.
-int residual_ksplit(int cfg, int K) {
-  const int rows = dec_gemm_rows_per_block(cfg);
-  return std::max(1, (K + rows - 1) / rows);
-}
-
 int lm_tiles(const akh_model_config& c) {
-  return (int)((c.vocab_size + kLmTileCols - 1) / kLmTileCols);
+  const int cols = dec_lm_tile_cols();
+  return (int)((c.vocab_size + cols - 1) / cols);
 }
 
 void free_prefill(akh_session* s) {
@@ -549,37 +547,40 @@ akh_status upload_positions(akh_session* s) {
 DecGemmParams dec_base(akh_session* s) {
   DecGemmParams p{};
   p.M = (int)s->B;
-  p.eps = s->m->cfg.norm_eps;
   return p;
 }
 
-// norm_1 + fused QKV projection + RoPE + KV append (inference_graphs.rs:
-// 363-426): one kernel.
+RowsNormParams norm_base(akh_session* s, const float* gain) {
+  RowsNormParams r{};
+  r.xt = s->xt;
+  r.xnt = s->xnt;
+  r.gain = gain;
+  r.eps = s->m->cfg.norm_eps;
+  r.d = (int)s->m->cfg.dim;
+  return r;
+}
+
+// qkv_proj on the normalised residual (inference_graphs.rs:363-384):
+// partial tiles, summed by the attention kernel.
 hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
-  p.xt = s->xt;
+  p.xt = s->xnt;
   p.w = s->m->layer(l, W_QKV);
+  p.y = s->p_qkv;
   p.N = 3 * c.dim;
   p.K = c.dim;
-  p.gain = s->m->layer(l, W_NORM1);
-  p.q_out = s->q;
-  p.kcache = s->kcache(l);
-  p.vcache = s->vcache(l);
-  p.seq_stride = s->seq_stride();
-  p.pos = s->pos;
-  p.rope = s->rope;
-  p.dim = c.dim;
-  p.head_dim = c.dim / c.num_heads;
-  return launch_dec_gemm(p, DEC_CFG_QKV, 1, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_QKV, s->be->stream);
 }
 
-// attn_qk_cached + softmax_rect + attn_av_cached (inference_graphs.rs:
-// 428-456): one kernel.
+// q/k/v split + RoPE + cache append + cached attention
+// (inference_graphs.rs:385-456): one kernel.
 hipError_t enqueue_attn(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecAttnParams p{};
-  p.q = s->q;
+  p.qkv = s->p_qkv;
+  p.nparts = s->ks_qkv;
+  p.rope = s->rope;
   p.kc = s->kcache(l);
   p.vc = s->vcache(l);
   p.out_t = s->attn_t;
@@ -592,79 +593,95 @@ hipError_t enqueue_attn(akh_session* s, uint32_t l) {
   return launch_dec_attn(p, (int)s->B, (int)hd, s->be->stream);
 }
 
-// out_proj + residual (inference_graphs.rs:458-470).
+// out_proj (inference_graphs.rs:458-470): partial tiles.
 hipError_t enqueue_out(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->attn_t;
   p.w = s->m->layer(l, W_OUT);
-  p.yt = s->xt;
+  p.y = s->p_out;
   p.N = c.dim;
   p.K = c.dim;
-  return launch_dec_gemm(p, DEC_CFG_OUT, s->ks_out, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_OUT, s->be->stream);
 }
 
-// norm_2 + ffn_up + SiLU (inference_graphs.rs:472-495).
+// Residual add of a GEMM's partial tiles + the next RMSNorm.
+hipError_t enqueue_resid_norm(akh_session* s, const float* parts, int nparts,
+                              const float* gain) {
+  RowsNormParams r = norm_base(s, gain);
+  r.parts = parts;
+  r.nparts = nparts;
+  return launch_rows_norm(r, (int)s->B, s->be->stream);
+}
+
+// ffn_up on norm_2 of the residual (inference_graphs.rs:472-493).
 hipError_t enqueue_up(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
-  p.xt = s->xt;
+  p.xt = s->xnt;
   p.w = s->m->layer(l, W_UP);
-  p.yt = s->ffn_t;
+  p.y = s->p_up;
   p.N = c.ffn_hidden;
   p.K = c.dim;
-  p.gain = s->m->layer(l, W_NORM2);
-  return launch_dec_gemm(p, DEC_CFG_UP, 1, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_UP, s->be->stream);
 }
 
-// ffn_down + residual (inference_graphs.rs:497-508).
+// SiLU + ffn_down (inference_graphs.rs:495-508): partial tiles.
 hipError_t enqueue_down(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
-  p.xt = s->ffn_t;
+  p.xt = s->p_up;
+  p.nparts = s->ks_up;
   p.w = s->m->layer(l, W_DOWN);
-  p.yt = s->xt;
+  p.y = s->p_down;
   p.N = c.dim;
   p.K = c.ffn_hidden;
-  return launch_dec_gemm(p, DEC_CFG_DOWN, s->ks_down, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_DOWN, s->be->stream);
 }
 
-// final_norm + lm_head + per-tile argmax (inference.rs:228-252).
+// lm_head on the final-normed residual + per-tile argmax (inference.rs:
+// 228-252).
 hipError_t enqueue_lm_head(akh_session* s) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
-  p.xt = s->xt;
+  p.xt = s->xnt;
   p.w = s->m->lm_head();
   p.y = s->logits;
   p.amax = s->amax;
   p.N = c.vocab_size;
   p.K = c.dim;
-  p.gain = s->m->final_norm();
-  return launch_dec_gemm(p, DEC_CFG_LM, 1, s->be->stream);
+  return launch_dec_gemm(p, DEC_CFG_LM, s->be->stream);
 }
 
 // One decode step of build_decode_layer (inference_graphs.rs:339-509) for
-// every sequence: embedding, 5 kernels per layer, lm_head, greedy argmax +
-// position advance.  Reads tok/pos from the device, so it can be replayed
-// step after step with no host work.
+// every sequence: embedding + norm_1, then per layer qkv GEMM, attention,
+// out GEMM, residual + norm_2, up GEMM, down GEMM, residual + next norm;
+// lm_head, greedy argmax + position advance.  Reads tok/pos from the
+// device, so it can be replayed step after step with no host work.
 hipError_t enqueue_decode(akh_session* s) {
   const akh_model_config& c = s->m->cfg;
   hipStream_t st = s->be->stream;
-  hipError_t e = launch_rows_to_kq(s->m->embedding(), s->tok, c.vocab_size,
-                                   nullptr, 0, 0, s->xt, (int)s->B,
-                                   (int)c.dim, st);
+  RowsNormParams emb = norm_base(s, s->m->layer(0, W_NORM1));
+  emb.table = s->m->embedding();
+  emb.ids = s->tok;
+  emb.vocab = c.vocab_size;
+  hipError_t e = launch_rows_norm(emb, (int)s->B, st);
   for (uint32_t l = 0; l < c.num_layers && e == hipSuccess; ++l) {
+    const float* next_gain =
+        l + 1 < c.num_layers ? s->m->layer(l + 1, W_NORM1) : s->m->final_norm();
     e = enqueue_qkv(s, l);
     if (e == hipSuccess) e = enqueue_attn(s, l);
     if (e == hipSuccess) e = enqueue_out(s, l);
+    if (e == hipSuccess)
+      e = enqueue_resid_norm(s, s->p_out, s->ks_out, s->m->layer(l, W_NORM2));
     if (e == hipSuccess) e = enqueue_up(s, l);
     if (e == hipSuccess) e = enqueue_down(s, l);
+    if (e == hipSuccess) e = enqueue_resid_norm(s, s->p_down, s->ks_down, next_gain);
   }
   if (e == hipSuccess) e = enqueue_lm_head(s);
   if (e == hipSuccess)
-    e = launch_argmax_final(s->amax, lm_tiles(c),
-                            (int)s->B, s->tok, s->pos, s->hist,
-                            (int)s->max_ctx + 1, 0, st);
+    e = launch_argmax_final(s->amax, lm_tiles(c), (int)s->B, s->tok, s->pos,
+                            s->hist, (int)s->max_ctx + 1, 0, st);
   return e;
 }
 
@@ -715,8 +732,9 @@ extern "C" void akh_session_free(akh_session* s) {
   if (s->gexec) hipGraphExecDestroy(s->gexec);
   if (s->graph) hipGraphDestroy(s->graph);
   free_prefill(s);
-  void* bufs[] = {s->kv,     s->rope, s->xt,  s->q,   s->attn_t, s->ffn_t,
-                  s->logits, s->amax, s->tok, s->pos, s->hist};
+  void* bufs[] = {s->kv,    s->rope,   s->xt,     s->xnt,  s->attn_t,
+                  s->p_qkv, s->p_out,  s->p_up,   s->p_down, s->logits,
+                  s->amax,  s->tok,    s->pos,    s->hist};
   for (void* p : bufs)
     if (p) hipFree(p);
   delete s;
@@ -733,7 +751,8 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   const uint32_t hd = c.dim / c.num_heads;
   CHECK_ARG(supported_head_dim(hd) && hd >= 4,
             "akh_session_new: head_dim must be a power of two in 4..128");
-  CHECK_ARG(c.dim % 32 == 0, "akh_session_new: dim must be a multiple of 32");
+  CHECK_ARG(c.dim % 32 == 0 && c.dim <= 4096,
+            "akh_session_new: dim must be a multiple of 32, at most 4096");
   CHECK_ARG(c.ffn_hidden % 32 == 0,
             "akh_session_new: ffn_hidden must be a multiple of 32");
 
@@ -743,11 +762,12 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   s->max_ctx = max_context_len;
   s->B = batch;
   s->cur_len.assign(batch, 0);
-  s->ks_out = residual_ksplit(DEC_CFG_OUT, c.dim);
-  s->ks_down = residual_ksplit(DEC_CFG_DOWN, c.ffn_hidden);
+  s->ks_qkv = dec_gemm_splits(DEC_CFG_QKV, c.dim);
+  s->ks_out = dec_gemm_splits(DEC_CFG_OUT, c.dim);
+  s->ks_up = dec_gemm_splits(DEC_CFG_UP, c.dim);
+  s->ks_down = dec_gemm_splits(DEC_CFG_DOWN, c.ffn_hidden);
 
   const size_t d = c.dim, V = c.vocab_size, F = c.ffn_hidden, R = kMaxBatch;
-  const size_t ntl = (V + 31) / 32;
   hipError_t e = hipSetDevice(s->be->device);
   auto alloc = [&](void** p, size_t bytes) {
     if (e == hipSuccess) e = hipMalloc(p, bytes);
@@ -756,11 +776,14 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   alloc((void**)&s->kv, (size_t)c.num_layers * 2 * batch * max_context_len * d * 4);
   alloc((void**)&s->rope, (size_t)max_context_len * (hd / 2) * sizeof(float2));
   alloc((void**)&s->xt, R * d * 4);
-  alloc((void**)&s->q, R * d * 4);
+  alloc((void**)&s->xnt, R * d * 4);
   alloc((void**)&s->attn_t, R * d * 4);
-  alloc((void**)&s->ffn_t, R * F * 4);
+  alloc((void**)&s->p_qkv, (size_t)s->ks_qkv * R * 3 * d * 4);
+  alloc((void**)&s->p_out, (size_t)s->ks_out * R * d * 4);
+  alloc((void**)&s->p_up, (size_t)s->ks_up * R * F * 4);
+  alloc((void**)&s->p_down, (size_t)s->ks_down * R * d * 4);
   alloc((void**)&s->logits, R * V * 4);
-  alloc((void**)&s->amax, R * ntl * sizeof(uint2));
+  alloc((void**)&s->amax, R * (size_t)lm_tiles(c) * sizeof(uint2));
   alloc((void**)&s->tok, R * 4);
   alloc((void**)&s->pos, R * 4);
   alloc((void**)&s->hist, (size_t)batch * (max_context_len + 1) * 4);
@@ -906,10 +929,15 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     w.K = c.ffn_hidden;
     HIP_TRY(launch_gemm(w, GEMM_ADD, st));
   }
-  // Last row of every sequence -> final RMSNorm (folded into lm_head) ->
-  // lm_head -> greedy token (inference.rs:120-168).
-  HIP_TRY(launch_rows_to_kq(nullptr, nullptr, 0, s->px, (long)S - 1, (long)S,
-                            s->xt, (int)s->B, (int)d, st));
+  // Last row of every sequence -> final RMSNorm -> lm_head -> greedy token
+  // (inference.rs:120-168).
+  {
+    RowsNormParams r = norm_base(s, s->m->final_norm());
+    r.src = s->px;
+    r.row0 = (long)S - 1;
+    r.row_stride = (long)S;
+    HIP_TRY(launch_rows_norm(r, (int)s->B, st));
+  }
   HIP_TRY(enqueue_lm_head(s));
   HIP_TRY(launch_argmax_final(s->amax, lm_tiles(c),
                               (int)s->B, s->tok, nullptr, s->hist,
@@ -986,7 +1014,7 @@ extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,
                                                      uint32_t reps,
                                                      float* avg_ms) {
   CHECK_ARG(s && avg_ms && reps > 0, "akh_session_time_decode_kernel: bad argument");
-  CHECK_ARG(kernel >= 0 && kernel <= 5, "akh_session_time_decode_kernel: bad kernel");
+  CHECK_ARG(kernel >= 0 && kernel <= 6, "akh_session_time_decode_kernel: bad kernel");
   for (uint32_t b = 0; b < s->B; ++b)
     CHECK_ARG(s->cur_len[b] >= 1 && s->cur_len[b] < s->max_ctx,
               "akh_session_time_decode_kernel: needs 1 <= cur_len < max_ctx");
@@ -998,7 +1026,9 @@ extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,
       case 2: return enqueue_out(s, 0);
       case 3: return enqueue_up(s, 0);
       case 4: return enqueue_down(s, 0);
-      default: return enqueue_lm_head(s);
+      case 5: return enqueue_lm_head(s);
+      default:
+        return enqueue_resid_norm(s, s->p_out, s->ks_out, s->m->layer(0, W_NORM2));
     }
   };
   HIP_TRY(one());  // warm

@@ -139,19 +139,21 @@ def main():
     sess.truncate(P)
     sess.decode_greedy(32, want_tokens=False)
     T = P + 32 + 1
-    names = ["decode_attn", "qkv_rope_append", "out_proj_residual", "ffn_up_silu",
-             "ffn_down_residual", "lm_head_argmax"]
+    names = ["decode_attn", "qkv_proj", "out_proj", "ffn_up", "ffn_down",
+             "lm_head_argmax", "resid_norm"]
     kms = {n: sess.time_decode_kernel(i, args.kernel_reps) for i, n in enumerate(names)}
     d, L, V, F = cfg.dim, cfg.num_layers, cfg.vocab_size, cfg.ffn_hidden
+    # Compulsory bytes per launch: weights once, activations in and out once.
     attn_bytes = 2 * B * T * d * 4 + 2 * B * d * 4
     attn_gbs = attn_bytes / (kms["decode_attn"] / 1e3) / 1e9
     kbytes = {
         "decode_attn": attn_bytes,
-        "qkv_rope_append": d * 3 * d * 4 + d * 4 + B * 3 * d * 4,
-        "out_proj_residual": d * d * 4 + 3 * B * d * 4,
-        "ffn_up_silu": d * F * 4 + d * 4 + B * (d + F) * 4,
-        "ffn_down_residual": F * d * 4 + B * (F + 2 * d) * 4,
-        "lm_head_argmax": d * V * 4 + d * 4 + B * V * 4,
+        "qkv_proj": d * 3 * d * 4 + B * 4 * d * 4,
+        "out_proj": d * d * 4 + 2 * B * d * 4,
+        "ffn_up": d * F * 4 + B * (d + F) * 4,
+        "ffn_down": F * d * 4 + B * (F + d) * 4,
+        "lm_head_argmax": d * V * 4 + B * d * 4 + B * V * 4,
+        "resid_norm": 4 * B * d * 4 + d * 4,
     }
     kernels = {n: {"ms": round(kms[n], 5), "bytes": kbytes[n],
                    "GB/s": round(kbytes[n] / (kms[n] / 1e3) / 1e9, 1)} for n in names}

@@ -239,7 +239,9 @@ akh_status akh_timer_stop(akh_backend* be, float* ms);
 /* Replay one kernel of the decode step `reps` times alone between events
  * and report its mean duration.  kernel: 0 = attention of layer 0,
  * 1 = qkv projection, 2 = out projection, 3 = ffn up, 4 = ffn down,
- * 5 = lm_head. */
+ * 5 = lm_head, 6 = residual add + RMSNorm.  The step's buffers are reused:
+ * the residual stream is clobbered until the next decode step rewrites it
+ * from the embedding. */
 akh_status akh_session_time_decode_kernel(akh_session* s, int kernel,
                                           uint32_t reps, float* avg_ms);
 
