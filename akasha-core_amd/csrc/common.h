@@ -109,4 +109,30 @@ __device__ __forceinline__ size_t kq_index(int m, int k) {
   return ((size_t)(k >> 2) * 32 + m) * 4 + (k & 3);
 }
 
+__device__ __forceinline__ void add4(float4& a, const float4 b) {
+  a.x += b.x;
+  a.y += b.y;
+  a.z += b.z;
+  a.w += b.w;
+}
+
+// acc + p[0] + p[stride] + ... + p[(n - 1) * stride], added in index order.
+// The loads are issued NB at a time, so NB partials cost one memory latency
+// instead of NB dependent ones.
+template <int NB>
+__device__ __forceinline__ float4 sum_parts4(float4 acc, const float* p,
+                                             size_t stride, int n) {
+  int s = 0;
+  for (; s + NB <= n; s += NB) {
+    float4 t[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      t[i] = *reinterpret_cast<const float4*>(p + (size_t)(s + i) * stride);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) add4(acc, t[i]);
+  }
+  for (; s < n; ++s) add4(acc, *reinterpret_cast<const float4*>(p + (size_t)s * stride));
+  return acc;
+}
+
 }  // namespace akh

@@ -17,6 +17,8 @@
 // are used, so results are deterministic.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -85,14 +87,7 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
       if (4 * kq < ke) {
         const size_t off = ((size_t)kq * 32 + j) * 4;
         if (PRO == PRO_SILU_SUM) {
-          for (int s = 0; s < p.nparts; ++s) {
-            const float4 v =
-                *reinterpret_cast<const float4*>(p.xt + (size_t)s * 32 * K + off);
-            t.x += v.x;
-            t.y += v.y;
-            t.z += v.z;
-            t.w += v.w;
-          }
+          t = sum_parts4<4>(t, p.xt + off, (size_t)32 * K, p.nparts);
           t = make_float4(silu(t.x), silu(t.y), silu(t.z), silu(t.w));
         } else {
           t = *reinterpret_cast<const float4*>(p.xt + off);
@@ -167,6 +162,134 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   }
 }
 
+// lm_head (logits = A . W, K <= 2*W*HL) and the first maximum of every row.
+//
+// A persistent grid of G blocks (one per CU): block b owns the 32-column
+// tiles b, b+G, b+2G, ... in increasing order.  Wave w covers rows
+// [2*HL*w, 2*HL*(w+1)) of K, the MFMA k-pair u taking rows 2u and 2u+1 of
+// that range (one per half-wave), so its A operand (HL floats per lane) is
+// loaded once and stays in registers; the weights of the block's next tile
+// are loaded while the MFMAs of the current one run.  The W per-wave 32x32
+// tiles are summed in LDS (waves in order), each wave finishing 32/W rows:
+// it stores their logits and keeps a running (value, index) maximum per row.
+// amax[m, b] is the first maximum of row m over block b's columns.
+
+// Weights of tile `tile` for k-pairs u < HL of a wave, through a buffer
+// resource: the per-lane part of the address (half-wave row and column) is
+// one VGPR, the row-pair and tile offsets are scalar.  K is even, so a pair
+// is wholly inside or outside [0, K); pairs outside re-read the last pair
+// (their A is zero).  Lanes whose column is at or beyond N (including every
+// lane of a tile past the end) take an offset outside the resource, which
+// reads as zero without touching memory.
+template <int HL>
+__device__ __forceinline__ void lm_load_b(float (&bb)[HL], __amdgpu_buffer_rsrc_t w,
+                                          uint32_t voff, int N, int K, int kr0,
+                                          int tile, int j) {
+  // Bit 31 of the aux operand marks the loads volatile: the compiler keeps
+  // them where they are issued instead of sinking them to their first use
+  // (which would serialise the prefetch), and gives them system-scope
+  // coherence bits, harmless for weights that are read once per step.
+  constexpr int kKeepOrder = (int)0x80000000u;
+  const uint32_t vo = tile * 32 + j < N ? voff : 0x80000000u;
+#pragma unroll
+  for (int u = 0; u < HL; ++u) {
+    const int so = (min(kr0 + 2 * u, K - 2) * N + tile * 32) * 4;
+    bb[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(w, (int)vo, so, kKeepOrder));
+  }
+}
+
+template <int W, int HL>
+__device__ __forceinline__ void lm_tile(const float (&a)[HL], const float (&bb)[HL],
+                                        float (*red)[32][33], int tile, const DecGemmParams& p,
+                                        float& bv, uint32_t& bi) {
+  constexpr int RW = 32 / W;     // rows finished per wave
+  constexpr int LPR = 64 / RW;   // lanes per finished row
+  constexpr int E = 32 / LPR;    // columns per lane
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int u = 0; u < HL; ++u) acc = mfma32(a[u], bb[u], acc);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[wave][acc_row(r, h)][j] = acc[r];
+  __syncthreads();
+  const int m = wave * RW + lane / LPR;
+  const int c0 = (lane % LPR) * E;
+  float v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = red[0][m][c0 + e];
+#pragma unroll
+  for (int w = 1; w < W; ++w)
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] += red[w][m][c0 + e];
+  if (m < p.M) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int col = tile * 32 + c0 + e;
+      if (col < p.N) {
+        p.y[(size_t)m * p.N + col] = v[e];
+        amax_merge(bv, bi, v[e], (uint32_t)col);
+      }
+    }
+  }
+}
+
+template <int W, int HL>
+__global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
+  constexpr int RW = 32 / W;
+  constexpr int LPR = 64 / RW;
+  static_assert(W * RW == 32 && LPR <= 64, "W must divide 32");
+  static_assert(HL % 2 == 0, "HL must cover whole k-quads");
+  __shared__ float red[2][W][32][33];
+  const int N = p.N, K = p.K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int ntiles = (N + 31) / 32;
+  const int G = gridDim.x;
+  const int kr0 = __builtin_amdgcn_readfirstlane(wave) * 2 * HL;
+  const uint32_t voff = (uint32_t)(h * N + j) * 4u;
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.w), (short)0, K * N * 4, 0x00020000);
+
+  // a[u] = A[j][kr0 + 2u + h]: k-quad q holds pairs u = 2q and 2q + 1.
+  float a[HL];
+#pragma unroll
+  for (int q = 0; q < HL / 2; ++q) {
+    const int kq = (kr0 >> 2) + q;
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * kq < K) t = *reinterpret_cast<const float4*>(p.xt + ((size_t)kq * 32 + j) * 4);
+    a[2 * q] = h ? t.y : t.x;
+    a[2 * q + 1] = h ? t.w : t.z;
+  }
+
+  float bv = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  // cur holds this tile's weights; nxt receives the next tile's while the
+  // MFMAs run (a tile past the end reads zeros without memory traffic), and
+  // is handed over after the epilogue.
+  float cur[HL], nxt[HL];
+  lm_load_b(cur, wres, voff, N, K, kr0, blockIdx.x, j);
+  int par = 0;
+#pragma unroll 1
+  for (int tile = blockIdx.x; tile < ntiles; tile += G) {
+    lm_load_b(nxt, wres, voff, N, K, kr0, tile + G, j);
+    lm_tile<W, HL>(a, cur, red[par], tile, p, bv, bi);
+    par ^= 1;
+#pragma unroll
+    for (int u = 0; u < HL; ++u) cur[u] = nxt[u];
+  }
+  // First maximum of each finished row over this block's columns.
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const uint32_t oi = __shfl_xor(bi, o, 64);
+    amax_merge(bv, bi, ov, oi);
+  }
+  const int m = wave * RW + lane / LPR;
+  if (lane % LPR == 0 && m < p.M)
+    p.amax[(size_t)m * G + blockIdx.x] = make_uint2(__float_as_uint(bv), bi);
+}
+
 // Single-query attention over the KV cache for one (sequence, head) per
 // block, with the fused head of the layer's attention:
 //   q, k, v of the new token = the sum of the QKV GEMM's partial tiles, with
@@ -196,16 +319,11 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   // The new token's q, k, v (columns hh*HD + 4g .. +3 of each role).
   float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), kn = q4, vn = q4;
   {
-    const size_t cq = (size_t)hh * HD + 4 * g;
-    for (int s = 0; s < p.nparts; ++s) {
-      const float* row = p.qkv + ((size_t)s * 32 + b) * 3 * d;
-      const float4 a = *reinterpret_cast<const float4*>(row + cq);
-      const float4 k = *reinterpret_cast<const float4*>(row + d + cq);
-      const float4 v = *reinterpret_cast<const float4*>(row + 2 * d + cq);
-      q4.x += a.x; q4.y += a.y; q4.z += a.z; q4.w += a.w;
-      kn.x += k.x; kn.y += k.y; kn.z += k.z; kn.w += k.w;
-      vn.x += v.x; vn.y += v.y; vn.z += v.z; vn.w += v.w;
-    }
+    const float* row = p.qkv + (size_t)b * 3 * d + (size_t)hh * HD + 4 * g;
+    const size_t ps = (size_t)32 * 3 * d;
+    q4 = sum_parts4<4>(q4, row, ps, p.nparts);
+    kn = sum_parts4<4>(kn, row + d, ps, p.nparts);
+    vn = sum_parts4<4>(vn, row + 2 * d, ps, p.nparts);
     // Pairs (4g, 4g+1) and (4g+2, 4g+3) of the head: rope entries 2g, 2g+1.
     const float2 c0 = p.rope[(size_t)pos * (HD / 2) + 2 * g];
     const float2 c1 = p.rope[(size_t)pos * (HD / 2) + 2 * g + 1];
@@ -345,15 +463,8 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
       if (gather) {
         if (row) v = *reinterpret_cast<const float4*>(row + 4 * q);
       } else {
-        v = *reinterpret_cast<const float4*>(xq);
-        for (int s = 0; s < p.nparts; ++s) {
-          const float4 t =
-              *reinterpret_cast<const float4*>(p.parts + ((size_t)s * 32 + m) * d + 4 * q);
-          v.x += t.x;
-          v.y += t.y;
-          v.z += t.z;
-          v.w += t.w;
-        }
+        v = sum_parts4<8>(*reinterpret_cast<const float4*>(xq),
+                          p.parts + (size_t)m * d + 4 * q, (size_t)32 * d, p.nparts);
       }
       *reinterpret_cast<float4*>(xq) = v;
       ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
@@ -408,15 +519,35 @@ __global__ __launch_bounds__(256) void k_argmax_final(
 namespace {
 
 // Launch shapes per role (C sub-tiles, W waves, HL rows per half-wave),
-// chosen by a sweep on MI355X.  The four layer GEMMs split K into many
-// small blocks; lm_head runs whole-K blocks of 128 columns.
+// chosen by timing whole decode steps on MI355X; each can be overridden at
+// build time, e.g. -DAKH_SHAPE_QKV=1,4,24.  The four layer GEMMs split K
+// into a few chunks (enough blocks to occupy the GPU, few partial tiles for
+// the consumer to sum); lm_head runs whole-K blocks.
+#ifndef AKH_SHAPE_QKV
+#define AKH_SHAPE_QKV 1, 4, 24
+#endif
+#ifndef AKH_SHAPE_OUT
+#define AKH_SHAPE_OUT 1, 4, 12
+#endif
+#ifndef AKH_SHAPE_UP
+#define AKH_SHAPE_UP 1, 8, 24
+#endif
+#ifndef AKH_SHAPE_DOWN
+#define AKH_SHAPE_DOWN 1, 8, 8
+#endif
+#ifndef AKH_SHAPE_LM
+#define AKH_SHAPE_LM 4, 4, 16
+#endif
 template <int ROLE>
 struct RoleShape;
-template <> struct RoleShape<DEC_CFG_QKV> { static constexpr int C = 1, W = 2, HL = 16; };
-template <> struct RoleShape<DEC_CFG_OUT> { static constexpr int C = 1, W = 2, HL = 8; };
-template <> struct RoleShape<DEC_CFG_UP> { static constexpr int C = 1, W = 2, HL = 16; };
-template <> struct RoleShape<DEC_CFG_DOWN> { static constexpr int C = 1, W = 2, HL = 16; };
-template <> struct RoleShape<DEC_CFG_LM> { static constexpr int C = 4, W = 4, HL = 16; };
+#define AKH_ROLE_SHAPE(R, c, w, hl) \
+  template <> struct RoleShape<R> { static constexpr int C = c, W = w, HL = hl; };
+#define AKH_ROLE_SHAPE_(...) AKH_ROLE_SHAPE(__VA_ARGS__)
+AKH_ROLE_SHAPE_(DEC_CFG_QKV, AKH_SHAPE_QKV)
+AKH_ROLE_SHAPE_(DEC_CFG_OUT, AKH_SHAPE_OUT)
+AKH_ROLE_SHAPE_(DEC_CFG_UP, AKH_SHAPE_UP)
+AKH_ROLE_SHAPE_(DEC_CFG_DOWN, AKH_SHAPE_DOWN)
+AKH_ROLE_SHAPE_(DEC_CFG_LM, AKH_SHAPE_LM)
 
 template <int ROLE>
 int role_splits(int K) {
@@ -446,7 +577,31 @@ int dec_gemm_splits(int role, int K) {
   }
 }
 
-int dec_lm_tile_cols() { return 32 * RoleShape<DEC_CFG_LM>::C; }
+// lm_head: the persistent kernel covers K <= 2 * 8 * 64 (A held in
+// registers) and weights under 2 GiB (32-bit buffer offsets); other shapes
+// run the generic GEMM (128-column whole-K blocks).
+namespace {
+bool lm_persistent(int N, int K) { return K <= 1024 && (long)K * N * 4 < (1l << 31); }
+}  // namespace
+
+int dec_lm_parts(int N, int K, int num_cus) {
+  if (lm_persistent(N, K)) return std::max(1, std::min((N + 31) / 32, num_cus));
+  constexpr int NT = 32 * RoleShape<DEC_CFG_LM>::C;
+  return (N + NT - 1) / NT;
+}
+
+hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s) {
+  const dim3 g(dec_lm_parts(p.N, p.K, num_cus));
+  if (!lm_persistent(p.N, p.K))
+    return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
+  if (p.K <= 256)
+    hipLaunchKernelGGL((k_dec_lm<8, 16>), g, dim3(512), 0, s, p);
+  else if (p.K <= 768)
+    hipLaunchKernelGGL((k_dec_lm<8, 48>), g, dim3(512), 0, s, p);
+  else if (p.K <= 1024)
+    hipLaunchKernelGGL((k_dec_lm<8, 64>), g, dim3(512), 0, s, p);
+  return hipGetLastError();
+}
 
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
   switch (role) {
@@ -454,7 +609,6 @@ hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
     case DEC_CFG_OUT: return dec_go<DEC_CFG_OUT, DEC_PART, PRO_NONE>(p, s);
     case DEC_CFG_UP: return dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NONE>(p, s);
     case DEC_CFG_DOWN: return dec_go<DEC_CFG_DOWN, DEC_PART, PRO_SILU_SUM>(p, s);
-    case DEC_CFG_LM: return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
   }
   return hipErrorInvalidValue;
 }

@@ -142,10 +142,15 @@ struct DecGemmParams {
 };
 
 // Number of K chunks (partial tiles) a role's GEMM produces for contraction
-// length K, and the column count of one lm_head tile.
+// length K.
 int dec_gemm_splits(int role, int K);
-int dec_lm_tile_cols();
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s);
+
+// lm_head: logits y[M, N] = xt . w and argmax partials amax[M, parts], where
+// parts = dec_lm_parts(N, K, num_cus) (each the first maximum of the row
+// over a subset of the columns).
+int dec_lm_parts(int N, int K, int num_cus);
+hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s);
 
 struct DecAttnParams {
   const float* qkv;  // nparts partial tiles [nparts][32][3*d]

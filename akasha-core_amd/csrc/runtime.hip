@@ -507,9 +507,8 @@ struct akh_session {
 
 namespace {
 
-int lm_tiles(const akh_model_config& c) {
-  const int cols = dec_lm_tile_cols();
-  return (int)((c.vocab_size + cols - 1) / cols);
+int lm_parts(const akh_session* s) {
+  return dec_lm_parts((int)s->m->cfg.vocab_size, (int)s->m->cfg.dim, s->be->num_cus);
 }
 
 void free_prefill(akh_session* s) {
@@ -650,7 +649,7 @@ hipError_t enqueue_lm_head(akh_session* s) {
   p.amax = s->amax;
   p.N = c.vocab_size;
   p.K = c.dim;
-  return launch_dec_gemm(p, DEC_CFG_LM, s->be->stream);
+  return launch_dec_lm(p, s->be->num_cus, s->be->stream);
 }
 
 // One decode step of build_decode_layer (inference_graphs.rs:339-509) for
@@ -680,7 +679,7 @@ hipError_t enqueue_decode(akh_session* s) {
   }
   if (e == hipSuccess) e = enqueue_lm_head(s);
   if (e == hipSuccess)
-    e = launch_argmax_final(s->amax, lm_tiles(c), (int)s->B, s->tok, s->pos,
+    e = launch_argmax_final(s->amax, lm_parts(s), (int)s->B, s->tok, s->pos,
                             s->hist, (int)s->max_ctx + 1, 0, st);
   return e;
 }
@@ -783,7 +782,7 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   alloc((void**)&s->p_up, (size_t)s->ks_up * R * F * 4);
   alloc((void**)&s->p_down, (size_t)s->ks_down * R * d * 4);
   alloc((void**)&s->logits, R * V * 4);
-  alloc((void**)&s->amax, R * (size_t)lm_tiles(c) * sizeof(uint2));
+  alloc((void**)&s->amax, R * (size_t)lm_parts(s) * sizeof(uint2));
   alloc((void**)&s->tok, R * 4);
   alloc((void**)&s->pos, R * 4);
   alloc((void**)&s->hist, (size_t)batch * (max_context_len + 1) * 4);
@@ -939,7 +938,7 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     HIP_TRY(launch_rows_norm(r, (int)s->B, st));
   }
   HIP_TRY(enqueue_lm_head(s));
-  HIP_TRY(launch_argmax_final(s->amax, lm_tiles(c),
+  HIP_TRY(launch_argmax_final(s->amax, lm_parts(s),
                               (int)s->B, s->tok, nullptr, s->hist,
                               (int)s->max_ctx + 1, (int)S, st));
   std::fill(s->cur_len.begin(), s->cur_len.end(), S);
