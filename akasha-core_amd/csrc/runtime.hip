@@ -1018,21 +1018,23 @@ extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,
     CHECK_ARG(s->cur_len[b] >= 1 && s->cur_len[b] < s->max_ctx,
               "akh_session_time_decode_kernel: needs 1 <= cur_len < max_ctx");
   akh_backend* be = s->be;
-  auto one = [&]() -> hipError_t {
+  const uint32_t L = s->m->cfg.num_layers;
+  auto one = [&](uint32_t i) -> hipError_t {
+    const uint32_t l = i % L;
     switch (kernel) {
-      case 0: return enqueue_attn(s, 0);
-      case 1: return enqueue_qkv(s, 0);
-      case 2: return enqueue_out(s, 0);
-      case 3: return enqueue_up(s, 0);
-      case 4: return enqueue_down(s, 0);
+      case 0: return enqueue_attn(s, l);
+      case 1: return enqueue_qkv(s, l);
+      case 2: return enqueue_out(s, l);
+      case 3: return enqueue_up(s, l);
+      case 4: return enqueue_down(s, l);
       case 5: return enqueue_lm_head(s);
       default:
-        return enqueue_resid_norm(s, s->p_out, s->ks_out, s->m->layer(0, W_NORM2));
+        return enqueue_resid_norm(s, s->p_out, s->ks_out, s->m->layer(l, W_NORM2));
     }
   };
-  HIP_TRY(one());  // warm
+  for (uint32_t l = 0; l < L; ++l) HIP_TRY(one(l));  // warm
   HIP_TRY(hipEventRecord(be->t0, be->stream));
-  for (uint32_t i = 0; i < reps; ++i) HIP_TRY(one());
+  for (uint32_t i = 0; i < reps; ++i) HIP_TRY(one(i));
   HIP_TRY(hipEventRecord(be->t1, be->stream));
   HIP_TRY(hipEventSynchronize(be->t1));
   float ms = 0.f;

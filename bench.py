@@ -7,11 +7,13 @@ decode at batch 32 -- every sequence prefilled with 448 random tokens
 512 tokens.  A "step" is one decode step of all 32 sequences (embedding ->
 12 layers -> lm_head -> argmax, graph-replayed, tokens fed back on the
 device).  ``value`` = 32 * steps / time (tok/s), inputs resident in HBM.
-Windows of up to 64 steps are replayed from position 448 (the cache is
-truncated back to 448 between windows).
+The default 64 steps are exactly positions 448..511; more steps replay
+windows of up to 64 from position 448 (the cache is truncated back to 448
+between windows).
 
 Also reported: the roofline of the dominant decode kernel (single-query
-attention over the cache, timed alone with HIP events), the whole-step HBM
+attention over the cache, its launches cycled over the layers and timed
+with HIP events on the session's stream), the whole-step HBM
 roofline, per-kernel times, config-3 prefill (16 x 512) throughput against
 the fp32 MFMA peak, and the CPU baseline: the oracle's decode step (a C
 restatement of the reference CPU backend) on this host.
@@ -39,6 +41,19 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def measured_traffic(path=ROOT / "profiles" / "decode_attn_b32_ctx512_pmc.md"):
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (counters cannot be read from
+    inside this process); None if the summary is absent."""
+    try:
+        for line in Path(path).read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def decode_step_bytes(cfg, B, T):
@@ -80,11 +95,11 @@ def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
-    ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--kernel-reps", type=int, default=60)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -135,7 +150,8 @@ def main():
         done += k
     step_gbs = total_bytes / (ms / 1e3) / 1e9
 
-    # Dominant kernel: decode attention of layer 0 at T = 481 (pos 480).
+    # Dominant kernel: decode attention at T = 481 (pos 480), launches cycled
+    # over the 12 layers so each reads its KV rows from HBM as in a step.
     sess.truncate(P)
     sess.decode_greedy(32, want_tokens=False)
     T = P + 32 + 1
@@ -215,9 +231,10 @@ def main():
                                "prefill 448 (seed 4), positions 448..511 (KV 449..512)",
                    "model": "akasha-hall-1.0 (162M)", "global_batch": B, "seq_len": CTX,
                    "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": "decode_attn (layer 0, T=481)", "bound": "hbm",
+        "roofline": {"kernel": "decode_attn (T=481, layers cycled)", "bound": "hbm",
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "algorithmic_bytes": attn_bytes},
         "step_roofline": {"achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                           "bytes_per_step_mean": int(total_bytes / args.steps)},

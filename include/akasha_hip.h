@@ -236,12 +236,16 @@ akh_status akh_session_download_cache(akh_session* s, uint32_t layer,
  * waits for completion and returns the elapsed milliseconds. */
 akh_status akh_timer_start(akh_backend* be);
 akh_status akh_timer_stop(akh_backend* be, float* ms);
-/* Replay one kernel of the decode step `reps` times alone between events
- * and report its mean duration.  kernel: 0 = attention of layer 0,
- * 1 = qkv projection, 2 = out projection, 3 = ffn up, 4 = ffn down,
- * 5 = lm_head, 6 = residual add + RMSNorm.  The step's buffers are reused:
- * the residual stream is clobbered until the next decode step rewrites it
- * from the embedding. */
+/* Replay one kernel of the decode step `reps` times between events and
+ * report its mean duration.  kernel: 0 = attention, 1 = qkv projection,
+ * 2 = out projection, 3 = ffn up, 4 = ffn down, 5 = lm_head, 6 = residual
+ * add + RMSNorm.  Launches cycle over the layers, so each one reads weights
+ * and KV rows that the other layers' launches have pushed out of the
+ * caches, as in a decode step (lm_head has one weight matrix).  The step's
+ * buffers are reused: the residual stream is clobbered until the next decode
+ * step rewrites it from the embedding, and attention writes the cache row at
+ * each sequence's next position, which the next decode step rewrites before
+ * reading it. */
 akh_status akh_session_time_decode_kernel(akh_session* s, int kernel,
                                           uint32_t reps, float* avg_ms);
 
