@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the akasha-core inference hot path on one MI355X.
 
-Headline (BASELINE.json metric, config 4): akasha-hall 1.0 fp32 greedy
+Headline metric (config 4): akasha-hall 1.0 fp32 greedy
 decode at batch 32 -- every sequence prefilled with 448 random tokens
 (seed 4), then decode steps at positions 448..511 so the KV cache reaches
 512 tokens.  A "step" is one decode step of all 32 sequences (embedding ->

@@ -3,7 +3,7 @@
  * akasha-core's inference path.
  *
  * This is the surface a Rust `hip` feature of akasha-core / wilupgu binds
- * through a thin FFI crate (see INTEGRATION.md for the binding).  It has
+ * through a thin FFI crate.  It has
  * three layers, each replacing a reference interface:
  *
  *   1. Backend, tensors and graphs: wilupgu's Backend / Tensor / ComputeGraph

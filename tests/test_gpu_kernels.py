@@ -160,7 +160,7 @@ def test_flash_attention(backend, pkg, ora, seq, heads, hd):
 
 
 def test_flash_attention_c2_config(backend, pkg, ora):
-    # batch 8, 12 heads, seq 512, head_dim 64, N(0,1)
+    # Config 2: batch 8, 12 heads, seq 512, head_dim 64, N(0,1)
     # from seed 2, scale 1/8; sequences are row_offset slices of [8*512, 768].
     h = pkg.hip
     B, S, H, hd = 8, 512, 12, 64

@@ -1,6 +1,6 @@
 """The batched InferenceSession of libakasha_hip.so against the CPU oracle.
 
-Parity bar (BASELINE.json north star): identical greedy tokens and logits
+Parity bar: identical greedy tokens and logits
 within max-abs 1e-3 on the fp32 path.  Full-size configurations are checked
 on a few sequences against the oracle and, for the whole batch, through
 size-independent properties (batch invariance, prefill == sequential
@@ -122,7 +122,7 @@ def test_session_errors(backend, pkg):
 
 
 def test_hall1_c1_greedy_parity(backend, pkg, ora):
-    # akasha-hall 1.0 fp32, weights N(0,0.02) seed 0,
+    # Config 1: akasha-hall 1.0 fp32, weights N(0,0.02) seed 0,
     # 64-token prompt (seed 1), 64 greedy tokens, batch 1.
     cfg = pkg.ModelConfig.akasha_hall_1()
     w = pkg.synthetic_weights(cfg, seed=0)
@@ -150,7 +150,7 @@ def test_hall1_c1_greedy_parity(backend, pkg, ora):
 
 
 def test_hall1_c4_batch_properties(backend, pkg, ora):
-    # BASELINE config 4 at full size: 32 sequences prefilled with 448 tokens
+    # Config 4 at full size: 32 sequences prefilled with 448 tokens
     # (seed 4), then greedy decode.  Sequence 0 is checked against the
     # oracle; the batch is checked for batch invariance against single-
     # sequence sessions.
@@ -190,7 +190,7 @@ def test_hall1_c4_batch_properties(backend, pkg, ora):
 
 
 def test_hall1_c3_prefill_sequence_matches_oracle(backend, pkg, ora):
-    # BASELINE config 3 shape: 16 x 512 prefill (seed 3); two sequences
+    # Config 3 shape: 16 x 512 prefill (seed 3); two sequences
     # checked against the oracle, all sequences' greedy tokens reported.
     cfg = pkg.ModelConfig.akasha_hall_1()
     w = pkg.synthetic_weights(cfg, seed=0)
