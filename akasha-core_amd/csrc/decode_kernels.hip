@@ -26,63 +26,74 @@ namespace akh {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
-// Y (epilogue) A[M, K] . W[K, N] for M <= 32.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+// One-time packing of a [K, N] row-major matrix into 32-column tiles of
+// Kp rows in the k-quad order (see launch_pack_tiles in kernels.h).
+__global__ __launch_bounds__(256) void k_pack_tiles(const float* __restrict__ w, int K,
+                                                    int N, int Kp, float* __restrict__ out) {
+  const int j = threadIdx.x & 31;
+  const int q = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int t = blockIdx.y;
+  if (4 * q >= Kp) return;
+  const int n = t * 32 + j;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n < N) {
+    const int k = 4 * q;
+    if (k < K) v.x = w[(size_t)k * N + n];
+    if (k + 1 < K) v.y = w[(size_t)(k + 1) * N + n];
+    if (k + 2 < K) v.z = w[(size_t)(k + 2) * N + n];
+    if (k + 3 < K) v.w = w[(size_t)(k + 3) * N + n];
+  }
+  *reinterpret_cast<float4*>(out + (((size_t)t * (Kp / 4) + q) * 32 + j) * 4) = v;
+}
+
+// Y (epilogue) A[M, K] . W[K, N] for M <= 32, W packed in 32-column tiles.
 //
-// Grid (N tiles of NT = 32*C columns, K chunks), W waves per block.  A block
-// tile is C sub-tiles of 32 consecutive columns; lane (j, h) owns column
-// n0 + 32c + j of sub-tile c, so every weight load of a half-wave is one
-// 128-byte row segment.  A pass covers KC = 2*W*HL rows of K: wave w takes
-// 2*HL of them and half h of its lanes HL, each lane supplying A[j][k] (a
-// float4 of the k-quad tile covers four k) to all C sub-tiles.  All loads of
-// a pass are issued before its first MFMA.  A block runs one pass when K is
-// split over the grid, and loops over all of K otherwise.  The waves' tiles
-// are reduced in LDS as a binary tree (fixed order); wave 0 runs the
-// epilogue.
+// Grid (N / 32 tiles, K chunks), W waves per block.  Lane (j, h) owns column
+// 32 * tile + j.  A pass covers KC = 2*W*HL rows of K: wave w takes 2*HL of
+// them and half h of its lanes HL, loading, per four rows, one float4 of the
+// packed weight tile (its column, four consecutive k) and one float4 of the
+// k-quad activation (its row m = j, the same four k); a half-wave's load is
+// 512 contiguous bytes.  All loads of a pass are issued before its first
+// MFMA.  A block runs one pass when K is split over the grid, and loops over
+// all of K otherwise.  The waves' tiles are reduced in LDS as a binary tree
+// (fixed order); wave 0 runs the epilogue.
 //
 // PRO_SILU_SUM: A = silu(sum of p.nparts k-quad partial tiles at p.xt).
-template <int C, int W, int HL, int EPI, int PRO>
+template <int W, int HL, int EPI, int PRO>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
-  constexpr int NT = 32 * C;
   constexpr int RH = W > 1 ? W / 2 : 1;
   constexpr int KC = 2 * W * HL;
+  constexpr int HQ = HL / 4;
   static_assert(HL % 4 == 0, "HL must cover whole k-quads");
-  __shared__ float red[RH][32][NT + 1];
+  __shared__ float red[RH][32][33];
 
   const int M = p.M, N = p.N, K = p.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, h = lane >> 5;
-  const int tile = blockIdx.x, n0 = tile * NT;
+  const int tile = blockIdx.x, col = tile * 32 + j;
+  const bool cok = col < N;
   const int per = (K + (int)gridDim.y - 1) / (int)gridDim.y;
   const int rows = (per + KC - 1) / KC * KC;  // whole passes per block
   const int kb = blockIdx.y * rows;
   if (kb >= K) return;
   const int ke = min(K, kb + rows);
-  int col[C];
-  bool cok[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) {
-    col[c] = n0 + 32 * c + j;
-    cok[c] = col[c] < N;
-  }
+  const float* wt = p.w + (size_t)tile * p.Kp * 32 + j * 4;
 
-  f32x16 acc[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) acc[c] = zero16();
+  f32x16 acc = zero16();
   for (int k0 = kb; k0 < ke; k0 += KC) {
-    const int kr = k0 + wave * 2 * HL + h * HL;  // first row of this half
-    float a[HL];
-    float wv[HL][C];
+    const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;  // first k-quad of this half
+    float4 b[HQ], a[HQ];
 #pragma unroll
-    for (int u = 0; u < HL; ++u) {
-      const int k = kr + u;
-      const bool ok = k < ke;
-      const float* wr = p.w + (size_t)(ok ? k : kb) * N;
-#pragma unroll
-      for (int c = 0; c < C; ++c) wv[u][c] = (ok && cok[c]) ? wr[col[c]] : 0.f;
+    for (int q = 0; q < HQ; ++q) {
+      const int kq = kq0 + q;
+      b[q] = 4 * kq < ke ? *reinterpret_cast<const float4*>(wt + (size_t)kq * 128)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int q = 0; q < HL / 4; ++q) {
-      const int kq = (kr >> 2) + q;
+    for (int q = 0; q < HQ; ++q) {
+      const int kq = kq0 + q;
       float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
       if (4 * kq < ke) {
         const size_t off = ((size_t)kq * 32 + j) * 4;
@@ -93,15 +104,15 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
           t = *reinterpret_cast<const float4*>(p.xt + off);
         }
       }
-      a[4 * q] = t.x;
-      a[4 * q + 1] = t.y;
-      a[4 * q + 2] = t.z;
-      a[4 * q + 3] = t.w;
+      a[q] = t;
     }
 #pragma unroll
-    for (int u = 0; u < HL; ++u)
-#pragma unroll
-      for (int c = 0; c < C; ++c) acc[c] = mfma32(a[u], wv[u][c], acc[c]);
+    for (int q = 0; q < HQ; ++q) {
+      acc = mfma32(a[q].x, b[q].x, acc);
+      acc = mfma32(a[q].y, b[q].y, acc);
+      acc = mfma32(a[q].z, b[q].z, acc);
+      acc = mfma32(a[q].w, b[q].w, acc);
+    }
   }
 
   if (W > 1) {
@@ -109,44 +120,31 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
       __syncthreads();
       if (wave >= half && wave < 2 * half)
 #pragma unroll
-        for (int c = 0; c < C; ++c)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            red[wave - half][acc_row(r, h)][32 * c + j] = acc[c][r];
+        for (int r = 0; r < 16; ++r) red[wave - half][acc_row(r, h)][j] = acc[r];
       __syncthreads();
       if (wave < half)
 #pragma unroll
-        for (int c = 0; c < C; ++c)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            acc[c][r] += red[wave][acc_row(r, h)][32 * c + j];
+        for (int r = 0; r < 16; ++r) acc[r] += red[wave][acc_row(r, h)][j];
     }
   }
   if (wave != 0) return;
 
+  float bv = -INFINITY;
+  uint32_t bi = (uint32_t)col;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int m = acc_row(r, h);
     if (EPI == DEC_PART) {
-      float* y = p.y + ((size_t)blockIdx.y * 32 + m) * N;
-#pragma unroll
-      for (int c = 0; c < C; ++c)
-        if (cok[c]) y[col[c]] = acc[c][r];
+      if (cok) p.y[((size_t)blockIdx.y * 32 + m) * N + col] = acc[r];
     } else if (EPI == DEC_PART_T) {
-      float* y = p.y + (size_t)blockIdx.y * 32 * N;
-#pragma unroll
-      for (int c = 0; c < C; ++c)
-        if (cok[c]) y[kq_index(m, col[c])] = acc[c][r];
+      if (cok) p.y[(size_t)blockIdx.y * 32 * N + kq_index(m, col)] = acc[r];
     } else if (EPI == DEC_LOGITS) {
       // Logits, and the first maximum of the row over this tile's columns.
-      float bv = -INFINITY;
-      uint32_t bi = (uint32_t)col[0];
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        if (m < M && cok[c]) {
-          p.y[(size_t)m * N + col[c]] = acc[c][r];
-          amax_merge(bv, bi, acc[c][r], (uint32_t)col[c]);
-        }
+      bv = -INFINITY;
+      bi = (uint32_t)col;
+      if (m < M && cok) {
+        p.y[(size_t)m * N + col] = acc[r];
+        bv = acc[r];
       }
 #pragma unroll
       for (int o = 16; o > 0; o >>= 1) {
@@ -154,52 +152,41 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
         const uint32_t oi = __shfl_xor(bi, o, 64);
         amax_merge(bv, bi, ov, oi);
       }
-      if (j == 0 && m < M) {
-        const int ntiles = (N + NT - 1) / NT;
-        p.amax[(size_t)m * ntiles + tile] = make_uint2(__float_as_uint(bv), bi);
-      }
+      if (j == 0 && m < M)
+        p.amax[(size_t)m * gridDim.x + tile] = make_uint2(__float_as_uint(bv), bi);
     }
   }
 }
 
-// lm_head (logits = A . W, K <= 2*W*HL) and the first maximum of every row.
+// lm_head (logits = A . W, K <= Kp = 2*W*HL) and the first maximum of every
+// row, W packed in 32-column tiles of Kp rows (zero beyond K).
 //
-// A persistent grid of G blocks (one per CU): block b owns the 32-column
-// tiles b, b+G, b+2G, ... in increasing order.  Wave w covers rows
-// [2*HL*w, 2*HL*(w+1)) of K, the MFMA k-pair u taking rows 2u and 2u+1 of
-// that range (one per half-wave), so its A operand (HL floats per lane) is
-// loaded once and stays in registers; the weights of the block's next tile
-// are loaded while the MFMAs of the current one run.  The W per-wave 32x32
-// tiles are summed in LDS (waves in order), each wave finishing 32/W rows:
-// it stores their logits and keeps a running (value, index) maximum per row.
-// amax[m, b] is the first maximum of row m over block b's columns.
-
-// Weights of tile `tile` for k-pairs u < HL of a wave, through a buffer
-// resource: the per-lane part of the address (half-wave row and column) is
-// one VGPR, the row-pair and tile offsets are scalar.  K is even, so a pair
-// is wholly inside or outside [0, K); pairs outside re-read the last pair
-// (their A is zero).  Lanes whose column is at or beyond N (including every
-// lane of a tile past the end) take an offset outside the resource, which
-// reads as zero without touching memory.
-template <int HL>
-__device__ __forceinline__ void lm_load_b(float (&bb)[HL], __amdgpu_buffer_rsrc_t w,
-                                          uint32_t voff, int N, int K, int kr0,
-                                          int tile, int j) {
-  // Bit 31 of the aux operand marks the loads volatile: the compiler keeps
-  // them where they are issued instead of sinking them to their first use
-  // (which would serialise the prefetch), and gives them system-scope
-  // coherence bits, harmless for weights that are read once per step.
-  constexpr int kKeepOrder = (int)0x80000000u;
-  const uint32_t vo = tile * 32 + j < N ? voff : 0x80000000u;
+// A persistent grid of G blocks (one per CU): block b owns the tiles b, b+G,
+// b+2G, ... in increasing order.  Wave w covers rows [2*HL*w, 2*HL*(w+1))
+// and half h of its lanes HL of them, so its A operand (HL floats per lane)
+// is loaded once and stays in registers.  The weights of the block's next
+// tile are loaded while the MFMAs of the current one run, through a buffer
+// resource: the lane's offset in the tile is one VGPR, the tile and k-quad
+// offsets are scalar, and a tile past the end gets an offset outside the
+// resource, which reads as zero without touching memory.  The W per-wave
+// 32x32 tiles are summed in LDS (waves in order), each wave finishing 32/W
+// rows: it stores their logits and keeps a running (value, index) maximum
+// per row.  amax[m, b] is the first maximum of row m over block b's columns.
+template <int HQ>
+__device__ __forceinline__ void lm_load_b(float4 (&bb)[HQ], __amdgpu_buffer_rsrc_t w,
+                                          uint32_t voff, int ntiles, int Kp, int tile) {
+  const uint32_t vo = tile < ntiles ? voff : 0x80000000u;
+  const int so = tile * Kp * 128;
 #pragma unroll
-  for (int u = 0; u < HL; ++u) {
-    const int so = (min(kr0 + 2 * u, K - 2) * N + tile * 32) * 4;
-    bb[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(w, (int)vo, so, kKeepOrder));
+  for (int q = 0; q < HQ; ++q) {
+    const f32x4v v = __builtin_bit_cast(
+        f32x4v, __builtin_amdgcn_raw_buffer_load_b128(w, (int)vo, so + q * 512, 0));
+    bb[q] = make_float4(v.x, v.y, v.z, v.w);
   }
 }
 
-template <int W, int HL>
-__device__ __forceinline__ void lm_tile(const float (&a)[HL], const float (&bb)[HL],
+template <int W, int HQ>
+__device__ __forceinline__ void lm_tile(const float4 (&a)[HQ], const float4 (&bb)[HQ],
                                         float (*red)[32][33], int tile, const DecGemmParams& p,
                                         float& bv, uint32_t& bi) {
   constexpr int RW = 32 / W;     // rows finished per wave
@@ -209,7 +196,12 @@ __device__ __forceinline__ void lm_tile(const float (&a)[HL], const float (&bb)[
   const int j = lane & 31, h = lane >> 5;
   f32x16 acc = zero16();
 #pragma unroll
-  for (int u = 0; u < HL; ++u) acc = mfma32(a[u], bb[u], acc);
+  for (int q = 0; q < HQ; ++q) {
+    acc = mfma32(a[q].x, bb[q].x, acc);
+    acc = mfma32(a[q].y, bb[q].y, acc);
+    acc = mfma32(a[q].z, bb[q].z, acc);
+    acc = mfma32(a[q].w, bb[q].w, acc);
+  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) red[wave][acc_row(r, h)][j] = acc[r];
   __syncthreads();
@@ -238,45 +230,45 @@ template <int W, int HL>
 __global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
   constexpr int RW = 32 / W;
   constexpr int LPR = 64 / RW;
+  constexpr int HQ = HL / 4;
   static_assert(W * RW == 32 && LPR <= 64, "W must divide 32");
-  static_assert(HL % 2 == 0, "HL must cover whole k-quads");
+  static_assert(HL % 4 == 0, "HL must cover whole k-quads");
   __shared__ float red[2][W][32][33];
-  const int N = p.N, K = p.K;
+  const int N = p.N, K = p.K, Kp = p.Kp;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, h = lane >> 5;
   const int ntiles = (N + 31) / 32;
   const int G = gridDim.x;
-  const int kr0 = __builtin_amdgcn_readfirstlane(wave) * 2 * HL;
-  const uint32_t voff = (uint32_t)(h * N + j) * 4u;
+  const int kq0 = (wave * 2 * HL + h * HL) >> 2;  // first k-quad of this half
+  const uint32_t voff = (uint32_t)(kq0 * 32 + j) * 16u;
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(p.w), (short)0, K * N * 4, 0x00020000);
+      const_cast<float*>(p.w), (short)0, ntiles * Kp * 128, 0x00020000);
 
-  // a[u] = A[j][kr0 + 2u + h]: k-quad q holds pairs u = 2q and 2q + 1.
-  float a[HL];
+  float4 a[HQ];
 #pragma unroll
-  for (int q = 0; q < HL / 2; ++q) {
-    const int kq = (kr0 >> 2) + q;
-    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * kq < K) t = *reinterpret_cast<const float4*>(p.xt + ((size_t)kq * 32 + j) * 4);
-    a[2 * q] = h ? t.y : t.x;
-    a[2 * q + 1] = h ? t.w : t.z;
+  for (int q = 0; q < HQ; ++q) {
+    const int kq = kq0 + q;
+    a[q] = 4 * kq < K ? *reinterpret_cast<const float4*>(p.xt + ((size_t)kq * 32 + j) * 4)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
   float bv = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
   // cur holds this tile's weights; nxt receives the next tile's while the
-  // MFMAs run (a tile past the end reads zeros without memory traffic), and
-  // is handed over after the epilogue.
-  float cur[HL], nxt[HL];
-  lm_load_b(cur, wres, voff, N, K, kr0, blockIdx.x, j);
+  // MFMAs run, and is handed over after the epilogue.
+  float4 cur[HQ], nxt[HQ];
+  lm_load_b(cur, wres, voff, ntiles, Kp, blockIdx.x);
   int par = 0;
 #pragma unroll 1
   for (int tile = blockIdx.x; tile < ntiles; tile += G) {
-    lm_load_b(nxt, wres, voff, N, K, kr0, tile + G, j);
-    lm_tile<W, HL>(a, cur, red[par], tile, p, bv, bi);
+    lm_load_b(nxt, wres, voff, ntiles, Kp, tile + G);
+    // Compiler-only barrier: the prefetch stays issued here instead of being
+    // sunk to its first use after the MFMAs (which would serialise it).
+    asm volatile("" ::: "memory");
+    lm_tile<W, HQ>(a, cur, red[par], tile, p, bv, bi);
     par ^= 1;
 #pragma unroll
-    for (int u = 0; u < HL; ++u) cur[u] = nxt[u];
+    for (int q = 0; q < HQ; ++q) cur[q] = nxt[q];
   }
   // First maximum of each finished row over this block's columns.
 #pragma unroll
@@ -518,30 +510,31 @@ __global__ __launch_bounds__(256) void k_argmax_final(
 
 namespace {
 
-// Launch shapes per role (C sub-tiles, W waves, HL rows per half-wave),
-// chosen by timing whole decode steps on MI355X; each can be overridden at
-// build time, e.g. -DAKH_SHAPE_QKV=1,4,24.  The four layer GEMMs split K
-// into a few chunks (enough blocks to occupy the GPU, few partial tiles for
-// the consumer to sum); lm_head runs whole-K blocks.
+// Launch shapes per role (W waves, HL rows per half-wave), chosen by timing
+// whole decode steps on MI355X; each can be overridden at build time, e.g.
+// -DAKH_SHAPE_QKV=4,24.  The four layer GEMMs split K into a few chunks
+// (enough blocks to occupy the GPU, few partial tiles for the consumer to
+// sum); the generic lm_head (K beyond the persistent kernel's reach) runs
+// whole-K blocks.
 #ifndef AKH_SHAPE_QKV
-#define AKH_SHAPE_QKV 1, 4, 24
+#define AKH_SHAPE_QKV 4, 24
 #endif
 #ifndef AKH_SHAPE_OUT
-#define AKH_SHAPE_OUT 1, 4, 12
+#define AKH_SHAPE_OUT 4, 12
 #endif
 #ifndef AKH_SHAPE_UP
-#define AKH_SHAPE_UP 1, 8, 24
+#define AKH_SHAPE_UP 8, 24
 #endif
 #ifndef AKH_SHAPE_DOWN
-#define AKH_SHAPE_DOWN 1, 8, 8
+#define AKH_SHAPE_DOWN 8, 8
 #endif
 #ifndef AKH_SHAPE_LM
-#define AKH_SHAPE_LM 4, 4, 16
+#define AKH_SHAPE_LM 4, 16
 #endif
 template <int ROLE>
 struct RoleShape;
-#define AKH_ROLE_SHAPE(R, c, w, hl) \
-  template <> struct RoleShape<R> { static constexpr int C = c, W = w, HL = hl; };
+#define AKH_ROLE_SHAPE(R, w, hl) \
+  template <> struct RoleShape<R> { static constexpr int W = w, HL = hl; };
 #define AKH_ROLE_SHAPE_(...) AKH_ROLE_SHAPE(__VA_ARGS__)
 AKH_ROLE_SHAPE_(DEC_CFG_QKV, AKH_SHAPE_QKV)
 AKH_ROLE_SHAPE_(DEC_CFG_OUT, AKH_SHAPE_OUT)
@@ -559,13 +552,35 @@ int role_splits(int K) {
 template <int ROLE, int EPI, int PRO>
 hipError_t dec_go(const DecGemmParams& p, hipStream_t s) {
   using S = RoleShape<ROLE>;
-  hipLaunchKernelGGL((k_dec_gemm<S::C, S::W, S::HL, EPI, PRO>),
-                     dim3((p.N + 32 * S::C - 1) / (32 * S::C), role_splits<ROLE>(p.K)),
-                     dim3(64 * S::W), 0, s, p);
+  hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO>),
+                     dim3((p.N + 31) / 32, role_splits<ROLE>(p.K)), dim3(64 * S::W), 0,
+                     s, p);
   return hipGetLastError();
 }
 
+// The persistent lm_head covers K <= 2 * 8 * 64 (A held in registers) and
+// packed weights under 2 GiB (32-bit buffer offsets); its tiles are padded
+// to exactly 2 * 8 * HL rows.
+int lm_rows(int K) { return K <= 256 ? 256 : K <= 768 ? 768 : 1024; }
+bool lm_persistent(int N, int K) {
+  return K <= 1024 && (long)((N + 31) / 32) * lm_rows(K) * 128 < (1l << 31);
+}
+
 }  // namespace
+
+hipError_t launch_pack_tiles(const float* w, int K, int N, int Kp, float* out,
+                             hipStream_t s) {
+  if (K <= 0 || N <= 0 || Kp < K || Kp % 4 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pack_tiles, dim3((Kp / 4 + 7) / 8, (N + 31) / 32), dim3(256), 0, s,
+                     w, K, N, Kp, out);
+  return hipGetLastError();
+}
+
+int dec_packed_rows(int role, int K) {
+  const int K4 = (K + 3) / 4 * 4;
+  if (role == DEC_CFG_LM && K <= 1024) return lm_rows(K);
+  return K4;
+}
 
 int dec_gemm_splits(int role, int K) {
   switch (role) {
@@ -577,28 +592,20 @@ int dec_gemm_splits(int role, int K) {
   }
 }
 
-// lm_head: the persistent kernel covers K <= 2 * 8 * 64 (A held in
-// registers) and weights under 2 GiB (32-bit buffer offsets); other shapes
-// run the generic GEMM (128-column whole-K blocks).
-namespace {
-bool lm_persistent(int N, int K) { return K <= 1024 && (long)K * N * 4 < (1l << 31); }
-}  // namespace
-
 int dec_lm_parts(int N, int K, int num_cus) {
   if (lm_persistent(N, K)) return std::max(1, std::min((N + 31) / 32, num_cus));
-  constexpr int NT = 32 * RoleShape<DEC_CFG_LM>::C;
-  return (N + NT - 1) / NT;
+  return (N + 31) / 32;
 }
 
 hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s) {
+  if (!lm_persistent(p.N, p.K)) return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
+  if (p.Kp != lm_rows(p.K)) return hipErrorInvalidValue;
   const dim3 g(dec_lm_parts(p.N, p.K, num_cus));
-  if (!lm_persistent(p.N, p.K))
-    return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
-  if (p.K <= 256)
+  if (p.Kp == 256)
     hipLaunchKernelGGL((k_dec_lm<8, 16>), g, dim3(512), 0, s, p);
-  else if (p.K <= 768)
+  else if (p.Kp == 768)
     hipLaunchKernelGGL((k_dec_lm<8, 48>), g, dim3(512), 0, s, p);
-  else if (p.K <= 1024)
+  else
     hipLaunchKernelGGL((k_dec_lm<8, 64>), g, dim3(512), 0, s, p);
   return hipGetLastError();
 }

@@ -135,11 +135,21 @@ enum DecCfg : int {
 struct DecGemmParams {
   const float* xt;  // A operand (k-quad), or nparts k-quad partial tiles
   int nparts;
-  const float* w;   // [K, N] row-major
-  int M, N, K;
+  const float* w;   // weights packed by launch_pack_tiles (Kp rows per tile)
+  int M, N, K, Kp;
   float* y;         // partial tiles or logits
-  uint2* amax;      // DEC_LOGITS: [32, ntiles] (value bits, index)
+  uint2* amax;      // DEC_LOGITS: [32, parts] (value bits, index)
 };
+
+// Decode weights are read from a copy packed once at upload: 32-column
+// tiles, each [Kp/4][32][4] (element (k, n) of tile t = n / 32 at
+// ((k / 4) * 32 + n % 32) * 4 + k % 4), zero-filled beyond K and N.  A block
+// streams one contiguous region, and a lane's float4 holds four consecutive
+// k of its column: four MFMA B operands in one load.
+hipError_t launch_pack_tiles(const float* w, int K, int N, int Kp, float* out,
+                             hipStream_t s);
+// Rows Kp of a role's packed tiles (K, or more for lm_head's padding).
+int dec_packed_rows(int role, int K);
 
 // Number of K chunks (partial tiles) a role's GEMM produces for contraction
 // length K.

@@ -375,16 +375,28 @@ extern "C" akh_status akh_argmax_rows(akh_backend* be, const float* logits,
 // Model weights
 // ---------------------------------------------------------------------------
 
+// A weight matrix as the decode kernels read it: packed 32-column tiles of
+// `rows` k (launch_pack_tiles), refreshed whenever the parameter is uploaded.
+struct PackedMatrix {
+  float* w = nullptr;
+  int K = 0, N = 0, rows = 0;
+};
+
 struct akh_model {
   akh_backend* be = nullptr;
   akh_model_config cfg{};
   std::vector<float*> params;  // ModelWeights::params() order
   std::vector<size_t> counts;
+  std::vector<PackedMatrix> packed;  // per parameter; w == nullptr if not a decode matrix
 
   float* embedding() const { return params[0]; }
   float* layer(uint32_t l, int which) const { return params[1 + 6 * l + which]; }
   float* final_norm() const { return params[1 + 6 * cfg.num_layers]; }
   float* lm_head() const { return params[2 + 6 * cfg.num_layers]; }
+  const PackedMatrix& packed_layer(uint32_t l, int which) const {
+    return packed[1 + 6 * l + which];
+  }
+  const PackedMatrix& packed_lm_head() const { return packed[2 + 6 * cfg.num_layers]; }
 };
 
 enum { W_NORM1 = 0, W_QKV = 1, W_OUT = 2, W_NORM2 = 3, W_UP = 4, W_DOWN = 5 };
@@ -395,6 +407,8 @@ extern "C" void akh_model_free(akh_model* m) {
   hipStreamSynchronize(m->be->stream);
   for (float* p : m->params)
     if (p) hipFree(p);
+  for (const PackedMatrix& pm : m->packed)
+    if (pm.w) hipFree(pm.w);
   delete m;
 }
 
@@ -433,6 +447,32 @@ extern "C" akh_status akh_model_new(akh_backend* be,
     }
     m->params.push_back(static_cast<float*>(p));
   }
+  // Packed copies of the decode matrices (zero until their upload).
+  m->packed.resize(m->params.size());
+  auto plan = [&](size_t index, int role, size_t K, size_t N) {
+    PackedMatrix& pm = m->packed[index];
+    pm.K = (int)K;
+    pm.N = (int)N;
+    pm.rows = dec_packed_rows(role, (int)K);
+  };
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    plan(1 + 6 * l + W_QKV, DEC_CFG_QKV, d, 3 * d);
+    plan(1 + 6 * l + W_OUT, DEC_CFG_OUT, d, d);
+    plan(1 + 6 * l + W_UP, DEC_CFG_UP, d, F);
+    plan(1 + 6 * l + W_DOWN, DEC_CFG_DOWN, F, d);
+  }
+  plan(2 + 6 * c.num_layers, DEC_CFG_LM, d, V);
+  for (PackedMatrix& pm : m->packed) {
+    if (!pm.rows) continue;
+    void* p = nullptr;
+    const size_t n = (size_t)(pm.N + 31) / 32 * 32 * pm.rows;
+    akh_status st = akh_tensor_alloc(be, n * sizeof(float), &p);
+    if (st != AKH_OK) {
+      akh_model_free(m);
+      return st;
+    }
+    pm.w = static_cast<float*>(p);
+  }
   *out = m;
   return AKH_OK;
 }
@@ -453,7 +493,14 @@ extern "C" akh_status akh_model_upload_param(akh_model* m, uint32_t index,
                                              const float* host, size_t count) {
   CHECK_ARG(m && index < m->params.size(), "akh_model_upload_param: bad index");
   CHECK_ARG(count == m->counts[index], "akh_model_upload_param: size mismatch");
-  return akh_tensor_upload(m->be, m->params[index], host, count * sizeof(float));
+  akh_status st = akh_tensor_upload(m->be, m->params[index], host, count * sizeof(float));
+  if (st != AKH_OK) return st;
+  const PackedMatrix& pm = m->packed[index];
+  if (pm.w) {
+    HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, m->be->stream));
+    HIP_TRY(hipStreamSynchronize(m->be->stream));
+  }
+  return AKH_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -565,7 +612,8 @@ hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->xnt;
-  p.w = s->m->layer(l, W_QKV);
+  p.w = s->m->packed_layer(l, W_QKV).w;
+  p.Kp = s->m->packed_layer(l, W_QKV).rows;
   p.y = s->p_qkv;
   p.N = 3 * c.dim;
   p.K = c.dim;
@@ -597,7 +645,8 @@ hipError_t enqueue_out(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->attn_t;
-  p.w = s->m->layer(l, W_OUT);
+  p.w = s->m->packed_layer(l, W_OUT).w;
+  p.Kp = s->m->packed_layer(l, W_OUT).rows;
   p.y = s->p_out;
   p.N = c.dim;
   p.K = c.dim;
@@ -618,7 +667,8 @@ hipError_t enqueue_up(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->xnt;
-  p.w = s->m->layer(l, W_UP);
+  p.w = s->m->packed_layer(l, W_UP).w;
+  p.Kp = s->m->packed_layer(l, W_UP).rows;
   p.y = s->p_up;
   p.N = c.ffn_hidden;
   p.K = c.dim;
@@ -631,7 +681,8 @@ hipError_t enqueue_down(akh_session* s, uint32_t l) {
   DecGemmParams p = dec_base(s);
   p.xt = s->p_up;
   p.nparts = s->ks_up;
-  p.w = s->m->layer(l, W_DOWN);
+  p.w = s->m->packed_layer(l, W_DOWN).w;
+  p.Kp = s->m->packed_layer(l, W_DOWN).rows;
   p.y = s->p_down;
   p.N = c.dim;
   p.K = c.ffn_hidden;
@@ -644,7 +695,8 @@ hipError_t enqueue_lm_head(akh_session* s) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->xnt;
-  p.w = s->m->lm_head();
+  p.w = s->m->packed_lm_head().w;
+  p.Kp = s->m->packed_lm_head().rows;
   p.y = s->logits;
   p.amax = s->amax;
   p.N = c.vocab_size;

@@ -188,10 +188,14 @@ void akh_model_free(akh_model* m);
  * embedding, then per layer norm_1, qkv_proj, out_proj, norm_2, ffn_up,
  * ffn_down, then final_norm, lm_head. */
 uint32_t akh_model_num_params(const akh_model* m);
-/* Device pointer and element count of parameter `index`. */
+/* Device pointer and element count of parameter `index`, in the reference
+ * layout.  A read-only view: the decode kernels read the matrices through
+ * a tiled copy that akh_model_upload_param refreshes, so parameters change
+ * only through akh_model_upload_param. */
 akh_status akh_model_param(akh_model* m, uint32_t index, float** dev,
                            size_t* count);
-/* Copy `count` floats from host into parameter `index` (count must match). */
+/* Copy `count` floats from host into parameter `index` (count must match),
+ * and refresh the decode path's tiled copy of a weight matrix. */
 akh_status akh_model_upload_param(akh_model* m, uint32_t index,
                                   const float* host, size_t count);
 
