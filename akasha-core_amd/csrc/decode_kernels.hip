@@ -100,6 +100,35 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
         if (PRO == PRO_SILU_SUM) {
           t = sum_parts4<4>(t, p.xt + off, (size_t)32 * K, p.nparts);
           t = make_float4(silu(t.x), silu(t.y), silu(t.z), silu(t.w));
+        } else if (PRO == PRO_ATTN_MERGE) {
+          // Softmax states (max, sum, unnormalised o) of the attention
+          // splits of row j, head (4 kq) / hd: o = sum_s w_s o_s / sum_s w_s l_s
+          // with w_s = exp(max_s - max).
+          const int H = K / p.hd, hq = (4 * kq) / p.hd;
+          float2 ml[kMaxAttnSplits];
+          float4 o[kMaxAttnSplits];
+#pragma unroll
+          for (int sp = 0; sp < kMaxAttnSplits; ++sp) {
+            const bool in = sp < p.nparts;
+            ml[sp] = in ? p.ml[((size_t)sp * H + hq) * 32 + j] : make_float2(-INFINITY, 0.f);
+            o[sp] = in ? *reinterpret_cast<const float4*>(p.xt + (size_t)sp * 32 * K + off)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+          float mx = ml[0].x;
+#pragma unroll
+          for (int sp = 1; sp < kMaxAttnSplits; ++sp) mx = fmaxf(mx, ml[sp].x);
+          float L = 0.f;
+#pragma unroll
+          for (int sp = 0; sp < kMaxAttnSplits; ++sp) {
+            const float w = ml[sp].x == -INFINITY ? 0.f : expf(ml[sp].x - mx);
+            L += w * ml[sp].y;
+            t.x += w * o[sp].x;
+            t.y += w * o[sp].y;
+            t.z += w * o[sp].z;
+            t.w += w * o[sp].w;
+          }
+          const float inv = L > 0.f ? 1.0f / L : 0.f;
+          t = make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
         } else {
           t = *reinterpret_cast<const float4*>(p.xt + off);
         }
@@ -282,31 +311,64 @@ __global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
     p.amax[(size_t)m * G + blockIdx.x] = make_uint2(__float_as_uint(bv), bi);
 }
 
-// Single-query attention over the KV cache for one (sequence, head) per
+// Single-query attention over the KV cache, one (sequence, head, split) per
 // block, with the fused head of the layer's attention:
 //   q, k, v of the new token = the sum of the QKV GEMM's partial tiles, with
 //   RoPE on q and k at position pos; k and v appended to the cache at row
 //   pos (inference_graphs.rs:398-426);
 //   softmax(scale * q . K[0..pos]) . V[0..pos] (attn_qk_cached + softmax_rect
-//   + attn_av_cached, inference_graphs.rs:428-456).
-// AW waves split the cached rows 0..pos-1; each streams its rows with HD/4
-// lanes per row (a float4 each) and RB row groups of K and V in flight,
-// keeping an online softmax; wave 0 also folds in the new row.  The waves'
-// (max, sum, o) are merged in LDS and the output row is written in the
-// k-quad layout for the out_proj GEMM.
-template <int HD, int AW>
+//   + attn_av_cached, inference_graphs.rs:428-456), computed as SP partial
+//   softmax states over SP ranges of the rows.
+// Split sp takes cached rows [sp*per, (sp+1)*per) of 0..pos-1; the last
+// split also folds in the new row and appends it to the cache.  AW waves
+// divide the split's rows; each streams its rows with HD/4 lanes per row (a
+// float4 each) and RB row groups of K and V in flight, keeping an online
+// softmax.  The waves' (max, sum, o) are merged in LDS and the split writes
+// its unnormalised o (k-quad layout, one tile per split) and (max, sum);
+// the out_proj GEMM merges the splits when it loads its A operand.
+template <int HD, int AW, int RB, int SP>
 __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   constexpr int LPR = HD / 4;    // lanes per row
   constexpr int RPW = 64 / LPR;  // rows per wave per load
-  constexpr int RB = 8;          // row groups per batch
   __shared__ float wm_s[AW], wl_s[AW];
   __shared__ float4 wo_s[AW][LPR];
 
-  const int bh = blockIdx.x, b = bh / p.H, hh = bh - b * p.H;
+  const int sp = blockIdx.x % SP, bh = blockIdx.x / SP;
+  const int b = bh / p.H, hh = bh - b * p.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane % LPR, rl = lane / LPR;
   const int pos = p.pos[b];
   const int d = p.d;
+  const bool last = sp == SP - 1;
+
+  const size_t hoff = (size_t)b * p.seq_stride + hh * HD + 4 * g;
+  const float* kbase = p.kc + hoff;
+  const float* vbase = p.vc + hoff;
+
+  // This split's share of the cached rows 0..pos-1, divided over the waves.
+  const int per = (pos + SP - 1) / SP;
+  const int t0 = min(pos, sp * per), t1 = min(pos, t0 + per);
+  const int ch = ((t1 - t0 + AW - 1) / AW + RPW - 1) / RPW * RPW;
+  const int r0 = t0 + wave * ch, r1 = min(t1, r0 + ch);
+
+  // The first row batch is requested before the new token's q, k, v, so the
+  // two memory round trips overlap.
+  float4 kv[RB], vv[RB];
+  bool ok[RB];
+  auto load_batch = [&](int base) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+      const int r = base + i * RPW + rl;
+      ok[i] = r < r1;
+      const size_t off = (size_t)(ok[i] ? r : r0) * d;
+      kv[i] = ok[i] ? *reinterpret_cast<const float4*>(kbase + off)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      vv[i] = ok[i] ? *reinterpret_cast<const float4*>(vbase + off)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  load_batch(r0);
+  asm volatile("" ::: "memory");
 
   // The new token's q, k, v (columns hh*HD + 4g .. +3 of each role).
   float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), kn = q4, vn = q4;
@@ -314,8 +376,10 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     const float* row = p.qkv + (size_t)b * 3 * d + (size_t)hh * HD + 4 * g;
     const size_t ps = (size_t)32 * 3 * d;
     q4 = sum_parts4<4>(q4, row, ps, p.nparts);
-    kn = sum_parts4<4>(kn, row + d, ps, p.nparts);
-    vn = sum_parts4<4>(vn, row + 2 * d, ps, p.nparts);
+    if (last) {
+      kn = sum_parts4<4>(kn, row + d, ps, p.nparts);
+      vn = sum_parts4<4>(vn, row + 2 * d, ps, p.nparts);
+    }
     // Pairs (4g, 4g+1) and (4g+2, 4g+3) of the head: rope entries 2g, 2g+1.
     const float2 c0 = p.rope[(size_t)pos * (HD / 2) + 2 * g];
     const float2 c1 = p.rope[(size_t)pos * (HD / 2) + 2 * g + 1];
@@ -324,22 +388,14 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     rope_pair(kn.x, kn.y, c0.x, c0.y);
     rope_pair(kn.z, kn.w, c1.x, c1.y);
   }
-  const size_t hoff = (size_t)b * p.seq_stride + hh * HD + 4 * g;
-  if (wave == 0 && rl == 0) {
+  if (last && wave == 0 && rl == 0) {
     *reinterpret_cast<float4*>(p.kc + hoff + (size_t)pos * d) = kn;
     *reinterpret_cast<float4*>(p.vc + hoff + (size_t)pos * d) = vn;
   }
 
-  // Cached rows 0..pos-1, split over the waves.
-  const int T = pos;
-  const int ch = ((T + AW - 1) / AW + RPW - 1) / RPW * RPW;
-  const int r0 = wave * ch, r1 = min(T, r0 + ch);
-  const float* kbase = p.kc + hoff;
-  const float* vbase = p.vc + hoff;
-
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (wave == 0) {
+  if (last && wave == 0) {
     // The new row; every lane of a row group holds its full score, and only
     // row slot 0 adds it so the slot sum below counts it once.
     float s = q4.x * kn.x + q4.y * kn.y + q4.z * kn.z + q4.w * kn.w;
@@ -350,16 +406,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     acc = rl == 0 ? vn : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   for (int base = r0; base < r1; base += RPW * RB) {
-    float4 kv[RB], vv[RB];
-    bool ok[RB];
-#pragma unroll
-    for (int i = 0; i < RB; ++i) {
-      const int r = base + i * RPW + rl;
-      ok[i] = r < r1;
-      const size_t off = (size_t)(ok[i] ? r : r0) * d;
-      kv[i] = *reinterpret_cast<const float4*>(kbase + off);
-      vv[i] = *reinterpret_cast<const float4*>(vbase + off);
-    }
+    if (base != r0) load_batch(base);
     float t[RB];
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
@@ -422,9 +469,9 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
       o.z += wg * wo_s[w][t].z;
       o.w += wg * wo_s[w][t].w;
     }
-    const float inv = 1.0f / L;
-    *reinterpret_cast<float4*>(p.out_t + ((size_t)(hh * (HD / 4) + t) * 32 + b) * 4) =
-        make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    *reinterpret_cast<float4*>(p.out_t + (size_t)sp * 32 * d +
+                               ((size_t)(hh * (HD / 4) + t) * 32 + b) * 4) = o;
+    if (t == 0) p.ml[((size_t)sp * p.H + hh) * 32 + b] = make_float2(M, L);
   }
 }
 
@@ -613,24 +660,39 @@ hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s) {
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
   switch (role) {
     case DEC_CFG_QKV: return dec_go<DEC_CFG_QKV, DEC_PART, PRO_NONE>(p, s);
-    case DEC_CFG_OUT: return dec_go<DEC_CFG_OUT, DEC_PART, PRO_NONE>(p, s);
+    case DEC_CFG_OUT: return dec_go<DEC_CFG_OUT, DEC_PART, PRO_ATTN_MERGE>(p, s);
     case DEC_CFG_UP: return dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NONE>(p, s);
     case DEC_CFG_DOWN: return dec_go<DEC_CFG_DOWN, DEC_PART, PRO_SILU_SUM>(p, s);
   }
   return hipErrorInvalidValue;
 }
 
+// Attention launch shape: AW waves, RB row groups in flight, SP splits.
+#ifndef AKH_SHAPE_ATTN
+#define AKH_SHAPE_ATTN 4, 8, 2
+#endif
+namespace {
+template <int AW_, int RB_, int SP_>
+struct AttnShape {
+  static constexpr int AW = AW_, RB = RB_, SP = SP_;
+};
+using AttnCfg = AttnShape<AKH_SHAPE_ATTN>;
+static_assert(AttnCfg::SP <= kMaxAttnSplits, "too many attention splits");
+}  // namespace
+
+int dec_attn_splits() { return AttnCfg::SP; }
+
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
                            hipStream_t s) {
-  constexpr int AW = 8;
-  dim3 g(batch * p.H), b(64 * AW);
+  constexpr int AW = AttnCfg::AW, RB = AttnCfg::RB, SP = AttnCfg::SP;
+  dim3 g(batch * p.H * SP), b(64 * AW);
   switch (hd) {
-    case 4: hipLaunchKernelGGL((k_dec_attn<4, AW>), g, b, 0, s, p); break;
-    case 8: hipLaunchKernelGGL((k_dec_attn<8, AW>), g, b, 0, s, p); break;
-    case 16: hipLaunchKernelGGL((k_dec_attn<16, AW>), g, b, 0, s, p); break;
-    case 32: hipLaunchKernelGGL((k_dec_attn<32, AW>), g, b, 0, s, p); break;
-    case 64: hipLaunchKernelGGL((k_dec_attn<64, AW>), g, b, 0, s, p); break;
-    case 128: hipLaunchKernelGGL((k_dec_attn<128, AW>), g, b, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((k_dec_attn<4, AW, RB, SP>), g, b, 0, s, p); break;
+    case 8: hipLaunchKernelGGL((k_dec_attn<8, AW, RB, SP>), g, b, 0, s, p); break;
+    case 16: hipLaunchKernelGGL((k_dec_attn<16, AW, RB, SP>), g, b, 0, s, p); break;
+    case 32: hipLaunchKernelGGL((k_dec_attn<32, AW, RB, SP>), g, b, 0, s, p); break;
+    case 64: hipLaunchKernelGGL((k_dec_attn<64, AW, RB, SP>), g, b, 0, s, p); break;
+    case 128: hipLaunchKernelGGL((k_dec_attn<128, AW, RB, SP>), g, b, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

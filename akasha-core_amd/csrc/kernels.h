@@ -119,9 +119,13 @@ enum DecEpi : int {
 };
 
 enum DecPro : int {
-  PRO_NONE = 0,      // A = xt
-  PRO_SILU_SUM = 1,  // A = silu(sum of nparts k-quad partial tiles at xt)
+  PRO_NONE = 0,        // A = xt
+  PRO_SILU_SUM = 1,    // A = silu(sum of nparts k-quad partial tiles at xt)
+  PRO_ATTN_MERGE = 2,  // A = merge of nparts attention splits (xt, ml)
 };
+
+// Most splits of one (sequence, head) attention.
+constexpr int kMaxAttnSplits = 4;
 
 // Roles of the decode GEMMs; each has its own launch shape.
 enum DecCfg : int {
@@ -139,6 +143,8 @@ struct DecGemmParams {
   int M, N, K, Kp;
   float* y;         // partial tiles or logits
   uint2* amax;      // DEC_LOGITS: [32, parts] (value bits, index)
+  const float2* ml;  // PRO_ATTN_MERGE: per split (max, sum) [nparts][K/hd][32]
+  int hd;            // PRO_ATTN_MERGE: head_dim
 };
 
 // Decode weights are read from a copy packed once at upload: 32-column
@@ -168,13 +174,16 @@ struct DecAttnParams {
   const float2* rope;  // [max_ctx, head_dim / 2] (cos, sin)
   float* kc;         // sequence b at kc + b * seq_stride, rows of d
   float* vc;
-  float* out_t;      // k-quad [d/4][32][4]
+  float* out_t;      // per split, unnormalised o in k-quad [splits][d/4][32][4]
+  float2* ml;        // per split (max, sum) [splits][H][32]
   const int* pos;    // position of the new token of each sequence
   long seq_stride;
   int H, d;
   float scale;
 };
 
+// Splits per (sequence, head): the partial states the out_proj GEMM merges.
+int dec_attn_splits();
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
                            hipStream_t s);
 

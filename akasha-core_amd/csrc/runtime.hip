@@ -522,7 +522,8 @@ struct akh_session {
   // the k-quad layout [K/4][32][4]; p_* hold a GEMM's partial tiles.
   float* xt = nullptr;      // residual stream
   float* xnt = nullptr;     // RMSNorm of the residual stream (GEMM input)
-  float* attn_t = nullptr;  // attention output
+  float* attn_t = nullptr;  // attention splits: unnormalised o [splits][32][dim]
+  float2* attn_ml = nullptr;  // attention splits: (max, sum) [splits][heads][32]
   float* p_qkv = nullptr;   // [ks_qkv][32][3*dim]
   float* p_out = nullptr;   // [ks_out][32][dim]
   float* p_up = nullptr;    // [ks_up] k-quad tiles of [32, ffn]
@@ -631,6 +632,7 @@ hipError_t enqueue_attn(akh_session* s, uint32_t l) {
   p.kc = s->kcache(l);
   p.vc = s->vcache(l);
   p.out_t = s->attn_t;
+  p.ml = s->attn_ml;
   p.pos = s->pos;
   p.seq_stride = s->seq_stride();
   p.H = (int)c.num_heads;
@@ -645,6 +647,9 @@ hipError_t enqueue_out(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->attn_t;
+  p.nparts = dec_attn_splits();
+  p.ml = s->attn_ml;
+  p.hd = (int)(c.dim / c.num_heads);
   p.w = s->m->packed_layer(l, W_OUT).w;
   p.Kp = s->m->packed_layer(l, W_OUT).rows;
   p.y = s->p_out;
@@ -783,7 +788,7 @@ extern "C" void akh_session_free(akh_session* s) {
   if (s->gexec) hipGraphExecDestroy(s->gexec);
   if (s->graph) hipGraphDestroy(s->graph);
   free_prefill(s);
-  void* bufs[] = {s->kv,    s->rope,   s->xt,     s->xnt,  s->attn_t,
+  void* bufs[] = {s->kv,    s->rope,   s->xt,     s->xnt,  s->attn_t, s->attn_ml,
                   s->p_qkv, s->p_out,  s->p_up,   s->p_down, s->logits,
                   s->amax,  s->tok,    s->pos,    s->hist};
   for (void* p : bufs)
@@ -828,7 +833,8 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   alloc((void**)&s->rope, (size_t)max_context_len * (hd / 2) * sizeof(float2));
   alloc((void**)&s->xt, R * d * 4);
   alloc((void**)&s->xnt, R * d * 4);
-  alloc((void**)&s->attn_t, R * d * 4);
+  alloc((void**)&s->attn_t, (size_t)dec_attn_splits() * R * d * 4);
+  alloc((void**)&s->attn_ml, (size_t)dec_attn_splits() * c.num_heads * R * sizeof(float2));
   alloc((void**)&s->p_qkv, (size_t)s->ks_qkv * R * 3 * d * 4);
   alloc((void**)&s->p_out, (size_t)s->ks_out * R * d * 4);
   alloc((void**)&s->p_up, (size_t)s->ks_up * R * F * 4);
