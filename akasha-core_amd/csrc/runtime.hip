@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "akasha_hip.h"
+#include "checkpoint.h"
 #include "kernels.h"
 
 using namespace akh;
@@ -500,6 +501,108 @@ extern "C" akh_status akh_model_upload_param(akh_model* m, uint32_t index,
     HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, m->be->stream));
     HIP_TRY(hipStreamSynchronize(m->be->stream));
   }
+  return AKH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Checkpoints (src/nn/checkpoint.rs)
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// Walks the tensor lists of an opened file (structure only).
+akh_status ckpt_walk(CkptReader& r, uint64_t* total, uint64_t* pairs) {
+  uint64_t t = 0, p = 0;
+  for (uint64_t i = 0; i < r.head.num_params; ++i) {
+    uint64_t n = 0;
+    if (!r.tensor_len(n) || !r.skip_floats(n)) return fail(AKH_E_IO, r.err);
+    t += n;
+  }
+  if (!r.u64(p)) return fail(AKH_E_IO, r.err);
+  for (uint64_t i = 0; i < 2 * p; ++i) {
+    uint64_t n = 0;
+    if (!r.tensor_len(n) || !r.skip_floats(n)) return fail(AKH_E_IO, r.err);
+  }
+  if (total) *total = t;
+  if (pairs) *pairs = p;
+  return AKH_OK;
+}
+
+akh_status ckpt_open(CkptReader& r, const char* path) {
+  if (!r.open(path)) return fail(r.io_error ? AKH_E_IO : AKH_E_INVALID, r.err);
+  return AKH_OK;
+}
+
+}  // namespace
+
+extern "C" akh_status akh_checkpoint_info(const char* path, akh_checkpoint_info_t* info) {
+  CHECK_ARG(path && info, "akh_checkpoint_info: NULL argument");
+  memset(info, 0, sizeof(*info));
+  CkptReader r;
+  akh_status st = ckpt_open(r, path);
+  if (st != AKH_OK) return st;
+  info->vocab_size = r.head.vocab_size;
+  info->dim = r.head.dim;
+  info->num_heads = r.head.num_heads;
+  info->num_layers = r.head.num_layers;
+  info->seq_len = r.head.seq_len;
+  info->ffn_hidden = r.head.ffn_hidden;
+  info->train_step = r.head.train_step;
+  info->schedule_step = r.head.schedule_step;
+  info->num_params = r.head.num_params;
+  return ckpt_walk(r, &info->total_param_floats, &info->num_moment_pairs);
+}
+
+extern "C" akh_status akh_model_load_checkpoint(akh_model* m, const char* path,
+                                                uint64_t* train_step,
+                                                int* has_optimizer) {
+  CHECK_ARG(m && path, "akh_model_load_checkpoint: NULL argument");
+  // bincode::deserialize_from reads the whole body before any check.
+  uint64_t pairs = 0;
+  {
+    CkptReader r;
+    akh_status st = ckpt_open(r, path);
+    if (st == AKH_OK) st = ckpt_walk(r, nullptr, &pairs);
+    if (st != AKH_OK) return st;
+  }
+  CkptReader r;
+  akh_status st = ckpt_open(r, path);
+  if (st != AKH_OK) return st;
+  const akh_model_config& c = m->cfg;
+  const CkptHeader& h = r.head;
+  if (h.vocab_size != c.vocab_size || h.dim != c.dim || h.num_heads != c.num_heads ||
+      h.num_layers != (uint64_t)c.num_layers || h.ffn_hidden != c.ffn_hidden) {
+    char msg[512];  // checkpoint.rs:111-129
+    snprintf(msg, sizeof msg,
+             "checkpoint architecture mismatch: file (%u, %u, %u, %llu, %u) vs model "
+             "(%u, %u, %u, %u, %u) (vocab_size, dim, num_heads, num_layers, ffn_hidden)",
+             h.vocab_size, h.dim, h.num_heads, (unsigned long long)h.num_layers,
+             h.ffn_hidden, c.vocab_size, c.dim, c.num_heads, c.num_layers, c.ffn_hidden);
+    return fail(AKH_E_INVALID, msg);
+  }
+  if (h.num_params != m->params.size())  // checkpoint.rs:162-168
+    return fail(AKH_E_INVALID, "checkpoint has " + std::to_string(h.num_params) +
+                                   " parameter tensors, model expects " +
+                                   std::to_string(m->params.size()));
+  std::vector<float> host;
+  for (uint32_t i = 0; i < m->params.size(); ++i) {
+    uint64_t n = 0;
+    if (!r.tensor_len(n)) return fail(AKH_E_IO, r.err);
+    if (n != m->counts[i])  // checkpoint.rs:173-181
+      return fail(AKH_E_INVALID, "checkpoint tensor " + std::to_string(i) + " has " +
+                                     std::to_string(n) + " elements, model expects " +
+                                     std::to_string(m->counts[i]));
+    host.resize((size_t)n);
+    if (!r.floats(host.data(), n)) return fail(AKH_E_IO, r.err);
+    st = akh_model_upload_param(m, i, host.data(), (size_t)n);
+    if (st != AKH_OK) return st;
+  }
+  if (pairs != 0 && pairs != m->params.size())  // checkpoint.rs:137-145
+    return fail(AKH_E_INVALID, "checkpoint has " + std::to_string(pairs) +
+                                   " moment pairs, model expects " +
+                                   std::to_string(m->params.size()));
+  if (train_step) *train_step = h.train_step;
+  if (has_optimizer) *has_optimizer = pairs != 0;
   return AKH_OK;
 }
 

@@ -66,9 +66,25 @@ class HipError(AkashaError):
     code = 7
 
 
+class FileError(AkashaError):
+    """A checkpoint file cannot be opened, read, or is truncated."""
+
+    code = 8
+
+
 _ERRORS = {c.code: c for c in (EmptyPrompt, PromptTooLong, ContextFull,
                                NoCache, CacheNotEmpty, InvalidArgument,
-                               HipError)}
+                               HipError, FileError)}
+
+
+class CheckpointInfo(C.Structure):
+    """akh_checkpoint_info_t: V3Body's header (src/nn/checkpoint.rs:20-35)."""
+
+    _fields_ = [("vocab_size", C.c_uint32), ("dim", C.c_uint32), ("num_heads", C.c_uint32),
+                ("num_layers", C.c_uint64), ("seq_len", C.c_uint32), ("ffn_hidden", C.c_uint32),
+                ("train_step", C.c_uint64), ("schedule_step", C.c_uint32),
+                ("num_params", C.c_uint64), ("total_param_floats", C.c_uint64),
+                ("num_moment_pairs", C.c_uint64)]
 
 
 # ---- meta structs (src/nn/ops/meta.rs) -----------------------------------
@@ -163,6 +179,9 @@ _SIGS = {
     "akh_model_num_params": (U32, [P]),
     "akh_model_param": (ST, [P, U32, C.POINTER(P), C.POINTER(C.c_size_t)]),
     "akh_model_upload_param": (ST, [P, U32, P, C.c_size_t]),
+    "akh_checkpoint_info": (ST, [C.c_char_p, C.POINTER(CheckpointInfo)]),
+    "akh_model_load_checkpoint": (ST, [P, C.c_char_p, C.POINTER(C.c_uint64),
+                                       C.POINTER(C.c_int)]),
     "akh_session_new": (ST, [P, U32, U32, C.POINTER(P)]),
     "akh_session_free": (None, [P]),
     "akh_session_reset": (ST, [P]),
@@ -182,6 +201,14 @@ EXPORTED = tuple(_SIGS)
 
 def lib_path() -> Path:
     return _LIB_PATH
+
+
+def checkpoint_info(path) -> dict:
+    """Header and tensor-list shape of a V3 checkpoint (no device needed)."""
+    lib = load()
+    info = CheckpointInfo()
+    _check(lib.akh_checkpoint_info(os.fsencode(path), C.byref(info)), "checkpoint_info")
+    return {name: getattr(info, name) for name, _ in CheckpointInfo._fields_}
 
 
 def load(path: str | os.PathLike | None = None):
@@ -433,6 +460,21 @@ class Model:
         for i, a in enumerate(params):
             a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
             _check(_lib.akh_model_upload_param(self.handle, i, _ptr(a), a.size), f"param {i}")
+
+    def download_param(self, index: int) -> np.ndarray:
+        """Host copy of parameter ``index`` (reference layout)."""
+        dev, n = self.param(index)
+        out = np.empty(n, np.float32)
+        _check(_lib.akh_tensor_download(self.backend.handle, _ptr(out), dev, out.nbytes),
+               "download_param")
+        return out
+
+    def load_checkpoint(self, path):
+        """checkpoint::load of a V3 file; returns (train_step, has_optimizer)."""
+        step, opt = C.c_uint64(), C.c_int()
+        _check(_lib.akh_model_load_checkpoint(self.handle, os.fsencode(path), C.byref(step),
+                                              C.byref(opt)), "load_checkpoint")
+        return step.value, bool(opt.value)
 
     def close(self):
         if self.handle:

@@ -47,7 +47,8 @@ typedef enum {
   AKH_E_NO_CACHE = 4,          /* AkashaError::NoCache */
   AKH_E_CACHE_NOT_EMPTY = 5,   /* AkashaError::CacheNotEmpty { cur_len } */
   AKH_E_INVALID = 6,           /* a precondition the reference assert!s */
-  AKH_E_HIP = 7                /* HIP runtime error */
+  AKH_E_HIP = 7,               /* HIP runtime error */
+  AKH_E_IO = 8                 /* a file cannot be opened or read */
 } akh_status;
 
 /* ---- metas: src/nn/ops/meta.rs, #[repr(C)] u32/f32 --------------------- */
@@ -198,6 +199,33 @@ akh_status akh_model_param(akh_model* m, uint32_t index, float** dev,
  * and refresh the decode path's tiled copy of a weight matrix. */
 akh_status akh_model_upload_param(akh_model* m, uint32_t index,
                                   const float* host, size_t count);
+
+/* ---- checkpoints: src/nn/checkpoint.rs (format V3) ---------------------- */
+
+/* V3Body's header and the shape of its tensor lists (checkpoint.rs:20-35). */
+typedef struct {
+  uint32_t vocab_size, dim, num_heads;
+  uint64_t num_layers;
+  uint32_t seq_len, ffn_hidden;
+  uint64_t train_step;
+  uint32_t schedule_step;
+  uint64_t num_params, total_param_floats, num_moment_pairs;
+} akh_checkpoint_info_t;
+
+/* Read and check the structure of a V3 file ("AKV3" + bincode fixint body)
+ * without a device.  AKH_E_INVALID: not a V3 file; AKH_E_IO: unreadable or
+ * truncated. */
+akh_status akh_checkpoint_info(const char* path, akh_checkpoint_info_t* info);
+/* checkpoint::load (checkpoint.rs:98-187): the file's parameters into the
+ * model, in params() order, with the reference's checks and messages: the
+ * whole body must parse (else AKH_E_IO); architecture (vocab_size, dim,
+ * num_heads, num_layers, ffn_hidden), tensor count and each tensor's size
+ * must match the model (else AKH_E_INVALID; tensors before a mismatching one
+ * are already loaded, as copy_params leaves them); a non-empty moment list
+ * must have one pair per parameter (checked after the weights are loaded).
+ * train_step and has_optimizer (moments present) may be NULL. */
+akh_status akh_model_load_checkpoint(akh_model* m, const char* path,
+                                     uint64_t* train_step, int* has_optimizer);
 
 /* InferenceSession::new + replace_cache(Cache::new(...)) for `batch`
  * independent sequences (inference.rs:25-54; inference_graphs.rs:520-538).
