@@ -216,4 +216,30 @@ hipError_t launch_argmax_final(const uint2* part, int ntiles, int M,
                                uint32_t* tok, int* pos, uint32_t* hist,
                                int hist_stride, int next_pos, hipStream_t s);
 
+// ---------------------------------------------------------------------------
+// Token sampling (sample_kernels.hip): sample_token of sampling.rs:3-81 per
+// row of logits, with the draw of rand::random() given per row.
+// ---------------------------------------------------------------------------
+
+constexpr int kMaxSampleVocab = 1 << 20;  // seen-id bitmap held in LDS
+
+struct SampleArgs {
+  const float* logits;  // row m at logits + m * row_stride
+  int n;
+  long row_stride;
+  float temperature;
+  int top_k;
+  float top_p;
+  float penalty;             // repetition penalty (1 = off)
+  const uint32_t* seen;      // row m's seen ids at seen + m * seen_stride
+  long seen_stride;
+  const uint32_t* seen_len;  // [rows]
+  const double* uniform;     // [rows] draws in [0, 1)
+  double* wbuf;              // scratch, sample_scratch_bytes(rows, n)
+  uint32_t* out;             // [rows]
+};
+
+size_t sample_scratch_bytes(int rows, int n);
+hipError_t launch_sample_rows(const SampleArgs& a, int rows, hipStream_t s);
+
 }  // namespace akh

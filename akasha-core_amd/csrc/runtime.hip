@@ -60,7 +60,28 @@ struct akh_backend {
   hipStream_t stream = nullptr;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   bool capturing = false;
+  void* scratch = nullptr;  // launcher scratch, grown on demand outside capture
+  size_t scratch_bytes = 0;
 };
+
+namespace {
+
+// Scratch of at least `bytes` on the backend's device.
+akh_status backend_scratch(akh_backend* be, size_t bytes, void** out) {
+  if (be->scratch_bytes < bytes) {
+    CHECK_ARG(!be->capturing, "scratch must grow outside graph capture (run once eagerly first)");
+    HIP_TRY(hipStreamSynchronize(be->stream));
+    if (be->scratch) HIP_TRY(hipFree(be->scratch));
+    be->scratch = nullptr;
+    be->scratch_bytes = 0;
+    HIP_TRY(hipMalloc(&be->scratch, bytes));
+    be->scratch_bytes = bytes;
+  }
+  *out = be->scratch;
+  return AKH_OK;
+}
+
+}  // namespace
 
 struct akh_graph {
   akh_backend* be = nullptr;
@@ -101,6 +122,7 @@ extern "C" void akh_backend_free(akh_backend* be) {
   if (be->stream) hipStreamSynchronize(be->stream);
   if (be->t0) hipEventDestroy(be->t0);
   if (be->t1) hipEventDestroy(be->t1);
+  if (be->scratch) hipFree(be->scratch);
   if (be->stream) hipStreamDestroy(be->stream);
   delete be;
 }
@@ -369,6 +391,36 @@ extern "C" akh_status akh_argmax_rows(akh_backend* be, const float* logits,
   CHECK_ARG(logits && out, "akh_argmax_rows: NULL buffer");
   CHECK_ARG(n > 0, "akh_argmax_rows: empty rows");
   HIP_TRY(shader_argmax_rows(logits, rows, n, out, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_sample_rows(akh_backend* be, const float* logits, uint32_t rows,
+                                      uint32_t n, akh_sampling params, const uint32_t* seen,
+                                      uint32_t seen_stride, const uint32_t* seen_len,
+                                      const double* uniforms, uint32_t* out) {
+  CHECK_ARG(be && logits && out && rows > 0 && n > 0, "akh_sample_rows: bad argument");
+  CHECK_ARG(n <= (uint32_t)kMaxSampleVocab, "akh_sample_rows: n exceeds 2^20");
+  CHECK_ARG(params.temperature <= 0.0f || uniforms,
+            "akh_sample_rows: sampling (temperature > 0) needs uniforms");
+  CHECK_ARG(!seen || (seen_len && seen_stride > 0), "akh_sample_rows: seen needs seen_len");
+  void* wb = nullptr;
+  akh_status st = backend_scratch(be, sample_scratch_bytes((int)rows, (int)n), &wb);
+  if (st != AKH_OK) return st;
+  SampleArgs a{};
+  a.logits = logits;
+  a.n = (int)n;
+  a.row_stride = n;
+  a.temperature = params.temperature;
+  a.top_k = (int)std::min<uint32_t>(params.top_k, 0x7FFFFFFFu);
+  a.top_p = params.top_p;
+  a.penalty = params.repetition_penalty;
+  a.seen = seen;
+  a.seen_stride = seen_stride;
+  a.seen_len = seen_len;
+  a.uniform = uniforms;
+  a.wbuf = static_cast<double*>(wb);
+  a.out = out;
+  HIP_TRY(launch_sample_rows(a, (int)rows, be->stream));
   return AKH_OK;
 }
 

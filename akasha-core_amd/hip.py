@@ -77,6 +77,13 @@ _ERRORS = {c.code: c for c in (EmptyPrompt, PromptTooLong, ContextFull,
                                HipError, FileError)}
 
 
+class Sampling(C.Structure):
+    """akh_sampling: sample_token's parameters (src/nn/sampling.rs:18-25)."""
+
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+                ("repetition_penalty", C.c_float)]
+
+
 class CheckpointInfo(C.Structure):
     """akh_checkpoint_info_t: V3Body's header (src/nn/checkpoint.rs:20-35)."""
 
@@ -174,6 +181,7 @@ _SIGS = {
     "akh_attn_av_cached": (ST, [P, P, P, P, U32, P]),
     "akh_silu": (ST, [P, P, U32]),
     "akh_argmax_rows": (ST, [P, P, U32, U32, P]),
+    "akh_sample_rows": (ST, [P, P, U32, U32, Sampling, P, U32, P, P, P]),
     "akh_model_new": (ST, [P, C.POINTER(ModelConfigC), C.POINTER(P)]),
     "akh_model_free": (None, [P]),
     "akh_model_num_params": (U32, [P]),
@@ -411,6 +419,17 @@ class Backend:
 
     def argmax_rows(self, logits, rows, n, out):
         _check(_lib.akh_argmax_rows(self.handle, _p(logits), rows, n, _p(out)), "argmax_rows")
+
+    def sample_rows(self, logits, rows, n, out, temperature=0.0, top_k=0, top_p=1.0,
+                    repetition_penalty=1.0, seen=None, seen_stride=0, seen_len=None,
+                    uniforms=None):
+        """sample_token per row of device logits (device buffers throughout)."""
+        sp = Sampling(temperature, top_k, top_p, repetition_penalty)
+        _check(_lib.akh_sample_rows(self.handle, _p(logits), rows, n, sp,
+                                    _p(seen) if seen is not None else None, seen_stride,
+                                    _p(seen_len) if seen_len is not None else None,
+                                    _p(uniforms) if uniforms is not None else None, _p(out)),
+               "sample_rows")
 
 
 class Graph:

@@ -169,6 +169,27 @@ akh_status akh_silu(akh_backend* be, float* buf, uint32_t len);
 akh_status akh_argmax_rows(akh_backend* be, const float* logits,
                            uint32_t rows, uint32_t n, uint32_t* out);
 
+/* Parameters of sample_token (src/nn/sampling.rs:18-25). */
+typedef struct {
+  float temperature;
+  uint32_t top_k;
+  float top_p;
+  float repetition_penalty;
+} akh_sampling;
+
+/* sample_token (sampling.rs:3-81) for `rows` rows of device logits [rows, n]:
+ * the repetition penalty over each row's seen ids, then the argmax
+ * (temperature <= 0) or temperature / top_k / top_p sampling, with the
+ * device draw uniforms[r] in [0, 1) standing in for rand::random().  seen is
+ * [rows, seen_stride] with seen_len[rows] valid entries (NULL: no seen ids);
+ * uniforms may be NULL when temperature <= 0.  Ids with equal logits are
+ * ordered lower index first (the reference's unstable sort leaves that
+ * order unspecified).  n <= 2^20. */
+akh_status akh_sample_rows(akh_backend* be, const float* logits, uint32_t rows,
+                           uint32_t n, akh_sampling params, const uint32_t* seen,
+                           uint32_t seen_stride, const uint32_t* seen_len,
+                           const double* uniforms, uint32_t* out);
+
 /* ---- 3. model weights and the batched session ---------------------------- */
 
 /* ModelConfig (src/config.rs:1-30). */

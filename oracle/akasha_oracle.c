@@ -260,6 +260,86 @@ uint32_t ora_argmax(const float* logits, uint32_t n) {
   return best;
 }
 
+/* sampling.rs:3-16 (apply_repetition_penalty) and 18-81 (sample_token), with
+ * the draw r = rand::random() passed in.  The reference sorts with
+ * sort_unstable_by, whose order among equal logits is unspecified; this
+ * restatement breaks ties by the lower index first. */
+static _Thread_local const float* ora_sort_logits;
+
+static int ora_desc_cmp(const void* pa, const void* pb) {
+  const uint32_t a = *(const uint32_t*)pa, b = *(const uint32_t*)pb;
+  const float la = ora_sort_logits[a], lb = ora_sort_logits[b];
+  if (la > lb) return -1;
+  if (la < lb) return 1;
+  return a < b ? -1 : a > b ? 1 : 0;
+}
+
+uint32_t ora_sample_token(const float* logits_in, uint32_t n, float temperature,
+                          uint32_t top_k, float top_p, const uint32_t* seen,
+                          uint32_t n_seen, float repetition_penalty, double r) {
+  float* logits = (float*)malloc((size_t)n * sizeof(float));
+  memcpy(logits, logits_in, (size_t)n * sizeof(float));
+  if (repetition_penalty != 1.0f) {
+    /* Every distinct seen id once, from its original value. */
+    for (uint32_t s = 0; s < n_seen; ++s) {
+      const uint32_t id = seen[s];
+      if (id >= n) continue;
+      int dup = 0;
+      for (uint32_t t = 0; t < s; ++t)
+        if (seen[t] == id) dup = 1;
+      if (dup) continue;
+      const float l = logits[id];
+      logits[id] = l > 0.0f ? l / repetition_penalty : l * repetition_penalty;
+    }
+  }
+  if (temperature <= 0.0f) {
+    const uint32_t best = ora_argmax(logits, n);
+    free(logits);
+    return best;
+  }
+  uint32_t* idx = (uint32_t*)malloc((size_t)n * sizeof(uint32_t));
+  for (uint32_t i = 0; i < n; ++i) idx[i] = i;
+  ora_sort_logits = logits;
+  qsort(idx, n, sizeof(uint32_t), ora_desc_cmp);
+  uint32_t len = n;
+  if (top_k > 0 && top_k < len) len = top_k;
+  const double mx = (double)logits[idx[0]];
+  double* probs = (double*)malloc((size_t)len * sizeof(double));
+  double sum = 0.0;
+  for (uint32_t i = 0; i < len; ++i) {
+    probs[i] = exp(((double)logits[idx[i]] - mx) / (double)temperature);
+  }
+  for (uint32_t i = 0; i < len; ++i) sum += probs[i];
+  for (uint32_t i = 0; i < len; ++i) probs[i] /= sum;
+  if (top_p < 1.0f) {
+    double cum = 0.0;
+    uint32_t keep = len;
+    for (uint32_t i = 0; i < len; ++i) {
+      cum += probs[i];
+      if (cum >= (double)top_p) {
+        keep = i + 1;
+        break;
+      }
+    }
+    len = keep;
+    double s = 0.0;
+    for (uint32_t i = 0; i < len; ++i) s += probs[i];
+    for (uint32_t i = 0; i < len; ++i) probs[i] /= s;
+  }
+  uint32_t pick = idx[len - 1];
+  for (uint32_t i = 0; i < len; ++i) {
+    if (r < probs[i]) {
+      pick = idx[i];
+      break;
+    }
+    r -= probs[i];
+  }
+  free(probs);
+  free(idx);
+  free(logits);
+  return pick;
+}
+
 /* ---- session ------------------------------------------------------------- */
 
 struct ora_session {

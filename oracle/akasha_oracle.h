@@ -80,6 +80,13 @@ void ora_causal_attention(const float* q, const float* k, const float* v,
                           uint32_t head_dim);
 /* src/nn/sampling.rs:83-91: first index of the maximum (strict >). */
 uint32_t ora_argmax(const float* logits, uint32_t n);
+/* sampling.rs:3-81: repetition penalty, temperature, top-k, top-p, and the
+ * walk of the distribution with the draw r in [0, 1).  Ties in the sort are
+ * broken by the lower index (the reference's unstable sort leaves them
+ * unspecified). */
+uint32_t ora_sample_token(const float* logits, uint32_t n, float temperature,
+                          uint32_t top_k, float top_p, const uint32_t* seen,
+                          uint32_t n_seen, float repetition_penalty, double r);
 
 /* ---- model + session (src/nn/inference.rs, inference_graphs.rs) -------- */
 

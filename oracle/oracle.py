@@ -62,6 +62,7 @@ def load():
         "ora_silu": (None, [F32P, sz]),
         "ora_causal_attention": (None, [F32P, F32P, F32P, F32P, u32, u32, u32]),
         "ora_argmax": (u32, [F32P, u32]),
+        "ora_sample_token": (u32, [F32P, u32, f32, u32, f32, U32P, u32, f32, C.c_double]),
         "ora_session_new": (C.c_void_p, [C.POINTER(OraConfig), C.POINTER(OraWeights), u32]),
         "ora_session_free": (None, [C.c_void_p]),
         "ora_session_reset": (None, [C.c_void_p]),
@@ -179,6 +180,19 @@ def causal_attention(q, k, v, seq_len, dim, head_dim):
 def argmax(x) -> int:
     x = _f(x)
     return int(load().ora_argmax(x, x.size))
+
+
+def sample_token(logits, temperature, top_k, top_p, seen, repetition_penalty, r) -> int:
+    """sampling.rs:18-81 with the draw ``r`` given (ties: lower index first)."""
+    x = _f(logits)
+    seen = np.ascontiguousarray(seen, np.uint32).reshape(-1)
+    if seen.size == 0:
+        seen = np.zeros(1, np.uint32)
+        n_seen = 0
+    else:
+        n_seen = seen.size
+    return int(load().ora_sample_token(x, x.size, float(temperature), int(top_k), float(top_p),
+                                       seen, n_seen, float(repetition_penalty), float(r)))
 
 
 def set_threads(n: int):
