@@ -335,6 +335,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
 
   const int sp = blockIdx.x % SP, bh = blockIdx.x / SP;
   const int b = bh / p.H, hh = bh - b * p.H;
+  if (p.active && !p.active[b]) return;  // a finished sequence: cache untouched
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane % LPR, rl = lane / LPR;
   const int pos = p.pos[b];

@@ -177,6 +177,7 @@ struct DecAttnParams {
   float* out_t;      // per split, unnormalised o in k-quad [splits][d/4][32][4]
   float2* ml;        // per split (max, sum) [splits][H][32]
   const int* pos;    // position of the new token of each sequence
+  const int* active;  // sequences with active[b] == 0 are skipped (none if null)
   long seq_stride;
   int H, d;
   float scale;
@@ -237,9 +238,32 @@ struct SampleArgs {
   const double* uniform;     // [rows] draws in [0, 1)
   double* wbuf;              // scratch, sample_scratch_bytes(rows, n)
   uint32_t* out;             // [rows]
+
+  // Session mode (tok != nullptr), one round of InferenceSession::generate
+  // (inference.rs:303-323) per launch.  A row with done[m] set is skipped
+  // (active[m] = 0).  Otherwise its seen ids are hist[m, start[m] .. pos[m])
+  // (this call's prompt and generated tokens), its draw is
+  // uniform[count[m] * rows + m], and its pick p is recorded:
+  // gen[m, count[m]++] = p, hist[m, pos[m]] = p, tok[m] = p; active[m] =
+  // (p != eos && pos[m] < max_ctx) -- the token is decoded next -- and
+  // done[m] once it stopped or produced max_new tokens.
+  uint32_t* tok;
+  const int* pos;
+  uint32_t* hist;
+  long hist_stride;
+  const int* start;
+  int* active;
+  int* done;
+  uint32_t* count;
+  uint32_t* gen;  // [rows, max_new]
+  int max_new;
+  int max_ctx;
+  uint32_t eos;
 };
 
 size_t sample_scratch_bytes(int rows, int n);
 hipError_t launch_sample_rows(const SampleArgs& a, int rows, hipStream_t s);
+// pos[m] += active[m] for m < rows: the positions of the rows decoded.
+hipError_t launch_advance(int* pos, const int* active, int rows, hipStream_t s);
 
 }  // namespace akh

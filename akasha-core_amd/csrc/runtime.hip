@@ -700,6 +700,20 @@ struct akh_session {
         *pffn = nullptr;
   uint32_t* ptok = nullptr;
 
+  // InferenceSession::generate on the device: per-row state of the rounds.
+  int* active = nullptr;   // row is decoded this round (attention skips others)
+  int* done = nullptr;     // row stopped sampling
+  int* gstart = nullptr;   // position of the call's first prompt token
+  uint32_t* gcount = nullptr;  // tokens generated so far
+  uint32_t* ggen = nullptr;    // [B, gcap] generated tokens
+  double* guni = nullptr;      // [gcap, B] draws
+  double* gwbuf = nullptr;     // sampler scratch
+  uint32_t gcap = 0;
+  hipGraph_t ggraph = nullptr;
+  hipGraphExec_t ggexec = nullptr;
+  akh_sampling gparams{};
+  uint32_t gmax_new = 0;
+
   size_t layer_stride() const { return (size_t)2 * B * max_ctx * m->cfg.dim; }
   float* kcache(uint32_t l) { return kv + l * layer_stride(); }
   float* vcache(uint32_t l) {
@@ -788,6 +802,7 @@ hipError_t enqueue_attn(akh_session* s, uint32_t l) {
   p.vc = s->vcache(l);
   p.out_t = s->attn_t;
   p.ml = s->attn_ml;
+  p.active = s->active;
   p.pos = s->pos;
   p.seq_stride = s->seq_stride();
   p.H = (int)c.num_heads;
@@ -869,7 +884,7 @@ hipError_t enqueue_lm_head(akh_session* s) {
 // out GEMM, residual + norm_2, up GEMM, down GEMM, residual + next norm;
 // lm_head, greedy argmax + position advance.  Reads tok/pos from the
 // device, so it can be replayed step after step with no host work.
-hipError_t enqueue_decode(akh_session* s) {
+hipError_t enqueue_decode_body(akh_session* s) {
   const akh_model_config& c = s->m->cfg;
   hipStream_t st = s->be->stream;
   RowsNormParams emb = norm_base(s, s->m->layer(0, W_NORM1));
@@ -890,34 +905,86 @@ hipError_t enqueue_decode(akh_session* s) {
     if (e == hipSuccess) e = enqueue_resid_norm(s, s->p_down, s->ks_down, next_gain);
   }
   if (e == hipSuccess) e = enqueue_lm_head(s);
-  if (e == hipSuccess)
-    e = launch_argmax_final(s->amax, lm_parts(s), (int)s->B, s->tok, s->pos,
-                            s->hist, (int)s->max_ctx + 1, 0, st);
   return e;
 }
 
-akh_status ensure_decode_graph(akh_session* s) {
-  if (s->gexec) return AKH_OK;
+hipError_t enqueue_decode(akh_session* s) {
+  hipError_t e = enqueue_decode_body(s);
+  if (e == hipSuccess)
+    e = launch_argmax_final(s->amax, lm_parts(s), (int)s->B, s->tok, s->pos, s->hist,
+                            (int)s->max_ctx + 1, 0, s->be->stream);
+  return e;
+}
+
+// One round of InferenceSession::generate (inference.rs:303-323) for every
+// sequence: sample_token on the current logits over the sequence's history,
+// record the token (stopping at eos or a full context), then decode the
+// sampled tokens of the rows still going and advance their positions.
+hipError_t enqueue_generate_round(akh_session* s) {
+  const akh_model_config& c = s->m->cfg;
+  SampleArgs a{};
+  a.logits = s->logits;
+  a.n = (int)c.vocab_size;
+  a.row_stride = c.vocab_size;
+  a.temperature = s->gparams.temperature;
+  a.top_k = (int)std::min<uint32_t>(s->gparams.top_k, 0x7FFFFFFFu);
+  a.top_p = s->gparams.top_p;
+  a.penalty = s->gparams.repetition_penalty;
+  a.uniform = s->gparams.temperature > 0.0f ? s->guni : nullptr;
+  a.wbuf = s->gwbuf;
+  a.tok = s->tok;
+  a.pos = s->pos;
+  a.hist = s->hist;
+  a.hist_stride = (long)s->max_ctx + 1;
+  a.start = s->gstart;
+  a.active = s->active;
+  a.done = s->done;
+  a.count = s->gcount;
+  a.gen = s->ggen;
+  a.max_new = (int)s->gmax_new;
+  a.max_ctx = (int)s->max_ctx;
+  a.eos = c.eos_token;
+  hipError_t e = launch_sample_rows(a, (int)s->B, s->be->stream);
+  if (e == hipSuccess) e = enqueue_decode_body(s);
+  if (e == hipSuccess) e = launch_advance(s->pos, s->active, (int)s->B, s->be->stream);
+  return e;
+}
+
+akh_status capture(akh_session* s, hipError_t (*enqueue)(akh_session*), hipGraph_t* graph,
+                   hipGraphExec_t* exec, const char* what) {
   hipStream_t st = s->be->stream;
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-  hipError_t e = enqueue_decode(s);
+  hipError_t e = enqueue(s);
   hipGraph_t g = nullptr;
   hipError_t e2 = hipStreamEndCapture(st, &g);
   if (e != hipSuccess || e2 != hipSuccess) {
     if (g) hipGraphDestroy(g);
-    return fail(AKH_E_HIP, std::string("decode graph capture: ") +
+    return fail(AKH_E_HIP, std::string(what) + " capture: " +
                                hipGetErrorString(e != hipSuccess ? e : e2));
   }
   hipGraphExec_t ex = nullptr;
   e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
   if (e != hipSuccess) {
     hipGraphDestroy(g);
-    return fail(AKH_E_HIP, std::string("decode graph instantiate: ") +
-                               hipGetErrorString(e));
+    return fail(AKH_E_HIP, std::string(what) + " instantiate: " + hipGetErrorString(e));
   }
-  s->graph = g;
-  s->gexec = ex;
+  *graph = g;
+  *exec = ex;
   return AKH_OK;
+}
+
+akh_status set_active(akh_session* s, bool all_rows) {
+  std::vector<int> v(kMaxBatch, 0);
+  for (uint32_t b = 0; b < s->B; ++b) v[b] = all_rows ? 1 : 0;
+  HIP_TRY(hipMemcpyAsync(s->active, v.data(), kMaxBatch * sizeof(int), hipMemcpyHostToDevice,
+                         s->be->stream));
+  HIP_TRY(hipStreamSynchronize(s->be->stream));
+  return AKH_OK;
+}
+
+akh_status ensure_decode_graph(akh_session* s) {
+  if (s->gexec) return AKH_OK;
+  return capture(s, enqueue_decode, &s->graph, &s->gexec, "decode graph");
 }
 
 akh_status download_outputs(akh_session* s, float* logits, uint32_t* next) {
@@ -942,10 +1009,13 @@ extern "C" void akh_session_free(akh_session* s) {
   hipStreamSynchronize(s->be->stream);
   if (s->gexec) hipGraphExecDestroy(s->gexec);
   if (s->graph) hipGraphDestroy(s->graph);
+  if (s->ggexec) hipGraphExecDestroy(s->ggexec);
+  if (s->ggraph) hipGraphDestroy(s->ggraph);
   free_prefill(s);
-  void* bufs[] = {s->kv,    s->rope,   s->xt,     s->xnt,  s->attn_t, s->attn_ml,
-                  s->p_qkv, s->p_out,  s->p_up,   s->p_down, s->logits,
-                  s->amax,  s->tok,    s->pos,    s->hist};
+  void* bufs[] = {s->kv,     s->rope,   s->xt,     s->xnt,    s->attn_t, s->attn_ml,
+                  s->p_qkv,  s->p_out,  s->p_up,   s->p_down, s->logits, s->amax,
+                  s->tok,    s->pos,    s->hist,   s->active, s->done,   s->gstart,
+                  s->gcount, s->ggen,   s->guni,   s->gwbuf};
   for (void* p : bufs)
     if (p) hipFree(p);
   delete s;
@@ -999,6 +1069,11 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   alloc((void**)&s->tok, R * 4);
   alloc((void**)&s->pos, R * 4);
   alloc((void**)&s->hist, (size_t)batch * (max_context_len + 1) * 4);
+  alloc((void**)&s->active, R * sizeof(int));
+  alloc((void**)&s->done, R * sizeof(int));
+  alloc((void**)&s->gstart, R * sizeof(int));
+  alloc((void**)&s->gcount, R * sizeof(uint32_t));
+  alloc((void**)&s->gwbuf, sample_scratch_bytes((int)batch, (int)V));
   if (e == hipSuccess) {
     // RoPE table in f32 exactly as src/shaders/cpu.rs:98-100 forms it:
     // freq = 1 / 10000^(2i / head_dim), angle = pos * freq, then sin/cos.
@@ -1016,6 +1091,11 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   if (e != hipSuccess) {
     akh_session_free(s);
     return fail(AKH_E_HIP, std::string("akh_session_new: ") + hipGetErrorString(e));
+  }
+  akh_status st = set_active(s, true);
+  if (st != AKH_OK) {
+    akh_session_free(s);
+    return st;
   }
   *out = s;
   return AKH_OK;
@@ -1207,6 +1287,102 @@ extern "C" akh_status akh_session_decode_greedy(akh_session* s,
             h[(size_t)b * (s->max_ctx + 1) + start[b] + 1 + i];
   }
   return AKH_OK;
+}
+
+namespace {
+
+// Buffers and graph of generate rounds for `max_new` tokens with `params`.
+akh_status ensure_generate(akh_session* s, uint32_t max_new, const akh_sampling& params) {
+  if (max_new > s->gcap) {
+    if (s->ggexec) hipGraphExecDestroy(s->ggexec);
+    if (s->ggraph) hipGraphDestroy(s->ggraph);
+    s->ggexec = nullptr;
+    s->ggraph = nullptr;
+    if (s->ggen) HIP_TRY(hipFree(s->ggen));
+    if (s->guni) HIP_TRY(hipFree(s->guni));
+    s->ggen = nullptr;
+    s->guni = nullptr;
+    HIP_TRY(hipMalloc(&s->ggen, (size_t)s->B * max_new * sizeof(uint32_t)));
+    HIP_TRY(hipMalloc(&s->guni, (size_t)max_new * s->B * sizeof(double)));
+    s->gcap = max_new;
+  }
+  const bool same = s->ggexec && s->gmax_new == max_new &&
+                    s->gparams.temperature == params.temperature &&
+                    s->gparams.top_k == params.top_k && s->gparams.top_p == params.top_p &&
+                    s->gparams.repetition_penalty == params.repetition_penalty;
+  if (same) return AKH_OK;
+  if (s->ggexec) hipGraphExecDestroy(s->ggexec);
+  if (s->ggraph) hipGraphDestroy(s->ggraph);
+  s->ggexec = nullptr;
+  s->ggraph = nullptr;
+  s->gparams = params;
+  s->gmax_new = max_new;
+  return capture(s, enqueue_generate_round, &s->ggraph, &s->ggexec, "generate graph");
+}
+
+}  // namespace
+
+extern "C" akh_status akh_session_generate(akh_session* s, const uint32_t* tokens,
+                                           uint32_t prompt_len, uint32_t max_new_tokens,
+                                           akh_sampling params, const double* uniforms,
+                                           uint32_t* out_tokens, uint32_t* out_counts) {
+  CHECK_ARG(s && (tokens || !prompt_len) && out_counts && (out_tokens || !max_new_tokens),
+            "akh_session_generate: NULL argument");
+  if (prompt_len == 0) return fail(AKH_E_EMPTY_PROMPT, "prompt is empty");
+  CHECK_ARG(params.temperature <= 0.0f || uniforms || max_new_tokens == 0,
+            "akh_session_generate: sampling (temperature > 0) needs uniforms");
+  bool all_empty = true, all_resumed = true;
+  for (uint32_t b = 0; b < s->B; ++b) {
+    all_empty = all_empty && s->cur_len[b] == 0;
+    all_resumed = all_resumed && s->cur_len[b] > 0;
+  }
+  CHECK_ARG(all_empty || all_resumed,
+            "akh_session_generate: sequences must all be empty or all hold a cache");
+  const uint32_t B = s->B;
+  std::vector<int> start(kMaxBatch, 0);
+  for (uint32_t b = 0; b < B; ++b) start[b] = (int)s->cur_len[b];
+  // The prompt: prefill on empty caches, else one decode step per token
+  // (inference.rs:290-299).
+  akh_status st = AKH_OK;
+  if (all_empty) {
+    st = akh_session_prefill(s, tokens, prompt_len, nullptr, nullptr);
+  } else {
+    std::vector<uint32_t> col(B);
+    for (uint32_t i = 0; i < prompt_len && st == AKH_OK; ++i) {
+      for (uint32_t b = 0; b < B; ++b) col[b] = tokens[(size_t)b * prompt_len + i];
+      st = akh_session_decode_step(s, col.data(), nullptr, nullptr);
+    }
+  }
+  if (st != AKH_OK) return st;
+  std::fill(out_counts, out_counts + B, 0u);
+  if (max_new_tokens == 0) return AKH_OK;
+
+  st = ensure_generate(s, max_new_tokens, params);
+  if (st != AKH_OK) return st;
+  hipStream_t hs = s->be->stream;
+  std::vector<int> zero(kMaxBatch, 0), done(kMaxBatch, 1);
+  for (uint32_t b = 0; b < B; ++b) done[b] = 0;
+  HIP_TRY(hipMemcpyAsync(s->gstart, start.data(), kMaxBatch * sizeof(int), hipMemcpyHostToDevice, hs));
+  HIP_TRY(hipMemcpyAsync(s->gcount, zero.data(), kMaxBatch * sizeof(int), hipMemcpyHostToDevice, hs));
+  HIP_TRY(hipMemcpyAsync(s->done, done.data(), kMaxBatch * sizeof(int), hipMemcpyHostToDevice, hs));
+  if (params.temperature > 0.0f)
+    HIP_TRY(hipMemcpyAsync(s->guni, uniforms, (size_t)max_new_tokens * B * sizeof(double),
+                           hipMemcpyHostToDevice, hs));
+  for (uint32_t i = 0; i < max_new_tokens; ++i) HIP_TRY(hipGraphLaunch(s->ggexec, hs));
+
+  std::vector<uint32_t> cnt(kMaxBatch), gen((size_t)B * max_new_tokens);
+  std::vector<int> pos(kMaxBatch);
+  HIP_TRY(hipMemcpyAsync(cnt.data(), s->gcount, kMaxBatch * sizeof(uint32_t), hipMemcpyDeviceToHost, hs));
+  HIP_TRY(hipMemcpyAsync(gen.data(), s->ggen, gen.size() * sizeof(uint32_t), hipMemcpyDeviceToHost, hs));
+  HIP_TRY(hipMemcpyAsync(pos.data(), s->pos, kMaxBatch * sizeof(int), hipMemcpyDeviceToHost, hs));
+  HIP_TRY(hipStreamSynchronize(hs));
+  for (uint32_t b = 0; b < B; ++b) {
+    out_counts[b] = cnt[b];
+    for (uint32_t i = 0; i < cnt[b]; ++i)
+      out_tokens[(size_t)b * max_new_tokens + i] = gen[(size_t)b * max_new_tokens + i];
+    s->cur_len[b] = (uint32_t)pos[b];
+  }
+  return set_active(s, true);
 }
 
 extern "C" akh_status akh_session_download_cache(akh_session* s,

@@ -187,14 +187,33 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
   const float* row = a.logits + (size_t)m * a.row_stride;
   double* w = a.wbuf + (size_t)m * n;
 
+  // This row's seen ids and draw.
+  const uint32_t* sr = nullptr;
+  uint32_t cnt = 0;
+  double r = 0.0;
+  if (a.tok) {
+    if (a.done[m]) {
+      if (threadIdx.x == 0) a.active[m] = 0;
+      return;
+    }
+    const int st = a.start[m], p = a.pos[m];
+    sr = a.hist + (size_t)m * a.hist_stride + st;
+    cnt = p > st ? (uint32_t)(p - st) : 0u;
+    if (a.uniform) r = a.uniform[(size_t)a.count[m] * gridDim.x + m];
+  } else {
+    if (a.seen) {
+      sr = a.seen + (size_t)m * a.seen_stride;
+      cnt = a.seen_len ? min(a.seen_len[m], (uint32_t)a.seen_stride) : 0u;
+    }
+    if (a.uniform) r = a.uniform[m];
+  }
+
   // Bitmap of this row's seen ids (only if the penalty changes anything).
   const uint32_t* bm = nullptr;
-  if (a.penalty != 1.0f && a.seen) {
+  if (a.penalty != 1.0f && sr) {
     const int words = (n + 31) / 32;
     for (int k = threadIdx.x; k < words; k += NT) bitmap[k] = 0;
     __syncthreads();
-    const uint32_t cnt = a.seen_len ? min(a.seen_len[m], (uint32_t)a.seen_stride) : 0;
-    const uint32_t* sr = a.seen + (size_t)m * a.seen_stride;
     for (uint32_t s = threadIdx.x; s < cnt; s += NT) {
       const uint32_t id = sr[s];
       if (id < (uint32_t)n) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
@@ -263,7 +282,6 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
 
     // The walk (sampling.rs:72-80): first element whose cumulative
     // probability exceeds r; the last kept element if none does.
-    const double r = a.uniform[m];
     pick = select_desc(n, key_of, w, r, false, sh);
     if (pick >= (uint32_t)n) {
       if (last >= (uint32_t)n) {
@@ -281,16 +299,43 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
       }
     }
   }
-  if (threadIdx.x == 0) a.out[m] = pick;
+  if (threadIdx.x == 0) {
+    if (a.out) a.out[m] = pick;
+    if (a.tok) {
+      const int p = a.pos[m];
+      const uint32_t c = a.count[m];
+      a.gen[(size_t)m * a.max_new + c] = pick;
+      a.count[m] = c + 1;
+      a.hist[(size_t)m * a.hist_stride + p] = pick;
+      a.tok[m] = pick;
+      const bool stop = pick == a.eos || p >= a.max_ctx;
+      a.active[m] = stop ? 0 : 1;
+      a.done[m] = stop || (int)c + 1 >= a.max_new ? 1 : 0;
+    }
+  }
+}
+
+__global__ void k_advance(int* pos, const int* active, int rows) {
+  const int m = threadIdx.x;
+  if (m < rows) pos[m] += active[m];
 }
 
 }  // namespace
 
 size_t sample_scratch_bytes(int rows, int n) { return (size_t)rows * n * sizeof(double); }
 
+hipError_t launch_advance(int* pos, const int* active, int rows, hipStream_t s) {
+  if (rows <= 0 || rows > 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_advance, dim3(1), dim3(64 * ((rows + 63) / 64)), 0, s, pos, active, rows);
+  return hipGetLastError();
+}
+
 hipError_t launch_sample_rows(const SampleArgs& a, int rows, hipStream_t s) {
   if (a.n <= 0 || a.n > kMaxSampleVocab || rows <= 0) return hipErrorInvalidValue;
-  const size_t lds = a.penalty != 1.0f && a.seen ? (size_t)(a.n + 31) / 32 * 4 : 0;
+  if (a.tok && (!a.pos || !a.hist || !a.start || !a.active || !a.done || !a.count || !a.gen ||
+                a.max_new <= 0))
+    return hipErrorInvalidValue;
+  const size_t lds = a.penalty != 1.0f && (a.seen || a.tok) ? (size_t)(a.n + 31) / 32 * 4 : 0;
   hipLaunchKernelGGL(k_sample_rows, dim3(rows), dim3(NT), lds, s, a);
   return hipGetLastError();
 }

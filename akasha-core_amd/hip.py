@@ -197,6 +197,7 @@ _SIGS = {
     "akh_session_prefill": (ST, [P, P, U32, P, P]),
     "akh_session_decode_step": (ST, [P, P, P, P]),
     "akh_session_decode_greedy": (ST, [P, U32, P]),
+    "akh_session_generate": (ST, [P, P, U32, U32, Sampling, P, P, P]),
     "akh_session_truncate": (ST, [P, U32]),
     "akh_session_download_cache": (ST, [P, U32, U32, C.c_int, P]),
     "akh_timer_start": (ST, [P]),
@@ -559,6 +560,25 @@ class Session:
                                               _ptr(out) if out is not None else None),
                "decode_greedy")
         return out
+
+    def generate(self, prompt, max_new_tokens: int, temperature: float = 0.0, top_k: int = 0,
+                 top_p: float = 1.0, repetition_penalty: float = 1.0, uniforms=None):
+        """InferenceSession::generate per sequence (token ids).  ``prompt`` is
+        [batch, prompt_len]; ``uniforms`` [max_new_tokens, batch] holds the
+        draws standing in for rand::random() (needed when temperature > 0).
+        Returns a list of uint32 arrays, one per sequence."""
+        prompt = np.ascontiguousarray(prompt, np.uint32).reshape(self.batch, -1)
+        out = np.zeros((self.batch, max(1, max_new_tokens)), np.uint32)
+        counts = np.zeros(self.batch, np.uint32)
+        uni = None
+        if uniforms is not None:
+            uni = np.ascontiguousarray(uniforms, np.float64).reshape(max_new_tokens, self.batch)
+        sp = Sampling(temperature, top_k, top_p, repetition_penalty)
+        _check(_lib.akh_session_generate(self.handle, _ptr(prompt), prompt.shape[1],
+                                         max_new_tokens, sp,
+                                         _ptr(uni) if uni is not None else None,
+                                         _ptr(out), _ptr(counts)), "generate")
+        return [out[b, :counts[b]].copy() for b in range(self.batch)]
 
     def truncate(self, length: int):
         _check(_lib.akh_session_truncate(self.handle, length), "truncate")

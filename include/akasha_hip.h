@@ -275,6 +275,24 @@ akh_status akh_session_decode_step(akh_session* s, const uint32_t* tokens,
  * out_tokens ([steps, batch]) may be NULL. */
 akh_status akh_session_decode_greedy(akh_session* s, uint32_t steps,
                                      uint32_t* out_tokens);
+/* InferenceSession::generate (inference.rs:264-326) for every sequence,
+ * returning token ids (the reference decodes them to text).  The prompt
+ * (tokens: [batch, prompt_len]) is prefilled if every cache is empty, or fed
+ * one decode step per token if every sequence holds a cache (a mix is
+ * AKH_E_INVALID); its errors are returned as the reference returns them.
+ * Then up to max_new_tokens rounds run on the device with no host round
+ * trip: sample_token over the sequence's history (this call's prompt and
+ * generated tokens) with params and the draw uniforms[round * batch + seq]
+ * (host array [max_new_tokens, batch]; may be NULL when temperature <= 0),
+ * then a decode step of the sampled token.  A sequence stops after sampling
+ * eos (returned, not decoded) or a token its full context cannot take
+ * (returned, not decoded: ContextFull ends generate quietly).  out_tokens is
+ * [batch, max_new_tokens] with out_counts[batch] valid tokens per row;
+ * cur_len follows each sequence's decoded tokens. */
+akh_status akh_session_generate(akh_session* s, const uint32_t* tokens,
+                                uint32_t prompt_len, uint32_t max_new_tokens,
+                                akh_sampling params, const double* uniforms,
+                                uint32_t* out_tokens, uint32_t* out_counts);
 /* Shorten every sequence to `len` cached tokens (len <= min cur_len); the
  * rows below `len` are kept.  Used to replay a timed decode window. */
 akh_status akh_session_truncate(akh_session* s, uint32_t len);
