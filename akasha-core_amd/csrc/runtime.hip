@@ -667,6 +667,7 @@ struct akh_session {
   akh_backend* be = nullptr;
   uint32_t max_ctx = 0, B = 0;
   std::vector<uint32_t> cur_len;
+  std::vector<uint8_t> has_cache;  // InferenceSession::cache is Some (per sequence)
 
   // Cache: per layer, K then V, each [B, max_ctx, dim]; sequence b's slice
   // is exactly the reference's per-session Cache tensor [max_ctx, dim].
@@ -748,6 +749,14 @@ akh_status ensure_prefill(akh_session* s, size_t rows) {
   HIP_TRY(hipMalloc(&s->pffn, rows * F * 4));
   HIP_TRY(hipMalloc(&s->ptok, rows * 4));
   s->prows = rows;
+  return AKH_OK;
+}
+
+// AkashaError::NoCache if a sequence's cache was taken (inference.rs:72, 180).
+akh_status need_caches(const akh_session* s) {
+  for (uint32_t b = 0; b < s->B; ++b)
+    if (!s->has_cache[b])
+      return fail(AKH_E_NO_CACHE, "sequence " + std::to_string(b) + " has no cache");
   return AKH_OK;
 }
 
@@ -1043,6 +1052,7 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   s->max_ctx = max_context_len;
   s->B = batch;
   s->cur_len.assign(batch, 0);
+  s->has_cache.assign(batch, 1);
   s->ks_qkv = dec_gemm_splits(DEC_CFG_QKV, c.dim);
   s->ks_out = dec_gemm_splits(DEC_CFG_OUT, c.dim);
   s->ks_up = dec_gemm_splits(DEC_CFG_UP, c.dim);
@@ -1140,6 +1150,8 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     return fail(AKH_E_PROMPT_TOO_LONG,
                 "prompt is " + std::to_string(prompt_len) +
                     " tokens, context window is " + std::to_string(s->max_ctx));
+  akh_status nc = need_caches(s);
+  if (nc != AKH_OK) return nc;
   for (uint32_t b = 0; b < s->B; ++b)
     if (s->cur_len[b] != 0)
       return fail(AKH_E_CACHE_NOT_EMPTY,
@@ -1244,6 +1256,8 @@ extern "C" akh_status akh_session_decode_step(akh_session* s,
                                               const uint32_t* tokens,
                                               float* logits, uint32_t* next) {
   CHECK_ARG(s, "akh_session_decode_step: NULL session");
+  akh_status nc = need_caches(s);
+  if (nc != AKH_OK) return nc;
   for (uint32_t b = 0; b < s->B; ++b)
     if (s->cur_len[b] >= s->max_ctx)
       return fail(AKH_E_CONTEXT_FULL, "context window is full (" +
@@ -1264,6 +1278,8 @@ extern "C" akh_status akh_session_decode_greedy(akh_session* s,
                                                 uint32_t steps,
                                                 uint32_t* out_tokens) {
   CHECK_ARG(s, "akh_session_decode_greedy: NULL session");
+  akh_status nc = need_caches(s);
+  if (nc != AKH_OK) return nc;
   for (uint32_t b = 0; b < s->B; ++b)
     if (s->cur_len[b] + steps > s->max_ctx)
       return fail(AKH_E_CONTEXT_FULL, "context window is full (" +
@@ -1331,6 +1347,12 @@ extern "C" akh_status akh_session_generate(akh_session* s, const uint32_t* token
   if (prompt_len == 0) return fail(AKH_E_EMPTY_PROMPT, "prompt is empty");
   CHECK_ARG(params.temperature <= 0.0f || uniforms || max_new_tokens == 0,
             "akh_session_generate: sampling (temperature > 0) needs uniforms");
+  // A sequence without a cache gets a fresh one (inference.rs:278-287).
+  for (uint32_t b = 0; b < s->B; ++b)
+    if (!s->has_cache[b]) {
+      s->has_cache[b] = 1;
+      s->cur_len[b] = 0;
+    }
   bool all_empty = true, all_resumed = true;
   for (uint32_t b = 0; b < s->B; ++b) {
     all_empty = all_empty && s->cur_len[b] == 0;
@@ -1383,6 +1405,49 @@ extern "C" akh_status akh_session_generate(akh_session* s, const uint32_t* token
     s->cur_len[b] = (uint32_t)pos[b];
   }
   return set_active(s, true);
+}
+
+extern "C" akh_status akh_session_take_cache(akh_session* s, uint32_t seq, float* k,
+                                             float* v, uint32_t* cur_len, int* had_cache) {
+  CHECK_ARG(s && seq < s->B, "akh_session_take_cache: bad argument");
+  const bool had = s->has_cache[seq] != 0;
+  if (had_cache) *had_cache = had ? 1 : 0;
+  if (cur_len) *cur_len = had ? s->cur_len[seq] : 0;
+  if (!had) return AKH_OK;
+  const size_t n = (size_t)s->seq_stride();
+  for (uint32_t l = 0; l < s->m->cfg.num_layers; ++l) {
+    if (k)
+      HIP_TRY(hipMemcpyAsync(k + l * n, s->kcache(l) + (size_t)seq * n, n * sizeof(float),
+                             hipMemcpyDeviceToHost, s->be->stream));
+    if (v)
+      HIP_TRY(hipMemcpyAsync(v + l * n, s->vcache(l) + (size_t)seq * n, n * sizeof(float),
+                             hipMemcpyDeviceToHost, s->be->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(s->be->stream));
+  s->has_cache[seq] = 0;
+  s->cur_len[seq] = 0;
+  return upload_positions(s);
+}
+
+extern "C" akh_status akh_session_replace_cache(akh_session* s, uint32_t seq, const float* k,
+                                                const float* v, uint32_t cur_len) {
+  CHECK_ARG(s && seq < s->B && k && v, "akh_session_replace_cache: bad argument");
+  CHECK_ARG(cur_len <= s->max_ctx, "Cache/session max_context_len mismatch");
+  const size_t n = (size_t)s->seq_stride();
+  hipStream_t st = s->be->stream;
+  for (uint32_t l = 0; l < s->m->cfg.num_layers; ++l) {
+    HIP_TRY(hipMemcpyAsync(s->kcache(l) + (size_t)seq * n, k + l * n, n * sizeof(float),
+                           hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(s->vcache(l) + (size_t)seq * n, v + l * n, n * sizeof(float),
+                           hipMemcpyHostToDevice, st));
+  }
+  // The installed cache carries no token history.
+  HIP_TRY(hipMemsetAsync(s->hist + (size_t)seq * (s->max_ctx + 1), 0,
+                         (size_t)(s->max_ctx + 1) * sizeof(uint32_t), st));
+  HIP_TRY(hipMemsetAsync(s->tok + seq, 0, sizeof(uint32_t), st));
+  s->has_cache[seq] = 1;
+  s->cur_len[seq] = cur_len;
+  return upload_positions(s);
 }
 
 extern "C" akh_status akh_session_download_cache(akh_session* s,

@@ -199,6 +199,8 @@ _SIGS = {
     "akh_session_decode_greedy": (ST, [P, U32, P]),
     "akh_session_generate": (ST, [P, P, U32, U32, Sampling, P, P, P]),
     "akh_session_truncate": (ST, [P, U32]),
+    "akh_session_take_cache": (ST, [P, U32, P, P, C.POINTER(U32), C.POINTER(C.c_int)]),
+    "akh_session_replace_cache": (ST, [P, U32, P, P, U32]),
     "akh_session_download_cache": (ST, [P, U32, U32, C.c_int, P]),
     "akh_timer_start": (ST, [P]),
     "akh_timer_stop": (ST, [P, C.POINTER(C.c_float)]),
@@ -582,6 +584,22 @@ class Session:
 
     def truncate(self, length: int):
         _check(_lib.akh_session_truncate(self.handle, length), "truncate")
+
+    def take_cache(self, seq: int):
+        """take_cache for one sequence: (k, v, cur_len) or None if it had none."""
+        c = self.model.cfg
+        shape = (c.num_layers, self.max_context_len, c.dim)
+        k, v = np.empty(shape, np.float32), np.empty(shape, np.float32)
+        n, had = U32(), C.c_int()
+        _check(_lib.akh_session_take_cache(self.handle, seq, _ptr(k), _ptr(v), C.byref(n),
+                                           C.byref(had)), "take_cache")
+        return (k, v, n.value) if had.value else None
+
+    def replace_cache(self, seq: int, k, v, cur_len: int):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        _check(_lib.akh_session_replace_cache(self.handle, seq, _ptr(k), _ptr(v), cur_len),
+               "replace_cache")
 
     def cache(self, layer: int, seq: int, which: int) -> np.ndarray:
         out = np.empty((self.max_context_len, self.model.cfg.dim), np.float32)

@@ -296,6 +296,19 @@ akh_status akh_session_generate(akh_session* s, const uint32_t* tokens,
 /* Shorten every sequence to `len` cached tokens (len <= min cur_len); the
  * rows below `len` are kept.  Used to replay a timed decode window. */
 akh_status akh_session_truncate(akh_session* s, uint32_t len);
+/* InferenceSession::take_cache (inference.rs:56-59) for sequence `seq`: its
+ * K and V ([layers, max_ctx, dim] host arrays, either may be NULL) and
+ * cur_len are copied out and the sequence is left without a cache, so that
+ * prefill and decode steps fail with AKH_E_NO_CACHE until a cache is
+ * installed (generate makes a fresh one, inference.rs:278-287).  had_cache
+ * reports whether there was one (the reference's Option). */
+akh_status akh_session_take_cache(akh_session* s, uint32_t seq, float* k, float* v,
+                                  uint32_t* cur_len, int* had_cache);
+/* replace_cache (inference.rs:42-54): install K, V ([layers, max_ctx, dim],
+ * the session's own shape) with cur_len cached tokens for sequence `seq`.
+ * The installed cache carries no token history. */
+akh_status akh_session_replace_cache(akh_session* s, uint32_t seq, const float* k,
+                                     const float* v, uint32_t cur_len);
 /* Copy sequence `seq`'s K or V cache of layer `layer` ([max_ctx, dim]) to
  * host (which: 0 = K, 1 = V). */
 akh_status akh_session_download_cache(akh_session* s, uint32_t layer,

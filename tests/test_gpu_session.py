@@ -209,3 +209,37 @@ def test_hall1_c3_prefill_sequence_matches_oracle(backend, pkg, ora):
             o.close()
     finally:
         ora.set_threads(1)
+
+
+def test_take_and_replace_cache_move_a_sequence(backend, pkg, ora):
+    # take_cache / replace_cache (inference.rs:42-59) and NoCache (:72, :180).
+    hip = pkg.hip
+    cfg = pkg.ModelConfig.new(97, 32, 4, 2, 16)
+    w = pkg.synthetic_weights(cfg, seed=31)
+    prompt = np.array([[3, 41, 7, 96, 0, 25], [11, 12, 13, 14, 15, 16]], np.uint32)
+    model, a = _session(pkg, backend, cfg, w, 16, 2)
+    a.prefill(prompt)
+    _, nxt = a.decode_step(None)
+    k, v, n = a.take_cache(1)
+    assert n == 7 and a.take_cache(1) is None
+    with pytest.raises(hip.NoCache):
+        a.decode_step(None)
+    with pytest.raises(hip.NoCache):
+        a.decode_greedy(1)
+    # Sequence 1 continues in another session's slot 0.
+    b = hip.Session(model, 16, 2)
+    b.replace_cache(0, k, v, n)
+    assert list(b.cur_len()) == [7, 0]
+    logits, _ = b.decode_step(np.array([nxt[1], 5], np.uint32))
+    o = ora.OracleSession(cfg, w, 16)
+    first = o.prefill(prompt[1])
+    o.decode_step(ora.argmax(first))
+    want = o.decode_step(int(nxt[1]))
+    o.close()
+    assert np.abs(logits[0] - want).max() < TOL
+    # Back into its own slot, sequence 1 decodes again in session a.
+    a.replace_cache(1, k, v, n)
+    a.decode_step(np.array([nxt[0], nxt[1]], np.uint32))
+    assert list(a.cur_len()) == [8, 8]
+    with pytest.raises(hip.InvalidArgument):
+        a.replace_cache(0, k, v, 17)
