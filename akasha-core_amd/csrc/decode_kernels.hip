@@ -484,6 +484,15 @@ template <int QPT>
 __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
   __shared__ float red4[4];
   const int m = blockIdx.x, d = p.d, nq = d / 4;
+  // The gain does not depend on the row: request it first, so its memory
+  // round trip overlaps the row's.
+  float4 g[QPT];
+#pragma unroll
+  for (int i = 0; i < QPT; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    g[i] = q < nq ? *reinterpret_cast<const float4*>(p.gain + 4 * q)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   const float* row = nullptr;
   if (p.ids) {
     const uint32_t id = p.ids[m];
@@ -517,11 +526,10 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
   for (int i = 0; i < QPT; ++i) {
     const int q = threadIdx.x + 256 * i;
     if (q < nq) {
-      const float4 g = *reinterpret_cast<const float4*>(p.gain + 4 * q);
       const float4 v = x[i];
       *reinterpret_cast<float4*>(p.xnt + ((size_t)q * 32 + m) * 4) = make_float4(
-          __fmul_rn(__fmul_rn(v.x, rs), g.x), __fmul_rn(__fmul_rn(v.y, rs), g.y),
-          __fmul_rn(__fmul_rn(v.z, rs), g.z), __fmul_rn(__fmul_rn(v.w, rs), g.w));
+          __fmul_rn(__fmul_rn(v.x, rs), g[i].x), __fmul_rn(__fmul_rn(v.y, rs), g[i].y),
+          __fmul_rn(__fmul_rn(v.z, rs), g[i].z), __fmul_rn(__fmul_rn(v.w, rs), g[i].w));
     }
   }
 }
