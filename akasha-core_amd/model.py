@@ -74,8 +74,18 @@ class ModelConfig:
         return int(sum(np.prod(s) for s in self.param_shapes()))
 
 
-def synthetic_weights(cfg: ModelConfig, seed: int, std: float = 0.02):
-    """Weights in params() order: matrices N(0, std), gains 1 + N(0, std)."""
+def round_to_bf16(a: np.ndarray) -> np.ndarray:
+    """float32 values rounded to the nearest bfloat16 (ties to even), kept in
+    float32: exactly representable in bf16."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    return r.view(np.float32)
+
+
+def synthetic_weights(cfg: ModelConfig, seed: int, std: float = 0.02, bf16: bool = False):
+    """Weights in params() order: matrices N(0, std), gains 1 + N(0, std).
+    With ``bf16`` every value is rounded to the nearest bfloat16 (the scaled
+    configuration's "bf16 weights"), still stored as float32."""
     rng = np.random.default_rng(seed)
     out = []
     for shape in cfg.param_shapes():
@@ -83,6 +93,8 @@ def synthetic_weights(cfg: ModelConfig, seed: int, std: float = 0.02):
         a *= np.float32(std)
         if len(shape) == 1:
             a += np.float32(1.0)
+        if bf16:
+            a = round_to_bf16(a)
         out.append(a.reshape(shape))
     return out
 

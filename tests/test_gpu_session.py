@@ -243,3 +243,32 @@ def test_take_and_replace_cache_move_a_sequence(backend, pkg, ora):
     assert list(a.cur_len()) == [8, 8]
     with pytest.raises(hip.InvalidArgument):
         a.replace_cache(0, k, v, 17)
+
+
+def test_scaled_config_matches_oracle(backend, pkg, ora):
+    # Config 5 architecture: dim 2048, 24 layers, 16 heads x 128, FFN 8192,
+    # vocab 50257, bf16-valued weights N(0,0.02) from seed 5.  Two sequences
+    # with 24-token prompts (seed 6) and 3 greedy steps against the oracle
+    # (a 2048-token prompt is beyond the CPU oracle's budget here).
+    cfg = pkg.ModelConfig.scaled()
+    w = pkg.synthetic_weights(cfg, seed=5, bf16=True)
+    prompt = pkg.synthetic_tokens(2 * 24, cfg.vocab_size, seed=6).reshape(2, 24)
+    model, s = _session(pkg, backend, cfg, w, 64, 2)
+    logits, nxt = s.prefill(prompt)
+    steps = [(logits, nxt)]
+    for _ in range(3):
+        steps.append(s.decode_step(None))
+    ora.set_threads(16)
+    try:
+        for b in range(2):
+            o = ora.OracleSession(cfg, w, 64)
+            ref = o.prefill(prompt[b])
+            for i, (lg, nx) in enumerate(steps):
+                if i:
+                    ref = o.decode_step(ora.argmax(ref))
+                assert np.abs(lg[b] - ref).max() < TOL, f"sequence {b} step {i}"
+                assert int(nx[b]) == ora.argmax(ref), f"sequence {b} step {i}"
+            o.close()
+    finally:
+        ora.set_threads(1)
+    del w
