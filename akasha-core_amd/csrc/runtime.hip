@@ -1123,6 +1123,14 @@ extern "C" akh_status akh_session_cur_len(const akh_session* s, uint32_t* out) {
   return AKH_OK;
 }
 
+extern "C" akh_status akh_session_set_len(akh_session* s, uint32_t len) {
+  CHECK_ARG(s && len <= s->max_ctx, "akh_session_set_len: bad argument");
+  akh_status nc = need_caches(s);
+  if (nc != AKH_OK) return nc;
+  std::fill(s->cur_len.begin(), s->cur_len.end(), len);
+  return upload_positions(s);
+}
+
 extern "C" akh_status akh_session_truncate(akh_session* s, uint32_t len) {
   CHECK_ARG(s, "akh_session_truncate: NULL session");
   for (uint32_t b = 0; b < s->B; ++b)

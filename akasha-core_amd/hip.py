@@ -199,6 +199,7 @@ _SIGS = {
     "akh_session_decode_greedy": (ST, [P, U32, P]),
     "akh_session_generate": (ST, [P, P, U32, U32, Sampling, P, P, P]),
     "akh_session_truncate": (ST, [P, U32]),
+    "akh_session_set_len": (ST, [P, U32]),
     "akh_session_take_cache": (ST, [P, U32, P, P, C.POINTER(U32), C.POINTER(C.c_int)]),
     "akh_session_replace_cache": (ST, [P, U32, P, P, U32]),
     "akh_session_download_cache": (ST, [P, U32, U32, C.c_int, P]),
@@ -584,6 +585,10 @@ class Session:
 
     def truncate(self, length: int):
         _check(_lib.akh_session_truncate(self.handle, length), "truncate")
+
+    def set_len(self, length: int):
+        """Cache::cur_len = length for every sequence (rows untouched)."""
+        _check(_lib.akh_session_set_len(self.handle, length), "set_len")
 
     def take_cache(self, seq: int):
         """take_cache for one sequence: (k, v, cur_len) or None if it had none."""

@@ -74,6 +74,61 @@ def prefill_flops(cfg, B, S):
     return gemm + attn + lm
 
 
+def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True):
+    """Config 5: the scaled architecture (dim 2048, 24 layers, 16 x 128, FFN
+    8192, vocab 50257) with bf16-valued weights (seed 5).  Decode: 64
+    sequences (two 32-row sessions) for `steps` steps ending at KV length
+    2048, over a zero KV prefix declared with set_len (the cost of a step does
+    not depend on the cached values).  Prefill: 8 x 2048 (seed 7)."""
+    cfg = pkg.ModelConfig.scaled()
+    log("bench: scaled config weights (seed 5, bf16 values)")
+    w = pkg.synthetic_weights(cfg, seed=5, bf16=True)
+    model = hip.Model(be, cfg)
+    model.upload(w)
+    del w
+    T = 2048
+    sess = [hip.Session(model, T, 32) for _ in range(2)]
+    for s in sess:
+        s.set_len(T - steps)
+        s.decode_greedy(1, want_tokens=False)  # capture + warm
+        s.set_len(T - steps)
+    be.synchronize()
+    be.timer_start()
+    for s in sess:
+        s.decode_greedy(steps, want_tokens=False)
+    ms = be.timer_stop()
+    d, L, V = cfg.dim, cfg.num_layers, cfg.vocab_size
+    weights = 4 * (sum(int(np.prod(x)) for x in cfg.param_shapes()) - V * d)
+    kv = sum(2 * L * 64 * (T - steps + i + 1) * d * 4 for i in range(steps))
+    step_bytes = (2 * weights * steps + kv) / steps
+    out = {"workload": "config 5: scaled architecture, bf16-valued weights (seed 5), decode of 64 "
+                       f"sequences (2 x 32-row sessions), {steps} steps to KV length 2048, fp32 KV",
+           "decode_ms_per_step": round(ms / steps, 3),
+           "decode_tok_s": round(64 * steps / (ms / 1e3), 1),
+           "decode_hbm_frac": round(step_bytes / (ms / steps / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+           "bytes_per_step": int(step_bytes)}
+    for s in sess:
+        s.close()
+    if with_prefill:
+        Bp, Sp = 8, 2048
+        ps = hip.Session(model, Sp, Bp)
+        toks = pkg.synthetic_tokens(Bp * Sp, V, seed=7).reshape(Bp, Sp)
+        log("bench: scaled config prefill 8 x 2048")
+        ps.prefill(toks, want_logits=False)
+        ps.reset()
+        be.synchronize()
+        be.timer_start()
+        ps.prefill(toks, want_logits=False)
+        pms = be.timer_stop()
+        fl = prefill_flops(cfg, Bp, Sp)
+        out.update({"prefill_ms": round(pms, 2), "prefill_tok_s": round(Bp * Sp / (pms / 1e3), 1),
+                    "prefill_tflops": round(fl / (pms / 1e3) / 1e12, 2),
+                    "prefill_mfma_frac_fp32": round(fl / (pms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)})
+        ps.close()
+    model.close()
+    return out
+
+
 def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=1):
     ora = entry.load_oracle()
     ora.set_threads(threads)
@@ -100,6 +155,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     ap.add_argument("--kernel-reps", type=int, default=60)
+    ap.add_argument("--scaled", action="store_true",
+                    help="also measure config 5 (scaled architecture) decode and prefill")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -196,6 +253,10 @@ def main():
                    "flop": fl}
         ps.close()
 
+    scaled = None
+    if args.scaled:
+        scaled = scaled_measurement(pkg, hip, be, with_prefill=not args.no_prefill)
+
     cpu = None
     if not args.no_cpu:
         log("bench: CPU baseline (oracle decode step, 1 thread)")
@@ -240,6 +301,7 @@ def main():
                           "bytes_per_step_mean": int(total_bytes / args.steps)},
         "kernels": kernels,
         "prefill": prefill,
+        "scaled": scaled,
         "cpu_baseline": cpu,
         "cpu_baseline_omp": cpu_omp,
     }

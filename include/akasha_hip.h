@@ -293,6 +293,11 @@ akh_status akh_session_generate(akh_session* s, const uint32_t* tokens,
                                 uint32_t prompt_len, uint32_t max_new_tokens,
                                 akh_sampling params, const double* uniforms,
                                 uint32_t* out_tokens, uint32_t* out_counts);
+/* Set every sequence's cached length to `len` (<= max_ctx) without touching
+ * the cache rows, as assigning the reference's public Cache::cur_len does
+ * (inference_graphs.rs:515); rows below `len` keep whatever they hold.  Used
+ * to time decode at a given context length. */
+akh_status akh_session_set_len(akh_session* s, uint32_t len);
 /* Shorten every sequence to `len` cached tokens (len <= min cur_len); the
  * rows below `len` are kept.  Used to replay a timed decode window. */
 akh_status akh_session_truncate(akh_session* s, uint32_t len);

@@ -98,6 +98,27 @@ def test_decode_greedy_matches_step_by_step(backend, pkg):
     assert np.array_equal(a.decode_greedy(20), toks)
 
 
+def test_set_len_keeps_rows(backend, pkg, ora):
+    # Cache::cur_len is a public field (inference_graphs.rs:515): moving it
+    # back and forth leaves the cached rows as they were.
+    cfg = pkg.ModelConfig.new(97, 32, 4, 2, 16)
+    w = pkg.synthetic_weights(cfg, seed=33)
+    prompt = np.array([[3, 41, 7, 96, 0, 25], [11, 12, 13, 14, 15, 16]], np.uint32)
+    _, s = _session(pkg, backend, cfg, w, 16, 2)
+    s.prefill(prompt)
+    s.set_len(2)
+    assert list(s.cur_len()) == [2, 2]
+    s.set_len(6)
+    logits, _ = s.decode_step(np.array([9, 9], np.uint32))
+    for b in range(2):
+        o = ora.OracleSession(cfg, w, 16)
+        o.prefill(prompt[b])
+        assert np.abs(logits[b] - o.decode_step(9)).max() < TOL
+        o.close()
+    with pytest.raises(pkg.hip.InvalidArgument):
+        s.set_len(17)
+
+
 def test_session_errors(backend, pkg):
     h = pkg.hip
     cfg = pkg.ModelConfig.new(97, 32, 4, 2, 16)
