@@ -188,17 +188,25 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     }
 }
 
-// Causal flash attention, head_dim 64, on MFMA.  Block = 4 waves x 32
-// queries of one (sequence, head); keys stream through LDS in blocks of 32.
-// Each wave computes S^T = K Q^T so every lane owns one query (column) and
-// 16 keys, making the online-softmax row statistics lane-local (plus one
+// Causal flash attention on MFMA for head_dim 64 and 128.  Block = 4 waves x
+// 32 queries of one (sequence, head); keys stream through LDS in blocks of
+// 32.  Each wave computes S^T = K Q^T so every lane owns one query (column)
+// and 16 keys, making the online-softmax row statistics lane-local (plus one
 // exchange between the two half-waves); P^T then feeds O^T += V^T P^T
-// straight from the accumulator registers.
-__global__ __launch_bounds__(256) void k_flash64(FlashParams p) {
-  constexpr int HD = 64, QB = 128, KB = 32;
-  __shared__ float Ks[KB][HD + 1];
-  __shared__ float Vs[KB][HD];
-  __shared__ float Os[4][32][HD + 1];
+// straight from the accumulator registers, one 32-dim tile per HD/32.
+// Query blocks run in reverse order so the longest (last) ones start first.
+template <int HD>
+__global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParams p) {
+  constexpr int QB = 128, KB = 32, NT = HD / 32, HQ = HD / 2;
+  constexpr int KP = HD + 1;            // padded K row
+  constexpr int CPR = HD / 4;           // float4 per K/V row
+  constexpr int RPP = 256 / CPR;        // rows per cooperative pass
+  constexpr int NP = KB / RPP;          // passes per key block
+  constexpr int KV_FLOATS = KB * KP + KB * HD;
+  constexpr int O_FLOATS = 4 * 32 * 33;  // one 32x32 tile per wave
+  __shared__ float lds[KV_FLOATS > O_FLOATS ? KV_FLOATS : O_FLOATS];
+  float (*Ks)[KP] = reinterpret_cast<float (*)[KP]>(lds);
+  float (*Vs)[HD] = reinterpret_cast<float (*)[HD]>(lds + KB * KP);
 
   int S = p.S, d = p.d;
   float scale = p.scale;
@@ -210,7 +218,7 @@ __global__ __launch_bounds__(256) void k_flash64(FlashParams p) {
     roff = (long)p.meta->row_offset * d;
   }
   const int H = d / HD;
-  const int qblk = blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int qblk = gridDim.x - 1 - blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -220,32 +228,34 @@ __global__ __launch_bounds__(256) void k_flash64(FlashParams p) {
   const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
   const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
 
-  // This lane's query row and its 32 dims (half h).
+  // This lane's query row and its HD/2 dims (half h).
   const int qi = q0 + wave * 32 + j;
-  float qreg[32];
+  float qreg[HQ];
   {
-    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 32 * h;
+    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + HQ * h;
 #pragma unroll
-    for (int s = 0; s < 32; s += 4) {
+    for (int s = 0; s < HQ; s += 4) {
       const float4 t = *reinterpret_cast<const float4*>(qr + s);
       qreg[s] = t.x; qreg[s + 1] = t.y; qreg[s + 2] = t.z; qreg[s + 3] = t.w;
     }
   }
-  f32x16 o0 = zero16(), o1 = zero16();
+  f32x16 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = zero16();
   float mrow = -INFINITY, lrow = 0.f;
 
   const int wave_qmax = q0 + wave * 32 + 31;
   const int kend = min(S, q0 + QB);  // keys needed by the block
   const int nkb = (kend + KB - 1) / KB;
 
-  // Cooperative K/V block load: thread t loads rows t/16 and t/16 + 16,
-  // float4 column t%16, of both tensors.
-  const int lr = tid >> 4, lc = (tid & 15) * 4;
-  float4 kr[2], vr[2];
+  // Cooperative K/V block load: thread t loads float4 column t % CPR of rows
+  // t / CPR + RPP * q, of both tensors.
+  const int lr = tid / CPR, lc = (tid % CPR) * 4;
+  float4 kr[NP], vr[NP];
   auto load_kv = [&](int kb) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int key = kb * KB + lr + 16 * q;
+    for (int q = 0; q < NP; ++q) {
+      const int key = kb * KB + lr + RPP * q;
       const size_t off = (size_t)(key < S ? key : 0) * d + lc;
       kr[q] = *reinterpret_cast<const float4*>(kp + off);
       vr[q] = *reinterpret_cast<const float4*>(vp + off);
@@ -255,20 +265,21 @@ __global__ __launch_bounds__(256) void k_flash64(FlashParams p) {
   for (int kb = 0; kb < nkb; ++kb) {
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int r = lr + 16 * q;
+    for (int q = 0; q < NP; ++q) {
+      const int r = lr + RPP * q;
       Ks[r][lc] = kr[q].x; Ks[r][lc + 1] = kr[q].y;
       Ks[r][lc + 2] = kr[q].z; Ks[r][lc + 3] = kr[q].w;
-      *reinterpret_cast<float4*>(&Vs[r][lc]) = vr[q];
+      *reinterpret_cast<float4*>(&Vs[r][lc]) =
+          make_float4(vr[q].x, vr[q].y, vr[q].z, vr[q].w);
     }
     __syncthreads();
-    if (kb + 1 < nkb) load_kv(kb + 1);
+    load_kv(kb + 1);  // rows past S read row 0: harmless, never used
     const int j0 = kb * KB;
     if (j0 > wave_qmax) continue;  // block entirely above this wave's rows
 
     f32x16 st = zero16();
 #pragma unroll
-    for (int s = 0; s < 32; ++s) st = mfma32(Ks[j][32 * h + s], qreg[s], st);
+    for (int s = 0; s < HQ; ++s) st = mfma32(Ks[j][HQ * h + s], qreg[s], st);
 
     float pm = -INFINITY;
 #pragma unroll
@@ -293,38 +304,39 @@ __global__ __launch_bounds__(256) void k_flash64(FlashParams p) {
     lrow = lrow * corr + ps;
     mrow = mnew;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      o0[r] *= corr;
-      o1[r] *= corr;
-    }
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
     // O^T += V^T P^T: step s uses key acc_row(s, h) on both operands.
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       const int key = acc_row(s, h);
-      o0 = mfma32(Vs[key][j], st[s], o0);
-      o1 = mfma32(Vs[key][32 + j], st[s], o1);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) o[t] = mfma32(Vs[key][32 * t + j], st[s], o[t]);
     }
   }
 
-  // O^T (rows = dims) -> LDS -> coalesced row writes.
+  // O^T (rows = dims) -> LDS, one 32-dim tile at a time -> coalesced rows.
   const float inv = 1.0f / lrow;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    Os[wave][j][acc_row(r, h)] = o0[r] * inv;
-    Os[wave][j][32 + acc_row(r, h)] = o1[r] * inv;
-  }
-  __syncthreads();
+  float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33);
   float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD;
-  for (int e = lane; e < 32 * HD; e += 64) {
-    const int r = e / HD, c = e % HD;
-    const int qrow = q0 + wave * 32 + r;
-    if (qrow < S) op[(size_t)qrow * d + c] = Os[wave][r][c];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Os[j][acc_row(r, h)] = o[t][r] * inv;
+    __syncthreads();
+    for (int e = lane; e < 32 * 32; e += 64) {
+      const int r = e >> 5, c = e & 31;
+      const int qrow = q0 + wave * 32 + r;
+      if (qrow < S) op[(size_t)qrow * d + 32 * t + c] = Os[r][c];
+    }
   }
   if (p.lse && h == 0 && qi < S) p.lse[(size_t)qi * H + hh] = mrow + logf(lrow);
 }
 
-// Causal flash attention for other head sizes (up to 128, as the reference
-// asserts, emit.rs:564-567): one thread per query row with an HD-float
+// Causal flash attention for the small head sizes (2..32; the reference
+// allows up to 128, emit.rs:564-567): one thread per query row with an HD-float
 // accumulator, keys staged through LDS in blocks of 64 shared by the
 // block's 64 queries.
 template <int HD>
@@ -405,9 +417,12 @@ hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
 hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
                         hipStream_t s) {
   const int H = p.d / p.hd;
-  if (p.hd == 64) {
-    hipLaunchKernelGGL(k_flash64, dim3((max_rows + 127) / 128, H, batch),
-                       dim3(256), 0, s, p);
+  if (p.hd == 64 || p.hd == 128) {
+    const dim3 g((max_rows + 127) / 128, H, batch);
+    if (p.hd == 64)
+      hipLaunchKernelGGL(k_flash_mfma<64>, g, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(k_flash_mfma<128>, g, dim3(256), 0, s, p);
     return hipGetLastError();
   }
   dim3 g((max_rows + 63) / 64, H, batch), b(64);
@@ -417,7 +432,6 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
     case 8: hipLaunchKernelGGL(k_flash_generic<8>, g, b, 0, s, p); break;
     case 16: hipLaunchKernelGGL(k_flash_generic<16>, g, b, 0, s, p); break;
     case 32: hipLaunchKernelGGL(k_flash_generic<32>, g, b, 0, s, p); break;
-    case 128: hipLaunchKernelGGL(k_flash_generic<128>, g, b, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -139,7 +139,7 @@ def _flash(backend, h, q, k, v, seq, dim, hd, row_offset=0, total_rows=None):
 
 
 @pytest.mark.parametrize("seq,heads,hd", [(8, 2, 4), (37, 3, 16), (65, 12, 64), (200, 2, 64),
-                                          (130, 1, 128)])
+                                          (130, 1, 128), (300, 2, 128), (1024, 4, 128)])
 def test_flash_attention(backend, pkg, ora, seq, heads, hd):
     # flash_attention_matches_cpu_reference (emit.rs:1001-1098), tol 1e-3.
     h = pkg.hip

@@ -232,6 +232,25 @@ def test_hall1_c3_prefill_sequence_matches_oracle(backend, pkg, ora):
         ora.set_threads(1)
 
 
+def test_head_dim_128_prefill_matches_oracle(backend, pkg, ora):
+    # head_dim 128 (the scaled configuration's heads) over 300-token prompts:
+    # several key blocks per query block and a ragged last query block.
+    cfg = pkg.ModelConfig.new(300, 256, 2, 2, 320)
+    w = pkg.synthetic_weights(cfg, seed=35)
+    toks = pkg.synthetic_tokens(3 * 300, cfg.vocab_size, seed=36).reshape(3, 300)
+    _, s = _session(pkg, backend, cfg, w, 320, 3)
+    logits, nxt = s.prefill(toks)
+    steps = [s.decode_step(None) for _ in range(2)]
+    for b in range(3):
+        o = ora.OracleSession(cfg, w, 320)
+        ref = o.prefill(toks[b])
+        assert np.abs(logits[b] - ref).max() < TOL and int(nxt[b]) == ora.argmax(ref)
+        for lg, nx in steps:
+            ref = o.decode_step(ora.argmax(ref))
+            assert np.abs(lg[b] - ref).max() < TOL and int(nx[b]) == ora.argmax(ref)
+        o.close()
+
+
 def test_take_and_replace_cache_move_a_sequence(backend, pkg, ora):
     # take_cache / replace_cache (inference.rs:42-59) and NoCache (:72, :180).
     hip = pkg.hip
