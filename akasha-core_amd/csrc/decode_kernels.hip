@@ -48,6 +48,45 @@ __global__ __launch_bounds__(256) void k_pack_tiles(const float* __restrict__ w,
   *reinterpret_cast<float4*>(out + (((size_t)t * (Kp / 4) + q) * 32 + j) * 4) = v;
 }
 
+// The same tiles with bfloat16 elements in k-octets: element (k, n) of tile
+// t = n / 32 at ((k / 8) * 32 + n % 32) * 8 + k % 8, so a lane's 16-byte load
+// holds eight consecutive k of its column.  Used only for matrices whose
+// every value is a bfloat16 (low 16 bits zero), so the conversion is exact.
+__global__ __launch_bounds__(256) void k_pack_tiles_bf16(const float* __restrict__ w, int K,
+                                                         int N, int Kp,
+                                                         uint16_t* __restrict__ out) {
+  const int j = threadIdx.x & 31;
+  const int o = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int t = blockIdx.y;
+  if (8 * o >= Kp) return;
+  const int n = t * 32 + j;
+  uint32_t v[4] = {0u, 0u, 0u, 0u};
+  if (n < N) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int k = 8 * o + e;
+      const uint32_t bits = k < K ? __float_as_uint(w[(size_t)k * N + n]) >> 16 : 0u;
+      v[e / 2] |= bits << (16 * (e % 2));
+    }
+  }
+  *reinterpret_cast<uint4*>(out + (((size_t)t * (Kp / 8) + o) * 32 + j) * 8) =
+      make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// flag = 1 if any of the n values has nonzero low 16 bits (not a bfloat16).
+__global__ __launch_bounds__(256) void k_check_bf16(const uint32_t* __restrict__ w, size_t n,
+                                                    int* flag) {
+  uint32_t any = 0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    any |= w[i] & 0xFFFFu;
+  if (__any(any != 0) && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+}
+
+__device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
+  return make_float4(__uint_as_float(lo << 16), __uint_as_float(lo & 0xFFFF0000u),
+                     __uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u));
+}
+
 // Y (epilogue) A[M, K] . W[K, N] for M <= 32, W packed in 32-column tiles.
 //
 // Grid (N / 32 tiles, K chunks), W waves per block.  Lane (j, h) owns column
@@ -61,12 +100,16 @@ __global__ __launch_bounds__(256) void k_pack_tiles(const float* __restrict__ w,
 // (fixed order); wave 0 runs the epilogue.
 //
 // PRO_SILU_SUM: A = silu(sum of p.nparts k-quad partial tiles at p.xt).
-template <int W, int HL, int EPI, int PRO>
+// BF: W is packed in bfloat16 k-octets (k_pack_tiles_bf16); a lane loads
+// eight k per 16 bytes and the MFMAs, their order and the results are those
+// of the float tiles holding the same values.
+template <int W, int HL, int EPI, int PRO, bool BF>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   constexpr int RH = W > 1 ? W / 2 : 1;
   constexpr int KC = 2 * W * HL;
   constexpr int HQ = HL / 4;
   static_assert(HL % 4 == 0, "HL must cover whole k-quads");
+  static_assert(!BF || HL % 8 == 0, "bfloat16 tiles need whole k-octets");
   __shared__ float red[RH][32][33];
 
   const int M = p.M, N = p.N, K = p.K;
@@ -74,22 +117,32 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   const int j = lane & 31, h = lane >> 5;
   const int tile = blockIdx.x, col = tile * 32 + j;
   const bool cok = col < N;
-  const int per = (K + (int)gridDim.y - 1) / (int)gridDim.y;
-  const int rows = (per + KC - 1) / KC * KC;  // whole passes per block
+  const int rows = p.kpass * KC;  // whole passes per block
   const int kb = blockIdx.y * rows;
   if (kb >= K) return;
   const int ke = min(K, kb + rows);
   const float* wt = p.w + (size_t)tile * p.Kp * 32 + j * 4;
+  const uint16_t* wh = reinterpret_cast<const uint16_t*>(p.w) + (size_t)tile * p.Kp * 32 + j * 8;
 
   f32x16 acc = zero16();
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;  // first k-quad of this half
     float4 b[HQ], a[HQ];
+    uint4 bh[BF ? HQ / 2 : 1];
+    if (BF) {
 #pragma unroll
-    for (int q = 0; q < HQ; ++q) {
-      const int kq = kq0 + q;
-      b[q] = 4 * kq < ke ? *reinterpret_cast<const float4*>(wt + (size_t)kq * 128)
-                         : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int q = 0; q < HQ; q += 2) {
+        const int kq = kq0 + q;  // even: HL is a multiple of 8
+        bh[q / 2] = 4 * kq < ke ? *reinterpret_cast<const uint4*>(wh + (size_t)kq * 128)
+                                : make_uint4(0u, 0u, 0u, 0u);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < HQ; ++q) {
+        const int kq = kq0 + q;
+        b[q] = 4 * kq < ke ? *reinterpret_cast<const float4*>(wt + (size_t)kq * 128)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
 #pragma unroll
     for (int q = 0; q < HQ; ++q) {
@@ -134,6 +187,13 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
         }
       }
       a[q] = t;
+    }
+    if (BF) {
+#pragma unroll
+      for (int q = 0; q < HQ; q += 2) {
+        b[q] = bf16x4(bh[q / 2].x, bh[q / 2].y);
+        b[q + 1] = bf16x4(bh[q / 2].z, bh[q / 2].w);
+      }
     }
 #pragma unroll
     for (int q = 0; q < HQ; ++q) {
@@ -567,11 +627,14 @@ __global__ __launch_bounds__(256) void k_argmax_final(
 namespace {
 
 // Launch shapes per role (W waves, HL rows per half-wave), chosen by timing
-// whole decode steps on MI355X; each can be overridden at build time, e.g.
-// -DAKH_SHAPE_QKV=4,24.  The four layer GEMMs split K into a few chunks
-// (enough blocks to occupy the GPU, few partial tiles for the consumer to
-// sum); the generic lm_head (K beyond the persistent kernel's reach) runs
-// whole-K blocks.
+// whole decode steps on MI355X, one set for matrices under AKH_LARGE_GEMM
+// elements (hall-1.0's) and one for larger (the scaled configuration's);
+// each can be overridden at build time, e.g. -DAKH_SHAPE_QKV=4,24 or
+// -DAKH_SHAPE_L_OUT=4,16.  The four layer GEMMs split K into chunks of
+// whole passes: one pass per block while the grid stays within
+// AKH_GEMM_BLOCKS blocks, more passes per block (fewer partial tiles for the
+// consumer to sum) beyond; the generic lm_head (K beyond the persistent
+// kernel's reach) runs whole-K blocks.
 #ifndef AKH_SHAPE_QKV
 #define AKH_SHAPE_QKV 4, 24
 #endif
@@ -587,31 +650,96 @@ namespace {
 #ifndef AKH_SHAPE_LM
 #define AKH_SHAPE_LM 4, 16
 #endif
-template <int ROLE>
+#ifndef AKH_SHAPE_L_QKV
+#define AKH_SHAPE_L_QKV 4, 24
+#endif
+#ifndef AKH_SHAPE_L_OUT
+#define AKH_SHAPE_L_OUT 4, 16
+#endif
+#ifndef AKH_SHAPE_L_UP
+#define AKH_SHAPE_L_UP 8, 32
+#endif
+#ifndef AKH_SHAPE_L_DOWN
+#define AKH_SHAPE_L_DOWN 8, 8
+#endif
+#ifndef AKH_SHAPE_L_LM
+#define AKH_SHAPE_L_LM 4, 16
+#endif
+#ifndef AKH_LARGE_GEMM
+#define AKH_LARGE_GEMM (1l << 22)
+#endif
+#ifndef AKH_GEMM_BLOCKS
+#define AKH_GEMM_BLOCKS 2048
+#endif
+
+template <int ROLE, bool LARGE>
 struct RoleShape;
-#define AKH_ROLE_SHAPE(R, w, hl) \
-  template <> struct RoleShape<R> { static constexpr int W = w, HL = hl; };
+#define AKH_ROLE_SHAPE(R, L, w, hl) \
+  template <> struct RoleShape<R, L> { static constexpr int W = w, HL = hl; };
 #define AKH_ROLE_SHAPE_(...) AKH_ROLE_SHAPE(__VA_ARGS__)
-AKH_ROLE_SHAPE_(DEC_CFG_QKV, AKH_SHAPE_QKV)
-AKH_ROLE_SHAPE_(DEC_CFG_OUT, AKH_SHAPE_OUT)
-AKH_ROLE_SHAPE_(DEC_CFG_UP, AKH_SHAPE_UP)
-AKH_ROLE_SHAPE_(DEC_CFG_DOWN, AKH_SHAPE_DOWN)
-AKH_ROLE_SHAPE_(DEC_CFG_LM, AKH_SHAPE_LM)
+AKH_ROLE_SHAPE_(DEC_CFG_QKV, false, AKH_SHAPE_QKV)
+AKH_ROLE_SHAPE_(DEC_CFG_OUT, false, AKH_SHAPE_OUT)
+AKH_ROLE_SHAPE_(DEC_CFG_UP, false, AKH_SHAPE_UP)
+AKH_ROLE_SHAPE_(DEC_CFG_DOWN, false, AKH_SHAPE_DOWN)
+AKH_ROLE_SHAPE_(DEC_CFG_LM, false, AKH_SHAPE_LM)
+AKH_ROLE_SHAPE_(DEC_CFG_QKV, true, AKH_SHAPE_L_QKV)
+AKH_ROLE_SHAPE_(DEC_CFG_OUT, true, AKH_SHAPE_L_OUT)
+AKH_ROLE_SHAPE_(DEC_CFG_UP, true, AKH_SHAPE_L_UP)
+AKH_ROLE_SHAPE_(DEC_CFG_DOWN, true, AKH_SHAPE_L_DOWN)
+AKH_ROLE_SHAPE_(DEC_CFG_LM, true, AKH_SHAPE_L_LM)
+
+bool large_gemm(int K, int N) { return (long)K * N >= AKH_LARGE_GEMM; }
+
+// K passes (of KC rows) per block; every one of the role_splits blocks of
+// a column tile gets at least one pass.
+template <int ROLE, bool LARGE>
+int role_kpass(int K, int N) {
+  constexpr int KC = 2 * RoleShape<ROLE, LARGE>::W * RoleShape<ROLE, LARGE>::HL;
+  const int passes = (K + KC - 1) / KC;
+  if (ROLE == DEC_CFG_LM) return passes;
+  const int want = std::max(1, std::min(passes, AKH_GEMM_BLOCKS / ((N + 31) / 32)));
+  return (passes + want - 1) / want;
+}
+
+template <int ROLE, bool LARGE>
+int role_splits(int K, int N) {
+  constexpr int KC = 2 * RoleShape<ROLE, LARGE>::W * RoleShape<ROLE, LARGE>::HL;
+  const int passes = (K + KC - 1) / KC, kp = role_kpass<ROLE, LARGE>(K, N);
+  return (passes + kp - 1) / kp;
+}
 
 template <int ROLE>
-int role_splits(int K) {
-  if (ROLE == DEC_CFG_LM) return 1;
-  constexpr int KC = 2 * RoleShape<ROLE>::W * RoleShape<ROLE>::HL;
-  return (K + KC - 1) / KC;
+int role_splits(int K, int N) {
+  return large_gemm(K, N) ? role_splits<ROLE, true>(K, N) : role_splits<ROLE, false>(K, N);
+}
+
+template <int ROLE>
+bool role_bf16(int K, int N) {
+  return large_gemm(K, N) ? RoleShape<ROLE, true>::HL % 8 == 0
+                          : RoleShape<ROLE, false>::HL % 8 == 0;
+}
+
+template <int ROLE, bool LARGE, int EPI, int PRO>
+hipError_t dec_go_shape(DecGemmParams p, hipStream_t s) {
+  using S = RoleShape<ROLE, LARGE>;
+  p.kpass = role_kpass<ROLE, LARGE>(p.K, p.N);
+  const dim3 g((p.N + 31) / 32, role_splits<ROLE, LARGE>(p.K, p.N)), b(64 * S::W);
+  if constexpr (S::HL % 8 == 0) {
+    if (p.wbf16) {
+      hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, true>), g, b, 0, s, p);
+      return hipGetLastError();
+    }
+  } else if (p.wbf16) {
+    return hipErrorInvalidValue;  // never tiled so (dec_bf16_capable)
+  }
+  hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, false>), g, b, 0, s, p);
+  return hipGetLastError();
 }
 
 template <int ROLE, int EPI, int PRO>
 hipError_t dec_go(const DecGemmParams& p, hipStream_t s) {
-  using S = RoleShape<ROLE>;
-  hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO>),
-                     dim3((p.N + 31) / 32, role_splits<ROLE>(p.K)), dim3(64 * S::W), 0,
-                     s, p);
-  return hipGetLastError();
+  return large_gemm(p.K, p.N) ? dec_go_shape<ROLE, true, EPI, PRO>(p, s)
+                              : dec_go_shape<ROLE, false, EPI, PRO>(p, s);
 }
 
 // The persistent lm_head covers K <= 2 * 8 * 64 (A held in registers) and
@@ -624,26 +752,46 @@ bool lm_persistent(int N, int K) {
 
 }  // namespace
 
-hipError_t launch_pack_tiles(const float* w, int K, int N, int Kp, float* out,
+hipError_t launch_pack_tiles(const float* w, int K, int N, int Kp, float* out, bool bf16,
                              hipStream_t s) {
-  if (K <= 0 || N <= 0 || Kp < K || Kp % 4 != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_pack_tiles, dim3((Kp / 4 + 7) / 8, (N + 31) / 32), dim3(256), 0, s,
-                     w, K, N, Kp, out);
+  if (K <= 0 || N <= 0 || Kp < K || Kp % (bf16 ? 8 : 4) != 0) return hipErrorInvalidValue;
+  if (bf16)
+    hipLaunchKernelGGL(k_pack_tiles_bf16, dim3((Kp / 8 + 7) / 8, (N + 31) / 32), dim3(256), 0,
+                       s, w, K, N, Kp, reinterpret_cast<uint16_t*>(out));
+  else
+    hipLaunchKernelGGL(k_pack_tiles, dim3((Kp / 4 + 7) / 8, (N + 31) / 32), dim3(256), 0, s,
+                       w, K, N, Kp, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_check_bf16(const float* w, size_t n, int* flag, hipStream_t s) {
+  const size_t blocks = std::min<size_t>(2048, (n + 255) / 256);
+  hipLaunchKernelGGL(k_check_bf16, dim3((unsigned)std::max<size_t>(1, blocks)), dim3(256), 0,
+                     s, reinterpret_cast<const uint32_t*>(w), n, flag);
   return hipGetLastError();
 }
 
 int dec_packed_rows(int role, int K) {
-  const int K4 = (K + 3) / 4 * 4;
   if (role == DEC_CFG_LM && K <= 1024) return lm_rows(K);
-  return K4;
+  return (K + 7) / 8 * 8;  // whole k-octets, for either element type
 }
 
-int dec_gemm_splits(int role, int K) {
+bool dec_bf16_capable(int role, int K, int N) {
   switch (role) {
-    case DEC_CFG_QKV: return role_splits<DEC_CFG_QKV>(K);
-    case DEC_CFG_OUT: return role_splits<DEC_CFG_OUT>(K);
-    case DEC_CFG_UP: return role_splits<DEC_CFG_UP>(K);
-    case DEC_CFG_DOWN: return role_splits<DEC_CFG_DOWN>(K);
+    case DEC_CFG_QKV: return role_bf16<DEC_CFG_QKV>(K, N);
+    case DEC_CFG_OUT: return role_bf16<DEC_CFG_OUT>(K, N);
+    case DEC_CFG_UP: return role_bf16<DEC_CFG_UP>(K, N);
+    case DEC_CFG_DOWN: return role_bf16<DEC_CFG_DOWN>(K, N);
+    default: return !lm_persistent(N, K) && role_bf16<DEC_CFG_LM>(K, N);
+  }
+}
+
+int dec_gemm_splits(int role, int K, int N) {
+  switch (role) {
+    case DEC_CFG_QKV: return role_splits<DEC_CFG_QKV>(K, N);
+    case DEC_CFG_OUT: return role_splits<DEC_CFG_OUT>(K, N);
+    case DEC_CFG_UP: return role_splits<DEC_CFG_UP>(K, N);
+    case DEC_CFG_DOWN: return role_splits<DEC_CFG_DOWN>(K, N);
     default: return 1;
   }
 }

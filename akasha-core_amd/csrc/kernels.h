@@ -140,26 +140,36 @@ struct DecGemmParams {
   const float* xt;  // A operand (k-quad), or nparts k-quad partial tiles
   int nparts;
   const float* w;   // weights packed by launch_pack_tiles (Kp rows per tile)
+  int wbf16;        // w holds bfloat16 k-octet tiles
   int M, N, K, Kp;
   float* y;         // partial tiles or logits
   uint2* amax;      // DEC_LOGITS: [32, parts] (value bits, index)
   const float2* ml;  // PRO_ATTN_MERGE: per split (max, sum) [nparts][K/hd][32]
   int hd;            // PRO_ATTN_MERGE: head_dim
+  int kpass;         // set by the launcher: K passes per block (grid.y chunks)
 };
 
 // Decode weights are read from a copy packed once at upload: 32-column
 // tiles, each [Kp/4][32][4] (element (k, n) of tile t = n / 32 at
 // ((k / 4) * 32 + n % 32) * 4 + k % 4), zero-filled beyond K and N.  A block
 // streams one contiguous region, and a lane's float4 holds four consecutive
-// k of its column: four MFMA B operands in one load.
-hipError_t launch_pack_tiles(const float* w, int K, int N, int Kp, float* out,
+// k of its column: four MFMA B operands in one load.  With bf16 the tiles
+// hold bfloat16 k-octets instead (element (k, n) at ((k / 8) * 32 + n % 32)
+// * 8 + k % 8), for matrices whose values are all bfloat16: half the bytes,
+// the same products.
+hipError_t launch_pack_tiles(const float* w, int K, int N, int Kp, float* out, bool bf16,
                              hipStream_t s);
-// Rows Kp of a role's packed tiles (K, or more for lm_head's padding).
+// *flag |= 1 if any of w[0..n) is not a bfloat16 value (low 16 bits set).
+hipError_t launch_check_bf16(const float* w, size_t n, int* flag, hipStream_t s);
+// Rows Kp of a role's packed tiles (K rounded up to 8, or more for
+// lm_head's padding).
 int dec_packed_rows(int role, int K);
+// Whether a role's GEMM for [K, N] weights runs on bfloat16 tiles.
+bool dec_bf16_capable(int role, int K, int N);
 
 // Number of K chunks (partial tiles) a role's GEMM produces for contraction
 // length K.
-int dec_gemm_splits(int role, int K);
+int dec_gemm_splits(int role, int K, int N);
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s);
 
 // lm_head: logits y[M, N] = xt . w and argmax partials amax[M, parts], where

@@ -429,10 +429,12 @@ extern "C" akh_status akh_sample_rows(akh_backend* be, const float* logits, uint
 // ---------------------------------------------------------------------------
 
 // A weight matrix as the decode kernels read it: packed 32-column tiles of
-// `rows` k (launch_pack_tiles), refreshed whenever the parameter is uploaded.
+// `rows` k (launch_pack_tiles), float or bfloat16, refreshed whenever the
+// parameter is uploaded.
 struct PackedMatrix {
   float* w = nullptr;
-  int K = 0, N = 0, rows = 0;
+  int K = 0, N = 0, rows = 0, role = 0;
+  bool bf16 = false;  // tiles hold bfloat16 (every value of the matrix is one)
 };
 
 struct akh_model {
@@ -441,6 +443,9 @@ struct akh_model {
   std::vector<float*> params;  // ModelWeights::params() order
   std::vector<size_t> counts;
   std::vector<PackedMatrix> packed;  // per parameter; w == nullptr if not a decode matrix
+  int* bf16_flag = nullptr;          // device scratch of the bfloat16 check
+  bool allow_bf16 = true;            // bfloat16 tiles where every value is one
+  uint64_t layout_gen = 0;           // bumped when a packed matrix changes element type
 
   float* embedding() const { return params[0]; }
   float* layer(uint32_t l, int which) const { return params[1 + 6 * l + which]; }
@@ -462,6 +467,7 @@ extern "C" void akh_model_free(akh_model* m) {
     if (p) hipFree(p);
   for (const PackedMatrix& pm : m->packed)
     if (pm.w) hipFree(pm.w);
+  if (m->bf16_flag) hipFree(m->bf16_flag);
   delete m;
 }
 
@@ -507,6 +513,7 @@ extern "C" akh_status akh_model_new(akh_backend* be,
     pm.K = (int)K;
     pm.N = (int)N;
     pm.rows = dec_packed_rows(role, (int)K);
+    pm.role = role;
   };
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     plan(1 + 6 * l + W_QKV, DEC_CFG_QKV, d, 3 * d);
@@ -526,6 +533,15 @@ extern "C" akh_status akh_model_new(akh_backend* be,
     }
     pm.w = static_cast<float*>(p);
   }
+  {
+    void* p = nullptr;
+    akh_status st = akh_tensor_alloc(be, sizeof(int), &p);
+    if (st != AKH_OK) {
+      akh_model_free(m);
+      return st;
+    }
+    m->bf16_flag = static_cast<int*>(p);
+  }
   *out = m;
   return AKH_OK;
 }
@@ -542,18 +558,56 @@ extern "C" akh_status akh_model_param(akh_model* m, uint32_t index,
   return AKH_OK;
 }
 
+namespace {
+
+// Rebuilds the packed decode copy of parameter `index` from its rows: in
+// bfloat16 when the role's kernel supports it and every value is a
+// bfloat16, else in float.
+akh_status repack(akh_model* m, uint32_t index) {
+  PackedMatrix& pm = m->packed[index];
+  if (!pm.w) return AKH_OK;
+  hipStream_t st = m->be->stream;
+  bool bf16 = false;
+  if (m->allow_bf16 && dec_bf16_capable(pm.role, pm.K, pm.N)) {
+    int flag = 0;
+    HIP_TRY(hipMemcpyAsync(m->bf16_flag, &flag, sizeof(int), hipMemcpyHostToDevice, st));
+    HIP_TRY(launch_check_bf16(m->params[index], (size_t)pm.K * pm.N, m->bf16_flag, st));
+    HIP_TRY(hipMemcpyAsync(&flag, m->bf16_flag, sizeof(int), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    bf16 = flag == 0;
+  }
+  HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, bf16, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (bf16 != pm.bf16) {
+    pm.bf16 = bf16;
+    ++m->layout_gen;  // captured decode graphs chose kernels by element type
+  }
+  return AKH_OK;
+}
+
+}  // namespace
+
+extern "C" akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16) {
+  CHECK_ARG(m && (allow == 0 || allow == 1), "akh_model_set_bf16_tiles: bad argument");
+  CHECK_ARG(!m->be->capturing, "akh_model_set_bf16_tiles: graph capture in progress");
+  m->allow_bf16 = allow != 0;
+  uint32_t n = 0;
+  for (uint32_t i = 0; i < m->packed.size(); ++i) {
+    akh_status st = repack(m, i);
+    if (st != AKH_OK) return st;
+    n += m->packed[i].bf16 ? 1u : 0u;
+  }
+  if (n_bf16) *n_bf16 = n;
+  return AKH_OK;
+}
+
 extern "C" akh_status akh_model_upload_param(akh_model* m, uint32_t index,
                                              const float* host, size_t count) {
   CHECK_ARG(m && index < m->params.size(), "akh_model_upload_param: bad index");
   CHECK_ARG(count == m->counts[index], "akh_model_upload_param: size mismatch");
   akh_status st = akh_tensor_upload(m->be, m->params[index], host, count * sizeof(float));
   if (st != AKH_OK) return st;
-  const PackedMatrix& pm = m->packed[index];
-  if (pm.w) {
-    HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, m->be->stream));
-    HIP_TRY(hipStreamSynchronize(m->be->stream));
-  }
-  return AKH_OK;
+  return repack(m, index);
 }
 
 // ---------------------------------------------------------------------------
@@ -694,6 +748,7 @@ struct akh_session {
 
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
+  uint64_t glayout = 0;  // model layout_gen the graphs were captured for
 
   // Prefill buffers, grown on demand to B * prompt_len rows.
   size_t prows = 0;
@@ -775,6 +830,12 @@ DecGemmParams dec_base(akh_session* s) {
   return p;
 }
 
+void use_packed(DecGemmParams& p, const PackedMatrix& pm) {
+  p.w = pm.w;
+  p.Kp = pm.rows;
+  p.wbf16 = pm.bf16 ? 1 : 0;
+}
+
 RowsNormParams norm_base(akh_session* s, const float* gain) {
   RowsNormParams r{};
   r.xt = s->xt;
@@ -791,8 +852,7 @@ hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->xnt;
-  p.w = s->m->packed_layer(l, W_QKV).w;
-  p.Kp = s->m->packed_layer(l, W_QKV).rows;
+  use_packed(p, s->m->packed_layer(l, W_QKV));
   p.y = s->p_qkv;
   p.N = 3 * c.dim;
   p.K = c.dim;
@@ -829,8 +889,7 @@ hipError_t enqueue_out(akh_session* s, uint32_t l) {
   p.nparts = dec_attn_splits();
   p.ml = s->attn_ml;
   p.hd = (int)(c.dim / c.num_heads);
-  p.w = s->m->packed_layer(l, W_OUT).w;
-  p.Kp = s->m->packed_layer(l, W_OUT).rows;
+  use_packed(p, s->m->packed_layer(l, W_OUT));
   p.y = s->p_out;
   p.N = c.dim;
   p.K = c.dim;
@@ -851,8 +910,7 @@ hipError_t enqueue_up(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->xnt;
-  p.w = s->m->packed_layer(l, W_UP).w;
-  p.Kp = s->m->packed_layer(l, W_UP).rows;
+  use_packed(p, s->m->packed_layer(l, W_UP));
   p.y = s->p_up;
   p.N = c.ffn_hidden;
   p.K = c.dim;
@@ -865,8 +923,7 @@ hipError_t enqueue_down(akh_session* s, uint32_t l) {
   DecGemmParams p = dec_base(s);
   p.xt = s->p_up;
   p.nparts = s->ks_up;
-  p.w = s->m->packed_layer(l, W_DOWN).w;
-  p.Kp = s->m->packed_layer(l, W_DOWN).rows;
+  use_packed(p, s->m->packed_layer(l, W_DOWN));
   p.y = s->p_down;
   p.N = c.dim;
   p.K = c.ffn_hidden;
@@ -879,8 +936,7 @@ hipError_t enqueue_lm_head(akh_session* s) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->xnt;
-  p.w = s->m->packed_lm_head().w;
-  p.Kp = s->m->packed_lm_head().rows;
+  use_packed(p, s->m->packed_lm_head());
   p.y = s->logits;
   p.amax = s->amax;
   p.N = c.vocab_size;
@@ -991,7 +1047,23 @@ akh_status set_active(akh_session* s, bool all_rows) {
   return AKH_OK;
 }
 
+// Captured graphs hold the kernels chosen for the packed weights' element
+// types: drop them when an upload changed one.
+void drop_stale_graphs(akh_session* s) {
+  if (s->glayout == s->m->layout_gen) return;
+  if (s->gexec) hipGraphExecDestroy(s->gexec);
+  if (s->graph) hipGraphDestroy(s->graph);
+  if (s->ggexec) hipGraphExecDestroy(s->ggexec);
+  if (s->ggraph) hipGraphDestroy(s->ggraph);
+  s->gexec = nullptr;
+  s->graph = nullptr;
+  s->ggexec = nullptr;
+  s->ggraph = nullptr;
+  s->glayout = s->m->layout_gen;
+}
+
 akh_status ensure_decode_graph(akh_session* s) {
+  drop_stale_graphs(s);
   if (s->gexec) return AKH_OK;
   return capture(s, enqueue_decode, &s->graph, &s->gexec, "decode graph");
 }
@@ -1053,10 +1125,10 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   s->B = batch;
   s->cur_len.assign(batch, 0);
   s->has_cache.assign(batch, 1);
-  s->ks_qkv = dec_gemm_splits(DEC_CFG_QKV, c.dim);
-  s->ks_out = dec_gemm_splits(DEC_CFG_OUT, c.dim);
-  s->ks_up = dec_gemm_splits(DEC_CFG_UP, c.dim);
-  s->ks_down = dec_gemm_splits(DEC_CFG_DOWN, c.ffn_hidden);
+  s->ks_qkv = dec_gemm_splits(DEC_CFG_QKV, c.dim, 3 * c.dim);
+  s->ks_out = dec_gemm_splits(DEC_CFG_OUT, c.dim, c.dim);
+  s->ks_up = dec_gemm_splits(DEC_CFG_UP, c.dim, c.ffn_hidden);
+  s->ks_down = dec_gemm_splits(DEC_CFG_DOWN, c.ffn_hidden, c.dim);
 
   const size_t d = c.dim, V = c.vocab_size, F = c.ffn_hidden, R = kMaxBatch;
   hipError_t e = hipSetDevice(s->be->device);
@@ -1317,6 +1389,7 @@ namespace {
 
 // Buffers and graph of generate rounds for `max_new` tokens with `params`.
 akh_status ensure_generate(akh_session* s, uint32_t max_new, const akh_sampling& params) {
+  drop_stale_graphs(s);
   if (max_new > s->gcap) {
     if (s->ggexec) hipGraphExecDestroy(s->ggexec);
     if (s->ggraph) hipGraphDestroy(s->ggraph);

@@ -187,6 +187,7 @@ _SIGS = {
     "akh_model_num_params": (U32, [P]),
     "akh_model_param": (ST, [P, U32, C.POINTER(P), C.POINTER(C.c_size_t)]),
     "akh_model_upload_param": (ST, [P, U32, P, C.c_size_t]),
+    "akh_model_set_bf16_tiles": (ST, [P, C.c_int, P]),
     "akh_checkpoint_info": (ST, [C.c_char_p, C.POINTER(CheckpointInfo)]),
     "akh_model_load_checkpoint": (ST, [P, C.c_char_p, C.POINTER(C.c_uint64),
                                        C.POINTER(C.c_int)]),
@@ -483,6 +484,14 @@ class Model:
         for i, a in enumerate(params):
             a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
             _check(_lib.akh_model_upload_param(self.handle, i, _ptr(a), a.size), f"param {i}")
+
+    def set_bf16_tiles(self, allow: bool) -> int:
+        """Allow or forbid bfloat16 decode tiles (re-tiles every matrix);
+        returns how many matrices are tiled in bfloat16."""
+        n = U32()
+        _check(_lib.akh_model_set_bf16_tiles(self.handle, 1 if allow else 0, C.byref(n)),
+               "set_bf16_tiles")
+        return n.value
 
     def download_param(self, index: int) -> np.ndarray:
         """Host copy of parameter ``index`` (reference layout)."""

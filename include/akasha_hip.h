@@ -217,9 +217,17 @@ uint32_t akh_model_num_params(const akh_model* m);
 akh_status akh_model_param(akh_model* m, uint32_t index, float** dev,
                            size_t* count);
 /* Copy `count` floats from host into parameter `index` (count must match),
- * and refresh the decode path's tiled copy of a weight matrix. */
+ * and refresh the decode path's tiled copy of a weight matrix.  A matrix
+ * whose every value is a bfloat16 (low 16 mantissa bits zero, e.g. weights
+ * trained or stored in bf16) is tiled in bfloat16: half the bytes per
+ * decode step, the same products and results. */
 akh_status akh_model_upload_param(akh_model* m, uint32_t index,
                                   const float* host, size_t count);
+/* No reference counterpart (the reference keeps f32 device weights): allow
+ * (1, the default) or forbid (0) bfloat16 tiles, re-tiling every decode
+ * matrix now; `n_bf16` (optional) receives how many matrices are tiled in
+ * bfloat16 afterwards. */
+akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16);
 
 /* ---- checkpoints: src/nn/checkpoint.rs (format V3) ---------------------- */
 

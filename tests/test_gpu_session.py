@@ -251,6 +251,47 @@ def test_head_dim_128_prefill_matches_oracle(backend, pkg, ora):
         o.close()
 
 
+def test_bf16_tiles_are_exact(backend, pkg, ora):
+    # Weights whose values are all bfloat16 are tiled in bfloat16 for decode:
+    # qkv, up and down of each layer and, with dim > 1024, the lm_head (out
+    # keeps float tiles).  The products are the same, so the logits must be
+    # bit-identical to float tiles of the same values.  Toggling the tiles
+    # after a decode graph was captured also checks that the graph is rebuilt.
+    cfg = pkg.ModelConfig.new(500, 1152, 9, 2, 40)
+    w = pkg.synthetic_weights(cfg, seed=41, bf16=True)
+    model, s = _session(pkg, backend, cfg, w, 40, 3)
+    assert model.set_bf16_tiles(True) == 3 * cfg.num_layers + 1
+    toks = pkg.synthetic_tokens(3 * 12, cfg.vocab_size, seed=42).reshape(3, 12)
+    logits, nxt = s.prefill(toks)
+    runs = {}
+    for allow in (True, False, True):
+        assert model.set_bf16_tiles(allow) == (3 * cfg.num_layers + 1 if allow else 0)
+        s.truncate(12)
+        feed, out = nxt, []
+        for _ in range(4):
+            lg, feed = s.decode_step(feed)
+            out.append((lg.copy(), feed.copy()))
+        if allow in runs:
+            for (a, ta), (b, tb) in zip(runs[allow], out):
+                assert np.array_equal(a, b) and np.array_equal(ta, tb)
+        runs[allow] = out
+    for (a, ta), (b, tb) in zip(runs[True], runs[False]):
+        assert np.array_equal(a, b) and np.array_equal(ta, tb)
+    o = ora.OracleSession(cfg, w, 40)
+    ref = o.prefill(toks[1])
+    assert np.abs(logits[1] - ref).max() < TOL
+    for lg, _ in runs[True]:
+        ref = o.decode_step(ora.argmax(ref))
+        assert np.abs(lg[1] - ref).max() < TOL
+    o.close()
+    # A matrix with one value off the bfloat16 grid goes back to float tiles.
+    w2 = list(w)
+    w2[2] = w[2].copy()
+    w2[2].flat[7] = np.nextafter(w2[2].flat[7], np.float32(1))
+    model.upload(w2)
+    assert model.set_bf16_tiles(True) == 3 * cfg.num_layers
+
+
 def test_take_and_replace_cache_move_a_sequence(backend, pkg, ora):
     # take_cache / replace_cache (inference.rs:42-59) and NoCache (:72, :180).
     hip = pkg.hip
