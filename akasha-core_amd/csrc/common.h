@@ -16,6 +16,28 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// bfloat16 operands of v_mfma_f32_32x32x16_bf16: lane l supplies
+// A[l % 32][8 * (l / 32) + i] and B[8 * (l / 32) + i][l % 32], i = 0..7; the
+// accumulator layout is mfma32's.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// float -> bfloat16 bits, round to nearest even.
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return bf16_bits(lo) | (bf16_bits(hi) << 16);
+}
+__device__ __forceinline__ bf16x8 bf16x8_of(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x8 bf16x8_of(float4 a, float4 b) {
+  return bf16x8_of(make_uint4(pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w),
+                              pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)));
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll

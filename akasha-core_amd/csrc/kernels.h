@@ -83,6 +83,10 @@ struct GemmParams {
   int S;
   const float2* rope;  // [max_ctx, head_dim / 2] (cos, sin)
   int dim, head_dim;
+  // bfloat16 path (launch_gemm_bf16): the transposed weights in bfloat16
+  // and A either in bfloat16 (a16) or fp32 (a, split into hi + lo parts).
+  const uint16_t* a16;   // [M, K]
+  const uint16_t* bt16;  // [N, K]
 };
 
 struct FlashParams {
@@ -96,6 +100,7 @@ struct FlashParams {
   float scale;
   const akh_flash_attn_meta* meta;  // per-shader path: S, dim, scale and
                                     // row_offset come from it (1 sequence)
+  uint16_t* o16;  // launch_flash_bf16: bfloat16 output (o unused)
 };
 
 hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s);
@@ -103,6 +108,17 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
                         hipStream_t s);
 hipError_t launch_rows_rmsnorm(const float* x, const float* w, float* out,
                                int rows, int size, float eps, hipStream_t s);
+
+// The optional bfloat16-MFMA prefill: bfloat16 MFMA operands (round to
+// nearest even), fp32 accumulation, fp32 residual stream and KV cache.
+// Weights are read from a transposed bfloat16 copy [N, K]; A is p.a16
+// (bfloat16) or p.a (fp32, entering as hi + lo bfloat16 parts).  K % 8 == 0.
+hipError_t launch_gemm_bf16(const GemmParams& p, int epi, hipStream_t s);
+// wt[n, k] = bf16(w[k, n]) for a [K, N] row-major matrix.
+hipError_t launch_transpose_bf16(const float* w, int K, int N, uint16_t* wt, hipStream_t s);
+// Causal flash attention (head_dim 64 or 128) with bfloat16 QK^T and PV
+// MFMAs; writes p.o16.
+hipError_t launch_flash_bf16(const FlashParams& p, int batch, int max_rows, hipStream_t s);
 hipError_t launch_embedding_rows(const uint32_t* tokens, const float* table,
                                  float* out, int rows, int d, uint32_t vocab,
                                  hipStream_t s);

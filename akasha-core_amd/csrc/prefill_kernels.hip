@@ -401,6 +401,300 @@ __global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// bfloat16-MFMA prefill
+
+// wt[n, k] = bf16(w[k, n]) through a 32x32 LDS tile.
+__global__ __launch_bounds__(256) void k_transpose_bf16(const float* __restrict__ w, int K,
+                                                        int N, uint16_t* __restrict__ wt) {
+  __shared__ float t[32][33];
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int c = threadIdx.x & 31, r = threadIdx.x >> 5;
+  for (int i = r; i < 32; i += 8) {
+    const int k = k0 + i, n = n0 + c;
+    t[i][c] = (k < K && n < N) ? w[(size_t)k * N + n] : 0.f;
+  }
+  __syncthreads();
+  for (int i = r; i < 32; i += 8) {
+    const int n = n0 + i, k = k0 + c;
+    if (n < N && k < K) wt[(size_t)n * K + k] = (uint16_t)bf16_bits(t[c][i]);
+  }
+}
+
+// C[M,N] = A[M,K] B[K,N] with bfloat16 A [M, K] and B^T [N, K], fp32
+// accumulation on v_mfma_f32_32x32x16_bf16.  Block tile 256x256, BK = 32,
+// 8 waves as 2 (rows) x 4 (columns), each wave 128x64 as 4x2 MFMA tiles.
+// Tiles are staged in LDS k-contiguous (rows padded to 80 bytes, so the
+// 16-byte fragment reads of 16 consecutive rows hit distinct banks), double
+// buffered with the next tile's global loads issued before the MFMAs.  B
+// rows are stored permuted so lane j of column tile t reads the row of
+// column 2j + t: each lane ends up with adjacent column pairs, as the
+// paired epilogues (RoPE) need.
+//
+// A32: A is fp32 (p.a) and enters as two bfloat16 parts, hi = bf16(a) and
+// lo = bf16(a - hi), each multiplied by B (two MFMAs): with bfloat16-exact
+// weights the products then carry a's first 16 significant bits.
+template <int EPI, bool A32>
+__global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
+  constexpr int BM = 256, BN = 256, BK = 32, LD = BK + 8;
+  constexpr int NA = A32 ? 2 : 1;
+  __shared__ __align__(16) uint16_t As[NA][2][BM][LD];
+  __shared__ __align__(16) uint16_t Bs[2][BN][LD];
+
+  const int M = p.M, N = p.N, K = p.K;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int j = lane & 31, h = lane >> 5;
+
+  // Global -> register staging: rows tid / 4 and tid / 4 + 128, eight k at
+  // (tid % 4) * 8, of both A and B^T.
+  const int sr = tid >> 2, sk = (tid & 3) * 8;
+  uint4 ra[2], rb[2];
+  float4 fa[2][2];  // A32 staging
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = sr + 128 * i, k = k0 + sk;
+      const int gm = m0 + r, gn = n0 + r;
+      if (A32) {
+        const bool in = gm < M && k < K;
+        const float* src = p.a + (size_t)gm * K + k;
+        fa[i][0] = in ? *reinterpret_cast<const float4*>(src)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        fa[i][1] = in ? *reinterpret_cast<const float4*>(src + 4)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        ra[i] = (gm < M && k < K) ? *reinterpret_cast<const uint4*>(p.a16 + (size_t)gm * K + k)
+                                  : make_uint4(0u, 0u, 0u, 0u);
+      }
+      rb[i] = (gn < N && k < K) ? *reinterpret_cast<const uint4*>(p.bt16 + (size_t)gn * K + k)
+                                : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = sr + 128 * i;
+      // Column c = 64 g + 2 jj + t of the block lives at LDS row 64 g + 32 t + jj.
+      const int br = (r & ~63) | ((r & 1) << 5) | ((r & 63) >> 1);
+      if (A32) {
+        const float4 x0 = fa[i][0], x1 = fa[i][1];
+        const uint4 hi = make_uint4(pack_bf16x2(x0.x, x0.y), pack_bf16x2(x0.z, x0.w),
+                                    pack_bf16x2(x1.x, x1.y), pack_bf16x2(x1.z, x1.w));
+        const float4 h0 = make_float4(__uint_as_float(hi.x << 16), __uint_as_float(hi.x & 0xFFFF0000u),
+                                      __uint_as_float(hi.y << 16), __uint_as_float(hi.y & 0xFFFF0000u));
+        const float4 h1 = make_float4(__uint_as_float(hi.z << 16), __uint_as_float(hi.z & 0xFFFF0000u),
+                                      __uint_as_float(hi.w << 16), __uint_as_float(hi.w & 0xFFFF0000u));
+        const uint4 lo = make_uint4(pack_bf16x2(x0.x - h0.x, x0.y - h0.y),
+                                    pack_bf16x2(x0.z - h0.z, x0.w - h0.w),
+                                    pack_bf16x2(x1.x - h1.x, x1.y - h1.y),
+                                    pack_bf16x2(x1.z - h1.z, x1.w - h1.w));
+        *reinterpret_cast<uint4*>(&As[0][buf][r][sk]) = hi;
+        *reinterpret_cast<uint4*>(&As[NA - 1][buf][r][sk]) = lo;
+      } else {
+        *reinterpret_cast<uint4*>(&As[0][buf][r][sk]) = ra[i];
+      }
+      *reinterpret_cast<uint4*>(&Bs[buf][br][sk]) = rb[i];
+    }
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[a][t] = zero16();
+
+  const int nk = (K + BK - 1) / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8 bfr[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        bfr[t] = bf16x8_of(*reinterpret_cast<const uint4*>(
+            &Bs[buf][wn * 64 + t * 32 + j][ks * 16 + 8 * h]));
+#pragma unroll
+      for (int part = 0; part < NA; ++part) {
+        bf16x8 af[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+          af[a] = bf16x8_of(*reinterpret_cast<const uint4*>(
+              &As[part][buf][wm * 128 + a * 32 + j][ks * 16 + 8 * h]));
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[a], bfr[t], acc[a][t]);
+      }
+    }
+    if (kt + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * 128 + a * 32 + acc_row(r, h);
+      const int n = n0 + wn * 64 + 2 * j;
+      epi_pair_gemm<EPI>(p, M, N, m, n, acc[a][0][r], acc[a][1][r]);
+    }
+}
+
+// Causal flash attention with bfloat16 MFMAs (head_dim 64 or 128), the
+// structure of k_flash_mfma: block = 4 waves x 32 queries, keys in blocks of
+// 32, S^T = K Q^T per wave so each lane owns one query.  Q, K and V are
+// rounded to bfloat16 (Q once into registers, K row-major and V transposed
+// into LDS per key block); P^T feeds O^T += V^T P^T from the accumulator
+// registers: MFMA 0 of a 32-key block takes accumulator entries 0..7 of each
+// lane (keys acc_row(0..7, h)), MFMA 1 entries 8..15, and the V^T fragment
+// reads the same keys, two runs of four.  Softmax statistics are fp32; the
+// output is bfloat16.
+template <int HD>
+__global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
+  constexpr int QB = 128, KB = 32, NT = HD / 32, NQ = HD / 16;
+  constexpr int KP = HD + 8;   // K row stride (bf16)
+  constexpr int VP = KB + 8;   // V^T row stride (bf16)
+  constexpr int CPR = HD / 4;  // float4 per K/V row
+  constexpr int RPP = 256 / CPR;
+  constexpr int NP = KB / RPP;
+  constexpr int KV_BYTES = (KB * KP + HD * VP) * 2;
+  constexpr int O_BYTES = 4 * 32 * 33 * 4;
+  __shared__ __align__(16) unsigned char lds[KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES];
+  uint16_t (*Ks)[KP] = reinterpret_cast<uint16_t (*)[KP]>(lds);
+  uint16_t (*Vt)[VP] = reinterpret_cast<uint16_t (*)[VP]>(lds + KB * KP * 2);
+
+  const int S = p.S, d = p.d;
+  const float scale = p.scale;
+  const int qblk = gridDim.x - 1 - blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int q0 = qblk * QB;
+  if (q0 >= S) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+
+  const float* qp = p.q + (size_t)b * p.q_bs + hh * HD;
+  const float* kp = p.k + (size_t)b * p.kv_bs + hh * HD;
+  const float* vp = p.v + (size_t)b * p.kv_bs + hh * HD;
+
+  const int qi = q0 + wave * 32 + j;
+  bf16x8 qf[NQ];  // dims 16 s + 8 h .. + 7 of query qi
+  {
+    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 8 * h;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s)
+      qf[s] = bf16x8_of(*reinterpret_cast<const float4*>(qr + 16 * s),
+                        *reinterpret_cast<const float4*>(qr + 16 * s + 4));
+  }
+  f32x16 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = zero16();
+  float mrow = -INFINITY, lrow = 0.f;
+
+  const int wave_qmax = q0 + wave * 32 + 31;
+  const int kend = min(S, q0 + QB);
+  const int nkb = (kend + KB - 1) / KB;
+
+  const int lr = tid / CPR, lc = (tid % CPR) * 4;
+  float4 kr[NP], vr[NP];
+  auto load_kv = [&](int kb) {
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int key = kb * KB + lr + RPP * q;
+      const size_t off = (size_t)(key < S ? key : 0) * d + lc;
+      kr[q] = *reinterpret_cast<const float4*>(kp + off);
+      vr[q] = *reinterpret_cast<const float4*>(vp + off);
+    }
+  };
+  load_kv(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int r = lr + RPP * q;
+      *reinterpret_cast<uint2*>(&Ks[r][lc]) =
+          make_uint2(pack_bf16x2(kr[q].x, kr[q].y), pack_bf16x2(kr[q].z, kr[q].w));
+      Vt[lc][r] = (uint16_t)bf16_bits(vr[q].x);
+      Vt[lc + 1][r] = (uint16_t)bf16_bits(vr[q].y);
+      Vt[lc + 2][r] = (uint16_t)bf16_bits(vr[q].z);
+      Vt[lc + 3][r] = (uint16_t)bf16_bits(vr[q].w);
+    }
+    __syncthreads();
+    load_kv(kb + 1);  // rows past S read row 0: harmless, never used
+    const int j0 = kb * KB;
+    if (j0 > wave_qmax) continue;
+
+    f32x16 st = zero16();
+#pragma unroll
+    for (int s = 0; s < NQ; ++s)
+      st = mfma_bf16(bf16x8_of(*reinterpret_cast<const uint4*>(&Ks[j][16 * s + 8 * h])), qf[s],
+                     st);
+
+    float pm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = j0 + acc_row(r, h);
+      float v = st[r] * scale;
+      if (key > qi || key >= S) v = -INFINITY;
+      st[r] = v;
+      pm = fmaxf(pm, v);
+    }
+    pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+    const float mnew = fmaxf(mrow, pm);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = st[r] == -INFINITY ? 0.f : expf(st[r] - mnew);
+      st[r] = e;
+      ps += e;
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    const float corr = mrow == -INFINITY ? 0.f : expf(mrow - mnew);
+    lrow = lrow * corr + ps;
+    mrow = mnew;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    const bf16x8 p0 = bf16x8_of(make_float4(st[0], st[1], st[2], st[3]),
+                                make_float4(st[4], st[5], st[6], st[7]));
+    const bf16x8 p1 = bf16x8_of(make_float4(st[8], st[9], st[10], st[11]),
+                                make_float4(st[12], st[13], st[14], st[15]));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const uint16_t* vrow = Vt[32 * t + j];
+      const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
+      const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
+      const uint2 a2 = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * h);
+      const uint2 a3 = *reinterpret_cast<const uint2*>(vrow + 24 + 4 * h);
+      o[t] = mfma_bf16(bf16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y)), p0, o[t]);
+      o[t] = mfma_bf16(bf16x8_of(make_uint4(a2.x, a2.y, a3.x, a3.y)), p1, o[t]);
+    }
+  }
+
+  const float inv = 1.0f / lrow;
+  float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33 * 4);
+  uint16_t* op = p.o16 + (size_t)b * p.o_bs + hh * HD;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Os[j][acc_row(r, h)] = o[t][r] * inv;
+    __syncthreads();
+    for (int e = lane; e < 32 * 16; e += 64) {
+      const int r = e >> 4, c = (e & 15) * 2;
+      const int qrow = q0 + wave * 32 + r;
+      if (qrow < S)
+        *reinterpret_cast<uint32_t*>(op + (size_t)qrow * d + 32 * t + c) =
+            pack_bf16x2(Os[r][c], Os[r][c + 1]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 
 hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
   dim3 g((p.N + 127) / 128, (p.M + 127) / 128), b(256);
@@ -434,6 +728,44 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
     case 32: hipLaunchKernelGGL(k_flash_generic<32>, g, b, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_bf16(const GemmParams& p, int epi, hipStream_t s) {
+  if (p.K % 8 != 0 || p.M <= 0 || p.N <= 0 || p.K <= 0) return hipErrorInvalidValue;
+  if (!p.a == !p.a16) return hipErrorInvalidValue;
+  dim3 g((p.N + 255) / 256, (p.M + 255) / 256), b(512);
+#define AKH_GO(E)                                                 \
+  if (p.a)                                                        \
+    hipLaunchKernelGGL((k_gemm_bf16<E, true>), g, b, 0, s, p);    \
+  else                                                            \
+    hipLaunchKernelGGL((k_gemm_bf16<E, false>), g, b, 0, s, p);
+  switch (epi) {
+    case GEMM_ADD: AKH_GO(GEMM_ADD) break;
+    case GEMM_SILU: AKH_GO(GEMM_SILU) break;
+    case GEMM_QKV: AKH_GO(GEMM_QKV) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef AKH_GO
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_bf16(const float* w, int K, int N, uint16_t* wt, hipStream_t s) {
+  if (K <= 0 || N <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_transpose_bf16, dim3((N + 31) / 32, (K + 31) / 32), dim3(256), 0, s, w,
+                     K, N, wt);
+  return hipGetLastError();
+}
+
+hipError_t launch_flash_bf16(const FlashParams& p, int batch, int max_rows, hipStream_t s) {
+  if (p.meta || !p.o16) return hipErrorInvalidValue;
+  const dim3 g((max_rows + 127) / 128, p.d / p.hd, batch);
+  if (p.hd == 64)
+    hipLaunchKernelGGL(k_flash_bf16<64>, g, dim3(256), 0, s, p);
+  else if (p.hd == 128)
+    hipLaunchKernelGGL(k_flash_bf16<128>, g, dim3(256), 0, s, p);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

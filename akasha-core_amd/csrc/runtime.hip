@@ -445,6 +445,8 @@ struct akh_model {
   std::vector<PackedMatrix> packed;  // per parameter; w == nullptr if not a decode matrix
   int* bf16_flag = nullptr;          // device scratch of the bfloat16 check
   bool allow_bf16 = true;            // bfloat16 tiles where every value is one
+  bool prefill_bf16 = false;         // the optional bfloat16-MFMA prefill
+  std::vector<uint16_t*> wt16;       // per parameter: bf16 [N, K] copy (layer matrices)
   uint64_t layout_gen = 0;           // bumped when a packed matrix changes element type
 
   float* embedding() const { return params[0]; }
@@ -468,6 +470,8 @@ extern "C" void akh_model_free(akh_model* m) {
   for (const PackedMatrix& pm : m->packed)
     if (pm.w) hipFree(pm.w);
   if (m->bf16_flag) hipFree(m->bf16_flag);
+  for (uint16_t* p : m->wt16)
+    if (p) hipFree(p);
   delete m;
 }
 
@@ -577,6 +581,8 @@ akh_status repack(akh_model* m, uint32_t index) {
     bf16 = flag == 0;
   }
   HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, bf16, st));
+  if (index < m->wt16.size() && m->wt16[index])
+    HIP_TRY(launch_transpose_bf16(m->params[index], pm.K, pm.N, m->wt16[index], st));
   HIP_TRY(hipStreamSynchronize(st));
   if (bf16 != pm.bf16) {
     pm.bf16 = bf16;
@@ -586,6 +592,39 @@ akh_status repack(akh_model* m, uint32_t index) {
 }
 
 }  // namespace
+
+extern "C" akh_status akh_model_set_prefill_bf16(akh_model* m, int enable) {
+  CHECK_ARG(m && (enable == 0 || enable == 1), "akh_model_set_prefill_bf16: bad argument");
+  CHECK_ARG(!m->be->capturing, "akh_model_set_prefill_bf16: graph capture in progress");
+  const akh_model_config& c = m->cfg;
+  const uint32_t hd = c.dim / c.num_heads;
+  CHECK_ARG(!enable || ((hd == 64 || hd == 128) && c.dim % 8 == 0 && c.ffn_hidden % 8 == 0),
+            "akh_model_set_prefill_bf16: needs head_dim 64 or 128 and dim, ffn_hidden "
+            "multiples of 8");
+  HIP_TRY(hipSetDevice(m->be->device));
+  HIP_TRY(hipStreamSynchronize(m->be->stream));
+  for (uint16_t*& p : m->wt16)
+    if (p) {
+      HIP_TRY(hipFree(p));
+      p = nullptr;
+    }
+  m->prefill_bf16 = false;
+  if (!enable) return AKH_OK;
+  m->wt16.assign(m->params.size(), nullptr);
+  for (uint32_t l = 0; l < c.num_layers; ++l)
+    for (int which : {W_QKV, W_OUT, W_UP, W_DOWN}) {
+      const uint32_t i = 1 + 6 * l + which;
+      const PackedMatrix& pm = m->packed[i];
+      void* p = nullptr;
+      akh_status st = akh_tensor_alloc(m->be, (size_t)pm.K * pm.N * sizeof(uint16_t), &p);
+      if (st != AKH_OK) return st;
+      m->wt16[i] = static_cast<uint16_t*>(p);
+      HIP_TRY(launch_transpose_bf16(m->params[i], pm.K, pm.N, m->wt16[i], m->be->stream));
+    }
+  HIP_TRY(hipStreamSynchronize(m->be->stream));
+  m->prefill_bf16 = true;
+  return AKH_OK;
+}
 
 extern "C" akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16) {
   CHECK_ARG(m && (allow == 0 || allow == 1), "akh_model_set_bf16_tiles: bad argument");
@@ -1216,6 +1255,169 @@ extern "C" akh_status akh_session_truncate(akh_session* s, uint32_t len) {
   return upload_positions(s);
 }
 
+namespace {
+
+// The prefill layers in fp32 (build_prefill_layer's node order).
+hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
+  const akh_model_config& c = s->m->cfg;
+  const uint32_t d = c.dim, hd = d / c.num_heads;
+  const size_t rows = (size_t)s->B * S;
+  hipStream_t st = s->be->stream;
+#define TRY_HIP(x)                      \
+  do {                                  \
+    const hipError_t e_ = (x);          \
+    if (e_ != hipSuccess) return e_;    \
+  } while (0)
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    TRY_HIP(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM1), s->pxn,
+                                (int)rows, (int)d, c.norm_eps, st));
+    GemmParams g{};
+    g.a = s->pxn;
+    g.b = s->m->layer(l, W_QKV);
+    g.M = (int)rows;
+    g.N = 3 * d;
+    g.K = d;
+    g.q_out = s->pq;
+    g.kcache = s->kcache(l);
+    g.vcache = s->vcache(l);
+    g.seq_stride = s->seq_stride();
+    g.S = (int)S;
+    g.rope = s->rope;
+    g.dim = d;
+    g.head_dim = hd;
+    TRY_HIP(launch_gemm(g, GEMM_QKV, st));
+
+    FlashParams f{};
+    f.q = s->pq;
+    f.k = s->kcache(l);
+    f.v = s->vcache(l);
+    f.o = s->pattn;
+    f.q_bs = (long)S * d;
+    f.kv_bs = s->seq_stride();
+    f.o_bs = (long)S * d;
+    f.S = (int)S;
+    f.d = (int)d;
+    f.hd = (int)hd;
+    f.scale = 1.0f / sqrtf((float)hd);
+    TRY_HIP(launch_flash(f, (int)s->B, (int)S, st));
+
+    GemmParams o{};
+    o.a = s->pattn;
+    o.b = s->m->layer(l, W_OUT);
+    o.c = s->px;
+    o.M = (int)rows;
+    o.N = d;
+    o.K = d;
+    TRY_HIP(launch_gemm(o, GEMM_ADD, st));
+
+    TRY_HIP(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM2), s->pxn,
+                                (int)rows, (int)d, c.norm_eps, st));
+    GemmParams u{};
+    u.a = s->pxn;
+    u.b = s->m->layer(l, W_UP);
+    u.c = s->pffn;
+    u.M = (int)rows;
+    u.N = c.ffn_hidden;
+    u.K = d;
+    TRY_HIP(launch_gemm(u, GEMM_SILU, st));
+
+    GemmParams w{};
+    w.a = s->pffn;
+    w.b = s->m->layer(l, W_DOWN);
+    w.c = s->px;
+    w.M = (int)rows;
+    w.N = d;
+    w.K = c.ffn_hidden;
+    TRY_HIP(launch_gemm(w, GEMM_ADD, st));
+  }
+#undef TRY_HIP
+  return hipSuccess;
+}
+
+// The prefill layers on the bfloat16 MFMAs (akh_model_set_prefill_bf16),
+// in build_prefill_layer's node order.  Weights come from the model's
+// transposed bfloat16 copies.  The QKV, ffn_up and ffn_down GEMMs take their
+// fp32 A operand (normed rows, SiLU output) as bfloat16 hi + lo parts, two
+// MFMAs per product: with bfloat16 weights those GEMMs are then accurate to
+// about 2^-16.  Flash attention runs on bfloat16 Q, K, V and P and writes
+// a bfloat16 output, which out_proj takes as is.  The residual stream px
+// and the KV cache stay fp32.
+hipError_t prefill_layers_bf16(akh_session* s, uint32_t S) {
+  const akh_model_config& c = s->m->cfg;
+  const uint32_t d = c.dim, hd = d / c.num_heads;
+  const size_t rows = (size_t)s->B * S;
+  hipStream_t st = s->be->stream;
+  uint16_t* attn16 = reinterpret_cast<uint16_t*>(s->pattn);
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    const uint32_t base = 1 + 6 * l;
+    hipError_t e = launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM1), s->pxn, (int)rows,
+                                       (int)d, c.norm_eps, st);
+    if (e != hipSuccess) return e;
+    GemmParams g{};
+    g.a = s->pxn;
+    g.bt16 = s->m->wt16[base + W_QKV];
+    g.M = (int)rows;
+    g.N = 3 * d;
+    g.K = d;
+    g.q_out = s->pq;
+    g.kcache = s->kcache(l);
+    g.vcache = s->vcache(l);
+    g.seq_stride = s->seq_stride();
+    g.S = (int)S;
+    g.rope = s->rope;
+    g.dim = d;
+    g.head_dim = hd;
+    if ((e = launch_gemm_bf16(g, GEMM_QKV, st)) != hipSuccess) return e;
+
+    FlashParams f{};
+    f.q = s->pq;
+    f.k = s->kcache(l);
+    f.v = s->vcache(l);
+    f.o16 = attn16;
+    f.q_bs = (long)S * d;
+    f.kv_bs = s->seq_stride();
+    f.o_bs = (long)S * d;
+    f.S = (int)S;
+    f.d = (int)d;
+    f.hd = (int)hd;
+    f.scale = 1.0f / sqrtf((float)hd);
+    if ((e = launch_flash_bf16(f, (int)s->B, (int)S, st)) != hipSuccess) return e;
+
+    GemmParams o{};
+    o.a16 = attn16;
+    o.bt16 = s->m->wt16[base + W_OUT];
+    o.c = s->px;
+    o.M = (int)rows;
+    o.N = d;
+    o.K = d;
+    if ((e = launch_gemm_bf16(o, GEMM_ADD, st)) != hipSuccess) return e;
+
+    if ((e = launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM2), s->pxn, (int)rows, (int)d,
+                                 c.norm_eps, st)) != hipSuccess)
+      return e;
+    GemmParams u{};
+    u.a = s->pxn;
+    u.bt16 = s->m->wt16[base + W_UP];
+    u.c = s->pffn;
+    u.M = (int)rows;
+    u.N = c.ffn_hidden;
+    u.K = d;
+    if ((e = launch_gemm_bf16(u, GEMM_SILU, st)) != hipSuccess) return e;
+
+    GemmParams w{};
+    w.a = s->pffn;
+    w.bt16 = s->m->wt16[base + W_DOWN];
+    w.c = s->px;
+    w.M = (int)rows;
+    w.N = d;
+    w.K = c.ffn_hidden;
+    if ((e = launch_gemm_bf16(w, GEMM_ADD, st)) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
 // InferenceSession::prefill (inference.rs:61-176) for all sequences, with
 // build_prefill_layer's node order (inference_graphs.rs:198-337): 7 kernels
 // per layer (RMSNorm, QKV GEMM + RoPE + cache append, flash attention,
@@ -1238,7 +1440,7 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
                   "prefill needs an empty cache, this one holds " +
                       std::to_string(s->cur_len[b]) + " tokens");
   const akh_model_config& c = s->m->cfg;
-  const uint32_t S = prompt_len, d = c.dim, hd = d / c.num_heads;
+  const uint32_t S = prompt_len, d = c.dim;
   const size_t rows = (size_t)s->B * S;
   akh_status st0 = ensure_prefill(s, rows);
   if (st0 != AKH_OK) return st0;
@@ -1251,68 +1453,7 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
 
   HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
                                 (int)d, c.vocab_size, st));
-  for (uint32_t l = 0; l < c.num_layers; ++l) {
-    HIP_TRY(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM1), s->pxn,
-                                (int)rows, (int)d, c.norm_eps, st));
-    GemmParams g{};
-    g.a = s->pxn;
-    g.b = s->m->layer(l, W_QKV);
-    g.M = (int)rows;
-    g.N = 3 * d;
-    g.K = d;
-    g.q_out = s->pq;
-    g.kcache = s->kcache(l);
-    g.vcache = s->vcache(l);
-    g.seq_stride = s->seq_stride();
-    g.S = (int)S;
-    g.rope = s->rope;
-    g.dim = d;
-    g.head_dim = hd;
-    HIP_TRY(launch_gemm(g, GEMM_QKV, st));
-
-    FlashParams f{};
-    f.q = s->pq;
-    f.k = s->kcache(l);
-    f.v = s->vcache(l);
-    f.o = s->pattn;
-    f.q_bs = (long)S * d;
-    f.kv_bs = s->seq_stride();
-    f.o_bs = (long)S * d;
-    f.S = (int)S;
-    f.d = (int)d;
-    f.hd = (int)hd;
-    f.scale = 1.0f / sqrtf((float)hd);
-    HIP_TRY(launch_flash(f, (int)s->B, (int)S, st));
-
-    GemmParams o{};
-    o.a = s->pattn;
-    o.b = s->m->layer(l, W_OUT);
-    o.c = s->px;
-    o.M = (int)rows;
-    o.N = d;
-    o.K = d;
-    HIP_TRY(launch_gemm(o, GEMM_ADD, st));
-
-    HIP_TRY(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM2), s->pxn,
-                                (int)rows, (int)d, c.norm_eps, st));
-    GemmParams u{};
-    u.a = s->pxn;
-    u.b = s->m->layer(l, W_UP);
-    u.c = s->pffn;
-    u.M = (int)rows;
-    u.N = c.ffn_hidden;
-    u.K = d;
-    HIP_TRY(launch_gemm(u, GEMM_SILU, st));
-
-    GemmParams w{};
-    w.a = s->pffn;
-    w.b = s->m->layer(l, W_DOWN);
-    w.c = s->px;
-    w.M = (int)rows;
-    w.N = d;
-    w.K = c.ffn_hidden;
-    HIP_TRY(launch_gemm(w, GEMM_ADD, st));
-  }
+  HIP_TRY(s->m->prefill_bf16 ? prefill_layers_bf16(s, S) : prefill_layers_f32(s, S));
   // Last row of every sequence -> final RMSNorm -> lm_head -> greedy token
   // (inference.rs:120-168).
   {

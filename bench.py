@@ -37,6 +37,7 @@ import __graft_entry__ as entry  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2516.6  # dense
 
 
 def log(*a):
@@ -124,6 +125,21 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True):
         out.update({"prefill_ms": round(pms, 2), "prefill_tok_s": round(Bp * Sp / (pms / 1e3), 1),
                     "prefill_tflops": round(fl / (pms / 1e3) / 1e12, 2),
                     "prefill_mfma_frac_fp32": round(fl / (pms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)})
+        # The optional bf16-MFMA prefill (logits within 2e-2 of f32).
+        log("bench: scaled config prefill 8 x 2048, bf16 MFMA")
+        model.set_prefill_bf16(True)
+        ps.reset()
+        ps.prefill(toks, want_logits=False)
+        ps.reset()
+        be.synchronize()
+        be.timer_start()
+        ps.prefill(toks, want_logits=False)
+        bms = be.timer_stop()
+        model.set_prefill_bf16(False)
+        out.update({"prefill_bf16_ms": round(bms, 2),
+                    "prefill_bf16_tok_s": round(Bp * Sp / (bms / 1e3), 1),
+                    "prefill_bf16_tflops": round(fl / (bms / 1e3) / 1e12, 2),
+                    "prefill_bf16_mfma_frac_bf16": round(fl / (bms / 1e3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)})
         ps.close()
     model.close()
     return out

@@ -228,6 +228,18 @@ akh_status akh_model_upload_param(akh_model* m, uint32_t index,
  * matrix now; `n_bf16` (optional) receives how many matrices are tiled in
  * bfloat16 afterwards. */
 akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16);
+/* No reference counterpart (the reference computes prefill in f32): with
+ * enable = 1, prefill runs its layer GEMMs and flash attention on the
+ * bfloat16 MFMAs with fp32 accumulation.  Weights are rounded to bfloat16
+ * (exact for bf16-valued weights); the QKV, ffn_up and ffn_down GEMMs take
+ * their fp32 inputs as bfloat16 hi + lo pairs, out_proj and attention take
+ * bfloat16 operands.  The residual stream, KV cache, final norm, lm_head and
+ * decode stay f32.  This is the optional bf16-MFMA path: logits track the
+ * f32 path within 2e-2 instead of 1e-3.  While enabled the model keeps a
+ * transposed bfloat16 copy of every layer matrix (refreshed by
+ * akh_model_upload_param).  Needs head_dim 64 or 128 and dim, ffn_hidden
+ * multiples of 8. */
+akh_status akh_model_set_prefill_bf16(akh_model* m, int enable);
 
 /* ---- checkpoints: src/nn/checkpoint.rs (format V3) ---------------------- */
 
