@@ -441,7 +441,13 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
   __shared__ __align__(16) uint16_t Bs[2][BN][LD];
 
   const int M = p.M, N = p.N, K = p.K;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // Workgroups go to the 8 XCDs round-robin in launch order; give each XCD
+  // a contiguous run of tiles (N fastest) so the blocks sharing an A panel
+  // share that XCD's L2.
+  int id = blockIdx.x + gridDim.x * blockIdx.y;
+  const int per_xcd = (int)(gridDim.x * gridDim.y) / 8;
+  if (id < per_xcd * 8) id = (id % 8) * per_xcd + id / 8;
+  const int m0 = (id / gridDim.x) * BM, n0 = (id % gridDim.x) * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
   const int j = lane & 31, h = lane >> 5;
@@ -560,8 +566,8 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
   constexpr int KP = HD + 8;   // K row stride (bf16)
   constexpr int VP = KB + 8;   // V^T row stride (bf16)
   constexpr int CPR = HD / 4;  // float4 per K/V row
-  constexpr int RPP = 256 / CPR;
-  constexpr int NP = KB / RPP;
+  constexpr int KPT = KB * CPR / 256;  // consecutive keys staged per thread
+  static_assert(KPT == 2 || KPT == 4, "staging covers 2 or 4 keys per thread");
   constexpr int KV_BYTES = (KB * KP + HD * VP) * 2;
   constexpr int O_BYTES = 4 * 32 * 33 * 4;
   __shared__ __align__(16) unsigned char lds[KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES];
@@ -569,7 +575,8 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
   uint16_t (*Vt)[VP] = reinterpret_cast<uint16_t (*)[VP]>(lds + KB * KP * 2);
 
   const int S = p.S, d = p.d;
-  const float scale = p.scale;
+  // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
+  const float qscale = p.scale * 1.44269504088896341f;
   const int qblk = gridDim.x - 1 - blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
@@ -594,33 +601,45 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
   for (int t = 0; t < NT; ++t) o[t] = zero16();
   float mrow = -INFINITY, lrow = 0.f;
 
-  const int wave_qmax = q0 + wave * 32 + 31;
+  const int wave_qmin = q0 + wave * 32, wave_qmax = wave_qmin + 31;
   const int kend = min(S, q0 + QB);
   const int nkb = (kend + KB - 1) / KB;
 
-  const int lr = tid / CPR, lc = (tid % CPR) * 4;
-  float4 kr[NP], vr[NP];
+  // Staging: thread t takes dims 4 (t % CPR) .. + 3 of KPT consecutive keys
+  // from KPT (t / CPR), so K rows and V^T rows are both written 4 or 8 bytes
+  // at a time.
+  const int sc = (tid % CPR) * 4, sk = (tid / CPR) * KPT;
+  float4 kr[KPT], vr[KPT];
   auto load_kv = [&](int kb) {
 #pragma unroll
-    for (int q = 0; q < NP; ++q) {
-      const int key = kb * KB + lr + RPP * q;
-      const size_t off = (size_t)(key < S ? key : 0) * d + lc;
-      kr[q] = *reinterpret_cast<const float4*>(kp + off);
-      vr[q] = *reinterpret_cast<const float4*>(vp + off);
+    for (int i = 0; i < KPT; ++i) {
+      const int key = kb * KB + sk + i;
+      const size_t off = (size_t)(key < S ? key : 0) * d + sc;
+      kr[i] = *reinterpret_cast<const float4*>(kp + off);
+      vr[i] = *reinterpret_cast<const float4*>(vp + off);
     }
   };
   load_kv(0);
   for (int kb = 0; kb < nkb; ++kb) {
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < NP; ++q) {
-      const int r = lr + RPP * q;
-      *reinterpret_cast<uint2*>(&Ks[r][lc]) =
-          make_uint2(pack_bf16x2(kr[q].x, kr[q].y), pack_bf16x2(kr[q].z, kr[q].w));
-      Vt[lc][r] = (uint16_t)bf16_bits(vr[q].x);
-      Vt[lc + 1][r] = (uint16_t)bf16_bits(vr[q].y);
-      Vt[lc + 2][r] = (uint16_t)bf16_bits(vr[q].z);
-      Vt[lc + 3][r] = (uint16_t)bf16_bits(vr[q].w);
+    for (int i = 0; i < KPT; ++i)
+      *reinterpret_cast<uint2*>(&Ks[sk + i][sc]) =
+          make_uint2(pack_bf16x2(kr[i].x, kr[i].y), pack_bf16x2(kr[i].z, kr[i].w));
+    if constexpr (KPT == 4) {
+      *reinterpret_cast<uint2*>(&Vt[sc][sk]) =
+          make_uint2(pack_bf16x2(vr[0].x, vr[1].x), pack_bf16x2(vr[2].x, vr[3].x));
+      *reinterpret_cast<uint2*>(&Vt[sc + 1][sk]) =
+          make_uint2(pack_bf16x2(vr[0].y, vr[1].y), pack_bf16x2(vr[2].y, vr[3].y));
+      *reinterpret_cast<uint2*>(&Vt[sc + 2][sk]) =
+          make_uint2(pack_bf16x2(vr[0].z, vr[1].z), pack_bf16x2(vr[2].z, vr[3].z));
+      *reinterpret_cast<uint2*>(&Vt[sc + 3][sk]) =
+          make_uint2(pack_bf16x2(vr[0].w, vr[1].w), pack_bf16x2(vr[2].w, vr[3].w));
+    } else {
+      *reinterpret_cast<uint32_t*>(&Vt[sc][sk]) = pack_bf16x2(vr[0].x, vr[1].x);
+      *reinterpret_cast<uint32_t*>(&Vt[sc + 1][sk]) = pack_bf16x2(vr[0].y, vr[1].y);
+      *reinterpret_cast<uint32_t*>(&Vt[sc + 2][sk]) = pack_bf16x2(vr[0].z, vr[1].z);
+      *reinterpret_cast<uint32_t*>(&Vt[sc + 3][sk]) = pack_bf16x2(vr[0].w, vr[1].w);
     }
     __syncthreads();
     load_kv(kb + 1);  // rows past S read row 0: harmless, never used
@@ -633,32 +652,38 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
       st = mfma_bf16(bf16x8_of(*reinterpret_cast<const uint4*>(&Ks[j][16 * s + 8 * h])), qf[s],
                      st);
 
+    // Keys above a query (the diagonal block) or past S are masked.
+    const bool masked = j0 + KB - 1 > wave_qmin || j0 + KB > S;
     float pm = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int key = j0 + acc_row(r, h);
-      float v = st[r] * scale;
-      if (key > qi || key >= S) v = -INFINITY;
+      float v = st[r] * qscale;
+      if (masked) {
+        const int key = j0 + acc_row(r, h);
+        if (key > qi || key >= S) v = -INFINITY;
+      }
       st[r] = v;
       pm = fmaxf(pm, v);
     }
     pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
-    const float mnew = fmaxf(mrow, pm);
+    const float mnew = fmaxf(mrow, pm);  // finite: key 0 is in every query's range
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float e = st[r] == -INFINITY ? 0.f : expf(st[r] - mnew);
+      const float e = __builtin_amdgcn_exp2f(st[r] - mnew);
       st[r] = e;
       ps += e;
     }
     ps += __shfl_xor(ps, 32, 64);
-    const float corr = mrow == -INFINITY ? 0.f : expf(mrow - mnew);
+    const float corr = __builtin_amdgcn_exp2f(mrow - mnew);  // 0 on the first block
     lrow = lrow * corr + ps;
+    if (__any(mnew != mrow)) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    }
     mrow = mnew;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
     const bf16x8 p0 = bf16x8_of(make_float4(st[0], st[1], st[2], st[3]),
                                 make_float4(st[4], st[5], st[6], st[7]));
     const bf16x8 p1 = bf16x8_of(make_float4(st[8], st[9], st[10], st[11]),
