@@ -94,7 +94,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     N = (int)p.meta->n;
     K = (int)p.meta->k;
   }
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // Each XCD takes a contiguous run of tiles (see k_gemm_bf16).
+  int id = blockIdx.x + gridDim.x * blockIdx.y;
+  const int per_xcd = (int)(gridDim.x * gridDim.y) / 8;
+  if (id < per_xcd * 8) id = (id % 8) * per_xcd + id / 8;
+  const int m0 = (id / gridDim.x) * BM, n0 = (id % gridDim.x) * BN;
   if (m0 >= M || n0 >= N) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
