@@ -55,6 +55,17 @@ hipError_t shader_attn_av_cached(const float* scores, const float* vc,
                                  const akh_attn_cached_meta* meta,
                                  hipStream_t s);
 hipError_t shader_silu(float* buf, uint32_t len, hipStream_t s);
+hipError_t shader_qkv_split(const float* src, float* q, float* k, float* v,
+                            akh_head_move_meta shape, const akh_head_move_meta* meta,
+                            hipStream_t s);
+hipError_t shader_rope_qk(float* q, float* k, akh_rope_meta shape, const akh_rope_meta* meta,
+                          hipStream_t s);
+hipError_t shader_add(const float* a, const float* b, float* out, uint32_t len, hipStream_t s);
+hipError_t shader_silu_out(const float* x, float* out, uint32_t len, hipStream_t s);
+// CROSS_ENTROPY over `rows` rows (grid); the live meta bounds the work.
+hipError_t launch_cross_entropy(float* logits, const uint32_t* targets, float* losses,
+                                uint32_t rows, const akh_cross_entropy_meta* meta,
+                                hipStream_t s);
 hipError_t shader_argmax_rows(const float* logits, uint32_t rows, uint32_t n,
                               uint32_t* out, hipStream_t s);
 

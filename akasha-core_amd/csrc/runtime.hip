@@ -384,6 +384,60 @@ extern "C" akh_status akh_silu(akh_backend* be, float* buf, uint32_t len) {
   return AKH_OK;
 }
 
+extern "C" akh_status akh_qkv_split(akh_backend* be, const float* src, float* q, float* k,
+                                    float* v, akh_head_move_meta shape,
+                                    const akh_head_move_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(src && q && k && v && meta, "akh_qkv_split: NULL buffer");
+  CHECK_ARG(shape.full_dim >= 3 * shape.head_dim, "akh_qkv_split: full_dim < 3 * head_dim");
+  HIP_TRY(shader_qkv_split(src, q, k, v, shape, meta, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_rope_qk(akh_backend* be, float* q, float* k, akh_rope_meta shape,
+                                  const akh_rope_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(q && k && meta, "akh_rope_qk: NULL buffer");
+  CHECK_ARG(shape.head_dim && shape.dim % shape.head_dim == 0 && shape.head_dim % 2 == 0,
+            "akh_rope_qk: head_dim must be even and divide dim");
+  HIP_TRY(shader_rope_qk(q, k, shape, meta, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_add(akh_backend* be, const float* a, const float* b, float* out,
+                              uint32_t len) {
+  BE_CHECK(be);
+  CHECK_ARG((a && b && out) || !len, "akh_add: NULL buffer");
+  HIP_TRY(shader_add(a, b, out, len, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_residual_add(akh_backend* be, float* target, const float* source,
+                                       uint32_t len) {
+  BE_CHECK(be);
+  CHECK_ARG((target && source) || !len, "akh_residual_add: NULL buffer");
+  HIP_TRY(shader_add(target, source, target, len, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_silu_out(akh_backend* be, const float* input, float* out,
+                                   uint32_t len) {
+  BE_CHECK(be);
+  CHECK_ARG((input && out) || !len, "akh_silu_out: NULL buffer");
+  HIP_TRY(shader_silu_out(input, out, len, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_cross_entropy(akh_backend* be, float* logits, const uint32_t* targets,
+                                        float* losses, akh_cross_entropy_meta shape,
+                                        const akh_cross_entropy_meta* meta) {
+  BE_CHECK(be);
+  CHECK_ARG(logits && targets && losses && meta, "akh_cross_entropy: NULL buffer");
+  CHECK_ARG(shape.vocab_size > 0, "akh_cross_entropy: empty rows");
+  HIP_TRY(launch_cross_entropy(logits, targets, losses, shape.num_rows, meta, be->stream));
+  return AKH_OK;
+}
+
 extern "C" akh_status akh_argmax_rows(akh_backend* be, const float* logits,
                                       uint32_t rows, uint32_t n,
                                       uint32_t* out) {
@@ -1141,20 +1195,25 @@ extern "C" void akh_session_free(akh_session* s) {
   delete s;
 }
 
-extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
-                                      uint32_t batch, akh_session** out) {
+namespace {
+
+// A session's buffers.  With decode false only what prefill needs (KV
+// cache, RoPE table) is allocated, and the decode kernels' shape limits do
+// not apply: the trainer's forward uses such a session.
+akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch, bool decode,
+                          akh_session** out) {
   CHECK_ARG(m && out, "akh_session_new: NULL argument");
   *out = nullptr;
   const akh_model_config& c = m->cfg;
-  CHECK_ARG(batch >= 1 && batch <= (uint32_t)kMaxBatch,
+  CHECK_ARG(batch >= 1 && (!decode || batch <= (uint32_t)kMaxBatch),
             "akh_session_new: batch must be in 1..32");
   CHECK_ARG(max_context_len >= 1, "akh_session_new: max_context_len is 0");
   const uint32_t hd = c.dim / c.num_heads;
-  CHECK_ARG(supported_head_dim(hd) && hd >= 4,
+  CHECK_ARG(supported_head_dim(hd) && (hd >= 4 || !decode),
             "akh_session_new: head_dim must be a power of two in 4..128");
-  CHECK_ARG(c.dim % 32 == 0 && c.dim <= 4096,
+  CHECK_ARG(!decode || (c.dim % 32 == 0 && c.dim <= 4096),
             "akh_session_new: dim must be a multiple of 32, at most 4096");
-  CHECK_ARG(c.ffn_hidden % 32 == 0,
+  CHECK_ARG(!decode || c.ffn_hidden % 32 == 0,
             "akh_session_new: ffn_hidden must be a multiple of 32");
 
   akh_session* s = new akh_session();
@@ -1177,6 +1236,7 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   };
   alloc((void**)&s->kv, (size_t)c.num_layers * 2 * batch * max_context_len * d * 4);
   alloc((void**)&s->rope, (size_t)max_context_len * (hd / 2) * sizeof(float2));
+  if (decode) {
   alloc((void**)&s->xt, R * d * 4);
   alloc((void**)&s->xnt, R * d * 4);
   alloc((void**)&s->attn_t, (size_t)dec_attn_splits() * R * d * 4);
@@ -1195,6 +1255,7 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
   alloc((void**)&s->gstart, R * sizeof(int));
   alloc((void**)&s->gcount, R * sizeof(uint32_t));
   alloc((void**)&s->gwbuf, sample_scratch_bytes((int)batch, (int)V));
+  }
   if (e == hipSuccess) {
     // RoPE table in f32 exactly as src/shaders/cpu.rs:98-100 forms it:
     // freq = 1 / 10000^(2i / head_dim), angle = pos * freq, then sin/cos.
@@ -1213,13 +1274,20 @@ extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
     akh_session_free(s);
     return fail(AKH_E_HIP, std::string("akh_session_new: ") + hipGetErrorString(e));
   }
-  akh_status st = set_active(s, true);
+  akh_status st = decode ? set_active(s, true) : AKH_OK;
   if (st != AKH_OK) {
     akh_session_free(s);
     return st;
   }
   *out = s;
   return AKH_OK;
+}
+
+}  // namespace
+
+extern "C" akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
+                                      uint32_t batch, akh_session** out) {
+  return session_create(m, max_context_len, batch, true, out);
 }
 
 extern "C" akh_status akh_session_reset(akh_session* s) {
@@ -1716,5 +1784,117 @@ extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,
   float ms = 0.f;
   HIP_TRY(hipEventElapsedTime(&ms, be->t0, be->t1));
   *avg_ms = ms / (float)reps;
+  return AKH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The trainer's fused forward (Trainer::forward + CrossEntropy)
+// ---------------------------------------------------------------------------
+
+struct akh_forward {
+  akh_model* m = nullptr;
+  akh_session* s = nullptr;  // prefill buffers; its KV cache is scratch
+  uint32_t B = 0, S = 0;
+  float* logits = nullptr;    // [rows, vocab]: logits, then probabilities
+  float* losses = nullptr;    // [rows]
+  uint32_t* targets = nullptr;
+  akh_cross_entropy_meta* ce = nullptr;  // device meta
+};
+
+extern "C" void akh_forward_free(akh_forward* f) {
+  if (!f) return;
+  if (f->s) akh_session_free(f->s);
+  void* bufs[] = {f->logits, f->losses, f->targets, f->ce};
+  for (void* p : bufs)
+    if (p) hipFree(p);
+  delete f;
+}
+
+extern "C" akh_status akh_forward_new(akh_model* m, uint32_t batch, uint32_t seq_len,
+                                      akh_forward** out) {
+  CHECK_ARG(m && out, "akh_forward_new: NULL argument");
+  CHECK_ARG(batch >= 1 && seq_len >= 1, "akh_forward_new: needs batch >= 1 and seq_len >= 1");
+  *out = nullptr;
+  akh_forward* f = new akh_forward();
+  f->m = m;
+  f->B = batch;
+  f->S = seq_len;
+  akh_status st = session_create(m, seq_len, batch, false, &f->s);
+  if (st != AKH_OK) {
+    akh_forward_free(f);
+    return st;
+  }
+  const size_t rows = (size_t)batch * seq_len, V = m->cfg.vocab_size;
+  hipError_t e = hipMalloc(&f->logits, rows * V * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&f->losses, rows * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&f->targets, rows * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMalloc(&f->ce, sizeof(akh_cross_entropy_meta));
+  akh_cross_entropy_meta ce{(uint32_t)V, (uint32_t)rows};
+  if (e == hipSuccess) e = hipMemcpy(f->ce, &ce, sizeof ce, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    akh_forward_free(f);
+    return fail(AKH_E_HIP, std::string("akh_forward_new: ") + hipGetErrorString(e));
+  }
+  *out = f;
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_forward_loss(akh_forward* f, const uint32_t* tokens,
+                                       const uint32_t* targets, float* losses,
+                                       float* mean_loss) {
+  CHECK_ARG(f && tokens && targets && mean_loss, "akh_forward_loss: NULL argument");
+  akh_session* s = f->s;
+  const akh_model_config& c = f->m->cfg;
+  const uint32_t S = f->S, d = c.dim, V = c.vocab_size;
+  const size_t rows = (size_t)f->B * S;
+  for (size_t r = 0; r < rows; ++r)
+    CHECK_ARG(targets[r] < V, "akh_forward_loss: target token " + std::to_string(targets[r]) +
+                                  " is out of the vocabulary");
+  akh_status st0 = ensure_prefill(s, rows);
+  if (st0 != AKH_OK) return st0;
+  hipStream_t st = s->be->stream;
+  HIP_TRY(hipMemcpyAsync(s->ptok, tokens, rows * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(f->targets, targets, rows * 4, hipMemcpyHostToDevice, st));
+  HIP_TRY(launch_embedding_rows(s->ptok, f->m->embedding(), s->px, (int)rows, (int)d, V, st));
+  HIP_TRY(f->m->prefill_bf16 ? prefill_layers_bf16(s, S) : prefill_layers_f32(s, S));
+  // final_norm and lm_head on every row (train.rs:154-177), then the loss.
+  HIP_TRY(launch_rows_rmsnorm(s->px, f->m->final_norm(), s->pxn, (int)rows, (int)d, c.norm_eps,
+                              st));
+  GemmParams g{};
+  g.a = s->pxn;
+  g.b = f->m->lm_head();
+  g.c = f->logits;
+  g.M = (int)rows;
+  g.N = (int)V;
+  g.K = (int)d;
+  HIP_TRY(launch_gemm(g, GEMM_STORE, st));
+  HIP_TRY(launch_cross_entropy(f->logits, f->targets, f->losses, (uint32_t)rows, f->ce, st));
+  std::vector<float> l(rows);
+  HIP_TRY(hipMemcpyAsync(l.data(), f->losses, rows * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  // CrossEntropy::loss (layers.rs:512-515): sequential f32 sum over rows.
+  float sum = 0.f;
+  for (float v : l) sum += v;
+  *mean_loss = sum / (float)rows;
+  if (losses) std::copy(l.begin(), l.end(), losses);
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_forward_probs(akh_forward* f, uint32_t row0, uint32_t n, float* host) {
+  CHECK_ARG(f && (host || !n), "akh_forward_probs: NULL argument");
+  CHECK_ARG((size_t)row0 + n <= (size_t)f->B * f->S, "akh_forward_probs: rows out of range");
+  const size_t V = f->m->cfg.vocab_size;
+  HIP_TRY(hipMemcpyAsync(host, f->logits + (size_t)row0 * V, (size_t)n * V * 4,
+                         hipMemcpyDeviceToHost, f->s->be->stream));
+  HIP_TRY(hipStreamSynchronize(f->s->be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_forward_hidden(akh_forward* f, float* host) {
+  CHECK_ARG(f && host, "akh_forward_hidden: NULL argument");
+  CHECK_ARG(f->s->px, "akh_forward_hidden: no forward has run");
+  HIP_TRY(hipMemcpyAsync(host, f->s->px, (size_t)f->B * f->S * f->m->cfg.dim * 4,
+                         hipMemcpyDeviceToHost, f->s->be->stream));
+  HIP_TRY(hipStreamSynchronize(f->s->be->stream));
   return AKH_OK;
 }

@@ -373,6 +373,139 @@ hipError_t shader_attn_av_cached(const float* scores, const float* vc,
   return hipGetLastError();
 }
 
+// ---- the trainer's forward shaders (src/nn/train.rs:256-275) -------------
+
+// QKV_SPLIT (src/shaders/mod.rs:376-395, CUDA twin cuda.rs:296-318): the
+// three head_dim-wide column slices of each src row.
+__global__ void k_qkv_split(const float* src, float* q, float* k, float* v,
+                            const akh_head_move_meta* meta) {
+  const uint32_t rows = meta->seq_len, full = meta->full_dim, w = meta->head_dim;
+  const size_t n = (size_t)rows * w;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t row = i / w, col = i % w;
+    const float* r = src + row * full;
+    q[i] = r[col];
+    k[i] = r[w + col];
+    v[i] = r[2 * w + col];
+  }
+}
+
+// ROPE_QK (src/shaders/mod.rs:139-158, CUDA twin cuda.rs:152-185): RoPE on
+// rows row_offset + t of q and k at local position t (cpu.rs:98-103 angle).
+__global__ void k_rope_qk(float* q, float* k, const akh_rope_meta* meta) {
+  const uint32_t rows = meta->seq_len, dim = meta->dim, hd = meta->head_dim;
+  const size_t base = (size_t)meta->row_offset * dim;
+  const size_t pairs = (size_t)rows * (dim / 2);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < pairs;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t t = (uint32_t)(i / (dim / 2));
+    const uint32_t c = (uint32_t)(i % (dim / 2)) * 2u;
+    const float freq = 1.0f / powf(10000.0f, (float)(c % hd) / (float)hd);
+    float sn, cs;
+    sincosf((float)t * freq, &sn, &cs);
+    const size_t o = base + (size_t)t * dim + c;
+    float a0 = q[o], a1 = q[o + 1];
+    rope_pair(a0, a1, cs, sn);
+    q[o] = a0;
+    q[o + 1] = a1;
+    float b0 = k[o], b1 = k[o + 1];
+    rope_pair(b0, b1, cs, sn);
+    k[o] = b0;
+    k[o + 1] = b1;
+  }
+}
+
+// ADD (cpu.rs:77-82) with sub == 0: out = a + b; the RESIDUAL_ADD builtin
+// (emit.rs:733-748) is the same kernel with out == a.
+__global__ void k_add(const float* a, const float* b, float* out, uint32_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = a[i] + b[i];
+}
+
+// SILU_OUT (cpu.rs:71-75).
+__global__ void k_silu_out(const float* x, float* out, uint32_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = x[i] / (1.0f + expf(-x[i]));
+}
+
+// Reductions over a 1024-thread block in a fixed order.
+__device__ __forceinline__ float block_red1024(float v, float* red, bool is_max) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < 16; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+  return r;
+}
+
+// CROSS_ENTROPY (cpu.rs:277-306), one 1024-thread block per row, in place:
+// m = row max, s = sum of e^(x - m), loss = -(x[target] - m - ln s), and the
+// row becomes e^(x - m) / s.  A target id >= vocab has no logit; its loss is
+// NaN (the reference indexes out of bounds there).
+__global__ __launch_bounds__(1024) void k_cross_entropy(float* x, const uint32_t* targets,
+                                                        float* losses,
+                                                        const akh_cross_entropy_meta* meta) {
+  __shared__ float red[16];
+  const uint32_t V = meta->vocab_size, row = blockIdx.x;
+  if (row >= meta->num_rows) return;
+  float* r = x + (size_t)row * V;
+  float m = -INFINITY;
+  for (uint32_t i = threadIdx.x; i < V; i += 1024) m = fmaxf(m, r[i]);
+  m = block_red1024(m, red, true);
+  float sum = 0.f;
+  for (uint32_t i = threadIdx.x; i < V; i += 1024) sum += expf(r[i] - m);
+  sum = block_red1024(sum, red, false);
+  if (threadIdx.x == 0) {
+    const uint32_t t = targets[row];
+    losses[row] = t < V ? -(r[t] - m - logf(sum)) : __builtin_nanf("");
+  }
+  __syncthreads();  // the target's logit is read before the row is rewritten
+  for (uint32_t i = threadIdx.x; i < V; i += 1024) r[i] = expf(r[i] - m) / sum;
+}
+
+hipError_t shader_qkv_split(const float* src, float* q, float* k, float* v,
+                            akh_head_move_meta shape, const akh_head_move_meta* meta,
+                            hipStream_t s) {
+  const size_t n = (size_t)shape.seq_len * shape.head_dim;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_qkv_split, dim3(grid1d(n, 256)), dim3(256), 0, s, src, q, k, v, meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_rope_qk(float* q, float* k, akh_rope_meta shape, const akh_rope_meta* meta,
+                          hipStream_t s) {
+  const size_t n = (size_t)shape.seq_len * (shape.dim / 2);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rope_qk, dim3(grid1d(n, 256)), dim3(256), 0, s, q, k, meta);
+  return hipGetLastError();
+}
+
+hipError_t shader_add(const float* a, const float* b, float* out, uint32_t len, hipStream_t s) {
+  if (len == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_add, dim3(grid1d(len, 256)), dim3(256), 0, s, a, b, out, len);
+  return hipGetLastError();
+}
+
+hipError_t shader_silu_out(const float* x, float* out, uint32_t len, hipStream_t s) {
+  if (len == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_silu_out, dim3(grid1d(len, 256)), dim3(256), 0, s, x, out, len);
+  return hipGetLastError();
+}
+
+hipError_t launch_cross_entropy(float* logits, const uint32_t* targets, float* losses,
+                                uint32_t rows, const akh_cross_entropy_meta* meta,
+                                hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_cross_entropy, dim3(rows), dim3(1024), 0, s, logits, targets, losses,
+                     meta);
+  return hipGetLastError();
+}
+
 hipError_t shader_silu(float* buf, uint32_t len, hipStream_t s) {
   if (len == 0) return hipSuccess;
   hipLaunchKernelGGL(k_silu, dim3(grid1d(len, 256)), dim3(256), 0, s, buf,

@@ -141,6 +141,10 @@ class FlashAttnMeta(C.Structure):
                 ("scale", C.c_float), ("row_offset", C.c_uint32)]
 
 
+class CrossEntropyMeta(C.Structure):
+    _fields_ = [("vocab_size", C.c_uint32), ("num_rows", C.c_uint32)]
+
+
 class ModelConfigC(C.Structure):
     _fields_ = [("vocab_size", C.c_uint32), ("dim", C.c_uint32),
                 ("num_heads", C.c_uint32), ("num_layers", C.c_uint32),
@@ -180,6 +184,17 @@ _SIGS = {
     "akh_softmax_rect": (ST, [P, P, SoftmaxRectMeta, P]),
     "akh_attn_av_cached": (ST, [P, P, P, P, U32, P]),
     "akh_silu": (ST, [P, P, U32]),
+    "akh_qkv_split": (ST, [P, P, P, P, P, HeadMoveMeta, P]),
+    "akh_rope_qk": (ST, [P, P, P, RopeMeta, P]),
+    "akh_add": (ST, [P, P, P, P, U32]),
+    "akh_residual_add": (ST, [P, P, P, U32]),
+    "akh_silu_out": (ST, [P, P, P, U32]),
+    "akh_cross_entropy": (ST, [P, P, P, P, CrossEntropyMeta, P]),
+    "akh_forward_new": (ST, [P, U32, U32, C.POINTER(P)]),
+    "akh_forward_free": (None, [P]),
+    "akh_forward_loss": (ST, [P, P, P, P, C.POINTER(C.c_float)]),
+    "akh_forward_probs": (ST, [P, U32, U32, P]),
+    "akh_forward_hidden": (ST, [P, P]),
     "akh_argmax_rows": (ST, [P, P, U32, U32, P]),
     "akh_sample_rows": (ST, [P, P, U32, U32, Sampling, P, U32, P, P, P]),
     "akh_model_new": (ST, [P, C.POINTER(ModelConfigC), C.POINTER(P)]),
@@ -423,6 +438,26 @@ class Backend:
     def silu(self, buf, length):
         _check(_lib.akh_silu(self.handle, _p(buf), length), "silu")
 
+    def qkv_split(self, src, q, k, v, shape: HeadMoveMeta, meta):
+        _check(_lib.akh_qkv_split(self.handle, _p(src), _p(q), _p(k), _p(v), shape, _p(meta)),
+               "qkv_split")
+
+    def rope_qk(self, q, k, shape: RopeMeta, meta):
+        _check(_lib.akh_rope_qk(self.handle, _p(q), _p(k), shape, _p(meta)), "rope_qk")
+
+    def add(self, a, b, out, length):
+        _check(_lib.akh_add(self.handle, _p(a), _p(b), _p(out), length), "add")
+
+    def residual_add(self, target, source, length):
+        _check(_lib.akh_residual_add(self.handle, _p(target), _p(source), length), "residual_add")
+
+    def silu_out(self, x, out, length):
+        _check(_lib.akh_silu_out(self.handle, _p(x), _p(out), length), "silu_out")
+
+    def cross_entropy(self, logits, targets, losses, shape: CrossEntropyMeta, meta):
+        _check(_lib.akh_cross_entropy(self.handle, _p(logits), _p(targets), _p(losses), shape,
+                                      _p(meta)), "cross_entropy")
+
     def argmax_rows(self, logits, rows, n, out):
         _check(_lib.akh_argmax_rows(self.handle, _p(logits), rows, n, _p(out)), "argmax_rows")
 
@@ -524,6 +559,43 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+class Forward:
+    """Trainer::forward + CrossEntropy over batch x seq_len rows
+    (src/nn/train.rs:256-275), on the prefill kernels."""
+
+    def __init__(self, model: "Model", batch: int, seq_len: int):
+        self.model, self.batch, self.seq_len = model, batch, seq_len
+        h = P()
+        _check(_lib.akh_forward_new(model.handle, batch, seq_len, C.byref(h)), "forward_new")
+        self.handle = h
+
+    def loss(self, tokens, targets):
+        """(mean_loss, losses [batch * seq_len])."""
+        t = np.ascontiguousarray(tokens, np.uint32).reshape(-1)
+        g = np.ascontiguousarray(targets, np.uint32).reshape(-1)
+        assert t.size == g.size == self.batch * self.seq_len
+        losses = np.empty(t.size, np.float32)
+        mean = C.c_float()
+        _check(_lib.akh_forward_loss(self.handle, _ptr(t), _ptr(g), _ptr(losses),
+                                     C.byref(mean)), "forward_loss")
+        return mean.value, losses
+
+    def probs(self, row0: int, n: int) -> np.ndarray:
+        out = np.empty((n, self.model.cfg.vocab_size), np.float32)
+        _check(_lib.akh_forward_probs(self.handle, row0, n, _ptr(out)), "forward_probs")
+        return out
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty((self.batch * self.seq_len, self.model.cfg.dim), np.float32)
+        _check(_lib.akh_forward_hidden(self.handle, _ptr(out)), "forward_hidden")
+        return out
+
+    def close(self):
+        if self.handle:
+            _lib.akh_forward_free(self.handle)
+            self.handle = None
 
 
 class Session:

@@ -268,6 +268,26 @@ def main():
                    "mfma_frac": round(fl / (pms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
                    "flop": fl}
         ps.close()
+        # Trainer::forward + CrossEntropy on the same 16 x 512 rows: the
+        # lm_head runs on every row (+2 rows d V flop) and the loss follows.
+        fw = hip.Forward(model, Bp, Sp)
+        targets = np.roll(ptoks, -1, axis=1)
+        fw.loss(ptoks, targets)  # warm
+        ftimes = []
+        for _ in range(3):
+            be.synchronize()
+            be.timer_start()
+            mean_loss, _ = fw.loss(ptoks, targets)
+            ftimes.append(be.timer_stop())
+        fms = min(ftimes)
+        ffl = fl - 2 * Bp * cfg.dim * cfg.vocab_size + 2 * Bp * Sp * cfg.dim * cfg.vocab_size
+        prefill["train_forward"] = {
+            "workload": "Trainer::forward + CrossEntropy, 16 x 512 rows (seed 3), all-rows lm_head",
+            "ms": round(fms, 3), "tok_s": round(Bp * Sp / (fms / 1e3), 1),
+            "tflops": round(ffl / (fms / 1e3) / 1e12, 2),
+            "mfma_frac": round(ffl / (fms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "mean_loss": round(mean_loss, 4), "flop": ffl}
+        fw.close()
 
     scaled = None
     if args.scaled:

@@ -68,6 +68,7 @@ typedef struct {
   float scale;
   uint32_t row_offset;
 } akh_flash_attn_meta;                                                 /* :156-164 */
+typedef struct { uint32_t vocab_size, num_rows; } akh_cross_entropy_meta; /* :124-130 */
 
 /* ---- 1. backend, tensors, graphs ----------------------------------------- */
 
@@ -169,6 +170,33 @@ akh_status akh_silu(akh_backend* be, float* buf, uint32_t len);
 akh_status akh_argmax_rows(akh_backend* be, const float* logits,
                            uint32_t rows, uint32_t n, uint32_t* out);
 
+/* The trainer's forward shaders (Trainer::forward, src/nn/train.rs:256-275). */
+/* QKV_SPLIT, ops::qkv_split (emit.rs:438-458; CUDA twin cuda.rs:296-318):
+ * q/k/v[row, col] = src[row, role * head_dim + col] for row < seq_len,
+ * col < head_dim, src rows full_dim wide.  Slots: src, q, k, v, meta. */
+akh_status akh_qkv_split(akh_backend* be, const float* src, float* q, float* k, float* v,
+                         akh_head_move_meta shape, const akh_head_move_meta* meta);
+/* ROPE_QK, ops::rope_qk (emit.rs:344-360; CUDA twin cuda.rs:152-185): RoPE
+ * in place on rows row_offset .. row_offset + seq_len of q and k, at local
+ * positions 0 .. seq_len - 1.  Slots: q, k, meta. */
+akh_status akh_rope_qk(akh_backend* be, float* q, float* k, akh_rope_meta shape,
+                       const akh_rope_meta* meta);
+/* ADD, ops::add_out (emit.rs:750-767; cpu.rs:77-82): out = a + b. */
+akh_status akh_add(akh_backend* be, const float* a, const float* b, float* out, uint32_t len);
+/* RESIDUAL_ADD builtin, ops::residual_add (emit.rs:733-748): target += source. */
+akh_status akh_residual_add(akh_backend* be, float* target, const float* source,
+                            uint32_t len);
+/* SILU_OUT, ops::silu_out (emit.rs:698-713; cpu.rs:71-75): out = x / (1 + e^-x). */
+akh_status akh_silu_out(akh_backend* be, const float* input, float* out, uint32_t len);
+/* CROSS_ENTROPY, ops::cross_entropy (emit.rs:864-882; cpu.rs:277-306), in
+ * place: each row of logits [num_rows, vocab] becomes its softmax and
+ * losses[row] = -(x[target] - max - ln sum).  A target id >= vocab_size
+ * gives a NaN loss (the reference indexes out of bounds).  Slots: logits,
+ * targets, losses, meta. */
+akh_status akh_cross_entropy(akh_backend* be, float* logits, const uint32_t* targets,
+                             float* losses, akh_cross_entropy_meta shape,
+                             const akh_cross_entropy_meta* meta);
+
 /* Parameters of sample_token (src/nn/sampling.rs:18-25). */
 typedef struct {
   float temperature;
@@ -240,6 +268,29 @@ akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16);
  * akh_model_upload_param).  Needs head_dim 64 or 128 and dim, ffn_hidden
  * multiples of 8. */
 akh_status akh_model_set_prefill_bf16(akh_model* m, int enable);
+
+/* ---- the trainer's fused forward: src/nn/train.rs:256-275, 394-401 ------- */
+
+/* Trainer::forward over batch sequences of seq_len tokens with row_offset
+ * batching (TransformerBlock, layers.rs:551-760), the lm_head on every row
+ * and CrossEntropy (layers.rs:465-522), on the prefill kernels: one
+ * `fused_forward_graph.execute_captured()` plus `CrossEntropy::loss()`
+ * (train.rs:380-385).  Any batch; head_dim a power of two up to 128.  Runs
+ * the bf16-MFMA layers when the model has akh_model_set_prefill_bf16 on. */
+typedef struct akh_forward akh_forward;
+akh_status akh_forward_new(akh_model* m, uint32_t batch, uint32_t seq_len, akh_forward** out);
+void akh_forward_free(akh_forward* f);
+/* tokens, targets: host [batch * seq_len] (the trainer's input_tokens and
+ * cross_entropy.target_tokens).  losses (optional): host [batch * seq_len].
+ * mean_loss: CrossEntropy::loss(), the f32 mean of the row losses.  A
+ * target id >= vocab_size is AKH_E_INVALID (the reference panics). */
+akh_status akh_forward_loss(akh_forward* f, const uint32_t* tokens, const uint32_t* targets,
+                            float* losses, float* mean_loss);
+/* After akh_forward_loss: softmax probabilities of rows [row0, row0 + n)
+ * (what CROSS_ENTROPY leaves in the logits buffer), host [n, vocab]. */
+akh_status akh_forward_probs(akh_forward* f, uint32_t row0, uint32_t n, float* host);
+/* After akh_forward_loss: the last block's add_2 output, host [rows, dim]. */
+akh_status akh_forward_hidden(akh_forward* f, float* host);
 
 /* ---- checkpoints: src/nn/checkpoint.rs (format V3) ---------------------- */
 

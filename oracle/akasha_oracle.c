@@ -218,6 +218,55 @@ void ora_silu(float* x, size_t n) {
   for (size_t i = 0; i < n; ++i) x[i] = x[i] / (1.0f + expf(-x[i]));
 }
 
+/* QKV_SPLIT: cuda.rs:296-318 (no CPU twin). */
+void ora_qkv_split(const float* src, float* q, float* k, float* v, uint32_t seq_len,
+                   uint32_t full_dim, uint32_t head_dim) {
+  for (uint32_t row = 0; row < seq_len; ++row)
+    for (uint32_t col = 0; col < head_dim; ++col) {
+      const float* r = src + (size_t)row * full_dim;
+      q[(size_t)row * head_dim + col] = r[col];
+      k[(size_t)row * head_dim + col] = r[head_dim + col];
+      v[(size_t)row * head_dim + col] = r[2 * head_dim + col];
+    }
+}
+
+/* ROPE_QK: cuda.rs:152-185 (no CPU twin); local positions, rows shifted by
+ * row_offset. */
+void ora_rope_qk(float* q, float* k, uint32_t seq_len, uint32_t dim, uint32_t head_dim,
+                 uint32_t row_offset) {
+  rope_rows(q + (size_t)row_offset * dim, seq_len, dim, head_dim, 0);
+  rope_rows(k + (size_t)row_offset * dim, seq_len, dim, head_dim, 0);
+}
+
+/* cpu.rs:77-82 */
+void ora_add(const float* a, const float* b, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+
+/* emit.rs:733-748 (RESIDUAL_ADD, target += source) */
+void ora_residual_add(float* target, const float* source, size_t n) {
+  for (size_t i = 0; i < n; ++i) target[i] += source[i];
+}
+
+/* cpu.rs:71-75 */
+void ora_silu_out(const float* x, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = x[i] / (1.0f + expf(-x[i]));
+}
+
+/* cpu.rs:277-306 */
+void ora_cross_entropy(float* x, const uint32_t* targets, float* losses, uint32_t vocab_size,
+                       uint32_t num_rows) {
+  for (uint32_t row = 0; row < num_rows; ++row) {
+    float* r = x + (size_t)row * vocab_size;
+    float m = -INFINITY;
+    for (uint32_t i = 0; i < vocab_size; ++i) m = fmaxf(m, r[i]);
+    float s = 0.0f;
+    for (uint32_t i = 0; i < vocab_size; ++i) s += expf(r[i] - m);
+    losses[row] = -(r[targets[row]] - m - logf(s));
+    for (uint32_t i = 0; i < vocab_size; ++i) r[i] = expf(r[i] - m) / s;
+  }
+}
+
 /* emit.rs:931-999, forward half of cpu_attention. */
 void ora_causal_attention(const float* q, const float* k, const float* v,
                           float* out, uint32_t seq_len, uint32_t dim,
@@ -443,6 +492,63 @@ int ora_session_prefill(ora_session* s, const uint32_t* tokens, uint32_t n,
   free(hidden); free(norm); free(qkv); free(q); free(k); free(v);
   free(attn); free(ffn);
   return ORA_OK;
+}
+
+/* Trainer::forward (train.rs:256-275) with TransformerBlock's node order
+ * (layers.rs:551-760): norm_1, qkv_proj, qkv_split, rope_qk and flash
+ * attention per sequence at row_offset b * seq_len, out_proj, add_1, norm_2,
+ * ffn_up, silu_out, ffn_down, add_2; then final_norm and lm_head on every
+ * row and CrossEntropy (layers.rs:465-522).  Flash attention has no CPU twin
+ * (shaders/mod.rs:422); it is restated from cpu_attention (emit.rs:931-999)
+ * as for prefill. */
+float ora_forward_train(const ora_config* c, const ora_weights* w, const uint32_t* tokens,
+                        const uint32_t* targets, uint32_t batch, uint32_t seq_len,
+                        float* losses, float* probs, float* hidden) {
+  const uint32_t d = c->dim, hd = d / c->num_heads, f = c->ffn_hidden, V = c->vocab_size;
+  const uint32_t rows = batch * seq_len;
+  const size_t rd = (size_t)rows * d;
+  float* x = (float*)malloc(4 * rd);
+  float* x1 = (float*)malloc(4 * rd);
+  float* norm = (float*)malloc(4 * rd);
+  float* qkv = (float*)malloc(4 * rd * 3);
+  float* q = (float*)malloc(4 * rd);
+  float* k = (float*)malloc(4 * rd);
+  float* v = (float*)malloc(4 * rd);
+  float* attn = (float*)malloc(4 * rd);
+  float* proj = (float*)malloc(4 * rd);
+  float* up = (float*)malloc(4 * (size_t)rows * f);
+  float* act = (float*)malloc(4 * (size_t)rows * f);
+  float* logits = (float*)malloc(4 * (size_t)rows * V);
+
+  ora_embedding(tokens, w->embedding, x, V, d, rows);
+  for (uint32_t l = 0; l < c->num_layers; ++l) {
+    ora_rmsnorm(x, w->norm_1[l], norm, rows, d, c->norm_eps);
+    ora_matmul(norm, w->qkv_proj[l], qkv, rows, 3 * d, d);
+    ora_qkv_split(qkv, q, k, v, rows, 3 * d, d);
+    for (uint32_t b = 0; b < batch; ++b) ora_rope_qk(q, k, seq_len, d, hd, b * seq_len);
+    for (uint32_t b = 0; b < batch; ++b) {
+      const size_t o = (size_t)b * seq_len * d;
+      ora_causal_attention(q + o, k + o, v + o, attn + o, seq_len, d, hd);
+    }
+    ora_matmul(attn, w->out_proj[l], proj, rows, d, d);
+    ora_add(x, proj, x1, rd);
+    ora_rmsnorm(x1, w->norm_2[l], norm, rows, d, c->norm_eps);
+    ora_matmul(norm, w->ffn_up[l], up, rows, f, d);
+    ora_silu_out(up, act, (size_t)rows * f);
+    ora_matmul(act, w->ffn_down[l], proj, rows, d, f);
+    ora_add(x1, proj, x, rd);
+  }
+  if (hidden) memcpy(hidden, x, 4 * rd);
+  ora_rmsnorm(x, w->final_norm, norm, rows, d, c->norm_eps);
+  ora_matmul(norm, w->lm_head, logits, rows, V, d);
+  ora_cross_entropy(logits, targets, losses, V, rows);
+  if (probs) memcpy(probs, logits, 4 * (size_t)rows * V);
+  /* CrossEntropy::loss (layers.rs:512-515): sequential f32 sum / len. */
+  float sum = 0.0f;
+  for (uint32_t r = 0; r < rows; ++r) sum += losses[r];
+  free(x); free(x1); free(norm); free(qkv); free(q); free(k); free(v); free(attn);
+  free(proj); free(up); free(act); free(logits);
+  return sum / (float)rows;
 }
 
 /* inference.rs:178-262 with build_decode_layer (inference_graphs.rs:339-509)

@@ -78,6 +78,34 @@ void ora_silu(float* x, size_t n);
 void ora_causal_attention(const float* q, const float* k, const float* v,
                           float* out, uint32_t seq_len, uint32_t dim,
                           uint32_t head_dim);
+/* ---- the trainer's forward shaders (src/nn/train.rs:256-275) ----------- */
+
+/* QKV_SPLIT (src/shaders/mod.rs:376-395).  The reference has no CPU twin;
+ * this follows its CUDA twin (src/shaders/cuda.rs:296-318): for row <
+ * seq_len and col < head_dim, q/k/v[row * head_dim + col] = src[row *
+ * full_dim + role * head_dim + col], role 0/1/2. */
+void ora_qkv_split(const float* src, float* q, float* k, float* v, uint32_t seq_len,
+                   uint32_t full_dim, uint32_t head_dim);
+/* ROPE_QK (src/shaders/mod.rs:139-158; no CPU twin, CUDA twin
+ * cuda.rs:152-185): RoPE on rows row_offset .. row_offset + seq_len of both
+ * q and k ([*, dim]), at local positions 0 .. seq_len - 1, with cpu.rs's
+ * angle (cpu.rs:98-100). */
+void ora_rope_qk(float* q, float* k, uint32_t seq_len, uint32_t dim, uint32_t head_dim,
+                 uint32_t row_offset);
+/* ADD (src/shaders/cpu.rs:77-82): out = a + b. */
+void ora_add(const float* a, const float* b, float* out, size_t n);
+/* RESIDUAL_ADD builtin, ops::residual_add (src/nn/ops/emit.rs:733-748):
+ * target += source.  The builtin lives in the absent wilupgu; the emitter's
+ * doc comment and binding modes (Accumulate, Input) fix the semantics. */
+void ora_residual_add(float* target, const float* source, size_t n);
+/* SILU_OUT (src/shaders/cpu.rs:71-75): out = x / (1 + e^-x). */
+void ora_silu_out(const float* x, float* out, size_t n);
+/* CROSS_ENTROPY (src/shaders/cpu.rs:277-306), in place: per row of
+ * [rows, vocab] logits, m = max (fold from -inf), s = sum of e^(x - m) (a
+ * sequential fold), losses[row] = -(x[target] - m - ln s), and x becomes
+ * the softmax probabilities e^(x - m) / s. */
+void ora_cross_entropy(float* x, const uint32_t* targets, float* losses, uint32_t vocab_size,
+                       uint32_t num_rows);
 /* src/nn/sampling.rs:83-91: first index of the maximum (strict >). */
 uint32_t ora_argmax(const float* logits, uint32_t n);
 /* sampling.rs:3-81: repetition penalty, temperature, top-k, top-p, and the
@@ -150,6 +178,17 @@ const float* ora_session_v_cache(const ora_session* s, uint32_t layer);
  * the cache holds, zeros for a fresh session), so a decode step at
  * position `len` can be timed without a long CPU prefill first. */
 void ora_session_set_len(ora_session* s, uint32_t len);
+
+/* Trainer::forward then CrossEntropy (src/nn/train.rs:256-275, 394-401;
+ * TransformerBlock, layers.rs:551-760; CrossEntropy, layers.rs:465-522) over
+ * batch sequences of seq_len tokens with row_offset batching.  Writes
+ * losses[batch * seq_len]; probs (optional) receives the CE's in-place
+ * probabilities [rows, vocab]; hidden (optional) the last block's add_2
+ * output [rows, dim].  Returns CrossEntropy::loss(), the mean loss. */
+float ora_forward_train(const ora_config* cfg, const ora_weights* w, const uint32_t* tokens,
+                        const uint32_t* targets, uint32_t batch, uint32_t seq_len,
+                        float* losses, float* probs, float* hidden);
+
 
 /* Host-thread count used by ora_matmul / ora_matmul_add (OpenMP over
  * output columns; every output element keeps its own k-ascending fold, so

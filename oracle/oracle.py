@@ -73,6 +73,14 @@ def load():
         "ora_session_v_cache": (FP, [C.c_void_p, u32]),
         "ora_set_threads": (None, [C.c_int]),
         "ora_session_set_len": (None, [C.c_void_p, u32]),
+        "ora_qkv_split": (None, [F32P, F32P, F32P, F32P, u32, u32, u32]),
+        "ora_rope_qk": (None, [F32P, F32P, u32, u32, u32, u32]),
+        "ora_add": (None, [F32P, F32P, F32P, sz]),
+        "ora_residual_add": (None, [F32P, F32P, sz]),
+        "ora_silu_out": (None, [F32P, F32P, sz]),
+        "ora_cross_entropy": (None, [F32P, U32P, F32P, u32, u32]),
+        "ora_forward_train": (f32, [C.POINTER(OraConfig), C.POINTER(OraWeights), U32P, U32P,
+                                    u32, u32, F32P, C.c_void_p, C.c_void_p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -193,6 +201,76 @@ def sample_token(logits, temperature, top_k, top_p, seen, repetition_penalty, r)
         n_seen = seen.size
     return int(load().ora_sample_token(x, x.size, float(temperature), int(top_k), float(top_p),
                                        seen, n_seen, float(repetition_penalty), float(r)))
+
+
+def qkv_split(src, seq_len, full_dim, head_dim):
+    n = seq_len * head_dim
+    q, k, v = (np.empty(n, np.float32) for _ in range(3))
+    load().ora_qkv_split(_f(src), q, k, v, seq_len, full_dim, head_dim)
+    return q, k, v
+
+
+def rope_qk(q, k, seq_len, dim, head_dim, row_offset):
+    q, k = _f(q).copy(), _f(k).copy()
+    load().ora_rope_qk(q, k, seq_len, dim, head_dim, row_offset)
+    return q, k
+
+
+def add(a, b):
+    a, b = _f(a), _f(b)
+    out = np.empty(a.size, np.float32)
+    load().ora_add(a, b, out, a.size)
+    return out
+
+
+def residual_add(target, source):
+    out, source = _f(target).copy(), _f(source)
+    load().ora_residual_add(out, source, out.size)
+    return out
+
+
+def silu_out(x):
+    x = _f(x)
+    out = np.empty(x.size, np.float32)
+    load().ora_silu_out(x, out, x.size)
+    return out
+
+
+def cross_entropy(logits, targets, vocab_size, num_rows):
+    """(probs, losses): CROSS_ENTROPY's in-place probabilities and the losses."""
+    x = _f(logits).copy()
+    losses = np.empty(num_rows, np.float32)
+    load().ora_cross_entropy(x, np.ascontiguousarray(targets, np.uint32), losses, vocab_size,
+                             num_rows)
+    return x, losses
+
+
+def forward_train(cfg, weights, tokens, targets, batch, seq_len, want_probs=False,
+                  want_hidden=False):
+    """Trainer::forward + CrossEntropy: (mean_loss, losses, probs, hidden)."""
+    lib = load()
+    ws = [_f(w).reshape(-1) for w in weights]
+    L = cfg.num_layers
+
+    def fp(a):
+        return a.ctypes.data_as(FP)
+
+    per = [[ws[1 + 6 * l + j] for l in range(L)] for j in range(6)]
+    arrs = [(FP * L)(*[fp(a) for a in per[j]]) for j in range(6)]
+    w = OraWeights(fp(ws[0]), *arrs, fp(ws[1 + 6 * L]), fp(ws[2 + 6 * L]))
+    c = OraConfig(cfg.vocab_size, cfg.dim, cfg.num_heads, cfg.num_layers, cfg.ffn_hidden,
+                  cfg.norm_eps, cfg.eos_token)
+    rows = batch * seq_len
+    losses = np.empty(rows, np.float32)
+    probs = np.empty((rows, cfg.vocab_size), np.float32) if want_probs else None
+    hidden = np.empty((rows, cfg.dim), np.float32) if want_hidden else None
+    mean = lib.ora_forward_train(C.byref(c), C.byref(w),
+                                 np.ascontiguousarray(tokens, np.uint32).reshape(-1),
+                                 np.ascontiguousarray(targets, np.uint32).reshape(-1),
+                                 batch, seq_len, losses,
+                                 probs.ctypes.data if probs is not None else None,
+                                 hidden.ctypes.data if hidden is not None else None)
+    return float(mean), losses, probs, hidden
 
 
 def set_threads(n: int):

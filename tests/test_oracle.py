@@ -341,3 +341,80 @@ def test_matmul_threads_do_not_change_results(ora):
     r4 = ora.matmul(a, b, m, n, k)
     ora.set_threads(1)
     assert np.array_equal(r1, r4)
+
+
+# ---- the trainer's forward (src/nn/train.rs:256-275) ----------------------
+
+def test_qkv_split_slices_columns(ora):
+    rows, d = 5, 12
+    src = ora.rand_vec(rows * 3 * d, 3).reshape(rows, 3 * d)
+    q, k, v = ora.qkv_split(src, rows, 3 * d, d)
+    for i, part in enumerate((q, k, v)):
+        assert np.array_equal(part.reshape(rows, d), src[:, i * d:(i + 1) * d])
+
+
+def test_rope_qk_is_rope_at_local_positions(ora):
+    S, d, hd, off = 6, 16, 8, 4
+    q, k = ora.rand_vec((off + S + 2) * d, 4), ora.rand_vec((off + S + 2) * d, 5)
+    rq, rk = ora.rope_qk(q, k, S, d, hd, off)
+    for x, rx in ((q, rq), (k, rk)):
+        x, rx = x.reshape(-1, d), rx.reshape(-1, d)
+        # rows of the window rotate as rope's rows 0.. do; the others stay
+        np.testing.assert_array_equal(rx[off:off + S], ora.rope(x[off:off + S], S, d, hd).reshape(S, d))
+        np.testing.assert_array_equal(rx[:off], x[:off])
+        np.testing.assert_array_equal(rx[off + S:], x[off + S:])
+
+
+def test_add_residual_add_silu_out_closed_forms(ora):
+    a, b = ora.rand_vec(300, 6), ora.rand_vec(300, 7)
+    assert np.array_equal(ora.add(a, b), a + b)
+    assert np.array_equal(ora.residual_add(a, b), a + b)
+    x = (a * 8).astype(np.float32)
+    np.testing.assert_allclose(ora.silu_out(x), x / (1 + np.exp(-x.astype(np.float64))), rtol=2e-6)
+
+
+def test_cross_entropy_against_float64_log_softmax(ora):
+    rows, V = 7, 1000
+    x = (ora.rand_vec(rows * V, 8) * 6).astype(np.float32)
+    t = ora.rand_tokens(rows, V, 9)
+    probs, losses = ora.cross_entropy(x, t, V, rows)
+    x64 = x.reshape(rows, V).astype(np.float64)
+    lse = np.log(np.exp(x64 - x64.max(1, keepdims=True)).sum(1)) + x64.max(1)
+    np.testing.assert_allclose(losses, lse - x64[np.arange(rows), t], atol=2e-5)
+    np.testing.assert_allclose(probs.reshape(rows, V), np.exp(x64 - lse[:, None]), atol=1e-7)
+    # Known answer: equal logits give loss ln V and probabilities 1 / V.
+    p, l = ora.cross_entropy(np.full(2 * 50, 3.0, np.float32), [0, 49], 50, 2)
+    np.testing.assert_allclose(l, np.log(50), rtol=1e-6)
+    np.testing.assert_allclose(p, 1 / 50, rtol=1e-6)
+
+
+def test_forward_train_batching_and_prefill_agree(pkg, ora):
+    # real_batching_matches_sequential_accumulation's shapes (train.rs:852-860):
+    # ModelConfig::new(37, 16, 4, 2, 11), batch 3, token LCG seeds 100+b / 200+b.
+    cfg = pkg.ModelConfig.new(37, 16, 4, 2, 11)
+    w = pkg.synthetic_weights(cfg, seed=3)
+    B, S = 3, 11
+    toks = np.stack([ora.rand_tokens(S, 37, 100 + b) for b in range(B)])
+    tgts = np.stack([ora.rand_tokens(S, 37, 200 + b) for b in range(B)])
+    mean, losses, probs, hidden = ora.forward_train(cfg, w, toks, tgts, B, S, True, True)
+    # Batched rows == each sequence alone (row_offset batching), bit for bit.
+    for b in range(B):
+        m1, l1, p1, h1 = ora.forward_train(cfg, w, toks[b], tgts[b], 1, S, True, True)
+        assert np.array_equal(l1, losses[b * S:(b + 1) * S])
+        assert np.array_equal(h1, hidden[b * S:(b + 1) * S])
+        assert np.array_equal(p1, probs[b * S:(b + 1) * S])
+    # CrossEntropy::loss is the f32 mean of the row losses.
+    acc = np.float32(0)
+    for v in losses:
+        acc = np.float32(acc + v)
+    assert mean == np.float32(acc / np.float32(B * S))
+    # The last row of each sequence is prefill's last row: probs == softmax of
+    # the session's logits, loss == -log of the target's probability.
+    for b in range(B):
+        o = ora.OracleSession(cfg, w, S)
+        lg = o.prefill(toks[b]).astype(np.float64)
+        o.close()
+        sm = np.exp(lg - lg.max())
+        sm /= sm.sum()
+        np.testing.assert_allclose(probs[b * S + S - 1], sm, atol=1e-7)
+        assert abs(losses[b * S + S - 1] + np.log(sm[tgts[b, -1]])) < 1e-5
