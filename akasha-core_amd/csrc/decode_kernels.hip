@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -386,7 +387,11 @@ __global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
 // softmax.  The waves' (max, sum, o) are merged in LDS and the split writes
 // its unnormalised o (k-quad layout, one tile per split) and (max, sum);
 // the out_proj GEMM merges the splits when it loads its A operand.
-template <int HD, int AW, int RB, int SP>
+//
+// KV16: the cache holds bfloat16 rows (a lane loads 8 bytes per row and
+// widens them); the new row is rounded to bfloat16 before it is used and
+// appended, so every step sees the cache's values.
+template <int HD, int AW, int RB, int SP, bool KV16>
 __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   constexpr int LPR = HD / 4;    // lanes per row
   constexpr int RPW = 64 / LPR;  // rows per wave per load
@@ -403,8 +408,9 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   const bool last = sp == SP - 1;
 
   const size_t hoff = (size_t)b * p.seq_stride + hh * HD + 4 * g;
-  const float* kbase = p.kc + hoff;
-  const float* vbase = p.vc + hoff;
+  using KT = typename std::conditional<KV16, uint16_t, float>::type;
+  const KT* kbase = static_cast<const KT*>(p.kc) + hoff;
+  const KT* vbase = static_cast<const KT*>(p.vc) + hoff;
 
   // This split's share of the cached rows 0..pos-1, divided over the waves.
   const int per = (pos + SP - 1) / SP;
@@ -414,7 +420,9 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
 
   // The first row batch is requested before the new token's q, k, v, so the
   // two memory round trips overlap.
-  float4 kv[RB], vv[RB];
+  // Rows are held as loaded (bfloat16 pairs stay packed until used).
+  using Raw = typename std::conditional<KV16, uint2, float4>::type;
+  Raw kv[RB], vv[RB];
   bool ok[RB];
   auto load_batch = [&](int base) {
 #pragma unroll
@@ -422,11 +430,15 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
       const int r = base + i * RPW + rl;
       ok[i] = r < r1;
       const size_t off = (size_t)(ok[i] ? r : r0) * d;
-      kv[i] = ok[i] ? *reinterpret_cast<const float4*>(kbase + off)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
-      vv[i] = ok[i] ? *reinterpret_cast<const float4*>(vbase + off)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      kv[i] = ok[i] ? *reinterpret_cast<const Raw*>(kbase + off) : Raw{};
+      vv[i] = ok[i] ? *reinterpret_cast<const Raw*>(vbase + off) : Raw{};
     }
+  };
+  auto wide = [](const Raw& x) -> float4 {
+    if constexpr (KV16)
+      return bf16x4(x.x, x.y);
+    else
+      return x;
   };
   load_batch(r0);
   asm volatile("" ::: "memory");
@@ -449,9 +461,18 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     rope_pair(kn.x, kn.y, c0.x, c0.y);
     rope_pair(kn.z, kn.w, c1.x, c1.y);
   }
-  if (last && wave == 0 && rl == 0) {
-    *reinterpret_cast<float4*>(p.kc + hoff + (size_t)pos * d) = kn;
-    *reinterpret_cast<float4*>(p.vc + hoff + (size_t)pos * d) = vn;
+  if constexpr (KV16) {
+    const uint2 ku = make_uint2(pack_bf16x2(kn.x, kn.y), pack_bf16x2(kn.z, kn.w));
+    const uint2 vu = make_uint2(pack_bf16x2(vn.x, vn.y), pack_bf16x2(vn.z, vn.w));
+    kn = bf16x4(ku.x, ku.y);
+    vn = bf16x4(vu.x, vu.y);
+    if (last && wave == 0 && rl == 0) {
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.kc) + hoff + (size_t)pos * d) = ku;
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.vc) + hoff + (size_t)pos * d) = vu;
+    }
+  } else if (last && wave == 0 && rl == 0) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p.kc) + hoff + (size_t)pos * d) = kn;
+    *reinterpret_cast<float4*>(static_cast<float*>(p.vc) + hoff + (size_t)pos * d) = vn;
   }
 
   float m = -INFINITY, l = 0.f;
@@ -471,7 +492,8 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     float t[RB];
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
-      float s = q4.x * kv[i].x + q4.y * kv[i].y + q4.z * kv[i].z + q4.w * kv[i].w;
+      const float4 kk = wide(kv[i]);
+      float s = q4.x * kk.x + q4.y * kk.y + q4.z * kk.z + q4.w * kk.w;
 #pragma unroll
       for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
       t[i] = ok[i] ? s * p.scale : -INFINITY;
@@ -488,11 +510,12 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
       const float e = ok[i] ? expf(t[i] - mn) : 0.f;
+      const float4 vw = wide(vv[i]);
       ps += e;
-      pv.x += e * vv[i].x;
-      pv.y += e * vv[i].y;
-      pv.z += e * vv[i].z;
-      pv.w += e * vv[i].w;
+      pv.x += e * vw.x;
+      pv.y += e * vw.y;
+      pv.z += e * vw.z;
+      pv.w += e * vw.w;
     }
     l = l * corr + ps;
     acc.x = acc.x * corr + pv.x;
@@ -842,16 +865,53 @@ int dec_attn_splits() { return AttnCfg::SP; }
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
                            hipStream_t s) {
   constexpr int AW = AttnCfg::AW, RB = AttnCfg::RB, SP = AttnCfg::SP;
+  // Row groups in flight for a bfloat16 cache (config 5: 8 beat 16, 24, 32).
+#ifndef AKH_ATTN_KV16_RB
+#define AKH_ATTN_KV16_RB RB
+#endif
+  constexpr int RB16 = AKH_ATTN_KV16_RB;
   dim3 g(batch * p.H * SP), b(64 * AW);
+#define AKH_ATTN(HD)                                                               \
+  if (p.kv16)                                                                      \
+    hipLaunchKernelGGL((k_dec_attn<HD, AW, RB16, SP, true>), g, b, 0, s, p);      \
+  else                                                                             \
+    hipLaunchKernelGGL((k_dec_attn<HD, AW, RB, SP, false>), g, b, 0, s, p);
   switch (hd) {
-    case 4: hipLaunchKernelGGL((k_dec_attn<4, AW, RB, SP>), g, b, 0, s, p); break;
-    case 8: hipLaunchKernelGGL((k_dec_attn<8, AW, RB, SP>), g, b, 0, s, p); break;
-    case 16: hipLaunchKernelGGL((k_dec_attn<16, AW, RB, SP>), g, b, 0, s, p); break;
-    case 32: hipLaunchKernelGGL((k_dec_attn<32, AW, RB, SP>), g, b, 0, s, p); break;
-    case 64: hipLaunchKernelGGL((k_dec_attn<64, AW, RB, SP>), g, b, 0, s, p); break;
-    case 128: hipLaunchKernelGGL((k_dec_attn<128, AW, RB, SP>), g, b, 0, s, p); break;
+    case 4: AKH_ATTN(4) break;
+    case 8: AKH_ATTN(8) break;
+    case 16: AKH_ATTN(16) break;
+    case 32: AKH_ATTN(32) break;
+    case 64: AKH_ATTN(64) break;
+    case 128: AKH_ATTN(128) break;
     default: return hipErrorInvalidValue;
   }
+#undef AKH_ATTN
+  return hipGetLastError();
+}
+
+// Prefill's fp32 K/V rows into a bfloat16 cache, four elements per thread.
+__global__ void k_kv_store_bf16(const float* __restrict__ k, const float* __restrict__ v,
+                                uint16_t* kc, uint16_t* vc, int S, int d, long seq_stride,
+                                size_t n4) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t row = i / (d / 4), c = (i % (d / 4)) * 4;
+    const size_t b = row / S, t = row % S;
+    const size_t dst = b * seq_stride + t * d + c;
+    const float4 a = *reinterpret_cast<const float4*>(k + row * d + c);
+    const float4 e = *reinterpret_cast<const float4*>(v + row * d + c);
+    *reinterpret_cast<uint2*>(kc + dst) = make_uint2(pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w));
+    *reinterpret_cast<uint2*>(vc + dst) = make_uint2(pack_bf16x2(e.x, e.y), pack_bf16x2(e.z, e.w));
+  }
+}
+
+hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
+                                int batch, int S, int d, long seq_stride, hipStream_t s) {
+  if (d % 4 != 0) return hipErrorInvalidValue;
+  const size_t n4 = (size_t)batch * S * (d / 4);
+  const size_t blocks = std::min<size_t>((n4 + 255) / 256, 65535u * 16u);
+  hipLaunchKernelGGL(k_kv_store_bf16, dim3((unsigned)std::max<size_t>(1, blocks)), dim3(256), 0,
+                     s, k, v, kc, vc, S, d, seq_stride, n4);
   return hipGetLastError();
 }
 

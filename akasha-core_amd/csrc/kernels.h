@@ -209,8 +209,9 @@ struct DecAttnParams {
   const float* qkv;  // nparts partial tiles [nparts][32][3*d]
   int nparts;
   const float2* rope;  // [max_ctx, head_dim / 2] (cos, sin)
-  float* kc;         // sequence b at kc + b * seq_stride, rows of d
-  float* vc;
+  void* kc;          // sequence b at kc + b * seq_stride, rows of d elements
+  void* vc;          // (float, or bfloat16 when kv16)
+  int kv16;
   float* out_t;      // per split, unnormalised o in k-quad [splits][d/4][32][4]
   float2* ml;        // per split (max, sum) [splits][H][32]
   const int* pos;    // position of the new token of each sequence
@@ -222,6 +223,10 @@ struct DecAttnParams {
 
 // Splits per (sequence, head): the partial states the out_proj GEMM merges.
 int dec_attn_splits();
+// Prefill rows k, v [batch * S, d] (fp32) into a bfloat16 KV cache
+// (sequence b at b * seq_stride, row t at t * d).
+hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
+                                int batch, int S, int d, long seq_stride, hipStream_t s);
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
                            hipStream_t s);
 

@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <string>
+#include <cstring>
 #include <vector>
 
 #include "akasha_hip.h"
@@ -863,11 +864,17 @@ struct akh_session {
   akh_sampling gparams{};
   uint32_t gmax_new = 0;
 
+  // KV cache: [L][K,V][B][max_ctx][d] elements, fp32 or (kv16) bfloat16.
+  bool kv16 = false;
+  float *pk = nullptr, *pv = nullptr;  // kv16 prefill: K/V rows in fp32 [rows, d]
+  size_t kv_elem() const { return kv16 ? 2 : 4; }
   size_t layer_stride() const { return (size_t)2 * B * max_ctx * m->cfg.dim; }
-  float* kcache(uint32_t l) { return kv + l * layer_stride(); }
-  float* vcache(uint32_t l) {
-    return kv + l * layer_stride() + (size_t)B * max_ctx * m->cfg.dim;
+  void* kv_at(uint32_t l, int which) {
+    const size_t e = l * layer_stride() + (size_t)which * B * max_ctx * m->cfg.dim;
+    return reinterpret_cast<char*>(kv) + e * kv_elem();
   }
+  float* kcache(uint32_t l) { return static_cast<float*>(kv_at(l, 0)); }  // fp32 caches
+  float* vcache(uint32_t l) { return static_cast<float*>(kv_at(l, 1)); }
   long seq_stride() const { return (long)max_ctx * m->cfg.dim; }
 };
 
@@ -878,10 +885,10 @@ int lm_parts(const akh_session* s) {
 }
 
 void free_prefill(akh_session* s) {
-  for (float* p : {s->px, s->pxn, s->pq, s->pattn, s->pffn})
+  for (float* p : {s->px, s->pxn, s->pq, s->pattn, s->pffn, s->pk, s->pv})
     if (p) hipFree(p);
   if (s->ptok) hipFree(s->ptok);
-  s->px = s->pxn = s->pq = s->pattn = s->pffn = nullptr;
+  s->px = s->pxn = s->pq = s->pattn = s->pffn = s->pk = s->pv = nullptr;
   s->ptok = nullptr;
   s->prows = 0;
 }
@@ -896,6 +903,10 @@ akh_status ensure_prefill(akh_session* s, size_t rows) {
   HIP_TRY(hipMalloc(&s->pattn, rows * d * 4));
   HIP_TRY(hipMalloc(&s->pffn, rows * F * 4));
   HIP_TRY(hipMalloc(&s->ptok, rows * 4));
+  if (s->kv16) {
+    HIP_TRY(hipMalloc(&s->pk, rows * d * 4));
+    HIP_TRY(hipMalloc(&s->pv, rows * d * 4));
+  }
   s->prows = rows;
   return AKH_OK;
 }
@@ -960,8 +971,9 @@ hipError_t enqueue_attn(akh_session* s, uint32_t l) {
   p.qkv = s->p_qkv;
   p.nparts = s->ks_qkv;
   p.rope = s->rope;
-  p.kc = s->kcache(l);
-  p.vc = s->vcache(l);
+  p.kc = s->kv_at(l, 0);
+  p.vc = s->kv_at(l, 1);
+  p.kv16 = s->kv16 ? 1 : 0;
   p.out_t = s->attn_t;
   p.ml = s->attn_ml;
   p.active = s->active;
@@ -1346,22 +1358,28 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     g.N = 3 * d;
     g.K = d;
     g.q_out = s->pq;
-    g.kcache = s->kcache(l);
-    g.vcache = s->vcache(l);
-    g.seq_stride = s->seq_stride();
+    // With a bfloat16 cache, K and V go to fp32 rows for this prompt's
+    // attention and are stored into the cache after it.
+    g.kcache = s->kv16 ? s->pk : s->kcache(l);
+    g.vcache = s->kv16 ? s->pv : s->vcache(l);
+    g.seq_stride = s->kv16 ? (long)S * d : s->seq_stride();
     g.S = (int)S;
     g.rope = s->rope;
     g.dim = d;
     g.head_dim = hd;
     TRY_HIP(launch_gemm(g, GEMM_QKV, st));
+    if (s->kv16)
+      TRY_HIP(launch_kv_store_bf16(s->pk, s->pv, static_cast<uint16_t*>(s->kv_at(l, 0)),
+                                   static_cast<uint16_t*>(s->kv_at(l, 1)), (int)s->B, (int)S,
+                                   (int)d, s->seq_stride(), st));
 
     FlashParams f{};
     f.q = s->pq;
-    f.k = s->kcache(l);
-    f.v = s->vcache(l);
+    f.k = g.kcache;
+    f.v = g.vcache;
     f.o = s->pattn;
     f.q_bs = (long)S * d;
-    f.kv_bs = s->seq_stride();
+    f.kv_bs = g.seq_stride;
     f.o_bs = (long)S * d;
     f.S = (int)S;
     f.d = (int)d;
@@ -1428,22 +1446,29 @@ hipError_t prefill_layers_bf16(akh_session* s, uint32_t S) {
     g.N = 3 * d;
     g.K = d;
     g.q_out = s->pq;
-    g.kcache = s->kcache(l);
-    g.vcache = s->vcache(l);
-    g.seq_stride = s->seq_stride();
+    // With a bfloat16 cache, K and V go to fp32 rows for this prompt's
+    // attention and are stored into the cache after it.
+    g.kcache = s->kv16 ? s->pk : s->kcache(l);
+    g.vcache = s->kv16 ? s->pv : s->vcache(l);
+    g.seq_stride = s->kv16 ? (long)S * d : s->seq_stride();
     g.S = (int)S;
     g.rope = s->rope;
     g.dim = d;
     g.head_dim = hd;
     if ((e = launch_gemm_bf16(g, GEMM_QKV, st)) != hipSuccess) return e;
+    if (s->kv16 &&
+        (e = launch_kv_store_bf16(s->pk, s->pv, static_cast<uint16_t*>(s->kv_at(l, 0)),
+                                  static_cast<uint16_t*>(s->kv_at(l, 1)), (int)s->B, (int)S,
+                                  (int)d, s->seq_stride(), st)) != hipSuccess)
+      return e;
 
     FlashParams f{};
     f.q = s->pq;
-    f.k = s->kcache(l);
-    f.v = s->vcache(l);
+    f.k = g.kcache;
+    f.v = g.vcache;
     f.o16 = attn16;
     f.q_bs = (long)S * d;
-    f.kv_bs = s->seq_stride();
+    f.kv_bs = g.seq_stride;
     f.o_bs = (long)S * d;
     f.S = (int)S;
     f.d = (int)d;
@@ -1697,6 +1722,80 @@ extern "C" akh_status akh_session_generate(akh_session* s, const uint32_t* token
   return set_active(s, true);
 }
 
+namespace {
+
+// One sequence's [max_ctx, d] rows of layer l, K (which 0) or V (1), to or
+// from host fp32, widening or rounding (to nearest even) a bfloat16 cache.
+akh_status cache_rows_out(akh_session* s, uint32_t l, int which, uint32_t seq, float* host) {
+  const size_t n = (size_t)s->seq_stride();
+  const char* src = static_cast<const char*>(s->kv_at(l, which)) + seq * n * s->kv_elem();
+  if (!s->kv16) {
+    HIP_TRY(hipMemcpyAsync(host, src, n * 4, hipMemcpyDeviceToHost, s->be->stream));
+    HIP_TRY(hipStreamSynchronize(s->be->stream));
+    return AKH_OK;
+  }
+  std::vector<uint16_t> t(n);
+  HIP_TRY(hipMemcpyAsync(t.data(), src, n * 2, hipMemcpyDeviceToHost, s->be->stream));
+  HIP_TRY(hipStreamSynchronize(s->be->stream));
+  for (size_t i = 0; i < n; ++i) {
+    const uint32_t u = (uint32_t)t[i] << 16;
+    std::memcpy(host + i, &u, 4);
+  }
+  return AKH_OK;
+}
+
+akh_status cache_rows_in(akh_session* s, uint32_t l, int which, uint32_t seq, const float* host) {
+  const size_t n = (size_t)s->seq_stride();
+  char* dst = static_cast<char*>(s->kv_at(l, which)) + seq * n * s->kv_elem();
+  if (!s->kv16) {
+    HIP_TRY(hipMemcpyAsync(dst, host, n * 4, hipMemcpyHostToDevice, s->be->stream));
+    HIP_TRY(hipStreamSynchronize(s->be->stream));
+    return AKH_OK;
+  }
+  std::vector<uint16_t> t(n);
+  for (size_t i = 0; i < n; ++i) {
+    uint32_t u;
+    std::memcpy(&u, host + i, 4);
+    t[i] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+  }
+  HIP_TRY(hipMemcpyAsync(dst, t.data(), n * 2, hipMemcpyHostToDevice, s->be->stream));
+  HIP_TRY(hipStreamSynchronize(s->be->stream));
+  return AKH_OK;
+}
+
+}  // namespace
+
+extern "C" akh_status akh_session_set_kv_bf16(akh_session* s, int enable) {
+  CHECK_ARG(s && (enable == 0 || enable == 1), "akh_session_set_kv_bf16: bad argument");
+  CHECK_ARG(!s->be->capturing, "akh_session_set_kv_bf16: graph capture in progress");
+  for (uint32_t b = 0; b < s->B; ++b)
+    if (s->cur_len[b] != 0)
+      return fail(AKH_E_CACHE_NOT_EMPTY, "akh_session_set_kv_bf16 needs empty caches, sequence " +
+                                             std::to_string(b) + " holds " +
+                                             std::to_string(s->cur_len[b]) + " tokens");
+  if ((enable != 0) == s->kv16) return AKH_OK;
+  const akh_model_config& c = s->m->cfg;
+  const size_t elems = (size_t)c.num_layers * s->layer_stride();
+  HIP_TRY(hipSetDevice(s->be->device));
+  HIP_TRY(hipStreamSynchronize(s->be->stream));
+  // Graphs hold the attention kernel of the old element type.
+  if (s->gexec) hipGraphExecDestroy(s->gexec);
+  if (s->graph) hipGraphDestroy(s->graph);
+  if (s->ggexec) hipGraphExecDestroy(s->ggexec);
+  if (s->ggraph) hipGraphDestroy(s->ggraph);
+  s->gexec = nullptr;
+  s->graph = nullptr;
+  s->ggexec = nullptr;
+  s->ggraph = nullptr;
+  free_prefill(s);
+  HIP_TRY(hipFree(s->kv));
+  s->kv = nullptr;
+  s->kv16 = enable != 0;
+  HIP_TRY(hipMalloc(&s->kv, elems * s->kv_elem()));
+  HIP_TRY(hipMemset(s->kv, 0, elems * s->kv_elem()));
+  return AKH_OK;
+}
+
 extern "C" akh_status akh_session_take_cache(akh_session* s, uint32_t seq, float* k,
                                              float* v, uint32_t* cur_len, int* had_cache) {
   CHECK_ARG(s && seq < s->B, "akh_session_take_cache: bad argument");
@@ -1706,14 +1805,10 @@ extern "C" akh_status akh_session_take_cache(akh_session* s, uint32_t seq, float
   if (!had) return AKH_OK;
   const size_t n = (size_t)s->seq_stride();
   for (uint32_t l = 0; l < s->m->cfg.num_layers; ++l) {
-    if (k)
-      HIP_TRY(hipMemcpyAsync(k + l * n, s->kcache(l) + (size_t)seq * n, n * sizeof(float),
-                             hipMemcpyDeviceToHost, s->be->stream));
-    if (v)
-      HIP_TRY(hipMemcpyAsync(v + l * n, s->vcache(l) + (size_t)seq * n, n * sizeof(float),
-                             hipMemcpyDeviceToHost, s->be->stream));
+    akh_status st = k ? cache_rows_out(s, l, 0, seq, k + l * n) : AKH_OK;
+    if (st == AKH_OK && v) st = cache_rows_out(s, l, 1, seq, v + l * n);
+    if (st != AKH_OK) return st;
   }
-  HIP_TRY(hipStreamSynchronize(s->be->stream));
   s->has_cache[seq] = 0;
   s->cur_len[seq] = 0;
   return upload_positions(s);
@@ -1726,10 +1821,9 @@ extern "C" akh_status akh_session_replace_cache(akh_session* s, uint32_t seq, co
   const size_t n = (size_t)s->seq_stride();
   hipStream_t st = s->be->stream;
   for (uint32_t l = 0; l < s->m->cfg.num_layers; ++l) {
-    HIP_TRY(hipMemcpyAsync(s->kcache(l) + (size_t)seq * n, k + l * n, n * sizeof(float),
-                           hipMemcpyHostToDevice, st));
-    HIP_TRY(hipMemcpyAsync(s->vcache(l) + (size_t)seq * n, v + l * n, n * sizeof(float),
-                           hipMemcpyHostToDevice, st));
+    akh_status cs = cache_rows_in(s, l, 0, seq, k + l * n);
+    if (cs == AKH_OK) cs = cache_rows_in(s, l, 1, seq, v + l * n);
+    if (cs != AKH_OK) return cs;
   }
   // The installed cache carries no token history.
   HIP_TRY(hipMemsetAsync(s->hist + (size_t)seq * (s->max_ctx + 1), 0,
@@ -1746,10 +1840,7 @@ extern "C" akh_status akh_session_download_cache(akh_session* s,
   CHECK_ARG(s && host && layer < s->m->cfg.num_layers && seq < s->B &&
                 (which == 0 || which == 1),
             "akh_session_download_cache: bad argument");
-  const float* src = (which == 0 ? s->kcache(layer) : s->vcache(layer)) +
-                     (size_t)seq * s->seq_stride();
-  return akh_tensor_download(s->be, host, src,
-                             (size_t)s->seq_stride() * sizeof(float));
+  return cache_rows_out(s, layer, which, seq, host);
 }
 
 extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,

@@ -217,6 +217,7 @@ _SIGS = {
     "akh_session_generate": (ST, [P, P, U32, U32, Sampling, P, P, P]),
     "akh_session_truncate": (ST, [P, U32]),
     "akh_session_set_len": (ST, [P, U32]),
+    "akh_session_set_kv_bf16": (ST, [P, C.c_int]),
     "akh_session_take_cache": (ST, [P, U32, P, P, C.POINTER(U32), C.POINTER(C.c_int)]),
     "akh_session_replace_cache": (ST, [P, U32, P, P, U32]),
     "akh_session_download_cache": (ST, [P, U32, U32, C.c_int, P]),
@@ -676,6 +677,10 @@ class Session:
     def set_len(self, length: int):
         """Cache::cur_len = length for every sequence (rows untouched)."""
         _check(_lib.akh_session_set_len(self.handle, length), "set_len")
+
+    def set_kv_bf16(self, enable: bool):
+        """bfloat16 KV cache (the optional bf16 path); caches must be empty."""
+        _check(_lib.akh_session_set_kv_bf16(self.handle, 1 if enable else 0), "set_kv_bf16")
 
     def take_cache(self, seq: int):
         """take_cache for one sequence: (k, v, cur_len) or None if it had none."""

@@ -108,6 +108,23 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True):
            "decode_tok_s": round(64 * steps / (ms / 1e3), 1),
            "decode_hbm_frac": round(step_bytes / (ms / steps / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
            "bytes_per_step": int(step_bytes)}
+    # The optional bfloat16 KV cache: half the KV bytes, the same schedule.
+    for s in sess:
+        s.set_len(0)
+        s.set_kv_bf16(True)
+        s.set_len(T - steps)
+        s.decode_greedy(1, want_tokens=False)
+        s.set_len(T - steps)
+    be.synchronize()
+    be.timer_start()
+    for s in sess:
+        s.decode_greedy(steps, want_tokens=False)
+    kms = be.timer_stop()
+    kv16_bytes = (2 * weights * steps + kv / 2) / steps
+    out.update({"decode_kv16_ms_per_step": round(kms / steps, 3),
+                "decode_kv16_tok_s": round(64 * steps / (kms / 1e3), 1),
+                "decode_kv16_hbm_frac": round(kv16_bytes / (kms / steps / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                "decode_kv16_bytes_per_step": int(kv16_bytes)})
     for s in sess:
         s.close()
     if with_prefill:

@@ -369,6 +369,13 @@ akh_status akh_session_generate(akh_session* s, const uint32_t* tokens,
  * (inference_graphs.rs:515); rows below `len` keep whatever they hold.  Used
  * to time decode at a given context length. */
 akh_status akh_session_set_len(akh_session* s, uint32_t len);
+/* No reference counterpart (the reference's Cache is f32): with enable = 1
+ * the session's KV cache holds bfloat16 rows (rounded to nearest even),
+ * half the bytes decode attention streams; decode still computes in f32.
+ * Part of the optional bf16 path: logits track the f32 path within 2e-2.
+ * Needs every cache empty (AKH_E_CACHE_NOT_EMPTY otherwise); take_cache,
+ * replace_cache and download_cache convert to and from f32. */
+akh_status akh_session_set_kv_bf16(akh_session* s, int enable);
 /* Shorten every sequence to `len` cached tokens (len <= min cur_len); the
  * rows below `len` are kept.  Used to replay a timed decode window. */
 akh_status akh_session_truncate(akh_session* s, uint32_t len);

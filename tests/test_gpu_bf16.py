@@ -98,3 +98,87 @@ def test_bf16_prefill_rejects_unsupported_heads(backend, pkg):
     model = pkg.hip.Model(backend, cfg)
     with pytest.raises(pkg.hip.InvalidArgument, match="head_dim 64 or 128"):
         model.set_prefill_bf16(True)
+
+
+# ---- the bfloat16 KV cache (akh_session_set_kv_bf16) ----------------------
+
+def test_kv_bf16_decode_tracks_oracle(backend, pkg, ora):
+    cfg = pkg.ModelConfig.new(300, 256, 4, 2, 80)
+    w = pkg.synthetic_weights(cfg, seed=55)
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    s = pkg.hip.Session(model, 80, 2)
+    s.set_kv_bf16(True)
+    toks = pkg.synthetic_tokens(2 * 60, cfg.vocab_size, seed=56).reshape(2, 60)
+    logits, nxt = s.prefill(toks)
+    steps = []
+    feed = nxt
+    for _ in range(5):
+        lg, nx = s.decode_step(feed)
+        steps.append((lg, feed.copy()))
+        feed = nx
+    for b in range(2):
+        o = ora.OracleSession(cfg, w, 80)
+        # Prefill's own attention used f32 K/V: its logits meet the f32 bar.
+        assert np.abs(logits[b] - o.prefill(toks[b])).max() < 1e-3
+        # The cache holds the oracle's rows rounded to bfloat16.
+        ref = o.k_cache(1)[:60]
+        got = s.cache(1, b, 0)[:60]
+        assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6)
+        for i, (lg, fed) in enumerate(steps):
+            _check_logits(lg[b], o.decode_step(int(fed[b])), ora, f"sequence {b} step {i}")
+        o.close()
+
+
+def test_kv_bf16_cache_hand_over_and_errors(backend, pkg):
+    hip = pkg.hip
+    cfg = pkg.ModelConfig.new(97, 64, 1, 2, 16)
+    w = pkg.synthetic_weights(cfg, seed=57)
+    model = hip.Model(backend, cfg)
+    model.upload(w)
+    a = hip.Session(model, 16, 2)
+    a.set_kv_bf16(True)
+    a.prefill(np.array([[3, 41, 7, 9], [11, 12, 13, 14]], np.uint32))
+    with pytest.raises(hip.CacheNotEmpty):
+        a.set_kv_bf16(False)
+    k, v, n = a.take_cache(1)
+    assert n == 4
+    # Values come back widened from bfloat16: low 16 bits zero.
+    assert not np.any(k.view(np.uint32) & 0xFFFF)
+    b = hip.Session(model, 16, 2)
+    b.set_kv_bf16(True)
+    b.replace_cache(0, k, v, n)
+    assert np.array_equal(b.cache(1, 0, 1), v[1])
+    # An f32 session takes the same cache exactly.
+    c = hip.Session(model, 16, 2)
+    c.replace_cache(1, k, v, n)
+    assert np.array_equal(c.cache(0, 1, 0), k[0])
+
+
+def test_kv_bf16_scaled_config(backend, pkg, ora):
+    # Config 5's optional bf16 path end to end: bf16-MFMA prefill, bfloat16
+    # KV cache, f32 decode; two 24-token prompts and 3 decode steps.
+    cfg = pkg.ModelConfig.scaled()
+    w = pkg.synthetic_weights(cfg, seed=5, bf16=True)
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    model.set_prefill_bf16(True)
+    s = pkg.hip.Session(model, 64, 2)
+    s.set_kv_bf16(True)
+    toks = pkg.synthetic_tokens(2 * 24, cfg.vocab_size, seed=6).reshape(2, 24)
+    logits, nxt = s.prefill(toks)
+    steps, feed = [], nxt
+    for _ in range(3):
+        lg, nx = s.decode_step(feed)
+        steps.append((lg, feed.copy()))
+        feed = nx
+    ora.set_threads(16)
+    try:
+        for b in range(2):
+            o = ora.OracleSession(cfg, w, 64)
+            _check_logits(logits[b], o.prefill(toks[b]), ora, f"sequence {b} prefill")
+            for i, (lg, fed) in enumerate(steps):
+                _check_logits(lg[b], o.decode_step(int(fed[b])), ora, f"sequence {b} step {i}")
+            o.close()
+    finally:
+        ora.set_threads(1)
