@@ -842,7 +842,9 @@ hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
     case DEC_CFG_QKV: return dec_go<DEC_CFG_QKV, DEC_PART, PRO_NONE>(p, s);
     case DEC_CFG_OUT: return dec_go<DEC_CFG_OUT, DEC_PART, PRO_ATTN_MERGE>(p, s);
     case DEC_CFG_UP: return dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NONE>(p, s);
-    case DEC_CFG_DOWN: return dec_go<DEC_CFG_DOWN, DEC_PART, PRO_SILU_SUM>(p, s);
+    case DEC_CFG_DOWN:
+      return p.nparts ? dec_go<DEC_CFG_DOWN, DEC_PART, PRO_SILU_SUM>(p, s)
+                      : dec_go<DEC_CFG_DOWN, DEC_PART, PRO_NONE>(p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -886,6 +888,27 @@ hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
     default: return hipErrorInvalidValue;
   }
 #undef AKH_ATTN
+  return hipGetLastError();
+}
+
+// act = silu(sum of the partial tiles), four elements per thread.
+__global__ void k_silu_sum(const float* __restrict__ parts, int nparts, float* __restrict__ act,
+                           size_t n4) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    t = sum_parts4<4>(t, parts + 4 * i, 4 * n4, nparts);
+    reinterpret_cast<float4*>(act)[i] = make_float4(silu(t.x), silu(t.y), silu(t.z), silu(t.w));
+  }
+}
+
+hipError_t launch_silu_sum(const float* parts, int nparts, float* act, size_t n,
+                           hipStream_t s) {
+  if (n % 4 != 0 || nparts < 1) return hipErrorInvalidValue;
+  const size_t n4 = n / 4;
+  const size_t blocks = std::min<size_t>((n4 + 255) / 256, 65535u * 16u);
+  hipLaunchKernelGGL(k_silu_sum, dim3((unsigned)std::max<size_t>(1, blocks)), dim3(256), 0, s,
+                     parts, nparts, act, n4);
   return hipGetLastError();
 }
 

@@ -221,6 +221,11 @@ struct DecAttnParams {
   float scale;
 };
 
+// act = silu(sum of nparts k-quad partial tiles), n elements per tile,
+// summed in split order (what PRO_SILU_SUM computes while loading A).
+hipError_t launch_silu_sum(const float* parts, int nparts, float* act, size_t n,
+                           hipStream_t s);
+
 // Splits per (sequence, head): the partial states the out_proj GEMM merges.
 int dec_attn_splits();
 // Prefill rows k, v [batch * S, d] (fp32) into a bfloat16 KV cache

@@ -831,6 +831,7 @@ struct akh_session {
   float* p_qkv = nullptr;   // [ks_qkv][32][3*dim]
   float* p_out = nullptr;   // [ks_out][32][dim]
   float* p_up = nullptr;    // [ks_up] k-quad tiles of [32, ffn]
+  float* up_act = nullptr;  // silu(ffn_up) when summed by its own kernel
   float* p_down = nullptr;  // [ks_down][32][dim]
   float* logits = nullptr;  // [32, vocab]
   uint2* amax = nullptr;    // [32, lm tiles] argmax partials
@@ -1022,12 +1023,23 @@ hipError_t enqueue_up(akh_session* s, uint32_t l) {
   return launch_dec_gemm(p, DEC_CFG_UP, s->be->stream);
 }
 
-// SiLU + ffn_down (inference_graphs.rs:495-508): partial tiles.
+// SiLU + ffn_down (inference_graphs.rs:495-508): partial tiles.  The
+// SiLU of the summed ffn_up partials is computed while down loads its A
+// operand, once per column tile of down; where that re-reads the partials
+// too often (config 5: 64 tiles x 4 splits, 268 MB of L2 reads per call)
+// one small kernel computes it first.
 hipError_t enqueue_down(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
-  p.xt = s->p_up;
-  p.nparts = s->ks_up;
+  if (s->up_act) {
+    hipError_t e = launch_silu_sum(s->p_up, s->ks_up, s->up_act, (size_t)32 * c.ffn_hidden,
+                                   s->be->stream);
+    if (e != hipSuccess) return e;
+    p.xt = s->up_act;
+  } else {
+    p.xt = s->p_up;
+    p.nparts = s->ks_up;
+  }
   use_packed(p, s->m->packed_layer(l, W_DOWN));
   p.y = s->p_down;
   p.N = c.dim;
@@ -1199,7 +1211,8 @@ extern "C" void akh_session_free(akh_session* s) {
   if (s->ggraph) hipGraphDestroy(s->ggraph);
   free_prefill(s);
   void* bufs[] = {s->kv,     s->rope,   s->xt,     s->xnt,    s->attn_t, s->attn_ml,
-                  s->p_qkv,  s->p_out,  s->p_up,   s->p_down, s->logits, s->amax,
+                  s->p_qkv,  s->p_out,  s->p_up,   s->up_act, s->p_down,
+                  s->logits, s->amax,
                   s->tok,    s->pos,    s->hist,   s->active, s->done,   s->gstart,
                   s->gcount, s->ggen,   s->guni,   s->gwbuf};
   for (void* p : bufs)
@@ -1208,6 +1221,17 @@ extern "C" void akh_session_free(akh_session* s) {
 }
 
 namespace {
+
+#ifndef AKH_SILU_KERNEL_READS
+#define AKH_SILU_KERNEL_READS 128
+#endif
+// Whether down's SiLU runs as its own kernel: when down's column tiles
+// times ffn_up's splits (partial re-reads per element) reach
+// AKH_SILU_KERNEL_READS.
+bool silu_own_kernel(const akh_session* s) {
+  const akh_model_config& c = s->m->cfg;
+  return (long)(c.dim / 32) * s->ks_up >= AKH_SILU_KERNEL_READS;
+}
 
 // A session's buffers.  With decode false only what prefill needs (KV
 // cache, RoPE table) is allocated, and the decode kernels' shape limits do
@@ -1256,6 +1280,7 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
   alloc((void**)&s->p_qkv, (size_t)s->ks_qkv * R * 3 * d * 4);
   alloc((void**)&s->p_out, (size_t)s->ks_out * R * d * 4);
   alloc((void**)&s->p_up, (size_t)s->ks_up * R * F * 4);
+  if (silu_own_kernel(s)) alloc((void**)&s->up_act, R * F * 4);
   alloc((void**)&s->p_down, (size_t)s->ks_down * R * d * 4);
   alloc((void**)&s->logits, R * V * 4);
   alloc((void**)&s->amax, R * (size_t)lm_parts(s) * sizeof(uint2));
