@@ -75,7 +75,43 @@ def prefill_flops(cfg, B, S):
     return gemm + attn + lm
 
 
-def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True):
+def scaled_decode(hip, be, model, cfg, T, steps):
+    """Config 5 decode legs: 64 sequences as two 32-row sessions, `steps`
+    steps ending at KV length T, with the f32 KV cache and then the optional
+    bfloat16 one.  The weights are bf16-valued and read as bfloat16 tiles, so
+    their algorithmic bytes are 2 per parameter (twice: one read per
+    session)."""
+    d, L, V = cfg.dim, cfg.num_layers, cfg.vocab_size
+    weights = 2 * (sum(int(np.prod(x)) for x in cfg.param_shapes()) - V * d)
+    kv = sum(2 * L * 64 * (T - steps + i + 1) * d * 4 for i in range(steps))
+    sess = [hip.Session(model, T, 32) for _ in range(2)]
+    out = {"decode_workload": f"64 sequences (2 x 32-row sessions), {steps} steps to KV length "
+                              f"{T} over a zero KV prefix (set_len)"}
+    for kv16 in (False, True):
+        for s in sess:
+            if kv16:
+                s.set_len(0)
+                s.set_kv_bf16(True)
+            s.set_len(T - steps)
+            s.decode_greedy(1, want_tokens=False)  # capture + warm
+            s.set_len(T - steps)
+        be.synchronize()
+        be.timer_start()
+        for s in sess:
+            s.decode_greedy(steps, want_tokens=False)
+        ms = be.timer_stop()
+        step_bytes = (2 * weights * steps + (kv / 2 if kv16 else kv)) / steps
+        key = "decode_kv16" if kv16 else "decode"
+        out.update({f"{key}_ms_per_step": round(ms / steps, 3),
+                    f"{key}_tok_s": round(64 * steps / (ms / 1e3), 1),
+                    f"{key}_hbm_frac": round(step_bytes / (ms / steps / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                    f"{key}_bytes_per_step": int(step_bytes)})
+    for s in sess:
+        s.close()
+    return out
+
+
+def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=True):
     """Config 5: the scaled architecture (dim 2048, 24 layers, 16 x 128, FFN
     8192, vocab 50257) with bf16-valued weights (seed 5).  Decode: 64
     sequences (two 32-row sessions) for `steps` steps ending at KV length
@@ -87,46 +123,10 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True):
     model = hip.Model(be, cfg)
     model.upload(w)
     del w
-    T = 2048
-    sess = [hip.Session(model, T, 32) for _ in range(2)]
-    for s in sess:
-        s.set_len(T - steps)
-        s.decode_greedy(1, want_tokens=False)  # capture + warm
-        s.set_len(T - steps)
-    be.synchronize()
-    be.timer_start()
-    for s in sess:
-        s.decode_greedy(steps, want_tokens=False)
-    ms = be.timer_stop()
-    d, L, V = cfg.dim, cfg.num_layers, cfg.vocab_size
-    weights = 4 * (sum(int(np.prod(x)) for x in cfg.param_shapes()) - V * d)
-    kv = sum(2 * L * 64 * (T - steps + i + 1) * d * 4 for i in range(steps))
-    step_bytes = (2 * weights * steps + kv) / steps
-    out = {"workload": "config 5: scaled architecture, bf16-valued weights (seed 5), decode of 64 "
-                       f"sequences (2 x 32-row sessions), {steps} steps to KV length 2048, fp32 KV",
-           "decode_ms_per_step": round(ms / steps, 3),
-           "decode_tok_s": round(64 * steps / (ms / 1e3), 1),
-           "decode_hbm_frac": round(step_bytes / (ms / steps / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-           "bytes_per_step": int(step_bytes)}
-    # The optional bfloat16 KV cache: half the KV bytes, the same schedule.
-    for s in sess:
-        s.set_len(0)
-        s.set_kv_bf16(True)
-        s.set_len(T - steps)
-        s.decode_greedy(1, want_tokens=False)
-        s.set_len(T - steps)
-    be.synchronize()
-    be.timer_start()
-    for s in sess:
-        s.decode_greedy(steps, want_tokens=False)
-    kms = be.timer_stop()
-    kv16_bytes = (2 * weights * steps + kv / 2) / steps
-    out.update({"decode_kv16_ms_per_step": round(kms / steps, 3),
-                "decode_kv16_tok_s": round(64 * steps / (kms / 1e3), 1),
-                "decode_kv16_hbm_frac": round(kv16_bytes / (kms / steps / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-                "decode_kv16_bytes_per_step": int(kv16_bytes)})
-    for s in sess:
-        s.close()
+    T, V = 2048, cfg.vocab_size
+    out = {"workload": "config 5: scaled architecture, bf16-valued weights (seed 5)"}
+    if with_decode:
+        out.update(scaled_decode(hip, be, model, cfg, T, steps))
     if with_prefill:
         Bp, Sp = 8, 2048
         ps = hip.Session(model, Sp, Bp)
@@ -190,6 +190,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=60)
     ap.add_argument("--scaled", action="store_true",
                     help="also measure config 5 (scaled architecture) decode and prefill")
+    ap.add_argument("--no-scaled-decode", action="store_true",
+                    help="with --scaled, measure config 5's prefill legs only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -308,7 +310,8 @@ def main():
 
     scaled = None
     if args.scaled:
-        scaled = scaled_measurement(pkg, hip, be, with_prefill=not args.no_prefill)
+        scaled = scaled_measurement(pkg, hip, be, with_prefill=not args.no_prefill,
+                                    with_decode=not args.no_scaled_decode)
 
     cpu = None
     if not args.no_cpu:
