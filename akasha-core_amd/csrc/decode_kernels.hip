@@ -819,8 +819,12 @@ int dec_gemm_splits(int role, int K, int N) {
   }
 }
 
+#ifndef AKH_LM_BLOCKS_PER_CU
+#define AKH_LM_BLOCKS_PER_CU 2  // 2 beat 1 and 3 (config 4: 34.7 us vs 39.6)
+#endif
 int dec_lm_parts(int N, int K, int num_cus) {
-  if (lm_persistent(N, K)) return std::max(1, std::min((N + 31) / 32, num_cus));
+  if (lm_persistent(N, K))
+    return std::max(1, std::min((N + 31) / 32, AKH_LM_BLOCKS_PER_CU * num_cus));
   return (N + 31) / 32;
 }
 
