@@ -41,7 +41,7 @@ hipError_t shader_flash_attention(const float* q, const float* k,
                                   const float* v, float* out, float* lse,
                                   akh_flash_attn_meta shape,
                                   const akh_flash_attn_meta* meta,
-                                  hipStream_t s);
+                                  uint32_t batch, hipStream_t s);
 hipError_t shader_attn_qk_cached(const float* q, const float* kc,
                                  float* scores, uint32_t num_heads,
                                  uint32_t max_attn_len,
@@ -105,8 +105,9 @@ struct FlashParams {
   const float* k;
   const float* v;
   float* o;
-  float* lse;              // optional [S, H]: max + ln(sum)
+  float* lse;              // optional [S, H] per sequence: max + ln(sum)
   long q_bs, kv_bs, o_bs;  // per-sequence strides (elements)
+  long lse_bs;             // per-sequence stride of lse
   int S, d, hd;
   float scale;
   const akh_flash_attn_meta* meta;  // per-shader path: S, dim, scale and

@@ -336,7 +336,8 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
       if (qrow < S) op[(size_t)qrow * d + 32 * t + c] = Os[r][c];
     }
   }
-  if (p.lse && h == 0 && qi < S) p.lse[(size_t)qi * H + hh] = mrow + logf(lrow);
+  if (p.lse && h == 0 && qi < S)
+    p.lse[(size_t)b * p.lse_bs + (size_t)qi * H + hh] = mrow + logf(lrow);
 }
 
 // Causal flash attention for the small head sizes (2..32; the reference
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
   float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD + (size_t)i * d;
 #pragma unroll
   for (int c = 0; c < HD; ++c) op[c] = acc[c] / lrow;
-  if (p.lse) p.lse[(size_t)i * H + hh] = mrow + logf(lrow);
+  if (p.lse) p.lse[(size_t)b * p.lse_bs + (size_t)i * H + hh] = mrow + logf(lrow);
 }
 
 // ---------------------------------------------------------------------------

@@ -341,7 +341,24 @@ extern "C" akh_status akh_flash_attention(akh_backend* be, const float* q,
             "flash_attention: dim must be divisible by head_dim");
   CHECK_ARG(supported_head_dim(shape.head_dim),
             "flash_attention: head_dim must be a power of two");
-  HIP_TRY(shader_flash_attention(q, k, v, out, l_cache, shape, meta, be->stream));
+  HIP_TRY(shader_flash_attention(q, k, v, out, l_cache, shape, meta, 1, be->stream));
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_flash_attention_batched(akh_backend* be, const float* q,
+                                                  const float* k, const float* v, float* out,
+                                                  float* l_cache, akh_flash_attn_meta shape,
+                                                  const akh_flash_attn_meta* meta,
+                                                  uint32_t batch) {
+  BE_CHECK(be);
+  CHECK_ARG(q && k && v && out && meta, "akh_flash_attention_batched: NULL buffer");
+  CHECK_ARG(shape.head_dim > 0 && shape.head_dim <= 128,
+            "flash_attention: head_dim must be <= 128");
+  CHECK_ARG(shape.dim % shape.head_dim == 0,
+            "flash_attention: dim must be divisible by head_dim");
+  CHECK_ARG(supported_head_dim(shape.head_dim),
+            "flash_attention: head_dim must be a power of two");
+  HIP_TRY(shader_flash_attention(q, k, v, out, l_cache, shape, meta, batch, be->stream));
   return AKH_OK;
 }
 

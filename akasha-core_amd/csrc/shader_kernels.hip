@@ -328,8 +328,8 @@ hipError_t shader_flash_attention(const float* q, const float* k,
                                   const float* v, float* out, float* lse,
                                   akh_flash_attn_meta shape,
                                   const akh_flash_attn_meta* meta,
-                                  hipStream_t s) {
-  if (shape.seq_len == 0) return hipSuccess;
+                                  uint32_t batch, hipStream_t s) {
+  if (shape.seq_len == 0 || batch == 0) return hipSuccess;
   FlashParams p{};
   p.q = q;
   p.k = k;
@@ -341,7 +341,10 @@ hipError_t shader_flash_attention(const float* q, const float* k,
   p.hd = shape.head_dim;
   p.scale = shape.scale;
   p.meta = meta;
-  return launch_flash(p, 1, shape.seq_len, s);
+  // Sequence b is the node at row_offset + b * seq_len.
+  p.q_bs = p.kv_bs = p.o_bs = (long)shape.seq_len * shape.dim;
+  p.lse_bs = (long)shape.seq_len * (shape.dim / shape.head_dim);
+  return launch_flash(p, (int)batch, shape.seq_len, s);
 }
 
 hipError_t shader_attn_qk_cached(const float* q, const float* kc,

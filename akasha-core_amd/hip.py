@@ -180,6 +180,7 @@ _SIGS = {
     "akh_rope_offset": (ST, [P, P, RopeOffsetMeta, P]),
     "akh_cache_write": (ST, [P, P, P, CacheWriteMeta, P]),
     "akh_flash_attention": (ST, [P, P, P, P, P, P, FlashAttnMeta, P]),
+    "akh_flash_attention_batched": (ST, [P, P, P, P, P, P, FlashAttnMeta, P, U32]),
     "akh_attn_qk_cached": (ST, [P, P, P, P, U32, U32, P]),
     "akh_softmax_rect": (ST, [P, P, SoftmaxRectMeta, P]),
     "akh_attn_av_cached": (ST, [P, P, P, P, U32, P]),
@@ -420,6 +421,11 @@ class Backend:
     def cache_write(self, src, cache, shape: CacheWriteMeta, meta):
         _check(_lib.akh_cache_write(self.handle, _p(src), _p(cache), shape, _p(meta)),
                "cache_write")
+
+    def flash_attention_batched(self, q, k, v, out, l_cache, shape: FlashAttnMeta, meta, batch):
+        _check(_lib.akh_flash_attention_batched(self.handle, _p(q), _p(k), _p(v), _p(out),
+                                                _p(l_cache), shape, _p(meta), batch),
+               "flash_attention_batched")
 
     def flash_attention(self, q, k, v, out, l_cache, shape: FlashAttnMeta, meta):
         _check(_lib.akh_flash_attention(self.handle, _p(q), _p(k), _p(v), _p(out),

@@ -308,6 +308,60 @@ def main():
             "mean_loss": round(mean_loss, 4), "flop": ffl}
         fw.close()
 
+    # Config 1: batch-1 greedy latency (64-token prompt, seed 1; 64 steps).
+    s1 = hip.Session(model, 128, 1)
+    p1 = pkg.synthetic_tokens(64, cfg.vocab_size, seed=1).reshape(1, 64)
+    s1.prefill(p1, want_logits=False)
+    s1.decode_greedy(8, want_tokens=False)  # capture + warm
+    s1.truncate(64)
+    be.synchronize()
+    be.timer_start()
+    s1.decode_greedy(64, want_tokens=False)
+    c1_ms = be.timer_stop()
+    s1.close()
+    c1_bytes = decode_step_bytes(cfg, 1, 64 + 32)
+    config1 = {"workload": "config 1: hall-1.0 batch 1, 64-token prompt (seed 1), 64 greedy steps",
+               "ms_per_token": round(c1_ms / 64, 4), "tok_s": round(64 / (c1_ms / 1e3), 1),
+               "hbm_frac": round(c1_bytes / (c1_ms / 64 / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    # Config 2: the flash-attention op, 8 sequences x 12 heads x 512 x 64,
+    # N(0,1) from seed 2, scale 1/8, one launch per sequence at row_offset
+    # b * 512 as the reference's batched attention issues it.
+    B2, S2, H2, hd2 = 8, 512, 12, 64
+    d2 = H2 * hd2
+    rng2 = np.random.default_rng(2)
+    q2, k2, v2 = (be.tensor(rng2.standard_normal(B2 * S2 * d2, dtype=np.float32)) for _ in range(3))
+    o2, l2 = be.zeros(B2 * S2 * d2), be.zeros(S2 * H2)
+    metas = [(hip.FlashAttnMeta(S2, d2, hd2, 0.125, b * S2),) for b in range(B2)]
+    metas = [(m[0], be.meta(m[0])) for m in metas]
+
+    def flash_all():
+        for shape, meta in metas:
+            be.flash_attention(q2, k2, v2, o2, l2, shape, meta)
+    flash_all()
+    be.synchronize()
+    be.timer_start()
+    for _ in range(10):
+        flash_all()
+    c2_ms = be.timer_stop() / 10
+    c2_flop = 2 * hd2 * S2 * (S2 + 1) * B2 * H2
+    # The same nodes as one launch (akh_flash_attention_batched).
+    bshape = hip.FlashAttnMeta(S2, d2, hd2, 0.125, 0)
+    bmeta = be.meta(bshape)
+    l2b = be.zeros(B2 * S2 * H2)
+    be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
+    be.synchronize()
+    be.timer_start()
+    for _ in range(10):
+        be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
+    c2b_ms = be.timer_stop() / 10
+    config2 = {"workload": "config 2: flash attention 8 x 12 x 512 x 64 (seed 2)",
+               "per_node_ms": round(c2_ms, 4),
+               "per_node_tflops": round(c2_flop / (c2_ms / 1e3) / 1e12, 2),
+               "batched_ms": round(c2b_ms, 4),
+               "batched_tflops": round(c2_flop / (c2b_ms / 1e3) / 1e12, 2),
+               "batched_mfma_frac": round(c2_flop / (c2b_ms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
+
     scaled = None
     if args.scaled:
         scaled = scaled_measurement(pkg, hip, be, with_prefill=not args.no_prefill,
@@ -357,6 +411,8 @@ def main():
                           "bytes_per_step_mean": int(total_bytes / args.steps)},
         "kernels": kernels,
         "prefill": prefill,
+        "config1": config1,
+        "config2": config2,
         "scaled": scaled,
         "cpu_baseline": cpu,
         "cpu_baseline_omp": cpu_omp,

@@ -149,6 +149,14 @@ akh_status akh_flash_attention(akh_backend* be, const float* q,
                                const float* k, const float* v, float* out,
                                float* l_cache, akh_flash_attn_meta shape,
                                const akh_flash_attn_meta* meta);
+/* SelfAttention's forward (layers.rs:408-421): its batch_size
+ * FLASH_ATTENTION nodes, node b at row_offset meta->row_offset + b *
+ * seq_len, as one launch.  l_cache holds the nodes' [seq_len, H] blocks one
+ * after another (batch * seq_len * H floats). */
+akh_status akh_flash_attention_batched(akh_backend* be, const float* q, const float* k,
+                                       const float* v, float* out, float* l_cache,
+                                       akh_flash_attn_meta shape,
+                                       const akh_flash_attn_meta* meta, uint32_t batch);
 /* ATTN_QK_CACHED, ops::attn_qk_cached_with (emit.rs:485-504). */
 akh_status akh_attn_qk_cached(akh_backend* be, const float* q,
                               const float* k_cache, float* scores,
