@@ -222,6 +222,7 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
     roff = (long)p.meta->row_offset * d;
   }
   const int H = d / HD;
+  const float qscale = scale * 1.44269504088896341f;
   const int qblk = gridDim.x - 1 - blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
@@ -285,32 +286,40 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
 #pragma unroll
     for (int s = 0; s < HQ; ++s) st = mfma32(Ks[j][HQ * h + s], qreg[s], st);
 
+    // Scores in the log2 domain (exp(scale x - m) = exp2(scale log2(e) x -
+    // m')); keys above a query or past S exist only in diagonal or ragged
+    // blocks, the only ones masked.
+    const bool masked = j0 + KB - 1 > q0 + wave * 32 || j0 + KB > S;
     float pm = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int key = j0 + acc_row(r, h);
-      float v = st[r] * scale;
-      if (key > qi || key >= S) v = -INFINITY;
+      float v = st[r] * qscale;
+      if (masked) {
+        const int key = j0 + acc_row(r, h);
+        if (key > qi || key >= S) v = -INFINITY;
+      }
       st[r] = v;
       pm = fmaxf(pm, v);
     }
     pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
-    const float mnew = fmaxf(mrow, pm);
+    const float mnew = fmaxf(mrow, pm);  // finite: key 0 is in every query's range
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float e = st[r] == -INFINITY ? 0.f : expf(st[r] - mnew);
+      const float e = __builtin_amdgcn_exp2f(st[r] - mnew);
       st[r] = e;
       ps += e;
     }
     ps += __shfl_xor(ps, 32, 64);
-    const float corr = mrow == -INFINITY ? 0.f : expf(mrow - mnew);
+    const float corr = __builtin_amdgcn_exp2f(mrow - mnew);  // 0 on the first block
     lrow = lrow * corr + ps;
+    if (__any(mnew != mrow)) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    }
     mrow = mnew;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= corr;
     // O^T += V^T P^T: step s uses key acc_row(s, h) on both operands.
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
@@ -336,8 +345,9 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
       if (qrow < S) op[(size_t)qrow * d + 32 * t + c] = Os[r][c];
     }
   }
-  if (p.lse && h == 0 && qi < S)
-    p.lse[(size_t)b * p.lse_bs + (size_t)qi * H + hh] = mrow + logf(lrow);
+  if (p.lse && h == 0 && qi < S)  // max + ln(sum), back in natural units
+    p.lse[(size_t)b * p.lse_bs + (size_t)qi * H + hh] =
+        mrow * 0.69314718055994531f + logf(lrow);
 }
 
 // Causal flash attention for the small head sizes (2..32; the reference
