@@ -860,6 +860,8 @@ struct akh_session {
 
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
+  hipGraph_t graph_n = nullptr;       // kStepsPerGraph decode steps in one graph
+  hipGraphExec_t gexec_n = nullptr;
   uint64_t glayout = 0;  // model layout_gen the graphs were captured for
 
   // Prefill buffers, grown on demand to B * prompt_len rows.
@@ -1181,25 +1183,52 @@ akh_status set_active(akh_session* s, bool all_rows) {
   return AKH_OK;
 }
 
+void drop_graphs(akh_session* s) {
+  for (hipGraphExec_t* e : {&s->gexec, &s->gexec_n, &s->ggexec})
+    if (*e) {
+      hipGraphExecDestroy(*e);
+      *e = nullptr;
+    }
+  for (hipGraph_t* g : {&s->graph, &s->graph_n, &s->ggraph})
+    if (*g) {
+      hipGraphDestroy(*g);
+      *g = nullptr;
+    }
+}
+
 // Captured graphs hold the kernels chosen for the packed weights' element
 // types: drop them when an upload changed one.
 void drop_stale_graphs(akh_session* s) {
   if (s->glayout == s->m->layout_gen) return;
-  if (s->gexec) hipGraphExecDestroy(s->gexec);
-  if (s->graph) hipGraphDestroy(s->graph);
-  if (s->ggexec) hipGraphExecDestroy(s->ggexec);
-  if (s->ggraph) hipGraphDestroy(s->ggraph);
-  s->gexec = nullptr;
-  s->graph = nullptr;
-  s->ggexec = nullptr;
-  s->ggraph = nullptr;
+  drop_graphs(s);
   s->glayout = s->m->layout_gen;
 }
 
+#ifndef AKH_STEPS_PER_GRAPH
+#define AKH_STEPS_PER_GRAPH 8
+#endif
+constexpr uint32_t kStepsPerGraph = AKH_STEPS_PER_GRAPH;
+
+hipError_t enqueue_decode_n(akh_session* s) {
+  for (uint32_t i = 0; i < kStepsPerGraph; ++i) {
+    const hipError_t e = enqueue_decode(s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// The one-step decode graph and, when steps are batched, the
+// kStepsPerGraph-step one (positions and tokens live on the device, so
+// consecutive steps replay without the host).
 akh_status ensure_decode_graph(akh_session* s) {
   drop_stale_graphs(s);
-  if (s->gexec) return AKH_OK;
-  return capture(s, enqueue_decode, &s->graph, &s->gexec, "decode graph");
+  if (!s->gexec) {
+    akh_status st = capture(s, enqueue_decode, &s->graph, &s->gexec, "decode graph");
+    if (st != AKH_OK) return st;
+  }
+  if (kStepsPerGraph > 1 && !s->gexec_n)
+    return capture(s, enqueue_decode_n, &s->graph_n, &s->gexec_n, "decode graph");
+  return AKH_OK;
 }
 
 akh_status download_outputs(akh_session* s, float* logits, uint32_t* next) {
@@ -1222,10 +1251,7 @@ extern "C" void akh_session_free(akh_session* s) {
   if (!s) return;
   hipSetDevice(s->be->device);
   hipStreamSynchronize(s->be->stream);
-  if (s->gexec) hipGraphExecDestroy(s->gexec);
-  if (s->graph) hipGraphDestroy(s->graph);
-  if (s->ggexec) hipGraphExecDestroy(s->ggexec);
-  if (s->ggraph) hipGraphDestroy(s->ggraph);
+  drop_graphs(s);
   free_prefill(s);
   void* bufs[] = {s->kv,     s->rope,   s->xt,     s->xnt,    s->attn_t, s->attn_ml,
                   s->p_qkv,  s->p_out,  s->p_up,   s->up_act, s->p_down,
@@ -1646,7 +1672,11 @@ extern "C" akh_status akh_session_decode_greedy(akh_session* s,
   if (st0 != AKH_OK) return st0;
   hipStream_t st = s->be->stream;
   std::vector<uint32_t> start(s->cur_len);
-  for (uint32_t i = 0; i < steps; ++i) HIP_TRY(hipGraphLaunch(s->gexec, st));
+  uint32_t i = 0;
+  if (kStepsPerGraph > 1)
+    for (; i + kStepsPerGraph <= steps; i += kStepsPerGraph)
+      HIP_TRY(hipGraphLaunch(s->gexec_n, st));
+  for (; i < steps; ++i) HIP_TRY(hipGraphLaunch(s->gexec, st));
   for (uint32_t b = 0; b < s->B; ++b) s->cur_len[b] += steps;
   if (out_tokens) {
     std::vector<uint32_t> h((size_t)s->B * (s->max_ctx + 1));
@@ -1821,14 +1851,7 @@ extern "C" akh_status akh_session_set_kv_bf16(akh_session* s, int enable) {
   HIP_TRY(hipSetDevice(s->be->device));
   HIP_TRY(hipStreamSynchronize(s->be->stream));
   // Graphs hold the attention kernel of the old element type.
-  if (s->gexec) hipGraphExecDestroy(s->gexec);
-  if (s->graph) hipGraphDestroy(s->graph);
-  if (s->ggexec) hipGraphExecDestroy(s->ggexec);
-  if (s->ggraph) hipGraphDestroy(s->ggraph);
-  s->gexec = nullptr;
-  s->graph = nullptr;
-  s->ggexec = nullptr;
-  s->ggraph = nullptr;
+  drop_graphs(s);
   free_prefill(s);
   HIP_TRY(hipFree(s->kv));
   s->kv = nullptr;
