@@ -33,6 +33,33 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return bf16_bits(lo) | (bf16_bits(hi) << 16);
 }
 __device__ __forceinline__ bf16x8 bf16x8_of(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Eight floats (x0, x1) as three bfloat16 octets with x = hi + mid + lo
+// exactly: hi keeps the top 8 significant bits (truncation), mid the top 8
+// of the exact remainder x - hi (at most 16 bits), and the last remainder
+// has at most 8 significant bits, so lo holds it without rounding.  With
+// bfloat16 weights every product of a term with a weight is exact in fp32,
+// so three bf16 MFMAs give an fp32-accurate A . W.
+__device__ __forceinline__ void split3_bf16(float4 x0, float4 x1, uint4& hi, uint4& mid,
+                                            uint4& lo) {
+  const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t ua = __float_as_uint(v[2 * i]), ub = __float_as_uint(v[2 * i + 1]);
+    const float ra = v[2 * i] - __uint_as_float(ua & 0xFFFF0000u);
+    const float rb = v[2 * i + 1] - __uint_as_float(ub & 0xFFFF0000u);
+    const uint32_t sa = __float_as_uint(ra), sb = __float_as_uint(rb);
+    const uint32_t la = __float_as_uint(ra - __uint_as_float(sa & 0xFFFF0000u));
+    const uint32_t lb = __float_as_uint(rb - __uint_as_float(sb & 0xFFFF0000u));
+    ph[i] = (ua >> 16) | (ub & 0xFFFF0000u);
+    pm[i] = (sa >> 16) | (sb & 0xFFFF0000u);
+    pl[i] = (la >> 16) | (lb & 0xFFFF0000u);
+  }
+  hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+  mid = make_uint4(pm[0], pm[1], pm[2], pm[3]);
+  lo = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+}
 __device__ __forceinline__ bf16x8 bf16x8_of(float4 a, float4 b) {
   return bf16x8_of(make_uint4(pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w),
                               pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)));

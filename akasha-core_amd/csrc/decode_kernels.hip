@@ -102,8 +102,10 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
 //
 // PRO_SILU_SUM: A = silu(sum of p.nparts k-quad partial tiles at p.xt).
 // BF: W is packed in bfloat16 k-octets (k_pack_tiles_bf16); a lane loads
-// eight k per 16 bytes and the MFMAs, their order and the results are those
-// of the float tiles holding the same values.
+// eight k per 16 bytes.  Its octet and the same eight k of its row of A are
+// the operands of v_mfma_f32_32x32x16_bf16, with A split exactly into three
+// bfloat16 terms (split3_bf16): every product is exact, so the result has
+// fp32 accuracy at 3 x 32 instead of 8 x 64 MFMA cycles per 16 k.
 template <int W, int HL, int EPI, int PRO, bool BF>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   constexpr int RH = W > 1 ? W / 2 : 1;
@@ -128,23 +130,21 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   f32x16 acc = zero16();
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;  // first k-quad of this half
-    float4 b[HQ], a[HQ];
-    uint4 bh[BF ? HQ / 2 : 1];
-    if (BF) {
+    // The pass's weights: bfloat16 octets or float quads.
+    using WRaw = typename std::conditional<BF, uint4, float4>::type;
+    constexpr int NW = BF ? HQ / 2 : HQ;
+    WRaw wc[NW];
 #pragma unroll
-      for (int q = 0; q < HQ; q += 2) {
-        const int kq = kq0 + q;  // even: HL is a multiple of 8
-        bh[q / 2] = 4 * kq < ke ? *reinterpret_cast<const uint4*>(wh + (size_t)kq * 128)
-                                : make_uint4(0u, 0u, 0u, 0u);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < HQ; ++q) {
-        const int kq = kq0 + q;
-        b[q] = 4 * kq < ke ? *reinterpret_cast<const float4*>(wt + (size_t)kq * 128)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+    for (int i = 0; i < NW; ++i) {
+      const int kq = kq0 + (BF ? 2 * i : i);  // BF: even, HL is a multiple of 8
+      if constexpr (BF)
+        wc[i] = 4 * kq < ke ? *reinterpret_cast<const uint4*>(wh + (size_t)kq * 128)
+                            : make_uint4(0u, 0u, 0u, 0u);
+      else
+        wc[i] = 4 * kq < ke ? *reinterpret_cast<const float4*>(wt + (size_t)kq * 128)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    float4 a[HQ];
 #pragma unroll
     for (int q = 0; q < HQ; ++q) {
       const int kq = kq0 + q;
@@ -189,19 +189,24 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
       }
       a[q] = t;
     }
-    if (BF) {
+    if constexpr (BF) {
 #pragma unroll
       for (int q = 0; q < HQ; q += 2) {
-        b[q] = bf16x4(bh[q / 2].x, bh[q / 2].y);
-        b[q + 1] = bf16x4(bh[q / 2].z, bh[q / 2].w);
+        const bf16x8 w8 = bf16x8_of(wc[q / 2]);
+        uint4 hi, mid, lo;
+        split3_bf16(a[q], a[q + 1], hi, mid, lo);
+        acc = mfma_bf16(bf16x8_of(hi), w8, acc);
+        acc = mfma_bf16(bf16x8_of(mid), w8, acc);
+        acc = mfma_bf16(bf16x8_of(lo), w8, acc);
       }
-    }
+    } else {
 #pragma unroll
-    for (int q = 0; q < HQ; ++q) {
-      acc = mfma32(a[q].x, b[q].x, acc);
-      acc = mfma32(a[q].y, b[q].y, acc);
-      acc = mfma32(a[q].z, b[q].z, acc);
-      acc = mfma32(a[q].w, b[q].w, acc);
+      for (int q = 0; q < HQ; ++q) {
+        acc = mfma32(a[q].x, wc[q].x, acc);
+        acc = mfma32(a[q].y, wc[q].y, acc);
+        acc = mfma32(a[q].z, wc[q].z, acc);
+        acc = mfma32(a[q].w, wc[q].w, acc);
+      }
     }
   }
 

@@ -256,7 +256,9 @@ akh_status akh_model_param(akh_model* m, uint32_t index, float** dev,
  * and refresh the decode path's tiled copy of a weight matrix.  A matrix
  * whose every value is a bfloat16 (low 16 mantissa bits zero, e.g. weights
  * trained or stored in bf16) is tiled in bfloat16: half the bytes per
- * decode step, the same products and results. */
+ * decode step, and bf16 MFMAs on the activations split exactly into three
+ * bfloat16 terms, so every product is exact (fp32-accurate results, summed
+ * in another order than f32 tiles). */
 akh_status akh_model_upload_param(akh_model* m, uint32_t index,
                                   const float* host, size_t count);
 /* No reference counterpart (the reference keeps f32 device weights): allow

@@ -251,12 +251,15 @@ def test_head_dim_128_prefill_matches_oracle(backend, pkg, ora):
         o.close()
 
 
-def test_bf16_tiles_are_exact(backend, pkg, ora):
+def test_bf16_tiles_keep_fp32_accuracy(backend, pkg, ora):
     # Weights whose values are all bfloat16 are tiled in bfloat16 for decode:
     # qkv, up and down of each layer and, with dim > 1024, the lm_head (out
-    # keeps float tiles).  The products are the same, so the logits must be
-    # bit-identical to float tiles of the same values.  Toggling the tiles
-    # after a decode graph was captured also checks that the graph is rebuilt.
+    # keeps float tiles).  Those GEMMs run bf16 MFMAs on A split exactly into
+    # three bfloat16 terms, so every product is exact and only the summation
+    # order differs from the float tiles: logits agree to fp32 rounding
+    # (1e-4 here, against the 1e-3 oracle bar) with the same tokens, and each
+    # setting is bit-reproducible.  Toggling the tiles after a decode graph
+    # was captured also checks that the graph is rebuilt.
     cfg = pkg.ModelConfig.new(500, 1152, 9, 2, 40)
     w = pkg.synthetic_weights(cfg, seed=41, bf16=True)
     model, s = _session(pkg, backend, cfg, w, 40, 3)
@@ -276,7 +279,7 @@ def test_bf16_tiles_are_exact(backend, pkg, ora):
                 assert np.array_equal(a, b) and np.array_equal(ta, tb)
         runs[allow] = out
     for (a, ta), (b, tb) in zip(runs[True], runs[False]):
-        assert np.array_equal(a, b) and np.array_equal(ta, tb)
+        assert np.abs(a - b).max() < 1e-4 and np.array_equal(ta, tb)
     o = ora.OracleSession(cfg, w, 40)
     ref = o.prefill(toks[1])
     assert np.abs(logits[1] - ref).max() < TOL
