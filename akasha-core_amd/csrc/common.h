@@ -65,6 +65,37 @@ __device__ __forceinline__ bf16x8 bf16x8_of(float4 a, float4 b) {
                               pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)));
 }
 
+// Two floats as packed bfloat16, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const f2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
+}
+
+// Eight floats as three bfloat16 octets with x = hi + mid + lo exactly,
+// rounding to nearest: |x - hi| <= 2^-8 |x| and the remainder x - hi is
+// exact (Sterbenz) with at most 16 significant bits; mid rounds it the same
+// way, and the last remainder (at most 8 significant bits, |lo| <= 2^-16 |x|)
+// converts without rounding.
+__device__ __forceinline__ void split3_rne(float4 x0, float4 x1, uint4& hi, uint4& mid,
+                                           uint4& lo) {
+  const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = v[2 * i], b = v[2 * i + 1];
+    ph[i] = cvt_pk_bf16(a, b);
+    const float ra = a - __uint_as_float(ph[i] << 16);
+    const float rb = b - __uint_as_float(ph[i] & 0xFFFF0000u);
+    pm[i] = cvt_pk_bf16(ra, rb);
+    pl[i] = cvt_pk_bf16(ra - __uint_as_float(pm[i] << 16), rb - __uint_as_float(pm[i] & 0xFFFF0000u));
+  }
+  hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+  mid = make_uint4(pm[0], pm[1], pm[2], pm[3]);
+  lo = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll

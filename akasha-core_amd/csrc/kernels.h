@@ -98,6 +98,8 @@ struct GemmParams {
   // and A either in bfloat16 (a16) or fp32 (a, split into hi + lo parts).
   const uint16_t* a16;   // [M, K]
   const uint16_t* bt16;  // [N, K]
+  // launch_gemm_x6: the transposed fp32 weights.
+  const float* bt;  // [N, K]
 };
 
 struct FlashParams {
@@ -128,6 +130,12 @@ hipError_t launch_rows_rmsnorm(const float* x, const float* w, float* out,
 hipError_t launch_gemm_bf16(const GemmParams& p, int epi, hipStream_t s);
 // wt[n, k] = bf16(w[k, n]) for a [K, N] row-major matrix.
 hipError_t launch_transpose_bf16(const float* w, int K, int N, uint16_t* wt, hipStream_t s);
+// fp32-accurate GEMM on bfloat16 MFMAs: A (p.a, fp32 [M, K]) and the
+// transposed fp32 weights (p.bt, [N, K]) enter as three bfloat16 terms
+// each, six products accumulated in fp32.  K % 8 == 0.
+hipError_t launch_gemm_x6(const GemmParams& p, int epi, hipStream_t s);
+// wt[n, k] = w[k, n] for a [K, N] row-major matrix.
+hipError_t launch_transpose_f32(const float* w, int K, int N, float* wt, hipStream_t s);
 // Causal flash attention (head_dim 64 or 128) with bfloat16 QK^T and PV
 // MFMAs; writes p.o16.
 hipError_t launch_flash_bf16(const FlashParams& p, int batch, int max_rows, hipStream_t s);

@@ -566,6 +566,162 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 GEMM on bfloat16 MFMAs (launch_gemm_x6)
+
+// wt[n, k] = w[k, n] for a [K, N] row-major matrix, through a 32x32 LDS tile.
+__global__ __launch_bounds__(256) void k_transpose_f32(const float* __restrict__ w, int K, int N,
+                                                       float* __restrict__ wt) {
+  __shared__ float t[32][33];
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int c = threadIdx.x & 31, r = threadIdx.x >> 5;
+  for (int i = r; i < 32; i += 8) {
+    const int k = k0 + i, n = n0 + c;
+    t[i][c] = (k < K && n < N) ? w[(size_t)k * N + n] : 0.f;
+  }
+  __syncthreads();
+  for (int i = r; i < 32; i += 8) {
+    const int n = n0 + i, k = k0 + c;
+    if (n < N && k < K) wt[(size_t)n * K + k] = t[c][i];
+  }
+}
+
+// C[M,N] = A[M,K] B[K,N] in fp32 accuracy on v_mfma_f32_32x32x16_bf16.
+// A (p.a, [M, K]) and the transposed weights B^T (p.bt, [N, K]) are fp32;
+// each element enters LDS as three bfloat16 terms (split3_rne: a = a1 + a2
+// + a3 exactly, |a2| <= 2^-8 |a|, |a3| <= 2^-16 |a|).  Every product of
+// terms is exact in fp32; the six whose size reaches 2^-16 |a b| are
+// accumulated (a1b1, a1b2, a2b1, a1b3, a2b2, a3b1), so each product a.b is
+// carried to within 2^-23 relative, about fp32's own rounding, at 6 x 32
+// instead of 8 x 64 MFMA cycles per 16 k.
+//
+// Block tile BM x BN, BK = 16, waves WM (rows) x WN (columns); a wave owns
+// (BM / WM) x 64 as TA x 2 MFMA tiles.  LDS holds the three planes of both
+// operands k-contiguous (rows of 16 k padded to 48 bytes, so 16-byte
+// fragment reads of 8 consecutive rows hit distinct banks), double
+// buffered; the next k step's global loads are issued before the MFMAs.  B
+// rows are stored permuted so lane j of column tile t reads column 2j + t
+// (adjacent column pairs for the paired epilogues).  K % 8 == 0.
+template <int EPI, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
+  constexpr int BK = 16, LD = BK + 8, NT = 64 * WM * WN;
+  constexpr int TA = BM / WM / 32;
+  static_assert(BN == 64 * WN && BM % (32 * WM) == 0, "wave tiles are (32 TA) x 64");
+  // k-octets staged per thread (some threads idle when fewer than NT).
+  constexpr int OA = (2 * BM + NT - 1) / NT, OB = (2 * BN + NT - 1) / NT;
+  __shared__ __align__(16) uint16_t As[2][3][BM][LD];
+  __shared__ __align__(16) uint16_t Bs[2][3][BN][LD];
+
+  const int M = p.M, N = p.N, K = p.K;
+  // Each XCD takes a contiguous run of tiles (see k_gemm_bf16).
+  int id = blockIdx.x + gridDim.x * blockIdx.y;
+  const int per_xcd = (int)(gridDim.x * gridDim.y) / 8;
+  if (id < per_xcd * 8) id = (id % 8) * per_xcd + id / 8;
+  const int m0 = (id / gridDim.x) * BM, n0 = (id % gridDim.x) * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int j = lane & 31, h = lane >> 5;
+
+  // Staging: octet o = tid + NT * i covers row o / 2, k (o % 2) * 8 .. + 7.
+  float4 fa[OA][2], fb[OB][2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < OA; ++i) {
+      const int o = tid + NT * i, r = o >> 1, k = k0 + (o & 1) * 8, gm = m0 + r;
+      const bool in = o < 2 * BM && gm < M && k < K;
+      const float* src = p.a + (size_t)(in ? gm : 0) * K + (in ? k : 0);
+      fa[i][0] = in ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+      fa[i][1] = in ? *reinterpret_cast<const float4*>(src + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < OB; ++i) {
+      const int o = tid + NT * i, r = o >> 1, k = k0 + (o & 1) * 8, gn = n0 + r;
+      const bool in = o < 2 * BN && gn < N && k < K;
+      const float* src = p.bt + (size_t)(in ? gn : 0) * K + (in ? k : 0);
+      fb[i][0] = in ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+      fb[i][1] = in ? *reinterpret_cast<const float4*>(src + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < OA; ++i) {
+      const int o = tid + NT * i, r = o >> 1, k = (o & 1) * 8;
+      if (o >= 2 * BM) break;
+      uint4 t0, t1, t2;
+      split3_rne(fa[i][0], fa[i][1], t0, t1, t2);
+      *reinterpret_cast<uint4*>(&As[buf][0][r][k]) = t0;
+      *reinterpret_cast<uint4*>(&As[buf][1][r][k]) = t1;
+      *reinterpret_cast<uint4*>(&As[buf][2][r][k]) = t2;
+    }
+#pragma unroll
+    for (int i = 0; i < OB; ++i) {
+      const int o = tid + NT * i, r = o >> 1, k = (o & 1) * 8;
+      if (o >= 2 * BN) break;
+      // Column c = 64 g + 2 jj + t of the block lives at LDS row 64 g + 32 t + jj.
+      const int br = (r & ~63) | ((r & 1) << 5) | ((r & 63) >> 1);
+      uint4 t0, t1, t2;
+      split3_rne(fb[i][0], fb[i][1], t0, t1, t2);
+      *reinterpret_cast<uint4*>(&Bs[buf][0][br][k]) = t0;
+      *reinterpret_cast<uint4*>(&Bs[buf][1][br][k]) = t1;
+      *reinterpret_cast<uint4*>(&Bs[buf][2][br][k]) = t2;
+    }
+  };
+
+  f32x16 acc[TA][2];
+#pragma unroll
+  for (int a = 0; a < TA; ++a)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[a][t] = zero16();
+
+  const int nk = (K + BK - 1) / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+    bf16x8 bfr[2][3];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        bfr[t][pl] = bf16x8_of(
+            *reinterpret_cast<const uint4*>(&Bs[buf][pl][wn * 64 + t * 32 + j][8 * h]));
+#pragma unroll
+    for (int a = 0; a < TA; ++a) {
+      bf16x8 af[3];
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        af[pl] = bf16x8_of(
+            *reinterpret_cast<const uint4*>(&As[buf][pl][wm * (32 * TA) + a * 32 + j][8 * h]));
+      // Smallest terms first.
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[2], bfr[t][0], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[1], bfr[t][1], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], bfr[t][2], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[1], bfr[t][0], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], bfr[t][1], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], bfr[t][0], acc[a][t]);
+    }
+    if (kt + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int a = 0; a < TA; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * (32 * TA) + a * 32 + acc_row(r, h);
+      const int n = n0 + wn * 64 + 2 * j;
+      epi_pair_gemm<EPI>(p, M, N, m, n, acc[a][0][r], acc[a][1][r]);
+    }
+}
+
 // Causal flash attention with bfloat16 MFMAs (head_dim 64 or 128), the
 // structure of k_flash_mfma: block = 4 waves x 32 queries, keys in blocks of
 // 32, S^T = K Q^T per wave so each lane owns one query.  Q, K and V are
@@ -787,6 +943,37 @@ hipError_t launch_gemm_bf16(const GemmParams& p, int epi, hipStream_t s) {
     default: return hipErrorInvalidValue;
   }
 #undef AKH_GO
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_x6(const GemmParams& p, int epi, hipStream_t s) {
+  if (p.K % 8 != 0 || p.M <= 0 || p.N <= 0 || p.K <= 0 || !p.a || !p.bt)
+    return hipErrorInvalidValue;
+  // 256x256 tiles when they fill the chip twice over, else 256x128 (fewer
+  // idle CUs on the last round of tiles); measured on MI355X.
+  const bool big = (long)((p.M + 255) / 256) * ((p.N + 255) / 256) >= 512;
+#define AKH_X6_GO(E)                                                                        \
+  if (big)                                                                                  \
+    hipLaunchKernelGGL((k_gemm_x6<E, 256, 256, 2, 4>), dim3((p.N + 255) / 256, (p.M + 255) / 256), \
+                       dim3(512), 0, s, p);                                                 \
+  else                                                                                      \
+    hipLaunchKernelGGL((k_gemm_x6<E, 256, 128, 4, 2>), dim3((p.N + 127) / 128, (p.M + 255) / 256), \
+                       dim3(512), 0, s, p);
+  switch (epi) {
+    case GEMM_STORE: AKH_X6_GO(GEMM_STORE) break;
+    case GEMM_ADD: AKH_X6_GO(GEMM_ADD) break;
+    case GEMM_SILU: AKH_X6_GO(GEMM_SILU) break;
+    case GEMM_QKV: AKH_X6_GO(GEMM_QKV) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef AKH_X6_GO
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_f32(const float* w, int K, int N, float* wt, hipStream_t s) {
+  if (K <= 0 || N <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_transpose_f32, dim3((N + 31) / 32, (K + 31) / 32), dim3(256), 0, s, w, K,
+                     N, wt);
   return hipGetLastError();
 }
 

@@ -519,6 +519,11 @@ struct akh_model {
   bool allow_bf16 = true;            // bfloat16 tiles where every value is one
   bool prefill_bf16 = false;         // the optional bfloat16-MFMA prefill
   std::vector<uint16_t*> wt16;       // per parameter: bf16 [N, K] copy (layer matrices)
+  // The prefill GEMMs on split-bfloat16 MFMAs (fp32 accuracy, on by default
+  // where dim and ffn_hidden are multiples of 8): transposed fp32 [N, K]
+  // copies of the layer matrices and lm_head.
+  bool prefill_x6 = false;
+  std::vector<float*> wt32;
   uint64_t layout_gen = 0;           // bumped when a packed matrix changes element type
 
   float* embedding() const { return params[0]; }
@@ -544,8 +549,44 @@ extern "C" void akh_model_free(akh_model* m) {
   if (m->bf16_flag) hipFree(m->bf16_flag);
   for (uint16_t* p : m->wt16)
     if (p) hipFree(p);
+  for (float* p : m->wt32)
+    if (p) hipFree(p);
   delete m;
 }
+
+namespace {
+
+bool x6_capable(const akh_model_config& c) { return c.dim % 8 == 0 && c.ffn_hidden % 8 == 0; }
+
+// Allocates (zeroed) or frees the transposed fp32 copies used by the
+// split-bfloat16 prefill GEMMs; `transpose` fills them from the parameters.
+akh_status set_x6(akh_model* m, bool enable, bool transpose) {
+  HIP_TRY(hipSetDevice(m->be->device));
+  HIP_TRY(hipStreamSynchronize(m->be->stream));
+  for (float*& p : m->wt32)
+    if (p) {
+      HIP_TRY(hipFree(p));
+      p = nullptr;
+    }
+  m->prefill_x6 = false;
+  if (!enable) return AKH_OK;
+  m->wt32.assign(m->params.size(), nullptr);
+  for (size_t i = 0; i < m->packed.size(); ++i) {
+    const PackedMatrix& pm = m->packed[i];
+    if (!pm.rows) continue;
+    void* p = nullptr;
+    akh_status st = akh_tensor_alloc(m->be, (size_t)pm.K * pm.N * sizeof(float), &p);
+    if (st != AKH_OK) return st;
+    m->wt32[i] = static_cast<float*>(p);
+    if (transpose)
+      HIP_TRY(launch_transpose_f32(m->params[i], pm.K, pm.N, m->wt32[i], m->be->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(m->be->stream));
+  m->prefill_x6 = true;
+  return AKH_OK;
+}
+
+}  // namespace
 
 extern "C" akh_status akh_model_new(akh_backend* be,
                                     const akh_model_config* cfg,
@@ -618,6 +659,13 @@ extern "C" akh_status akh_model_new(akh_backend* be,
     }
     m->bf16_flag = static_cast<int*>(p);
   }
+  if (x6_capable(c)) {
+    akh_status st = set_x6(m, true, false);  // filled as parameters are uploaded
+    if (st != AKH_OK) {
+      akh_model_free(m);
+      return st;
+    }
+  }
   *out = m;
   return AKH_OK;
 }
@@ -655,6 +703,8 @@ akh_status repack(akh_model* m, uint32_t index) {
   HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, bf16, st));
   if (index < m->wt16.size() && m->wt16[index])
     HIP_TRY(launch_transpose_bf16(m->params[index], pm.K, pm.N, m->wt16[index], st));
+  if (index < m->wt32.size() && m->wt32[index])
+    HIP_TRY(launch_transpose_f32(m->params[index], pm.K, pm.N, m->wt32[index], st));
   HIP_TRY(hipStreamSynchronize(st));
   if (bf16 != pm.bf16) {
     pm.bf16 = bf16;
@@ -696,6 +746,15 @@ extern "C" akh_status akh_model_set_prefill_bf16(akh_model* m, int enable) {
   HIP_TRY(hipStreamSynchronize(m->be->stream));
   m->prefill_bf16 = true;
   return AKH_OK;
+}
+
+extern "C" akh_status akh_model_set_prefill_x6(akh_model* m, int enable) {
+  CHECK_ARG(m && (enable == 0 || enable == 1), "akh_model_set_prefill_x6: bad argument");
+  CHECK_ARG(!m->be->capturing, "akh_model_set_prefill_x6: graph capture in progress");
+  CHECK_ARG(!enable || x6_capable(m->cfg),
+            "akh_model_set_prefill_x6: needs dim and ffn_hidden multiples of 8");
+  if ((enable != 0) == m->prefill_x6) return AKH_OK;
+  return set_x6(m, enable != 0, true);
 }
 
 extern "C" akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16) {
@@ -1405,6 +1464,17 @@ extern "C" akh_status akh_session_truncate(akh_session* s, uint32_t len) {
 
 namespace {
 
+// A prefill GEMM on parameter `index`: the split-bfloat16 kernel on its
+// transposed copy when the model has it, else the fp32-MFMA kernel.
+hipError_t prefill_gemm(const akh_model* m, GemmParams& g, uint32_t index, int epi,
+                        hipStream_t st) {
+  if (m->prefill_x6 && index < m->wt32.size() && m->wt32[index]) {
+    g.bt = m->wt32[index];
+    return launch_gemm_x6(g, epi, st);
+  }
+  return launch_gemm(g, epi, st);
+}
+
 // The prefill layers in fp32 (build_prefill_layer's node order).
 hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
   const akh_model_config& c = s->m->cfg;
@@ -1435,7 +1505,8 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     g.rope = s->rope;
     g.dim = d;
     g.head_dim = hd;
-    TRY_HIP(launch_gemm(g, GEMM_QKV, st));
+    const uint32_t base = 1 + 6 * l;
+    TRY_HIP(prefill_gemm(s->m, g, base + W_QKV, GEMM_QKV, st));
     if (s->kv16)
       TRY_HIP(launch_kv_store_bf16(s->pk, s->pv, static_cast<uint16_t*>(s->kv_at(l, 0)),
                                    static_cast<uint16_t*>(s->kv_at(l, 1)), (int)s->B, (int)S,
@@ -1462,7 +1533,7 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     o.M = (int)rows;
     o.N = d;
     o.K = d;
-    TRY_HIP(launch_gemm(o, GEMM_ADD, st));
+    TRY_HIP(prefill_gemm(s->m, o, base + W_OUT, GEMM_ADD, st));
 
     TRY_HIP(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM2), s->pxn,
                                 (int)rows, (int)d, c.norm_eps, st));
@@ -1473,7 +1544,7 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     u.M = (int)rows;
     u.N = c.ffn_hidden;
     u.K = d;
-    TRY_HIP(launch_gemm(u, GEMM_SILU, st));
+    TRY_HIP(prefill_gemm(s->m, u, base + W_UP, GEMM_SILU, st));
 
     GemmParams w{};
     w.a = s->pffn;
@@ -1482,7 +1553,7 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     w.M = (int)rows;
     w.N = d;
     w.K = c.ffn_hidden;
-    TRY_HIP(launch_gemm(w, GEMM_ADD, st));
+    TRY_HIP(prefill_gemm(s->m, w, base + W_DOWN, GEMM_ADD, st));
   }
 #undef TRY_HIP
   return hipSuccess;
@@ -2023,7 +2094,7 @@ extern "C" akh_status akh_forward_loss(akh_forward* f, const uint32_t* tokens,
   g.M = (int)rows;
   g.N = (int)V;
   g.K = (int)d;
-  HIP_TRY(launch_gemm(g, GEMM_STORE, st));
+  HIP_TRY(prefill_gemm(f->m, g, 2 + 6 * c.num_layers, GEMM_STORE, st));
   HIP_TRY(launch_cross_entropy(f->logits, f->targets, f->losses, (uint32_t)rows, f->ce, st));
   std::vector<float> l(rows);
   HIP_TRY(hipMemcpyAsync(l.data(), f->losses, rows * 4, hipMemcpyDeviceToHost, st));

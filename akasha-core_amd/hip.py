@@ -205,6 +205,7 @@ _SIGS = {
     "akh_model_upload_param": (ST, [P, U32, P, C.c_size_t]),
     "akh_model_set_bf16_tiles": (ST, [P, C.c_int, P]),
     "akh_model_set_prefill_bf16": (ST, [P, C.c_int]),
+    "akh_model_set_prefill_x6": (ST, [P, C.c_int]),
     "akh_checkpoint_info": (ST, [C.c_char_p, C.POINTER(CheckpointInfo)]),
     "akh_model_load_checkpoint": (ST, [P, C.c_char_p, C.POINTER(C.c_uint64),
                                        C.POINTER(C.c_int)]),
@@ -535,6 +536,13 @@ class Model:
         _check(_lib.akh_model_set_bf16_tiles(self.handle, 1 if allow else 0, C.byref(n)),
                "set_bf16_tiles")
         return n.value
+
+    def set_prefill_x6(self, enable: bool):
+        """Prefill GEMMs on split-bfloat16 MFMAs (fp32 accuracy; the default
+        where dim and ffn_hidden are multiples of 8) or, with False, on the
+        fp32 MFMAs."""
+        _check(_lib.akh_model_set_prefill_x6(self.handle, 1 if enable else 0),
+               "set_prefill_x6")
 
     def set_prefill_bf16(self, enable: bool):
         """The optional bf16-MFMA prefill (logits within 2e-2 of f32)."""

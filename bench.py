@@ -67,12 +67,29 @@ def decode_step_bytes(cfg, B, T):
     return weights + kv_read + kv_append + B * d * 4 + B * V * 4
 
 
-def prefill_flops(cfg, B, S):
+def prefill_flop_parts(cfg, B, S, lm_rows=None):
+    """(layer GEMM, attention, lm_head) flops of a B x S prefill; lm_head on
+    `lm_rows` rows (default: the last row of every sequence)."""
     d, F, L, H, hd, V = cfg.dim, cfg.ffn_hidden, cfg.num_layers, cfg.num_heads, cfg.head_dim, cfg.vocab_size
     gemm = 2 * B * S * L * (d * 3 * d + d * d + d * F + F * d)
     attn = 2 * hd * S * (S + 1) * B * H * L
-    lm = 2 * B * d * V
-    return gemm + attn + lm
+    lm = 2 * (B if lm_rows is None else lm_rows) * d * V
+    return gemm, attn, lm
+
+
+def prefill_rates(ms, gemm, attn, lm, x6_flop):
+    """Rates of a prefill that took `ms`: useful fp32 TFLOP/s; their fraction
+    of the fp32 MFMA peak (the roofline of fp32 arithmetic on this part);
+    and the MFMA pipes' busy fraction, the executed MFMA work at the peak rate
+    of the instructions that ran it: the split-bfloat16 GEMMs (`x6_flop` of
+    the useful flops) execute six bf16 products per multiply-add at the bf16
+    peak, everything else runs on fp32 MFMAs."""
+    t = ms / 1e3
+    useful = gemm + attn + lm
+    busy = 6 * x6_flop / (BF16_MFMA_PEAK_TFLOPS * 1e12) + (useful - x6_flop) / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+    return {"tflops": round(useful / t / 1e12, 2),
+            "fp32_roofline_frac": round(useful / t / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "mfma_busy_frac": round(busy / t, 4)}
 
 
 def scaled_decode(hip, be, model, cfg, T, steps):
@@ -138,10 +155,28 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
         be.timer_start()
         ps.prefill(toks, want_logits=False)
         pms = be.timer_stop()
-        fl = prefill_flops(cfg, Bp, Sp)
-        out.update({"prefill_ms": round(pms, 2), "prefill_tok_s": round(Bp * Sp / (pms / 1e3), 1),
-                    "prefill_tflops": round(fl / (pms / 1e3) / 1e12, 2),
-                    "prefill_mfma_frac_fp32": round(fl / (pms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)})
+        g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
+        fl = g + a + lm
+        r = prefill_rates(pms, g, a, lm, g)
+        out.update({"prefill_gemms": "split-bf16 (fp32-accurate, default)",
+                    "prefill_ms": round(pms, 2), "prefill_tok_s": round(Bp * Sp / (pms / 1e3), 1),
+                    "prefill_tflops": r["tflops"],
+                    "prefill_fp32_roofline_frac": r["fp32_roofline_frac"],
+                    "prefill_mfma_busy_frac": r["mfma_busy_frac"]})
+        # The same prefill with the layer GEMMs on the fp32 MFMAs.
+        log("bench: scaled config prefill 8 x 2048, fp32-MFMA GEMMs")
+        model.set_prefill_x6(False)
+        ps.reset()
+        ps.prefill(toks, want_logits=False)
+        ps.reset()
+        be.synchronize()
+        be.timer_start()
+        ps.prefill(toks, want_logits=False)
+        fms = be.timer_stop()
+        model.set_prefill_x6(True)
+        out.update({"prefill_fp32_mfma_ms": round(fms, 2),
+                    "prefill_fp32_mfma_tok_s": round(Bp * Sp / (fms / 1e3), 1),
+                    "prefill_fp32_mfma_frac": round(fl / (fms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)})
         # The optional bf16-MFMA prefill (logits within 2e-2 of f32).
         log("bench: scaled config prefill 8 x 2048, bf16 MFMA")
         model.set_prefill_bf16(True)
@@ -280,12 +315,29 @@ def main():
             ps.prefill(ptoks, want_logits=False)
             times.append(be.timer_stop())
         pms = min(times)
-        fl = prefill_flops(cfg, Bp, Sp)
+        g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
+        fl = g + a + lm
         prefill = {"workload": "config 3: hall-1.0 fp32 prefill 16 x 512 (seed 3), last-row logits",
+                   "gemms": "split-bf16: fp32 operands as three bf16 terms, six products "
+                            "(fp32-accurate, the default)",
                    "ms": round(pms, 3), "tok_s": round(Bp * Sp / (pms / 1e3), 1),
-                   "tflops": round(fl / (pms / 1e3) / 1e12, 2),
-                   "mfma_frac": round(fl / (pms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
-                   "flop": fl}
+                   **prefill_rates(pms, g, a, lm, g), "flop": fl}
+        # The same prefill with the layer GEMMs on the fp32 MFMAs.
+        model.set_prefill_x6(False)
+        ps.reset()
+        ps.prefill(ptoks, want_logits=False)  # warm
+        ftimes32 = []
+        for _ in range(3):
+            ps.reset()
+            be.synchronize()
+            be.timer_start()
+            ps.prefill(ptoks, want_logits=False)
+            ftimes32.append(be.timer_stop())
+        model.set_prefill_x6(True)
+        p32 = min(ftimes32)
+        prefill["fp32_mfma_gemms"] = {"ms": round(p32, 3), "tok_s": round(Bp * Sp / (p32 / 1e3), 1),
+                                      "tflops": round(fl / (p32 / 1e3) / 1e12, 2),
+                                      "mfma_frac": round(fl / (p32 / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
         ps.close()
         # Trainer::forward + CrossEntropy on the same 16 x 512 rows: the
         # lm_head runs on every row (+2 rows d V flop) and the loss follows.
@@ -299,12 +351,12 @@ def main():
             mean_loss, _ = fw.loss(ptoks, targets)
             ftimes.append(be.timer_stop())
         fms = min(ftimes)
-        ffl = fl - 2 * Bp * cfg.dim * cfg.vocab_size + 2 * Bp * Sp * cfg.dim * cfg.vocab_size
+        g, a, flm = prefill_flop_parts(cfg, Bp, Sp, lm_rows=Bp * Sp)
+        ffl = g + a + flm
         prefill["train_forward"] = {
             "workload": "Trainer::forward + CrossEntropy, 16 x 512 rows (seed 3), all-rows lm_head",
             "ms": round(fms, 3), "tok_s": round(Bp * Sp / (fms / 1e3), 1),
-            "tflops": round(ffl / (fms / 1e3) / 1e12, 2),
-            "mfma_frac": round(ffl / (fms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            **prefill_rates(fms, g, a, flm, g + flm),
             "mean_loss": round(mean_loss, 4), "flop": ffl}
         fw.close()
 

@@ -278,6 +278,18 @@ akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16);
  * akh_model_upload_param).  Needs head_dim 64 or 128 and dim, ffn_hidden
  * multiples of 8. */
 akh_status akh_model_set_prefill_bf16(akh_model* m, int enable);
+/* No reference counterpart (a choice of kernel, not of numerics): with
+ * enable = 1 (the default when dim and ffn_hidden are multiples of 8) the
+ * f32 prefill's layer GEMMs and the trainer forward's lm_head run on
+ * bfloat16 MFMAs with both fp32 operands split exactly into three bfloat16
+ * terms and the six products down to 2^-16 of the full product accumulated
+ * in fp32: each product is carried to within 2^-23 relative, so results
+ * keep fp32 accuracy (the f32 path's 1e-3 bar) at about 1.5-1.9x the fp32
+ * MFMA kernel's speed.  The model then keeps a transposed fp32 copy of every
+ * layer matrix and of lm_head (refreshed by akh_model_upload_param).
+ * enable = 0 frees it and returns to the fp32-MFMA GEMMs.  The bf16-MFMA
+ * prefill (akh_model_set_prefill_bf16), when on, takes precedence. */
+akh_status akh_model_set_prefill_x6(akh_model* m, int enable);
 
 /* ---- the trainer's fused forward: src/nn/train.rs:256-275, 394-401 ------- */
 

@@ -356,3 +356,35 @@ def test_scaled_config_matches_oracle(backend, pkg, ora):
     finally:
         ora.set_threads(1)
     del w
+
+
+def test_prefill_x6_matches_fp32_mfma_and_oracle(backend, pkg, ora):
+    # The default prefill GEMMs (bf16 MFMAs on operands split exactly into
+    # three bfloat16 terms, six products) against the fp32-MFMA GEMMs
+    # (set_prefill_x6(False)) and the oracle: both meet the fp32 bar, agree
+    # with each other to fp32 rounding (1e-4) with the same tokens, and
+    # toggling back reproduces the first run bit for bit.  dim 256, head_dim
+    # 64, ffn 1024: ragged tiles at M = 3 x 70 rows.
+    cfg = pkg.ModelConfig.new(300, 256, 4, 2, 80)
+    w = pkg.synthetic_weights(cfg, seed=61)
+    model, s = _session(pkg, backend, cfg, w, 80, 3)
+    toks = pkg.synthetic_tokens(3 * 70, cfg.vocab_size, seed=62).reshape(3, 70)
+    lx, nx = s.prefill(toks)
+    kx = s.cache(1, 2, 0)[:70].copy()
+    model.set_prefill_x6(False)
+    s.reset()
+    lf, nf = s.prefill(toks)
+    assert np.abs(lx - lf).max() < 1e-4 and np.array_equal(nx, nf)
+    np.testing.assert_allclose(kx, s.cache(1, 2, 0)[:70], atol=1e-5)
+    model.set_prefill_x6(True)
+    s.reset()
+    lx2, nx2 = s.prefill(toks)
+    assert np.array_equal(lx, lx2) and np.array_equal(nx, nx2)
+    for b in (0, 2):
+        o = ora.OracleSession(cfg, w, 80)
+        ref = o.prefill(toks[b])
+        o.close()
+        for got, nxt in ((lx, nx), (lf, nf)):
+            assert np.abs(got[b] - ref).max() < TOL
+            assert int(nxt[b]) == ora.argmax(ref)
+

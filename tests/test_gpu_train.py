@@ -134,3 +134,46 @@ def test_forward_errors(backend, pkg):
     with pytest.raises(hip.InvalidArgument, match="out of the vocabulary"):
         f.loss(np.zeros(4, np.uint32), np.array([1, 2, 37, 3], np.uint32))
     f.close()
+
+
+def test_forward_x6_matches_fp32_mfma(backend, pkg, ora):
+    # The trainer forward's GEMMs (layers and the all-rows lm_head) on the
+    # split-bf16 kernel and on the fp32 MFMAs: losses and probabilities agree
+    # to fp32 rounding.  dim 64, 2 x 40 rows, vocab 300.
+    cfg = pkg.ModelConfig.new(300, 64, 4, 2, 40)
+    w = pkg.synthetic_weights(cfg, seed=64)
+    B, S = 2, 40
+    toks = np.stack([ora.rand_tokens(S, 300, 300 + b) for b in range(B)])
+    tgts = np.stack([ora.rand_tokens(S, 300, 400 + b) for b in range(B)])
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    f = pkg.hip.Forward(model, B, S)
+    mx, lx = f.loss(toks, tgts)
+    px = f.probs(0, B * S)
+    model.set_prefill_x6(False)
+    mf, lf = f.loss(toks, tgts)
+    np.testing.assert_allclose(lx, lf, atol=1e-5)
+    np.testing.assert_allclose(px, f.probs(0, B * S), atol=1e-6)
+    assert abs(mx - mf) < 1e-5
+    om, ol, _, _ = ora.forward_train(cfg, w, toks, tgts, B, S, False, False)
+    np.testing.assert_allclose(lx, ol, atol=1e-4)
+    f.close()
+
+
+def test_forward_x6_needs_multiples_of_8(backend, pkg, ora):
+    # dim 20 (5 heads of 4): the fp32-MFMA GEMMs run, and the split-bf16
+    # GEMMs cannot be switched on.
+    cfg = pkg.ModelConfig.new(37, 20, 5, 1, 11)
+    w = pkg.synthetic_weights(cfg, seed=65)
+    toks = np.stack([ora.rand_tokens(11, 37, 500 + b) for b in range(2)])
+    tgts = np.stack([ora.rand_tokens(11, 37, 600 + b) for b in range(2)])
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    with pytest.raises(pkg.hip.InvalidArgument, match="multiples of 8"):
+        model.set_prefill_x6(True)
+    model.set_prefill_x6(False)
+    f = pkg.hip.Forward(model, 2, 11)
+    mean, losses = f.loss(toks, tgts)
+    om, ol, _, _ = ora.forward_train(cfg, w, toks, tgts, 2, 11, False, False)
+    np.testing.assert_allclose(losses, ol, atol=1e-4)
+    f.close()
