@@ -599,16 +599,18 @@ __global__ __launch_bounds__(256) void k_transpose_f32(const float* __restrict__
 // (BM / WM) x 64 as TA x 2 MFMA tiles.  LDS holds the three planes of both
 // operands k-contiguous (rows of 16 k padded to 48 bytes, so 16-byte
 // fragment reads of 8 consecutive rows hit distinct banks), double
-// buffered; the next k step's global loads are issued before the MFMAs.  B
-// rows are stored permuted so lane j of column tile t reads column 2j + t
-// (adjacent column pairs for the paired epilogues).  K % 8 == 0.
+// buffered.  Global loads run two k steps ahead through two register sets;
+// each step splits and stores step k + 1 (loaded a step earlier) in the same
+// straight-line block as step k's MFMAs, so the split's VALU work and the
+// LDS writes overlap the matrix pipe.  K % 8 == 0.
 template <int EPI, int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
   constexpr int BK = 16, LD = BK + 8, NT = 64 * WM * WN;
   constexpr int TA = BM / WM / 32;
   static_assert(BN == 64 * WN && BM % (32 * WM) == 0, "wave tiles are (32 TA) x 64");
-  // k-octets staged per thread (some threads idle when fewer than NT).
-  constexpr int OA = (2 * BM + NT - 1) / NT, OB = (2 * BN + NT - 1) / NT;
+  constexpr int OA = 2 * BM / NT, OB = 2 * BN / NT;  // k-octets staged per thread
+  static_assert(OA >= 1 && OB >= 1 && OA * NT == 2 * BM && OB * NT == 2 * BN,
+                "every thread stages whole octets of both operands");
   __shared__ __align__(16) uint16_t As[2][3][BM][LD];
   __shared__ __align__(16) uint16_t Bs[2][3][BN][LD];
 
@@ -622,48 +624,68 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
   const int wm = wave / WN, wn = wave % WN;
   const int j = lane & 31, h = lane >> 5;
 
-  // Staging: octet o = tid + NT * i covers row o / 2, k (o % 2) * 8 .. + 7.
-  float4 fa[OA][2], fb[OB][2];
-  auto gload = [&](int k0) {
+  // Staging: octet o = tid + NT * i covers LDS row (o % 16) + 16 (o / 32),
+  // k 8 ((o / 16) % 2) .. + 7: lanes l and l + 16 load the two halves of one
+  // row in the same instruction, and 16 consecutive lanes write 16
+  // consecutive 48-byte rows (conflict-free).  B's LDS row L = 64 g + 32 t + jj holds column 64 g +
+  // 2 jj + t of the block (lane j of column tile t then reads column 2j + t:
+  // adjacent column pairs for the paired epilogues).
+  // Out-of-range octets load element 0 and are masked to zero when they are
+  // split: the loads stay unconditional (no exec-masked branch) and nothing
+  // touches their registers before the split, so the compiler can count
+  // them and wait for one register set while the other's loads are still
+  // in flight.
+  float4 ra[2][OA][2], rb[2][OB][2];
+  uint32_t ma[2][OA], mb[2][OB];
+  auto masked = [](float4 v, uint32_t m) {
+    return make_float4(__uint_as_float(__float_as_uint(v.x) & m),
+                       __uint_as_float(__float_as_uint(v.y) & m),
+                       __uint_as_float(__float_as_uint(v.z) & m),
+                       __uint_as_float(__float_as_uint(v.w) & m));
+  };
+  auto bcol = [](int L) { return (L & ~63) | ((L & 31) << 1) | ((L >> 5) & 1); };
+  auto orow = [](int o) { return (o & 15) | ((o >> 5) << 4); };
+  auto okof = [](int o) { return ((o >> 4) & 1) * 8; };
+  auto gload = [&](int k0, int set) {
 #pragma unroll
     for (int i = 0; i < OA; ++i) {
-      const int o = tid + NT * i, r = o >> 1, k = k0 + (o & 1) * 8, gm = m0 + r;
-      const bool in = o < 2 * BM && gm < M && k < K;
+      const int o = tid + NT * i, r = orow(o), k = k0 + okof(o), gm = m0 + r;
+      const bool in = gm < M && k < K;
+      ma[set][i] = in ? 0xFFFFFFFFu : 0u;
       const float* src = p.a + (size_t)(in ? gm : 0) * K + (in ? k : 0);
-      fa[i][0] = in ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
-      fa[i][1] = in ? *reinterpret_cast<const float4*>(src + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      ra[set][i][0] = *reinterpret_cast<const float4*>(src);
+      ra[set][i][1] = *reinterpret_cast<const float4*>(src + 4);
     }
 #pragma unroll
     for (int i = 0; i < OB; ++i) {
-      const int o = tid + NT * i, r = o >> 1, k = k0 + (o & 1) * 8, gn = n0 + r;
-      const bool in = o < 2 * BN && gn < N && k < K;
+      const int o = tid + NT * i, k = k0 + okof(o), gn = n0 + bcol(orow(o));
+      const bool in = gn < N && k < K;
+      mb[set][i] = in ? 0xFFFFFFFFu : 0u;
       const float* src = p.bt + (size_t)(in ? gn : 0) * K + (in ? k : 0);
-      fb[i][0] = in ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
-      fb[i][1] = in ? *reinterpret_cast<const float4*>(src + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      rb[set][i][0] = *reinterpret_cast<const float4*>(src);
+      rb[set][i][1] = *reinterpret_cast<const float4*>(src + 4);
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, int set) {
 #pragma unroll
     for (int i = 0; i < OA; ++i) {
-      const int o = tid + NT * i, r = o >> 1, k = (o & 1) * 8;
-      if (o >= 2 * BM) break;
+      const int o = tid + NT * i, r = orow(o), k = okof(o);
       uint4 t0, t1, t2;
-      split3_rne(fa[i][0], fa[i][1], t0, t1, t2);
+      split3_rne(masked(ra[set][i][0], ma[set][i]), masked(ra[set][i][1], ma[set][i]), t0, t1,
+                 t2);
       *reinterpret_cast<uint4*>(&As[buf][0][r][k]) = t0;
       *reinterpret_cast<uint4*>(&As[buf][1][r][k]) = t1;
       *reinterpret_cast<uint4*>(&As[buf][2][r][k]) = t2;
     }
 #pragma unroll
     for (int i = 0; i < OB; ++i) {
-      const int o = tid + NT * i, r = o >> 1, k = (o & 1) * 8;
-      if (o >= 2 * BN) break;
-      // Column c = 64 g + 2 jj + t of the block lives at LDS row 64 g + 32 t + jj.
-      const int br = (r & ~63) | ((r & 1) << 5) | ((r & 63) >> 1);
+      const int o = tid + NT * i, L = orow(o), k = okof(o);
       uint4 t0, t1, t2;
-      split3_rne(fb[i][0], fb[i][1], t0, t1, t2);
-      *reinterpret_cast<uint4*>(&Bs[buf][0][br][k]) = t0;
-      *reinterpret_cast<uint4*>(&Bs[buf][1][br][k]) = t1;
-      *reinterpret_cast<uint4*>(&Bs[buf][2][br][k]) = t2;
+      split3_rne(masked(rb[set][i][0], mb[set][i]), masked(rb[set][i][1], mb[set][i]), t0, t1,
+                 t2);
+      *reinterpret_cast<uint4*>(&Bs[buf][0][L][k]) = t0;
+      *reinterpret_cast<uint4*>(&Bs[buf][1][L][k]) = t1;
+      *reinterpret_cast<uint4*>(&Bs[buf][2][L][k]) = t2;
     }
   };
 
@@ -673,13 +695,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) acc[a][t] = zero16();
 
-  const int nk = (K + BK - 1) / BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
+  auto step = [&](int buf) {
     bf16x8 bfr[2][3];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -708,9 +724,36 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], bfr[t][0], acc[a][t]);
     }
-    if (kt + 1 < nk) lstore(buf ^ 1);
+  };
+
+  // Steps past the end load zeros (k >= K), so the pipeline needs no tail
+  // cases beyond skipping the last stores.
+  const int nk = (K + BK - 1) / BK;
+  gload(0, 0);
+  gload(BK, 1);
+  lstore(0, 0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    // Step kt (buffer 0, register set 1 holds step kt + 1), then kt + 1.
+    // Scheduling barriers keep each half's instructions in its half: the
+    // prefetch is issued first, and nothing that reads its registers moves
+    // up next to it (which would make the half wait for it).
+    __builtin_amdgcn_sched_barrier(0);
+    gload((kt + 2) * BK, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    lstore(1, 1);
+    step(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    gload((kt + 3) * BK, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    lstore(0, 0);
+    step(1);
     __syncthreads();
   }
+  __builtin_amdgcn_sched_barrier(0);
+  if (kt < nk) step(0);  // odd step count: the last step sits in buffer 0
 
 #pragma unroll
   for (int a = 0; a < TA; ++a)
@@ -949,7 +992,7 @@ hipError_t launch_gemm_bf16(const GemmParams& p, int epi, hipStream_t s) {
 hipError_t launch_gemm_x6(const GemmParams& p, int epi, hipStream_t s) {
   if (p.K % 8 != 0 || p.M <= 0 || p.N <= 0 || p.K <= 0 || !p.a || !p.bt)
     return hipErrorInvalidValue;
-  // 256x256 tiles when they fill the chip twice over, else 256x128 (fewer
+  // 256x256 tiles when they fill the chip twice over, else 128x128 (fewer
   // idle CUs on the last round of tiles); measured on MI355X.
   const bool big = (long)((p.M + 255) / 256) * ((p.N + 255) / 256) >= 512;
 #define AKH_X6_GO(E)                                                                        \
@@ -957,8 +1000,8 @@ hipError_t launch_gemm_x6(const GemmParams& p, int epi, hipStream_t s) {
     hipLaunchKernelGGL((k_gemm_x6<E, 256, 256, 2, 4>), dim3((p.N + 255) / 256, (p.M + 255) / 256), \
                        dim3(512), 0, s, p);                                                 \
   else                                                                                      \
-    hipLaunchKernelGGL((k_gemm_x6<E, 256, 128, 4, 2>), dim3((p.N + 127) / 128, (p.M + 255) / 256), \
-                       dim3(512), 0, s, p);
+    hipLaunchKernelGGL((k_gemm_x6<E, 128, 128, 2, 2>), dim3((p.N + 127) / 128, (p.M + 127) / 128), \
+                       dim3(256), 0, s, p);
   switch (epi) {
     case GEMM_STORE: AKH_X6_GO(GEMM_STORE) break;
     case GEMM_ADD: AKH_X6_GO(GEMM_ADD) break;
