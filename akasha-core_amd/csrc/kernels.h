@@ -115,6 +115,8 @@ struct FlashParams {
   const akh_flash_attn_meta* meta;  // per-shader path: S, dim, scale and
                                     // row_offset come from it (1 sequence)
   uint16_t* o16;  // launch_flash_bf16: bfloat16 output (o unused)
+  int x6;         // launch_flash, head_dim 64 / 128: split-bfloat16 MFMAs
+                  // (fp32 accuracy) instead of fp32 MFMAs
 };
 
 hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s);

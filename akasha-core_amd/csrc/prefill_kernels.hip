@@ -933,6 +933,234 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
   }
 }
 
+// Causal flash attention (head_dim 64 or 128) in fp32 accuracy on
+// v_mfma_f32_32x32x16_bf16: k_flash_bf16's structure (block = 4 waves x 32
+// queries, 32-key blocks, S^T = K Q^T so each lane owns one query, P^T fed
+// from the accumulators) with every fp32 operand split exactly into three
+// bfloat16 terms (split3_rne): Q once into registers, K and V^T into three
+// LDS planes per key block, the probabilities P per key block.  Both
+// contractions accumulate the six products down to 2^-16 of each full
+// product (as k_gemm_x6), so scores and outputs carry fp32-level error.
+// Softmax statistics, the output and lse are fp32, as in k_flash_mfma,
+// whose per-shader meta handling (row_offset) this follows.
+template <int HD>
+__global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
+  constexpr int QB = 128, KB = 32, NT = HD / 32, NQ = HD / 16;
+  constexpr int KP = HD + 8;   // K row stride (bf16)
+  constexpr int VP = KB + 8;   // V^T row stride (bf16)
+  constexpr int CPR = HD / 4;  // float4 per K/V row
+  constexpr int KPT = KB * CPR / 256;  // consecutive keys staged per thread
+  static_assert(KPT == 2 || KPT == 4, "staging covers 2 or 4 keys per thread");
+  constexpr int K_PLANE = KB * KP, V_PLANE = HD * VP;  // bf16 elements
+  constexpr int KV_BYTES = 3 * (K_PLANE + V_PLANE) * 2;
+  constexpr int O_BYTES = 4 * 32 * 33 * 4;
+  __shared__ __align__(16) unsigned char lds[KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES];
+  auto Ks = [&](int pl) { return reinterpret_cast<uint16_t (*)[KP]>(lds) + pl * KB; };
+  auto Vt = [&](int pl) {
+    return reinterpret_cast<uint16_t (*)[VP]>(lds + 3 * K_PLANE * 2) + pl * HD;
+  };
+
+  int S = p.S, d = p.d;
+  float scale = p.scale;
+  long roff = 0;
+  if (p.meta) {
+    S = (int)p.meta->seq_len;
+    d = (int)p.meta->dim;
+    scale = p.meta->scale;
+    roff = (long)p.meta->row_offset * d;
+  }
+  const int H = d / HD;
+  // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
+  const float qscale = scale * 1.44269504088896341f;
+  const int qblk = gridDim.x - 1 - blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int q0 = qblk * QB;
+  if (q0 >= S) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+
+  const float* qp = p.q + roff + (size_t)b * p.q_bs + hh * HD;
+  const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
+  const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
+
+  const int qi = q0 + wave * 32 + j;
+  uint4 qf[3][NQ];  // the three planes of dims 16 s + 8 h .. + 7 of query qi
+  {
+    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 8 * h;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s)
+      split3_rne(*reinterpret_cast<const float4*>(qr + 16 * s),
+                 *reinterpret_cast<const float4*>(qr + 16 * s + 4), qf[0][s], qf[1][s],
+                 qf[2][s]);
+  }
+  f32x16 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = zero16();
+  float mrow = -INFINITY, lrow = 0.f;
+
+  const int wave_qmin = q0 + wave * 32, wave_qmax = wave_qmin + 31;
+  const int kend = min(S, q0 + QB);
+  const int nkb = (kend + KB - 1) / KB;
+
+  // Staging: thread t takes dims 4 (t % CPR) .. + 3 of KPT consecutive keys
+  // from KPT (t / CPR), so K rows and V^T rows are both written 4 or 8 bytes
+  // at a time per plane.
+  const int sc = (tid % CPR) * 4, sk = (tid / CPR) * KPT;
+  float4 kr[KPT], vr[KPT];
+  auto load_kv = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int key = kb * KB + sk + i;
+      const size_t off = (size_t)(key < S ? key : 0) * d + sc;
+      kr[i] = *reinterpret_cast<const float4*>(kp + off);
+      vr[i] = *reinterpret_cast<const float4*>(vp + off);
+    }
+  };
+  // Three bfloat16 terms of a and b, packed as pairs (a_pl, b_pl).
+  auto split_pair = [](float a, float b, uint32_t (&t)[3]) {
+    t[0] = cvt_pk_bf16(a, b);
+    const float ra = a - __uint_as_float(t[0] << 16), rb = b - __uint_as_float(t[0] & 0xFFFF0000u);
+    t[1] = cvt_pk_bf16(ra, rb);
+    t[2] = cvt_pk_bf16(ra - __uint_as_float(t[1] << 16), rb - __uint_as_float(t[1] & 0xFFFF0000u));
+  };
+  load_kv(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      uint32_t lo[3], hi[3];
+      split_pair(kr[i].x, kr[i].y, lo);
+      split_pair(kr[i].z, kr[i].w, hi);
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        *reinterpret_cast<uint2*>(&Ks(pl)[sk + i][sc]) = make_uint2(lo[pl], hi[pl]);
+    }
+    // V^T: dim row sc + c, keys sk .. sk + KPT - 1.
+    const float vc[4][4] = {
+#define AKH_VCOL(f) {vr[0].f, vr[1].f, KPT == 4 ? vr[KPT - 2].f : 0.f, KPT == 4 ? vr[KPT - 1].f : 0.f}
+        AKH_VCOL(x), AKH_VCOL(y), AKH_VCOL(z), AKH_VCOL(w)
+#undef AKH_VCOL
+    };
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint32_t t01[3], t23[3];
+      split_pair(vc[c][0], vc[c][1], t01);
+      if constexpr (KPT == 4) {
+        split_pair(vc[c][2], vc[c][3], t23);
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][sk]) = make_uint2(t01[pl], t23[pl]);
+      } else {
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint32_t*>(&Vt(pl)[sc + c][sk]) = t01[pl];
+      }
+    }
+    __syncthreads();
+    load_kv(kb + 1);  // rows past S read row 0: harmless, never used
+    const int j0 = kb * KB;
+    if (j0 > wave_qmax) continue;
+
+    f32x16 st = zero16();
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      bf16x8 kf[3];
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        kf[pl] = bf16x8_of(*reinterpret_cast<const uint4*>(&Ks(pl)[j][16 * s + 8 * h]));
+      // Smallest terms first.
+      st = mfma_bf16(kf[2], bf16x8_of(qf[0][s]), st);
+      st = mfma_bf16(kf[1], bf16x8_of(qf[1][s]), st);
+      st = mfma_bf16(kf[0], bf16x8_of(qf[2][s]), st);
+      st = mfma_bf16(kf[1], bf16x8_of(qf[0][s]), st);
+      st = mfma_bf16(kf[0], bf16x8_of(qf[1][s]), st);
+      st = mfma_bf16(kf[0], bf16x8_of(qf[0][s]), st);
+    }
+
+    // Keys above a query (the diagonal block) or past S are masked.
+    const bool masked = j0 + KB - 1 > wave_qmin || j0 + KB > S;
+    float pm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = st[r] * qscale;
+      if (masked) {
+        const int key = j0 + acc_row(r, h);
+        if (key > qi || key >= S) v = -INFINITY;
+      }
+      st[r] = v;
+      pm = fmaxf(pm, v);
+    }
+    pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+    const float mnew = fmaxf(mrow, pm);  // finite: key 0 is in every query's range
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = __builtin_amdgcn_exp2f(st[r] - mnew);
+      st[r] = e;
+      ps += e;
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    const float corr = __builtin_amdgcn_exp2f(mrow - mnew);  // 0 on the first block
+    lrow = lrow * corr + ps;
+    if (__any(mnew != mrow)) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    }
+    mrow = mnew;
+    // P^T planes: MFMA 0 of the block takes entries 0..7 of each lane (keys
+    // acc_row(0..7, h)), MFMA 1 entries 8..15.
+    uint4 pf[2][3];
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+      split3_rne(make_float4(st[8 * half], st[8 * half + 1], st[8 * half + 2], st[8 * half + 3]),
+                 make_float4(st[8 * half + 4], st[8 * half + 5], st[8 * half + 6],
+                             st[8 * half + 7]),
+                 pf[half][0], pf[half][1], pf[half][2]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        // V^T rows of the same keys: two runs of four.
+        bf16x8 vf[3];
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+          const uint16_t* vrow = Vt(pl)[32 * t + j] + 16 * half;
+          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
+          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
+          vf[pl] = bf16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
+        }
+        o[t] = mfma_bf16(vf[2], bf16x8_of(pf[half][0]), o[t]);
+        o[t] = mfma_bf16(vf[1], bf16x8_of(pf[half][1]), o[t]);
+        o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][2]), o[t]);
+        o[t] = mfma_bf16(vf[1], bf16x8_of(pf[half][0]), o[t]);
+        o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][1]), o[t]);
+        o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][0]), o[t]);
+      }
+    }
+  }
+
+  // O^T (rows = dims) -> LDS, one 32-dim tile at a time -> coalesced rows.
+  const float inv = 1.0f / lrow;
+  float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33 * 4);
+  float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Os[j][acc_row(r, h)] = o[t][r] * inv;
+    __syncthreads();
+    for (int e = lane; e < 32 * 32; e += 64) {
+      const int r = e >> 5, c = e & 31;
+      const int qrow = q0 + wave * 32 + r;
+      if (qrow < S) op[(size_t)qrow * d + 32 * t + c] = Os[r][c];
+    }
+  }
+  if (p.lse && h == 0 && qi < S)  // max + ln(sum), back in natural units
+    p.lse[(size_t)b * p.lse_bs + (size_t)qi * H + hh] =
+        mrow * 0.69314718055994531f + logf(lrow);
+}
+
 // ---------------------------------------------------------------------------
 
 hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
@@ -952,10 +1180,16 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
   const int H = p.d / p.hd;
   if (p.hd == 64 || p.hd == 128) {
     const dim3 g((max_rows + 127) / 128, H, batch);
-    if (p.hd == 64)
+    if (p.x6) {
+      if (p.hd == 64)
+        hipLaunchKernelGGL(k_flash_x6<64>, g, dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL(k_flash_x6<128>, g, dim3(256), 0, s, p);
+    } else if (p.hd == 64) {
       hipLaunchKernelGGL(k_flash_mfma<64>, g, dim3(256), 0, s, p);
-    else
+    } else {
       hipLaunchKernelGGL(k_flash_mfma<128>, g, dim3(256), 0, s, p);
+    }
     return hipGetLastError();
   }
   dim3 g((max_rows + 63) / 64, H, batch), b(64);

@@ -1524,6 +1524,7 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     f.d = (int)d;
     f.hd = (int)hd;
     f.scale = 1.0f / sqrtf((float)hd);
+    f.x6 = s->m->prefill_x6 ? 1 : 0;
     TRY_HIP(launch_flash(f, (int)s->B, (int)S, st));
 
     GemmParams o{};

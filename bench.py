@@ -81,9 +81,9 @@ def prefill_rates(ms, gemm, attn, lm, x6_flop):
     """Rates of a prefill that took `ms`: useful fp32 TFLOP/s; their fraction
     of the fp32 MFMA peak (the roofline of fp32 arithmetic on this part);
     and the MFMA pipes' busy fraction, the executed MFMA work at the peak rate
-    of the instructions that ran it: the split-bfloat16 GEMMs (`x6_flop` of
-    the useful flops) execute six bf16 products per multiply-add at the bf16
-    peak, everything else runs on fp32 MFMAs."""
+    of the instructions that ran it: the split-bfloat16 GEMMs and flash
+    attention (`x6_flop` of the useful flops) execute six bf16 products per
+    multiply-add at the bf16 peak, everything else runs on fp32 MFMAs."""
     t = ms / 1e3
     useful = gemm + attn + lm
     busy = 6 * x6_flop / (BF16_MFMA_PEAK_TFLOPS * 1e12) + (useful - x6_flop) / (FP32_MFMA_PEAK_TFLOPS * 1e12)
@@ -157,14 +157,14 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
         pms = be.timer_stop()
         g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
         fl = g + a + lm
-        r = prefill_rates(pms, g, a, lm, g)
-        out.update({"prefill_gemms": "split-bf16 (fp32-accurate, default)",
+        r = prefill_rates(pms, g, a, lm, g + a)
+        out.update({"prefill_kernels": "split-bf16 GEMMs and flash (fp32-accurate, default)",
                     "prefill_ms": round(pms, 2), "prefill_tok_s": round(Bp * Sp / (pms / 1e3), 1),
                     "prefill_tflops": r["tflops"],
                     "prefill_fp32_roofline_frac": r["fp32_roofline_frac"],
                     "prefill_mfma_busy_frac": r["mfma_busy_frac"]})
-        # The same prefill with the layer GEMMs on the fp32 MFMAs.
-        log("bench: scaled config prefill 8 x 2048, fp32-MFMA GEMMs")
+        # The same prefill with the layer GEMMs and flash on the fp32 MFMAs.
+        log("bench: scaled config prefill 8 x 2048, fp32 MFMAs")
         model.set_prefill_x6(False)
         ps.reset()
         ps.prefill(toks, want_logits=False)
@@ -318,11 +318,11 @@ def main():
         g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
         fl = g + a + lm
         prefill = {"workload": "config 3: hall-1.0 fp32 prefill 16 x 512 (seed 3), last-row logits",
-                   "gemms": "split-bf16: fp32 operands as three bf16 terms, six products "
-                            "(fp32-accurate, the default)",
+                   "kernels": "split-bf16 GEMMs and flash: fp32 operands as three bf16 terms, "
+                              "six products (fp32-accurate, the default)",
                    "ms": round(pms, 3), "tok_s": round(Bp * Sp / (pms / 1e3), 1),
-                   **prefill_rates(pms, g, a, lm, g), "flop": fl}
-        # The same prefill with the layer GEMMs on the fp32 MFMAs.
+                   **prefill_rates(pms, g, a, lm, g + a), "flop": fl}
+        # The same prefill with the layer GEMMs and flash on the fp32 MFMAs.
         model.set_prefill_x6(False)
         ps.reset()
         ps.prefill(ptoks, want_logits=False)  # warm
@@ -335,7 +335,7 @@ def main():
             ftimes32.append(be.timer_stop())
         model.set_prefill_x6(True)
         p32 = min(ftimes32)
-        prefill["fp32_mfma_gemms"] = {"ms": round(p32, 3), "tok_s": round(Bp * Sp / (p32 / 1e3), 1),
+        prefill["fp32_mfma"] = {"ms": round(p32, 3), "tok_s": round(Bp * Sp / (p32 / 1e3), 1),
                                       "tflops": round(fl / (p32 / 1e3) / 1e12, 2),
                                       "mfma_frac": round(fl / (p32 / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
         ps.close()
@@ -356,7 +356,7 @@ def main():
         prefill["train_forward"] = {
             "workload": "Trainer::forward + CrossEntropy, 16 x 512 rows (seed 3), all-rows lm_head",
             "ms": round(fms, 3), "tok_s": round(Bp * Sp / (fms / 1e3), 1),
-            **prefill_rates(fms, g, a, flm, g + flm),
+            **prefill_rates(fms, g, a, flm, g + a + flm),
             "mean_loss": round(mean_loss, 4), "flop": ffl}
         fw.close()
 
@@ -407,12 +407,15 @@ def main():
     for _ in range(10):
         be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
     c2b_ms = be.timer_stop() / 10
+    rb = prefill_rates(c2b_ms, 0, c2_flop, 0, c2_flop)
     config2 = {"workload": "config 2: flash attention 8 x 12 x 512 x 64 (seed 2)",
+               "kernel": "split-bf16 flash (fp32-accurate)",
                "per_node_ms": round(c2_ms, 4),
                "per_node_tflops": round(c2_flop / (c2_ms / 1e3) / 1e12, 2),
                "batched_ms": round(c2b_ms, 4),
-               "batched_tflops": round(c2_flop / (c2b_ms / 1e3) / 1e12, 2),
-               "batched_mfma_frac": round(c2_flop / (c2b_ms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
+               "batched_tflops": rb["tflops"],
+               "batched_fp32_roofline_frac": rb["fp32_roofline_frac"],
+               "batched_mfma_busy_frac": rb["mfma_busy_frac"]}
 
     scaled = None
     if args.scaled:
