@@ -144,7 +144,9 @@ akh_status akh_cache_write(akh_backend* be, const float* src, float* cache,
 /* FLASH_ATTENTION, ops::flash_attention (emit.rs:556-597): causal
  * softmax(scale Q K^T) V for one sequence of rows [row_offset,
  * row_offset+seq_len) of [*, dim] buffers; l_cache[row*H + h] receives
- * max + ln(sum).  head_dim <= 128 (emit.rs:564-567). */
+ * max + ln(sum).  head_dim <= 128 (emit.rs:564-567).  head_dim 64 and
+ * 128 run on bf16 MFMAs with every fp32 operand split exactly into three
+ * bfloat16 terms (six products per contraction, fp32-level error). */
 akh_status akh_flash_attention(akh_backend* be, const float* q,
                                const float* k, const float* v, float* out,
                                float* l_cache, akh_flash_attn_meta shape,
@@ -280,7 +282,8 @@ akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16);
 akh_status akh_model_set_prefill_bf16(akh_model* m, int enable);
 /* No reference counterpart (a choice of kernel, not of numerics): with
  * enable = 1 (the default when dim and ffn_hidden are multiples of 8) the
- * f32 prefill's layer GEMMs and the trainer forward's lm_head run on
+ * f32 prefill's layer GEMMs and flash attention (head_dim 64 / 128) and the
+ * trainer forward's lm_head run on
  * bfloat16 MFMAs with both fp32 operands split exactly into three bfloat16
  * terms and the six products down to 2^-16 of the full product accumulated
  * in fp32: each product is carried to within 2^-23 relative, so results
