@@ -177,3 +177,22 @@ def test_forward_x6_needs_multiples_of_8(backend, pkg, ora):
     om, ol, _, _ = ora.forward_train(cfg, w, toks, tgts, 2, 11, False, False)
     np.testing.assert_allclose(losses, ol, atol=1e-4)
     f.close()
+
+
+def test_forward_x6_ragged_k(backend, pkg, ora):
+    # dim 40: K = 40 is a multiple of 8 but not of the split-bf16 GEMM's
+    # 16-wide k step (the last step is half masked); 2 x 11 rows and vocab 37
+    # leave every tile ragged in M and N.
+    cfg = pkg.ModelConfig.new(37, 40, 5, 1, 11)
+    w = pkg.synthetic_weights(cfg, seed=66)
+    toks = np.stack([ora.rand_tokens(11, 37, 700 + b) for b in range(2)])
+    tgts = np.stack([ora.rand_tokens(11, 37, 800 + b) for b in range(2)])
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    f = pkg.hip.Forward(model, 2, 11)
+    mean, losses = f.loss(toks, tgts)
+    om, ol, op, oh = ora.forward_train(cfg, w, toks, tgts, 2, 11, True, True)
+    np.testing.assert_allclose(losses, ol, atol=1e-4)
+    np.testing.assert_allclose(f.hidden(), oh, atol=1e-4)
+    np.testing.assert_allclose(f.probs(0, 22), op, atol=1e-5)
+    f.close()
