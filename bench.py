@@ -197,6 +197,68 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
     return out
 
 
+def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
+    """Config 3 (16 x 512 prefill, seed 3) on the default split-bf16 kernels
+    and on the fp32 MFMAs, then the trainer forward on the same rows."""
+    Bp, Sp = 16, 512
+    ps = hip.Session(model, CTX, Bp)
+    ptoks = pkg.synthetic_tokens(Bp * Sp, cfg.vocab_size, seed=3).reshape(Bp, Sp)
+    ps.prefill(ptoks, want_logits=False)  # warm
+    times = []
+    for _ in range(reps):
+        ps.reset()
+        be.synchronize()
+        be.timer_start()
+        ps.prefill(ptoks, want_logits=False)
+        times.append(be.timer_stop())
+    pms = min(times)
+    g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
+    fl = g + a + lm
+    prefill = {"workload": "config 3: hall-1.0 fp32 prefill 16 x 512 (seed 3), last-row logits",
+               "kernels": "split-bf16 GEMMs and flash: fp32 operands as three bf16 terms, "
+                          "six products (fp32-accurate, the default)",
+               "ms": round(pms, 3), "tok_s": round(Bp * Sp / (pms / 1e3), 1),
+               **prefill_rates(pms, g, a, lm, g + a), "flop": fl}
+    # The same prefill with the layer GEMMs and flash on the fp32 MFMAs.
+    model.set_prefill_x6(False)
+    ps.reset()
+    ps.prefill(ptoks, want_logits=False)  # warm
+    ftimes32 = []
+    for _ in range(reps):
+        ps.reset()
+        be.synchronize()
+        be.timer_start()
+        ps.prefill(ptoks, want_logits=False)
+        ftimes32.append(be.timer_stop())
+    model.set_prefill_x6(True)
+    p32 = min(ftimes32)
+    prefill["fp32_mfma"] = {"ms": round(p32, 3), "tok_s": round(Bp * Sp / (p32 / 1e3), 1),
+                            "tflops": round(fl / (p32 / 1e3) / 1e12, 2),
+                            "mfma_frac": round(fl / (p32 / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
+    ps.close()
+    # Trainer::forward + CrossEntropy on the same 16 x 512 rows: the
+    # lm_head runs on every row (+2 rows d V flop) and the loss follows.
+    fw = hip.Forward(model, Bp, Sp)
+    targets = np.roll(ptoks, -1, axis=1)
+    fw.loss(ptoks, targets)  # warm
+    ftimes = []
+    for _ in range(reps):
+        be.synchronize()
+        be.timer_start()
+        mean_loss, _ = fw.loss(ptoks, targets)
+        ftimes.append(be.timer_stop())
+    fms = min(ftimes)
+    g, a, flm = prefill_flop_parts(cfg, Bp, Sp, lm_rows=Bp * Sp)
+    ffl = g + a + flm
+    prefill["train_forward"] = {
+        "workload": "Trainer::forward + CrossEntropy, 16 x 512 rows (seed 3), all-rows lm_head",
+        "ms": round(fms, 3), "tok_s": round(Bp * Sp / (fms / 1e3), 1),
+        **prefill_rates(fms, g, a, flm, g + a + flm),
+        "mean_loss": round(mean_loss, 4), "flop": ffl}
+    fw.close()
+    return prefill
+
+
 def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=1):
     ora = entry.load_oracle()
     ora.set_threads(threads)
@@ -227,6 +289,8 @@ def main():
                     help="also measure config 5 (scaled architecture) decode and prefill")
     ap.add_argument("--no-scaled-decode", action="store_true",
                     help="with --scaled, measure config 5's prefill legs only")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="measure only config 3's prefill legs and print them (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -243,6 +307,12 @@ def main():
     be = hip.Backend(0)
     model = hip.Model(be, cfg)
     model.upload(w)
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=2)}),
+              flush=True)
+        model.close()
+        be.close()
+        return
     sess = hip.Session(model, CTX, B)
     prompt = pkg.synthetic_tokens(B * P, cfg.vocab_size, seed=4).reshape(B, P)
     log("bench: prefill 32 x 448")
@@ -301,64 +371,7 @@ def main():
     kernels = {n: {"ms": round(kms[n], 5), "bytes": kbytes[n],
                    "GB/s": round(kbytes[n] / (kms[n] / 1e3) / 1e9, 1)} for n in names}
 
-    prefill = None
-    if not args.no_prefill:
-        Bp, Sp = 16, 512
-        ps = hip.Session(model, CTX, Bp)
-        ptoks = pkg.synthetic_tokens(Bp * Sp, cfg.vocab_size, seed=3).reshape(Bp, Sp)
-        ps.prefill(ptoks, want_logits=False)  # warm
-        times = []
-        for _ in range(3):
-            ps.reset()
-            be.synchronize()
-            be.timer_start()
-            ps.prefill(ptoks, want_logits=False)
-            times.append(be.timer_stop())
-        pms = min(times)
-        g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
-        fl = g + a + lm
-        prefill = {"workload": "config 3: hall-1.0 fp32 prefill 16 x 512 (seed 3), last-row logits",
-                   "kernels": "split-bf16 GEMMs and flash: fp32 operands as three bf16 terms, "
-                              "six products (fp32-accurate, the default)",
-                   "ms": round(pms, 3), "tok_s": round(Bp * Sp / (pms / 1e3), 1),
-                   **prefill_rates(pms, g, a, lm, g + a), "flop": fl}
-        # The same prefill with the layer GEMMs and flash on the fp32 MFMAs.
-        model.set_prefill_x6(False)
-        ps.reset()
-        ps.prefill(ptoks, want_logits=False)  # warm
-        ftimes32 = []
-        for _ in range(3):
-            ps.reset()
-            be.synchronize()
-            be.timer_start()
-            ps.prefill(ptoks, want_logits=False)
-            ftimes32.append(be.timer_stop())
-        model.set_prefill_x6(True)
-        p32 = min(ftimes32)
-        prefill["fp32_mfma"] = {"ms": round(p32, 3), "tok_s": round(Bp * Sp / (p32 / 1e3), 1),
-                                      "tflops": round(fl / (p32 / 1e3) / 1e12, 2),
-                                      "mfma_frac": round(fl / (p32 / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
-        ps.close()
-        # Trainer::forward + CrossEntropy on the same 16 x 512 rows: the
-        # lm_head runs on every row (+2 rows d V flop) and the loss follows.
-        fw = hip.Forward(model, Bp, Sp)
-        targets = np.roll(ptoks, -1, axis=1)
-        fw.loss(ptoks, targets)  # warm
-        ftimes = []
-        for _ in range(3):
-            be.synchronize()
-            be.timer_start()
-            mean_loss, _ = fw.loss(ptoks, targets)
-            ftimes.append(be.timer_stop())
-        fms = min(ftimes)
-        g, a, flm = prefill_flop_parts(cfg, Bp, Sp, lm_rows=Bp * Sp)
-        ffl = g + a + flm
-        prefill["train_forward"] = {
-            "workload": "Trainer::forward + CrossEntropy, 16 x 512 rows (seed 3), all-rows lm_head",
-            "ms": round(fms, 3), "tok_s": round(Bp * Sp / (fms / 1e3), 1),
-            **prefill_rates(fms, g, a, flm, g + a + flm),
-            "mean_loss": round(mean_loss, 4), "flop": ffl}
-        fw.close()
+    prefill = None if args.no_prefill else prefill_measurement(pkg, hip, be, model, cfg, CTX)
 
     # Config 1: batch-1 greedy latency (64-token prompt, seed 1; 64 steps).
     s1 = hip.Session(model, 128, 1)
