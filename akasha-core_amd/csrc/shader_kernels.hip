@@ -450,7 +450,15 @@ __device__ __forceinline__ float block_red1024(float v, float* red, bool is_max)
 // CROSS_ENTROPY (cpu.rs:277-306), one 1024-thread block per row, in place:
 // m = row max, s = sum of e^(x - m), loss = -(x[target] - m - ln s), and the
 // row becomes e^(x - m) / s.  A target id >= vocab has no logit; its loss is
-// NaN (the reference indexes out of bounds there).
+// NaN (the reference indexes out of bounds there).  The first 1024 * kCeRegs
+// entries of the row stay in registers between the passes (one read and one
+// write of the row for vocabularies up to 65536); entries past them are
+// re-read.  They move through a buffer resource over the row: one
+// per-lane offset and a scalar offset per entry instead of a 64-bit address
+// each, and reads past the row return zero.  Each thread folds its entries
+// in index order either way, so the results do not depend on where an entry
+// was held.
+constexpr int kCeRegs = 64;
 __global__ __launch_bounds__(1024) void k_cross_entropy(float* x, const uint32_t* targets,
                                                         float* losses,
                                                         const akh_cross_entropy_meta* meta) {
@@ -458,18 +466,38 @@ __global__ __launch_bounds__(1024) void k_cross_entropy(float* x, const uint32_t
   const uint32_t V = meta->vocab_size, row = blockIdx.x;
   if (row >= meta->num_rows) return;
   float* r = x + (size_t)row * V;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(r, (short)0, (int)(V * 4u), 0x00020000);
+  const uint32_t tid = threadIdx.x, held = 1024u * kCeRegs;
+  const int vo = (int)(tid * 4u);
+  float v[kCeRegs];
   float m = -INFINITY;
-  for (uint32_t i = threadIdx.x; i < V; i += 1024) m = fmaxf(m, r[i]);
+#pragma unroll
+  for (int e = 0; e < kCeRegs; ++e) {
+    const float t = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, vo, e * 4096, 0));
+    v[e] = tid + 1024u * e < V ? t : -INFINITY;
+    m = fmaxf(m, v[e]);
+  }
+  for (uint32_t i = held + tid; i < V; i += 1024) m = fmaxf(m, r[i]);
   m = block_red1024(m, red, true);
   float sum = 0.f;
-  for (uint32_t i = threadIdx.x; i < V; i += 1024) sum += expf(r[i] - m);
+#pragma unroll
+  for (int e = 0; e < kCeRegs; ++e) {
+    v[e] = expf(v[e] - m);  // 0 past the end of the row
+    sum += v[e];
+  }
+  for (uint32_t i = held + tid; i < V; i += 1024) sum += expf(r[i] - m);
   sum = block_red1024(sum, red, false);
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     const uint32_t t = targets[row];
     losses[row] = t < V ? -(r[t] - m - logf(sum)) : __builtin_nanf("");
   }
   __syncthreads();  // the target's logit is read before the row is rewritten
-  for (uint32_t i = threadIdx.x; i < V; i += 1024) r[i] = expf(r[i] - m) / sum;
+  // Stores past the end of the row are dropped by the resource's range.
+#pragma unroll
+  for (int e = 0; e < kCeRegs; ++e)
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[e] / sum), rs, vo, e * 4096, 0);
+  for (uint32_t i = held + tid; i < V; i += 1024) r[i] = expf(r[i] - m) / sum;
 }
 
 hipError_t shader_qkv_split(const float* src, float* q, float* k, float* v,
