@@ -215,4 +215,20 @@ __device__ __forceinline__ float4 sum_parts4(float4 acc, const float* p,
   return acc;
 }
 
+// sum_parts4 issuing NB1 loads at a time while at least NB1 remain, then NB2.
+template <int NB1, int NB2>
+__device__ __forceinline__ float4 sum_parts4_2(float4 acc, const float* p, size_t stride,
+                                               int n) {
+  int s = 0;
+  for (; s + NB1 <= n; s += NB1) {
+    float4 t[NB1];
+#pragma unroll
+    for (int i = 0; i < NB1; ++i)
+      t[i] = *reinterpret_cast<const float4*>(p + (size_t)(s + i) * stride);
+#pragma unroll
+    for (int i = 0; i < NB1; ++i) add4(acc, t[i]);
+  }
+  return sum_parts4<NB2>(acc, p + (size_t)s * stride, stride, n - s);
+}
+
 }  // namespace akh
