@@ -106,6 +106,12 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
 // the operands of v_mfma_f32_32x32x16_bf16, with A split exactly into three
 // bfloat16 terms (split3_bf16): every product is exact, so the result has
 // fp32 accuracy at 3 x 32 instead of 8 x 64 MFMA cycles per 16 k.
+#ifndef AKH_GEMM_NT
+#define AKH_GEMM_NT 1
+#endif
+#ifndef AKH_LM_GEMM_NT
+#define AKH_LM_GEMM_NT 0
+#endif
 template <int W, int HL, int EPI, int PRO, bool BF>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   constexpr int RH = W > 1 ? W / 2 : 1;
@@ -130,19 +136,23 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   f32x16 acc = zero16();
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;  // first k-quad of this half
-    // The pass's weights: bfloat16 octets or float quads.
+    // The pass's weights: bfloat16 octets or float quads, read once per
+    // step, so non-temporal in the layer GEMMs (a measured 2 % per decode
+    // step, though each GEMM alone is a little slower).  The lm_head (many
+    // passes per block) streams better through the caches.
+    constexpr bool kNT = AKH_GEMM_NT && (AKH_LM_GEMM_NT || EPI != DEC_LOGITS);
     using WRaw = typename std::conditional<BF, uint4, float4>::type;
     constexpr int NW = BF ? HQ / 2 : HQ;
+    typedef float f4 __attribute__((ext_vector_type(4)));
     WRaw wc[NW];
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
       const int kq = kq0 + (BF ? 2 * i : i);  // BF: even, HL is a multiple of 8
-      if constexpr (BF)
-        wc[i] = 4 * kq < ke ? *reinterpret_cast<const uint4*>(wh + (size_t)kq * 128)
-                            : make_uint4(0u, 0u, 0u, 0u);
-      else
-        wc[i] = 4 * kq < ke ? *reinterpret_cast<const float4*>(wt + (size_t)kq * 128)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
+      const f4* src = reinterpret_cast<const f4*>(BF ? static_cast<const void*>(wh + (size_t)kq * 128)
+                                                     : static_cast<const void*>(wt + (size_t)kq * 128));
+      const f4 t = 4 * kq < ke ? (kNT ? __builtin_nontemporal_load(src) : *src)
+                               : f4{0.f, 0.f, 0.f, 0.f};
+      wc[i] = __builtin_bit_cast(WRaw, t);
     }
     float4 a[HQ];
 #pragma unroll
@@ -267,6 +277,9 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
 // 32x32 tiles are summed in LDS (waves in order), each wave finishing 32/W
 // rows: it stores their logits and keeps a running (value, index) maximum
 // per row.  amax[m, b] is the first maximum of row m over block b's columns.
+#ifndef AKH_LM_CPOL
+#define AKH_LM_CPOL 0
+#endif
 template <int HQ>
 __device__ __forceinline__ void lm_load_b(float4 (&bb)[HQ], __amdgpu_buffer_rsrc_t w,
                                           uint32_t voff, int ntiles, int Kp, int tile) {
@@ -274,8 +287,10 @@ __device__ __forceinline__ void lm_load_b(float4 (&bb)[HQ], __amdgpu_buffer_rsrc
   const int so = tile * Kp * 128;
 #pragma unroll
   for (int q = 0; q < HQ; ++q) {
+    // Cache policy AKH_LM_CPOL: 0 (cached) measured faster per decode step
+    // than 2 (non-temporal) here.
     const f32x4v v = __builtin_bit_cast(
-        f32x4v, __builtin_amdgcn_raw_buffer_load_b128(w, (int)vo, so + q * 512, 0));
+        f32x4v, __builtin_amdgcn_raw_buffer_load_b128(w, (int)vo, so + q * 512, AKH_LM_CPOL));
     bb[q] = make_float4(v.x, v.y, v.z, v.w);
   }
 }
@@ -426,17 +441,30 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   // The first row batch is requested before the new token's q, k, v, so the
   // two memory round trips overlap.
   // Rows are held as loaded (bfloat16 pairs stay packed until used).
+  // The rows are read once per step: non-temporal loads keep them from
+  // displacing the caches' other contents (measured ~10 % faster streaming).
   using Raw = typename std::conditional<KV16, uint2, float4>::type;
   Raw kv[RB], vv[RB];
   bool ok[RB];
+  auto nt_load = [](const KT* p) -> Raw {
+    if constexpr (KV16) {
+      typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+      const u2 t = __builtin_nontemporal_load(reinterpret_cast<const u2*>(p));
+      return make_uint2(t.x, t.y);
+    } else {
+      typedef float f4 __attribute__((ext_vector_type(4)));
+      const f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+      return make_float4(t.x, t.y, t.z, t.w);
+    }
+  };
   auto load_batch = [&](int base) {
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
       const int r = base + i * RPW + rl;
       ok[i] = r < r1;
       const size_t off = (size_t)(ok[i] ? r : r0) * d;
-      kv[i] = ok[i] ? *reinterpret_cast<const Raw*>(kbase + off) : Raw{};
-      vv[i] = ok[i] ? *reinterpret_cast<const Raw*>(vbase + off) : Raw{};
+      kv[i] = ok[i] ? nt_load(kbase + off) : Raw{};
+      vv[i] = ok[i] ? nt_load(vbase + off) : Raw{};
     }
   };
   auto wide = [](const Raw& x) -> float4 {
