@@ -277,6 +277,34 @@ def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=
     return n / dt, n, dt
 
 
+def cpu_prefill_baseline(cfg, weights, tokens, threads):
+    """The oracle's prefill of one prompt (the reference CPU backend's
+    InferenceSession::prefill restated), tok/s."""
+    ora = entry.load_oracle()
+    ora.set_threads(threads)
+    s = ora.OracleSession(cfg, weights, cfg.seq_len)
+    t0 = time.perf_counter()
+    s.prefill(tokens)
+    dt = time.perf_counter() - t0
+    s.close()
+    ora.set_threads(1)
+    return len(tokens) / dt, dt
+
+
+def host_cpu():
+    """(model name, logical CPUs) of the host."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return name, os.cpu_count() or 1
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -446,6 +474,15 @@ def main():
         nt = min(16, os.cpu_count() or 1)
         vN, nN, tN = cpu_baseline(cfg, w, P, budget_s=6.0, threads=nt)
         cpu_omp = {"value": round(vN, 3), "cores": nt, "steps": nN, "seconds": round(tN, 2)}
+        # A labelled prefill slice: one 64-token prompt of config 3's seed.
+        log(f"bench: CPU baseline (oracle prefill of 64 tokens, {nt} threads)")
+        ptok = pkg.synthetic_tokens(16 * 512, cfg.vocab_size, seed=3)[:64]
+        vp, tp = cpu_prefill_baseline(cfg, w, ptok, nt)
+        cname, ncpu = host_cpu()
+        cpu["host"] = cpu_omp["host"] = {"cpu_model": cname, "nproc": ncpu}
+        cpu_omp["prefill"] = {"value": round(vp, 2), "unit": "tok/s", "cores": nt,
+                              "sample": f"oracle prefill of the first 64 tokens of config 3's "
+                                        f"sequence 0 ({tp:.1f} s)"}
     else:
         cpu_omp = None
 
