@@ -15,6 +15,7 @@
 // tiles; the consumer of each GEMM sums the partials in a fixed order.
 // Nothing synchronises across work-groups inside a kernel and no atomics
 // are used, so results are deterministic.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -908,7 +909,7 @@ static_assert(AttnCfg::SP <= kMaxAttnSplits, "too many attention splits");
 int dec_attn_splits() { return AttnCfg::SP; }
 
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
-                           hipStream_t s) {
+                           hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
   constexpr int AW = AttnCfg::AW, RB = AttnCfg::RB, SP = AttnCfg::SP;
   // Row groups in flight for a bfloat16 cache (config 5: 8 beat 16, 24, 32).
 #ifndef AKH_ATTN_KV16_RB
@@ -916,11 +917,19 @@ hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
 #endif
   constexpr int RB16 = AKH_ATTN_KV16_RB;
   dim3 g(batch * p.H * SP), b(64 * AW);
-#define AKH_ATTN(HD)                                                               \
-  if (p.kv16)                                                                      \
-    hipLaunchKernelGGL((k_dec_attn<HD, AW, RB16, SP, true>), g, b, 0, s, p);      \
+  // With events, the dispatch itself carries their timestamps
+  // (hipExtLaunchKernelGGL): t0 to t1 spans the kernel alone.
+#define AKH_ATTN_GO(K)                                                             \
+  if (t0)                                                                          \
+    hipExtLaunchKernelGGL(K, g, b, 0, s, t0, t1, 0, p);                             \
   else                                                                             \
-    hipLaunchKernelGGL((k_dec_attn<HD, AW, RB, SP, false>), g, b, 0, s, p);
+    hipLaunchKernelGGL(K, g, b, 0, s, p);
+#define AKH_ATTN(HD)                                                               \
+  if (p.kv16) {                                                                    \
+    AKH_ATTN_GO((k_dec_attn<HD, AW, RB16, SP, true>))                              \
+  } else {                                                                         \
+    AKH_ATTN_GO((k_dec_attn<HD, AW, RB, SP, false>))                               \
+  }
   switch (hd) {
     case 4: AKH_ATTN(4) break;
     case 8: AKH_ATTN(8) break;
@@ -931,6 +940,7 @@ hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
     default: return hipErrorInvalidValue;
   }
 #undef AKH_ATTN
+#undef AKH_ATTN_GO
   return hipGetLastError();
 }
 

@@ -243,8 +243,9 @@ int dec_attn_splits();
 // (sequence b at b * seq_stride, row t at t * d).
 hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
                                 int batch, int S, int d, long seq_stride, hipStream_t s);
+// With t0 and t1 set, the dispatch records them at its own start and end.
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
-                           hipStream_t s);
+                           hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 
 // Per-row residual update + RMSNorm: x = table[ids[m]] (zero row if the id
 // is out of vocab), or src row (row0 + m * row_stride), or xt + the sum of

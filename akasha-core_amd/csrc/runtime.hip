@@ -1044,7 +1044,8 @@ hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
 
 // q/k/v split + RoPE + cache append + cached attention
 // (inference_graphs.rs:385-456): one kernel.
-hipError_t enqueue_attn(akh_session* s, uint32_t l) {
+hipError_t enqueue_attn(akh_session* s, uint32_t l, hipEvent_t t0 = nullptr,
+                        hipEvent_t t1 = nullptr) {
   const akh_model_config& c = s->m->cfg;
   DecAttnParams p{};
   p.qkv = s->p_qkv;
@@ -1062,7 +1063,7 @@ hipError_t enqueue_attn(akh_session* s, uint32_t l) {
   p.d = (int)c.dim;
   const uint32_t hd = c.dim / c.num_heads;
   p.scale = 1.0f / sqrtf((float)hd);
-  return launch_dec_attn(p, (int)s->B, (int)hd, s->be->stream);
+  return launch_dec_attn(p, (int)s->B, (int)hd, s->be->stream, t0, t1);
 }
 
 // out_proj (inference_graphs.rs:458-470): partial tiles.
@@ -2012,6 +2013,34 @@ extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,
   float ms = 0.f;
   HIP_TRY(hipEventElapsedTime(&ms, be->t0, be->t1));
   *avg_ms = ms / (float)reps;
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_session_time_decode_attn(akh_session* s, uint32_t reps,
+                                                   float* avg_ms) {
+  CHECK_ARG(s && avg_ms && reps > 0 && reps <= 4096,
+            "akh_session_time_decode_attn: bad argument");
+  for (uint32_t b = 0; b < s->B; ++b)
+    CHECK_ARG(s->cur_len[b] >= 1 && s->cur_len[b] < s->max_ctx,
+              "akh_session_time_decode_attn: needs 1 <= cur_len < max_ctx");
+  const uint32_t L = s->m->cfg.num_layers;
+  std::vector<hipEvent_t> ev(2 * (size_t)reps, nullptr);
+  hipError_t e = hipSuccess;
+  for (size_t i = 0; i < ev.size() && e == hipSuccess; ++i) e = hipEventCreate(&ev[i]);
+  for (uint32_t l = 0; l < L && e == hipSuccess; ++l) e = enqueue_attn(s, l);  // warm
+  for (uint32_t i = 0; i < reps && e == hipSuccess; ++i)
+    e = enqueue_attn(s, i % L, ev[2 * i], ev[2 * i + 1]);
+  if (e == hipSuccess) e = hipStreamSynchronize(s->be->stream);
+  double total = 0.0;
+  for (uint32_t i = 0; i < reps && e == hipSuccess; ++i) {
+    float ms = 0.f;
+    e = hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
+    total += ms;
+  }
+  for (hipEvent_t x : ev)
+    if (x) hipEventDestroy(x);
+  HIP_TRY(e);
+  *avg_ms = (float)(total / reps);
   return AKH_OK;
 }
 

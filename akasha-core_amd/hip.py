@@ -226,6 +226,7 @@ _SIGS = {
     "akh_timer_start": (ST, [P]),
     "akh_timer_stop": (ST, [P, C.POINTER(C.c_float)]),
     "akh_session_time_decode_kernel": (ST, [P, C.c_int, U32, C.POINTER(C.c_float)]),
+    "akh_session_time_decode_attn": (ST, [P, U32, C.POINTER(C.c_float)]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -722,6 +723,14 @@ class Session:
         ms = C.c_float()
         _check(_lib.akh_session_time_decode_kernel(self.handle, kernel, reps, C.byref(ms)),
                "time_decode_kernel")
+        return ms.value
+
+    def time_decode_attn(self, reps: int) -> float:
+        """Mean duration (ms) of the decode attention dispatch alone, from
+        events the dispatches carry (no gaps between launches)."""
+        ms = C.c_float()
+        _check(_lib.akh_session_time_decode_attn(self.handle, reps, C.byref(ms)),
+               "time_decode_attn")
         return ms.value
 
     def close(self):

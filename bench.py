@@ -383,6 +383,11 @@ def main():
     names = ["decode_attn", "qkv_proj", "out_proj", "ffn_up", "ffn_down",
              "lm_head_argmax", "resid_norm"]
     kms = {n: sess.time_decode_kernel(i, args.kernel_reps) for i, n in enumerate(names)}
+    # The roofline divides by the back-to-back launches' mean (two events
+    # around all of them, the gaps between launches included).  Beside it,
+    # the attention's duration per dispatch from events the dispatches carry
+    # themselves (no gaps).
+    attn_dispatch_ms = sess.time_decode_attn(args.kernel_reps)
     d, L, V, F = cfg.dim, cfg.num_layers, cfg.vocab_size, cfg.ffn_hidden
     # Compulsory bytes per launch: weights once, activations in and out once.
     attn_bytes = 2 * B * T * d * 4 + 2 * B * d * 4
@@ -508,6 +513,8 @@ def main():
                    "model": "akasha-hall-1.0 (162M)", "global_batch": B, "seq_len": CTX,
                    "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": "decode_attn (T=481, layers cycled)", "bound": "hbm",
+                     "kernel_ms": round(kms["decode_attn"], 5),
+                     "dispatch_ms": round(attn_dispatch_ms, 5),
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes": attn_bytes},

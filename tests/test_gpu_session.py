@@ -392,3 +392,21 @@ def test_prefill_x6_matches_fp32_mfma_and_oracle(backend, pkg, ora):
             assert np.abs(got[b] - ref).max() < TOL
             assert int(nxt[b]) == ora.argmax(ref)
 
+
+
+def test_decode_kernel_timers(backend, pkg):
+    # akh_session_time_decode_attn (events carried by the dispatches) times
+    # the attention kernel alone: positive and no longer than back-to-back
+    # launches with their gaps; both reject bad arguments.
+    cfg = pkg.ModelConfig.new(97, 64, 4, 2, 64)
+    w = pkg.synthetic_weights(cfg, seed=71)
+    _, s = _session(pkg, backend, cfg, w, 64, 4)
+    s.prefill(pkg.synthetic_tokens(4 * 20, cfg.vocab_size, seed=72).reshape(4, 20),
+              want_logits=False)
+    one = s.time_decode_attn(64)
+    b2b = s.time_decode_kernel(0, 64)
+    assert 0 < one <= b2b * 1.05
+    with pytest.raises(pkg.hip.InvalidArgument):
+        s.time_decode_attn(0)
+    with pytest.raises(pkg.hip.InvalidArgument):
+        s.time_decode_kernel(7, 4)
