@@ -223,7 +223,7 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
   }
   const int H = d / HD;
   const float qscale = scale * 1.44269504088896341f;
-  const int qblk = gridDim.x - 1 - blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -791,7 +791,7 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
   const int S = p.S, d = p.d;
   // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
   const float qscale = p.scale * 1.44269504088896341f;
-  const int qblk = gridDim.x - 1 - blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -972,7 +972,7 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   const int H = d / HD;
   // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
   const float qscale = scale * 1.44269504088896341f;
-  const int qblk = gridDim.x - 1 - blockIdx.x, hh = blockIdx.y, b = blockIdx.z;
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1179,7 +1179,10 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
                         hipStream_t s) {
   const int H = p.d / p.hd;
   if (p.hd == 64 || p.hd == 128) {
-    const dim3 g((max_rows + 127) / 128, H, batch);
+    // Query blocks slowest and last-first: every (sequence, head)'s longest
+    // causal block is dispatched before any shorter one, so the grid ends on
+    // short blocks (longest-first scheduling).
+    const dim3 g(H, batch, (max_rows + 127) / 128);
     if (p.x6) {
       if (p.hd == 64)
         hipLaunchKernelGGL(k_flash_x6<64>, g, dim3(256), 0, s, p);
@@ -1263,7 +1266,7 @@ hipError_t launch_transpose_bf16(const float* w, int K, int N, uint16_t* wt, hip
 
 hipError_t launch_flash_bf16(const FlashParams& p, int batch, int max_rows, hipStream_t s) {
   if (p.meta || !p.o16) return hipErrorInvalidValue;
-  const dim3 g((max_rows + 127) / 128, p.d / p.hd, batch);
+  const dim3 g(p.d / p.hd, batch, (max_rows + 127) / 128);  // as launch_flash
   if (p.hd == 64)
     hipLaunchKernelGGL(k_flash_bf16<64>, g, dim3(256), 0, s, p);
   else if (p.hd == 128)
