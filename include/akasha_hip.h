@@ -443,8 +443,8 @@ akh_status akh_session_time_decode_kernel(akh_session* s, int kernel,
 /* The decode attention kernel alone: `reps` (at most 4096) dispatches
  * cycling over the layers, as akh_session_time_decode_kernel(s, 0, ...),
  * each carrying its own start and end events (hipExtLaunchKernelGGL), so
- * the mean excludes the gaps between dispatches -- the figure a kernel
- * trace reports.  No counterpart in the reference (measurement only). */
+ * the mean excludes the gaps between dispatches.  No counterpart in the
+ * reference (measurement only). */
 akh_status akh_session_time_decode_attn(akh_session* s, uint32_t reps, float* avg_ms);
 
 #ifdef __cplusplus
