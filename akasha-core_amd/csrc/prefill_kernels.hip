@@ -1161,6 +1161,234 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
         mrow * 0.69314718055994531f + logf(lrow);
 }
 
+// k_flash_x6 for grids too small to fill the part (a single sequence's
+// FLASH_ATTENTION node): one 32-query tile per block, its key blocks dealt
+// round-robin to the 4 waves.  Each wave stages its own K and V^T planes in
+// a private LDS region (no block barrier in the key loop) and keeps its own
+// softmax state; at the end the four partial states merge through LDS:
+// M = max m_w, O = sum O_w 2^(m_w - M) / sum l_w 2^(m_w - M).  The heaviest
+// tile walks a quarter of the key blocks on its critical path.  Scores,
+// products and statistics are those of k_flash_x6.
+template <int HD>
+__global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
+  constexpr int KB = 32, NW = 4, NT = HD / 32, NQ = HD / 16;
+  constexpr int KP = HD + 8, VP = KB + 8, CPR = HD / 4;
+  constexpr int KPT = KB * CPR / 64;  // consecutive keys staged per lane
+  static_assert(KPT == 8, "a wave stages 32 keys as 4 groups of 8");
+  constexpr int K_PLANE = KB * KP, V_PLANE = HD * VP;  // bf16 elements
+  constexpr int W_BYTES = 3 * (K_PLANE + V_PLANE) * 2;
+  constexpr int OS = 33;                                // merge row stride
+  constexpr int M_BYTES = NW * (HD * OS + 64) * 4;
+  __shared__ __align__(16) unsigned char lds[NW * W_BYTES > M_BYTES ? NW * W_BYTES : M_BYTES];
+
+  int S = p.S, d = p.d;
+  float scale = p.scale;
+  long roff = 0;
+  if (p.meta) {
+    S = (int)p.meta->seq_len;
+    d = (int)p.meta->dim;
+    scale = p.meta->scale;
+    roff = (long)p.meta->row_offset * d;
+  }
+  const int H = d / HD;
+  const float qscale = scale * 1.44269504088896341f;
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
+  const int q0 = qblk * 32;
+  if (q0 >= S) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  unsigned char* wl = lds + wave * W_BYTES;
+  auto Ks = [&](int pl) { return reinterpret_cast<uint16_t (*)[KP]>(wl) + pl * KB; };
+  auto Vt = [&](int pl) {
+    return reinterpret_cast<uint16_t (*)[VP]>(wl + 3 * K_PLANE * 2) + pl * HD;
+  };
+
+  const float* qp = p.q + roff + (size_t)b * p.q_bs + hh * HD;
+  const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
+  const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
+
+  const int qi = q0 + j;
+  uint4 qf[3][NQ];
+  {
+    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 8 * h;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s)
+      split3_rne(*reinterpret_cast<const float4*>(qr + 16 * s),
+                 *reinterpret_cast<const float4*>(qr + 16 * s + 4), qf[0][s], qf[1][s],
+                 qf[2][s]);
+  }
+  f32x16 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = zero16();
+  float mrow = -INFINITY, lrow = 0.f;
+
+  const int kend = min(S, q0 + 32);
+  const int nkb = (kend + KB - 1) / KB;
+
+  // Staging: lane l takes dims 4 (l % CPR) .. + 3 of keys 8 (l / CPR) .. + 7.
+  const int sc = (lane % CPR) * 4, sk = (lane / CPR) * KPT;
+  float4 kr[KPT], vr[KPT];
+  auto load_kv = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int key = kb * KB + sk + i;
+      const size_t off = (size_t)(key < S ? key : 0) * d + sc;
+      kr[i] = *reinterpret_cast<const float4*>(kp + off);
+      vr[i] = *reinterpret_cast<const float4*>(vp + off);
+    }
+  };
+  auto split_pair = [](float a, float c, uint32_t (&t)[3]) {
+    t[0] = cvt_pk_bf16(a, c);
+    const float ra = a - __uint_as_float(t[0] << 16), rc = c - __uint_as_float(t[0] & 0xFFFF0000u);
+    t[1] = cvt_pk_bf16(ra, rc);
+    t[2] = cvt_pk_bf16(ra - __uint_as_float(t[1] << 16), rc - __uint_as_float(t[1] & 0xFFFF0000u));
+  };
+  if (wave < nkb) load_kv(wave);
+  for (int kb = wave; kb < nkb; kb += NW) {
+    // The wave's own region: its reads of the previous key block were
+    // issued before these writes, and one wave's LDS operations complete in
+    // order; the wave barrier keeps the compiler from moving them across.
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      uint32_t lo[3], hi[3];
+      split_pair(kr[i].x, kr[i].y, lo);
+      split_pair(kr[i].z, kr[i].w, hi);
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        *reinterpret_cast<uint2*>(&Ks(pl)[sk + i][sc]) = make_uint2(lo[pl], hi[pl]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint32_t t[4][3];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 a = vr[2 * g], e = vr[2 * g + 1];
+        const float x0 = c == 0 ? a.x : c == 1 ? a.y : c == 2 ? a.z : a.w;
+        const float x1 = c == 0 ? e.x : c == 1 ? e.y : c == 2 ? e.z : e.w;
+        split_pair(x0, x1, t[g]);
+      }
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        *reinterpret_cast<uint4*>(&Vt(pl)[sc + c][sk]) =
+            make_uint4(t[0][pl], t[1][pl], t[2][pl], t[3][pl]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the writes have landed
+    __builtin_amdgcn_wave_barrier();
+    if (kb + NW < nkb) load_kv(kb + NW);
+    const int j0 = kb * KB;
+
+    f32x16 st = zero16();
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      bf16x8 kf[3];
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        kf[pl] = bf16x8_of(*reinterpret_cast<const uint4*>(&Ks(pl)[j][16 * s + 8 * h]));
+      st = mfma_bf16(kf[2], bf16x8_of(qf[0][s]), st);
+      st = mfma_bf16(kf[1], bf16x8_of(qf[1][s]), st);
+      st = mfma_bf16(kf[0], bf16x8_of(qf[2][s]), st);
+      st = mfma_bf16(kf[1], bf16x8_of(qf[0][s]), st);
+      st = mfma_bf16(kf[0], bf16x8_of(qf[1][s]), st);
+      st = mfma_bf16(kf[0], bf16x8_of(qf[0][s]), st);
+    }
+    const bool masked = j0 + KB - 1 > q0 || j0 + KB > S;
+    float pm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = st[r] * qscale;
+      if (masked) {
+        const int key = j0 + acc_row(r, h);
+        if (key > qi || key >= S) v = -INFINITY;
+      }
+      st[r] = v;
+      pm = fmaxf(pm, v);
+    }
+    pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+    // Every block this wave takes has a key at or below each query of the
+    // tile except on the diagonal, where key j0 <= q0 <= qi: pm is finite.
+    const float mnew = fmaxf(mrow, pm);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = __builtin_amdgcn_exp2f(st[r] - mnew);
+      st[r] = e;
+      ps += e;
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    const float corr = __builtin_amdgcn_exp2f(mrow - mnew);
+    lrow = lrow * corr + ps;
+    if (__any(mnew != mrow)) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    }
+    mrow = mnew;
+    uint4 pf[2][3];
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+      split3_rne(make_float4(st[8 * half], st[8 * half + 1], st[8 * half + 2], st[8 * half + 3]),
+                 make_float4(st[8 * half + 4], st[8 * half + 5], st[8 * half + 6],
+                             st[8 * half + 7]),
+                 pf[half][0], pf[half][1], pf[half][2]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        bf16x8 vf[3];
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+          const uint16_t* vrow = Vt(pl)[32 * t + j] + 16 * half;
+          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
+          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
+          vf[pl] = bf16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
+        }
+        o[t] = mfma_bf16(vf[2], bf16x8_of(pf[half][0]), o[t]);
+        o[t] = mfma_bf16(vf[1], bf16x8_of(pf[half][1]), o[t]);
+        o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][2]), o[t]);
+        o[t] = mfma_bf16(vf[1], bf16x8_of(pf[half][0]), o[t]);
+        o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][1]), o[t]);
+        o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][0]), o[t]);
+      }
+    }
+  }
+
+  // Merge.  Wave w's O^T goes to Om[w][dim][query] and its (m, l) per query
+  // to ML[w]; a wave that took no key block holds m = -inf, l = 0, O = 0.
+  __syncthreads();
+  float* Om = reinterpret_cast<float*>(lds);
+  float2* ML = reinterpret_cast<float2*>(lds + NW * HD * OS * 4);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Om[(wave * HD + 32 * t + acc_row(r, h)) * OS + j] = o[t][r];
+  if (h == 0) ML[wave * 32 + j] = make_float2(mrow, lrow);
+  __syncthreads();
+  float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD;
+  for (int e = tid; e < 32 * HD; e += 256) {
+    const int qr = e / HD, dim = e % HD, qrow = q0 + qr;
+    if (qrow >= S) continue;
+    float2 ml[NW];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      ml[w] = ML[w * 32 + qr];
+      mx = fmaxf(mx, ml[w].x);  // finite: wave 0 took key block 0
+    }
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = __builtin_amdgcn_exp2f(ml[w].x - mx);
+      num += Om[(w * HD + dim) * OS + qr] * f;
+      den += ml[w].y * f;
+    }
+    op[(size_t)qrow * d + dim] = num / den;
+    if (p.lse && dim == 0)
+      p.lse[(size_t)b * p.lse_bs + (size_t)qrow * H + hh] = mx * 0.69314718055994531f + logf(den);
+  }
+}
+
 // ---------------------------------------------------------------------------
 
 hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
@@ -1175,6 +1403,21 @@ hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The part's CU count: below it, a 128-query flash grid leaves CUs idle.
+static int flash_small_grid() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0)
+      n = cus;
+    else
+      n = 256;
+  }
+  return n;
+}
+
 hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
                         hipStream_t s) {
   const int H = p.d / p.hd;
@@ -1183,7 +1426,12 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
     // causal block is dispatched before any shorter one, so the grid ends on
     // short blocks (longest-first scheduling).
     const dim3 g(H, batch, (max_rows + 127) / 128);
-    if (p.x6) {
+    if (p.x6 && p.hd == 64 && (long)g.x * g.y * g.z < flash_small_grid()) {
+      // Fewer 128-query blocks than CUs: 32-query tiles, keys split over
+      // the block's waves (k_flash_x6w).
+      hipLaunchKernelGGL(k_flash_x6w<64>, dim3(H, batch, (max_rows + 31) / 32), dim3(256), 0,
+                         s, p);
+    } else if (p.x6) {
       if (p.hd == 64)
         hipLaunchKernelGGL(k_flash_x6<64>, g, dim3(256), 0, s, p);
       else

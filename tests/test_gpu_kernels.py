@@ -186,15 +186,19 @@ def test_flash_attention_c2_config(backend, pkg, ora):
         sl = slice(b * S * d, (b + 1) * S * d)
         ref = ora.causal_attention(q[sl], k[sl], v[sl], S, d, hd)
         assert np.abs(got[b] - ref).max() < 1e-3
-    # The same 8 nodes as one batched launch: identical outputs, and each
-    # node's l_cache block in turn.
+    # The same 8 nodes as one batched launch, and each node's l_cache block
+    # in turn.  A single node's grid is too small for the part, so it runs
+    # the key-split kernel (32-query tiles, keys dealt to 4 waves, partial
+    # states merged); the batched grid runs the 128-query kernel: the two
+    # agree to fp32 rounding.
     out2, lse2 = backend.zeros(B * S * d), backend.zeros(B * S * H)
     shape = h.FlashAttnMeta(S, d, hd, 0.125, 0)
     backend.flash_attention_batched(tq, tk, tv, out2, lse2, shape, _meta(backend, shape), B)
-    assert np.array_equal(out2.download().reshape(B, S * d), got)
+    np.testing.assert_allclose(out2.download().reshape(B, S * d), got, rtol=0, atol=2e-6)
     last = h.FlashAttnMeta(S, d, hd, 0.125, (B - 1) * S)
     backend.flash_attention(tq, tk, tv, out, lse, last, _meta(backend, last))
-    assert np.array_equal(lse2.download()[(B - 1) * S * H:], lse.download())
+    np.testing.assert_allclose(lse2.download()[(B - 1) * S * H:], lse.download(), rtol=0,
+                               atol=2e-6)
 
 
 @pytest.mark.parametrize("attn_len,heads,hd", [(1, 2, 4), (5, 3, 16), (33, 12, 64)])
