@@ -630,18 +630,21 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
   // consecutive 48-byte rows (conflict-free).  B's LDS row L = 64 g + 32 t + jj holds column 64 g +
   // 2 jj + t of the block (lane j of column tile t then reads column 2j + t:
   // adjacent column pairs for the paired epilogues).
-  // Out-of-range octets load element 0 and are masked to zero when they are
-  // split: the loads stay unconditional (no exec-masked branch) and nothing
-  // touches their registers before the split, so the compiler can count
-  // them and wait for one register set while the other's loads are still
-  // in flight.
+  // Loads go through buffer resources bounded to the block's rows of A and
+  // B^T: octets past M or N fall outside them, octets past K get an offset
+  // outside them, and the hardware returns zeros for both.  The loads stay
+  // unconditional (no exec-masked branch) and nothing touches their
+  // registers before the split, so the compiler can count them and wait for
+  // one register set while the other's loads are still in flight.
   float4 ra[2][OA][2], rb[2][OB][2];
-  uint32_t ma[2][OA], mb[2][OB];
-  auto masked = [](float4 v, uint32_t m) {
-    return make_float4(__uint_as_float(__float_as_uint(v.x) & m),
-                       __uint_as_float(__float_as_uint(v.y) & m),
-                       __uint_as_float(__float_as_uint(v.z) & m),
-                       __uint_as_float(__float_as_uint(v.w) & m));
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.a + (size_t)m0 * K), (short)0, min(M - m0, BM) * K * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.bt + (size_t)n0 * K), (short)0, min(N - n0, BN) * K * 4, 0x00020000);
+  auto ld4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t vo, int so) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, so, 0));
+    return make_float4(v.x, v.y, v.z, v.w);
   };
   auto bcol = [](int L) { return (L & ~63) | ((L & 31) << 1) | ((L >> 5) & 1); };
   auto orow = [](int o) { return (o & 15) | ((o >> 5) << 4); };
@@ -649,21 +652,17 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
   auto gload = [&](int k0, int set) {
 #pragma unroll
     for (int i = 0; i < OA; ++i) {
-      const int o = tid + NT * i, r = orow(o), k = k0 + okof(o), gm = m0 + r;
-      const bool in = gm < M && k < K;
-      ma[set][i] = in ? 0xFFFFFFFFu : 0u;
-      const float* src = p.a + (size_t)(in ? gm : 0) * K + (in ? k : 0);
-      ra[set][i][0] = *reinterpret_cast<const float4*>(src);
-      ra[set][i][1] = *reinterpret_cast<const float4*>(src + 4);
+      const int o = tid + NT * i, k = k0 + okof(o);
+      const uint32_t vo = k < K ? (uint32_t)(orow(o) * K + k) * 4u : 0x80000000u;
+      ra[set][i][0] = ld4(rsa, vo, 0);
+      ra[set][i][1] = ld4(rsa, vo, 16);
     }
 #pragma unroll
     for (int i = 0; i < OB; ++i) {
-      const int o = tid + NT * i, k = k0 + okof(o), gn = n0 + bcol(orow(o));
-      const bool in = gn < N && k < K;
-      mb[set][i] = in ? 0xFFFFFFFFu : 0u;
-      const float* src = p.bt + (size_t)(in ? gn : 0) * K + (in ? k : 0);
-      rb[set][i][0] = *reinterpret_cast<const float4*>(src);
-      rb[set][i][1] = *reinterpret_cast<const float4*>(src + 4);
+      const int o = tid + NT * i, k = k0 + okof(o);
+      const uint32_t vo = k < K ? (uint32_t)(bcol(orow(o)) * K + k) * 4u : 0x80000000u;
+      rb[set][i][0] = ld4(rsb, vo, 0);
+      rb[set][i][1] = ld4(rsb, vo, 16);
     }
   };
   auto lstore = [&](int buf, int set) {
@@ -671,8 +670,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
     for (int i = 0; i < OA; ++i) {
       const int o = tid + NT * i, r = orow(o), k = okof(o);
       uint4 t0, t1, t2;
-      split3_rne(masked(ra[set][i][0], ma[set][i]), masked(ra[set][i][1], ma[set][i]), t0, t1,
-                 t2);
+      split3_rne(ra[set][i][0], ra[set][i][1], t0, t1, t2);
       *reinterpret_cast<uint4*>(&As[buf][0][r][k]) = t0;
       *reinterpret_cast<uint4*>(&As[buf][1][r][k]) = t1;
       *reinterpret_cast<uint4*>(&As[buf][2][r][k]) = t2;
@@ -681,8 +679,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
     for (int i = 0; i < OB; ++i) {
       const int o = tid + NT * i, L = orow(o), k = okof(o);
       uint4 t0, t1, t2;
-      split3_rne(masked(rb[set][i][0], mb[set][i]), masked(rb[set][i][1], mb[set][i]), t0, t1,
-                 t2);
+      split3_rne(rb[set][i][0], rb[set][i][1], t0, t1, t2);
       *reinterpret_cast<uint4*>(&Bs[buf][0][L][k]) = t0;
       *reinterpret_cast<uint4*>(&Bs[buf][1][L][k]) = t1;
       *reinterpret_cast<uint4*>(&Bs[buf][2][L][k]) = t2;
@@ -1475,7 +1472,9 @@ hipError_t launch_gemm_bf16(const GemmParams& p, int epi, hipStream_t s) {
 }
 
 hipError_t launch_gemm_x6(const GemmParams& p, int epi, hipStream_t s) {
-  if (p.K % 8 != 0 || p.M <= 0 || p.N <= 0 || p.K <= 0 || !p.a || !p.bt)
+  // K bounded so a block's rows (at most 256 of K floats) fit a buffer
+  // resource's 32-bit byte range.
+  if (p.K % 8 != 0 || p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K > (1 << 20) || !p.a || !p.bt)
     return hipErrorInvalidValue;
   // 256x256 tiles when they fill the chip twice over, else 128x128 (fewer
   // idle CUs on the last round of tiles); measured on MI355X.
