@@ -468,28 +468,34 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
   const int j = lane & 31, h = lane >> 5;
 
   // Global -> register staging: rows tid / 4 and tid / 4 + 128, eight k at
-  // (tid % 4) * 8, of both A and B^T.
+  // (tid % 4) * 8, of both A and B^T.  Loads go through buffer resources
+  // bounded to the block's rows; rows past M or N and octets past K (given
+  // an offset outside the resource) read zeros from the hardware.
   const int sr = tid >> 2, sk = (tid & 3) * 8;
   uint4 ra[2], rb[2];
   float4 fa[2][2];  // A32 staging
+  const int ea = A32 ? 4 : 2;  // bytes per A element
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      A32 ? (void*)(p.a + (size_t)m0 * K) : (void*)(p.a16 + (size_t)m0 * K), (short)0,
+      min(M - m0, BM) * K * ea, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.bt16 + (size_t)n0 * K), (short)0, min(N - n0, BN) * K * 2, 0x00020000);
+  auto ld = [](__amdgpu_buffer_rsrc_t rs, uint32_t vo, int so) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, so, 0));
+  };
   auto gload = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = sr + 128 * i, k = k0 + sk;
-      const int gm = m0 + r, gn = n0 + r;
+      const uint32_t off = (uint32_t)(r * K + k);
+      const uint32_t va = k < K ? off * ea : 0x80000000u, vb = k < K ? off * 2 : 0x80000000u;
       if (A32) {
-        const bool in = gm < M && k < K;
-        const float* src = p.a + (size_t)gm * K + k;
-        fa[i][0] = in ? *reinterpret_cast<const float4*>(src)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
-        fa[i][1] = in ? *reinterpret_cast<const float4*>(src + 4)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        fa[i][0] = __builtin_bit_cast(float4, ld(rsa, va, 0));
+        fa[i][1] = __builtin_bit_cast(float4, ld(rsa, va, 16));
       } else {
-        ra[i] = (gm < M && k < K) ? *reinterpret_cast<const uint4*>(p.a16 + (size_t)gm * K + k)
-                                  : make_uint4(0u, 0u, 0u, 0u);
+        ra[i] = ld(rsa, va, 0);
       }
-      rb[i] = (gn < N && k < K) ? *reinterpret_cast<const uint4*>(p.bt16 + (size_t)gn * K + k)
-                                : make_uint4(0u, 0u, 0u, 0u);
+      rb[i] = ld(rsb, vb, 0);
     }
   };
   auto lstore = [&](int buf) {
@@ -500,16 +506,16 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
       const int br = (r & ~63) | ((r & 1) << 5) | ((r & 63) >> 1);
       if (A32) {
         const float4 x0 = fa[i][0], x1 = fa[i][1];
-        const uint4 hi = make_uint4(pack_bf16x2(x0.x, x0.y), pack_bf16x2(x0.z, x0.w),
-                                    pack_bf16x2(x1.x, x1.y), pack_bf16x2(x1.z, x1.w));
+        const uint4 hi = make_uint4(cvt_pk_bf16(x0.x, x0.y), cvt_pk_bf16(x0.z, x0.w),
+                                    cvt_pk_bf16(x1.x, x1.y), cvt_pk_bf16(x1.z, x1.w));
         const float4 h0 = make_float4(__uint_as_float(hi.x << 16), __uint_as_float(hi.x & 0xFFFF0000u),
                                       __uint_as_float(hi.y << 16), __uint_as_float(hi.y & 0xFFFF0000u));
         const float4 h1 = make_float4(__uint_as_float(hi.z << 16), __uint_as_float(hi.z & 0xFFFF0000u),
                                       __uint_as_float(hi.w << 16), __uint_as_float(hi.w & 0xFFFF0000u));
-        const uint4 lo = make_uint4(pack_bf16x2(x0.x - h0.x, x0.y - h0.y),
-                                    pack_bf16x2(x0.z - h0.z, x0.w - h0.w),
-                                    pack_bf16x2(x1.x - h1.x, x1.y - h1.y),
-                                    pack_bf16x2(x1.z - h1.z, x1.w - h1.w));
+        const uint4 lo = make_uint4(cvt_pk_bf16(x0.x - h0.x, x0.y - h0.y),
+                                    cvt_pk_bf16(x0.z - h0.z, x0.w - h0.w),
+                                    cvt_pk_bf16(x1.x - h1.x, x1.y - h1.y),
+                                    cvt_pk_bf16(x1.z - h1.z, x1.w - h1.w));
         *reinterpret_cast<uint4*>(&As[0][buf][r][sk]) = hi;
         *reinterpret_cast<uint4*>(&As[NA - 1][buf][r][sk]) = lo;
       } else {
@@ -1453,7 +1459,9 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
 }
 
 hipError_t launch_gemm_bf16(const GemmParams& p, int epi, hipStream_t s) {
-  if (p.K % 8 != 0 || p.M <= 0 || p.N <= 0 || p.K <= 0) return hipErrorInvalidValue;
+  // K bounded so a block's 256 rows fit a buffer resource's byte range.
+  if (p.K % 8 != 0 || p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K > (1 << 20))
+    return hipErrorInvalidValue;
   if (!p.a == !p.a16) return hipErrorInvalidValue;
   dim3 g((p.N + 255) / 256, (p.M + 255) / 256), b(512);
 #define AKH_GO(E)                                                 \
