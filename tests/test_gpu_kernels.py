@@ -167,6 +167,31 @@ def test_flash_attention(backend, pkg, ora, seq, heads, hd):
             assert np.abs(lse.reshape(seq, heads)[:, hh] - ref_l).max() < 1e-5
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_flash_attention_live_meta_bounds_work(backend, pkg, ora, hd):
+    # The grid is sized from the recorded shape (200 rows); the meta read
+    # when the kernel runs says 150: rows 0..149 are attention over the first
+    # 150 tokens, rows past them stay untouched, and l_cache covers 150 rows.
+    # hd 64 runs the key-split kernel (a small grid), hd 128 the 128-query one.
+    h = pkg.hip
+    heads, S, live = 2, 200, 150
+    dim = heads * hd
+    q, k, v = (ora.rand_vec(S * dim, 40 + i) for i in range(3))
+    out = backend.tensor(np.full(S * dim, 7.0, np.float32))
+    lse = backend.tensor(np.full(S * heads, 7.0, np.float32))
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    shape = h.FlashAttnMeta(S, dim, hd, scale, 0)
+    meta = _meta(backend, h.FlashAttnMeta(live, dim, hd, scale, 0))
+    backend.flash_attention(backend.tensor(q), backend.tensor(k), backend.tensor(v), out, lse,
+                            shape, meta)
+    got = out.download().reshape(S, dim)
+    ref = ora.causal_attention(q[:live * dim], k[:live * dim], v[:live * dim], live, dim, hd)
+    assert np.abs(got[:live] - ref.reshape(live, dim)).max() < 1e-4
+    assert np.all(got[live:] == 7.0)
+    l = lse.download().reshape(S, heads)
+    assert np.all(np.isfinite(l[:live])) and np.all(l[live:] == 7.0)
+
+
 def test_flash_attention_c2_config(backend, pkg, ora):
     # Config 2: batch 8, 12 heads, seq 512, head_dim 64, N(0,1)
     # from seed 2, scale 1/8; sequences are row_offset slices of [8*512, 768].
