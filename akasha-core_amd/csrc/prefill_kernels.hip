@@ -609,7 +609,7 @@ __global__ __launch_bounds__(256) void k_transpose_f32(const float* __restrict__
 // each step splits and stores step k + 1 (loaded a step earlier) in the same
 // straight-line block as step k's MFMAs, so the split's VALU work and the
 // LDS writes overlap the matrix pipe.  K % 8 == 0.
-template <int EPI, int BM, int BN, int WM, int WN>
+template <int EPI, int BM, int BN, int WM, int WN, bool IL>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
   constexpr int BK = 16, LD = BK + 8, NT = 64 * WM * WN;
   constexpr int TA = BM / WM / 32;
@@ -698,6 +698,42 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) acc[a][t] = zero16();
 
+  // One k step: in two parts (the fragment reads of LDS buffer `buf`, the
+  // MFMAs on them) for the interleaved schedule, in one (`step`) otherwise.
+  typedef bf16x8 Frags[2 + TA][3];  // [0..1]: B column tiles, [2 + a]: A row tiles
+  auto frags = [&](int buf, Frags& f) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        f[t][pl] = bf16x8_of(
+            *reinterpret_cast<const uint4*>(&Bs[buf][pl][wn * 64 + t * 32 + j][8 * h]));
+#pragma unroll
+    for (int a = 0; a < TA; ++a)
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        f[2 + a][pl] = bf16x8_of(
+            *reinterpret_cast<const uint4*>(&As[buf][pl][wm * (32 * TA) + a * 32 + j][8 * h]));
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int a = 0; a < TA; ++a) {
+      const bf16x8* af = f[2 + a];
+      // Smallest terms first.
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[2], f[t][0], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[1], f[t][1], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], f[t][2], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[1], f[t][0], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], f[t][1], acc[a][t]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], f[t][0], acc[a][t]);
+    }
+  };
   auto step = [&](int buf) {
     bf16x8 bfr[2][3];
 #pragma unroll
@@ -713,7 +749,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
       for (int pl = 0; pl < 3; ++pl)
         af[pl] = bf16x8_of(
             *reinterpret_cast<const uint4*>(&As[buf][pl][wm * (32 * TA) + a * 32 + j][8 * h]));
-      // Smallest terms first.
 #pragma unroll
       for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[2], bfr[t][0], acc[a][t]);
 #pragma unroll
@@ -726,6 +761,32 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
       for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], bfr[t][1], acc[a][t]);
 #pragma unroll
       for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[0], bfr[t][0], acc[a][t]);
+    }
+  };
+  // Step `buf` while the next step (register set `set`) is split into the
+  // other buffer.  Without IL the compiler issues the whole split, then the
+  // MFMAs (the fragment reads follow the LDS writes, which may alias them).
+  // With IL the reads come first and the MFMAs are spread one per group of
+  // VALU instructions, so the matrix pipe runs while the same wave splits;
+  // it measured faster for K = 768 and slower for K = 3072 and at 256 x 256.
+  auto half = [&](int buf, int set) {
+    Frags f;
+    if constexpr (IL) {
+      frags(buf, f);
+      lstore(1 - buf, set);
+      mma(f);
+      constexpr int NMF = TA * 2 * 6;
+      constexpr int NVAL = (OA + OB) * 44 / NMF + 1;
+      __builtin_amdgcn_sched_group_barrier(0x100, 6 + 3 * TA, 0);  // DS reads
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, NVAL, 0);  // VALU
+      }
+      __builtin_amdgcn_sched_group_barrier(0x200, 3 * (OA + OB), 0);  // DS writes
+    } else {
+      lstore(1 - buf, set);
+      step(buf);
     }
   };
 
@@ -745,14 +806,12 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
     gload((kt + 2) * BK, 0);
     __builtin_amdgcn_sched_barrier(0);
-    lstore(1, 1);
-    step(0);
+    half(0, 1);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     gload((kt + 3) * BK, 1);
     __builtin_amdgcn_sched_barrier(0);
-    lstore(0, 0);
-    step(1);
+    half(1, 0);
     __syncthreads();
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -1487,13 +1546,18 @@ hipError_t launch_gemm_x6(const GemmParams& p, int epi, hipStream_t s) {
   // 256x256 tiles when they fill the chip twice over, else 128x128 (fewer
   // idle CUs on the last round of tiles); measured on MI355X.
   const bool big = (long)((p.M + 255) / 256) * ((p.N + 255) / 256) >= 512;
+  // 128 x 128 tiles interleave MFMAs with the split where K is short.
+  const bool il = p.K <= 1024;
 #define AKH_X6_GO(E)                                                                        \
   if (big)                                                                                  \
-    hipLaunchKernelGGL((k_gemm_x6<E, 256, 256, 2, 4>), dim3((p.N + 255) / 256, (p.M + 255) / 256), \
-                       dim3(512), 0, s, p);                                                 \
+    hipLaunchKernelGGL((k_gemm_x6<E, 256, 256, 2, 4, false>),                               \
+                       dim3((p.N + 255) / 256, (p.M + 255) / 256), dim3(512), 0, s, p);      \
+  else if (il)                                                                              \
+    hipLaunchKernelGGL((k_gemm_x6<E, 128, 128, 2, 2, true>),                                \
+                       dim3((p.N + 127) / 128, (p.M + 127) / 128), dim3(256), 0, s, p);      \
   else                                                                                      \
-    hipLaunchKernelGGL((k_gemm_x6<E, 128, 128, 2, 2>), dim3((p.N + 127) / 128, (p.M + 127) / 128), \
-                       dim3(256), 0, s, p);
+    hipLaunchKernelGGL((k_gemm_x6<E, 128, 128, 2, 2, false>),                               \
+                       dim3((p.N + 127) / 128, (p.M + 127) / 128), dim3(256), 0, s, p);
   switch (epi) {
     case GEMM_STORE: AKH_X6_GO(GEMM_STORE) break;
     case GEMM_ADD: AKH_X6_GO(GEMM_ADD) break;
