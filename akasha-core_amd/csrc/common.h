@@ -197,8 +197,9 @@ __device__ __forceinline__ void add4(float4& a, const float4 b) {
 }
 
 // acc + p[0] + p[stride] + ... + p[(n - 1) * stride], added in index order.
-// The loads are issued NB at a time, so NB partials cost one memory latency
-// instead of NB dependent ones.
+// The loads are issued NB at a time, the remainder (fewer than NB) as one
+// more batch, so up to NB partials cost one memory latency instead of NB
+// dependent ones.
 template <int NB>
 __device__ __forceinline__ float4 sum_parts4(float4 acc, const float* p,
                                              size_t stride, int n) {
@@ -211,7 +212,15 @@ __device__ __forceinline__ float4 sum_parts4(float4 acc, const float* p,
 #pragma unroll
     for (int i = 0; i < NB; ++i) add4(acc, t[i]);
   }
-  for (; s < n; ++s) add4(acc, *reinterpret_cast<const float4*>(p + (size_t)s * stride));
+  if (s < n) {
+    float4 t[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      if (s + i < n) t[i] = *reinterpret_cast<const float4*>(p + (size_t)(s + i) * stride);
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      if (s + i < n) add4(acc, t[i]);
+  }
   return acc;
 }
 

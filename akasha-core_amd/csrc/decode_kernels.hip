@@ -115,12 +115,12 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
 #endif
 template <int W, int HL, int EPI, int PRO, bool BF>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
-  constexpr int RH = W > 1 ? W / 2 : 1;
   constexpr int KC = 2 * W * HL;
   constexpr int HQ = HL / 4;
   static_assert(HL % 4 == 0, "HL must cover whole k-quads");
   static_assert(!BF || HL % 8 == 0, "bfloat16 tiles need whole k-octets");
-  __shared__ float red[RH][32][33];
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16, "W must be a power of 2 <= 16");
+  __shared__ float red[W][32][33];
 
   const int M = p.M, N = p.N, K = p.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -221,8 +221,32 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
     }
   }
 
+  if (W > 1 && EPI != DEC_LOGITS) {
+    // Partial tiles: every wave's 32x32 tile goes to LDS behind one barrier,
+    // then wave w sums rows [w * 32 / W, (w + 1) * 32 / W) over the waves in
+    // index order and stores them (lane: column j, rows h, h + 2, ...).
+    constexpr int RW = 32 / W;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave][acc_row(r, h)][j] = acc[r];
+    __syncthreads();
+    if (!cok) return;
+#pragma unroll
+    for (int i = 0; i < RW / 2; ++i) {
+      const int m = wave * RW + h + 2 * i;
+      float v = red[0][m][j];
+#pragma unroll
+      for (int w = 1; w < W; ++w) v += red[w][m][j];
+      if (EPI == DEC_PART)
+        p.y[((size_t)blockIdx.y * 32 + m) * N + col] = v;
+      else if (EPI == DEC_PART_T)
+        p.y[(size_t)blockIdx.y * 32 * N + kq_index(m, col)] = v;
+      else
+        p.y[kq_index(m, col)] = silu(v);
+    }
+    return;
+  }
   if (W > 1) {
-    for (int half = RH; half >= 1; half >>= 1) {
+    for (int half = W / 2; half >= 1; half >>= 1) {
       __syncthreads();
       if (wave >= half && wave < 2 * half)
 #pragma unroll
@@ -244,6 +268,8 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
       if (cok) p.y[((size_t)blockIdx.y * 32 + m) * N + col] = acc[r];
     } else if (EPI == DEC_PART_T) {
       if (cok) p.y[(size_t)blockIdx.y * 32 * N + kq_index(m, col)] = acc[r];
+    } else if (EPI == DEC_SILU_T) {
+      if (cok) p.y[kq_index(m, col)] = silu(acc[r]);
     } else if (EPI == DEC_LOGITS) {
       // Logits, and the first maximum of the row over this tile's columns.
       bv = -INFINITY;
@@ -699,16 +725,16 @@ namespace {
 // consumer to sum) beyond; the generic lm_head (K beyond the persistent
 // kernel's reach) runs whole-K blocks.
 #ifndef AKH_SHAPE_QKV
-#define AKH_SHAPE_QKV 4, 24
+#define AKH_SHAPE_QKV 16, 12
 #endif
 #ifndef AKH_SHAPE_OUT
 #define AKH_SHAPE_OUT 4, 12
 #endif
 #ifndef AKH_SHAPE_UP
-#define AKH_SHAPE_UP 8, 24
+#define AKH_SHAPE_UP 4, 12
 #endif
 #ifndef AKH_SHAPE_DOWN
-#define AKH_SHAPE_DOWN 8, 8
+#define AKH_SHAPE_DOWN 16, 12
 #endif
 #ifndef AKH_SHAPE_LM
 #define AKH_SHAPE_LM 4, 16
@@ -778,24 +804,28 @@ int role_splits(int K, int N) {
 
 template <int ROLE>
 bool role_bf16(int K, int N) {
-  return large_gemm(K, N) ? RoleShape<ROLE, true>::HL % 8 == 0
-                          : RoleShape<ROLE, false>::HL % 8 == 0;
+  // A k-octet shape exists (dec_go_shape): HL a multiple of 8, or an even W.
+  using S = RoleShape<ROLE, false>;
+  using SL = RoleShape<ROLE, true>;
+  return large_gemm(K, N) ? SL::HL % 8 == 0 || SL::W % 2 == 0
+                          : S::HL % 8 == 0 || S::W % 2 == 0;
 }
 
 template <int ROLE, bool LARGE, int EPI, int PRO>
 hipError_t dec_go_shape(DecGemmParams p, hipStream_t s) {
   using S = RoleShape<ROLE, LARGE>;
+  // bfloat16 tiles need whole k-octets per half-wave: a shape whose HL is
+  // not a multiple of 8 runs them as W / 2 waves of 2 HL rows, the same pass
+  // length KC and so the same partial tiles.
+  constexpr bool kOct = S::HL % 8 == 0;
+  static_assert(kOct || S::W % 2 == 0, "no k-octet shape with the same pass length");
+  constexpr int WB = kOct ? S::W : S::W / 2, HLB = kOct ? S::HL : 2 * S::HL;
   p.kpass = role_kpass<ROLE, LARGE>(p.K, p.N);
-  const dim3 g((p.N + 31) / 32, role_splits<ROLE, LARGE>(p.K, p.N)), b(64 * S::W);
-  if constexpr (S::HL % 8 == 0) {
-    if (p.wbf16) {
-      hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, true>), g, b, 0, s, p);
-      return hipGetLastError();
-    }
-  } else if (p.wbf16) {
-    return hipErrorInvalidValue;  // never tiled so (dec_bf16_capable)
-  }
-  hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, false>), g, b, 0, s, p);
+  const dim3 g((p.N + 31) / 32, role_splits<ROLE, LARGE>(p.K, p.N));
+  if (p.wbf16)
+    hipLaunchKernelGGL((k_dec_gemm<WB, HLB, EPI, PRO, true>), g, dim3(64 * WB), 0, s, p);
+  else
+    hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, false>), g, dim3(64 * S::W), 0, s, p);
   return hipGetLastError();
 }
 
@@ -885,7 +915,11 @@ hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
   switch (role) {
     case DEC_CFG_QKV: return dec_go<DEC_CFG_QKV, DEC_PART, PRO_NONE>(p, s);
     case DEC_CFG_OUT: return dec_go<DEC_CFG_OUT, DEC_PART, PRO_ATTN_MERGE>(p, s);
-    case DEC_CFG_UP: return dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NONE>(p, s);
+    case DEC_CFG_UP:
+      // One split: the whole sum is in the block, so SiLU is applied here.
+      return dec_gemm_splits(DEC_CFG_UP, p.K, p.N) == 1
+                 ? dec_go<DEC_CFG_UP, DEC_SILU_T, PRO_NONE>(p, s)
+                 : dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NONE>(p, s);
     case DEC_CFG_DOWN:
       return p.nparts ? dec_go<DEC_CFG_DOWN, DEC_PART, PRO_SILU_SUM>(p, s)
                       : dec_go<DEC_CFG_DOWN, DEC_PART, PRO_NONE>(p, s);

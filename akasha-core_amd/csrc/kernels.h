@@ -154,6 +154,7 @@ enum DecEpi : int {
   DEC_PART = 0,    // y[split, m, n] = partial tile of K chunk `split`
   DEC_PART_T = 1,  // the same, each partial tile in the k-quad layout
   DEC_LOGITS = 2,  // y[m, n] = whole-K result + per-tile argmax partials
+  DEC_SILU_T = 3,  // y = silu(whole-K result) in the k-quad layout (one split)
 };
 
 enum DecPro : int {

@@ -192,6 +192,30 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     }
 }
 
+// The shape a flash block works on: the recorded one, or the live meta of a
+// per-shader launch (FlashAttnMeta, read when the kernel runs; meta.rs).  A
+// live meta may shrink the recorded shape the grid was sized for, never grow
+// it or change the head size; for such a meta, and for a head past the live
+// head count (the reference kernel returns for head >= num_heads,
+// cuda.rs:647), the block returns false and touches no memory.
+template <int HD>
+__device__ __forceinline__ bool flash_shape(const FlashParams& p, int hh, int& S, int& d,
+                                            float& scale, long& roff) {
+  S = p.S;
+  d = p.d;
+  scale = p.scale;
+  roff = 0;
+  if (p.meta) {
+    const akh_flash_attn_meta m = *p.meta;
+    if ((int)m.head_dim != HD || (int)m.seq_len > p.S || (int)m.dim > p.d) return false;
+    S = (int)m.seq_len;
+    d = (int)m.dim;
+    scale = m.scale;
+    roff = (long)m.row_offset * d;
+  }
+  return hh < d / HD;
+}
+
 // Causal flash attention on MFMA for head_dim 64 and 128.  Block = 4 waves x
 // 32 queries of one (sequence, head); keys stream through LDS in blocks of
 // 32.  Each wave computes S^T = K Q^T so every lane owns one query (column)
@@ -212,18 +236,13 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
   float (*Ks)[KP] = reinterpret_cast<float (*)[KP]>(lds);
   float (*Vs)[HD] = reinterpret_cast<float (*)[HD]>(lds + KB * KP);
 
-  int S = p.S, d = p.d;
-  float scale = p.scale;
-  long roff = 0;
-  if (p.meta) {
-    S = (int)p.meta->seq_len;
-    d = (int)p.meta->dim;
-    scale = p.meta->scale;
-    roff = (long)p.meta->row_offset * d;
-  }
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
+  int S, d;
+  float scale;
+  long roff;
+  if (!flash_shape<HD>(p, hh, S, d, scale, roff)) return;
   const int H = d / HD;
   const float qscale = scale * 1.44269504088896341f;
-  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -359,17 +378,12 @@ __global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
   constexpr int KB = 64;
   __shared__ float Ks[KB][HD];
   __shared__ float Vs[KB][HD];
-  int S = p.S, d = p.d;
-  float scale = p.scale;
-  long roff = 0;
-  if (p.meta) {
-    S = (int)p.meta->seq_len;
-    d = (int)p.meta->dim;
-    scale = p.meta->scale;
-    roff = (long)p.meta->row_offset * d;
-  }
-  const int H = d / HD;
   const int hh = blockIdx.y, b = blockIdx.z;
+  int S, d;
+  float scale;
+  long roff;
+  if (!flash_shape<HD>(p, hh, S, d, scale, roff)) return;
+  const int H = d / HD;
   const int q0 = blockIdx.x * 64;
   if (q0 >= S) return;
   const int i = q0 + threadIdx.x;
@@ -1022,19 +1036,14 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
     return reinterpret_cast<uint16_t (*)[VP]>(lds + 3 * K_PLANE * 2) + pl * HD;
   };
 
-  int S = p.S, d = p.d;
-  float scale = p.scale;
-  long roff = 0;
-  if (p.meta) {
-    S = (int)p.meta->seq_len;
-    d = (int)p.meta->dim;
-    scale = p.meta->scale;
-    roff = (long)p.meta->row_offset * d;
-  }
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
+  int S, d;
+  float scale;
+  long roff;
+  if (!flash_shape<HD>(p, hh, S, d, scale, roff)) return;
   const int H = d / HD;
   // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
   const float qscale = scale * 1.44269504088896341f;
-  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1243,18 +1252,13 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
   constexpr int M_BYTES = NW * (HD * OS + 64) * 4;
   __shared__ __align__(16) unsigned char lds[NW * W_BYTES > M_BYTES ? NW * W_BYTES : M_BYTES];
 
-  int S = p.S, d = p.d;
-  float scale = p.scale;
-  long roff = 0;
-  if (p.meta) {
-    S = (int)p.meta->seq_len;
-    d = (int)p.meta->dim;
-    scale = p.meta->scale;
-    roff = (long)p.meta->row_offset * d;
-  }
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
+  int S, d;
+  float scale;
+  long roff;
+  if (!flash_shape<HD>(p, hh, S, d, scale, roff)) return;
   const int H = d / HD;
   const float qscale = scale * 1.44269504088896341f;
-  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   const int q0 = qblk * 32;
   if (q0 >= S) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

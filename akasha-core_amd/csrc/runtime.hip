@@ -992,6 +992,7 @@ akh_status ensure_prefill(akh_session* s, size_t rows) {
 
 // AkashaError::NoCache if a sequence's cache was taken (inference.rs:72, 180).
 akh_status need_caches(const akh_session* s) {
+  if (!s->kv) return fail(AKH_E_HIP, "session has no KV cache allocation");
   for (uint32_t b = 0; b < s->B; ++b)
     if (!s->has_cache[b])
       return fail(AKH_E_NO_CACHE, "sequence " + std::to_string(b) + " has no cache");
@@ -1110,7 +1111,9 @@ hipError_t enqueue_up(akh_session* s, uint32_t l) {
 hipError_t enqueue_down(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
-  if (s->up_act) {
+  if (s->ks_up == 1) {
+    p.xt = s->p_up;  // ffn_up applied SiLU to its whole sums
+  } else if (s->up_act) {
     hipError_t e = launch_silu_sum(s->p_up, s->ks_up, s->up_act, (size_t)32 * c.ffn_hidden,
                                    s->be->stream);
     if (e != hipSuccess) return e;
@@ -1333,7 +1336,7 @@ namespace {
 // AKH_SILU_KERNEL_READS.
 bool silu_own_kernel(const akh_session* s) {
   const akh_model_config& c = s->m->cfg;
-  return (long)(c.dim / 32) * s->ks_up >= AKH_SILU_KERNEL_READS;
+  return s->ks_up > 1 && (long)(c.dim / 32) * s->ks_up >= AKH_SILU_KERNEL_READS;
 }
 
 // A session's buffers.  With decode false only what prefill needs (KV
@@ -1926,11 +1929,19 @@ extern "C" akh_status akh_session_set_kv_bf16(akh_session* s, int enable) {
   // Graphs hold the attention kernel of the old element type.
   drop_graphs(s);
   free_prefill(s);
-  HIP_TRY(hipFree(s->kv));
-  s->kv = nullptr;
+  // The new cache is allocated before the old one is freed: on failure the
+  // session keeps its old cache and element type unchanged.
+  const size_t bytes = elems * (enable ? 2 : 4);
+  void* nkv = nullptr;
+  HIP_TRY(hipMalloc(&nkv, bytes));
+  hipError_t e = hipMemset(nkv, 0, bytes);
+  if (e != hipSuccess) {
+    hipFree(nkv);
+    return fail(AKH_E_HIP, std::string("akh_session_set_kv_bf16: ") + hipGetErrorString(e));
+  }
+  hipFree(s->kv);
+  s->kv = static_cast<float*>(nkv);
   s->kv16 = enable != 0;
-  HIP_TRY(hipMalloc(&s->kv, elems * s->kv_elem()));
-  HIP_TRY(hipMemset(s->kv, 0, elems * s->kv_elem()));
   return AKH_OK;
 }
 
@@ -2041,6 +2052,26 @@ extern "C" akh_status akh_session_time_decode_attn(akh_session* s, uint32_t reps
     if (x) hipEventDestroy(x);
   HIP_TRY(e);
   *avg_ms = (float)(total / reps);
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_session_decode_launches(akh_session* s, uint32_t* launches) {
+  CHECK_ARG(s && launches, "akh_session_decode_launches: bad argument");
+  CHECK_ARG(!s->be->capturing, "akh_session_decode_launches: graph capture in progress");
+  HIP_TRY(hipSetDevice(s->be->device));
+  akh_status st = ensure_decode_graph(s);
+  if (st != AKH_OK) return st;
+  size_t n = 0;
+  HIP_TRY(hipGraphGetNodes(s->graph, nullptr, &n));
+  std::vector<hipGraphNode_t> nodes(n);
+  HIP_TRY(hipGraphGetNodes(s->graph, nodes.data(), &n));
+  uint32_t k = 0;
+  for (hipGraphNode_t node : nodes) {
+    hipGraphNodeType t;
+    HIP_TRY(hipGraphNodeGetType(node, &t));
+    if (t == hipGraphNodeTypeKernel) ++k;
+  }
+  *launches = k;
   return AKH_OK;
 }
 

@@ -227,6 +227,7 @@ _SIGS = {
     "akh_timer_stop": (ST, [P, C.POINTER(C.c_float)]),
     "akh_session_time_decode_kernel": (ST, [P, C.c_int, U32, C.POINTER(C.c_float)]),
     "akh_session_time_decode_attn": (ST, [P, U32, C.POINTER(C.c_float)]),
+    "akh_session_decode_launches": (ST, [P, C.POINTER(U32)]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -732,6 +733,12 @@ class Session:
         _check(_lib.akh_session_time_decode_attn(self.handle, reps, C.byref(ms)),
                "time_decode_attn")
         return ms.value
+
+    def decode_launches(self) -> int:
+        """Kernel launches in one decode step (nodes of the step's graph)."""
+        n = U32()
+        _check(_lib.akh_session_decode_launches(self.handle, C.byref(n)), "decode_launches")
+        return n.value
 
     def close(self):
         if self.handle:

@@ -7,9 +7,9 @@ decode at batch 32 -- every sequence prefilled with 448 random tokens
 512 tokens.  A "step" is one decode step of all 32 sequences (embedding ->
 12 layers -> lm_head -> argmax, graph-replayed, tokens fed back on the
 device).  ``value`` = 32 * steps / time (tok/s), inputs resident in HBM.
-The default 64 steps are exactly positions 448..511; more steps replay
-windows of up to 64 from position 448 (the cache is truncated back to 448
-between windows).
+The timed steps are always whole windows of 64 at positions 448..511 (KV
+449..512): ``--steps K`` times ceil(K / 64) windows, the cache truncated
+back to 448 between them, and the line reports the steps actually timed.
 
 Also reported: the roofline of the dominant decode kernel (single-query
 attention over the cache, its launches cycled over the layers and timed
@@ -44,7 +44,14 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def measured_traffic(path=ROOT / "profiles" / "decode_attn_b32_ctx512_pmc.md"):
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_attn_b32_ctx512_pmc.md"
+TRAFFIC_SOURCE = ("not measured in this run: rocprofv3 FETCH_SIZE + WRITE_SIZE passes over the "
+                  "same kernel, scaled by a copy kernel, committed in "
+                  "profiles/decode_attn_b32_ctx512_pmc.md (regenerated with each change to "
+                  "k_dec_attn)")
+
+
+def measured_traffic(path=TRAFFIC_PROFILE):
     """HBM bytes per launch of the roofline kernel, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE passes (counters cannot be read from
     inside this process); None if the summary is absent."""
@@ -277,6 +284,40 @@ def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=
     return n / dt, n, dt
 
 
+def cpu_baseline_sequences(cfg, weights, prompt_len, threads, steps=16):
+    """All host cores the way batch-32 decode uses them: `threads` sequences
+    decoded at once, one single-threaded oracle session per host thread (the
+    sessions share the weights; ctypes releases the GIL for each call).
+    Aggregate tok/s, (steps per sequence, seconds)."""
+    import threading
+    ora = entry.load_oracle()
+    ora.set_threads(1)
+    sess = []
+    for _ in range(threads):
+        s = ora.OracleSession(cfg, weights, cfg.seq_len)
+        s.set_len(prompt_len)
+        sess.append(s)
+    start = threading.Barrier(threads + 1)
+
+    def run(s):
+        start.wait()
+        tok = 1
+        for _ in range(steps):
+            tok = ora.argmax(s.decode_step(tok))
+
+    ts = [threading.Thread(target=run, args=(s,)) for s in sess]
+    for t in ts:
+        t.start()
+    start.wait()
+    t0 = time.perf_counter()
+    for t in ts:
+        t.join()
+    dt = time.perf_counter() - t0
+    for s in sess:
+        s.close()
+    return threads * steps / dt, steps, dt
+
+
 def cpu_prefill_baseline(cfg, weights, tokens, threads):
     """The oracle's prefill of one prompt (the reference CPU backend's
     InferenceSession::prefill restated), tok/s."""
@@ -305,6 +346,29 @@ def host_cpu():
     return name, os.cpu_count() or 1
 
 
+def cpu_limits():
+    """CPUs this process may run on (affinity) and its cgroup CPU quota
+    (cpu.max / cfs quota in CPUs; None when unlimited or unreadable)."""
+    quota = None
+    for qf, pf in (("/sys/fs/cgroup/cpu.max", None),
+                   ("/sys/fs/cgroup/cpu/cpu.cfs_quota_us", "/sys/fs/cgroup/cpu/cpu.cfs_period_us")):
+        try:
+            if pf is None:
+                q, p = open(qf).read().split()[:2]
+            else:
+                q, p = open(qf).read().strip(), open(pf).read().strip()
+            if q not in ("max", "-1"):
+                quota = round(int(q) / int(p), 2)
+            break
+        except (OSError, ValueError):
+            continue
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count() or 1
+    return aff, quota
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -313,10 +377,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     ap.add_argument("--kernel-reps", type=int, default=60)
-    ap.add_argument("--scaled", action="store_true",
-                    help="also measure config 5 (scaled architecture) decode and prefill")
+    ap.add_argument("--no-scaled", action="store_true",
+                    help="skip config 5 (scaled architecture) decode and prefill")
     ap.add_argument("--no-scaled-decode", action="store_true",
-                    help="with --scaled, measure config 5's prefill legs only")
+                    help="measure config 5's prefill legs only")
     ap.add_argument("--prefill-only", action="store_true",
                     help="measure only config 3's prefill legs and print them (for profiling)")
     args = ap.parse_args()
@@ -362,18 +426,20 @@ def main():
     log(f"bench: warmup {args.warmup} decode steps")
     if args.warmup:
         run_steps(args.warmup)
-    log(f"bench: timing {args.steps} decode steps")
-    ms = run_steps(args.steps)
-    ms_per_step = ms / args.steps
-    tok_s = B * args.steps / (ms / 1e3)
+    # Whole 64-step windows (positions 448..511), whatever --steps asks for,
+    # so the line always measures config 4's full KV range.
+    windows = max(1, -(-args.steps // window))
+    steps = windows * window
+    log(f"bench: timing {steps} decode steps ({windows} window(s) of positions "
+        f"{P}..{CTX - 1}; {args.steps} requested)")
+    ms = run_steps(steps)
+    ms_per_step = ms / steps
+    tok_s = B * steps / (ms / 1e3)
 
     # Whole-step HBM roofline over the same position schedule.
-    total_bytes, done = 0, 0
-    while done < args.steps:
-        k = min(window, args.steps - done)
-        total_bytes += sum(decode_step_bytes(cfg, B, P + i + 1) for i in range(k))
-        done += k
+    total_bytes = windows * sum(decode_step_bytes(cfg, B, P + i + 1) for i in range(window))
     step_gbs = total_bytes / (ms / 1e3) / 1e9
+    launches_per_step = sess.decode_launches()
 
     # Dominant kernel: decode attention at T = 481 (pos 480), launches cycled
     # over the 12 layers so each reads its KV rows from HBM as in a step.
@@ -464,7 +530,7 @@ def main():
                "batched_mfma_busy_frac": rb["mfma_busy_frac"]}
 
     scaled = None
-    if args.scaled:
+    if not args.no_scaled:
         scaled = scaled_measurement(pkg, hip, be, with_prefill=not args.no_prefill,
                                     with_decode=not args.no_scaled_decode)
 
@@ -476,18 +542,30 @@ def main():
                "sample": f"oracle decode of 1 sequence, {n1} steps at positions 448.. "
                          f"({t1:.1f} s), zero KV prefix; the reference CPU backend runs "
                          f"one sequence per session"}
-        nt = min(16, os.cpu_count() or 1)
-        vN, nN, tN = cpu_baseline(cfg, w, P, budget_s=6.0, threads=nt)
-        cpu_omp = {"value": round(vN, 3), "cores": nt, "steps": nN, "seconds": round(tN, 2)}
+        aff, quota = cpu_limits()
+        # The box's CPU share is 16 (its OMP_NUM_THREADS), whatever nproc says.
+        nt = max(1, min(16, aff, int(quota) if quota else 16))
+        log(f"bench: CPU baseline ({nt} sequences at once, one thread each)")
+        vN, nN, tN = cpu_baseline_sequences(cfg, w, P, nt)
+        cpu_omp = {"value": round(vN, 3), "unit": "tok/s", "cores": nt, "kind": "port",
+                   "sample": f"{nt} sequences decoded at once, one oracle session per host "
+                             f"thread, {nN} steps each at positions 448.. ({tN:.1f} s); "
+                             f"batch-32 decode over all host cores"}
+        # The column-split OpenMP GEMV of one sequence, for comparison: the
+        # reference's per-sequence path with its matmuls spread over threads.
+        vO, nO, tO = cpu_baseline(cfg, w, P, budget_s=4.0, max_steps=32, threads=nt)
+        cpu_omp["one_sequence_omp"] = {"value": round(vO, 3), "threads": nt, "steps": nO,
+                                       "seconds": round(tO, 2)}
         # A labelled prefill slice: one 64-token prompt of config 3's seed.
         log(f"bench: CPU baseline (oracle prefill of 64 tokens, {nt} threads)")
         ptok = pkg.synthetic_tokens(16 * 512, cfg.vocab_size, seed=3)[:64]
         vp, tp = cpu_prefill_baseline(cfg, w, ptok, nt)
         cname, ncpu = host_cpu()
-        cpu["host"] = cpu_omp["host"] = {"cpu_model": cname, "nproc": ncpu}
+        cpu["host"] = cpu_omp["host"] = {"cpu_model": cname, "nproc": ncpu,
+                                         "affinity_cpus": aff, "cgroup_cpu_quota": quota}
         cpu_omp["prefill"] = {"value": round(vp, 2), "unit": "tok/s", "cores": nt,
                               "sample": f"oracle prefill of the first 64 tokens of config 3's "
-                                        f"sequence 0 ({tp:.1f} s)"}
+                                        f"sequence 0, column-split OpenMP ({tp:.1f} s)"}
     else:
         cpu_omp = None
 
@@ -500,7 +578,8 @@ def main():
         "value": round(tok_s, 1),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
+        "steps_requested": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
@@ -508,15 +587,18 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic",
-        "config": {"workload": "config 4: akasha-hall 1.0 greedy decode, batch 32, "
-                               "prefill 448 (seed 4), positions 448..511 (KV 449..512)",
+        "config": {"workload": f"config 4: akasha-hall 1.0 greedy decode, batch 32, "
+                               f"prefill 448 (seed 4), {windows} x 64 steps at positions "
+                               f"{P}..{CTX - 1} (KV {P + 1}..{CTX})",
                    "model": "akasha-hall-1.0 (162M)", "global_batch": B, "seq_len": CTX,
-                   "parallelism": "none (1 GPU)"},
+                   "parallelism": "none (1 GPU)",
+                   "launches_per_step": launches_per_step},
         "roofline": {"kernel": "decode_attn (T=481, layers cycled)", "bound": "hbm",
                      "kernel_ms": round(kms["decode_attn"], 5),
                      "dispatch_ms": round(attn_dispatch_ms, 5),
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": TRAFFIC_SOURCE,
                      "algorithmic_bytes": attn_bytes},
         "step_roofline": {"achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4),

@@ -446,6 +446,11 @@ akh_status akh_session_time_decode_kernel(akh_session* s, int kernel,
  * the mean excludes the gaps between dispatches.  No counterpart in the
  * reference (measurement only). */
 akh_status akh_session_time_decode_attn(akh_session* s, uint32_t reps, float* avg_ms);
+/* Kernel launches in one decode step: the kernel nodes of the captured
+ * one-step decode graph (captured here if it is not yet).  No counterpart
+ * in the reference (measurement only; the reference dispatches ~195 nodes
+ * per sequence per token, inference_graphs.rs:339-509). */
+akh_status akh_session_decode_launches(akh_session* s, uint32_t* launches);
 
 #ifdef __cplusplus
 }

@@ -257,8 +257,8 @@ def test_head_dim_128_prefill_matches_oracle(backend, pkg, ora):
 
 def test_bf16_tiles_keep_fp32_accuracy(backend, pkg, ora):
     # Weights whose values are all bfloat16 are tiled in bfloat16 for decode:
-    # qkv, up and down of each layer and, with dim > 1024, the lm_head (out
-    # keeps float tiles).  Those GEMMs run bf16 MFMAs on A split exactly into
+    # the four matrices of each layer and, with dim > 1024, the lm_head.
+    # Those GEMMs run bf16 MFMAs on A split exactly into
     # three bfloat16 terms, so every product is exact and only the summation
     # order differs from the float tiles: logits agree to fp32 rounding
     # (1e-4 here, against the 1e-3 oracle bar) with the same tokens, and each
@@ -267,12 +267,12 @@ def test_bf16_tiles_keep_fp32_accuracy(backend, pkg, ora):
     cfg = pkg.ModelConfig.new(500, 1152, 9, 2, 40)
     w = pkg.synthetic_weights(cfg, seed=41, bf16=True)
     model, s = _session(pkg, backend, cfg, w, 40, 3)
-    assert model.set_bf16_tiles(True) == 3 * cfg.num_layers + 1
+    assert model.set_bf16_tiles(True) == 4 * cfg.num_layers + 1
     toks = pkg.synthetic_tokens(3 * 12, cfg.vocab_size, seed=42).reshape(3, 12)
     logits, nxt = s.prefill(toks)
     runs = {}
     for allow in (True, False, True):
-        assert model.set_bf16_tiles(allow) == (3 * cfg.num_layers + 1 if allow else 0)
+        assert model.set_bf16_tiles(allow) == (4 * cfg.num_layers + 1 if allow else 0)
         s.truncate(12)
         feed, out = nxt, []
         for _ in range(4):
@@ -296,7 +296,7 @@ def test_bf16_tiles_keep_fp32_accuracy(backend, pkg, ora):
     w2[2] = w[2].copy()
     w2[2].flat[7] = np.nextafter(w2[2].flat[7], np.float32(1))
     model.upload(w2)
-    assert model.set_bf16_tiles(True) == 3 * cfg.num_layers
+    assert model.set_bf16_tiles(True) == 4 * cfg.num_layers
 
 
 def test_take_and_replace_cache_move_a_sequence(backend, pkg, ora):
