@@ -322,6 +322,14 @@ struct SampleArgs {
 };
 
 size_t sample_scratch_bytes(int rows, int n);
+
+// The allocation-free sampler's workspace: a device array of
+// kNoAllocSampleElems doubles (rows * n at most), one copy per GPU.
+// sample_noalloc_scratch resolves its address on `device`, which must be the
+// current device, once per device (later calls return the kept address).
+constexpr size_t kNoAllocSampleElems = (size_t)1 << 21;
+constexpr int kMaxDevices = 64;
+hipError_t sample_noalloc_scratch(int device, double** ptr);
 hipError_t launch_sample_rows(const SampleArgs& a, int rows, hipStream_t s);
 // pos[m] += active[m] for m < rows: the positions of the rows decoded.
 hipError_t launch_advance(int* pos, const int* active, int rows, hipStream_t s);

@@ -63,6 +63,7 @@ struct akh_backend {
   bool capturing = false;
   void* scratch = nullptr;  // launcher scratch, grown on demand outside capture
   size_t scratch_bytes = 0;
+  double* noalloc_scratch = nullptr;  // the device's fixed sampler workspace
 };
 
 namespace {
@@ -109,6 +110,9 @@ extern "C" akh_status akh_backend_new(int device, akh_backend** out) {
   hipError_t e = hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreate(&be->t0);
   if (e == hipSuccess) e = hipEventCreate(&be->t1);
+  // The device's copy of the allocation-free sampler's workspace (device
+  // current above).
+  if (e == hipSuccess) e = sample_noalloc_scratch(device, &be->noalloc_scratch);
   if (e != hipSuccess) {
     akh_backend_free(be);
     return fail(AKH_E_HIP, std::string("akh_backend_new: ") + hipGetErrorString(e));
@@ -466,6 +470,13 @@ extern "C" akh_status akh_argmax_rows(akh_backend* be, const float* logits,
   return AKH_OK;
 }
 
+namespace {
+akh_status sample_rows_into(akh_backend* be, const float* logits, uint32_t rows, uint32_t n,
+                            akh_sampling params, const uint32_t* seen, uint32_t seen_stride,
+                            const uint32_t* seen_len, const double* uniforms, uint32_t* out,
+                            double* wbuf);
+}  // namespace
+
 extern "C" akh_status akh_sample_rows(akh_backend* be, const float* logits, uint32_t rows,
                                       uint32_t n, akh_sampling params, const uint32_t* seen,
                                       uint32_t seen_stride, const uint32_t* seen_len,
@@ -478,6 +489,36 @@ extern "C" akh_status akh_sample_rows(akh_backend* be, const float* logits, uint
   void* wb = nullptr;
   akh_status st = backend_scratch(be, sample_scratch_bytes((int)rows, (int)n), &wb);
   if (st != AKH_OK) return st;
+  return sample_rows_into(be, logits, rows, n, params, seen, seen_stride, seen_len, uniforms,
+                          out, static_cast<double*>(wb));
+}
+
+extern "C" akh_status akh_sample_rows_noalloc(akh_backend* be, const float* logits,
+                                              uint32_t rows, uint32_t n, akh_sampling params,
+                                              const uint32_t* seen, uint32_t seen_stride,
+                                              const uint32_t* seen_len, const double* uniforms,
+                                              uint32_t* out) {
+  CHECK_ARG(be && logits && out && rows > 0 && n > 0, "akh_sample_rows_noalloc: bad argument");
+  CHECK_ARG(n <= (uint32_t)kMaxSampleVocab, "akh_sample_rows_noalloc: n exceeds 2^20");
+  CHECK_ARG((size_t)rows * n <= kNoAllocSampleElems,
+            "akh_sample_rows_noalloc: rows * n exceeds 2^21, the fixed workspace");
+  CHECK_ARG(params.temperature <= 0.0f || uniforms,
+            "akh_sample_rows_noalloc: sampling (temperature > 0) needs uniforms");
+  CHECK_ARG(!seen || (seen_len && seen_stride > 0),
+            "akh_sample_rows_noalloc: seen needs seen_len");
+  CHECK_ARG(be->noalloc_scratch, "akh_sample_rows_noalloc: no workspace on this device");
+  return sample_rows_into(be, logits, rows, n, params, seen, seen_stride, seen_len, uniforms,
+                          out, be->noalloc_scratch);
+}
+
+namespace {
+
+// The sampler launch of akh_sample_rows / akh_sample_rows_noalloc, on the
+// workspace `wbuf` (rows * n doubles); allocates nothing.
+akh_status sample_rows_into(akh_backend* be, const float* logits, uint32_t rows, uint32_t n,
+                            akh_sampling params, const uint32_t* seen, uint32_t seen_stride,
+                            const uint32_t* seen_len, const double* uniforms, uint32_t* out,
+                            double* wbuf) {
   SampleArgs a{};
   a.logits = logits;
   a.n = (int)n;
@@ -490,11 +531,13 @@ extern "C" akh_status akh_sample_rows(akh_backend* be, const float* logits, uint
   a.seen_stride = seen_stride;
   a.seen_len = seen_len;
   a.uniform = uniforms;
-  a.wbuf = static_cast<double*>(wb);
+  a.wbuf = wbuf;
   a.out = out;
   HIP_TRY(launch_sample_rows(a, (int)rows, be->stream));
   return AKH_OK;
 }
+
+}  // namespace
 
 // ---------------------------------------------------------------------------
 // Model weights

@@ -20,6 +20,8 @@
 // of the seen ids in LDS.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -323,6 +325,32 @@ __global__ void k_advance(int* pos, const int* active, int rows) {
 }  // namespace
 
 size_t sample_scratch_bytes(int rows, int n) { return (size_t)rows * n * sizeof(double); }
+
+// Workspace of the allocation-free sampler entry point (the per-row f64
+// weights, kNoAllocSampleElems doubles = 16 MiB).  Every GPU the library
+// runs on holds its own copy until the process ends.  In host code the
+// array's name is not a device address: kernels get the address from
+// sample_noalloc_scratch().  k_sample_rows writes every weight it reads
+// within the same launch, so the array needs no clearing between calls.
+namespace {
+__device__ __align__(256) double scratch[kNoAllocSampleElems];
+std::mutex g_scratch_mu;
+double* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t sample_noalloc_scratch(int device, double** ptr) {
+  if (device < 0 || device >= kMaxDevices || !ptr) return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    // The caller made `device` current: its copy of the array is resolved.
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = static_cast<double*>(p);
+  }
+  *ptr = g_scratch_ptr[device];
+  return hipSuccess;
+}
 
 hipError_t launch_advance(int* pos, const int* active, int rows, hipStream_t s) {
   if (rows <= 0 || rows > 1024) return hipErrorInvalidValue;

@@ -198,6 +198,7 @@ _SIGS = {
     "akh_forward_hidden": (ST, [P, P]),
     "akh_argmax_rows": (ST, [P, P, U32, U32, P]),
     "akh_sample_rows": (ST, [P, P, U32, U32, Sampling, P, U32, P, P, P]),
+    "akh_sample_rows_noalloc": (ST, [P, P, U32, U32, Sampling, P, U32, P, P, P]),
     "akh_model_new": (ST, [P, C.POINTER(ModelConfigC), C.POINTER(P)]),
     "akh_model_free": (None, [P]),
     "akh_model_num_params": (U32, [P]),
@@ -481,6 +482,19 @@ class Backend:
                                     _p(seen_len) if seen_len is not None else None,
                                     _p(uniforms) if uniforms is not None else None, _p(out)),
                "sample_rows")
+
+    def sample_rows_noalloc(self, logits, rows, n, out, temperature=0.0, top_k=0, top_p=1.0,
+                            repetition_penalty=1.0, seen=None, seen_stride=0, seen_len=None,
+                            uniforms=None):
+        """sample_rows on the device's fixed workspace: allocates nothing
+        (rows * n <= 2^21)."""
+        sp = Sampling(temperature, top_k, top_p, repetition_penalty)
+        _check(_lib.akh_sample_rows_noalloc(self.handle, _p(logits), rows, n, sp,
+                                            _p(seen) if seen is not None else None, seen_stride,
+                                            _p(seen_len) if seen_len is not None else None,
+                                            _p(uniforms) if uniforms is not None else None,
+                                            _p(out)),
+               "sample_rows_noalloc")
 
 
 class Graph:

@@ -227,6 +227,18 @@ akh_status akh_sample_rows(akh_backend* be, const float* logits, uint32_t rows,
                            uint32_t n, akh_sampling params, const uint32_t* seen,
                            uint32_t seen_stride, const uint32_t* seen_len,
                            const double* uniforms, uint32_t* out);
+/* akh_sample_rows without any allocation: no counterpart in the reference.
+ * It is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, checks and results as akh_sample_rows; its workspace is a fixed
+ * per-GPU device array of 2^21 doubles (16 MiB, held until the process
+ * ends), so rows * n must be at most 2^21 (AKH_E_INVALID beyond).  All calls
+ * on one GPU share that array: calls that overlap on one GPU (other streams
+ * or backends) race. */
+akh_status akh_sample_rows_noalloc(akh_backend* be, const float* logits, uint32_t rows,
+                                   uint32_t n, akh_sampling params, const uint32_t* seen,
+                                   uint32_t seen_stride, const uint32_t* seen_len,
+                                   const double* uniforms, uint32_t* out);
 
 /* ---- 3. model weights and the batched session ---------------------------- */
 
