@@ -98,7 +98,10 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
                      __uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u));
 }
 
-// Y (epilogue) A[M, K] . W[K, N] for M <= 32, W packed in 32-column tiles.
+// Y (epilogue) A[M, K] . W[K, N] for M <= 32 * MT, W packed in 32-column
+// tiles.  The rows are MT tiles of 32 (activations [MT][K/4][32][4], row m
+// in tile m / 32); each weight load feeds the MFMAs of every row tile, so
+// the weights are read once for up to 64 rows.
 //
 // Grid (N / 32 tiles, K chunks), W waves per block.  Lane (j, h) owns column
 // 32 * tile + j.  A pass covers KC = 2*W*HL rows of K: wave w takes 2*HL of
@@ -122,13 +125,15 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
 #ifndef AKH_LM_GEMM_NT
 #define AKH_LM_GEMM_NT 0
 #endif
-template <int W, int HL, int EPI, int PRO, bool BF>
+template <int W, int HL, int EPI, int PRO, bool BF, int MT>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   constexpr int KC = 2 * W * HL;
   constexpr int HQ = HL / 4;
+  constexpr int R = 32 * MT;  // rows of the activation and partial tiles
   static_assert(HL % 4 == 0, "HL must cover whole k-quads");
   static_assert(!BF || HL % 8 == 0, "bfloat16 tiles need whole k-octets");
   static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16, "W must be a power of 2 <= 16");
+  static_assert(MT == 1 || MT == 2, "one or two row tiles");
   __shared__ float red[W][32][33];
 
   const int M = p.M, N = p.N, K = p.K;
@@ -143,7 +148,9 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   const float* wt = p.w + (size_t)tile * p.Kp * 32 + j * 4;
   const uint16_t* wh = reinterpret_cast<const uint16_t*>(p.w) + (size_t)tile * p.Kp * 32 + j * 8;
 
-  f32x16 acc = zero16();
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;  // first k-quad of this half
     // The pass's weights: bfloat16 octets or float quads, read once per
@@ -164,28 +171,32 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
                                : f4{0.f, 0.f, 0.f, 0.f};
       wc[i] = __builtin_bit_cast(WRaw, t);
     }
-    float4 a[HQ];
+    float4 a[MT][HQ];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int q = 0; q < HQ; ++q) {
       const int kq = kq0 + q;
       float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
       if (4 * kq < ke) {
-        const size_t off = ((size_t)kq * 32 + j) * 4;
+        // Row 32 mt + j of the k-quad tiles; partial tiles / splits R * K apart.
+        const size_t off = (size_t)mt * 32 * K + ((size_t)kq * 32 + j) * 4;
         if (PRO == PRO_SILU_SUM) {
-          t = sum_parts4<4>(t, p.xt + off, (size_t)32 * K, p.nparts);
+          t = sum_parts4<4>(t, p.xt + off, (size_t)R * K, p.nparts);
           t = make_float4(silu_fast(t.x), silu_fast(t.y), silu_fast(t.z), silu_fast(t.w));
         } else if (PRO == PRO_ATTN_MERGE) {
           // Softmax states (max, sum, unnormalised o) of the attention
-          // splits of row j, head (4 kq) / hd: o = sum_s w_s o_s / sum_s w_s l_s
-          // with w_s = exp(max_s - max).
+          // splits of row 32 mt + j, head (4 kq) / hd:
+          // o = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(max_s - max).
           const int H = K / p.hd, hq = (4 * kq) / p.hd;
           float2 ml[kMaxAttnSplits];
           float4 o[kMaxAttnSplits];
 #pragma unroll
           for (int sp = 0; sp < kMaxAttnSplits; ++sp) {
             const bool in = sp < p.nparts;
-            ml[sp] = in ? p.ml[((size_t)sp * H + hq) * 32 + j] : make_float2(-INFINITY, 0.f);
-            o[sp] = in ? *reinterpret_cast<const float4*>(p.xt + (size_t)sp * 32 * K + off)
+            ml[sp] = in ? p.ml[((size_t)sp * H + hq) * R + mt * 32 + j]
+                        : make_float2(-INFINITY, 0.f);
+            o[sp] = in ? *reinterpret_cast<const float4*>(p.xt + (size_t)sp * R * K + off)
                        : make_float4(0.f, 0.f, 0.f, 0.f);
           }
           float mx = ml[0].x;
@@ -207,25 +218,28 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
           t = *reinterpret_cast<const float4*>(p.xt + off);
         }
       }
-      a[q] = t;
+      a[mt][q] = t;
     }
-    if constexpr (BF) {
 #pragma unroll
-      for (int q = 0; q < HQ; q += 2) {
-        const bf16x8 w8 = bf16x8_of(wc[q / 2]);
-        uint4 hi, mid, lo;
-        split3_bf16(a[q], a[q + 1], hi, mid, lo);
-        acc = mfma_bf16(bf16x8_of(hi), w8, acc);
-        acc = mfma_bf16(bf16x8_of(mid), w8, acc);
-        acc = mfma_bf16(bf16x8_of(lo), w8, acc);
-      }
-    } else {
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (BF) {
 #pragma unroll
-      for (int q = 0; q < HQ; ++q) {
-        acc = mfma32(a[q].x, wc[q].x, acc);
-        acc = mfma32(a[q].y, wc[q].y, acc);
-        acc = mfma32(a[q].z, wc[q].z, acc);
-        acc = mfma32(a[q].w, wc[q].w, acc);
+        for (int q = 0; q < HQ; q += 2) {
+          const bf16x8 w8 = bf16x8_of(wc[q / 2]);
+          uint4 hi, mid, lo;
+          split3_bf16(a[mt][q], a[mt][q + 1], hi, mid, lo);
+          acc[mt] = mfma_bf16(bf16x8_of(hi), w8, acc[mt]);
+          acc[mt] = mfma_bf16(bf16x8_of(mid), w8, acc[mt]);
+          acc[mt] = mfma_bf16(bf16x8_of(lo), w8, acc[mt]);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < HQ; ++q) {
+          acc[mt] = mfma32(a[mt][q].x, wc[q].x, acc[mt]);
+          acc[mt] = mfma32(a[mt][q].y, wc[q].y, acc[mt]);
+          acc[mt] = mfma32(a[mt][q].z, wc[q].z, acc[mt]);
+          acc[mt] = mfma32(a[mt][q].w, wc[q].w, acc[mt]);
+        }
       }
     }
   }
@@ -234,67 +248,77 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
     // Partial tiles: every wave's 32x32 tile goes to LDS behind one barrier,
     // then wave w sums rows [w * 32 / W, (w + 1) * 32 / W) over the waves in
     // index order and stores them (lane: column j, rows h, h + 2, ...).
+    // Row tile by row tile, one barrier before each tile's reads and one
+    // before the next tile overwrites the LDS.
     constexpr int RW = 32 / W;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[wave][acc_row(r, h)][j] = acc[r];
-    __syncthreads();
-    if (!cok) return;
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt > 0) __syncthreads();
 #pragma unroll
-    for (int i = 0; i < RW / 2; ++i) {
-      const int m = wave * RW + h + 2 * i;
-      float v = red[0][m][j];
+      for (int r = 0; r < 16; ++r) red[wave][acc_row(r, h)][j] = acc[mt][r];
+      __syncthreads();
+      if (cok) {
 #pragma unroll
-      for (int w = 1; w < W; ++w) v += red[w][m][j];
-      if (EPI == DEC_PART)
-        p.y[((size_t)blockIdx.y * 32 + m) * N + col] = v;
-      else if (EPI == DEC_PART_T)
-        p.y[(size_t)blockIdx.y * 32 * N + kq_index(m, col)] = v;
-      else
-        p.y[kq_index(m, col)] = silu(v);
+        for (int i = 0; i < RW / 2; ++i) {
+          const int ml = wave * RW + h + 2 * i, m = mt * 32 + ml;
+          float v = red[0][ml][j];
+#pragma unroll
+          for (int w = 1; w < W; ++w) v += red[w][ml][j];
+          if (EPI == DEC_PART)
+            p.y[((size_t)blockIdx.y * R + m) * N + col] = v;
+          else if (EPI == DEC_PART_T)
+            p.y[((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, col)] = v;
+          else
+            p.y[(size_t)mt * 32 * N + kq_index(ml, col)] = silu(v);
+        }
+      }
     }
     return;
   }
-  if (W > 1) {
-    for (int half = W / 2; half >= 1; half >>= 1) {
-      __syncthreads();
-      if (wave >= half && wave < 2 * half)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[wave - half][acc_row(r, h)][j] = acc[r];
-      __syncthreads();
-      if (wave < half)
+  for (int mt = 0; mt < MT; ++mt) {
+    if (W > 1) {
+      for (int half = W / 2; half >= 1; half >>= 1) {
+        __syncthreads();
+        if (wave >= half && wave < 2 * half)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += red[wave][acc_row(r, h)][j];
+          for (int r = 0; r < 16; ++r) red[wave - half][acc_row(r, h)][j] = acc[mt][r];
+        __syncthreads();
+        if (wave < half)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mt][r] += red[wave][acc_row(r, h)][j];
+      }
     }
-  }
-  if (wave != 0) return;
+    if (wave != 0) continue;
 
-  float bv = -INFINITY;
-  uint32_t bi = (uint32_t)col;
+    float bv = -INFINITY;
+    uint32_t bi = (uint32_t)col;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int m = acc_row(r, h);
-    if (EPI == DEC_PART) {
-      if (cok) p.y[((size_t)blockIdx.y * 32 + m) * N + col] = acc[r];
-    } else if (EPI == DEC_PART_T) {
-      if (cok) p.y[(size_t)blockIdx.y * 32 * N + kq_index(m, col)] = acc[r];
-    } else if (EPI == DEC_SILU_T) {
-      if (cok) p.y[kq_index(m, col)] = silu(acc[r]);
-    } else if (EPI == DEC_LOGITS) {
-      // Logits, and the first maximum of the row over this tile's columns.
-      bv = -INFINITY;
-      bi = (uint32_t)col;
-      if (m < M && cok) {
-        p.y[(size_t)m * N + col] = acc[r];
-        bv = acc[r];
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int ml = acc_row(r, h), m = mt * 32 + ml;
+      if (EPI == DEC_PART) {
+        if (cok) p.y[((size_t)blockIdx.y * R + m) * N + col] = acc[mt][r];
+      } else if (EPI == DEC_PART_T) {
+        if (cok) p.y[((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, col)] = acc[mt][r];
+      } else if (EPI == DEC_SILU_T) {
+        if (cok) p.y[(size_t)mt * 32 * N + kq_index(ml, col)] = silu(acc[mt][r]);
+      } else if (EPI == DEC_LOGITS) {
+        // Logits, and the first maximum of the row over this tile's columns.
+        bv = -INFINITY;
+        bi = (uint32_t)col;
+        if (m < M && cok) {
+          p.y[(size_t)m * N + col] = acc[mt][r];
+          bv = acc[mt][r];
+        }
 #pragma unroll
-      for (int o = 16; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const uint32_t oi = __shfl_xor(bi, o, 64);
-        amax_merge(bv, bi, ov, oi);
+        for (int o = 16; o > 0; o >>= 1) {
+          const float ov = __shfl_xor(bv, o, 64);
+          const uint32_t oi = __shfl_xor(bi, o, 64);
+          amax_merge(bv, bi, ov, oi);
+        }
+        if (j == 0 && m < M)
+          p.amax[(size_t)m * gridDim.x + tile] = make_uint2(__float_as_uint(bv), bi);
       }
-      if (j == 0 && m < M)
-        p.amax[(size_t)m * gridDim.x + tile] = make_uint2(__float_as_uint(bv), bi);
     }
   }
 }
@@ -331,35 +355,29 @@ __device__ __forceinline__ void lm_load_b(float4 (&bb)[HQ], __amdgpu_buffer_rsrc
   }
 }
 
-template <int W, int HQ>
-__device__ __forceinline__ void lm_tile(const float4 (&a)[HQ], const float4 (&bb)[HQ],
-                                        float (*red)[32][33], int tile, const DecGemmParams& p,
-                                        float& bv, uint32_t& bi) {
+// One row tile's logits of one column tile: the waves' 32x32 tiles are
+// summed in LDS (waves in order), each wave finishing 32 / W rows.
+template <int W>
+__device__ __forceinline__ void lm_finish(const f32x16& acc, float (*red)[32][33], int tile,
+                                          int row0, const DecGemmParams& p, float& bv,
+                                          uint32_t& bi) {
   constexpr int RW = 32 / W;     // rows finished per wave
   constexpr int LPR = 64 / RW;   // lanes per finished row
   constexpr int E = 32 / LPR;    // columns per lane
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, h = lane >> 5;
-  f32x16 acc = zero16();
-#pragma unroll
-  for (int q = 0; q < HQ; ++q) {
-    acc = mfma32(a[q].x, bb[q].x, acc);
-    acc = mfma32(a[q].y, bb[q].y, acc);
-    acc = mfma32(a[q].z, bb[q].z, acc);
-    acc = mfma32(a[q].w, bb[q].w, acc);
-  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) red[wave][acc_row(r, h)][j] = acc[r];
   __syncthreads();
-  const int m = wave * RW + lane / LPR;
+  const int ml = wave * RW + lane / LPR, m = row0 + ml;
   const int c0 = (lane % LPR) * E;
   float v[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = red[0][m][c0 + e];
+  for (int e = 0; e < E; ++e) v[e] = red[0][ml][c0 + e];
 #pragma unroll
   for (int w = 1; w < W; ++w)
 #pragma unroll
-    for (int e = 0; e < E; ++e) v[e] += red[w][m][c0 + e];
+    for (int e = 0; e < E; ++e) v[e] += red[w][ml][c0 + e];
   if (m < p.M) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -372,13 +390,18 @@ __device__ __forceinline__ void lm_tile(const float4 (&a)[HQ], const float4 (&bb
   }
 }
 
-template <int W, int HL>
+// MT row tiles: A for all of them stays in registers and each weight tile
+// feeds the MFMAs of every row tile, so the weights are read once.  The LDS
+// buffers alternate per (column tile, row tile), so one barrier per row tile
+// orders each buffer's reads before its next writes.
+template <int W, int HL, int MT>
 __global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
   constexpr int RW = 32 / W;
   constexpr int LPR = 64 / RW;
   constexpr int HQ = HL / 4;
   static_assert(W * RW == 32 && LPR <= 64, "W must divide 32");
   static_assert(HL % 4 == 0, "HL must cover whole k-quads");
+  static_assert(MT == 1 || MT == 2, "one or two row tiles");
   __shared__ float red[2][W][32][33];
   const int N = p.N, K = p.K, Kp = p.Kp;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -390,16 +413,24 @@ __global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(p.w), (short)0, ntiles * Kp * 128, 0x00020000);
 
-  float4 a[HQ];
+  float4 a[MT][HQ];
 #pragma unroll
-  for (int q = 0; q < HQ; ++q) {
-    const int kq = kq0 + q;
-    a[q] = 4 * kq < K ? *reinterpret_cast<const float4*>(p.xt + ((size_t)kq * 32 + j) * 4)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+      const int kq = kq0 + q;
+      a[mt][q] = 4 * kq < K ? *reinterpret_cast<const float4*>(
+                                  p.xt + (size_t)mt * 32 * K + ((size_t)kq * 32 + j) * 4)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 
-  float bv = -INFINITY;
-  uint32_t bi = 0xFFFFFFFFu;
+  float bv[MT];
+  uint32_t bi[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    bv[mt] = -INFINITY;
+    bi[mt] = 0xFFFFFFFFu;
+  }
   // cur holds this tile's weights; nxt receives the next tile's while the
   // MFMAs run, and is handed over after the epilogue.
   float4 cur[HQ], nxt[HQ];
@@ -411,21 +442,39 @@ __global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
     // Compiler-only barrier: the prefetch stays issued here instead of being
     // sunk to its first use after the MFMAs (which would serialise it).
     asm volatile("" ::: "memory");
-    lm_tile<W, HQ>(a, cur, red[par], tile, p, bv, bi);
-    par ^= 1;
+    f32x16 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc[mt] = zero16();
+#pragma unroll
+      for (int q = 0; q < HQ; ++q) {
+        acc[mt] = mfma32(a[mt][q].x, cur[q].x, acc[mt]);
+        acc[mt] = mfma32(a[mt][q].y, cur[q].y, acc[mt]);
+        acc[mt] = mfma32(a[mt][q].z, cur[q].z, acc[mt]);
+        acc[mt] = mfma32(a[mt][q].w, cur[q].w, acc[mt]);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      lm_finish<W>(acc[mt], red[par], tile, 32 * mt, p, bv[mt], bi[mt]);
+      par ^= 1;
+    }
 #pragma unroll
     for (int q = 0; q < HQ; ++q) cur[q] = nxt[q];
   }
   // First maximum of each finished row over this block's columns.
 #pragma unroll
-  for (int o = LPR / 2; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, 64);
-    const uint32_t oi = __shfl_xor(bi, o, 64);
-    amax_merge(bv, bi, ov, oi);
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv[mt], o, 64);
+      const uint32_t oi = __shfl_xor(bi[mt], o, 64);
+      amax_merge(bv[mt], bi[mt], ov, oi);
+    }
+    const int m = 32 * mt + wave * RW + lane / LPR;
+    if (lane % LPR == 0 && m < p.M)
+      p.amax[(size_t)m * G + blockIdx.x] = make_uint2(__float_as_uint(bv[mt]), bi[mt]);
   }
-  const int m = wave * RW + lane / LPR;
-  if (lane % LPR == 0 && m < p.M)
-    p.amax[(size_t)m * G + blockIdx.x] = make_uint2(__float_as_uint(bv), bi);
 }
 
 // Single-query attention over the KV cache, one (sequence, head, split) per
@@ -516,7 +565,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), kn = q4, vn = q4;
   {
     const float* row = p.qkv + (size_t)b * 3 * d + (size_t)hh * HD + 4 * g;
-    const size_t ps = (size_t)32 * 3 * d;
+    const size_t ps = (size_t)p.rows * 3 * d;
     q4 = sum_parts4<4>(q4, row, ps, p.nparts);
     if (last) {
       kn = sum_parts4<4>(kn, row + d, ps, p.nparts);
@@ -622,9 +671,9 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
       o.z += wg * wo_s[w][t].z;
       o.w += wg * wo_s[w][t].w;
     }
-    *reinterpret_cast<float4*>(p.out_t + (size_t)sp * 32 * d +
-                               ((size_t)(hh * (HD / 4) + t) * 32 + b) * 4) = o;
-    if (t == 0) p.ml[((size_t)sp * p.H + hh) * 32 + b] = make_float2(M, L);
+    *reinterpret_cast<float4*>(p.out_t + (size_t)sp * p.rows * d + (size_t)(b >> 5) * 32 * d +
+                               ((size_t)(hh * (HD / 4) + t) * 32 + (b & 31)) * 4) = o;
+    if (t == 0) p.ml[((size_t)sp * p.H + hh) * p.rows + b] = make_float2(M, L);
   }
 }
 
@@ -641,6 +690,7 @@ template <int QPT>
 __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
   __shared__ float red4[4];
   const int m = blockIdx.x, d = p.d, nq = d / 4;
+  const size_t tile_off = (size_t)(m >> 5) * 32 * d;  // row m's 32-row k-quad tile
   // The gain does not depend on the row: request it first, so its memory
   // round trip overlaps the row's.
   float4 g[QPT];
@@ -665,12 +715,12 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
     const int q = threadIdx.x + 256 * i;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (q < nq) {
-      float* xq = p.xt + ((size_t)q * 32 + m) * 4;
+      float* xq = p.xt + tile_off + ((size_t)q * 32 + (m & 31)) * 4;
       if (gather) {
         if (row) v = *reinterpret_cast<const float4*>(row + 4 * q);
       } else {
         v = sum_parts4_2<AKH_NORM_NB1, 8>(*reinterpret_cast<const float4*>(xq),
-                                          p.parts + (size_t)m * d + 4 * q, (size_t)32 * d,
+                                          p.parts + (size_t)m * d + 4 * q, (size_t)p.rows * d,
                                           p.nparts);
       }
       *reinterpret_cast<float4*>(xq) = v;
@@ -685,7 +735,7 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
     const int q = threadIdx.x + 256 * i;
     if (q < nq) {
       const float4 v = x[i];
-      *reinterpret_cast<float4*>(p.xnt + ((size_t)q * 32 + m) * 4) = make_float4(
+      *reinterpret_cast<float4*>(p.xnt + tile_off + ((size_t)q * 32 + (m & 31)) * 4) = make_float4(
           __fmul_rn(__fmul_rn(v.x, rs), g[i].x), __fmul_rn(__fmul_rn(v.y, rs), g[i].y),
           __fmul_rn(__fmul_rn(v.z, rs), g[i].z), __fmul_rn(__fmul_rn(v.w, rs), g[i].w));
     }
@@ -831,10 +881,20 @@ hipError_t dec_go_shape(DecGemmParams p, hipStream_t s) {
   constexpr int WB = kOct ? S::W : S::W / 2, HLB = kOct ? S::HL : 2 * S::HL;
   p.kpass = role_kpass<ROLE, LARGE>(p.K, p.N);
   const dim3 g((p.N + 31) / 32, role_splits<ROLE, LARGE>(p.K, p.N));
-  if (p.wbf16)
-    hipLaunchKernelGGL((k_dec_gemm<WB, HLB, EPI, PRO, true>), g, dim3(64 * WB), 0, s, p);
-  else
-    hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, false>), g, dim3(64 * S::W), 0, s, p);
+#define AKH_DEC_GO(MT)                                                                        \
+  if (p.wbf16)                                                                                \
+    hipLaunchKernelGGL((k_dec_gemm<WB, HLB, EPI, PRO, true, MT>), g, dim3(64 * WB), 0, s, p); \
+  else                                                                                        \
+    hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, false, MT>), g, dim3(64 * S::W), 0, \
+                       s, p);
+  if (p.mt == 1) {
+    AKH_DEC_GO(1)
+  } else if (p.mt == 2) {
+    AKH_DEC_GO(2)
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef AKH_DEC_GO
   return hipGetLastError();
 }
 
@@ -844,12 +904,13 @@ hipError_t dec_go(const DecGemmParams& p, hipStream_t s) {
                               : dec_go_shape<ROLE, false, EPI, PRO>(p, s);
 }
 
-// The persistent lm_head covers K <= 2 * 8 * 64 (A held in registers) and
-// packed weights under 2 GiB (32-bit buffer offsets); its tiles are padded
-// to exactly 2 * 8 * HL rows.
+// The persistent lm_head covers K <= 2 * 8 * 64 (A held in registers; for
+// two row tiles K <= 768) and packed weights under 2 GiB (32-bit buffer
+// offsets); its tiles are padded to exactly 2 * 8 * HL rows.
 int lm_rows(int K) { return K <= 256 ? 256 : K <= 768 ? 768 : 1024; }
-bool lm_persistent(int N, int K) {
-  return K <= 1024 && (long)((N + 31) / 32) * lm_rows(K) * 128 < (1l << 31);
+bool lm_persistent(int N, int K, int mt) {
+  return K <= (mt == 1 ? 1024 : 768) &&
+         (long)((N + 31) / 32) * lm_rows(K) * 128 < (1l << 31);
 }
 
 }  // namespace
@@ -884,7 +945,9 @@ bool dec_bf16_capable(int role, int K, int N) {
     case DEC_CFG_OUT: return role_bf16<DEC_CFG_OUT>(K, N);
     case DEC_CFG_UP: return role_bf16<DEC_CFG_UP>(K, N);
     case DEC_CFG_DOWN: return role_bf16<DEC_CFG_DOWN>(K, N);
-    default: return !lm_persistent(N, K) && role_bf16<DEC_CFG_LM>(K, N);
+    // Tiles whose lm_head runs the persistent kernel at one row tile stay
+    // float (that kernel reads float quads).
+    default: return !lm_persistent(N, K, 1) && role_bf16<DEC_CFG_LM>(K, N);
   }
 }
 
@@ -901,22 +964,31 @@ int dec_gemm_splits(int role, int K, int N) {
 #ifndef AKH_LM_BLOCKS_PER_CU
 #define AKH_LM_BLOCKS_PER_CU 2  // 2 beat 1 and 3 (config 4: 34.7 us vs 39.6)
 #endif
-int dec_lm_parts(int N, int K, int num_cus) {
-  if (lm_persistent(N, K))
-    return std::max(1, std::min((N + 31) / 32, AKH_LM_BLOCKS_PER_CU * num_cus));
+int dec_lm_parts(int N, int K, int num_cus, int mt) {
+  // Two row tiles hold twice the A registers: one block per CU fits.
+  const int per_cu = mt == 1 ? AKH_LM_BLOCKS_PER_CU : 1;
+  if (lm_persistent(N, K, mt)) return std::max(1, std::min((N + 31) / 32, per_cu * num_cus));
   return (N + 31) / 32;
 }
 
 hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s) {
-  if (!lm_persistent(p.N, p.K)) return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
+  if (p.mt != 1 && p.mt != 2) return hipErrorInvalidValue;
+  if (!lm_persistent(p.N, p.K, p.mt)) return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
   if (p.Kp != lm_rows(p.K)) return hipErrorInvalidValue;
-  const dim3 g(dec_lm_parts(p.N, p.K, num_cus));
-  if (p.Kp == 256)
-    hipLaunchKernelGGL((k_dec_lm<8, 16>), g, dim3(512), 0, s, p);
-  else if (p.Kp == 768)
-    hipLaunchKernelGGL((k_dec_lm<8, 48>), g, dim3(512), 0, s, p);
-  else
-    hipLaunchKernelGGL((k_dec_lm<8, 64>), g, dim3(512), 0, s, p);
+  const dim3 g(dec_lm_parts(p.N, p.K, num_cus, p.mt));
+#define AKH_LM_GO(MT)                                           \
+  if (p.Kp == 256)                                              \
+    hipLaunchKernelGGL((k_dec_lm<8, 16, MT>), g, dim3(512), 0, s, p); \
+  else if (p.Kp == 768)                                         \
+    hipLaunchKernelGGL((k_dec_lm<8, 48, MT>), g, dim3(512), 0, s, p); \
+  else if (MT == 1)                                             \
+    hipLaunchKernelGGL((k_dec_lm<8, 64, 1>), g, dim3(512), 0, s, p);
+  if (p.mt == 1) {
+    AKH_LM_GO(1)
+  } else {
+    AKH_LM_GO(2)
+  }
+#undef AKH_LM_GO
   return hipGetLastError();
 }
 

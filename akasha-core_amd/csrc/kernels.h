@@ -10,8 +10,10 @@
 namespace akh {
 
 // Rows of the batched decode path: every fused decode kernel holds all
-// sequences of a step in one 32-row MFMA tile.
-constexpr int kMaxBatch = 32;
+// sequences of a step in one or two 32-row MFMA tiles (activations
+// [tiles][K/4][32][4]), so each weight byte is read once per step for up to
+// 64 sequences.
+constexpr int kMaxBatch = 64;
 
 // ---------------------------------------------------------------------------
 // Per-shader launchers (shader_kernels.hip): the reference Shader semantics,
@@ -186,6 +188,8 @@ struct DecGemmParams {
   const float2* ml;  // PRO_ATTN_MERGE: per split (max, sum) [nparts][K/hd][32]
   int hd;            // PRO_ATTN_MERGE: head_dim
   int kpass;         // set by the launcher: K passes per block (grid.y chunks)
+  int mt;            // 32-row tiles of the rows (1 or 2); partial tiles and
+                     // attention splits hold 32 * mt rows
 };
 
 // Decode weights are read from a copy packed once at upload: 32-column
@@ -212,25 +216,27 @@ int dec_gemm_splits(int role, int K, int N);
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s);
 
 // lm_head: logits y[M, N] = xt . w and argmax partials amax[M, parts], where
-// parts = dec_lm_parts(N, K, num_cus) (each the first maximum of the row
+// parts = dec_lm_parts(N, K, num_cus, mt) (each the first maximum of the row
 // over a subset of the columns).
-int dec_lm_parts(int N, int K, int num_cus);
+int dec_lm_parts(int N, int K, int num_cus, int mt);
 hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s);
 
 struct DecAttnParams {
-  const float* qkv;  // nparts partial tiles [nparts][32][3*d]
+  const float* qkv;  // nparts partial tiles [nparts][rows][3*d]
   int nparts;
   const float2* rope;  // [max_ctx, head_dim / 2] (cos, sin)
   void* kc;          // sequence b at kc + b * seq_stride, rows of d elements
   void* vc;          // (float, or bfloat16 when kv16)
   int kv16;
-  float* out_t;      // per split, unnormalised o in k-quad [splits][d/4][32][4]
-  float2* ml;        // per split (max, sum) [splits][H][32]
+  float* out_t;      // per split, unnormalised o in k-quad tiles
+                     // [splits][rows / 32][d/4][32][4]
+  float2* ml;        // per split (max, sum) [splits][H][rows]
   const int* pos;    // position of the new token of each sequence
   const int* active;  // sequences with active[b] == 0 are skipped (none if null)
   long seq_stride;
   int H, d;
   float scale;
+  int rows;          // 32 * the row tiles of the session
 };
 
 // act = silu(sum of nparts k-quad partial tiles), n elements per tile,
@@ -265,6 +271,8 @@ struct RowsNormParams {
   float eps;
   float* xnt;
   int d;
+  int rows;  // 32 * the row tiles: xt / xnt are [rows / 32][d/4][32][4] and
+             // the partial tiles [nparts][rows][d]
 };
 
 hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s);

@@ -959,6 +959,10 @@ struct akh_session {
   uint32_t* hist = nullptr; // [B, max_ctx + 1] token at each position
 
   int ks_qkv = 1, ks_out = 1, ks_up = 1, ks_down = 1;
+  // 32-row tiles of the decode rows (B <= 32 * mt): activations are
+  // [mt][K/4][32][4], partial tiles [splits][32 * mt][N].
+  int mt = 1;
+  size_t rows() const { return (size_t)32 * mt; }
 
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -1003,7 +1007,7 @@ struct akh_session {
 namespace {
 
 int lm_parts(const akh_session* s) {
-  return dec_lm_parts((int)s->m->cfg.vocab_size, (int)s->m->cfg.dim, s->be->num_cus);
+  return dec_lm_parts((int)s->m->cfg.vocab_size, (int)s->m->cfg.dim, s->be->num_cus, s->mt);
 }
 
 void free_prefill(akh_session* s) {
@@ -1054,6 +1058,7 @@ akh_status upload_positions(akh_session* s) {
 DecGemmParams dec_base(akh_session* s) {
   DecGemmParams p{};
   p.M = (int)s->B;
+  p.mt = s->mt;
   return p;
 }
 
@@ -1070,6 +1075,7 @@ RowsNormParams norm_base(akh_session* s, const float* gain) {
   r.gain = gain;
   r.eps = s->m->cfg.norm_eps;
   r.d = (int)s->m->cfg.dim;
+  r.rows = (int)s->rows();
   return r;
 }
 
@@ -1107,6 +1113,7 @@ hipError_t enqueue_attn(akh_session* s, uint32_t l, hipEvent_t t0 = nullptr,
   p.d = (int)c.dim;
   const uint32_t hd = c.dim / c.num_heads;
   p.scale = 1.0f / sqrtf((float)hd);
+  p.rows = (int)s->rows();
   return launch_dec_attn(p, (int)s->B, (int)hd, s->be->stream, t0, t1);
 }
 
@@ -1157,7 +1164,7 @@ hipError_t enqueue_down(akh_session* s, uint32_t l) {
   if (s->ks_up == 1) {
     p.xt = s->p_up;  // ffn_up applied SiLU to its whole sums
   } else if (s->up_act) {
-    hipError_t e = launch_silu_sum(s->p_up, s->ks_up, s->up_act, (size_t)32 * c.ffn_hidden,
+    hipError_t e = launch_silu_sum(s->p_up, s->ks_up, s->up_act, s->rows() * c.ffn_hidden,
                                    s->be->stream);
     if (e != hipSuccess) return e;
     p.xt = s->up_act;
@@ -1391,7 +1398,7 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
   *out = nullptr;
   const akh_model_config& c = m->cfg;
   CHECK_ARG(batch >= 1 && (!decode || batch <= (uint32_t)kMaxBatch),
-            "akh_session_new: batch must be in 1..32");
+            "akh_session_new: batch must be in 1..64");
   CHECK_ARG(max_context_len >= 1, "akh_session_new: max_context_len is 0");
   const uint32_t hd = c.dim / c.num_heads;
   CHECK_ARG(supported_head_dim(hd) && (hd >= 4 || !decode),
@@ -1413,7 +1420,10 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
   s->ks_up = dec_gemm_splits(DEC_CFG_UP, c.dim, c.ffn_hidden);
   s->ks_down = dec_gemm_splits(DEC_CFG_DOWN, c.ffn_hidden, c.dim);
 
-  const size_t d = c.dim, V = c.vocab_size, F = c.ffn_hidden, R = kMaxBatch;
+  s->mt = batch > 32 ? 2 : 1;
+  // Activation and partial tiles hold R rows; the per-row step state holds
+  // kMaxBatch entries (it is uploaded and downloaded whole).
+  const size_t d = c.dim, V = c.vocab_size, F = c.ffn_hidden, R = s->rows(), RB = kMaxBatch;
   hipError_t e = hipSetDevice(s->be->device);
   auto alloc = [&](void** p, size_t bytes) {
     if (e == hipSuccess) e = hipMalloc(p, bytes);
@@ -1433,13 +1443,13 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
   alloc((void**)&s->p_down, (size_t)s->ks_down * R * d * 4);
   alloc((void**)&s->logits, R * V * 4);
   alloc((void**)&s->amax, R * (size_t)lm_parts(s) * sizeof(uint2));
-  alloc((void**)&s->tok, R * 4);
-  alloc((void**)&s->pos, R * 4);
+  alloc((void**)&s->tok, RB * 4);
+  alloc((void**)&s->pos, RB * 4);
   alloc((void**)&s->hist, (size_t)batch * (max_context_len + 1) * 4);
-  alloc((void**)&s->active, R * sizeof(int));
-  alloc((void**)&s->done, R * sizeof(int));
-  alloc((void**)&s->gstart, R * sizeof(int));
-  alloc((void**)&s->gcount, R * sizeof(uint32_t));
+  alloc((void**)&s->active, RB * sizeof(int));
+  alloc((void**)&s->done, RB * sizeof(int));
+  alloc((void**)&s->gstart, RB * sizeof(int));
+  alloc((void**)&s->gcount, RB * sizeof(uint32_t));
   alloc((void**)&s->gwbuf, sample_scratch_bytes((int)batch, (int)V));
   }
   if (e == hipSuccess) {

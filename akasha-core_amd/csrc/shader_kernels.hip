@@ -281,7 +281,7 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
                          akh_matmul_meta shape, const akh_matmul_meta* meta,
                          int accumulate, hipStream_t s) {
   if (shape.m == 0 || shape.n == 0) return hipSuccess;
-  if (shape.m <= (uint32_t)kMaxBatch) {
+  if (shape.m <= 32u) {  // one 32-row MFMA tile
     hipLaunchKernelGGL(k_shader_skinny, dim3((shape.n + 31) / 32), dim3(256),
                        0, s, a, b, c, meta, accumulate);
     return hipGetLastError();

@@ -100,45 +100,44 @@ def prefill_rates(ms, gemm, attn, lm, x6_flop):
 
 
 def scaled_decode(hip, be, model, cfg, T, steps):
-    """Config 5 decode legs: 64 sequences as two 32-row sessions, `steps`
-    steps ending at KV length T, with the f32 KV cache and then the optional
-    bfloat16 one.  The weights are bf16-valued and read as bfloat16 tiles, so
-    their algorithmic bytes are 2 per parameter (twice: one read per
-    session)."""
+    """Config 5 decode legs: 64 sequences in one session (two 32-row MFMA
+    tiles sharing every weight read), `steps` steps ending at KV length T,
+    with the f32 KV cache and then the optional bfloat16 one.  The weights
+    are bf16-valued and read as bfloat16 tiles, so their algorithmic bytes
+    are 2 per parameter, read once per step."""
     d, L, V = cfg.dim, cfg.num_layers, cfg.vocab_size
+    B = 64
     weights = 2 * (sum(int(np.prod(x)) for x in cfg.param_shapes()) - V * d)
-    kv = sum(2 * L * 64 * (T - steps + i + 1) * d * 4 for i in range(steps))
-    sess = [hip.Session(model, T, 32) for _ in range(2)]
-    out = {"decode_workload": f"64 sequences (2 x 32-row sessions), {steps} steps to KV length "
-                              f"{T} over a zero KV prefix (set_len)"}
+    kv = sum(2 * L * B * (T - steps + i + 1) * d * 4 for i in range(steps))
+    s = hip.Session(model, T, B)
+    out = {"decode_workload": f"{B} sequences in one session, {steps} steps to KV length "
+                              f"{T} over a zero KV prefix (set_len)",
+           "decode_launches_per_step": s.decode_launches()}
     for kv16 in (False, True):
-        for s in sess:
-            if kv16:
-                s.set_len(0)
-                s.set_kv_bf16(True)
-            s.set_len(T - steps)
-            s.decode_greedy(1, want_tokens=False)  # capture + warm
-            s.set_len(T - steps)
+        if kv16:
+            s.set_len(0)
+            s.set_kv_bf16(True)
+        s.set_len(T - steps)
+        s.decode_greedy(1, want_tokens=False)  # capture + warm
+        s.set_len(T - steps)
         be.synchronize()
         be.timer_start()
-        for s in sess:
-            s.decode_greedy(steps, want_tokens=False)
+        s.decode_greedy(steps, want_tokens=False)
         ms = be.timer_stop()
-        step_bytes = (2 * weights * steps + (kv / 2 if kv16 else kv)) / steps
+        step_bytes = (weights * steps + (kv / 2 if kv16 else kv)) / steps
         key = "decode_kv16" if kv16 else "decode"
         out.update({f"{key}_ms_per_step": round(ms / steps, 3),
-                    f"{key}_tok_s": round(64 * steps / (ms / 1e3), 1),
+                    f"{key}_tok_s": round(B * steps / (ms / 1e3), 1),
                     f"{key}_hbm_frac": round(step_bytes / (ms / steps / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
                     f"{key}_bytes_per_step": int(step_bytes)})
-    for s in sess:
-        s.close()
+    s.close()
     return out
 
 
 def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=True):
     """Config 5: the scaled architecture (dim 2048, 24 layers, 16 x 128, FFN
     8192, vocab 50257) with bf16-valued weights (seed 5).  Decode: 64
-    sequences (two 32-row sessions) for `steps` steps ending at KV length
+    sequences (one session) for `steps` steps ending at KV length
     2048, over a zero KV prefix declared with set_len (the cost of a step does
     not depend on the cached values).  Prefill: 8 x 2048 (seed 7)."""
     cfg = pkg.ModelConfig.scaled()

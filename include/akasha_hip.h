@@ -358,7 +358,7 @@ akh_status akh_model_load_checkpoint(akh_model* m, const char* path,
 
 /* InferenceSession::new + replace_cache(Cache::new(...)) for `batch`
  * independent sequences (inference.rs:25-54; inference_graphs.rs:520-538).
- * batch <= 32. */
+ * batch <= 64: up to two 32-row MFMA tiles share every weight read. */
 akh_status akh_session_new(akh_model* m, uint32_t max_context_len,
                            uint32_t batch, akh_session** out);
 void akh_session_free(akh_session* s);

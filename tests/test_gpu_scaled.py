@@ -1,0 +1,108 @@
+"""Config 5 (the scaled architecture: dim 2048, 24 layers, 16 heads x 128,
+FFN 8192, vocab 50257, ctx 2048, bfloat16-valued weights from seed 5) at its
+full shapes on the GPU.
+
+The CPU oracle cannot run this model at these sizes in test time (its
+prefill of one 2040-token prompt is ~5 TFLOP of scalar loops); parity with
+the oracle is checked on this architecture at small sizes in
+test_gpu_session.py and test_gpu_bf16.py.  Here the full shapes are held to
+size-independent properties:
+
+- batch invariance inside the 64-sequence decode at KV length 2048 (two
+  32-row tiles, one weight read): a sequence's logits and tokens equal the
+  same prompt decoded alone;
+- bfloat16 weight tiles against float tiles of the same values at KV 2048;
+- the 8 x 2048 prefill on the split-bf16 kernels against the fp32-MFMA
+  kernels;
+- prefill == sequential decode (inference.rs:334-359): a 2048-token prefill
+  against a 2040-token prefill followed by the last 8 tokens as decode
+  steps.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def scaled(backend, pkg):
+    cfg = pkg.ModelConfig.scaled()
+    w = pkg.synthetic_weights(cfg, seed=5, bf16=True)
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    del w
+    yield cfg, model
+    model.close()
+
+
+def _decode(s, steps):
+    return [s.decode_step(None) for _ in range(steps)]
+
+
+def test_scaled_decode_64_rows_at_kv_2048(pkg, scaled):
+    cfg, model = scaled
+    hip = pkg.hip
+    B, S, steps = 64, 2040, 8
+    toks = pkg.synthetic_tokens(B * S, cfg.vocab_size, seed=8).reshape(B, S)
+    s = hip.Session(model, 2048, B)
+    first = s.prefill(toks)
+    run = [first] + _decode(s, steps)
+    assert list(s.cur_len()) == [2048] * B
+    # Batch invariance: rows of the first tile, of the second, and the last.
+    for b in (5, 37, 63):
+        one = hip.Session(model, 2048, 1)
+        alone = [one.prefill(toks[b][None])] + _decode(one, steps)
+        for i, ((lg, tk), (l1, t1)) in enumerate(zip(run, alone)):
+            assert np.abs(lg[b] - l1[0]).max() < 1e-4, f"sequence {b} step {i}"
+            assert int(tk[b]) == int(t1[0]), f"sequence {b} step {i}"
+        one.close()
+    # bfloat16 weight tiles (the default for these weights) against float
+    # tiles of the same values, the same 8 steps from the same caches.
+    assert model.set_bf16_tiles(False) == 0
+    try:
+        s.truncate(S)
+        f32 = _decode(s, steps)
+    finally:
+        model.set_bf16_tiles(True)
+    for i, ((a, ta), (b, tb)) in enumerate(zip(run[1:], f32)):
+        assert np.abs(a - b).max() < 1e-4, f"step {i}"
+        assert np.array_equal(ta, tb), f"step {i}"
+    s.close()
+
+
+def test_scaled_prefill_8x2048_split_bf16_vs_fp32_mfma(pkg, scaled):
+    cfg, model = scaled
+    B, S = 8, 2048
+    toks = pkg.synthetic_tokens(B * S, cfg.vocab_size, seed=7).reshape(B, S)
+    s = pkg.hip.Session(model, S, B)
+    l6, t6 = s.prefill(toks)
+    k6 = s.cache(23, 6, 0)
+    s.reset()
+    model.set_prefill_x6(False)
+    try:
+        l32, t32 = s.prefill(toks)
+        k32 = s.cache(23, 6, 0)
+    finally:
+        model.set_prefill_x6(True)
+    assert np.abs(l6 - l32).max() < 1e-4
+    assert np.array_equal(t6, t32)
+    np.testing.assert_allclose(k6, k32, rtol=0, atol=1e-4)
+    s.close()
+
+
+def test_scaled_prefill_equals_sequential_decode(pkg, scaled):
+    cfg, model = scaled
+    B, S, tail = 2, 2048, 8
+    toks = pkg.synthetic_tokens(B * S, cfg.vocab_size, seed=9).reshape(B, S)
+    a = pkg.hip.Session(model, S, B)
+    full, _ = a.prefill(toks)
+    b = pkg.hip.Session(model, S, B)
+    b.prefill(toks[:, :S - tail])
+    for t in range(S - tail, S):
+        last, _ = b.decode_step(np.ascontiguousarray(toks[:, t]))
+    assert np.abs(full - last).max() < 1e-3
+    np.testing.assert_allclose(a.cache(20, 1, 1)[S - tail:], b.cache(20, 1, 1)[S - tail:],
+                               rtol=0, atol=1e-3)
+    a.close()
+    b.close()

@@ -32,6 +32,25 @@ def _oracle_greedy(ora, cfg, w, max_ctx, prompt, steps):
     return logits, toks
 
 
+def _oracle_greedy_many(ora, cfg, w, max_ctx, prompts, steps):
+    """_oracle_greedy for several prompts at once: one single-threaded
+    oracle session per host thread (the checker's time, not the product's)."""
+    import threading
+    out = [None] * len(prompts)
+
+    def run(i):
+        out[i] = _oracle_greedy(ora, cfg, w, max_ctx, prompts[i], steps)
+
+    ora.set_threads(1)
+    ts = [threading.Thread(target=run, args=(i,)) for i in range(len(prompts))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert all(o is not None for o in out)
+    return out
+
+
 def test_tiny_prefill_and_decode_match_oracle(backend, pkg, ora):
     # ModelConfig::new(97,32,4,2,16), prompt [3,41,7,96,0,25]
     # (inference.rs:334-359).
@@ -80,6 +99,72 @@ def test_batched_sessions_are_independent(backend, pkg, ora):
         for i in range(steps + 1):
             assert np.abs(got_l[i][b] - rl[i]).max() < TOL
             assert int(got_t[i][b]) == rt[i]
+
+
+def _run(s, prompts, steps):
+    out = [s.prefill(prompts)]
+    out += [s.decode_step(None) for _ in range(steps)]
+    return out
+
+
+@pytest.mark.parametrize("kv16", [False, True])
+def test_two_row_tiles_match_oracle_and_smaller_sessions(backend, pkg, ora, kv16):
+    # A session of 33..64 sequences holds its rows as two 32-row MFMA tiles
+    # that share every weight read.  40 sequences (rows 32..39 in a second,
+    # partly filled tile) give, row for row, what a 32-row and an 8-row
+    # session give on the same prompts (each row's arithmetic does not
+    # depend on the batch), and, on the fp32 cache, what the oracle gives.
+    cfg = pkg.ModelConfig.new(300, 128, 2, 2, 40)
+    w = pkg.synthetic_weights(cfg, seed=51)
+    B, S, steps = 40, 13, 6
+    prompts = pkg.synthetic_tokens(B * S, cfg.vocab_size, 52).reshape(B, S)
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    sess = [pkg.hip.Session(model, 40, n) for n in (B, 32, 8)]
+    if kv16:
+        for s in sess:
+            s.set_kv_bf16(True)
+    got = _run(sess[0], prompts, steps)
+    lo = _run(sess[1], prompts[:32], steps)
+    hi = _run(sess[2], prompts[32:], steps)
+    for i in range(steps + 1):
+        lg, tk = got[i]
+        np.testing.assert_allclose(lg[:32], lo[i][0], rtol=0, atol=1e-5)
+        np.testing.assert_allclose(lg[32:], hi[i][0], rtol=0, atol=1e-5)
+        assert np.array_equal(tk, np.concatenate([lo[i][1], hi[i][1]]))
+    # Graph replays of the same steps give the same tokens.
+    sess[0].truncate(S)
+    assert np.array_equal(sess[0].decode_greedy(steps),
+                          np.stack([got[i][1] for i in range(1, steps + 1)]))
+    if not kv16:
+        refs = _oracle_greedy_many(ora, cfg, w, 40, list(prompts), steps)
+        for b, (rl, rt) in enumerate(refs):
+            for i in range(steps + 1):
+                assert np.abs(got[i][0][b] - rl[i]).max() < TOL, f"sequence {b} step {i}"
+                assert int(got[i][1][b]) == rt[i], f"sequence {b} step {i}"
+    for s in sess:
+        s.close()
+    model.close()
+
+
+def test_two_row_tiles_bf16_weight_tiles(backend, pkg):
+    # bfloat16-valued weights read as bfloat16 tiles by a 40-row session:
+    # within fp32 rounding of the float tiles, same tokens (as at 32 rows).
+    cfg = pkg.ModelConfig.new(500, 1152, 9, 2, 40)
+    w = pkg.synthetic_weights(cfg, seed=53, bf16=True)
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    s = pkg.hip.Session(model, 40, 40)
+    toks = pkg.synthetic_tokens(40 * 9, cfg.vocab_size, seed=54).reshape(40, 9)
+    runs = {}
+    for allow in (True, False):
+        model.set_bf16_tiles(allow)
+        s.reset()
+        runs[allow] = _run(s, toks, 3)
+    for (a, ta), (b, tb) in zip(runs[True], runs[False]):
+        assert np.abs(a - b).max() < 1e-4 and np.array_equal(ta, tb)
+    s.close()
+    model.close()
 
 
 def test_decode_greedy_matches_step_by_step(backend, pkg):
@@ -139,7 +224,7 @@ def test_session_errors(backend, pkg):
     with pytest.raises(h.ContextFull):
         s.decode_step(None)
     with pytest.raises(h.InvalidArgument):
-        h.Session(s.model, 16, 33)
+        h.Session(s.model, 16, 65)
 
 
 def test_hall1_c1_greedy_parity(backend, pkg, ora):
@@ -173,23 +258,24 @@ def test_hall1_c1_greedy_parity(backend, pkg, ora):
 def test_hall1_c4_batch_properties(backend, pkg, ora):
     # Config 4 at full size: 32 sequences prefilled with 448 tokens
     # (seed 4), then the 64 greedy decode steps at positions 448..511 that
-    # fill the 512-row cache (the bench's workload).  Sequence 0 is checked against the oracle at
-    # every step (identical tokens, logits within 1e-3); the batch is checked
-    # for batch invariance against single-sequence sessions.
+    # fill the 512-row cache (the bench's workload).  Eight sequences are
+    # checked against the oracle over the whole run (identical tokens at
+    # every step, logits within 1e-3); the batch is checked for batch
+    # invariance against single-sequence sessions.
     cfg = pkg.ModelConfig.akasha_hall_1()
     w = pkg.synthetic_weights(cfg, seed=0)
     B, S, steps, inv_steps = 32, 448, 64, 4
+    checked = [0, 3, 9, 14, 20, 25, 28, 31]
     toks = pkg.synthetic_tokens(B * S, cfg.vocab_size, seed=4).reshape(B, S)
     model, s = _session(pkg, backend, cfg, w, 512, B)
     logits, nxt = s.prefill(toks)
-    all_l, all_t = [logits[:, :]], [nxt]
+    all_l, all_t = [logits[checked]], [nxt]
     for _ in range(steps):
         logits, nxt = s.decode_step(None)
-        all_l.append(logits[[0, 3, 31]])
+        all_l.append(logits[checked])
         all_t.append(nxt)
-    all_l[0] = all_l[0][[0, 3, 31]]
     # Batch invariance: sequence b alone gives the same results.
-    for j, b in ((1, 3), (2, 31)):
+    for j, b in ((1, 3), (7, 31)):
         single = pkg.hip.Session(model, 512, 1)
         l1, t1 = single.prefill(toks[b][None])
         assert np.abs(l1[0] - all_l[0][j]).max() < 1e-4
@@ -199,14 +285,11 @@ def test_hall1_c4_batch_properties(backend, pkg, ora):
             assert np.abs(l1[0] - all_l[i][j]).max() < 1e-4
             assert int(t1[0]) == int(all_t[i][b])
         single.close()
-    ora.set_threads(16)
-    try:
-        rl, rt = _oracle_greedy(ora, cfg, w, 512, toks[0], steps)
-    finally:
-        ora.set_threads(1)
-    for i in range(steps + 1):
-        assert np.abs(all_l[i][0] - rl[i]).max() < TOL, f"step {i}"
-        assert int(all_t[i][0]) == rt[i], f"step {i}"
+    refs = _oracle_greedy_many(ora, cfg, w, 512, [toks[b] for b in checked], steps)
+    for j, (b, (rl, rt)) in enumerate(zip(checked, refs)):
+        for i in range(steps + 1):
+            assert np.abs(all_l[i][j] - rl[i]).max() < TOL, f"sequence {b} step {i}"
+            assert int(all_t[i][b]) == rt[i], f"sequence {b} step {i}"
     # KV append landed at the right rows: the whole 512-row cache is filled.
     kc = s.cache(5, 7, 0)
     assert S + steps == 512 and np.all(np.abs(kc).sum(1) > 0)
