@@ -705,7 +705,7 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
     const uint32_t id = p.ids[m];
     row = id < p.vocab ? p.table + (size_t)id * d : nullptr;
   } else if (p.src) {
-    row = p.src + (size_t)(p.row0 + (long)m * p.row_stride) * d;
+    row = p.src + (size_t)(p.src_rows ? (long)p.src_rows[m] : p.row0 + (long)m * p.row_stride) * d;
   }
   const bool gather = p.ids || p.src;
   float4 x[QPT];
@@ -744,7 +744,7 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
 
 __global__ __launch_bounds__(256) void k_argmax_final(
     const uint2* part, int ntiles, uint32_t* tok, int* pos, uint32_t* hist,
-    int hist_stride, int next_pos) {
+    int hist_stride, int next_pos, const int* at) {
   const int m = blockIdx.x;
   float bv = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
@@ -764,7 +764,7 @@ __global__ __launch_bounds__(256) void k_argmax_final(
       }
       pos[m] = p0 + 1;
     } else if (hrow) {
-      hrow[next_pos] = id;
+      hrow[at ? at[m] : next_pos] = id;
     }
     tok[m] = id;
   }
@@ -1083,11 +1083,19 @@ hipError_t launch_silu_sum(const float* parts, int nparts, float* act, size_t n,
 // Prefill's fp32 K/V rows into a bfloat16 cache, four elements per thread.
 __global__ void k_kv_store_bf16(const float* __restrict__ k, const float* __restrict__ v,
                                 uint16_t* kc, uint16_t* vc, int S, int d, long seq_stride,
-                                size_t n4) {
+                                const int2* __restrict__ rowmap, size_t n4) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
        i += (size_t)gridDim.x * blockDim.x) {
     const size_t row = i / (d / 4), c = (i % (d / 4)) * 4;
-    const size_t b = row / S, t = row % S;
+    size_t b, t;
+    if (rowmap) {
+      const int2 st = rowmap[row];
+      b = (size_t)st.x;
+      t = (size_t)st.y;
+    } else {
+      b = row / S;
+      t = row % S;
+    }
     const size_t dst = b * seq_stride + t * d + c;
     const float4 a = *reinterpret_cast<const float4*>(k + row * d + c);
     const float4 e = *reinterpret_cast<const float4*>(v + row * d + c);
@@ -1097,12 +1105,13 @@ __global__ void k_kv_store_bf16(const float* __restrict__ k, const float* __rest
 }
 
 hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
-                                int batch, int S, int d, long seq_stride, hipStream_t s) {
-  if (d % 4 != 0) return hipErrorInvalidValue;
-  const size_t n4 = (size_t)batch * S * (d / 4);
+                                size_t rows, int S, int d, long seq_stride,
+                                const int2* rowmap, hipStream_t s) {
+  if (d % 4 != 0 || (!rowmap && S <= 0)) return hipErrorInvalidValue;
+  const size_t n4 = rows * (d / 4);
   const size_t blocks = std::min<size_t>((n4 + 255) / 256, 65535u * 16u);
   hipLaunchKernelGGL(k_kv_store_bf16, dim3((unsigned)std::max<size_t>(1, blocks)), dim3(256), 0,
-                     s, k, v, kc, vc, S, d, seq_stride, n4);
+                     s, k, v, kc, vc, S, d, seq_stride, rowmap, n4);
   return hipGetLastError();
 }
 
@@ -1121,9 +1130,9 @@ hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s) {
 
 hipError_t launch_argmax_final(const uint2* part, int ntiles, int M,
                                uint32_t* tok, int* pos, uint32_t* hist,
-                               int hist_stride, int next_pos, hipStream_t s) {
+                               int hist_stride, int next_pos, hipStream_t s, const int* at) {
   hipLaunchKernelGGL(k_argmax_final, dim3(M), dim3(256), 0, s, part, ntiles,
-                     tok, pos, hist, hist_stride, next_pos);
+                     tok, pos, hist, hist_stride, next_pos, at);
   return hipGetLastError();
 }
 

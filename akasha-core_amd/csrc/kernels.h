@@ -102,6 +102,12 @@ struct GemmParams {
   const uint16_t* bt16;  // [N, K]
   // launch_gemm_x6: the transposed fp32 weights.
   const float* bt;  // [N, K]
+  // GEMM_QKV on ragged prompts packed back to back: row m is position
+  // rowmap[m].y of sequence rowmap[m].x (instead of m / S, m % S).
+  const int2* rowmap;
+  // GEMM_QKV: K and V rows go to kcache / vcache at row m (rows packed like
+  // the prompt's) instead of sequence * seq_stride + position.
+  int kv_packed;
 };
 
 struct FlashParams {
@@ -119,6 +125,12 @@ struct FlashParams {
   uint16_t* o16;  // launch_flash_bf16: bfloat16 output (o unused)
   int x6;         // launch_flash, head_dim 64 / 128: split-bfloat16 MFMAs
                   // (fp32 accuracy) instead of fp32 MFMAs
+  // Ragged prompts packed back to back: sequence b's rows of q, o (and lse)
+  // are [rows_at[b], rows_at[b + 1]) and its length is their count (S is
+  // then the longest); K and V rows likewise if kv_packed, else at
+  // b * kv_bs.  Null: the uniform layout above.
+  const int* rows_at;
+  int kv_packed;
 };
 
 hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s);
@@ -246,10 +258,12 @@ hipError_t launch_silu_sum(const float* parts, int nparts, float* act, size_t n,
 
 // Splits per (sequence, head): the partial states the out_proj GEMM merges.
 int dec_attn_splits();
-// Prefill rows k, v [batch * S, d] (fp32) into a bfloat16 KV cache
-// (sequence b at b * seq_stride, row t at t * d).
+// Prefill rows k, v [rows, d] (fp32) into a bfloat16 KV cache (sequence b
+// at b * seq_stride, position t at t * d): row = b * S + t, or, for ragged
+// prompts packed back to back, (b, t) = rowmap[row].
 hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
-                                int batch, int S, int d, long seq_stride, hipStream_t s);
+                                size_t rows, int S, int d, long seq_stride,
+                                const int2* rowmap, hipStream_t s);
 // With t0 and t1 set, the dispatch records them at its own start and end.
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
                            hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
@@ -264,6 +278,7 @@ struct RowsNormParams {
   uint32_t vocab;
   const float* src;
   long row0, row_stride;
+  const int* src_rows;  // if set, row m of src is src_rows[m] (ragged last rows)
   const float* parts;
   int nparts;
   float* xt;
@@ -280,10 +295,12 @@ hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s);
 // Greedy token per row from the lm_head partials.  With `pos`, also the
 // decode step's bookkeeping on the device: hist[m, pos] = consumed token,
 // hist[m, pos + 1] = chosen token, pos[m] += 1.  Without it (prefill) the
-// chosen token is recorded at hist[m, next_pos].
+// chosen token is recorded at hist[m, next_pos], or at hist[m, at[m]] when
+// `at` is given (ragged prompts).
 hipError_t launch_argmax_final(const uint2* part, int ntiles, int M,
                                uint32_t* tok, int* pos, uint32_t* hist,
-                               int hist_stride, int next_pos, hipStream_t s);
+                               int hist_stride, int next_pos, hipStream_t s,
+                               const int* at = nullptr);
 
 // ---------------------------------------------------------------------------
 // Token sampling (sample_kernels.hip): sample_token of sampling.rs:3-81 per
@@ -339,7 +356,11 @@ constexpr size_t kNoAllocSampleElems = (size_t)1 << 21;
 constexpr int kMaxDevices = 64;
 hipError_t sample_noalloc_scratch(int device, double** ptr);
 hipError_t launch_sample_rows(const SampleArgs& a, int rows, hipStream_t s);
-// pos[m] += active[m] for m < rows: the positions of the rows decoded.
-hipError_t launch_advance(int* pos, const int* active, int rows, hipStream_t s);
+// pos[m] += active[m] for m < rows: the positions of the rows decoded.  With
+// tok, each active row first records its decoded token tok[m] at
+// hist[m, pos[m]].
+hipError_t launch_advance(int* pos, const int* active, int rows, hipStream_t s,
+                          const uint32_t* tok = nullptr, uint32_t* hist = nullptr,
+                          long hist_stride = 0);
 
 }  // namespace akh

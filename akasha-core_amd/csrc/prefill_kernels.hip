@@ -58,7 +58,15 @@ __device__ __forceinline__ void epi_pair_gemm(const GemmParams& p, int M,
     // Columns [0, d) are Q, [d, 2d) K, [2d, 3d) V (weights.rs:49-58).
     const int dim = p.dim;
     const int region = n / dim, c = n - region * dim;
-    const int seq = m / p.S, t = m - seq * p.S;
+    int seq, t;
+    if (p.rowmap) {
+      const int2 st = p.rowmap[m];
+      seq = st.x;
+      t = st.y;
+    } else {
+      seq = m / p.S;
+      t = m - seq * p.S;
+    }
     if (region < 2) {
       const int i = (c % p.head_dim) >> 1;
       const float2 cs = p.rope[(size_t)t * (p.head_dim >> 1) + i];
@@ -67,6 +75,8 @@ __device__ __forceinline__ void epi_pair_gemm(const GemmParams& p, int M,
     float* dst;
     if (region == 0)
       dst = p.q_out + (size_t)m * dim + c;
+    else if (p.kv_packed)
+      dst = (region == 1 ? p.kcache : p.vcache) + (size_t)m * dim + c;
     else
       dst = (region == 1 ? p.kcache : p.vcache) + (size_t)seq * p.seq_stride +
             (size_t)t * dim + c;
@@ -198,22 +208,44 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 // it or change the head size; for such a meta, and for a head past the live
 // head count (the reference kernel returns for head >= num_heads,
 // cuda.rs:647), the block returns false and touches no memory.
+//
+// It also places sequence b: element offsets of its first row in q, in k
+// and v, and in o, and of its lse rows -- per-sequence strides, the live
+// meta's row_offset, or, for ragged prompts packed back to back, the rows
+// rows_at[b] .. rows_at[b + 1] (whose count is then its length S).
+struct FlashSeq {
+  int S, d;
+  float scale;
+  long q, kv, o, l;
+};
 template <int HD>
-__device__ __forceinline__ bool flash_shape(const FlashParams& p, int hh, int& S, int& d,
-                                            float& scale, long& roff) {
-  S = p.S;
-  d = p.d;
-  scale = p.scale;
-  roff = 0;
+__device__ __forceinline__ bool flash_seq(const FlashParams& p, int hh, int b, FlashSeq& f) {
+  f.S = p.S;
+  f.d = p.d;
+  f.scale = p.scale;
+  long roff = 0;
   if (p.meta) {
     const akh_flash_attn_meta m = *p.meta;
     if ((int)m.head_dim != HD || (int)m.seq_len > p.S || (int)m.dim > p.d) return false;
-    S = (int)m.seq_len;
-    d = (int)m.dim;
-    scale = m.scale;
-    roff = (long)m.row_offset * d;
+    f.S = (int)m.seq_len;
+    f.d = (int)m.dim;
+    f.scale = m.scale;
+    roff = (long)m.row_offset * f.d;
   }
-  return hh < d / HD;
+  if (hh >= f.d / HD) return false;
+  if (p.rows_at) {
+    const int r0 = p.rows_at[b];
+    f.S = min(p.rows_at[b + 1] - r0, p.S);
+    f.q = f.o = (long)r0 * f.d;
+    f.kv = p.kv_packed ? f.q : (long)b * p.kv_bs;
+    f.l = (long)r0 * (f.d / HD);
+  } else {
+    f.q = roff + (long)b * p.q_bs;
+    f.kv = roff + (long)b * p.kv_bs;
+    f.o = roff + (long)b * p.o_bs;
+    f.l = (long)b * p.lse_bs;
+  }
+  return true;
 }
 
 // Causal flash attention on MFMA for head_dim 64 and 128.  Block = 4 waves x
@@ -237,10 +269,10 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
   float (*Vs)[HD] = reinterpret_cast<float (*)[HD]>(lds + KB * KP);
 
   const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
-  int S, d;
-  float scale;
-  long roff;
-  if (!flash_shape<HD>(p, hh, S, d, scale, roff)) return;
+  FlashSeq fs;
+  if (!flash_seq<HD>(p, hh, b, fs)) return;
+  const int S = fs.S, d = fs.d;
+  const float scale = fs.scale;
   const int H = d / HD;
   const float qscale = scale * 1.44269504088896341f;
   const int q0 = qblk * QB;
@@ -248,9 +280,9 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
 
-  const float* qp = p.q + roff + (size_t)b * p.q_bs + hh * HD;
-  const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
-  const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
+  const float* qp = p.q + fs.q + hh * HD;
+  const float* kp = p.k + fs.kv + hh * HD;
+  const float* vp = p.v + fs.kv + hh * HD;
 
   // This lane's query row and its HD/2 dims (half h).
   const int qi = q0 + wave * 32 + j;
@@ -351,7 +383,7 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
   // O^T (rows = dims) -> LDS, one 32-dim tile at a time -> coalesced rows.
   const float inv = 1.0f / lrow;
   float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33);
-  float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD;
+  float* op = p.o + fs.o + hh * HD;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     __syncthreads();
@@ -365,7 +397,7 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_flash_mfma(FlashParam
     }
   }
   if (p.lse && h == 0 && qi < S)  // max + ln(sum), back in natural units
-    p.lse[(size_t)b * p.lse_bs + (size_t)qi * H + hh] =
+    p.lse[fs.l + (size_t)qi * H + hh] =
         mrow * 0.69314718055994531f + logf(lrow);
 }
 
@@ -379,17 +411,17 @@ __global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
   __shared__ float Ks[KB][HD];
   __shared__ float Vs[KB][HD];
   const int hh = blockIdx.y, b = blockIdx.z;
-  int S, d;
-  float scale;
-  long roff;
-  if (!flash_shape<HD>(p, hh, S, d, scale, roff)) return;
+  FlashSeq fs;
+  if (!flash_seq<HD>(p, hh, b, fs)) return;
+  const int S = fs.S, d = fs.d;
+  const float scale = fs.scale;
   const int H = d / HD;
   const int q0 = blockIdx.x * 64;
   if (q0 >= S) return;
   const int i = q0 + threadIdx.x;
-  const float* qp = p.q + roff + (size_t)b * p.q_bs + hh * HD;
-  const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
-  const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
+  const float* qp = p.q + fs.q + hh * HD;
+  const float* kp = p.k + fs.kv + hh * HD;
+  const float* vp = p.v + fs.kv + hh * HD;
   float q[HD], acc[HD];
 #pragma unroll
   for (int c = 0; c < HD; ++c) {
@@ -423,10 +455,10 @@ __global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
     }
   }
   if (i >= S) return;
-  float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD + (size_t)i * d;
+  float* op = p.o + fs.o + hh * HD + (size_t)i * d;
 #pragma unroll
   for (int c = 0; c < HD; ++c) op[c] = acc[c] / lrow;
-  if (p.lse) p.lse[(size_t)b * p.lse_bs + (size_t)i * H + hh] = mrow + logf(lrow);
+  if (p.lse) p.lse[fs.l + (size_t)i * H + hh] = mrow + logf(lrow);
 }
 
 // ---------------------------------------------------------------------------
@@ -864,18 +896,20 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
   uint16_t (*Ks)[KP] = reinterpret_cast<uint16_t (*)[KP]>(lds);
   uint16_t (*Vt)[VP] = reinterpret_cast<uint16_t (*)[VP]>(lds + KB * KP * 2);
 
-  const int S = p.S, d = p.d;
-  // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
-  const float qscale = p.scale * 1.44269504088896341f;
   const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
+  FlashSeq fs;
+  if (!flash_seq<HD>(p, hh, b, fs)) return;
+  const int S = fs.S, d = fs.d;
+  // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
+  const float qscale = fs.scale * 1.44269504088896341f;
   const int q0 = qblk * QB;
   if (q0 >= S) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
 
-  const float* qp = p.q + (size_t)b * p.q_bs + hh * HD;
-  const float* kp = p.k + (size_t)b * p.kv_bs + hh * HD;
-  const float* vp = p.v + (size_t)b * p.kv_bs + hh * HD;
+  const float* qp = p.q + fs.q + hh * HD;
+  const float* kp = p.k + fs.kv + hh * HD;
+  const float* vp = p.v + fs.kv + hh * HD;
 
   const int qi = q0 + wave * 32 + j;
   bf16x8 qf[NQ];  // dims 16 s + 8 h .. + 7 of query qi
@@ -992,7 +1026,7 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
 
   const float inv = 1.0f / lrow;
   float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33 * 4);
-  uint16_t* op = p.o16 + (size_t)b * p.o_bs + hh * HD;
+  uint16_t* op = p.o16 + fs.o + hh * HD;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     __syncthreads();
@@ -1037,10 +1071,10 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   };
 
   const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
-  int S, d;
-  float scale;
-  long roff;
-  if (!flash_shape<HD>(p, hh, S, d, scale, roff)) return;
+  FlashSeq fs;
+  if (!flash_seq<HD>(p, hh, b, fs)) return;
+  const int S = fs.S, d = fs.d;
+  const float scale = fs.scale;
   const int H = d / HD;
   // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
   const float qscale = scale * 1.44269504088896341f;
@@ -1049,9 +1083,9 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
 
-  const float* qp = p.q + roff + (size_t)b * p.q_bs + hh * HD;
-  const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
-  const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
+  const float* qp = p.q + fs.q + hh * HD;
+  const float* kp = p.k + fs.kv + hh * HD;
+  const float* vp = p.v + fs.kv + hh * HD;
 
   const int qi = q0 + wave * 32 + j;
   uint4 qf[3][NQ];  // the three planes of dims 16 s + 8 h .. + 7 of query qi
@@ -1214,7 +1248,7 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   // O^T (rows = dims) -> LDS, one 32-dim tile at a time -> coalesced rows.
   const float inv = 1.0f / lrow;
   float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33 * 4);
-  float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD;
+  float* op = p.o + fs.o + hh * HD;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     __syncthreads();
@@ -1228,7 +1262,7 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
     }
   }
   if (p.lse && h == 0 && qi < S)  // max + ln(sum), back in natural units
-    p.lse[(size_t)b * p.lse_bs + (size_t)qi * H + hh] =
+    p.lse[fs.l + (size_t)qi * H + hh] =
         mrow * 0.69314718055994531f + logf(lrow);
 }
 
@@ -1253,10 +1287,10 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
   __shared__ __align__(16) unsigned char lds[NW * W_BYTES > M_BYTES ? NW * W_BYTES : M_BYTES];
 
   const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
-  int S, d;
-  float scale;
-  long roff;
-  if (!flash_shape<HD>(p, hh, S, d, scale, roff)) return;
+  FlashSeq fs;
+  if (!flash_seq<HD>(p, hh, b, fs)) return;
+  const int S = fs.S, d = fs.d;
+  const float scale = fs.scale;
   const int H = d / HD;
   const float qscale = scale * 1.44269504088896341f;
   const int q0 = qblk * 32;
@@ -1269,9 +1303,9 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
     return reinterpret_cast<uint16_t (*)[VP]>(wl + 3 * K_PLANE * 2) + pl * HD;
   };
 
-  const float* qp = p.q + roff + (size_t)b * p.q_bs + hh * HD;
-  const float* kp = p.k + roff + (size_t)b * p.kv_bs + hh * HD;
-  const float* vp = p.v + roff + (size_t)b * p.kv_bs + hh * HD;
+  const float* qp = p.q + fs.q + hh * HD;
+  const float* kp = p.k + fs.kv + hh * HD;
+  const float* vp = p.v + fs.kv + hh * HD;
 
   const int qi = q0 + j;
   uint4 qf[3][NQ];
@@ -1431,7 +1465,7 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
     for (int r = 0; r < 16; ++r) Om[(wave * HD + 32 * t + acc_row(r, h)) * OS + j] = o[t][r];
   if (h == 0) ML[wave * 32 + j] = make_float2(mrow, lrow);
   __syncthreads();
-  float* op = p.o + roff + (size_t)b * p.o_bs + hh * HD;
+  float* op = p.o + fs.o + hh * HD;
   for (int e = tid; e < 32 * HD; e += 256) {
     const int qr = e / HD, dim = e % HD, qrow = q0 + qr;
     if (qrow >= S) continue;
@@ -1451,7 +1485,7 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
     }
     op[(size_t)qrow * d + dim] = num / den;
     if (p.lse && dim == 0)
-      p.lse[(size_t)b * p.lse_bs + (size_t)qrow * H + hh] = mx * 0.69314718055994531f + logf(den);
+      p.lse[fs.l + (size_t)qrow * H + hh] = mx * 0.69314718055994531f + logf(den);
   }
 }
 

@@ -970,11 +970,18 @@ struct akh_session {
   hipGraphExec_t gexec_n = nullptr;
   uint64_t glayout = 0;  // model layout_gen the graphs were captured for
 
-  // Prefill buffers, grown on demand to B * prompt_len rows.
+  // Prefill buffers, grown on demand to the prompt rows (B * prompt_len, or
+  // the sum of ragged prompt lengths).
   size_t prows = 0;
   float *px = nullptr, *pxn = nullptr, *pq = nullptr, *pattn = nullptr,
         *pffn = nullptr;
   uint32_t* ptok = nullptr;
+  // Ragged prompts packed back to back: sequence b's rows [p_at[b],
+  // p_at[b + 1]), row r = position p_map[r].y of sequence p_map[r].x, its
+  // last row p_last[b] and its length p_len[b].
+  int* p_at = nullptr;
+  int2* p_map = nullptr;
+  int *p_last = nullptr, *p_len = nullptr;
 
   // InferenceSession::generate on the device: per-row state of the rounds.
   int* active = nullptr;   // row is decoded this round (attention skips others)
@@ -1013,9 +1020,13 @@ int lm_parts(const akh_session* s) {
 void free_prefill(akh_session* s) {
   for (float* p : {s->px, s->pxn, s->pq, s->pattn, s->pffn, s->pk, s->pv})
     if (p) hipFree(p);
-  if (s->ptok) hipFree(s->ptok);
+  for (void* p : {(void*)s->ptok, (void*)s->p_at, (void*)s->p_map, (void*)s->p_last,
+                  (void*)s->p_len})
+    if (p) hipFree(p);
   s->px = s->pxn = s->pq = s->pattn = s->pffn = s->pk = s->pv = nullptr;
   s->ptok = nullptr;
+  s->p_at = s->p_last = s->p_len = nullptr;
+  s->p_map = nullptr;
   s->prows = 0;
 }
 
@@ -1029,6 +1040,10 @@ akh_status ensure_prefill(akh_session* s, size_t rows) {
   HIP_TRY(hipMalloc(&s->pattn, rows * d * 4));
   HIP_TRY(hipMalloc(&s->pffn, rows * F * 4));
   HIP_TRY(hipMalloc(&s->ptok, rows * 4));
+  HIP_TRY(hipMalloc(&s->p_at, (s->B + 1) * sizeof(int)));
+  HIP_TRY(hipMalloc(&s->p_map, rows * sizeof(int2)));
+  HIP_TRY(hipMalloc(&s->p_last, s->B * sizeof(int)));
+  HIP_TRY(hipMalloc(&s->p_len, s->B * sizeof(int)));
   if (s->kv16) {
     HIP_TRY(hipMalloc(&s->pk, rows * d * 4));
     HIP_TRY(hipMalloc(&s->pv, rows * d * 4));
@@ -1532,11 +1547,20 @@ hipError_t prefill_gemm(const akh_model* m, GemmParams& g, uint32_t index, int e
   return launch_gemm(g, epi, st);
 }
 
+// The rows of one prefill.  Uniform prompts of length S keep the layout
+// row = b * S + t and need no tables; ragged prompts are packed back to back
+// with the session's tables (p_at, p_map) on the device.
+struct PrefillRows {
+  size_t rows = 0;
+  uint32_t S = 0;  // the longest prompt
+  bool ragged = false;
+};
+
 // The prefill layers in fp32 (build_prefill_layer's node order).
-hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
+hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr) {
   const akh_model_config& c = s->m->cfg;
-  const uint32_t d = c.dim, hd = d / c.num_heads;
-  const size_t rows = (size_t)s->B * S;
+  const uint32_t d = c.dim, hd = d / c.num_heads, S = pr.S;
+  const size_t rows = pr.rows;
   hipStream_t st = s->be->stream;
 #define TRY_HIP(x)                      \
   do {                                  \
@@ -1553,12 +1577,15 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     g.N = 3 * d;
     g.K = d;
     g.q_out = s->pq;
-    // With a bfloat16 cache, K and V go to fp32 rows for this prompt's
-    // attention and are stored into the cache after it.
+    // With a bfloat16 cache, K and V go to fp32 rows (packed like the
+    // prompt's) for this prompt's attention and are stored into the cache
+    // after it.
     g.kcache = s->kv16 ? s->pk : s->kcache(l);
     g.vcache = s->kv16 ? s->pv : s->vcache(l);
-    g.seq_stride = s->kv16 ? (long)S * d : s->seq_stride();
+    g.kv_packed = s->kv16 ? 1 : 0;
+    g.seq_stride = s->seq_stride();
     g.S = (int)S;
+    g.rowmap = pr.ragged ? s->p_map : nullptr;
     g.rope = s->rope;
     g.dim = d;
     g.head_dim = hd;
@@ -1566,8 +1593,8 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     TRY_HIP(prefill_gemm(s->m, g, base + W_QKV, GEMM_QKV, st));
     if (s->kv16)
       TRY_HIP(launch_kv_store_bf16(s->pk, s->pv, static_cast<uint16_t*>(s->kv_at(l, 0)),
-                                   static_cast<uint16_t*>(s->kv_at(l, 1)), (int)s->B, (int)S,
-                                   (int)d, s->seq_stride(), st));
+                                   static_cast<uint16_t*>(s->kv_at(l, 1)), rows, (int)S,
+                                   (int)d, s->seq_stride(), g.rowmap, st));
 
     FlashParams f{};
     f.q = s->pq;
@@ -1575,8 +1602,10 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
     f.v = g.vcache;
     f.o = s->pattn;
     f.q_bs = (long)S * d;
-    f.kv_bs = g.seq_stride;
+    f.kv_bs = s->kv16 ? (long)S * d : s->seq_stride();
     f.o_bs = (long)S * d;
+    f.rows_at = pr.ragged ? s->p_at : nullptr;
+    f.kv_packed = s->kv16 ? 1 : 0;
     f.S = (int)S;
     f.d = (int)d;
     f.hd = (int)hd;
@@ -1625,10 +1654,10 @@ hipError_t prefill_layers_f32(akh_session* s, uint32_t S) {
 // about 2^-16.  Flash attention runs on bfloat16 Q, K, V and P and writes
 // a bfloat16 output, which out_proj takes as is.  The residual stream px
 // and the KV cache stay fp32.
-hipError_t prefill_layers_bf16(akh_session* s, uint32_t S) {
+hipError_t prefill_layers_bf16(akh_session* s, const PrefillRows& pr) {
   const akh_model_config& c = s->m->cfg;
-  const uint32_t d = c.dim, hd = d / c.num_heads;
-  const size_t rows = (size_t)s->B * S;
+  const uint32_t d = c.dim, hd = d / c.num_heads, S = pr.S;
+  const size_t rows = pr.rows;
   hipStream_t st = s->be->stream;
   uint16_t* attn16 = reinterpret_cast<uint16_t*>(s->pattn);
   for (uint32_t l = 0; l < c.num_layers; ++l) {
@@ -1643,20 +1672,23 @@ hipError_t prefill_layers_bf16(akh_session* s, uint32_t S) {
     g.N = 3 * d;
     g.K = d;
     g.q_out = s->pq;
-    // With a bfloat16 cache, K and V go to fp32 rows for this prompt's
-    // attention and are stored into the cache after it.
+    // With a bfloat16 cache, K and V go to fp32 rows (packed like the
+    // prompt's) for this prompt's attention and are stored into the cache
+    // after it.
     g.kcache = s->kv16 ? s->pk : s->kcache(l);
     g.vcache = s->kv16 ? s->pv : s->vcache(l);
-    g.seq_stride = s->kv16 ? (long)S * d : s->seq_stride();
+    g.kv_packed = s->kv16 ? 1 : 0;
+    g.seq_stride = s->seq_stride();
     g.S = (int)S;
+    g.rowmap = pr.ragged ? s->p_map : nullptr;
     g.rope = s->rope;
     g.dim = d;
     g.head_dim = hd;
     if ((e = launch_gemm_bf16(g, GEMM_QKV, st)) != hipSuccess) return e;
     if (s->kv16 &&
         (e = launch_kv_store_bf16(s->pk, s->pv, static_cast<uint16_t*>(s->kv_at(l, 0)),
-                                  static_cast<uint16_t*>(s->kv_at(l, 1)), (int)s->B, (int)S,
-                                  (int)d, s->seq_stride(), st)) != hipSuccess)
+                                  static_cast<uint16_t*>(s->kv_at(l, 1)), rows, (int)S,
+                                  (int)d, s->seq_stride(), g.rowmap, st)) != hipSuccess)
       return e;
 
     FlashParams f{};
@@ -1665,8 +1697,10 @@ hipError_t prefill_layers_bf16(akh_session* s, uint32_t S) {
     f.v = g.vcache;
     f.o16 = attn16;
     f.q_bs = (long)S * d;
-    f.kv_bs = g.seq_stride;
+    f.kv_bs = s->kv16 ? (long)S * d : s->seq_stride();
     f.o_bs = (long)S * d;
+    f.rows_at = pr.ragged ? s->p_at : nullptr;
+    f.kv_packed = s->kv16 ? 1 : 0;
     f.S = (int)S;
     f.d = (int)d;
     f.hd = (int)hd;
@@ -1712,16 +1746,27 @@ hipError_t prefill_layers_bf16(akh_session* s, uint32_t S) {
 // build_prefill_layer's node order (inference_graphs.rs:198-337): 7 kernels
 // per layer (RMSNorm, QKV GEMM + RoPE + cache append, flash attention,
 // out_proj + residual, RMSNorm, ffn_up + SiLU, ffn_down + residual).
-extern "C" akh_status akh_session_prefill(akh_session* s,
-                                          const uint32_t* tokens,
-                                          uint32_t prompt_len, float* logits,
-                                          uint32_t* next) {
-  CHECK_ARG(s && (tokens || !prompt_len), "akh_session_prefill: NULL argument");
-  if (prompt_len == 0) return fail(AKH_E_EMPTY_PROMPT, "prompt is empty");
-  if (prompt_len > s->max_ctx)
-    return fail(AKH_E_PROMPT_TOO_LONG,
-                "prompt is " + std::to_string(prompt_len) +
-                    " tokens, context window is " + std::to_string(s->max_ctx));
+namespace {
+
+// InferenceSession::prefill for every sequence, sequence b with lens[b]
+// tokens (tokens packed back to back).  The reference checks each prompt
+// (inference.rs:61-75): empty, longer than the context, or a cache that is
+// not empty fail with its errors before any work.
+akh_status prefill_impl(akh_session* s, const uint32_t* tokens, const uint32_t* lens,
+                        float* logits, uint32_t* next) {
+  uint32_t S = 0;
+  size_t rows = 0;
+  bool ragged = false;
+  for (uint32_t b = 0; b < s->B; ++b) {
+    if (lens[b] == 0) return fail(AKH_E_EMPTY_PROMPT, "prompt is empty");
+    if (lens[b] > s->max_ctx)
+      return fail(AKH_E_PROMPT_TOO_LONG,
+                  "prompt is " + std::to_string(lens[b]) +
+                      " tokens, context window is " + std::to_string(s->max_ctx));
+    S = std::max(S, lens[b]);
+    ragged = ragged || lens[b] != lens[0];
+    rows += lens[b];
+  }
   akh_status nc = need_caches(s);
   if (nc != AKH_OK) return nc;
   for (uint32_t b = 0; b < s->B; ++b)
@@ -1730,20 +1775,48 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
                   "prefill needs an empty cache, this one holds " +
                       std::to_string(s->cur_len[b]) + " tokens");
   const akh_model_config& c = s->m->cfg;
-  const uint32_t S = prompt_len, d = c.dim;
-  const size_t rows = (size_t)s->B * S;
+  const uint32_t d = c.dim;
   akh_status st0 = ensure_prefill(s, rows);
   if (st0 != AKH_OK) return st0;
   hipStream_t st = s->be->stream;
   HIP_TRY(hipMemcpyAsync(s->ptok, tokens, rows * 4, hipMemcpyHostToDevice, st));
-  // Token history: the prompt occupies positions 0..S-1 of every sequence.
-  HIP_TRY(hipMemcpy2DAsync(s->hist, (size_t)(s->max_ctx + 1) * 4, s->ptok,
-                           (size_t)S * 4, (size_t)S * 4, s->B,
-                           hipMemcpyDeviceToDevice, st));
+  // Ragged prompts: the row tables (first row and length per sequence,
+  // (sequence, position) per row, last row per sequence).
+  std::vector<int> at(s->B + 1, 0), last(s->B), len(s->B);
+  for (uint32_t b = 0; b < s->B; ++b) {
+    at[b + 1] = at[b] + (int)lens[b];
+    last[b] = at[b + 1] - 1;
+    len[b] = (int)lens[b];
+  }
+  if (ragged) {
+    std::vector<int2> map(rows);
+    for (uint32_t b = 0; b < s->B; ++b)
+      for (uint32_t t = 0; t < lens[b]; ++t) map[at[b] + t] = make_int2((int)b, (int)t);
+    HIP_TRY(hipMemcpyAsync(s->p_at, at.data(), at.size() * sizeof(int), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(s->p_map, map.data(), rows * sizeof(int2), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(s->p_last, last.data(), s->B * sizeof(int), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(s->p_len, len.data(), s->B * sizeof(int), hipMemcpyHostToDevice, st));
+    // The host tables are read by the copies above before they go away.
+    HIP_TRY(hipStreamSynchronize(st));
+  }
+  // Token history: each prompt occupies positions 0..len-1 of its sequence.
+  if (ragged) {
+    for (uint32_t b = 0; b < s->B; ++b)
+      HIP_TRY(hipMemcpyAsync(s->hist + (size_t)b * (s->max_ctx + 1), s->ptok + at[b],
+                             (size_t)lens[b] * 4, hipMemcpyDeviceToDevice, st));
+  } else {
+    HIP_TRY(hipMemcpy2DAsync(s->hist, (size_t)(s->max_ctx + 1) * 4, s->ptok,
+                             (size_t)S * 4, (size_t)S * 4, s->B,
+                             hipMemcpyDeviceToDevice, st));
+  }
 
   HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
                                 (int)d, c.vocab_size, st));
-  HIP_TRY(s->m->prefill_bf16 ? prefill_layers_bf16(s, S) : prefill_layers_f32(s, S));
+  PrefillRows pr;
+  pr.rows = rows;
+  pr.S = S;
+  pr.ragged = ragged;
+  HIP_TRY(s->m->prefill_bf16 ? prefill_layers_bf16(s, pr) : prefill_layers_f32(s, pr));
   // Last row of every sequence -> final RMSNorm -> lm_head -> greedy token
   // (inference.rs:120-168).
   {
@@ -1751,16 +1824,38 @@ extern "C" akh_status akh_session_prefill(akh_session* s,
     r.src = s->px;
     r.row0 = (long)S - 1;
     r.row_stride = (long)S;
+    r.src_rows = ragged ? s->p_last : nullptr;
     HIP_TRY(launch_rows_norm(r, (int)s->B, st));
   }
   HIP_TRY(enqueue_lm_head(s));
   HIP_TRY(launch_argmax_final(s->amax, lm_parts(s),
                               (int)s->B, s->tok, nullptr, s->hist,
-                              (int)s->max_ctx + 1, (int)S, st));
-  std::fill(s->cur_len.begin(), s->cur_len.end(), S);
+                              (int)s->max_ctx + 1, (int)S, st, ragged ? s->p_len : nullptr));
+  for (uint32_t b = 0; b < s->B; ++b) s->cur_len[b] = lens[b];
   akh_status ps = upload_positions(s);
   if (ps != AKH_OK) return ps;
   return download_outputs(s, logits, next);
+}
+
+}  // namespace
+
+extern "C" akh_status akh_session_prefill(akh_session* s,
+                                          const uint32_t* tokens,
+                                          uint32_t prompt_len, float* logits,
+                                          uint32_t* next) {
+  CHECK_ARG(s && (tokens || !prompt_len), "akh_session_prefill: NULL argument");
+  const std::vector<uint32_t> lens(s->B, prompt_len);
+  return prefill_impl(s, tokens, lens.data(), logits, next);
+}
+
+extern "C" akh_status akh_session_prefill_ragged(akh_session* s, const uint32_t* tokens,
+                                                 const uint32_t* prompt_lens, float* logits,
+                                                 uint32_t* next) {
+  CHECK_ARG(s && prompt_lens, "akh_session_prefill_ragged: NULL argument");
+  size_t n = 0;
+  for (uint32_t b = 0; b < s->B; ++b) n += prompt_lens[b];
+  CHECK_ARG(tokens || n == 0, "akh_session_prefill_ragged: NULL tokens");
+  return prefill_impl(s, tokens, prompt_lens, logits, next);
 }
 
 extern "C" akh_status akh_session_decode_step(akh_session* s,
@@ -1854,13 +1949,68 @@ akh_status ensure_generate(akh_session* s, uint32_t max_new, const akh_sampling&
 
 }  // namespace
 
-extern "C" akh_status akh_session_generate(akh_session* s, const uint32_t* tokens,
-                                           uint32_t prompt_len, uint32_t max_new_tokens,
-                                           akh_sampling params, const double* uniforms,
-                                           uint32_t* out_tokens, uint32_t* out_counts) {
-  CHECK_ARG(s && (tokens || !prompt_len) && out_counts && (out_tokens || !max_new_tokens),
-            "akh_session_generate: NULL argument");
-  if (prompt_len == 0) return fail(AKH_E_EMPTY_PROMPT, "prompt is empty");
+namespace {
+
+// Prompts of different lengths fed to sequences that hold caches
+// (inference.rs:290-299: one decode step per prompt token), right-aligned:
+// in step i of L = the longest prompt, sequence b decodes its token
+// i - (L - lens[b]) if that is >= 0 and is left out otherwise (attention
+// skips it, its cache and position stay).  Every sequence decodes its last
+// prompt token in the final step, so the logits then are each sequence's
+// own.  ContextFull as decode_step raises it (inference.rs:179-187): the
+// steps before the first token some context cannot take are decoded, then
+// the call fails.
+akh_status feed_ragged(akh_session* s, const uint32_t* tokens, const uint32_t* lens) {
+  const uint32_t B = s->B;
+  uint32_t L = 0;
+  std::vector<size_t> at(B + 1, 0);
+  for (uint32_t b = 0; b < B; ++b) {
+    L = std::max(L, lens[b]);
+    at[b + 1] = at[b] + lens[b];
+  }
+  hipStream_t st = s->be->stream;
+  // Every step's tokens and rows, kept until the stream has read them.
+  std::vector<uint32_t> cols((size_t)L * kMaxBatch, 0u);
+  std::vector<int> acts((size_t)L * kMaxBatch, 0);
+  for (uint32_t i = 0; i < L; ++i)
+    for (uint32_t b = 0; b < B; ++b) {
+      const uint32_t lead = L - lens[b];
+      if (i < lead) continue;
+      cols[(size_t)i * kMaxBatch + b] = tokens[at[b] + (i - lead)];
+      acts[(size_t)i * kMaxBatch + b] = 1;
+    }
+  bool full = false;
+  for (uint32_t i = 0; i < L && !full; ++i) {
+    for (uint32_t b = 0; b < B; ++b)
+      full = full || (acts[(size_t)i * kMaxBatch + b] && s->cur_len[b] >= s->max_ctx);
+    if (full) break;
+    HIP_TRY(hipMemcpyAsync(s->tok, cols.data() + (size_t)i * kMaxBatch, B * sizeof(uint32_t),
+                           hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(s->active, acts.data() + (size_t)i * kMaxBatch,
+                           kMaxBatch * sizeof(int), hipMemcpyHostToDevice, st));
+    HIP_TRY(enqueue_decode_body(s));
+    HIP_TRY(launch_advance(s->pos, s->active, (int)B, st, s->tok, s->hist,
+                           (long)s->max_ctx + 1));
+    for (uint32_t b = 0; b < B; ++b) s->cur_len[b] += acts[(size_t)i * kMaxBatch + b];
+  }
+  HIP_TRY(hipStreamSynchronize(st));
+  akh_status sa = set_active(s, true);
+  if (full)
+    return fail(AKH_E_CONTEXT_FULL,
+                "context window is full (" + std::to_string(s->max_ctx) + " tokens)");
+  return sa;
+}
+
+akh_status generate_impl(akh_session* s, const uint32_t* tokens, const uint32_t* lens,
+                         uint32_t max_new_tokens, akh_sampling params,
+                         const double* uniforms, uint32_t* out_tokens,
+                         uint32_t* out_counts) {
+  bool uniform = true;
+  for (uint32_t b = 0; b < s->B; ++b) {
+    if (lens[b] == 0) return fail(AKH_E_EMPTY_PROMPT, "prompt is empty");
+    uniform = uniform && lens[b] == lens[0];
+  }
+  const uint32_t prompt_len = lens[0];
   CHECK_ARG(params.temperature <= 0.0f || uniforms || max_new_tokens == 0,
             "akh_session_generate: sampling (temperature > 0) needs uniforms");
   // A sequence without a cache gets a fresh one (inference.rs:278-287).
@@ -1883,13 +2033,15 @@ extern "C" akh_status akh_session_generate(akh_session* s, const uint32_t* token
   // (inference.rs:290-299).
   akh_status st = AKH_OK;
   if (all_empty) {
-    st = akh_session_prefill(s, tokens, prompt_len, nullptr, nullptr);
-  } else {
+    st = prefill_impl(s, tokens, lens, nullptr, nullptr);
+  } else if (uniform) {
     std::vector<uint32_t> col(B);
     for (uint32_t i = 0; i < prompt_len && st == AKH_OK; ++i) {
       for (uint32_t b = 0; b < B; ++b) col[b] = tokens[(size_t)b * prompt_len + i];
       st = akh_session_decode_step(s, col.data(), nullptr, nullptr);
     }
+  } else {
+    st = feed_ragged(s, tokens, lens);
   }
   if (st != AKH_OK) return st;
   std::fill(out_counts, out_counts + B, 0u);
@@ -1921,6 +2073,33 @@ extern "C" akh_status akh_session_generate(akh_session* s, const uint32_t* token
     s->cur_len[b] = (uint32_t)pos[b];
   }
   return set_active(s, true);
+}
+
+}  // namespace
+
+extern "C" akh_status akh_session_generate(akh_session* s, const uint32_t* tokens,
+                                           uint32_t prompt_len, uint32_t max_new_tokens,
+                                           akh_sampling params, const double* uniforms,
+                                           uint32_t* out_tokens, uint32_t* out_counts) {
+  CHECK_ARG(s && (tokens || !prompt_len) && out_counts && (out_tokens || !max_new_tokens),
+            "akh_session_generate: NULL argument");
+  const std::vector<uint32_t> lens(s->B, prompt_len);
+  return generate_impl(s, tokens, lens.data(), max_new_tokens, params, uniforms, out_tokens,
+                       out_counts);
+}
+
+extern "C" akh_status akh_session_generate_ragged(akh_session* s, const uint32_t* tokens,
+                                                  const uint32_t* prompt_lens,
+                                                  uint32_t max_new_tokens, akh_sampling params,
+                                                  const double* uniforms, uint32_t* out_tokens,
+                                                  uint32_t* out_counts) {
+  CHECK_ARG(s && prompt_lens && out_counts && (out_tokens || !max_new_tokens),
+            "akh_session_generate_ragged: NULL argument");
+  size_t n = 0;
+  for (uint32_t b = 0; b < s->B; ++b) n += prompt_lens[b];
+  CHECK_ARG(tokens || n == 0, "akh_session_generate_ragged: NULL tokens");
+  return generate_impl(s, tokens, prompt_lens, max_new_tokens, params, uniforms, out_tokens,
+                       out_counts);
 }
 
 namespace {
@@ -2197,7 +2376,10 @@ extern "C" akh_status akh_forward_loss(akh_forward* f, const uint32_t* tokens,
   HIP_TRY(hipMemcpyAsync(s->ptok, tokens, rows * 4, hipMemcpyHostToDevice, st));
   HIP_TRY(hipMemcpyAsync(f->targets, targets, rows * 4, hipMemcpyHostToDevice, st));
   HIP_TRY(launch_embedding_rows(s->ptok, f->m->embedding(), s->px, (int)rows, (int)d, V, st));
-  HIP_TRY(f->m->prefill_bf16 ? prefill_layers_bf16(s, S) : prefill_layers_f32(s, S));
+  PrefillRows pr;
+  pr.rows = rows;
+  pr.S = S;
+  HIP_TRY(f->m->prefill_bf16 ? prefill_layers_bf16(s, pr) : prefill_layers_f32(s, pr));
   // final_norm and lm_head on every row (train.rs:154-177), then the loss.
   HIP_TRY(launch_rows_rmsnorm(s->px, f->m->final_norm(), s->pxn, (int)rows, (int)d, c.norm_eps,
                               st));

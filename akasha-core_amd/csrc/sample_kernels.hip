@@ -317,9 +317,12 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
   }
 }
 
-__global__ void k_advance(int* pos, const int* active, int rows) {
+__global__ void k_advance(int* pos, const int* active, int rows, const uint32_t* tok,
+                          uint32_t* hist, long hist_stride) {
   const int m = threadIdx.x;
-  if (m < rows) pos[m] += active[m];
+  if (m >= rows || !active[m]) return;
+  if (tok) hist[(size_t)m * hist_stride + pos[m]] = tok[m];
+  pos[m] += 1;
 }
 
 }  // namespace
@@ -352,9 +355,11 @@ hipError_t sample_noalloc_scratch(int device, double** ptr) {
   return hipSuccess;
 }
 
-hipError_t launch_advance(int* pos, const int* active, int rows, hipStream_t s) {
-  if (rows <= 0 || rows > 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_advance, dim3(1), dim3(64 * ((rows + 63) / 64)), 0, s, pos, active, rows);
+hipError_t launch_advance(int* pos, const int* active, int rows, hipStream_t s,
+                          const uint32_t* tok, uint32_t* hist, long hist_stride) {
+  if (rows <= 0 || rows > 1024 || (tok && !hist)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_advance, dim3(1), dim3(64 * ((rows + 63) / 64)), 0, s, pos, active, rows,
+                     tok, hist, hist_stride);
   return hipGetLastError();
 }
 

@@ -218,6 +218,8 @@ _SIGS = {
     "akh_session_decode_step": (ST, [P, P, P, P]),
     "akh_session_decode_greedy": (ST, [P, U32, P]),
     "akh_session_generate": (ST, [P, P, U32, U32, Sampling, P, P, P]),
+    "akh_session_generate_ragged": (ST, [P, P, P, U32, Sampling, P, P, P]),
+    "akh_session_prefill_ragged": (ST, [P, P, P, P, P]),
     "akh_session_truncate": (ST, [P, U32]),
     "akh_session_set_len": (ST, [P, U32]),
     "akh_session_set_kv_bf16": (ST, [P, C.c_int]),
@@ -650,15 +652,32 @@ class Session:
         _check(_lib.akh_session_cur_len(self.handle, _ptr(out)), "cur_len")
         return out
 
-    def prefill(self, tokens: np.ndarray, want_logits: bool = True):
-        """tokens [batch, S] -> (logits [batch, vocab] or None, next [batch])."""
-        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(self.batch, -1))
+    @staticmethod
+    def _packed(prompts, batch):
+        """A list of per-sequence prompts -> (tokens back to back, lengths)."""
+        if len(prompts) != batch:
+            raise InvalidArgument(f"{len(prompts)} prompts for {batch} sequences")
+        lens = np.array([len(p) for p in prompts], np.uint32)
+        toks = (np.concatenate([np.asarray(p, np.uint32).reshape(-1) for p in prompts])
+                if lens.sum() else np.zeros(1, np.uint32))
+        return np.ascontiguousarray(toks, np.uint32), lens
+
+    def prefill(self, tokens, want_logits: bool = True):
+        """tokens [batch, S], or a list of batch prompts of any lengths
+        (akh_session_prefill_ragged) -> (logits [batch, vocab] or None,
+        next [batch])."""
         logits = (np.empty((self.batch, self.model.cfg.vocab_size), np.float32)
                   if want_logits else None)
         nxt = np.empty(self.batch, np.uint32)
-        _check(_lib.akh_session_prefill(self.handle, _ptr(t), t.shape[1],
-                                        _ptr(logits) if logits is not None else None,
-                                        _ptr(nxt)), "prefill")
+        lp = _ptr(logits) if logits is not None else None
+        if isinstance(tokens, (list, tuple)):
+            t, lens = self._packed(tokens, self.batch)
+            _check(_lib.akh_session_prefill_ragged(self.handle, _ptr(t), _ptr(lens), lp,
+                                                   _ptr(nxt)), "prefill_ragged")
+            return logits, nxt
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(self.batch, -1))
+        _check(_lib.akh_session_prefill(self.handle, _ptr(t), t.shape[1], lp, _ptr(nxt)),
+               "prefill")
         return logits, nxt
 
     def decode_step(self, tokens=None, want_logits: bool = True):
@@ -685,20 +704,28 @@ class Session:
     def generate(self, prompt, max_new_tokens: int, temperature: float = 0.0, top_k: int = 0,
                  top_p: float = 1.0, repetition_penalty: float = 1.0, uniforms=None):
         """InferenceSession::generate per sequence (token ids).  ``prompt`` is
-        [batch, prompt_len]; ``uniforms`` [max_new_tokens, batch] holds the
-        draws standing in for rand::random() (needed when temperature > 0).
-        Returns a list of uint32 arrays, one per sequence."""
-        prompt = np.ascontiguousarray(prompt, np.uint32).reshape(self.batch, -1)
+        [batch, prompt_len], or a list of batch prompts of any lengths
+        (akh_session_generate_ragged); ``uniforms`` [max_new_tokens, batch]
+        holds the draws standing in for rand::random() (needed when
+        temperature > 0).  Returns a list of uint32 arrays, one per
+        sequence."""
         out = np.zeros((self.batch, max(1, max_new_tokens)), np.uint32)
         counts = np.zeros(self.batch, np.uint32)
         uni = None
         if uniforms is not None:
             uni = np.ascontiguousarray(uniforms, np.float64).reshape(max_new_tokens, self.batch)
         sp = Sampling(temperature, top_k, top_p, repetition_penalty)
-        _check(_lib.akh_session_generate(self.handle, _ptr(prompt), prompt.shape[1],
-                                         max_new_tokens, sp,
-                                         _ptr(uni) if uni is not None else None,
-                                         _ptr(out), _ptr(counts)), "generate")
+        up = _ptr(uni) if uni is not None else None
+        if isinstance(prompt, (list, tuple)):
+            t, lens = self._packed(prompt, self.batch)
+            _check(_lib.akh_session_generate_ragged(self.handle, _ptr(t), _ptr(lens),
+                                                    max_new_tokens, sp, up, _ptr(out),
+                                                    _ptr(counts)), "generate_ragged")
+        else:
+            prompt = np.ascontiguousarray(prompt, np.uint32).reshape(self.batch, -1)
+            _check(_lib.akh_session_generate(self.handle, _ptr(prompt), prompt.shape[1],
+                                             max_new_tokens, sp, up, _ptr(out), _ptr(counts)),
+                   "generate")
         return [out[b, :counts[b]].copy() for b in range(self.batch)]
 
     def truncate(self, length: int):

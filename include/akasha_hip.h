@@ -372,6 +372,14 @@ akh_status akh_session_cur_len(const akh_session* s, uint32_t* out);
 akh_status akh_session_prefill(akh_session* s, const uint32_t* tokens,
                                uint32_t prompt_len, float* logits,
                                uint32_t* next);
+/* InferenceSession::prefill (inference.rs:61-176, one &[u32] per session)
+ * with a prompt length per sequence: tokens holds the prompts back to back
+ * (sequence b's prompt_lens[b] tokens after those of sequences 0..b-1).
+ * Each prompt is checked as the reference checks it (EmptyPrompt,
+ * PromptTooLong, NoCache, CacheNotEmpty); cur_len[b] = prompt_lens[b]. */
+akh_status akh_session_prefill_ragged(akh_session* s, const uint32_t* tokens,
+                                      const uint32_t* prompt_lens, float* logits,
+                                      uint32_t* next);
 /* InferenceSession::decode_step (inference.rs:178-262) for every sequence:
  * tokens is [batch] (NULL = feed each sequence its previous greedy token,
  * kept on the device).  logits / next may be NULL. */
@@ -401,6 +409,14 @@ akh_status akh_session_generate(akh_session* s, const uint32_t* tokens,
                                 uint32_t prompt_len, uint32_t max_new_tokens,
                                 akh_sampling params, const double* uniforms,
                                 uint32_t* out_tokens, uint32_t* out_counts);
+/* akh_session_generate with a prompt length per sequence (the prompts back
+ * to back, as akh_session_prefill_ragged takes them): prefilled on empty
+ * caches; on resumed caches fed as decode steps right-aligned, so every
+ * sequence decodes its last prompt token in the same final step. */
+akh_status akh_session_generate_ragged(akh_session* s, const uint32_t* tokens,
+                                       const uint32_t* prompt_lens, uint32_t max_new_tokens,
+                                       akh_sampling params, const double* uniforms,
+                                       uint32_t* out_tokens, uint32_t* out_counts);
 /* Set every sequence's cached length to `len` (<= max_ctx) without touching
  * the cache rows, as assigning the reference's public Cache::cur_len does
  * (inference_graphs.rs:515); rows below `len` keep whatever they hold.  Used

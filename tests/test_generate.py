@@ -70,6 +70,20 @@ def test_generate_greedy_and_sampled_match_oracle(backend, pkg, ora):
     _check(pkg, ora, s, o, cfg, more, 6, 1.2, 0, 0.9, 1.0, rng.random((6, 3)))
 
 
+def test_generate_ragged_prompts_match_oracle(backend, pkg, ora):
+    # Prompts of different lengths in one call (the reference takes one
+    # prompt per session): prefilled together on empty caches, then fed as
+    # decode steps on the resumed caches, each sequence against its own
+    # restated generate loop.
+    cfg = pkg.ModelConfig.new(97, 32, 4, 2, 16)
+    rng = np.random.default_rng(8)
+    prompts = [rng.integers(0, cfg.vocab_size - 1, n).astype(np.uint32) for n in (5, 1, 9, 3)]
+    _, s, o = _setup(pkg, backend, ora, cfg, 26, 48, 4)
+    _check(pkg, ora, s, o, cfg, prompts, 7, 0.8, 40, 0.95, 1.15, rng.random((7, 4)))
+    more = [rng.integers(0, cfg.vocab_size - 1, n).astype(np.uint32) for n in (2, 6, 1, 4)]
+    _check(pkg, ora, s, o, cfg, more, 5, 0.0, 0, 1.0, 1.2, None)
+
+
 def test_generate_stops_at_eos_and_full_context(backend, pkg, ora):
     cfg = pkg.ModelConfig.new(97, 32, 4, 2, 16)
     rng = np.random.default_rng(6)

@@ -167,6 +167,58 @@ def test_two_row_tiles_bf16_weight_tiles(backend, pkg):
     model.close()
 
 
+@pytest.mark.parametrize("dim", [128, 256])
+@pytest.mark.parametrize("mode", ["x6", "fp32_mfma", "kv16", "bf16"])
+def test_ragged_prefill_matches_per_sequence(backend, pkg, ora, dim, mode):
+    # InferenceSession::prefill takes any prompt length per session
+    # (inference.rs:61-75).  One batched prefill of prompts of 57, 3, 130, 1
+    # and 64 tokens (ragged query blocks; the longest spans two 128-query
+    # blocks; head_dim 64 runs the key-split flash kernel, 128 the 128-query
+    # one) gives each sequence what a one-sequence session gives, and, on
+    # the fp32 paths, what the oracle gives; decode continues from each
+    # sequence's own length.
+    cfg = pkg.ModelConfig.new(300, dim, 2, 2, 160)
+    w = pkg.synthetic_weights(cfg, seed=61)
+    lens = [57, 3, 130, 1, 64]
+    prompts = [pkg.synthetic_tokens(n, cfg.vocab_size, seed=62 + i) for i, n in enumerate(lens)]
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    if mode == "fp32_mfma":
+        model.set_prefill_x6(False)
+    if mode == "bf16":
+        model.set_prefill_bf16(True)
+
+    def session(n):
+        s = pkg.hip.Session(model, 160, n)
+        if mode == "kv16":
+            s.set_kv_bf16(True)
+        return s
+
+    s = session(len(lens))
+    got = [s.prefill(prompts)] + [s.decode_step(None) for _ in range(3)]
+    assert list(s.cur_len()) == [n + 3 for n in lens]
+    for b, n in enumerate(lens):
+        one = session(1)
+        alone = [one.prefill(prompts[b][None])] + [one.decode_step(None) for _ in range(3)]
+        for i, ((lg, tk), (l1, t1)) in enumerate(zip(got, alone)):
+            assert np.abs(lg[b] - l1[0]).max() < 1e-5, f"sequence {b} step {i}"
+            assert int(tk[b]) == int(t1[0]), f"sequence {b} step {i}"
+        one.close()
+    np.testing.assert_array_equal(s.cache(1, 2, 0)[130 + 3:], 0)
+    if mode in ("x6", "fp32_mfma"):
+        refs = _oracle_greedy_many(ora, cfg, w, 160, prompts, 3)
+        for b, (rl, rt) in enumerate(refs):
+            for i in range(4):
+                assert np.abs(got[i][0][b] - rl[i]).max() < TOL, f"sequence {b} step {i}"
+                assert int(got[i][1][b]) == rt[i], f"sequence {b} step {i}"
+    with pytest.raises(pkg.hip.EmptyPrompt):
+        session(2).prefill([prompts[0], prompts[0][:0]])
+    with pytest.raises(pkg.hip.PromptTooLong):
+        session(2).prefill([prompts[0], np.zeros(161, np.uint32)])
+    s.close()
+    model.close()
+
+
 def test_decode_greedy_matches_step_by_step(backend, pkg):
     cfg = pkg.ModelConfig.new(300, 128, 2, 2, 64)
     w = pkg.synthetic_weights(cfg, seed=9)
