@@ -511,8 +511,12 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   const int pos = p.pos[b];
   const int d = p.d;
   const bool last = sp == SP - 1;
+  // The head size hd <= HD (a multiple of 4): lanes whose four columns lie
+  // past it load zeros and store nothing.
+  const int hd = d / p.H;
+  const bool gin = 4 * g < hd;
 
-  const size_t hoff = (size_t)b * p.seq_stride + hh * HD + 4 * g;
+  const size_t hoff = (size_t)b * p.seq_stride + hh * hd + (gin ? 4 * g : 0);
   using KT = typename std::conditional<KV16, uint16_t, float>::type;
   const KT* kbase = static_cast<const KT*>(p.kc) + hoff;
   const KT* vbase = static_cast<const KT*>(p.vc) + hoff;
@@ -548,8 +552,8 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
       const int r = base + i * RPW + rl;
       ok[i] = r < r1;
       const size_t off = (size_t)(ok[i] ? r : r0) * d;
-      kv[i] = ok[i] ? nt_load(kbase + off) : Raw{};
-      vv[i] = ok[i] ? nt_load(vbase + off) : Raw{};
+      kv[i] = ok[i] && gin ? nt_load(kbase + off) : Raw{};
+      vv[i] = ok[i] && gin ? nt_load(vbase + off) : Raw{};
     }
   };
   auto wide = [](const Raw& x) -> float4 {
@@ -561,10 +565,10 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   load_batch(r0);
   asm volatile("" ::: "memory");
 
-  // The new token's q, k, v (columns hh*HD + 4g .. +3 of each role).
+  // The new token's q, k, v (columns hh*hd + 4g .. +3 of each role).
   float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), kn = q4, vn = q4;
-  {
-    const float* row = p.qkv + (size_t)b * 3 * d + (size_t)hh * HD + 4 * g;
+  if (gin) {
+    const float* row = p.qkv + (size_t)b * 3 * d + (size_t)hh * hd + 4 * g;
     const size_t ps = (size_t)p.rows * 3 * d;
     q4 = sum_parts4<4>(q4, row, ps, p.nparts);
     if (last) {
@@ -572,8 +576,8 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
       vn = sum_parts4<4>(vn, row + 2 * d, ps, p.nparts);
     }
     // Pairs (4g, 4g+1) and (4g+2, 4g+3) of the head: rope entries 2g, 2g+1.
-    const float2 c0 = p.rope[(size_t)pos * (HD / 2) + 2 * g];
-    const float2 c1 = p.rope[(size_t)pos * (HD / 2) + 2 * g + 1];
+    const float2 c0 = p.rope[(size_t)pos * (hd / 2) + 2 * g];
+    const float2 c1 = p.rope[(size_t)pos * (hd / 2) + 2 * g + 1];
     rope_pair(q4.x, q4.y, c0.x, c0.y);
     rope_pair(q4.z, q4.w, c1.x, c1.y);
     rope_pair(kn.x, kn.y, c0.x, c0.y);
@@ -584,11 +588,11 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     const uint2 vu = make_uint2(pack_bf16x2(vn.x, vn.y), pack_bf16x2(vn.z, vn.w));
     kn = bf16x4(ku.x, ku.y);
     vn = bf16x4(vu.x, vu.y);
-    if (last && wave == 0 && rl == 0) {
+    if (last && wave == 0 && rl == 0 && gin) {
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.kc) + hoff + (size_t)pos * d) = ku;
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.vc) + hoff + (size_t)pos * d) = vu;
     }
-  } else if (last && wave == 0 && rl == 0) {
+  } else if (last && wave == 0 && rl == 0 && gin) {
     *reinterpret_cast<float4*>(static_cast<float*>(p.kc) + hoff + (size_t)pos * d) = kn;
     *reinterpret_cast<float4*>(static_cast<float*>(p.vc) + hoff + (size_t)pos * d) = vn;
   }
@@ -657,7 +661,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     wl_s[wave] = l;
   }
   __syncthreads();
-  if (threadIdx.x < LPR) {
+  if (threadIdx.x < LPR && 4 * (int)threadIdx.x < hd) {
     const int t = threadIdx.x;
     float M = -INFINITY;
     for (int w = 0; w < AW; ++w) M = fmaxf(M, wm_s[w]);
@@ -672,7 +676,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
       o.w += wg * wo_s[w][t].w;
     }
     *reinterpret_cast<float4*>(p.out_t + (size_t)sp * p.rows * d + (size_t)(b >> 5) * 32 * d +
-                               ((size_t)(hh * (HD / 4) + t) * 32 + (b & 31)) * 4) = o;
+                               ((size_t)(hh * (hd / 4) + t) * 32 + (b & 31)) * 4) = o;
     if (t == 0) p.ml[((size_t)sp * p.H + hh) * p.rows + b] = make_float2(M, L);
   }
 }
@@ -1045,14 +1049,20 @@ hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
   } else {                                                                         \
     AKH_ATTN_GO((k_dec_attn<HD, AW, RB, SP, false>))                               \
   }
-  switch (hd) {
-    case 4: AKH_ATTN(4) break;
-    case 8: AKH_ATTN(8) break;
-    case 16: AKH_ATTN(16) break;
-    case 32: AKH_ATTN(32) break;
-    case 64: AKH_ATTN(64) break;
-    case 128: AKH_ATTN(128) break;
-    default: return hipErrorInvalidValue;
+  // The kernel of the next power of two; its lanes past hd stay idle.
+  if (hd < 4 || hd > 128 || hd % 4 != 0 || p.d != hd * p.H) return hipErrorInvalidValue;
+  if (hd <= 4) {
+    AKH_ATTN(4)
+  } else if (hd <= 8) {
+    AKH_ATTN(8)
+  } else if (hd <= 16) {
+    AKH_ATTN(16)
+  } else if (hd <= 32) {
+    AKH_ATTN(32)
+  } else if (hd <= 64) {
+    AKH_ATTN(64)
+  } else {
+    AKH_ATTN(128)
   }
 #undef AKH_ATTN
 #undef AKH_ATTN_GO

@@ -218,27 +218,32 @@ struct FlashSeq {
   float scale;
   long q, kv, o, l;
 };
+//
+// The kernels' HD is a register-tile size; the head size is p.hd <= HD (a
+// head_dim that is not a power of two runs in the next larger kernel, its
+// columns past p.hd read as zero and never stored).
 template <int HD>
 __device__ __forceinline__ bool flash_seq(const FlashParams& p, int hh, int b, FlashSeq& f) {
   f.S = p.S;
   f.d = p.d;
   f.scale = p.scale;
   long roff = 0;
+  if (p.hd > HD) return false;
   if (p.meta) {
     const akh_flash_attn_meta m = *p.meta;
-    if ((int)m.head_dim != HD || (int)m.seq_len > p.S || (int)m.dim > p.d) return false;
+    if ((int)m.head_dim != p.hd || (int)m.seq_len > p.S || (int)m.dim > p.d) return false;
     f.S = (int)m.seq_len;
     f.d = (int)m.dim;
     f.scale = m.scale;
     roff = (long)m.row_offset * f.d;
   }
-  if (hh >= f.d / HD) return false;
+  if (hh >= f.d / p.hd) return false;
   if (p.rows_at) {
     const int r0 = p.rows_at[b];
     f.S = min(p.rows_at[b + 1] - r0, p.S);
     f.q = f.o = (long)r0 * f.d;
     f.kv = p.kv_packed ? f.q : (long)b * p.kv_bs;
-    f.l = (long)r0 * (f.d / HD);
+    f.l = (long)r0 * (f.d / p.hd);
   } else {
     f.q = roff + (long)b * p.q_bs;
     f.kv = roff + (long)b * p.kv_bs;
@@ -413,19 +418,19 @@ __global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
   const int hh = blockIdx.y, b = blockIdx.z;
   FlashSeq fs;
   if (!flash_seq<HD>(p, hh, b, fs)) return;
-  const int S = fs.S, d = fs.d;
+  const int S = fs.S, d = fs.d, hd = p.hd;  // head size hd <= HD
   const float scale = fs.scale;
-  const int H = d / HD;
+  const int H = d / hd;
   const int q0 = blockIdx.x * 64;
   if (q0 >= S) return;
   const int i = q0 + threadIdx.x;
-  const float* qp = p.q + fs.q + hh * HD;
-  const float* kp = p.k + fs.kv + hh * HD;
-  const float* vp = p.v + fs.kv + hh * HD;
+  const float* qp = p.q + fs.q + hh * hd;
+  const float* kp = p.k + fs.kv + hh * hd;
+  const float* vp = p.v + fs.kv + hh * hd;
   float q[HD], acc[HD];
 #pragma unroll
   for (int c = 0; c < HD; ++c) {
-    q[c] = i < S ? qp[(size_t)i * d + c] : 0.f;
+    q[c] = i < S && c < hd ? qp[(size_t)i * d + c] : 0.f;
     acc[c] = 0.f;
   }
   float mrow = -INFINITY, lrow = 0.f;
@@ -435,8 +440,8 @@ __global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
     for (int e = threadIdx.x; e < KB * HD; e += 64) {
       const int r = e / HD, c = e % HD;
       const int key = k0 + r;
-      Ks[r][c] = key < S ? kp[(size_t)key * d + c] : 0.f;
-      Vs[r][c] = key < S ? vp[(size_t)key * d + c] : 0.f;
+      Ks[r][c] = key < S && c < hd ? kp[(size_t)key * d + c] : 0.f;
+      Vs[r][c] = key < S && c < hd ? vp[(size_t)key * d + c] : 0.f;
     }
     __syncthreads();
     const int lim = min(KB, (i < S ? i : -1) - k0 + 1);
@@ -455,9 +460,10 @@ __global__ __launch_bounds__(64) void k_flash_generic(FlashParams p) {
     }
   }
   if (i >= S) return;
-  float* op = p.o + fs.o + hh * HD + (size_t)i * d;
+  float* op = p.o + fs.o + hh * hd + (size_t)i * d;
 #pragma unroll
-  for (int c = 0; c < HD; ++c) op[c] = acc[c] / lrow;
+  for (int c = 0; c < HD; ++c)
+    if (c < hd) op[c] = acc[c] / lrow;
   if (p.lse) p.lse[fs.l + (size_t)i * H + hh] = mrow + logf(lrow);
 }
 
@@ -1073,9 +1079,9 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   FlashSeq fs;
   if (!flash_seq<HD>(p, hh, b, fs)) return;
-  const int S = fs.S, d = fs.d;
+  const int S = fs.S, d = fs.d, hd = p.hd;  // head size hd <= HD
   const float scale = fs.scale;
-  const int H = d / HD;
+  const int H = d / hd;
   // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
   const float qscale = scale * 1.44269504088896341f;
   const int q0 = qblk * QB;
@@ -1083,9 +1089,13 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
 
-  const float* qp = p.q + fs.q + hh * HD;
-  const float* kp = p.k + fs.kv + hh * HD;
-  const float* vp = p.v + fs.kv + hh * HD;
+  const float* qp = p.q + fs.q + hh * hd;
+  const float* kp = p.k + fs.kv + hh * hd;
+  const float* vp = p.v + fs.kv + hh * hd;
+  // Columns past the head size (hd a multiple of 4 below HD) read as zero.
+  auto col4 = [hd](const float* src, int c) {
+    return c < hd ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
 
   const int qi = q0 + wave * 32 + j;
   uint4 qf[3][NQ];  // the three planes of dims 16 s + 8 h .. + 7 of query qi
@@ -1093,9 +1103,8 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
     const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 8 * h;
 #pragma unroll
     for (int s = 0; s < NQ; ++s)
-      split3_rne(*reinterpret_cast<const float4*>(qr + 16 * s),
-                 *reinterpret_cast<const float4*>(qr + 16 * s + 4), qf[0][s], qf[1][s],
-                 qf[2][s]);
+      split3_rne(col4(qr + 16 * s, 16 * s + 8 * h), col4(qr + 16 * s + 4, 16 * s + 8 * h + 4),
+                 qf[0][s], qf[1][s], qf[2][s]);
   }
   f32x16 o[NT];
 #pragma unroll
@@ -1116,8 +1125,8 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
     for (int i = 0; i < KPT; ++i) {
       const int key = kb * KB + sk + i;
       const size_t off = (size_t)(key < S ? key : 0) * d + sc;
-      kr[i] = *reinterpret_cast<const float4*>(kp + off);
-      vr[i] = *reinterpret_cast<const float4*>(vp + off);
+      kr[i] = col4(kp + off, sc);
+      vr[i] = col4(vp + off, sc);
     }
   };
   // Three bfloat16 terms of a and b, packed as pairs (a_pl, b_pl).
@@ -1248,7 +1257,7 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   // O^T (rows = dims) -> LDS, one 32-dim tile at a time -> coalesced rows.
   const float inv = 1.0f / lrow;
   float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33 * 4);
-  float* op = p.o + fs.o + hh * HD;
+  float* op = p.o + fs.o + hh * hd;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     __syncthreads();
@@ -1258,7 +1267,7 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
     for (int e = lane; e < 32 * 32; e += 64) {
       const int r = e >> 5, c = e & 31;
       const int qrow = q0 + wave * 32 + r;
-      if (qrow < S) op[(size_t)qrow * d + 32 * t + c] = Os[r][c];
+      if (qrow < S && 32 * t + c < hd) op[(size_t)qrow * d + 32 * t + c] = Os[r][c];
     }
   }
   if (p.lse && h == 0 && qi < S)  // max + ln(sum), back in natural units
@@ -1520,7 +1529,20 @@ static int flash_small_grid() {
 
 hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
                         hipStream_t s) {
+  if (p.hd <= 0 || p.d % p.hd != 0) return hipErrorInvalidValue;
   const int H = p.d / p.hd;
+  if (p.hd > 32 && p.hd < 128 && p.hd != 64) {
+    // A head size between the MFMA kernels' (a multiple of 4): the split-bf16
+    // kernel of the next larger size, columns past hd zero (fp32-accurate,
+    // whatever p.x6 asks).
+    if (p.hd % 4 != 0) return hipErrorInvalidValue;
+    const dim3 g(H, batch, (max_rows + 127) / 128);
+    if (p.hd < 64)
+      hipLaunchKernelGGL(k_flash_x6<64>, g, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL(k_flash_x6<128>, g, dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
   if (p.hd == 64 || p.hd == 128) {
     // Query blocks slowest and last-first: every (sequence, head)'s longest
     // causal block is dispatched before any shorter one, so the grid ends on
@@ -1543,15 +1565,20 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
     }
     return hipGetLastError();
   }
+  // Head sizes up to 32: the scalar kernel of the next power of two.
   dim3 g((max_rows + 63) / 64, H, batch), b(64);
-  switch (p.hd) {
-    case 2: hipLaunchKernelGGL(k_flash_generic<2>, g, b, 0, s, p); break;
-    case 4: hipLaunchKernelGGL(k_flash_generic<4>, g, b, 0, s, p); break;
-    case 8: hipLaunchKernelGGL(k_flash_generic<8>, g, b, 0, s, p); break;
-    case 16: hipLaunchKernelGGL(k_flash_generic<16>, g, b, 0, s, p); break;
-    case 32: hipLaunchKernelGGL(k_flash_generic<32>, g, b, 0, s, p); break;
-    default: return hipErrorInvalidValue;
-  }
+  if (p.hd <= 2)
+    hipLaunchKernelGGL(k_flash_generic<2>, g, b, 0, s, p);
+  else if (p.hd <= 4)
+    hipLaunchKernelGGL(k_flash_generic<4>, g, b, 0, s, p);
+  else if (p.hd <= 8)
+    hipLaunchKernelGGL(k_flash_generic<8>, g, b, 0, s, p);
+  else if (p.hd <= 16)
+    hipLaunchKernelGGL(k_flash_generic<16>, g, b, 0, s, p);
+  else if (p.hd <= 32)
+    hipLaunchKernelGGL(k_flash_generic<32>, g, b, 0, s, p);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

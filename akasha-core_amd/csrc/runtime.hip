@@ -44,9 +44,12 @@ akh_status fail(akh_status st, const std::string& msg) {
     if (!(cond)) return fail(AKH_E_INVALID, std::string(msg)); \
   } while (0)
 
+// Head sizes the flash kernels take (the reference's FLASH_ATTENTION takes
+// any head_dim <= 128 dividing dim, emit.rs:564-572): up to 32 any (the
+// scalar kernel of the next power of two), beyond that a multiple of 4 up
+// to 128 (the MFMA kernel of 64 or 128 columns, the rest zero).
 bool supported_head_dim(uint32_t hd) {
-  return hd == 2 || hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64 ||
-         hd == 128;
+  return hd >= 1 && (hd <= 32 || (hd <= 128 && hd % 4 == 0));
 }
 
 }  // namespace
@@ -344,7 +347,7 @@ extern "C" akh_status akh_flash_attention(akh_backend* be, const float* q,
   CHECK_ARG(shape.dim % shape.head_dim == 0,
             "flash_attention: dim must be divisible by head_dim");
   CHECK_ARG(supported_head_dim(shape.head_dim),
-            "flash_attention: head_dim must be a power of two");
+            "flash_attention: head_dim above 32 must be a multiple of 4");
   HIP_TRY(shader_flash_attention(q, k, v, out, l_cache, shape, meta, 1, be->stream));
   return AKH_OK;
 }
@@ -361,7 +364,7 @@ extern "C" akh_status akh_flash_attention_batched(akh_backend* be, const float* 
   CHECK_ARG(shape.dim % shape.head_dim == 0,
             "flash_attention: dim must be divisible by head_dim");
   CHECK_ARG(supported_head_dim(shape.head_dim),
-            "flash_attention: head_dim must be a power of two");
+            "flash_attention: head_dim above 32 must be a multiple of 4");
   HIP_TRY(shader_flash_attention(q, k, v, out, l_cache, shape, meta, batch, be->stream));
   return AKH_OK;
 }
@@ -1416,8 +1419,11 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
             "akh_session_new: batch must be in 1..64");
   CHECK_ARG(max_context_len >= 1, "akh_session_new: max_context_len is 0");
   const uint32_t hd = c.dim / c.num_heads;
-  CHECK_ARG(supported_head_dim(hd) && (hd >= 4 || !decode),
-            "akh_session_new: head_dim must be a power of two in 4..128");
+  // RoPE rotates pairs inside a head (cpu.rs:84-109): an even head size; the
+  // decode attention reads rows four columns per lane.
+  CHECK_ARG(supported_head_dim(hd) && hd % 2 == 0 && (!decode || (hd >= 4 && hd % 4 == 0)),
+            "akh_session_new: head_dim must be even and at most 128, a multiple of 4 "
+            "for decoding");
   CHECK_ARG(!decode || (c.dim % 32 == 0 && c.dim <= 4096),
             "akh_session_new: dim must be a multiple of 32, at most 4096");
   CHECK_ARG(!decode || c.ffn_hidden % 32 == 0,

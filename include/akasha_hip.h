@@ -312,7 +312,8 @@ akh_status akh_model_set_prefill_x6(akh_model* m, int enable);
  * batching (TransformerBlock, layers.rs:551-760), the lm_head on every row
  * and CrossEntropy (layers.rs:465-522), on the prefill kernels: one
  * `fused_forward_graph.execute_captured()` plus `CrossEntropy::loss()`
- * (train.rs:380-385).  Any batch; head_dim a power of two up to 128.  Runs
+ * (train.rs:380-385).  Any batch; head_dim even, at most 128 (a multiple
+ * of 4 above 32).  Runs
  * the bf16-MFMA layers when the model has akh_model_set_prefill_bf16 on. */
 typedef struct akh_forward akh_forward;
 akh_status akh_forward_new(akh_model* m, uint32_t batch, uint32_t seq_len, akh_forward** out);

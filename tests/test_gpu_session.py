@@ -219,6 +219,26 @@ def test_ragged_prefill_matches_per_sequence(backend, pkg, ora, dim, mode):
     model.close()
 
 
+@pytest.mark.parametrize("dim,heads", [(192, 2), (160, 4), (96, 4)])  # head_dim 96, 40, 24
+def test_head_dim_not_power_of_two_matches_oracle(backend, pkg, ora, dim, heads):
+    # The reference takes any head_dim dividing dim (config.rs:15-30;
+    # FLASH_ATTENTION asserts head_dim <= 128, emit.rs:564-572).  Prefill
+    # runs the flash kernel of the next power of two with the extra columns
+    # zero; decode attention leaves the lanes past head_dim idle.
+    cfg = pkg.ModelConfig.new(300, dim, heads, 2, 96)
+    w = pkg.synthetic_weights(cfg, seed=71)
+    B, S, steps = 3, 70, 4
+    prompts = pkg.synthetic_tokens(B * S, cfg.vocab_size, seed=72).reshape(B, S)
+    _, s = _session(pkg, backend, cfg, w, 96, B)
+    got = _run(s, prompts, steps)
+    refs = _oracle_greedy_many(ora, cfg, w, 96, list(prompts), steps)
+    for b, (rl, rt) in enumerate(refs):
+        for i in range(steps + 1):
+            assert np.abs(got[i][0][b] - rl[i]).max() < TOL, f"sequence {b} step {i}"
+            assert int(got[i][1][b]) == rt[i], f"sequence {b} step {i}"
+    s.close()
+
+
 def test_decode_greedy_matches_step_by_step(backend, pkg):
     cfg = pkg.ModelConfig.new(300, 128, 2, 2, 64)
     w = pkg.synthetic_weights(cfg, seed=9)
