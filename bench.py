@@ -134,6 +134,66 @@ def scaled_decode(hip, be, model, cfg, T, steps):
     return out
 
 
+DECODE_KERNELS = ["decode_attn", "qkv_proj", "out_proj", "ffn_up", "ffn_down",
+                  "lm_head_argmax", "resid_norm"]
+
+
+def decode_kernel_legs(sess, cfg, B, T, reps, wbytes=4, kvbytes=4):
+    """Each decode kernel alone: `reps` back-to-back launches cycled over the
+    layers (each reads its layer's weights and KV rows as in a step), at KV
+    length T, timed by two events around them (gaps included).  Returns
+    ({name: ms, algorithmic bytes, GB/s}, attention ms per dispatch from
+    events the dispatches carry themselves).  Algorithmic bytes per launch:
+    weights once (`wbytes` per parameter), activations in and out once."""
+    kms = {n: sess.time_decode_kernel(i, reps) for i, n in enumerate(DECODE_KERNELS)}
+    attn_dispatch_ms = sess.time_decode_attn(reps)
+    d, V, F = cfg.dim, cfg.vocab_size, cfg.ffn_hidden
+    kbytes = {
+        "decode_attn": 2 * B * T * d * kvbytes + 2 * B * d * kvbytes,
+        "qkv_proj": d * 3 * d * wbytes + B * 4 * d * 4,
+        "out_proj": d * d * wbytes + 2 * B * d * 4,
+        "ffn_up": d * F * wbytes + B * (d + F) * 4,
+        "ffn_down": F * d * wbytes + B * (F + d) * 4,
+        "lm_head_argmax": d * V * wbytes + B * d * 4 + B * V * 4,
+        "resid_norm": 4 * B * d * 4 + d * 4,
+    }
+    kernels = {n: {"ms": round(kms[n], 5), "bytes": kbytes[n],
+                   "GB/s": round(kbytes[n] / (kms[n] / 1e3) / 1e9, 1)} for n in DECODE_KERNELS}
+    return kernels, attn_dispatch_ms
+
+
+def kernel_legs_only(pkg, hip, be, model, cfg, reps, scaled):
+    """The per-kernel decode legs without any graph replay (for counter
+    runs): config 4 at T = 481 after a 32 x 448 prefill with the KV length
+    then set to 480, and with `scaled` config 5's 64-row session at
+    T = 2048 over a zero KV prefix."""
+    B, P, CTX = 32, 448, 512
+    sess = hip.Session(model, CTX, B)
+    prompt = pkg.synthetic_tokens(B * P, cfg.vocab_size, seed=4).reshape(B, P)
+    log("bench: prefill 32 x 448")
+    sess.prefill(prompt, want_logits=False)
+    sess.set_len(480)
+    log(f"bench: config 4 decode kernels, {reps} launches each")
+    k4, a4 = decode_kernel_legs(sess, cfg, B, 481, reps)
+    sess.close()
+    out = {"config4": {"T": 481, "kernels": k4, "attn_dispatch_ms": round(a4, 5)}}
+    if scaled:
+        c5 = pkg.ModelConfig.scaled()
+        log("bench: scaled config weights (seed 5, bf16 values)")
+        w5 = pkg.synthetic_weights(c5, seed=5, bf16=True)
+        m5 = hip.Model(be, c5)
+        m5.upload(w5)
+        del w5
+        s5 = hip.Session(m5, 2048, 64)
+        s5.set_len(2047)
+        log(f"bench: config 5 decode kernels, {reps} launches each")
+        k5, a5 = decode_kernel_legs(s5, c5, 64, 2048, reps, wbytes=2)
+        s5.close()
+        m5.close()
+        out["config5"] = {"T": 2048, "kernels": k5, "attn_dispatch_ms": round(a5, 5)}
+    return out
+
+
 def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=True):
     """Config 5: the scaled architecture (dim 2048, 24 layers, 16 x 128, FFN
     8192, vocab 50257) with bf16-valued weights (seed 5).  Decode: 64
@@ -382,6 +442,9 @@ def main():
                     help="measure config 5's prefill legs only")
     ap.add_argument("--prefill-only", action="store_true",
                     help="measure only config 3's prefill legs and print them (for profiling)")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="run only the per-kernel decode legs, no graph replay (for counter "
+                         "runs); config 5's too unless --no-scaled")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -401,6 +464,12 @@ def main():
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=2)}),
               flush=True)
+        model.close()
+        be.close()
+        return
+    if args.kernels_only:
+        out = kernel_legs_only(pkg, hip, be, model, cfg, args.kernel_reps, not args.no_scaled)
+        print(json.dumps(out), flush=True)
         model.close()
         be.close()
         return
@@ -445,29 +514,10 @@ def main():
     sess.truncate(P)
     sess.decode_greedy(32, want_tokens=False)
     T = P + 32 + 1
-    names = ["decode_attn", "qkv_proj", "out_proj", "ffn_up", "ffn_down",
-             "lm_head_argmax", "resid_norm"]
-    kms = {n: sess.time_decode_kernel(i, args.kernel_reps) for i, n in enumerate(names)}
-    # The roofline divides by the back-to-back launches' mean (two events
-    # around all of them, the gaps between launches included).  Beside it,
-    # the attention's duration per dispatch from events the dispatches carry
-    # themselves (no gaps).
-    attn_dispatch_ms = sess.time_decode_attn(args.kernel_reps)
-    d, L, V, F = cfg.dim, cfg.num_layers, cfg.vocab_size, cfg.ffn_hidden
-    # Compulsory bytes per launch: weights once, activations in and out once.
-    attn_bytes = 2 * B * T * d * 4 + 2 * B * d * 4
+    kernels, attn_dispatch_ms = decode_kernel_legs(sess, cfg, B, T, args.kernel_reps)
+    kms = {n: k["ms"] for n, k in kernels.items()}
+    attn_bytes = kernels["decode_attn"]["bytes"]
     attn_gbs = attn_bytes / (kms["decode_attn"] / 1e3) / 1e9
-    kbytes = {
-        "decode_attn": attn_bytes,
-        "qkv_proj": d * 3 * d * 4 + B * 4 * d * 4,
-        "out_proj": d * d * 4 + 2 * B * d * 4,
-        "ffn_up": d * F * 4 + B * (d + F) * 4,
-        "ffn_down": F * d * 4 + B * (F + d) * 4,
-        "lm_head_argmax": d * V * 4 + B * d * 4 + B * V * 4,
-        "resid_norm": 4 * B * d * 4 + d * 4,
-    }
-    kernels = {n: {"ms": round(kms[n], 5), "bytes": kbytes[n],
-                   "GB/s": round(kbytes[n] / (kms[n] / 1e3) / 1e9, 1)} for n in names}
 
     prefill = None if args.no_prefill else prefill_measurement(pkg, hip, be, model, cfg, CTX)
 
@@ -601,7 +651,7 @@ def main():
                      "algorithmic_bytes": attn_bytes},
         "step_roofline": {"achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4),
-                          "bytes_per_step_mean": int(total_bytes / args.steps)},
+                          "bytes_per_step_mean": int(total_bytes / steps)},
         "kernels": kernels,
         "prefill": prefill,
         "config1": config1,
