@@ -134,7 +134,12 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   static_assert(!BF || HL % 8 == 0, "bfloat16 tiles need whole k-octets");
   static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16, "W must be a power of 2 <= 16");
   static_assert(MT == 1 || MT == 2, "one or two row tiles");
+  static_assert(EPI != DEC_RESID || W > 1, "the residual epilogue reduces across waves");
   __shared__ float red[W][32][33];
+  // PRO_NORM: per-row sums of four column tiles, and the rows' scales.
+  __shared__ float nsum[PRO == PRO_NORM ? R : 1][33];
+  __shared__ float nrs[PRO == PRO_NORM ? R : 1];
+  __shared__ int last_block;
 
   const int M = p.M, N = p.N, K = p.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -153,6 +158,24 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;  // first k-quad of this half
+    // PRO_NORM: the RMSNorm scale of every row from the residual's
+    // per-column-tile sums of squares [R][K / 32].  The block loads them in
+    // one batch (a float4 of four tiles per thread) ahead of the pass's
+    // weights: memory counters retire in order, so waiting for them does
+    // not wait for the weights.
+    constexpr int NL = PRO == PRO_NORM ? (R * 32 + 64 * W - 1) / (64 * W) : 1;
+    const int nq = K >> 7;  // float4 of sums per row (K % 128 == 0, K <= 4096)
+    float4 v[NL];
+    if constexpr (PRO == PRO_NORM) {
+      if (k0 == kb) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          const int e = threadIdx.x + i * 64 * W;
+          v[i] = e < R * nq ? *reinterpret_cast<const float4*>(p.ssq + 4 * (size_t)e)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
     // The pass's weights: bfloat16 octets or float quads, read once per
     // step, so non-temporal in the layer GEMMs (a measured 2 % per decode
     // step, though each GEMM alone is a little slower).  The lm_head (many
@@ -170,6 +193,15 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
       const f4 t = 4 * kq < ke ? (kNT ? __builtin_nontemporal_load(src) : *src)
                                : f4{0.f, 0.f, 0.f, 0.f};
       wc[i] = __builtin_bit_cast(WRaw, t);
+    }
+    float4 g[HQ];  // PRO_NORM: the gain of the pass's k
+    if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+      for (int q = 0; q < HQ; ++q) {
+        const int kq = kq0 + q;
+        g[q] = 4 * kq < ke ? *reinterpret_cast<const float4*>(p.gain + 4 * kq)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
     float4 a[MT][HQ];
 #pragma unroll
@@ -215,10 +247,41 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
           const float inv = L > 0.f ? 1.0f / L : 0.f;
           t = make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
         } else {
-          t = *reinterpret_cast<const float4*>(p.xt + off);
+          t = *reinterpret_cast<const float4*>(p.xt + off);  // PRO_NORM: the residual
         }
       }
       a[mt][q] = t;
+    }
+    if constexpr (PRO == PRO_NORM) {
+      if (k0 == kb) {
+        // Each float4 summed, then one thread per row adds its row's K / 128
+        // sums in order.
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          const int e = threadIdx.x + i * 64 * W;
+          if (e < R * nq) nsum[e / nq][e % nq] = ((v[i].x + v[i].y) + v[i].z) + v[i].w;
+        }
+        __syncthreads();
+        if (threadIdx.x < R) {
+          float ss = 0.f;
+          for (int c = 0; c < nq; ++c) ss += nsum[threadIdx.x][c];
+          nrs[threadIdx.x] = 1.0f / sqrtf(ss / (float)K + p.eps);
+        }
+        __syncthreads();
+      }
+      // A = (x * rs) * gain, as the RMSNorm kernel rounds it.
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const float rs = nrs[mt * 32 + j];
+#pragma unroll
+        for (int q = 0; q < HQ; ++q) {
+          const float4 x = a[mt][q];
+          a[mt][q] = make_float4(__fmul_rn(__fmul_rn(x.x, rs), g[q].x),
+                                 __fmul_rn(__fmul_rn(x.y, rs), g[q].y),
+                                 __fmul_rn(__fmul_rn(x.z, rs), g[q].z),
+                                 __fmul_rn(__fmul_rn(x.w, rs), g[q].w));
+        }
+      }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -264,13 +327,91 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
           float v = red[0][ml][j];
 #pragma unroll
           for (int w = 1; w < W; ++w) v += red[w][ml][j];
-          if (EPI == DEC_PART)
+          if (EPI == DEC_RESID && rows >= K) {
+            // One split: the block holds whole sums.  Residual add, and the
+            // row's sum of squares over the tile's 32 columns (a butterfly
+            // over the half-wave; lane 0's result is stored).
+            float* rp = p.res + (size_t)mt * 32 * N + kq_index(ml, col);
+            const float r = *rp + v;
+            *rp = r;
+            float q2 = r * r;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) q2 += __shfl_xor(q2, o, 64);
+            if (j == 0) p.ssq_out[(size_t)m * (N >> 5) + tile] = q2;
+          } else if (EPI == DEC_PART)
             p.y[((size_t)blockIdx.y * R + m) * N + col] = v;
           else if (EPI == DEC_PART_T)
             p.y[((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, col)] = v;
+          else if (EPI == DEC_RESID)
+            // Written through to device scope (a relaxed agent-scope atomic
+            // store): no cache write-back is needed before the count below.
+            __hip_atomic_store(p.y + ((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, col),
+                               v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           else
             p.y[(size_t)mt * 32 * N + kq_index(ml, col)] = silu(v);
         }
+      }
+    }
+    if constexpr (EPI == DEC_RESID) {
+      if (rows >= K) return;  // one split: done above
+      // The last of the column tile's blocks to finish adds the tile's
+      // partials, in split order, to the residual, and writes the per-row
+      // sums of squares of the tile's 32 new columns.  Each wave waits until
+      // its device-scope stores have completed, the block meets, then one
+      // thread counts the block; the last block reads the partials with
+      // device-scope loads.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      const int nsplit = (K + rows - 1) / rows;
+      if (threadIdx.x == 0) {
+        const int done =
+            __hip_atomic_fetch_add(p.count + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_block = done == nsplit - 1;
+        if (last_block)  // zero for the next launch
+          __hip_atomic_store(p.count + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (!last_block) return;
+      // One float4 (four columns of one row) per thread: row ml of row tile
+      // mt, column quad cq of the tile; k-quad offsets equal in the partial
+      // tiles (R * N apart) and the residual.
+      constexpr int NE = R * 8;
+      constexpr int NI = (NE + 64 * W - 1) / (64 * W);
+      auto ld = [](const float* q) {
+        return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      };
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int e = threadIdx.x + i * 64 * W;
+        if (e < NE) {
+          const int ml = e & 31, cq = (e >> 5) & 7, mt = e >> 8;
+          const size_t off = (size_t)mt * 32 * N + ((size_t)(tile * 8 + cq) * 32 + ml) * 4;
+          float4 v = *reinterpret_cast<const float4*>(p.res + off);
+          for (int s0 = 0; s0 < nsplit; s0 += 8) {
+            float4 t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const float* q = p.y + (size_t)(s0 + u) * R * N + off;
+              t[u] = s0 + u < nsplit ? make_float4(ld(q), ld(q + 1), ld(q + 2), ld(q + 3))
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+              if (s0 + u < nsplit) add4(v, t[u]);
+          }
+          *reinterpret_cast<float4*>(p.res + off) = v;
+          // e = (mt * 8 + cq) * 32 + ml: red viewed as [R / 32][8][32].
+          (&red[0][0][0])[e] = ((v.x * v.x + v.y * v.y) + v.z * v.z) + v.w * v.w;
+        }
+      }
+      __syncthreads();
+      if (threadIdx.x < R) {
+        const int mt = threadIdx.x >> 5, ml = threadIdx.x & 31;
+        const float* sq = &red[0][0][0] + mt * 256 + ml;
+        float ss = 0.f;
+#pragma unroll
+        for (int cq = 0; cq < 8; ++cq) ss += sq[cq * 32];
+        p.ssq_out[(size_t)threadIdx.x * (N >> 5) + tile] = ss;
       }
     }
     return;
@@ -720,19 +861,33 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (q < nq) {
       float* xq = p.xt + tile_off + ((size_t)q * 32 + (m & 31)) * 4;
-      if (gather) {
-        if (row) v = *reinterpret_cast<const float4*>(row + 4 * q);
+      if (p.ssq) {
+        v = *reinterpret_cast<const float4*>(xq);
       } else {
-        v = sum_parts4_2<AKH_NORM_NB1, 8>(*reinterpret_cast<const float4*>(xq),
-                                          p.parts + (size_t)m * d + 4 * q, (size_t)p.rows * d,
-                                          p.nparts);
+        if (gather) {
+          if (row) v = *reinterpret_cast<const float4*>(row + 4 * q);
+        } else {
+          v = sum_parts4_2<AKH_NORM_NB1, 8>(*reinterpret_cast<const float4*>(xq),
+                                            p.parts + (size_t)m * d + 4 * q, (size_t)p.rows * d,
+                                            p.nparts);
+        }
+        *reinterpret_cast<float4*>(xq) = v;
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
       }
-      *reinterpret_cast<float4*>(xq) = v;
-      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
     x[i] = v;
   }
-  ss = block_sum256(ss, red4);
+  if (p.ssq) {
+    // The residual's per-column-tile sums of squares, added as the decode
+    // GEMMs' RMSNorm prologue adds them (four tiles, then in order).
+    const float4* sq = reinterpret_cast<const float4*>(p.ssq + (size_t)m * (d >> 5));
+    for (int c = 0; c < (d >> 7); ++c) {
+      const float4 v = sq[c];
+      ss += ((v.x + v.y) + v.z) + v.w;
+    }
+  } else {
+    ss = block_sum256(ss, red4);
+  }
   const float rs = 1.0f / sqrtf(ss / (float)d + p.eps);
 #pragma unroll
   for (int i = 0; i < QPT; ++i) {
@@ -996,16 +1151,31 @@ hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s) {
   return hipGetLastError();
 }
 
+bool dec_norm_fusable(int K) { return K % 128 == 0 && K <= 4096; }
+
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
+  // PRO_NORM reads [rows][K / 32] sums of squares four tiles at a time;
+  // DEC_RESID writes them for N / 32 column tiles.
+  if (p.ssq && !dec_norm_fusable(p.K)) return hipErrorInvalidValue;
+  if (p.res && (!p.ssq_out || !p.count || !dec_norm_fusable(p.N))) return hipErrorInvalidValue;
   switch (role) {
-    case DEC_CFG_QKV: return dec_go<DEC_CFG_QKV, DEC_PART, PRO_NONE>(p, s);
-    case DEC_CFG_OUT: return dec_go<DEC_CFG_OUT, DEC_PART, PRO_ATTN_MERGE>(p, s);
+    case DEC_CFG_QKV:
+      return p.ssq ? dec_go<DEC_CFG_QKV, DEC_PART, PRO_NORM>(p, s)
+                   : dec_go<DEC_CFG_QKV, DEC_PART, PRO_NONE>(p, s);
+    case DEC_CFG_OUT:
+      return p.res ? dec_go<DEC_CFG_OUT, DEC_RESID, PRO_ATTN_MERGE>(p, s)
+                   : dec_go<DEC_CFG_OUT, DEC_PART, PRO_ATTN_MERGE>(p, s);
     case DEC_CFG_UP:
       // One split: the whole sum is in the block, so SiLU is applied here.
-      return dec_gemm_splits(DEC_CFG_UP, p.K, p.N) == 1
-                 ? dec_go<DEC_CFG_UP, DEC_SILU_T, PRO_NONE>(p, s)
-                 : dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NONE>(p, s);
+      if (dec_gemm_splits(DEC_CFG_UP, p.K, p.N) == 1)
+        return p.ssq ? dec_go<DEC_CFG_UP, DEC_SILU_T, PRO_NORM>(p, s)
+                     : dec_go<DEC_CFG_UP, DEC_SILU_T, PRO_NONE>(p, s);
+      return p.ssq ? dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NORM>(p, s)
+                   : dec_go<DEC_CFG_UP, DEC_PART_T, PRO_NONE>(p, s);
     case DEC_CFG_DOWN:
+      if (p.res)
+        return p.nparts ? dec_go<DEC_CFG_DOWN, DEC_RESID, PRO_SILU_SUM>(p, s)
+                        : dec_go<DEC_CFG_DOWN, DEC_RESID, PRO_NONE>(p, s);
       return p.nparts ? dec_go<DEC_CFG_DOWN, DEC_PART, PRO_SILU_SUM>(p, s)
                       : dec_go<DEC_CFG_DOWN, DEC_PART, PRO_NONE>(p, s);
   }

@@ -169,12 +169,17 @@ enum DecEpi : int {
   DEC_PART_T = 1,  // the same, each partial tile in the k-quad layout
   DEC_LOGITS = 2,  // y[m, n] = whole-K result + per-tile argmax partials
   DEC_SILU_T = 3,  // y = silu(whole-K result) in the k-quad layout (one split)
+  // k-quad partial tiles as DEC_PART_T; the last block of each column tile
+  // then adds their sum to the residual rows `res` and writes the tile's
+  // per-row sums of squares (the residual add of the next RMSNorm).
+  DEC_RESID = 4,
 };
 
 enum DecPro : int {
   PRO_NONE = 0,        // A = xt
   PRO_SILU_SUM = 1,    // A = silu(sum of nparts k-quad partial tiles at xt)
   PRO_ATTN_MERGE = 2,  // A = merge of nparts attention splits (xt, ml)
+  PRO_NORM = 3,        // A = RMSNorm(xt) * gain, from the sums of squares ssq
 };
 
 // Most splits of one (sequence, head) attention.
@@ -183,9 +188,9 @@ constexpr int kMaxAttnSplits = 4;
 // Roles of the decode GEMMs; each has its own launch shape.
 enum DecCfg : int {
   DEC_CFG_QKV = 0,   // qkv_proj  -> partials (summed by attention)
-  DEC_CFG_OUT = 1,   // out_proj  -> partials (summed by rows_norm)
+  DEC_CFG_OUT = 1,   // out_proj  -> residual add (DEC_RESID)
   DEC_CFG_UP = 2,    // ffn_up    -> k-quad partials (summed by down)
-  DEC_CFG_DOWN = 3,  // ffn_down on silu(sum) -> partials (rows_norm)
+  DEC_CFG_DOWN = 3,  // ffn_down on silu(sum) -> residual add (DEC_RESID)
   DEC_CFG_LM = 4,    // lm_head   -> logits + argmax partials
 };
 
@@ -202,6 +207,18 @@ struct DecGemmParams {
   int kpass;         // set by the launcher: K passes per block (grid.y chunks)
   int mt;            // 32-row tiles of the rows (1 or 2); partial tiles and
                      // attention splits hold 32 * mt rows
+  // PRO_NORM: xt holds the residual rows; A = xt * rs(m) * gain with
+  // rs(m) = 1 / sqrt(sum_t ssq[m, t] / K + eps) over the K / 32 column tiles.
+  const float* ssq;
+  const float* gain;
+  float eps;
+  // DEC_RESID: res (k-quad, [32 * mt][N] residual rows) += the sum of the
+  // partial tiles at y; ssq_out[m, tile] = sum over the tile's 32 columns of
+  // the new res[m, n]^2.  count[tile] (zero between launches) counts the
+  // finished blocks of a column tile.
+  float* res;
+  float* ssq_out;
+  int* count;
 };
 
 // Decode weights are read from a copy packed once at upload: 32-column
@@ -225,6 +242,9 @@ bool dec_bf16_capable(int role, int K, int N);
 // Number of K chunks (partial tiles) a role's GEMM produces for contraction
 // length K.
 int dec_gemm_splits(int role, int K, int N);
+// Whether the RMSNorm folds into the decode GEMMs (PRO_NORM / DEC_RESID)
+// for a residual width of K: a multiple of 128, at most 4096.
+bool dec_norm_fusable(int K);
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s);
 
 // lm_head: logits y[M, N] = xt . w and argmax partials amax[M, parts], where
@@ -288,6 +308,9 @@ struct RowsNormParams {
   int d;
   int rows;  // 32 * the row tiles: xt / xnt are [rows / 32][d/4][32][4] and
              // the partial tiles [nparts][rows][d]
+  // If set: xt already holds the residual rows and ssq[m, d / 32] their
+  // per-column-tile sums of squares (DEC_RESID); only xnt is written.
+  const float* ssq;
 };
 
 hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s);

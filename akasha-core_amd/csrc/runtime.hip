@@ -951,10 +951,21 @@ struct akh_session {
   float* attn_t = nullptr;  // attention splits: unnormalised o [splits][32][dim]
   float2* attn_ml = nullptr;  // attention splits: (max, sum) [splits][heads][32]
   float* p_qkv = nullptr;   // [ks_qkv][32][3*dim]
-  float* p_out = nullptr;   // [ks_out][32][dim]
+  float* p_out = nullptr;   // [ks_out] partial tiles of [32, dim] (k-quad when fused)
   float* p_up = nullptr;    // [ks_up] k-quad tiles of [32, ffn]
   float* up_act = nullptr;  // silu(ffn_up) when summed by its own kernel
-  float* p_down = nullptr;  // [ks_down][32][dim]
+  float* p_down = nullptr;  // [ks_down] partial tiles of [32, dim] (k-quad when fused)
+  // With the RMSNorm folded into the GEMMs (akh_session_set_fused_norm):
+  // out_proj (fuse_out) and ffn_down (fuse_down) add their sums to xt
+  // themselves and write ssq [32][dim / 32], the new residual's sums of
+  // squares per 32-column tile, which ffn_up, qkv_proj and the final norm
+  // turn into each row's scale: 5 launches per layer instead of 7.  Off by
+  // default: the cross-block handoff in those epilogues costs more than the
+  // two kernel boundaries it removes.  rcount holds the per-column-tile
+  // block counters of the epilogues (zero between launches).
+  bool fuse_out = false, fuse_down = false;
+  float* ssq = nullptr;
+  int* rcount = nullptr;
   float* logits = nullptr;  // [32, vocab]
   uint2* amax = nullptr;    // [32, lm tiles] argmax partials
   uint32_t* tok = nullptr;  // tokens fed to the next step
@@ -1097,12 +1108,34 @@ RowsNormParams norm_base(akh_session* s, const float* gain) {
   return r;
 }
 
+// A GEMM whose A operand is the RMSNorm of the residual with `gain`: the
+// normed rows xnt, or with the fused norm the residual and its sums of
+// squares (layer 0's qkv_proj reads the embedding kernel's xnt).
+void norm_operand(akh_session* s, DecGemmParams& p, const float* gain, bool fused) {
+  if (!fused) {
+    p.xt = s->xnt;
+    return;
+  }
+  p.xt = s->xt;
+  p.ssq = s->ssq;
+  p.gain = gain;
+  p.eps = s->m->cfg.norm_eps;
+}
+
+// The residual-add epilogue of out_proj and ffn_down when the norm is fused.
+void resid_epilogue(akh_session* s, DecGemmParams& p, bool fused) {
+  if (!fused) return;
+  p.res = s->xt;
+  p.ssq_out = s->ssq;
+  p.count = s->rcount;
+}
+
 // qkv_proj on the normalised residual (inference_graphs.rs:363-384):
 // partial tiles, summed by the attention kernel.
 hipError_t enqueue_qkv(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
-  p.xt = s->xnt;
+  norm_operand(s, p, s->m->layer(l, W_NORM1), s->fuse_down && l > 0);
   use_packed(p, s->m->packed_layer(l, W_QKV));
   p.y = s->p_qkv;
   p.N = 3 * c.dim;
@@ -1135,7 +1168,8 @@ hipError_t enqueue_attn(akh_session* s, uint32_t l, hipEvent_t t0 = nullptr,
   return launch_dec_attn(p, (int)s->B, (int)hd, s->be->stream, t0, t1);
 }
 
-// out_proj (inference_graphs.rs:458-470): partial tiles.
+// out_proj (inference_graphs.rs:458-470): partial tiles, or with the fused
+// norm the residual add (inference_graphs.rs:471) as well.
 hipError_t enqueue_out(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
@@ -1147,10 +1181,11 @@ hipError_t enqueue_out(akh_session* s, uint32_t l) {
   p.y = s->p_out;
   p.N = c.dim;
   p.K = c.dim;
+  resid_epilogue(s, p, s->fuse_out);
   return launch_dec_gemm(p, DEC_CFG_OUT, s->be->stream);
 }
 
-// Residual add of a GEMM's partial tiles + the next RMSNorm.
+// Residual add of a GEMM's partial tiles + the next RMSNorm (unfused norm).
 hipError_t enqueue_resid_norm(akh_session* s, const float* parts, int nparts,
                               const float* gain) {
   RowsNormParams r = norm_base(s, gain);
@@ -1159,11 +1194,19 @@ hipError_t enqueue_resid_norm(akh_session* s, const float* parts, int nparts,
   return launch_rows_norm(r, (int)s->B, s->be->stream);
 }
 
+// The RMSNorm of the residual rows alone, from the sums of squares the
+// fused epilogue wrote (the final norm before lm_head).
+hipError_t enqueue_norm_only(akh_session* s, const float* gain) {
+  RowsNormParams r = norm_base(s, gain);
+  r.ssq = s->ssq;
+  return launch_rows_norm(r, (int)s->B, s->be->stream);
+}
+
 // ffn_up on norm_2 of the residual (inference_graphs.rs:472-493).
 hipError_t enqueue_up(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
-  p.xt = s->xnt;
+  norm_operand(s, p, s->m->layer(l, W_NORM2), s->fuse_out);
   use_packed(p, s->m->packed_layer(l, W_UP));
   p.y = s->p_up;
   p.N = c.ffn_hidden;
@@ -1194,6 +1237,7 @@ hipError_t enqueue_down(akh_session* s, uint32_t l) {
   p.y = s->p_down;
   p.N = c.dim;
   p.K = c.ffn_hidden;
+  resid_epilogue(s, p, s->fuse_down);
   return launch_dec_gemm(p, DEC_CFG_DOWN, s->be->stream);
 }
 
@@ -1230,12 +1274,15 @@ hipError_t enqueue_decode_body(akh_session* s) {
     e = enqueue_qkv(s, l);
     if (e == hipSuccess) e = enqueue_attn(s, l);
     if (e == hipSuccess) e = enqueue_out(s, l);
-    if (e == hipSuccess)
+    if (e == hipSuccess && !s->fuse_out)
       e = enqueue_resid_norm(s, s->p_out, s->ks_out, s->m->layer(l, W_NORM2));
     if (e == hipSuccess) e = enqueue_up(s, l);
     if (e == hipSuccess) e = enqueue_down(s, l);
-    if (e == hipSuccess) e = enqueue_resid_norm(s, s->p_down, s->ks_down, next_gain);
+    if (e == hipSuccess && !s->fuse_down)
+      e = enqueue_resid_norm(s, s->p_down, s->ks_down, next_gain);
   }
+  // Fused: the last ffn_down left the residual and its sums of squares.
+  if (e == hipSuccess && s->fuse_down) e = enqueue_norm_only(s, s->m->final_norm());
   if (e == hipSuccess) e = enqueue_lm_head(s);
   return e;
 }
@@ -1386,7 +1433,7 @@ extern "C" void akh_session_free(akh_session* s) {
   free_prefill(s);
   void* bufs[] = {s->kv,     s->rope,   s->xt,     s->xnt,    s->attn_t, s->attn_ml,
                   s->p_qkv,  s->p_out,  s->p_up,   s->up_act, s->p_down,
-                  s->logits, s->amax,
+                  s->logits, s->amax,   s->ssq,    s->rcount,
                   s->tok,    s->pos,    s->hist,   s->active, s->done,   s->gstart,
                   s->gcount, s->ggen,   s->guni,   s->gwbuf};
   for (void* p : bufs)
@@ -1462,6 +1509,10 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
   alloc((void**)&s->p_up, (size_t)s->ks_up * R * F * 4);
   if (silu_own_kernel(s)) alloc((void**)&s->up_act, R * F * 4);
   alloc((void**)&s->p_down, (size_t)s->ks_down * R * d * 4);
+  if (dec_norm_fusable((int)d)) {  // for akh_session_set_fused_norm
+    alloc((void**)&s->ssq, R * (d / 32) * 4);
+    alloc((void**)&s->rcount, (d / 32) * sizeof(int));  // zeroed by alloc
+  }
   alloc((void**)&s->logits, R * V * 4);
   alloc((void**)&s->amax, R * (size_t)lm_parts(s) * sizeof(uint2));
   alloc((void**)&s->tok, RB * 4);
@@ -2251,7 +2302,11 @@ extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,
       case 4: return enqueue_down(s, l);
       case 5: return enqueue_lm_head(s);
       default:
-        return enqueue_resid_norm(s, s->p_out, s->ks_out, s->m->layer(l, W_NORM2));
+        // The step's RMSNorm kernel: the residual add + norm after each
+        // GEMM pair, or with the norm fused, the final norm alone.
+        return s->fuse_out && s->fuse_down
+                   ? enqueue_norm_only(s, s->m->final_norm())
+                   : enqueue_resid_norm(s, s->p_out, s->ks_out, s->m->layer(l, W_NORM2));
     }
   };
   for (uint32_t l = 0; l < L; ++l) HIP_TRY(one(l));  // warm
@@ -2310,6 +2365,21 @@ extern "C" akh_status akh_session_decode_launches(akh_session* s, uint32_t* laun
     if (t == hipGraphNodeTypeKernel) ++k;
   }
   *launches = k;
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_session_set_fused_norm(akh_session* s, int enable) {
+  CHECK_ARG(s, "akh_session_set_fused_norm: NULL session");
+  CHECK_ARG(!s->be->capturing, "akh_session_set_fused_norm: graph capture in progress");
+  CHECK_ARG(!enable || s->ssq,
+            "akh_session_set_fused_norm: needs a decode session whose dim is a multiple of "
+            "128, at most 4096");
+  if (s->fuse_out != (enable != 0)) {
+    HIP_TRY(hipSetDevice(s->be->device));
+    HIP_TRY(hipStreamSynchronize(s->be->stream));
+    drop_graphs(s);  // captured with the other kernels
+    s->fuse_out = s->fuse_down = enable != 0;
+  }
   return AKH_OK;
 }
 

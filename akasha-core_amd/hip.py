@@ -231,6 +231,7 @@ _SIGS = {
     "akh_session_time_decode_kernel": (ST, [P, C.c_int, U32, C.POINTER(C.c_float)]),
     "akh_session_time_decode_attn": (ST, [P, U32, C.POINTER(C.c_float)]),
     "akh_session_decode_launches": (ST, [P, C.POINTER(U32)]),
+    "akh_session_set_fused_norm": (ST, [P, C.c_int]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -780,6 +781,11 @@ class Session:
         n = U32()
         _check(_lib.akh_session_decode_launches(self.handle, C.byref(n)), "decode_launches")
         return n.value
+
+    def set_fused_norm(self, enable: bool):
+        """Fold the residual adds + RMSNorms into the decode GEMMs (five
+        launches per layer instead of seven; off by default)."""
+        _check(_lib.akh_session_set_fused_norm(self.handle, int(bool(enable))), "set_fused_norm")
 
     def close(self):
         if self.handle:

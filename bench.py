@@ -509,6 +509,17 @@ def main():
     step_gbs = total_bytes / (ms / 1e3) / 1e9
     launches_per_step = sess.decode_launches()
 
+    # The same windows with each layer's residual adds + RMSNorms folded into
+    # the GEMMs (five launches per layer instead of seven): not the default,
+    # reported beside it.
+    sess.set_fused_norm(True)
+    run_steps(window)  # capture + warm
+    fused_ms = run_steps(steps)
+    fused_norm = {"ms_per_step": round(fused_ms / steps, 5),
+                  "launches_per_step": sess.decode_launches(),
+                  "step_frac": round(total_bytes / (fused_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+    sess.set_fused_norm(False)
+
     # Dominant kernel: decode attention at T = 481 (pos 480), launches cycled
     # over the 12 layers so each reads its KV rows from HBM as in a step.
     sess.truncate(P)
@@ -652,6 +663,7 @@ def main():
         "step_roofline": {"achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                           "bytes_per_step_mean": int(total_bytes / steps)},
+        "decode_fused_norm": fused_norm,
         "kernels": kernels,
         "prefill": prefill,
         "config1": config1,

@@ -480,6 +480,18 @@ akh_status akh_session_time_decode_attn(akh_session* s, uint32_t reps, float* av
  * in the reference (measurement only; the reference dispatches ~195 nodes
  * per sequence per token, inference_graphs.rs:339-509). */
 akh_status akh_session_decode_launches(akh_session* s, uint32_t* launches);
+/* Fold each layer's two residual adds + RMSNorms into the decode GEMMs
+ * (enable != 0): out_proj and ffn_down add their sums to the residual
+ * themselves (the last block of each column tile to finish sums the K
+ * splits' partial tiles, handed over at device scope) and write per-tile
+ * sums of squares; qkv_proj, ffn_up and the final norm scale their A
+ * operand by each row's RMSNorm.  Five launches per layer instead of seven,
+ * the same results to rounding.  Off by default, because on MI355X the
+ * handoff costs more than the two kernel boundaries it saves (config 4:
+ * 0.677 against 0.632 ms per step).  Needs a decode session whose dim is a
+ * multiple of 128 (at most 4096); drops the captured graphs.  No
+ * counterpart in the reference (a launch-structure choice). */
+akh_status akh_session_set_fused_norm(akh_session* s, int enable);
 
 #ifdef __cplusplus
 }

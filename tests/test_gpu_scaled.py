@@ -68,6 +68,17 @@ def test_scaled_decode_64_rows_at_kv_2048(pkg, scaled):
     for i, ((a, ta), (b, tb)) in enumerate(zip(run[1:], f32)):
         assert np.abs(a - b).max() < 1e-4, f"step {i}"
         assert np.array_equal(ta, tb), f"step {i}"
+    # The residual adds + RMSNorms folded into the GEMMs (32 K splits of
+    # ffn_down summed by the last block of each column tile), same steps.
+    s.set_fused_norm(True)
+    try:
+        s.truncate(S)
+        fused = _decode(s, steps)
+    finally:
+        s.set_fused_norm(False)
+    for i, ((a, ta), (b, tb)) in enumerate(zip(run[1:], fused)):
+        assert np.abs(a - b).max() < 1e-4, f"fused norm, step {i}"
+        assert np.array_equal(ta, tb), f"fused norm, step {i}"
     s.close()
 
 

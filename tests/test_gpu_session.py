@@ -167,6 +167,38 @@ def test_two_row_tiles_bf16_weight_tiles(backend, pkg):
     model.close()
 
 
+@pytest.mark.parametrize("B", [5, 40])
+@pytest.mark.parametrize("bf16_tiles", [False, True])
+def test_fused_norm_matches_oracle(backend, pkg, ora, B, bf16_tiles):
+    # akh_session_set_fused_norm: the residual adds + RMSNorms folded into
+    # the decode GEMMs (out_proj and ffn_down sum their K splits into the
+    # residual, qkv_proj / ffn_up / the final norm scale their operand), on
+    # one and two 32-row tiles and on float and bfloat16 weight tiles.
+    cfg = pkg.ModelConfig.new(300, 256, 2, 2, 40)  # head_dim 128
+    w = pkg.synthetic_weights(cfg, seed=12, bf16=bf16_tiles)
+    S, steps = 17, 6
+    prompts = pkg.synthetic_tokens(B * S, cfg.vocab_size, 13).reshape(B, S)
+    model, s = _session(pkg, backend, cfg, w, 40, B)
+    # The layer matrices; lm_head (K = 256) runs the persistent float kernel.
+    assert model.set_bf16_tiles(True) == (4 * cfg.num_layers if bf16_tiles else 0)
+    plain = _run(s, prompts, steps)
+    s.reset()
+    s.set_fused_norm(True)
+    fused = _run(s, prompts, steps)
+    for i, ((lp, tp), (lf, tf)) in enumerate(zip(plain, fused)):
+        assert np.abs(lp - lf).max() < 1e-4, f"step {i}"
+        assert np.array_equal(tp, tf), f"step {i}"
+    for b in sorted({0, B // 2, B - 1}):
+        rl, rt = _oracle_greedy(ora, cfg, w, 40, prompts[b], steps)
+        for i in range(steps + 1):
+            assert np.abs(fused[i][0][b] - rl[i]).max() < TOL, f"sequence {b} step {i}"
+            assert int(fused[i][1][b]) == rt[i], f"sequence {b} step {i}"
+    c192 = pkg.ModelConfig.new(300, 192, 2, 2, 40)
+    _, odd = _session(pkg, backend, c192, pkg.synthetic_weights(c192, 1), 40, 2)
+    with pytest.raises(pkg.hip.InvalidArgument):
+        odd.set_fused_norm(True)  # dim not a multiple of 128
+
+
 @pytest.mark.parametrize("dim", [128, 256])
 @pytest.mark.parametrize("mode", ["x6", "fp32_mfma", "kv16", "bf16"])
 def test_ragged_prefill_matches_per_sequence(backend, pkg, ora, dim, mode):
@@ -362,6 +394,18 @@ def test_hall1_c4_batch_properties(backend, pkg, ora):
         for i in range(steps + 1):
             assert np.abs(all_l[i][j] - rl[i]).max() < TOL, f"sequence {b} step {i}"
             assert int(all_t[i][b]) == rt[i], f"sequence {b} step {i}"
+    # The residual adds + RMSNorms folded into the GEMMs (five launches per
+    # layer): the same 64 steps again from the prefilled caches.
+    s.truncate(S)
+    s.set_fused_norm(True)
+    assert s.decode_launches() == 5 * cfg.num_layers + 4
+    for i in range(1, steps + 1):
+        logits, nxt = s.decode_step(None)
+        assert np.array_equal(nxt, all_t[i]), f"fused norm, step {i}"
+        for j, (b, (rl, rt)) in enumerate(zip(checked, refs)):
+            assert np.abs(logits[b] - rl[i]).max() < TOL, f"fused norm, sequence {b} step {i}"
+    s.set_fused_norm(False)
+    assert s.decode_launches() == 7 * cfg.num_layers + 3
     # KV append landed at the right rows: the whole 512-row cache is filled.
     kc = s.cache(5, 7, 0)
     assert S + steps == 512 and np.all(np.abs(kc).sum(1) > 0)
