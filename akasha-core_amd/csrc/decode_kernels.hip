@@ -1,20 +1,24 @@
 // Batched decode kernels: every sequence of a step is one row of a 32-row
-// MFMA tile, so each weight byte is read once per step for the whole batch.
+// MFMA tile (two tiles for 33..64 sequences), so each weight byte is read
+// once per step for the whole batch.
 //
-// Dataflow of one layer (B <= 32 rows):
+// Dataflow of one layer (B <= 64 rows):
 //
 //   xn_t --qkv GEMM--> P_qkv --attention (sum, RoPE, KV append)--> attn_t
 //   attn_t --out GEMM--> P_out --rows_norm (x += sum, RMSNorm)--> x_t, xn_t
 //   xn_t --up GEMM--> P_up_t --down GEMM (A = silu(sum))--> P_down
 //   P_down --rows_norm (x += sum, next RMSNorm)--> x_t, xn_t
 //
-// Activations that feed a GEMM live in the k-quad layout [K/4][32][4]: the
-// MFMA A operand of a half-wave is one contiguous 512-byte float4 load per
-// four k.  A decode GEMM moves only a few MB, so the kernels split K over
-// many small blocks (the whole GPU works on each GEMM) and store partial
-// tiles; the consumer of each GEMM sums the partials in a fixed order.
-// Nothing synchronises across work-groups inside a kernel and no atomics
-// are used, so results are deterministic.
+// Activations that feed a GEMM live in the k-quad layout [R/32][K/4][32][4]:
+// the MFMA A operand of a half-wave is one contiguous 512-byte float4 load
+// per four k.  A decode GEMM moves only a few MB, so the kernels split K
+// over many small blocks (the whole GPU works on each GEMM) and store
+// partial tiles; the consumer of each GEMM sums the partials in a fixed
+// order, so results are deterministic.  In this default dataflow nothing
+// synchronises across work-groups inside a kernel.  The optional fused norm
+// (DEC_RESID / PRO_NORM) folds each rows_norm into the GEMMs around it; its
+// residual epilogue counts finished blocks with one atomic per block and
+// sums the partials in split order, so it is deterministic too.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -110,10 +114,16 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
 // k-quad activation (its row m = j, the same four k); a half-wave's load is
 // 512 contiguous bytes.  All loads of a pass are issued before its first
 // MFMA.  A block runs one pass when K is split over the grid, and loops over
-// all of K otherwise.  The waves' tiles are reduced in LDS as a binary tree
-// (fixed order); wave 0 runs the epilogue.
+// all of K otherwise.  Partial-tile epilogues write every wave's 32x32 tile
+// to LDS behind one barrier, then wave w sums rows [w * 32 / W, (w + 1) *
+// 32 / W) over the waves in index order; the logits epilogue reduces the
+// waves' tiles as a binary tree (fixed order) and wave 0 finishes it.
 //
 // PRO_SILU_SUM: A = silu(sum of p.nparts k-quad partial tiles at p.xt).
+// PRO_NORM: A = RMSNorm of the residual rows at p.xt (see DecGemmParams).
+// DEC_RESID: k-quad partial tiles, then the last block of each column tile
+// adds their sum to the residual p.res and writes the per-row sums of
+// squares of its 32 columns (one split: done directly in the epilogue).
 // BF: W is packed in bfloat16 k-octets (k_pack_tiles_bf16); a lane loads
 // eight k per 16 bytes.  Its octet and the same eight k of its row of A are
 // the operands of v_mfma_f32_32x32x16_bf16, with A split exactly into three
