@@ -948,10 +948,14 @@ namespace {
 // elements (hall-1.0's) and one for larger (the scaled configuration's);
 // each can be overridden at build time, e.g. -DAKH_SHAPE_QKV=4,24 or
 // -DAKH_SHAPE_L_OUT=4,16.  The four layer GEMMs split K into chunks of
-// whole passes: one pass per block while the grid stays within
-// AKH_GEMM_BLOCKS blocks, more passes per block (fewer partial tiles for the
-// consumer to sum) beyond; the generic lm_head (K beyond the persistent
-// kernel's reach) runs whole-K blocks.
+// whole passes: one pass per block while the grid stays within the role's
+// block cap (AKH_GEMM_BLOCKS_*), more passes per block (fewer partial tiles
+// for the consumer to sum) beyond; the generic lm_head (K beyond the
+// persistent kernel's reach) runs whole-K blocks.  The caps bind only for
+// the scaled configuration's matrices (config 5, one 64-row session: qkv
+// 1024, out 1024, up 256 -- one K split, so ffn_up applies SiLU itself and
+// the separate SiLU kernel goes -- and down 512 measured best per role,
+// 6.52 -> 6.13 ms per bf16-KV step); hall-1.0's grids stay below every cap.
 #ifndef AKH_SHAPE_QKV
 #define AKH_SHAPE_QKV 16, 12
 #endif
@@ -985,8 +989,17 @@ namespace {
 #ifndef AKH_LARGE_GEMM
 #define AKH_LARGE_GEMM (1l << 22)
 #endif
-#ifndef AKH_GEMM_BLOCKS
-#define AKH_GEMM_BLOCKS 2048
+#ifndef AKH_GEMM_BLOCKS_QKV
+#define AKH_GEMM_BLOCKS_QKV 1024
+#endif
+#ifndef AKH_GEMM_BLOCKS_OUT
+#define AKH_GEMM_BLOCKS_OUT 1024
+#endif
+#ifndef AKH_GEMM_BLOCKS_UP
+#define AKH_GEMM_BLOCKS_UP 256
+#endif
+#ifndef AKH_GEMM_BLOCKS_DOWN
+#define AKH_GEMM_BLOCKS_DOWN 512
 #endif
 
 template <int ROLE, bool LARGE>
@@ -1014,7 +1027,11 @@ int role_kpass(int K, int N) {
   constexpr int KC = 2 * RoleShape<ROLE, LARGE>::W * RoleShape<ROLE, LARGE>::HL;
   const int passes = (K + KC - 1) / KC;
   if (ROLE == DEC_CFG_LM) return passes;
-  const int want = std::max(1, std::min(passes, AKH_GEMM_BLOCKS / ((N + 31) / 32)));
+  constexpr int cap = ROLE == DEC_CFG_QKV  ? AKH_GEMM_BLOCKS_QKV
+                      : ROLE == DEC_CFG_OUT ? AKH_GEMM_BLOCKS_OUT
+                      : ROLE == DEC_CFG_UP  ? AKH_GEMM_BLOCKS_UP
+                                            : AKH_GEMM_BLOCKS_DOWN;
+  const int want = std::max(1, std::min(passes, cap / ((N + 31) / 32)));
   return (passes + want - 1) / want;
 }
 
