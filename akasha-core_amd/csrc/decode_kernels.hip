@@ -1209,9 +1209,20 @@ hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-// Attention launch shape: AW waves, RB row groups in flight, SP splits.
+// Attention launch shapes: AW waves, RB row groups in flight, SP splits.
+// The default serves short contexts and small grids (hall-1.0 at batch 32:
+// 384 (sequence, head) pairs over 449..512 rows).  Long contexts with at
+// least 512 pairs take 8 waves per block: with the f32 cache in 2 splits,
+// with the bfloat16 cache in 1 split of 4 row groups (config 5, 64 x 16
+// pairs at 2048 rows: 10.11 -> 9.58 and 6.15 -> 6.06 ms per step).
 #ifndef AKH_SHAPE_ATTN
 #define AKH_SHAPE_ATTN 4, 8, 2
+#endif
+#ifndef AKH_SHAPE_ATTN_LONG
+#define AKH_SHAPE_ATTN_LONG 8, 8, 2
+#endif
+#ifndef AKH_SHAPE_ATTN_LONG16
+#define AKH_SHAPE_ATTN_LONG16 8, 4, 1
 #endif
 namespace {
 template <int AW_, int RB_, int SP_>
@@ -1219,14 +1230,29 @@ struct AttnShape {
   static constexpr int AW = AW_, RB = RB_, SP = SP_;
 };
 using AttnCfg = AttnShape<AKH_SHAPE_ATTN>;
-static_assert(AttnCfg::SP <= kMaxAttnSplits, "too many attention splits");
+using AttnLong = AttnShape<AKH_SHAPE_ATTN_LONG>;
+using AttnLong16 = AttnShape<AKH_SHAPE_ATTN_LONG16>;
+static_assert(AttnCfg::SP <= kMaxAttnSplits && AttnLong::SP <= kMaxAttnSplits &&
+                  AttnLong16::SP <= kMaxAttnSplits,
+              "too many attention splits");
+bool attn_long(int batch, int heads, long max_ctx) {
+  return max_ctx >= 1024 && (long)batch * heads >= 512;
+}
 }  // namespace
 
-int dec_attn_splits() { return AttnCfg::SP; }
+int dec_attn_splits(int batch, int heads, long max_ctx, bool kv16) {
+  if (!attn_long(batch, heads, max_ctx)) return AttnCfg::SP;
+  return kv16 ? AttnLong16::SP : AttnLong::SP;
+}
+int dec_attn_max_splits() {
+  return std::max(AttnCfg::SP, std::max(AttnLong::SP, AttnLong16::SP));
+}
 
-hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
-                           hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
-  constexpr int AW = AttnCfg::AW, RB = AttnCfg::RB, SP = AttnCfg::SP;
+namespace {
+template <class SH>
+hipError_t launch_dec_attn_shape(const DecAttnParams& p, int batch, int hd,
+                                 hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
+  constexpr int AW = SH::AW, RB = SH::RB, SP = SH::SP;
   // Row groups in flight for a bfloat16 cache (config 5: 8 beat 16, 24, 32).
 #ifndef AKH_ATTN_KV16_RB
 #define AKH_ATTN_KV16_RB RB
@@ -1264,6 +1290,16 @@ hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
 #undef AKH_ATTN
 #undef AKH_ATTN_GO
   return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
+                           hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
+  if (p.d <= 0 || p.H <= 0) return hipErrorInvalidValue;
+  if (!attn_long(batch, p.H, p.seq_stride / p.d))
+    return launch_dec_attn_shape<AttnCfg>(p, batch, hd, s, t0, t1);
+  return p.kv16 ? launch_dec_attn_shape<AttnLong16>(p, batch, hd, s, t0, t1)
+                : launch_dec_attn_shape<AttnLong>(p, batch, hd, s, t0, t1);
 }
 
 // act = silu(sum of the partial tiles), four elements per thread.

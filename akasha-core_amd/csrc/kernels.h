@@ -276,8 +276,12 @@ struct DecAttnParams {
 hipError_t launch_silu_sum(const float* parts, int nparts, float* act, size_t n,
                            hipStream_t s);
 
-// Splits per (sequence, head): the partial states the out_proj GEMM merges.
-int dec_attn_splits();
+// Splits per (sequence, head): the partial states the out_proj GEMM merges,
+// for a session of `batch` sequences, `heads` heads and context max_ctx
+// (launch_dec_attn picks the same launch shape from the same facts), and
+// the most any session uses (the size of its split buffers).
+int dec_attn_splits(int batch, int heads, long max_ctx, bool kv16);
+int dec_attn_max_splits();
 // Prefill rows k, v [rows, d] (fp32) into a bfloat16 KV cache (sequence b
 // at b * seq_stride, position t at t * d): row = b * S + t, or, for ragged
 // prompts packed back to back, (b, t) = rowmap[row].

@@ -1174,7 +1174,7 @@ hipError_t enqueue_out(akh_session* s, uint32_t l) {
   const akh_model_config& c = s->m->cfg;
   DecGemmParams p = dec_base(s);
   p.xt = s->attn_t;
-  p.nparts = dec_attn_splits();
+  p.nparts = dec_attn_splits((int)s->B, (int)c.num_heads, (long)s->max_ctx, s->kv16);
   p.ml = s->attn_ml;
   p.hd = (int)(c.dim / c.num_heads);
   use_packed(p, s->m->packed_layer(l, W_OUT));
@@ -1502,8 +1502,8 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
   if (decode) {
   alloc((void**)&s->xt, R * d * 4);
   alloc((void**)&s->xnt, R * d * 4);
-  alloc((void**)&s->attn_t, (size_t)dec_attn_splits() * R * d * 4);
-  alloc((void**)&s->attn_ml, (size_t)dec_attn_splits() * c.num_heads * R * sizeof(float2));
+  alloc((void**)&s->attn_t, (size_t)dec_attn_max_splits() * R * d * 4);
+  alloc((void**)&s->attn_ml, (size_t)dec_attn_max_splits() * c.num_heads * R * sizeof(float2));
   alloc((void**)&s->p_qkv, (size_t)s->ks_qkv * R * 3 * d * 4);
   alloc((void**)&s->p_out, (size_t)s->ks_out * R * d * 4);
   alloc((void**)&s->p_up, (size_t)s->ks_up * R * F * 4);
