@@ -10,8 +10,9 @@ size-independent properties:
 
 - batch invariance inside the 64-sequence decode at KV length 2048 (two
   32-row tiles, one weight read): a sequence's logits and tokens equal the
-  same prompt decoded alone;
-- bfloat16 weight tiles against float tiles of the same values at KV 2048;
+  same prompt decoded alone, with the f32 and with the bfloat16 KV cache;
+- bfloat16 weight tiles against float tiles of the same values at KV 2048,
+  and the fused residual add + RMSNorm against the default;
 - the 8 x 2048 prefill on the split-bf16 kernels against the fp32-MFMA
   kernels;
 - prefill == sequential decode (inference.rs:334-359): a 2048-token prefill
@@ -68,8 +69,9 @@ def test_scaled_decode_64_rows_at_kv_2048(pkg, scaled):
     for i, ((a, ta), (b, tb)) in enumerate(zip(run[1:], f32)):
         assert np.abs(a - b).max() < 1e-4, f"step {i}"
         assert np.array_equal(ta, tb), f"step {i}"
-    # The residual adds + RMSNorms folded into the GEMMs (32 K splits of
-    # ffn_down summed by the last block of each column tile), same steps.
+    # The residual adds + RMSNorms folded into the GEMMs (the K splits of
+    # out_proj and ffn_down summed by the last block of each column tile),
+    # the same steps.
     s.set_fused_norm(True)
     try:
         s.truncate(S)
@@ -79,6 +81,31 @@ def test_scaled_decode_64_rows_at_kv_2048(pkg, scaled):
     for i, ((a, ta), (b, tb)) in enumerate(zip(run[1:], fused)):
         assert np.abs(a - b).max() < 1e-4, f"fused norm, step {i}"
         assert np.array_equal(ta, tb), f"fused norm, step {i}"
+    s.close()
+
+
+def test_scaled_decode_64_rows_bf16_kv_at_kv_2048(pkg, scaled):
+    # The bfloat16 KV cache at full shape: the 64-sequence session decodes
+    # with the long-context attention shape (8 waves, one row split), a
+    # single sequence with the short one (4 waves, two splits).  The prefill
+    # GEMMs tile the two sessions' rows differently, so an fp32 K or V
+    # value may round to a neighbouring bfloat16 in the cache: the bound is
+    # 2e-3, well inside the bf16 path's 2e-2 against the oracle.
+    cfg, model = scaled
+    hip = pkg.hip
+    B, S, steps = 64, 2040, 4
+    toks = pkg.synthetic_tokens(B * S, cfg.vocab_size, seed=10).reshape(B, S)
+    s = hip.Session(model, 2048, B)
+    s.set_kv_bf16(True)
+    run = [s.prefill(toks)] + _decode(s, steps)
+    for b in (0, 40):
+        one = hip.Session(model, 2048, 1)
+        one.set_kv_bf16(True)
+        alone = [one.prefill(toks[b][None])] + _decode(one, steps)
+        for i, ((lg, tk), (l1, t1)) in enumerate(zip(run, alone)):
+            assert np.abs(lg[b] - l1[0]).max() < 2e-3, f"sequence {b} step {i}"
+            assert int(tk[b]) == int(t1[0]), f"sequence {b} step {i}"
+        one.close()
     s.close()
 
 
