@@ -325,7 +325,10 @@ def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
     return prefill
 
 
-def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=1):
+def cpu_baseline(cfg, weights, prompt_len, budget_s=10.0, max_steps=None, threads=1):
+    """The oracle's decode steps over config 4's window (positions
+    prompt_len..seq_len-1, then back to prompt_len), one sequence, until
+    `budget_s` seconds (or `max_steps` steps) have run.  tok/s, steps, s."""
     ora = entry.load_oracle()
     ora.set_threads(threads)
     s = ora.OracleSession(cfg, weights, cfg.seq_len)
@@ -333,7 +336,10 @@ def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=
     tok = 1
     t0 = time.perf_counter()
     n = 0
-    while n < max_steps and time.perf_counter() - t0 < budget_s:
+    window = cfg.seq_len - prompt_len
+    while (max_steps is None or n < max_steps) and time.perf_counter() - t0 < budget_s:
+        if n and n % window == 0:
+            s.set_len(prompt_len)  # the next window
         logits = s.decode_step(tok)
         tok = ora.argmax(logits)
         n += 1
@@ -343,11 +349,12 @@ def cpu_baseline(cfg, weights, prompt_len, budget_s=12.0, max_steps=64, threads=
     return n / dt, n, dt
 
 
-def cpu_baseline_sequences(cfg, weights, prompt_len, threads, steps=16):
+def cpu_baseline_sequences(cfg, weights, prompt_len, threads, budget_s=8.0):
     """All host cores the way batch-32 decode uses them: `threads` sequences
     decoded at once, one single-threaded oracle session per host thread (the
-    sessions share the weights; ctypes releases the GIL for each call).
-    Aggregate tok/s, (steps per sequence, seconds)."""
+    sessions share the weights; ctypes releases the GIL for each call), each
+    over config 4's window until `budget_s` seconds have run.  Aggregate
+    tok/s, (mean steps per sequence, seconds)."""
     import threading
     ora = entry.load_oracle()
     ora.set_threads(1)
@@ -357,14 +364,20 @@ def cpu_baseline_sequences(cfg, weights, prompt_len, threads, steps=16):
         s.set_len(prompt_len)
         sess.append(s)
     start = threading.Barrier(threads + 1)
+    done = [0] * threads
+    window = cfg.seq_len - prompt_len
 
-    def run(s):
+    def run(i, s):
         start.wait()
-        tok = 1
-        for _ in range(steps):
+        tok, n, t0 = 1, 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s:
+            if n and n % window == 0:
+                s.set_len(prompt_len)
             tok = ora.argmax(s.decode_step(tok))
+            n += 1
+        done[i] = n
 
-    ts = [threading.Thread(target=run, args=(s,)) for s in sess]
+    ts = [threading.Thread(target=run, args=(i, s)) for i, s in enumerate(sess)]
     for t in ts:
         t.start()
     start.wait()
@@ -374,7 +387,7 @@ def cpu_baseline_sequences(cfg, weights, prompt_len, threads, steps=16):
     dt = time.perf_counter() - t0
     for s in sess:
         s.close()
-    return threads * steps / dt, steps, dt
+    return sum(done) / dt, sum(done) / threads, dt
 
 
 def cpu_prefill_baseline(cfg, weights, tokens, threads):
@@ -599,9 +612,9 @@ def main():
         log("bench: CPU baseline (oracle decode step, 1 thread)")
         v1, n1, t1 = cpu_baseline(cfg, w, P, threads=1)
         cpu = {"value": round(v1, 3), "unit": "tok/s", "cores": 1, "kind": "port",
-               "sample": f"oracle decode of 1 sequence, {n1} steps at positions 448.. "
-                         f"({t1:.1f} s), zero KV prefix; the reference CPU backend runs "
-                         f"one sequence per session"}
+               "sample": f"oracle decode of 1 sequence, {n1} steps over config 4's window "
+                         f"(positions 448..511, repeated; {t1:.1f} s), zero KV prefix; the "
+                         f"reference CPU backend runs one sequence per session"}
         aff, quota = cpu_limits()
         # The box's CPU share is 16 (its OMP_NUM_THREADS), whatever nproc says.
         nt = max(1, min(16, aff, int(quota) if quota else 16))
@@ -609,23 +622,23 @@ def main():
         vN, nN, tN = cpu_baseline_sequences(cfg, w, P, nt)
         cpu_omp = {"value": round(vN, 3), "unit": "tok/s", "cores": nt, "kind": "port",
                    "sample": f"{nt} sequences decoded at once, one oracle session per host "
-                             f"thread, {nN} steps each at positions 448.. ({tN:.1f} s); "
+                             f"thread, {nN:.0f} steps each over config 4's window ({tN:.1f} s); "
                              f"batch-32 decode over all host cores"}
         # The column-split OpenMP GEMV of one sequence, for comparison: the
         # reference's per-sequence path with its matmuls spread over threads.
         vO, nO, tO = cpu_baseline(cfg, w, P, budget_s=4.0, max_steps=32, threads=nt)
         cpu_omp["one_sequence_omp"] = {"value": round(vO, 3), "threads": nt, "steps": nO,
                                        "seconds": round(tO, 2)}
-        # A labelled prefill slice: one 64-token prompt of config 3's seed.
-        log(f"bench: CPU baseline (oracle prefill of 64 tokens, {nt} threads)")
-        ptok = pkg.synthetic_tokens(16 * 512, cfg.vocab_size, seed=3)[:64]
+        # A labelled prefill slice: config 3's sequence 0 (512 tokens).
+        log(f"bench: CPU baseline (oracle prefill of 512 tokens, {nt} threads)")
+        ptok = pkg.synthetic_tokens(16 * 512, cfg.vocab_size, seed=3)[:512]
         vp, tp = cpu_prefill_baseline(cfg, w, ptok, nt)
         cname, ncpu = host_cpu()
         cpu["host"] = cpu_omp["host"] = {"cpu_model": cname, "nproc": ncpu,
                                          "affinity_cpus": aff, "cgroup_cpu_quota": quota}
         cpu_omp["prefill"] = {"value": round(vp, 2), "unit": "tok/s", "cores": nt,
-                              "sample": f"oracle prefill of the first 64 tokens of config 3's "
-                                        f"sequence 0, column-split OpenMP ({tp:.1f} s)"}
+                              "sample": f"oracle prefill of config 3's sequence 0 (512 "
+                                        f"tokens), column-split OpenMP ({tp:.1f} s)"}
     else:
         cpu_omp = None
 
