@@ -96,6 +96,41 @@ __device__ __forceinline__ void split3_rne(float4 x0, float4 x1, uint4& hi, uint
   lo = make_uint4(pl[0], pl[1], pl[2], pl[3]);
 }
 
+// fp16 operands of v_mfma_f32_32x32x16_f16, laid out as mfma_bf16's.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x16 mfma_f16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f16x8 f16x8_of(uint4 v) { return __builtin_bit_cast(f16x8, v); }
+
+// Two floats as packed fp16, round to nearest even.
+__device__ __forceinline__ uint32_t cvt_pk_f16(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const f2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+}
+
+// Eight floats as two fp16 octets with x = hi + 2^-11 lo to within 2^-22 |x|
+// (the scaled-residual split of Ootomo and Yokota, IJHPCA 2022): hi rounds x
+// to 11 significant bits, the remainder x - hi is exact and at most 2^-11 |x|,
+// and lo rounds it scaled by 2^11.  Below fp16's normal range hi is
+// subnormal, which the fp16 MFMAs take exactly (checked on gfx950), and lo
+// still carries the remainder; |x| >= 65520 gives an infinite hi.
+__device__ __forceinline__ void split2_f16(float4 x0, float4 x1, uint4& hi, uint4& lo) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  uint32_t ph[4], pl[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ph[i] = cvt_pk_f16(v[2 * i], v[2 * i + 1]);
+    const h2 hv = __builtin_bit_cast(h2, ph[i]);
+    pl[i] = cvt_pk_f16((v[2 * i] - (float)hv[0]) * 2048.f, (v[2 * i + 1] - (float)hv[1]) * 2048.f);
+  }
+  hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+  lo = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll

@@ -100,8 +100,12 @@ struct GemmParams {
   // and A either in bfloat16 (a16) or fp32 (a, split into hi + lo parts).
   const uint16_t* a16;   // [M, K]
   const uint16_t* bt16;  // [N, K]
-  // launch_gemm_x6: the transposed fp32 weights.
+  // launch_gemm_x6 / launch_gemm_h3: the transposed fp32 weights.
   const float* bt;  // [N, K]
+  // launch_gemm_h3: the weights' fp16 planes (launch_split_weights_f16),
+  // and a flag set to 1 when a result is not finite.
+  const uint16_t* bp16;
+  int* range_flag;
   // GEMM_QKV on ragged prompts packed back to back: row m is position
   // rowmap[m].y of sequence rowmap[m].x (instead of m / S, m % S).
   const int2* rowmap;
@@ -150,6 +154,13 @@ hipError_t launch_transpose_bf16(const float* w, int K, int N, uint16_t* wt, hip
 // transposed fp32 weights (p.bt, [N, K]) enter as three bfloat16 terms
 // each, six products accumulated in fp32.  K % 8 == 0.
 hipError_t launch_gemm_x6(const GemmParams& p, int epi, hipStream_t s);
+// fp32-accurate GEMM on fp16 MFMAs: A (p.a, fp32 [M, K]) split into two fp16
+// terms as it is staged, the weights' fp16 planes (p.bp16), three products
+// per multiply-add.  Sets *p.range_flag when a result is not finite (an
+// operand beyond fp16's range); the caller then recomputes in fp32.  K % 8 == 0.
+hipError_t launch_gemm_h3(const GemmParams& p, int epi, hipStream_t s);
+// The fp16 planes of a [K, N] row-major matrix for launch_gemm_h3 (K * N * 4 bytes).
+hipError_t launch_split_weights_f16(const float* w, int K, int N, uint16_t* wp, hipStream_t s);
 // wt[n, k] = w[k, n] for a [K, N] row-major matrix.
 hipError_t launch_transpose_f32(const float* w, int K, int N, float* wt, hipStream_t s);
 // Causal flash attention (head_dim 64 or 128) with bfloat16 QK^T and PV

@@ -644,6 +644,35 @@ __global__ __launch_bounds__(256) void k_transpose_f32(const float* __restrict__
   }
 }
 
+// The fp16 planes of k_gemm_h3's weights: for a [K, N] row-major matrix,
+// wp[((n K/8 + k/8) 2 + p) 8 + k%8] = plane p (0: hi, 1: lo) of w[k, n] as
+// split by split2_f16, so one 32-byte run holds the hi and lo octets of
+// eight consecutive k of column n.  K % 8 == 0.  A 32 x 32 tile through LDS;
+// thread (n, octet) writes its 32 bytes.
+__global__ __launch_bounds__(256) void k_split_weights_f16(const float* __restrict__ w, int K,
+                                                           int N, uint16_t* __restrict__ wp) {
+  __shared__ float t[32][33];
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int c = threadIdx.x & 31, r = threadIdx.x >> 5;
+  for (int i = r; i < 32; i += 8) {
+    const int k = k0 + i, n = n0 + c;
+    t[i][c] = (k < K && n < N) ? w[(size_t)k * N + n] : 0.f;
+  }
+  __syncthreads();
+  if (threadIdx.x >= 128) return;
+  const int nl = threadIdx.x >> 2, q = threadIdx.x & 3;
+  const int n = n0 + nl, k = k0 + 8 * q;
+  if (n >= N || k >= K) return;
+  const float4 x0 = make_float4(t[8 * q][nl], t[8 * q + 1][nl], t[8 * q + 2][nl], t[8 * q + 3][nl]);
+  const float4 x1 =
+      make_float4(t[8 * q + 4][nl], t[8 * q + 5][nl], t[8 * q + 6][nl], t[8 * q + 7][nl]);
+  uint4 hi, lo;
+  split2_f16(x0, x1, hi, lo);
+  uint4* dst = reinterpret_cast<uint4*>(wp + ((size_t)n * (K / 8) + k / 8) * 16);
+  dst[0] = hi;
+  dst[1] = lo;
+}
+
 // C[M,N] = A[M,K] B[K,N] in fp32 accuracy on v_mfma_f32_32x32x16_bf16.
 // A (p.a, [M, K]) and the transposed weights B^T (p.bt, [N, K]) are fp32;
 // each element enters LDS as three bfloat16 terms (split3_rne: a = a1 + a2
@@ -877,6 +906,183 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
       const int n = n0 + wn * 64 + 2 * j;
       epi_pair_gemm<EPI>(p, M, N, m, n, acc[a][0][r], acc[a][1][r]);
     }
+}
+
+// C[M,N] = A[M,K] B[K,N] in fp32 accuracy on v_mfma_f32_32x32x16_f16.  Each
+// fp32 element enters LDS as two fp16 terms (split2_f16: x = hi + 2^-11 lo,
+// to within 2^-22 |x|): A is split while it is staged, the weights once, into
+// fp16 planes (p.bp16, k_split_weights_f16), so their staging is a plain
+// copy.  A product takes three MFMAs: hi.hi into one accumulator, hi.lo +
+// lo.hi into a second, summed as acc + 2^-11 acc' at the end; the dropped
+// lo.lo term is below 2^-22 |a b|.  So a product costs 3 x 32 MFMA cycles per
+// 16 k (6 x 32 on k_gemm_x6) and four LDS fragments (six).  An operand beyond
+// fp16's range (|x| >= 65520) becomes an infinite hi, which makes every sum
+// it enters infinite or NaN: a block with a non-finite result sets
+// *p.range_flag, and the caller recomputes on the fp32 kernels (non-finite
+// inputs flag too, and come out the same there).
+//
+// Block tile BM x BN, BK = 32, waves WM (rows) x WN (columns), each owning
+// (BM / WM) x 64 as TA x 2 MFMA tiles.  Staging reads whole 128-byte lines:
+// piece f of a step is row f / 8, bytes 16 (f % 8) .. + 15 of that row's
+// step, so eight consecutive lanes read one row's line (loads that scatter
+// a wave over 32 rows, as in k_gemm_x6, ran at half the speed: the vector
+// cache serves a wave's lines one by one).  A B row's 128 bytes are the hi
+// and lo planes of its four k-octets, at the byte offset of the same k in
+// an fp32 [N, K] matrix.  LDS holds both planes of both operands k-contiguous
+// (rows of 32 k padded to 80 bytes: 16-byte fragment reads of 8 consecutive
+// rows hit distinct banks), double buffered; the global loads of step s + 2
+// are issued before step s + 1 is stored.  K % 8 == 0.
+template <int EPI, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN, 2) void k_gemm_h3(GemmParams p) {
+  constexpr int BK = 32, LD = BK + 8, NT = 64 * WM * WN, NU = BK / 16;
+  constexpr int TA = BM / WM / 32;
+  static_assert(BN == 64 * WN && BM % (32 * WM) == 0, "wave tiles are (32 TA) x 64");
+  constexpr int PR = BK / 4;  // 16-byte pieces per row and step
+  constexpr int FA = PR * BM / NT, FB = PR * BN / NT;
+  static_assert(FA >= 1 && FB >= 1 && FA * NT == PR * BM && FB * NT == PR * BN,
+                "every thread stages whole pieces of both operands");
+  __shared__ __align__(16) uint16_t As[2][2][BM][LD];
+  __shared__ __align__(16) uint16_t Bs[2][2][BN][LD];
+
+  const int M = p.M, N = p.N, K = p.K;
+  // Each XCD takes a contiguous run of tiles (see k_gemm_bf16).
+  int id = blockIdx.x + gridDim.x * blockIdx.y;
+  const int per_xcd = (int)(gridDim.x * gridDim.y) / 8;
+  if (id < per_xcd * 8) id = (id % 8) * per_xcd + id / 8;
+  const int m0 = (id / gridDim.x) * BM, n0 = (id % gridDim.x) * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int j = lane & 31, h = lane >> 5;
+
+  // Loads go through buffer resources bounded to the block's rows of A and
+  // of the planes: pieces past M or N fall outside them, pieces past K get
+  // an offset outside them, and the hardware returns zeros for both.  B's
+  // LDS row L = 64 g + 32 t + jj holds column 64 g + 2 jj + t of the block
+  // (lane j of column tile t then reads column 2j + t: adjacent column pairs
+  // for the paired epilogues).
+  float4 ra[2][FA], rb[2][FB];
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.a + (size_t)m0 * K), (short)0, min(M - m0, BM) * K * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.bp16 + (size_t)n0 * K * 2), (short)0, min(N - n0, BN) * K * 4,
+      0x00020000);
+  auto ld4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t vo) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, 0, 0));
+    return make_float4(v.x, v.y, v.z, v.w);
+  };
+  auto bcol = [](int L) { return (L & ~63) | ((L & 31) << 1) | ((L >> 5) & 1); };
+  auto gload = [&](int k0, int set) {
+#pragma unroll
+    for (int i = 0; i < FA; ++i) {
+      const int f = tid + NT * i, r = f / PR, q = f % PR;
+      const uint32_t vo = k0 + 4 * q < K ? (uint32_t)(r * K + k0 + 4 * q) * 4u : 0x80000000u;
+      ra[set][i] = ld4(rsa, vo);
+    }
+#pragma unroll
+    for (int i = 0; i < FB; ++i) {
+      // Piece q of a B row: plane q % 2 of k-octet q / 2.
+      const int f = tid + NT * i, L = f / PR, q = f % PR;
+      const uint32_t vo =
+          k0 + 8 * (q >> 1) < K ? (uint32_t)(bcol(L) * K + k0) * 4u + 16u * q : 0x80000000u;
+      rb[set][i] = ld4(rsb, vo);
+    }
+  };
+  auto lstore = [&](int buf, int set) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int i = 0; i < FA; ++i) {
+      const int f = tid + NT * i, r = f / PR, q = f % PR;
+      const float4 x = ra[set][i];
+      const uint32_t h0 = cvt_pk_f16(x.x, x.y), h1 = cvt_pk_f16(x.z, x.w);
+      const h2 a0 = __builtin_bit_cast(h2, h0), a1 = __builtin_bit_cast(h2, h1);
+      const uint32_t l0 = cvt_pk_f16((x.x - (float)a0[0]) * 2048.f, (x.y - (float)a0[1]) * 2048.f);
+      const uint32_t l1 = cvt_pk_f16((x.z - (float)a1[0]) * 2048.f, (x.w - (float)a1[1]) * 2048.f);
+      *reinterpret_cast<uint2*>(&As[buf][0][r][4 * q]) = make_uint2(h0, h1);
+      *reinterpret_cast<uint2*>(&As[buf][1][r][4 * q]) = make_uint2(l0, l1);
+    }
+#pragma unroll
+    for (int i = 0; i < FB; ++i) {
+      const int f = tid + NT * i, L = f / PR, q = f % PR;
+      *reinterpret_cast<float4*>(&Bs[buf][q & 1][L][8 * (q >> 1)]) = rb[set][i];
+    }
+  };
+
+  f32x16 acc[TA][2], cor[TA][2];
+#pragma unroll
+  for (int a = 0; a < TA; ++a)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      acc[a][t] = zero16();
+      cor[a][t] = zero16();
+    }
+  // One step: fragments of both 16-k halves of buffer `buf`, then the MFMAs.
+  auto step = [&](int buf) {
+    f16x8 f[NU][2 + TA][2];  // [0..1]: B column tiles, [2 + a]: A row tiles
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+          f[u][t][pl] = f16x8_of(*reinterpret_cast<const uint4*>(
+              &Bs[buf][pl][wn * 64 + t * 32 + j][16 * u + 8 * h]));
+#pragma unroll
+      for (int a = 0; a < TA; ++a)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+          f[u][2 + a][pl] = f16x8_of(*reinterpret_cast<const uint4*>(
+              &As[buf][pl][wm * (32 * TA) + a * 32 + j][16 * u + 8 * h]));
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+      for (int a = 0; a < TA; ++a) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) cor[a][t] = mfma_f16(f[u][2 + a][1], f[u][t][0], cor[a][t]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) cor[a][t] = mfma_f16(f[u][2 + a][0], f[u][t][1], cor[a][t]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[a][t] = mfma_f16(f[u][2 + a][0], f[u][t][0], acc[a][t]);
+      }
+  };
+
+  // Step s computes on LDS buffer s % 2 after storing step s + 1 (register
+  // set (s + 1) % 2, loaded a step earlier) into the other buffer and issuing
+  // the loads of step s + 2 into set s % 2.  Steps past the end load zeros.
+  const int nk = (K + BK - 1) / BK;
+  gload(0, 0);
+  gload(BK, 1);
+  lstore(0, 0);
+  __syncthreads();
+  auto stepk = [&](int s, int buf) {
+    __builtin_amdgcn_sched_barrier(0);
+    gload((s + 2) * BK, buf);
+    __builtin_amdgcn_sched_barrier(0);
+    lstore(1 - buf, 1 - buf);
+    step(buf);
+    __syncthreads();
+  };
+  int s = 0;
+  for (; s + 2 <= nk; s += 2) {
+    stepk(s, 0);
+    stepk(s + 1, 1);
+  }
+  if (s < nk) stepk(s, 0);
+
+  bool finite = true;
+#pragma unroll
+  for (int a = 0; a < TA; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wm * (32 * TA) + a * 32 + acc_row(r, h);
+      const int n = n0 + wn * 64 + 2 * j;
+      const float v0 = acc[a][0][r] + cor[a][0][r] * 0x1p-11f;
+      const float v1 = acc[a][1][r] + cor[a][1][r] * 0x1p-11f;
+      finite = finite && __builtin_isfinite(v0) && __builtin_isfinite(v1);
+      epi_pair_gemm<EPI>(p, M, N, m, n, v0, v1);
+    }
+  if (!finite) *p.range_flag = 1;
 }
 
 // Causal flash attention with bfloat16 MFMAs (head_dim 64 or 128), the
@@ -1634,10 +1840,44 @@ hipError_t launch_gemm_x6(const GemmParams& p, int epi, hipStream_t s) {
   return hipGetLastError();
 }
 
+hipError_t launch_gemm_h3(const GemmParams& p, int epi, hipStream_t s) {
+  // K bounded so a block's rows (at most 256 of K floats) fit a buffer
+  // resource's 32-bit byte range.
+  if (p.K % 8 != 0 || p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K > (1 << 20) || !p.a || !p.bp16 ||
+      !p.range_flag)
+    return hipErrorInvalidValue;
+  // 256 x 128 tiles when there are at least four per CU, else 128 x 128
+  // (fewer idle CUs on the last round); measured on MI355X.
+  const bool big = (long)((p.M + 255) / 256) * ((p.N + 127) / 128) >= 1024;
+#define AKH_H3_GO(E)                                                                        \
+  if (big)                                                                                  \
+    hipLaunchKernelGGL((k_gemm_h3<E, 256, 128, 4, 2>),                                      \
+                       dim3((p.N + 127) / 128, (p.M + 255) / 256), dim3(512), 0, s, p);      \
+  else                                                                                      \
+    hipLaunchKernelGGL((k_gemm_h3<E, 128, 128, 2, 2>),                                      \
+                       dim3((p.N + 127) / 128, (p.M + 127) / 128), dim3(256), 0, s, p);
+  switch (epi) {
+    case GEMM_STORE: AKH_H3_GO(GEMM_STORE) break;
+    case GEMM_ADD: AKH_H3_GO(GEMM_ADD) break;
+    case GEMM_SILU: AKH_H3_GO(GEMM_SILU) break;
+    case GEMM_QKV: AKH_H3_GO(GEMM_QKV) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef AKH_H3_GO
+  return hipGetLastError();
+}
+
 hipError_t launch_transpose_f32(const float* w, int K, int N, float* wt, hipStream_t s) {
   if (K <= 0 || N <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_transpose_f32, dim3((N + 31) / 32, (K + 31) / 32), dim3(256), 0, s, w, K,
                      N, wt);
+  return hipGetLastError();
+}
+
+hipError_t launch_split_weights_f16(const float* w, int K, int N, uint16_t* wp, hipStream_t s) {
+  if (K <= 0 || N <= 0 || K % 8 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_split_weights_f16, dim3((N + 31) / 32, (K + 31) / 32), dim3(256), 0, s, w,
+                     K, N, wp);
   return hipGetLastError();
 }
 

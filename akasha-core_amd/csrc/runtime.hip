@@ -565,11 +565,16 @@ struct akh_model {
   bool allow_bf16 = true;            // bfloat16 tiles where every value is one
   bool prefill_bf16 = false;         // the optional bfloat16-MFMA prefill
   std::vector<uint16_t*> wt16;       // per parameter: bf16 [N, K] copy (layer matrices)
-  // The prefill GEMMs on split-bfloat16 MFMAs (fp32 accuracy, on by default
-  // where dim and ffn_hidden are multiples of 8): transposed fp32 [N, K]
-  // copies of the layer matrices and lm_head.
-  bool prefill_x6 = false;
-  std::vector<float*> wt32;
+  // The f32 prefill's layer GEMMs (and the trainer forward's lm_head) on
+  // split operands, fp32-accurate: SPLIT_NONE runs the fp32-MFMA kernels,
+  // SPLIT_X6 three bfloat16 terms per operand (k_gemm_x6, on transposed fp32
+  // [N, K] copies), SPLIT_H3 two fp16 terms (k_gemm_h3, on fp16 planes), the
+  // default where dim and ffn_hidden are multiples of 8.  wsplit holds the
+  // copies per parameter (layer matrices and lm_head); flash attention runs
+  // split-bfloat16 under either split.
+  int prefill_split = AKH_SPLIT_NONE;
+  std::vector<void*> wsplit;
+  int* range_flag = nullptr;  // set by k_gemm_h3 on a non-finite result
   uint64_t layout_gen = 0;           // bumped when a packed matrix changes element type
 
   float* embedding() const { return params[0]; }
@@ -595,40 +600,53 @@ extern "C" void akh_model_free(akh_model* m) {
   if (m->bf16_flag) hipFree(m->bf16_flag);
   for (uint16_t* p : m->wt16)
     if (p) hipFree(p);
-  for (float* p : m->wt32)
+  for (void* p : m->wsplit)
     if (p) hipFree(p);
   delete m;
 }
 
 namespace {
 
-bool x6_capable(const akh_model_config& c) { return c.dim % 8 == 0 && c.ffn_hidden % 8 == 0; }
+bool split_capable(const akh_model_config& c) { return c.dim % 8 == 0 && c.ffn_hidden % 8 == 0; }
 
-// Allocates (zeroed) or frees the transposed fp32 copies used by the
-// split-bfloat16 prefill GEMMs; `transpose` fills them from the parameters.
-akh_status set_x6(akh_model* m, bool enable, bool transpose) {
+// The split kernels' copy of parameter `index` from the parameter itself.
+hipError_t fill_split(akh_model* m, uint32_t index, hipStream_t st) {
+  const PackedMatrix& pm = m->packed[index];
+  if (m->prefill_split == AKH_SPLIT_X6)
+    return launch_transpose_f32(m->params[index], pm.K, pm.N, static_cast<float*>(m->wsplit[index]),
+                                st);
+  return launch_split_weights_f16(m->params[index], pm.K, pm.N,
+                                  static_cast<uint16_t*>(m->wsplit[index]), st);
+}
+
+// Frees the split copies and allocates (zeroed) those of `kind`; `fill`
+// fills them from the parameters (else their uploads do).
+akh_status set_split(akh_model* m, int kind, bool fill) {
   HIP_TRY(hipSetDevice(m->be->device));
   HIP_TRY(hipStreamSynchronize(m->be->stream));
-  for (float*& p : m->wt32)
+  for (void*& p : m->wsplit)
     if (p) {
       HIP_TRY(hipFree(p));
       p = nullptr;
     }
-  m->prefill_x6 = false;
-  if (!enable) return AKH_OK;
-  m->wt32.assign(m->params.size(), nullptr);
-  for (size_t i = 0; i < m->packed.size(); ++i) {
+  m->prefill_split = AKH_SPLIT_NONE;
+  if (kind == AKH_SPLIT_NONE) return AKH_OK;
+  m->wsplit.assign(m->params.size(), nullptr);
+  m->prefill_split = kind;
+  for (uint32_t i = 0; i < m->packed.size(); ++i) {
     const PackedMatrix& pm = m->packed[i];
     if (!pm.rows) continue;
+    // Both copies take 4 bytes per element: an fp32 value, or two fp16 terms.
     void* p = nullptr;
-    akh_status st = akh_tensor_alloc(m->be, (size_t)pm.K * pm.N * sizeof(float), &p);
-    if (st != AKH_OK) return st;
-    m->wt32[i] = static_cast<float*>(p);
-    if (transpose)
-      HIP_TRY(launch_transpose_f32(m->params[i], pm.K, pm.N, m->wt32[i], m->be->stream));
+    akh_status st = akh_tensor_alloc(m->be, (size_t)pm.K * pm.N * 4, &p);
+    if (st != AKH_OK) {
+      set_split(m, AKH_SPLIT_NONE, false);
+      return st;
+    }
+    m->wsplit[i] = p;
+    if (fill) HIP_TRY(fill_split(m, i, m->be->stream));
   }
   HIP_TRY(hipStreamSynchronize(m->be->stream));
-  m->prefill_x6 = true;
   return AKH_OK;
 }
 
@@ -698,15 +716,16 @@ extern "C" akh_status akh_model_new(akh_backend* be,
   }
   {
     void* p = nullptr;
-    akh_status st = akh_tensor_alloc(be, sizeof(int), &p);
+    akh_status st = akh_tensor_alloc(be, 2 * sizeof(int), &p);
     if (st != AKH_OK) {
       akh_model_free(m);
       return st;
     }
     m->bf16_flag = static_cast<int*>(p);
+    m->range_flag = m->bf16_flag + 1;
   }
-  if (x6_capable(c)) {
-    akh_status st = set_x6(m, true, false);  // filled as parameters are uploaded
+  if (split_capable(c)) {
+    akh_status st = set_split(m, AKH_SPLIT_H3, false);  // filled as parameters are uploaded
     if (st != AKH_OK) {
       akh_model_free(m);
       return st;
@@ -749,8 +768,7 @@ akh_status repack(akh_model* m, uint32_t index) {
   HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, bf16, st));
   if (index < m->wt16.size() && m->wt16[index])
     HIP_TRY(launch_transpose_bf16(m->params[index], pm.K, pm.N, m->wt16[index], st));
-  if (index < m->wt32.size() && m->wt32[index])
-    HIP_TRY(launch_transpose_f32(m->params[index], pm.K, pm.N, m->wt32[index], st));
+  if (index < m->wsplit.size() && m->wsplit[index]) HIP_TRY(fill_split(m, index, st));
   HIP_TRY(hipStreamSynchronize(st));
   if (bf16 != pm.bf16) {
     pm.bf16 = bf16;
@@ -794,13 +812,23 @@ extern "C" akh_status akh_model_set_prefill_bf16(akh_model* m, int enable) {
   return AKH_OK;
 }
 
+extern "C" akh_status akh_model_set_prefill_split(akh_model* m, int kind) {
+  CHECK_ARG(m && (kind == AKH_SPLIT_NONE || kind == AKH_SPLIT_X6 || kind == AKH_SPLIT_H3),
+            "akh_model_set_prefill_split: bad argument");
+  CHECK_ARG(!m->be->capturing, "akh_model_set_prefill_split: graph capture in progress");
+  CHECK_ARG(kind == AKH_SPLIT_NONE || split_capable(m->cfg),
+            "akh_model_set_prefill_split: needs dim and ffn_hidden multiples of 8");
+  if (kind == m->prefill_split) return AKH_OK;
+  return set_split(m, kind, true);
+}
+
+extern "C" int akh_model_prefill_split(const akh_model* m) {
+  return m ? m->prefill_split : AKH_SPLIT_NONE;
+}
+
 extern "C" akh_status akh_model_set_prefill_x6(akh_model* m, int enable) {
   CHECK_ARG(m && (enable == 0 || enable == 1), "akh_model_set_prefill_x6: bad argument");
-  CHECK_ARG(!m->be->capturing, "akh_model_set_prefill_x6: graph capture in progress");
-  CHECK_ARG(!enable || x6_capable(m->cfg),
-            "akh_model_set_prefill_x6: needs dim and ffn_hidden multiples of 8");
-  if ((enable != 0) == m->prefill_x6) return AKH_OK;
-  return set_x6(m, enable != 0, true);
+  return akh_model_set_prefill_split(m, enable ? AKH_SPLIT_X6 : AKH_SPLIT_NONE);
 }
 
 extern "C" akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16) {
@@ -1593,15 +1621,39 @@ extern "C" akh_status akh_session_truncate(akh_session* s, uint32_t len) {
 
 namespace {
 
-// A prefill GEMM on parameter `index`: the split-bfloat16 kernel on its
-// transposed copy when the model has it, else the fp32-MFMA kernel.
+// A prefill GEMM on parameter `index`: the model's split kernel on its copy
+// of the matrix, or the fp32-MFMA kernel (no copy, or `exact`).
 hipError_t prefill_gemm(const akh_model* m, GemmParams& g, uint32_t index, int epi,
-                        hipStream_t st) {
-  if (m->prefill_x6 && index < m->wt32.size() && m->wt32[index]) {
-    g.bt = m->wt32[index];
-    return launch_gemm_x6(g, epi, st);
+                        hipStream_t st, bool exact) {
+  if (!exact && index < m->wsplit.size() && m->wsplit[index]) {
+    if (m->prefill_split == AKH_SPLIT_X6) {
+      g.bt = static_cast<const float*>(m->wsplit[index]);
+      return launch_gemm_x6(g, epi, st);
+    }
+    g.bp16 = static_cast<const uint16_t*>(m->wsplit[index]);
+    g.range_flag = m->range_flag;
+    return launch_gemm_h3(g, epi, st);
   }
   return launch_gemm(g, epi, st);
+}
+
+// Whether the f32 prefill runs k_gemm_h3, whose range flag then needs a
+// check (and, if set, an exact rerun).
+bool h3_prefill(const akh_model* m) {
+  return m->prefill_split == AKH_SPLIT_H3 && !m->prefill_bf16;
+}
+
+hipError_t clear_range_flag(const akh_model* m, hipStream_t st) {
+  return hipMemsetAsync(m->range_flag, 0, sizeof(int), st);
+}
+
+// Waits for the stream and reads the range flag.
+hipError_t range_flag_set(const akh_model* m, hipStream_t st, bool* set) {
+  int v = 0;
+  hipError_t e = hipMemcpyAsync(&v, m->range_flag, sizeof(int), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  *set = v != 0;
+  return e;
 }
 
 // The rows of one prefill.  Uniform prompts of length S keep the layout
@@ -1613,8 +1665,9 @@ struct PrefillRows {
   bool ragged = false;
 };
 
-// The prefill layers in fp32 (build_prefill_layer's node order).
-hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr) {
+// The prefill layers in fp32 (build_prefill_layer's node order); `exact`
+// runs them on the fp32-MFMA kernels whatever the model's split kernels.
+hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr, bool exact) {
   const akh_model_config& c = s->m->cfg;
   const uint32_t d = c.dim, hd = d / c.num_heads, S = pr.S;
   const size_t rows = pr.rows;
@@ -1647,7 +1700,7 @@ hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr) {
     g.dim = d;
     g.head_dim = hd;
     const uint32_t base = 1 + 6 * l;
-    TRY_HIP(prefill_gemm(s->m, g, base + W_QKV, GEMM_QKV, st));
+    TRY_HIP(prefill_gemm(s->m, g, base + W_QKV, GEMM_QKV, st, exact));
     if (s->kv16)
       TRY_HIP(launch_kv_store_bf16(s->pk, s->pv, static_cast<uint16_t*>(s->kv_at(l, 0)),
                                    static_cast<uint16_t*>(s->kv_at(l, 1)), rows, (int)S,
@@ -1667,7 +1720,7 @@ hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr) {
     f.d = (int)d;
     f.hd = (int)hd;
     f.scale = 1.0f / sqrtf((float)hd);
-    f.x6 = s->m->prefill_x6 ? 1 : 0;
+    f.x6 = s->m->prefill_split != AKH_SPLIT_NONE && !exact ? 1 : 0;
     TRY_HIP(launch_flash(f, (int)s->B, (int)S, st));
 
     GemmParams o{};
@@ -1677,7 +1730,7 @@ hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr) {
     o.M = (int)rows;
     o.N = d;
     o.K = d;
-    TRY_HIP(prefill_gemm(s->m, o, base + W_OUT, GEMM_ADD, st));
+    TRY_HIP(prefill_gemm(s->m, o, base + W_OUT, GEMM_ADD, st, exact));
 
     TRY_HIP(launch_rows_rmsnorm(s->px, s->m->layer(l, W_NORM2), s->pxn,
                                 (int)rows, (int)d, c.norm_eps, st));
@@ -1688,7 +1741,7 @@ hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr) {
     u.M = (int)rows;
     u.N = c.ffn_hidden;
     u.K = d;
-    TRY_HIP(prefill_gemm(s->m, u, base + W_UP, GEMM_SILU, st));
+    TRY_HIP(prefill_gemm(s->m, u, base + W_UP, GEMM_SILU, st, exact));
 
     GemmParams w{};
     w.a = s->pffn;
@@ -1697,7 +1750,7 @@ hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr) {
     w.M = (int)rows;
     w.N = d;
     w.K = c.ffn_hidden;
-    TRY_HIP(prefill_gemm(s->m, w, base + W_DOWN, GEMM_ADD, st));
+    TRY_HIP(prefill_gemm(s->m, w, base + W_DOWN, GEMM_ADD, st, exact));
   }
 #undef TRY_HIP
   return hipSuccess;
@@ -1867,13 +1920,24 @@ akh_status prefill_impl(akh_session* s, const uint32_t* tokens, const uint32_t* 
                              hipMemcpyDeviceToDevice, st));
   }
 
-  HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
-                                (int)d, c.vocab_size, st));
   PrefillRows pr;
   pr.rows = rows;
   pr.S = S;
   pr.ragged = ragged;
-  HIP_TRY(s->m->prefill_bf16 ? prefill_layers_bf16(s, pr) : prefill_layers_f32(s, pr));
+  const bool h3 = h3_prefill(s->m);
+  if (h3) HIP_TRY(clear_range_flag(s->m, st));
+  HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
+                                (int)d, c.vocab_size, st));
+  HIP_TRY(s->m->prefill_bf16 ? prefill_layers_bf16(s, pr) : prefill_layers_f32(s, pr, false));
+  bool redo = false;
+  if (h3) HIP_TRY(range_flag_set(s->m, st, &redo));
+  if (redo) {
+    // An operand beyond fp16's range: the same layers on the fp32 kernels
+    // (they rewrite every row and cache entry the first pass wrote).
+    HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
+                                  (int)d, c.vocab_size, st));
+    HIP_TRY(prefill_layers_f32(s, pr, true));
+  }
   // Last row of every sequence -> final RMSNorm -> lm_head -> greedy token
   // (inference.rs:120-168).
   {
@@ -2451,22 +2515,35 @@ extern "C" akh_status akh_forward_loss(akh_forward* f, const uint32_t* tokens,
   hipStream_t st = s->be->stream;
   HIP_TRY(hipMemcpyAsync(s->ptok, tokens, rows * 4, hipMemcpyHostToDevice, st));
   HIP_TRY(hipMemcpyAsync(f->targets, targets, rows * 4, hipMemcpyHostToDevice, st));
-  HIP_TRY(launch_embedding_rows(s->ptok, f->m->embedding(), s->px, (int)rows, (int)d, V, st));
   PrefillRows pr;
   pr.rows = rows;
   pr.S = S;
-  HIP_TRY(f->m->prefill_bf16 ? prefill_layers_bf16(s, pr) : prefill_layers_f32(s, pr));
-  // final_norm and lm_head on every row (train.rs:154-177), then the loss.
-  HIP_TRY(launch_rows_rmsnorm(s->px, f->m->final_norm(), s->pxn, (int)rows, (int)d, c.norm_eps,
-                              st));
-  GemmParams g{};
-  g.a = s->pxn;
-  g.b = f->m->lm_head();
-  g.c = f->logits;
-  g.M = (int)rows;
-  g.N = (int)V;
-  g.K = (int)d;
-  HIP_TRY(prefill_gemm(f->m, g, 2 + 6 * c.num_layers, GEMM_STORE, st));
+  const bool h3 = h3_prefill(f->m);
+  // The layers, final_norm and lm_head on every row (train.rs:154-177).
+  auto forward = [&](bool exact) -> hipError_t {
+    hipError_t e = launch_embedding_rows(s->ptok, f->m->embedding(), s->px, (int)rows, (int)d,
+                                         V, st);
+    if (e == hipSuccess)
+      e = f->m->prefill_bf16 ? prefill_layers_bf16(s, pr) : prefill_layers_f32(s, pr, exact);
+    if (e == hipSuccess)
+      e = launch_rows_rmsnorm(s->px, f->m->final_norm(), s->pxn, (int)rows, (int)d, c.norm_eps,
+                              st);
+    GemmParams g{};
+    g.a = s->pxn;
+    g.b = f->m->lm_head();
+    g.c = f->logits;
+    g.M = (int)rows;
+    g.N = (int)V;
+    g.K = (int)d;
+    if (e == hipSuccess) e = prefill_gemm(f->m, g, 2 + 6 * c.num_layers, GEMM_STORE, st, exact);
+    return e;
+  };
+  if (h3) HIP_TRY(clear_range_flag(f->m, st));
+  HIP_TRY(forward(false));
+  bool redo = false;
+  if (h3) HIP_TRY(range_flag_set(f->m, st, &redo));
+  if (redo) HIP_TRY(forward(true));  // an operand beyond fp16's range
+  // The loss.
   HIP_TRY(launch_cross_entropy(f->logits, f->targets, f->losses, (uint32_t)rows, f->ce, st));
   std::vector<float> l(rows);
   HIP_TRY(hipMemcpyAsync(l.data(), f->losses, rows * 4, hipMemcpyDeviceToHost, st));

@@ -207,6 +207,8 @@ _SIGS = {
     "akh_model_set_bf16_tiles": (ST, [P, C.c_int, P]),
     "akh_model_set_prefill_bf16": (ST, [P, C.c_int]),
     "akh_model_set_prefill_x6": (ST, [P, C.c_int]),
+    "akh_model_set_prefill_split": (ST, [P, C.c_int]),
+    "akh_model_prefill_split": (C.c_int, [P]),
     "akh_checkpoint_info": (ST, [C.c_char_p, C.POINTER(CheckpointInfo)]),
     "akh_model_load_checkpoint": (ST, [P, C.c_char_p, C.POINTER(C.c_uint64),
                                        C.POINTER(C.c_int)]),
@@ -556,10 +558,20 @@ class Model:
                "set_bf16_tiles")
         return n.value
 
+    SPLIT_NONE, SPLIT_X6, SPLIT_H3 = 0, 1, 2
+
+    def set_prefill_split(self, kind: int):
+        """Kernels of the f32 prefill GEMMs, all fp32-accurate: SPLIT_H3 (two
+        fp16 terms per operand, three products; the default where dim and
+        ffn_hidden are multiples of 8), SPLIT_X6 (three bfloat16 terms, six
+        products) or SPLIT_NONE (the fp32 MFMAs)."""
+        _check(_lib.akh_model_set_prefill_split(self.handle, int(kind)), "set_prefill_split")
+
+    def prefill_split(self) -> int:
+        return int(_lib.akh_model_prefill_split(self.handle))
+
     def set_prefill_x6(self, enable: bool):
-        """Prefill GEMMs on split-bfloat16 MFMAs (fp32 accuracy; the default
-        where dim and ffn_hidden are multiples of 8) or, with False, on the
-        fp32 MFMAs."""
+        """set_prefill_split(SPLIT_X6 if enable else SPLIT_NONE)."""
         _check(_lib.akh_model_set_prefill_x6(self.handle, 1 if enable else 0),
                "set_prefill_x6")
 

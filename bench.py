@@ -84,16 +84,18 @@ def prefill_flop_parts(cfg, B, S, lm_rows=None):
     return gemm, attn, lm
 
 
-def prefill_rates(ms, gemm, attn, lm, x6_flop):
+def prefill_rates(ms, gemm, attn, lm, h3_flop, x6_flop):
     """Rates of a prefill that took `ms`: useful fp32 TFLOP/s; their fraction
     of the fp32 MFMA peak (the roofline of fp32 arithmetic on this part);
     and the MFMA pipes' busy fraction, the executed MFMA work at the peak rate
-    of the instructions that ran it: the split-bfloat16 GEMMs and flash
-    attention (`x6_flop` of the useful flops) execute six bf16 products per
-    multiply-add at the bf16 peak, everything else runs on fp32 MFMAs."""
+    of the instructions that ran it: the split-fp16 GEMMs (`h3_flop` of the
+    useful flops) execute three fp16 products per multiply-add, the
+    split-bfloat16 ones (`x6_flop`) six bf16 products, both at the 16-bit
+    peak; everything else runs on fp32 MFMAs."""
     t = ms / 1e3
     useful = gemm + attn + lm
-    busy = 6 * x6_flop / (BF16_MFMA_PEAK_TFLOPS * 1e12) + (useful - x6_flop) / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+    busy = ((3 * h3_flop + 6 * x6_flop) / (BF16_MFMA_PEAK_TFLOPS * 1e12)
+            + (useful - h3_flop - x6_flop) / (FP32_MFMA_PEAK_TFLOPS * 1e12))
     return {"tflops": round(useful / t / 1e12, 2),
             "fp32_roofline_frac": round(useful / t / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
             "mfma_busy_frac": round(busy / t, 4)}
@@ -223,15 +225,17 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
         pms = be.timer_stop()
         g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
         fl = g + a + lm
-        r = prefill_rates(pms, g, a, lm, g + a)
-        out.update({"prefill_kernels": "split-bf16 GEMMs and flash (fp32-accurate, default)",
+        r = prefill_rates(pms, g, a, lm, g, a)
+        out.update({"prefill_kernels": "split-fp16 GEMMs (two fp16 terms, three products) and "
+                                       "split-bf16 flash (fp32-accurate, default)",
                     "prefill_ms": round(pms, 2), "prefill_tok_s": round(Bp * Sp / (pms / 1e3), 1),
                     "prefill_tflops": r["tflops"],
                     "prefill_fp32_roofline_frac": r["fp32_roofline_frac"],
                     "prefill_mfma_busy_frac": r["mfma_busy_frac"]})
         # The same prefill with the layer GEMMs and flash on the fp32 MFMAs.
         log("bench: scaled config prefill 8 x 2048, fp32 MFMAs")
-        model.set_prefill_x6(False)
+        split = model.prefill_split()
+        model.set_prefill_split(hip.Model.SPLIT_NONE)
         ps.reset()
         ps.prefill(toks, want_logits=False)
         ps.reset()
@@ -239,7 +243,7 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
         be.timer_start()
         ps.prefill(toks, want_logits=False)
         fms = be.timer_stop()
-        model.set_prefill_x6(True)
+        model.set_prefill_split(split)
         out.update({"prefill_fp32_mfma_ms": round(fms, 2),
                     "prefill_fp32_mfma_tok_s": round(Bp * Sp / (fms / 1e3), 1),
                     "prefill_fp32_mfma_frac": round(fl / (fms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)})
@@ -281,23 +285,33 @@ def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
     g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
     fl = g + a + lm
     prefill = {"workload": "config 3: hall-1.0 fp32 prefill 16 x 512 (seed 3), last-row logits",
-               "kernels": "split-bf16 GEMMs and flash: fp32 operands as three bf16 terms, "
-                          "six products (fp32-accurate, the default)",
+               "kernels": "split-fp16 GEMMs (fp32 operands as two fp16 terms, three products) "
+                          "and split-bf16 flash (three bf16 terms, six products); "
+                          "fp32-accurate, the default",
                "ms": round(pms, 3), "tok_s": round(Bp * Sp / (pms / 1e3), 1),
-               **prefill_rates(pms, g, a, lm, g + a), "flop": fl}
-    # The same prefill with the layer GEMMs and flash on the fp32 MFMAs.
-    model.set_prefill_x6(False)
-    ps.reset()
-    ps.prefill(ptoks, want_logits=False)  # warm
-    ftimes32 = []
-    for _ in range(reps):
+               **prefill_rates(pms, g, a, lm, g, a), "flop": fl}
+    split = model.prefill_split()
+
+    def timed(kind):
+        model.set_prefill_split(kind)
         ps.reset()
-        be.synchronize()
-        be.timer_start()
-        ps.prefill(ptoks, want_logits=False)
-        ftimes32.append(be.timer_stop())
-    model.set_prefill_x6(True)
-    p32 = min(ftimes32)
+        ps.prefill(ptoks, want_logits=False)  # warm
+        ts = []
+        for _ in range(reps):
+            ps.reset()
+            be.synchronize()
+            be.timer_start()
+            ps.prefill(ptoks, want_logits=False)
+            ts.append(be.timer_stop())
+        return min(ts)
+
+    # The same prefill with the GEMMs split into three bfloat16 terms.
+    x6 = timed(hip.Model.SPLIT_X6)
+    prefill["split_bf16_x6"] = {"ms": round(x6, 3), "tok_s": round(Bp * Sp / (x6 / 1e3), 1),
+                                **prefill_rates(x6, g, a, lm, 0, g + a)}
+    # The same prefill with the layer GEMMs and flash on the fp32 MFMAs.
+    p32 = timed(hip.Model.SPLIT_NONE)
+    model.set_prefill_split(split)
     prefill["fp32_mfma"] = {"ms": round(p32, 3), "tok_s": round(Bp * Sp / (p32 / 1e3), 1),
                             "tflops": round(fl / (p32 / 1e3) / 1e12, 2),
                             "mfma_frac": round(fl / (p32 / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
@@ -319,7 +333,7 @@ def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
     prefill["train_forward"] = {
         "workload": "Trainer::forward + CrossEntropy, 16 x 512 rows (seed 3), all-rows lm_head",
         "ms": round(fms, 3), "tok_s": round(Bp * Sp / (fms / 1e3), 1),
-        **prefill_rates(fms, g, a, flm, g + a + flm),
+        **prefill_rates(fms, g, a, flm, g + flm, a),
         "mean_loss": round(mean_loss, 4), "flop": ffl}
     fw.close()
     return prefill
@@ -592,7 +606,7 @@ def main():
     for _ in range(10):
         be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
     c2b_ms = be.timer_stop() / 10
-    rb = prefill_rates(c2b_ms, 0, c2_flop, 0, c2_flop)
+    rb = prefill_rates(c2b_ms, 0, c2_flop, 0, 0, c2_flop)
     config2 = {"workload": "config 2: flash attention 8 x 12 x 512 x 64 (seed 2)",
                "kernel": "split-bf16 flash (fp32-accurate)",
                "per_node_ms": round(c2_ms, 4),

@@ -292,18 +292,30 @@ akh_status akh_model_set_bf16_tiles(akh_model* m, int allow, uint32_t* n_bf16);
  * akh_model_upload_param).  Needs head_dim 64 or 128 and dim, ffn_hidden
  * multiples of 8. */
 akh_status akh_model_set_prefill_bf16(akh_model* m, int enable);
-/* No reference counterpart (a choice of kernel, not of numerics): with
- * enable = 1 (the default when dim and ffn_hidden are multiples of 8) the
- * f32 prefill's layer GEMMs and flash attention (head_dim 64 / 128) and the
- * trainer forward's lm_head run on
- * bfloat16 MFMAs with both fp32 operands split exactly into three bfloat16
- * terms and the six products down to 2^-16 of the full product accumulated
- * in fp32: each product is carried to within 2^-23 relative, so results
- * keep fp32 accuracy (the f32 path's 1e-3 bar) at about 1.5-1.9x the fp32
- * MFMA kernel's speed.  The model then keeps a transposed fp32 copy of every
- * layer matrix and of lm_head (refreshed by akh_model_upload_param).
- * enable = 0 frees it and returns to the fp32-MFMA GEMMs.  The bf16-MFMA
- * prefill (akh_model_set_prefill_bf16), when on, takes precedence. */
+/* No reference counterpart (a choice of kernel, not of numerics): the
+ * kernels of the f32 prefill's layer GEMMs and of the trainer forward's
+ * lm_head, all fp32-accurate (the f32 path's 1e-3 bar):
+ *   AKH_SPLIT_H3 (the default when dim and ffn_hidden are multiples of 8):
+ *     fp16 MFMAs with each fp32 operand split into two fp16 terms, x = hi +
+ *     2^-11 lo (the scaled-residual split of Ootomo and Yokota), and the
+ *     three products down to 2^-22 of the full product accumulated in fp32
+ *     (hi.hi apart from the two cross terms).  An operand beyond fp16's range
+ *     (|x| >= 65520) is detected from the non-finite results it causes, and
+ *     that prefill or forward is recomputed on the fp32-MFMA kernels.
+ *   AKH_SPLIT_X6: bfloat16 MFMAs with each operand split exactly into three
+ *     bfloat16 terms and six products (each product within 2^-23).
+ *   AKH_SPLIT_NONE: the fp32 MFMAs (v_mfma_f32_32x32x2_f32).
+ * Either split keeps a copy of every layer matrix and of lm_head (4 bytes an
+ * element: fp16 planes, or transposed fp32), refreshed by
+ * akh_model_upload_param, and runs flash attention (head_dim 64 / 128) on
+ * split-bfloat16 MFMAs.  The bf16-MFMA prefill (akh_model_set_prefill_bf16),
+ * when on, takes precedence. */
+#define AKH_SPLIT_NONE 0
+#define AKH_SPLIT_X6 1
+#define AKH_SPLIT_H3 2
+akh_status akh_model_set_prefill_split(akh_model* m, int kind);
+int akh_model_prefill_split(const akh_model* m);
+/* akh_model_set_prefill_split(m, enable ? AKH_SPLIT_X6 : AKH_SPLIT_NONE). */
 akh_status akh_model_set_prefill_x6(akh_model* m, int enable);
 
 /* ---- the trainer's fused forward: src/nn/train.rs:256-275, 394-401 ------- */

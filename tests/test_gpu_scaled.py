@@ -13,8 +13,8 @@ size-independent properties:
   same prompt decoded alone, with the f32 and with the bfloat16 KV cache;
 - bfloat16 weight tiles against float tiles of the same values at KV 2048,
   and the fused residual add + RMSNorm against the default;
-- the 8 x 2048 prefill on the split-bf16 kernels against the fp32-MFMA
-  kernels;
+- the 8 x 2048 prefill on the split-fp16 and split-bf16 kernels against
+  the fp32-MFMA kernels;
 - prefill == sequential decode (inference.rs:334-359): a 2048-token prefill
   against a 2040-token prefill followed by the last 8 tokens as decode
   steps.
@@ -109,23 +109,30 @@ def test_scaled_decode_64_rows_bf16_kv_at_kv_2048(pkg, scaled):
     s.close()
 
 
-def test_scaled_prefill_8x2048_split_bf16_vs_fp32_mfma(pkg, scaled):
+def test_scaled_prefill_8x2048_split_vs_fp32_mfma(pkg, scaled):
+    # The 8 x 2048 prefill on the default split-fp16 GEMMs (256 x 128 tiles
+    # at these shapes) and on the split-bf16 ones, each against the
+    # fp32-MFMA kernels: logits and cache within fp32 rounding, same tokens.
     cfg, model = scaled
+    M = pkg.hip.Model
     B, S = 8, 2048
     toks = pkg.synthetic_tokens(B * S, cfg.vocab_size, seed=7).reshape(B, S)
     s = pkg.hip.Session(model, S, B)
-    l6, t6 = s.prefill(toks)
-    k6 = s.cache(23, 6, 0)
-    s.reset()
-    model.set_prefill_x6(False)
+    runs = {}
     try:
-        l32, t32 = s.prefill(toks)
-        k32 = s.cache(23, 6, 0)
+        for kind in (M.SPLIT_H3, M.SPLIT_X6, M.SPLIT_NONE):
+            model.set_prefill_split(kind)
+            s.reset()
+            lg, tk = s.prefill(toks)
+            runs[kind] = (lg, tk, s.cache(23, 6, 0))
     finally:
-        model.set_prefill_x6(True)
-    assert np.abs(l6 - l32).max() < 1e-4
-    assert np.array_equal(t6, t32)
-    np.testing.assert_allclose(k6, k32, rtol=0, atol=1e-4)
+        model.set_prefill_split(M.SPLIT_H3)
+    l32, t32, k32 = runs[M.SPLIT_NONE]
+    for kind in (M.SPLIT_H3, M.SPLIT_X6):
+        lg, tk, kc = runs[kind]
+        assert np.abs(lg - l32).max() < 1e-4, kind
+        assert np.array_equal(tk, t32), kind
+        np.testing.assert_allclose(kc, k32, rtol=0, atol=1e-4)
     s.close()
 
 

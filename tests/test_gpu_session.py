@@ -216,7 +216,7 @@ def test_ragged_prefill_matches_per_sequence(backend, pkg, ora, dim, mode):
     model = pkg.hip.Model(backend, cfg)
     model.upload(w)
     if mode == "fp32_mfma":
-        model.set_prefill_x6(False)
+        model.set_prefill_split(pkg.hip.Model.SPLIT_NONE)
     if mode == "bf16":
         model.set_prefill_bf16(True)
 
@@ -561,25 +561,33 @@ def test_scaled_config_matches_oracle(backend, pkg, ora):
     del w
 
 
-def test_prefill_x6_matches_fp32_mfma_and_oracle(backend, pkg, ora):
-    # The default prefill GEMMs (bf16 MFMAs on operands split exactly into
-    # three bfloat16 terms, six products) against the fp32-MFMA GEMMs
-    # (set_prefill_x6(False)) and the oracle: both meet the fp32 bar, agree
-    # with each other to fp32 rounding (1e-4) with the same tokens, and
-    # toggling back reproduces the first run bit for bit.  dim 256, head_dim
-    # 64, ffn 1024: ragged tiles at M = 3 x 70 rows.
+@pytest.mark.parametrize("kind", ["h3", "x6"])
+def test_prefill_split_matches_fp32_mfma_and_oracle(backend, pkg, ora, kind):
+    # The split prefill GEMMs (h3, the default: fp16 MFMAs on operands split
+    # into two fp16 terms, three products; x6: bf16 MFMAs on three bfloat16
+    # terms, six products) against the fp32-MFMA GEMMs (SPLIT_NONE) and the
+    # oracle: both meet the fp32 bar, agree with each other to fp32 rounding
+    # (1e-4) with the same tokens, and switching back reproduces the first
+    # run bit for bit.  The split run differs from the fp32 one in its last
+    # bits (no silent fallback to the fp32 kernels).  dim 256, head_dim 64,
+    # ffn 1024: ragged tiles at M = 3 x 70 rows.
+    M = pkg.hip.Model
     cfg = pkg.ModelConfig.new(300, 256, 4, 2, 80)
     w = pkg.synthetic_weights(cfg, seed=61)
     model, s = _session(pkg, backend, cfg, w, 80, 3)
+    assert model.prefill_split() == M.SPLIT_H3
+    split = M.SPLIT_H3 if kind == "h3" else M.SPLIT_X6
+    model.set_prefill_split(split)
     toks = pkg.synthetic_tokens(3 * 70, cfg.vocab_size, seed=62).reshape(3, 70)
     lx, nx = s.prefill(toks)
     kx = s.cache(1, 2, 0)[:70].copy()
-    model.set_prefill_x6(False)
+    model.set_prefill_split(M.SPLIT_NONE)
     s.reset()
     lf, nf = s.prefill(toks)
     assert np.abs(lx - lf).max() < 1e-4 and np.array_equal(nx, nf)
+    assert not np.array_equal(lx, lf)
     np.testing.assert_allclose(kx, s.cache(1, 2, 0)[:70], atol=1e-5)
-    model.set_prefill_x6(True)
+    model.set_prefill_split(split)
     s.reset()
     lx2, nx2 = s.prefill(toks)
     assert np.array_equal(lx, lx2) and np.array_equal(nx, nx2)
@@ -590,7 +598,46 @@ def test_prefill_x6_matches_fp32_mfma_and_oracle(backend, pkg, ora):
         for got, nxt in ((lx, nx), (lf, nf)):
             assert np.abs(got[b] - ref).max() < TOL
             assert int(nxt[b]) == ora.argmax(ref)
+    model.set_prefill_split(M.SPLIT_H3)
 
+
+@pytest.mark.parametrize("where", ["activation", "weight"])
+def test_prefill_h3_out_of_fp16_range_reruns_in_fp32(backend, pkg, where):
+    # An operand of the h3 GEMMs beyond fp16's range (|x| >= 65520) turns
+    # into an infinite hi term; the kernels flag the non-finite results and
+    # the prefill is recomputed on the fp32 kernels, so its logits, tokens
+    # and cache equal the fp32-MFMA prefill's bit for bit.  "activation":
+    # norm gains of 1e5 put the QKV and ffn_up inputs far beyond 65520;
+    # "weight": one ffn_up weight of 1e5.
+    M = pkg.hip.Model
+    cfg = pkg.ModelConfig.new(300, 256, 4, 2, 80)
+    w = pkg.synthetic_weights(cfg, seed=63)
+    if where == "activation":
+        w[1 + 6 * 1 + 0] = w[1 + 6 * 1 + 0] * 1e5  # layer 1 norm1 gain
+    else:
+        up = w[1 + 6 * 0 + 4].copy()
+        up.flat[12345] = 1e5
+        w[1 + 6 * 0 + 4] = up
+    model, s = _session(pkg, backend, cfg, w, 80, 3)
+    assert model.prefill_split() == M.SPLIT_H3
+    toks = pkg.synthetic_tokens(3 * 70, cfg.vocab_size, seed=64).reshape(3, 70)
+    lh, nh = s.prefill(toks)
+    kh = s.cache(1, 2, 0)[:70].copy()
+    assert np.isfinite(lh).all()
+    model.set_prefill_split(M.SPLIT_NONE)
+    s.reset()
+    lf, nf = s.prefill(toks)
+    assert np.array_equal(lh, lf) and np.array_equal(nh, nf)
+    assert np.array_equal(kh, s.cache(1, 2, 0)[:70])
+    # The trainer forward reruns the same way.
+    model.set_prefill_split(M.SPLIT_H3)
+    tg = np.roll(toks, -1, axis=1)
+    f = pkg.hip.Forward(model, 3, 70)
+    mh, lsh = f.loss(toks, tg)
+    model.set_prefill_split(M.SPLIT_NONE)
+    mf, lsf = f.loss(toks, tg)
+    assert np.array_equal(lsh, lsf) and mh == mf
+    f.close()
 
 
 def test_decode_kernel_timers(backend, pkg):

@@ -136,10 +136,13 @@ def test_forward_errors(backend, pkg):
     f.close()
 
 
-def test_forward_x6_matches_fp32_mfma(backend, pkg, ora):
+@pytest.mark.parametrize("kind", ["h3", "x6"])
+def test_forward_split_matches_fp32_mfma(backend, pkg, ora, kind):
     # The trainer forward's GEMMs (layers and the all-rows lm_head) on the
-    # split-bf16 kernel and on the fp32 MFMAs: losses and probabilities agree
-    # to fp32 rounding.  dim 64, 2 x 40 rows, vocab 300.
+    # split kernels (h3, the default, or x6) and on the fp32 MFMAs: losses
+    # and probabilities agree to fp32 rounding.  dim 64, 2 x 40 rows, vocab
+    # 300.
+    M = pkg.hip.Model
     cfg = pkg.ModelConfig.new(300, 64, 4, 2, 40)
     w = pkg.synthetic_weights(cfg, seed=64)
     B, S = 2, 40
@@ -147,10 +150,11 @@ def test_forward_x6_matches_fp32_mfma(backend, pkg, ora):
     tgts = np.stack([ora.rand_tokens(S, 300, 400 + b) for b in range(B)])
     model = pkg.hip.Model(backend, cfg)
     model.upload(w)
+    model.set_prefill_split(M.SPLIT_H3 if kind == "h3" else M.SPLIT_X6)
     f = pkg.hip.Forward(model, B, S)
     mx, lx = f.loss(toks, tgts)
     px = f.probs(0, B * S)
-    model.set_prefill_x6(False)
+    model.set_prefill_split(M.SPLIT_NONE)
     mf, lf = f.loss(toks, tgts)
     np.testing.assert_allclose(lx, lf, atol=1e-5)
     np.testing.assert_allclose(px, f.probs(0, B * S), atol=1e-6)
@@ -169,6 +173,10 @@ def test_forward_x6_needs_multiples_of_8(backend, pkg, ora):
     tgts = np.stack([ora.rand_tokens(11, 37, 600 + b) for b in range(2)])
     model = pkg.hip.Model(backend, cfg)
     model.upload(w)
+    assert model.prefill_split() == pkg.hip.Model.SPLIT_NONE
+    for kind in (pkg.hip.Model.SPLIT_H3, pkg.hip.Model.SPLIT_X6):
+        with pytest.raises(pkg.hip.InvalidArgument, match="multiples of 8"):
+            model.set_prefill_split(kind)
     with pytest.raises(pkg.hip.InvalidArgument, match="multiples of 8"):
         model.set_prefill_x6(True)
     model.set_prefill_x6(False)
