@@ -35,25 +35,58 @@ __global__ __launch_bounds__(256) void k_rows_rmsnorm(const float* x,
     o[c] = __fmul_rn(__fmul_rn(xr[c], rs), w[c]);
 }
 
-// Epilogue on the adjacent column pair (n, n + 1), n even, of row m.
+// m / S and m % S for 0 <= m < 2^23 through a float reciprocal (a quotient
+// off by at most one, then corrected): a few instructions instead of an
+// integer division per row of the QKV epilogue.
+__device__ __forceinline__ void div_rows(int m, int S, int& q, int& r) {
+  q = (int)((float)m * __builtin_amdgcn_rcpf((float)S));
+  r = m - q * S;
+  if (r < 0) {
+    --q;
+    r += S;
+  } else if (r >= S) {
+    ++q;
+    r -= S;
+  }
+}
+
+// Epilogue on the adjacent column pair (n, n + 1), n even, of row m.  With
+// N even a pair is one 8-byte-aligned store (an odd N, as a vocabulary-wide
+// lm_head, stores the two floats apart); the QKV destinations have even
+// strides.  After inlining into a kernel's unrolled output loop, everything
+// that depends on n alone is computed once per lane.
 template <int EPI>
 __device__ __forceinline__ void epi_pair_gemm(const GemmParams& p, int M,
                                               int N, int m, int n, float v0,
                                               float v1) {
   if (m >= M || n >= N) return;
-  const bool has1 = n + 1 < N;
+  const bool has1 = n + 1 < N, pair = (N & 1) == 0;
+  float* y = p.c + (size_t)m * N + n;
+  auto put = [&](float* dst, float a, float b) {
+    if (pair) {
+      *reinterpret_cast<float2*>(dst) = make_float2(a, b);
+    } else {
+      dst[0] = a;
+      if (has1) dst[1] = b;
+    }
+  };
   if (EPI == GEMM_STORE) {
-    float* y = p.c + (size_t)m * N + n;
-    y[0] = v0;
-    if (has1) y[1] = v1;
+    put(y, v0, v1);
   } else if (EPI == GEMM_ADD) {
-    float* y = p.c + (size_t)m * N + n;
-    y[0] = y[0] + v0;
-    if (has1) y[1] = y[1] + v1;
+    if (pair) {
+      const float2 o = *reinterpret_cast<const float2*>(y);
+      *reinterpret_cast<float2*>(y) = make_float2(o.x + v0, o.y + v1);
+    } else {
+      y[0] = y[0] + v0;
+      if (has1) y[1] = y[1] + v1;
+    }
   } else if (EPI == GEMM_SILU) {
-    float* y = p.c + (size_t)m * N + n;
-    y[0] = v0 / (1.0f + expf(-v0));
-    if (has1) y[1] = v1 / (1.0f + expf(-v1));
+    // x / (1 + e^-x) as x * rcp(1 + 2^(-x log2 e)): within a few ulp of the
+    // IEEE expression, at a fraction of its instructions.
+    auto silu = [](float v) {
+      return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.44269504088896341f));
+    };
+    put(y, silu(v0), silu(v1));
   } else if (EPI == GEMM_QKV) {
     // Columns [0, d) are Q, [d, 2d) K, [2d, 3d) V (weights.rs:49-58).
     const int dim = p.dim;
@@ -64,8 +97,7 @@ __device__ __forceinline__ void epi_pair_gemm(const GemmParams& p, int M,
       seq = st.x;
       t = st.y;
     } else {
-      seq = m / p.S;
-      t = m - seq * p.S;
+      div_rows(m, p.S, seq, t);
     }
     if (region < 2) {
       const int i = (c % p.head_dim) >> 1;
@@ -80,8 +112,7 @@ __device__ __forceinline__ void epi_pair_gemm(const GemmParams& p, int M,
     else
       dst = (region == 1 ? p.kcache : p.vcache) + (size_t)seq * p.seq_stride +
             (size_t)t * dim + c;
-    dst[0] = v0;
-    dst[1] = v1;
+    *reinterpret_cast<float2*>(dst) = make_float2(v0, v1);
   }
 }
 
