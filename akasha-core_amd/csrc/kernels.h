@@ -114,6 +114,8 @@ struct GemmParams {
   int kv_packed;
 };
 
+enum { FLASH_X6 = 1, FLASH_H3 = 2 };  // FlashParams::x6
+
 struct FlashParams {
   const float* q;
   const float* k;
@@ -128,7 +130,10 @@ struct FlashParams {
                                     // row_offset come from it (1 sequence)
   uint16_t* o16;  // launch_flash_bf16: bfloat16 output (o unused)
   int x6;         // launch_flash, head_dim 64 / 128: split-bfloat16 MFMAs
-                  // (fp32 accuracy) instead of fp32 MFMAs
+                  // (fp32 accuracy) instead of fp32 MFMAs; FLASH_H3: split
+                  // fp16 MFMAs (fp32 accuracy), setting *range_flag when an
+                  // operand is beyond fp16's range
+  int* range_flag;
   // Ragged prompts packed back to back: sequence b's rows of q, o (and lse)
   // are [rows_at[b], rows_at[b + 1]) and its length is their count (S is
   // then the longest); K and V rows likewise if kv_packed, else at

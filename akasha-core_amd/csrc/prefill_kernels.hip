@@ -1512,6 +1512,248 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
         mrow * 0.69314718055994531f + logf(lrow);
 }
 
+// Causal flash attention in fp32 accuracy on fp16 MFMAs, the structure of
+// k_flash_x6 with two-term fp16 splits (split2_f16: x = hi + 2^-11 lo) and
+// three products per contraction instead of six.  Scores: Q and K split,
+// hi.hi in one accumulator and the two cross terms in another (the
+// k_gemm_h3 scheme).  Output: P split the same way and V^T staged as hi, the
+// unscaled remainder v - hi and hi 2^-11, so one accumulator takes
+// p0 v0 + p0 v1 + p1 (2^-11 v0): the remainder and the scaled hi can be
+// subnormal, but each loses at most 2^-25 absolute, weighted by the
+// probabilities (sum 1).  Output, lse and softmax statistics stay fp32.  A
+// non-finite output (an operand beyond fp16's range) sets *p.range_flag.
+template <int HD>
+__global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
+  constexpr int QB = 128, KB = 32, NT = HD / 32, NQ = HD / 16;
+  constexpr int KP = HD + 8;   // K row stride (fp16)
+  constexpr int VP = KB + 8;   // V^T row stride (fp16)
+  constexpr int CPR = HD / 4;  // float4 per K/V row
+  constexpr int KPT = KB * CPR / 256;  // consecutive keys staged per thread
+  static_assert(KPT == 2 || KPT == 4, "staging covers 2 or 4 keys per thread");
+  constexpr int K_PLANE = KB * KP, V_PLANE = HD * VP;  // fp16 elements
+  constexpr int KV_BYTES = (2 * K_PLANE + 3 * V_PLANE) * 2;
+  constexpr int O_BYTES = 4 * 32 * 33 * 4;
+  __shared__ __align__(16) unsigned char lds[KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES];
+  auto Ks = [&](int pl) { return reinterpret_cast<uint16_t (*)[KP]>(lds) + pl * KB; };
+  auto Vt = [&](int pl) {
+    return reinterpret_cast<uint16_t (*)[VP]>(lds + 2 * K_PLANE * 2) + pl * HD;
+  };
+
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
+  FlashSeq fs;
+  if (!flash_seq<HD>(p, hh, b, fs)) return;
+  const int S = fs.S, d = fs.d, hd = p.hd;  // head size hd <= HD
+  const float scale = fs.scale;
+  const int H = d / hd;
+  // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
+  const float qscale = scale * 1.44269504088896341f;
+  const int q0 = qblk * QB;
+  if (q0 >= S) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+
+  const float* qp = p.q + fs.q + hh * hd;
+  const float* kp = p.k + fs.kv + hh * hd;
+  const float* vp = p.v + fs.kv + hh * hd;
+  // Columns past the head size (hd a multiple of 4 below HD) read as zero.
+  auto col4 = [hd](const float* src, int c) {
+    return c < hd ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+
+  const int qi = q0 + wave * 32 + j;
+  uint4 qf[2][NQ];  // hi and scaled lo of dims 16 s + 8 h .. + 7 of query qi
+  {
+    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 8 * h;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s)
+      split2_f16(col4(qr + 16 * s, 16 * s + 8 * h), col4(qr + 16 * s + 4, 16 * s + 8 * h + 4),
+                 qf[0][s], qf[1][s]);
+  }
+  f32x16 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = zero16();
+  float mrow = -INFINITY, lrow = 0.f;
+
+  const int wave_qmin = q0 + wave * 32, wave_qmax = wave_qmin + 31;
+  const int kend = min(S, q0 + QB);
+  const int nkb = (kend + KB - 1) / KB;
+
+  // Staging: thread t takes dims 4 (t % CPR) .. + 3 of KPT consecutive keys
+  // from KPT (t / CPR), so K rows and V^T rows are both written 4 or 8 bytes
+  // at a time per plane.
+  const int sc = (tid % CPR) * 4, sk = (tid / CPR) * KPT;
+  float4 kr[KPT], vr[KPT];
+  auto load_kv = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int key = kb * KB + sk + i;
+      const size_t off = (size_t)(key < S ? key : 0) * d + sc;
+      kr[i] = col4(kp + off, sc);
+      vr[i] = col4(vp + off, sc);
+    }
+  };
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  // K: hi and scaled lo (split2_f16) of a and b, packed as pairs.
+  auto split_k = [](float a, float b, uint32_t (&t)[2]) {
+    t[0] = cvt_pk_f16(a, b);
+    const h2 hv = __builtin_bit_cast(h2, t[0]);
+    t[1] = cvt_pk_f16((a - (float)hv[0]) * 2048.f, (b - (float)hv[1]) * 2048.f);
+  };
+  // V: hi, the unscaled remainder, and hi 2^-11, so that with P split as
+  // p0 + 2^-11 p1 one accumulator takes p0 v0 + p0 v1 + p1 (2^-11 v0).
+  auto split_v = [](float a, float b, uint32_t (&t)[3]) {
+    t[0] = cvt_pk_f16(a, b);
+    const h2 hv = __builtin_bit_cast(h2, t[0]);
+    const float ha = (float)hv[0], hb = (float)hv[1];
+    t[1] = cvt_pk_f16(a - ha, b - hb);
+    t[2] = cvt_pk_f16(ha * 0x1p-11f, hb * 0x1p-11f);
+  };
+  load_kv(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      uint32_t lo[2], hi[2];
+      split_k(kr[i].x, kr[i].y, lo);
+      split_k(kr[i].z, kr[i].w, hi);
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl)
+        *reinterpret_cast<uint2*>(&Ks(pl)[sk + i][sc]) = make_uint2(lo[pl], hi[pl]);
+    }
+    // V^T: dim row sc + c, keys sk .. sk + KPT - 1.
+    const float vc[4][4] = {
+#define AKH_VCOL(f) {vr[0].f, vr[1].f, KPT == 4 ? vr[KPT - 2].f : 0.f, KPT == 4 ? vr[KPT - 1].f : 0.f}
+        AKH_VCOL(x), AKH_VCOL(y), AKH_VCOL(z), AKH_VCOL(w)
+#undef AKH_VCOL
+    };
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint32_t t01[3], t23[3];
+      split_v(vc[c][0], vc[c][1], t01);
+      if constexpr (KPT == 4) {
+        split_v(vc[c][2], vc[c][3], t23);
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][sk]) = make_uint2(t01[pl], t23[pl]);
+      } else {
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint32_t*>(&Vt(pl)[sc + c][sk]) = t01[pl];
+      }
+    }
+    __syncthreads();
+    load_kv(kb + 1);  // rows past S read row 0: harmless, never used
+    const int j0 = kb * KB;
+    if (j0 > wave_qmax) continue;
+
+    // Scores: hi.hi in st, the cross terms in sc, st + 2^-11 sc.
+    f32x16 st = zero16(), scr = zero16();
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      f16x8 kf[2];
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl)
+        kf[pl] = f16x8_of(*reinterpret_cast<const uint4*>(&Ks(pl)[j][16 * s + 8 * h]));
+      scr = mfma_f16(kf[1], f16x8_of(qf[0][s]), scr);
+      scr = mfma_f16(kf[0], f16x8_of(qf[1][s]), scr);
+      st = mfma_f16(kf[0], f16x8_of(qf[0][s]), st);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[r] += scr[r] * 0x1p-11f;
+
+    // Keys above a query (the diagonal block) or past S are masked.
+    const bool masked = j0 + KB - 1 > wave_qmin || j0 + KB > S;
+    float pm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = st[r] * qscale;
+      if (masked) {
+        const int key = j0 + acc_row(r, h);
+        if (key > qi || key >= S) v = -INFINITY;
+      }
+      st[r] = v;
+      pm = fmaxf(pm, v);
+    }
+    pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+    const float mnew = fmaxf(mrow, pm);  // finite: key 0 is in every query's range
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = __builtin_amdgcn_exp2f(st[r] - mnew);
+      st[r] = e;
+      ps += e;
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    const float corr = __builtin_amdgcn_exp2f(mrow - mnew);  // 0 on the first block
+    lrow = lrow * corr + ps;
+    if (__any(mnew != mrow)) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    }
+    mrow = mnew;
+    // P^T planes: MFMA 0 of the block takes entries 0..7 of each lane (keys
+    // acc_row(0..7, h)), MFMA 1 entries 8..15.
+    uint4 pf[2][2];
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+      split2_f16(make_float4(st[8 * half], st[8 * half + 1], st[8 * half + 2], st[8 * half + 3]),
+                 make_float4(st[8 * half + 4], st[8 * half + 5], st[8 * half + 6],
+                             st[8 * half + 7]),
+                 pf[half][0], pf[half][1]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        // V^T rows of the same keys: two runs of four.
+        f16x8 vf[3];
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+          const uint16_t* vrow = Vt(pl)[32 * t + j] + 16 * half;
+          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
+          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
+          vf[pl] = f16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
+        }
+        // Smallest terms first: p1 (2^-11 v0), p0 v1, then p0 v0.
+        o[t] = mfma_f16(vf[2], f16x8_of(pf[half][1]), o[t]);
+        o[t] = mfma_f16(vf[1], f16x8_of(pf[half][0]), o[t]);
+        o[t] = mfma_f16(vf[0], f16x8_of(pf[half][0]), o[t]);
+      }
+    }
+  }
+
+  // O^T (rows = dims) -> LDS, one 32-dim tile at a time -> coalesced rows.
+  const float inv = 1.0f / lrow;
+  // An operand beyond fp16's range (|x| >= 65520) makes the output or the
+  // softmax state non-finite: flag it for the caller's fp32 rerun.
+  {
+    bool finite = __builtin_isfinite(inv);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) finite = finite && __builtin_isfinite(o[t][r]);
+    if (!finite && p.range_flag) *p.range_flag = 1;
+  }
+  float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33 * 4);
+  float* op = p.o + fs.o + hh * hd;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Os[j][acc_row(r, h)] = o[t][r] * inv;
+    __syncthreads();
+    for (int e = lane; e < 32 * 32; e += 64) {
+      const int r = e >> 5, c = e & 31;
+      const int qrow = q0 + wave * 32 + r;
+      if (qrow < S && 32 * t + c < hd) op[(size_t)qrow * d + 32 * t + c] = Os[r][c];
+    }
+  }
+  if (p.lse && h == 0 && qi < S)  // max + ln(sum), back in natural units
+    p.lse[fs.l + (size_t)qi * H + hh] =
+        mrow * 0.69314718055994531f + logf(lrow);
+}
+
 // k_flash_x6 for grids too small to fill the part (a single sequence's
 // FLASH_ATTENTION node): one 32-query tile per block, its key blocks dealt
 // round-robin to the 4 waves.  Each wave stages its own K and V^T planes in
@@ -1790,6 +2032,11 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
       // the block's waves (k_flash_x6w).
       hipLaunchKernelGGL(k_flash_x6w<64>, dim3(H, batch, (max_rows + 31) / 32), dim3(256), 0,
                          s, p);
+    } else if (p.x6 == FLASH_H3) {
+      if (p.hd == 64)
+        hipLaunchKernelGGL(k_flash_h3<64>, g, dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL(k_flash_h3<128>, g, dim3(256), 0, s, p);
     } else if (p.x6) {
       if (p.hd == 64)
         hipLaunchKernelGGL(k_flash_x6<64>, g, dim3(256), 0, s, p);

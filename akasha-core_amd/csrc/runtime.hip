@@ -1720,7 +1720,10 @@ hipError_t prefill_layers_f32(akh_session* s, const PrefillRows& pr, bool exact)
     f.d = (int)d;
     f.hd = (int)hd;
     f.scale = 1.0f / sqrtf((float)hd);
-    f.x6 = s->m->prefill_split != AKH_SPLIT_NONE && !exact ? 1 : 0;
+    f.x6 = exact || s->m->prefill_split == AKH_SPLIT_NONE ? 0
+           : s->m->prefill_split == AKH_SPLIT_H3          ? FLASH_H3
+                                                          : FLASH_X6;
+    f.range_flag = s->m->range_flag;
     TRY_HIP(launch_flash(f, (int)s->B, (int)S, st));
 
     GemmParams o{};

@@ -225,9 +225,9 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
         pms = be.timer_stop()
         g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
         fl = g + a + lm
-        r = prefill_rates(pms, g, a, lm, g, a)
-        out.update({"prefill_kernels": "split-fp16 GEMMs (two fp16 terms, three products) and "
-                                       "split-bf16 flash (fp32-accurate, default)",
+        r = prefill_rates(pms, g, a, lm, g + a, 0)
+        out.update({"prefill_kernels": "split-fp16 GEMMs and flash (two fp16 terms, three "
+                                       "products; fp32-accurate, default)",
                     "prefill_ms": round(pms, 2), "prefill_tok_s": round(Bp * Sp / (pms / 1e3), 1),
                     "prefill_tflops": r["tflops"],
                     "prefill_fp32_roofline_frac": r["fp32_roofline_frac"],
@@ -285,11 +285,10 @@ def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
     g, a, lm = prefill_flop_parts(cfg, Bp, Sp)
     fl = g + a + lm
     prefill = {"workload": "config 3: hall-1.0 fp32 prefill 16 x 512 (seed 3), last-row logits",
-               "kernels": "split-fp16 GEMMs (fp32 operands as two fp16 terms, three products) "
-                          "and split-bf16 flash (three bf16 terms, six products); "
-                          "fp32-accurate, the default",
+               "kernels": "split-fp16 GEMMs and flash (fp32 operands as two fp16 terms, three "
+                          "products); fp32-accurate, the default",
                "ms": round(pms, 3), "tok_s": round(Bp * Sp / (pms / 1e3), 1),
-               **prefill_rates(pms, g, a, lm, g, a), "flop": fl}
+               **prefill_rates(pms, g, a, lm, g + a, 0), "flop": fl}
     split = model.prefill_split()
 
     def timed(kind):
@@ -305,7 +304,7 @@ def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
             ts.append(be.timer_stop())
         return min(ts)
 
-    # The same prefill with the GEMMs split into three bfloat16 terms.
+    # The same prefill with the GEMMs and flash split into three bfloat16 terms.
     x6 = timed(hip.Model.SPLIT_X6)
     prefill["split_bf16_x6"] = {"ms": round(x6, 3), "tok_s": round(Bp * Sp / (x6 / 1e3), 1),
                                 **prefill_rates(x6, g, a, lm, 0, g + a)}
@@ -333,7 +332,7 @@ def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
     prefill["train_forward"] = {
         "workload": "Trainer::forward + CrossEntropy, 16 x 512 rows (seed 3), all-rows lm_head",
         "ms": round(fms, 3), "tok_s": round(Bp * Sp / (fms / 1e3), 1),
-        **prefill_rates(fms, g, a, flm, g + flm, a),
+        **prefill_rates(fms, g, a, flm, g + a + flm, 0),
         "mean_loss": round(mean_loss, 4), "flop": ffl}
     fw.close()
     return prefill

@@ -601,23 +601,30 @@ def test_prefill_split_matches_fp32_mfma_and_oracle(backend, pkg, ora, kind):
     model.set_prefill_split(M.SPLIT_H3)
 
 
-@pytest.mark.parametrize("where", ["activation", "weight"])
+@pytest.mark.parametrize("where", ["activation", "weight", "value"])
 def test_prefill_h3_out_of_fp16_range_reruns_in_fp32(backend, pkg, where):
-    # An operand of the h3 GEMMs beyond fp16's range (|x| >= 65520) turns
-    # into an infinite hi term; the kernels flag the non-finite results and
-    # the prefill is recomputed on the fp32 kernels, so its logits, tokens
-    # and cache equal the fp32-MFMA prefill's bit for bit.  "activation":
-    # norm gains of 1e5 put the QKV and ffn_up inputs far beyond 65520;
-    # "weight": one ffn_up weight of 1e5.
+    # An operand of the split-fp16 kernels beyond fp16's range (|x| >= 65520)
+    # turns into an infinite hi term; the kernels flag the non-finite results
+    # and the prefill is recomputed on the fp32 kernels, so its logits,
+    # tokens and cache equal the fp32-MFMA prefill's bit for bit.
+    # "activation": norm gains of 1e5 put the QKV and ffn_up inputs far
+    # beyond 65520; "weight": one ffn_up weight of 1e5; "value": layer 0's V
+    # weights scaled to N(0, 5000), so V (~1e5) overflows in the flash
+    # attention and in out_proj's input while every GEMM weight and input
+    # before it stays in range.
     M = pkg.hip.Model
     cfg = pkg.ModelConfig.new(300, 256, 4, 2, 80)
     w = pkg.synthetic_weights(cfg, seed=63)
     if where == "activation":
         w[1 + 6 * 1 + 0] = w[1 + 6 * 1 + 0] * 1e5  # layer 1 norm1 gain
-    else:
+    elif where == "weight":
         up = w[1 + 6 * 0 + 4].copy()
         up.flat[12345] = 1e5
         w[1 + 6 * 0 + 4] = up
+    else:
+        qkv = w[1 + 6 * 0 + 1].copy()  # [dim, 3 dim]: columns [2 dim, 3 dim) are V
+        qkv[:, 2 * cfg.dim:] *= np.float32(5000 / 0.02)
+        w[1 + 6 * 0 + 1] = qkv
     model, s = _session(pkg, backend, cfg, w, 80, 3)
     assert model.prefill_split() == M.SPLIT_H3
     toks = pkg.synthetic_tokens(3 * 70, cfg.vocab_size, seed=64).reshape(3, 70)
