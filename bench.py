@@ -468,6 +468,9 @@ def main():
                     help="measure config 5's prefill legs only")
     ap.add_argument("--prefill-only", action="store_true",
                     help="measure only config 3's prefill legs and print them (for profiling)")
+    ap.add_argument("--scaled-prefill-only", action="store_true",
+                    help="measure only config 5's prefill legs and print them (for profiling: "
+                         "no graph replays)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the per-kernel decode legs, no graph replay (for counter "
                          "runs); config 5's too unless --no-scaled")
@@ -480,6 +483,12 @@ def main():
 
     pkg = entry.load_package()
     hip = pkg.hip
+    if args.scaled_prefill_only:
+        be = hip.Backend(0)
+        print(json.dumps({"scaled": scaled_measurement(pkg, hip, be, with_decode=False)}),
+              flush=True)
+        be.close()
+        return
     cfg = pkg.ModelConfig.akasha_hall_1()
     B, P, CTX = 32, 448, 512
     log("bench: generating hall-1.0 weights (seed 0)")
