@@ -551,12 +551,15 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
   const int j = lane & 31, h = lane >> 5;
 
   // Global -> register staging: rows tid / 4 and tid / 4 + 128, eight k at
-  // (tid % 4) * 8, of both A and B^T.  Loads go through buffer resources
-  // bounded to the block's rows; rows past M or N and octets past K (given
-  // an offset outside the resource) read zeros from the hardware.
+  // (tid % 4) * 8, of B^T and of a bfloat16 A; an fp32 A (four times the
+  // pieces) goes as row f / 8, k 4 (f % 8) .. + 3 for piece f = tid + 512 i,
+  // so eight consecutive lanes read one row's 128-byte line.  Loads go
+  // through buffer resources bounded to the block's rows; rows past M or N
+  // and pieces past K (given an offset outside the resource) read zeros
+  // from the hardware.
   const int sr = tid >> 2, sk = (tid & 3) * 8;
   uint4 ra[2], rb[2];
-  float4 fa[2][2];  // A32 staging
+  float4 fa[4];  // A32 staging
   const int ea = A32 ? 4 : 2;  // bytes per A element
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
       A32 ? (void*)(p.a + (size_t)m0 * K) : (void*)(p.a16 + (size_t)m0 * K), (short)0,
@@ -572,13 +575,16 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
       const int r = sr + 128 * i, k = k0 + sk;
       const uint32_t off = (uint32_t)(r * K + k);
       const uint32_t va = k < K ? off * ea : 0x80000000u, vb = k < K ? off * 2 : 0x80000000u;
-      if (A32) {
-        fa[i][0] = __builtin_bit_cast(float4, ld(rsa, va, 0));
-        fa[i][1] = __builtin_bit_cast(float4, ld(rsa, va, 16));
-      } else {
-        ra[i] = ld(rsa, va, 0);
-      }
+      if (!A32) ra[i] = ld(rsa, va, 0);
       rb[i] = ld(rsb, vb, 0);
+    }
+    if (A32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int f = tid + 512 * i, r = f >> 3, k = k0 + 4 * (f & 7);
+        const uint32_t va = k < K ? (uint32_t)(r * K + k) * 4u : 0x80000000u;
+        fa[i] = __builtin_bit_cast(float4, ld(rsa, va, 0));
+      }
     }
   };
   auto lstore = [&](int buf) {
@@ -587,24 +593,21 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
       const int r = sr + 128 * i;
       // Column c = 64 g + 2 jj + t of the block lives at LDS row 64 g + 32 t + jj.
       const int br = (r & ~63) | ((r & 1) << 5) | ((r & 63) >> 1);
-      if (A32) {
-        const float4 x0 = fa[i][0], x1 = fa[i][1];
-        const uint4 hi = make_uint4(cvt_pk_bf16(x0.x, x0.y), cvt_pk_bf16(x0.z, x0.w),
-                                    cvt_pk_bf16(x1.x, x1.y), cvt_pk_bf16(x1.z, x1.w));
-        const float4 h0 = make_float4(__uint_as_float(hi.x << 16), __uint_as_float(hi.x & 0xFFFF0000u),
-                                      __uint_as_float(hi.y << 16), __uint_as_float(hi.y & 0xFFFF0000u));
-        const float4 h1 = make_float4(__uint_as_float(hi.z << 16), __uint_as_float(hi.z & 0xFFFF0000u),
-                                      __uint_as_float(hi.w << 16), __uint_as_float(hi.w & 0xFFFF0000u));
-        const uint4 lo = make_uint4(cvt_pk_bf16(x0.x - h0.x, x0.y - h0.y),
-                                    cvt_pk_bf16(x0.z - h0.z, x0.w - h0.w),
-                                    cvt_pk_bf16(x1.x - h1.x, x1.y - h1.y),
-                                    cvt_pk_bf16(x1.z - h1.z, x1.w - h1.w));
-        *reinterpret_cast<uint4*>(&As[0][buf][r][sk]) = hi;
-        *reinterpret_cast<uint4*>(&As[NA - 1][buf][r][sk]) = lo;
-      } else {
-        *reinterpret_cast<uint4*>(&As[0][buf][r][sk]) = ra[i];
-      }
+      if (!A32) *reinterpret_cast<uint4*>(&As[0][buf][r][sk]) = ra[i];
       *reinterpret_cast<uint4*>(&Bs[buf][br][sk]) = rb[i];
+    }
+    if (A32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int f = tid + 512 * i, r = f >> 3, k = 4 * (f & 7);
+        const float4 x = fa[i];
+        const uint2 hi = make_uint2(cvt_pk_bf16(x.x, x.y), cvt_pk_bf16(x.z, x.w));
+        const uint2 lo = make_uint2(
+            cvt_pk_bf16(x.x - __uint_as_float(hi.x << 16), x.y - __uint_as_float(hi.x & 0xFFFF0000u)),
+            cvt_pk_bf16(x.z - __uint_as_float(hi.y << 16), x.w - __uint_as_float(hi.y & 0xFFFF0000u)));
+        *reinterpret_cast<uint2*>(&As[0][buf][r][k]) = hi;
+        *reinterpret_cast<uint2*>(&As[NA - 1][buf][r][k]) = lo;
+      }
     }
   };
 
