@@ -558,8 +558,10 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
   // and pieces past K (given an offset outside the resource) read zeros
   // from the hardware.
   const int sr = tid >> 2, sk = (tid & 3) * 8;
-  uint4 ra[2], rb[2];
-  float4 fa[4];  // A32 staging
+  // Two register sets: the loads of step s + 2 are issued at the start of
+  // step s, and step s + 1's are stored to LDS after step s's MFMAs.
+  uint4 ra[2][2], rb[2][2];
+  float4 fa[2][4];  // A32 staging
   const int ea = A32 ? 4 : 2;  // bytes per A element
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
       A32 ? (void*)(p.a + (size_t)m0 * K) : (void*)(p.a16 + (size_t)m0 * K), (short)0,
@@ -569,38 +571,38 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
   auto ld = [](__amdgpu_buffer_rsrc_t rs, uint32_t vo, int so) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, so, 0));
   };
-  auto gload = [&](int k0) {
+  auto gload = [&](int k0, int set) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = sr + 128 * i, k = k0 + sk;
       const uint32_t off = (uint32_t)(r * K + k);
       const uint32_t va = k < K ? off * ea : 0x80000000u, vb = k < K ? off * 2 : 0x80000000u;
-      if (!A32) ra[i] = ld(rsa, va, 0);
-      rb[i] = ld(rsb, vb, 0);
+      if (!A32) ra[set][i] = ld(rsa, va, 0);
+      rb[set][i] = ld(rsb, vb, 0);
     }
     if (A32) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int f = tid + 512 * i, r = f >> 3, k = k0 + 4 * (f & 7);
         const uint32_t va = k < K ? (uint32_t)(r * K + k) * 4u : 0x80000000u;
-        fa[i] = __builtin_bit_cast(float4, ld(rsa, va, 0));
+        fa[set][i] = __builtin_bit_cast(float4, ld(rsa, va, 0));
       }
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, int set) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = sr + 128 * i;
       // Column c = 64 g + 2 jj + t of the block lives at LDS row 64 g + 32 t + jj.
       const int br = (r & ~63) | ((r & 1) << 5) | ((r & 63) >> 1);
-      if (!A32) *reinterpret_cast<uint4*>(&As[0][buf][r][sk]) = ra[i];
-      *reinterpret_cast<uint4*>(&Bs[buf][br][sk]) = rb[i];
+      if (!A32) *reinterpret_cast<uint4*>(&As[0][buf][r][sk]) = ra[set][i];
+      *reinterpret_cast<uint4*>(&Bs[buf][br][sk]) = rb[set][i];
     }
     if (A32) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int f = tid + 512 * i, r = f >> 3, k = 4 * (f & 7);
-        const float4 x = fa[i];
+        const float4 x = fa[set][i];
         const uint2 hi = make_uint2(cvt_pk_bf16(x.x, x.y), cvt_pk_bf16(x.z, x.w));
         const uint2 lo = make_uint2(
             cvt_pk_bf16(x.x - __uint_as_float(hi.x << 16), x.y - __uint_as_float(hi.x & 0xFFFF0000u)),
@@ -618,12 +620,15 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
     for (int t = 0; t < 2; ++t) acc[a][t] = zero16();
 
   const int nk = (K + BK - 1) / BK;
-  gload(0);
-  lstore(0);
+  gload(0, 0);
+  gload(BK, 1);
+  lstore(0, 0);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
+  // Step kt computes on LDS buffer kt % 2.  Steps past the end load zeros.
+  auto stepk = [&](int kt, int buf) {
+    __builtin_amdgcn_sched_barrier(0);
+    gload((kt + 2) * BK, buf);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8 bfr[2];
@@ -644,9 +649,15 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
           for (int t = 0; t < 2; ++t) acc[a][t] = mfma_bf16(af[a], bfr[t], acc[a][t]);
       }
     }
-    if (kt + 1 < nk) lstore(buf ^ 1);
+    lstore(buf ^ 1, buf ^ 1);
     __syncthreads();
+  };
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    stepk(kt, 0);
+    stepk(kt + 1, 1);
   }
+  if (kt < nk) stepk(kt, 0);
 
 #pragma unroll
   for (int a = 0; a < 4; ++a)
