@@ -136,18 +136,19 @@ def test_forward_errors(backend, pkg):
     f.close()
 
 
-@pytest.mark.parametrize("kind", ["h3", "x6"])
-def test_forward_split_matches_fp32_mfma(backend, pkg, ora, kind):
+@pytest.mark.parametrize("kind,vocab", [("h3", 300), ("h3", 301), ("x6", 300)])
+def test_forward_split_matches_fp32_mfma(backend, pkg, ora, kind, vocab):
     # The trainer forward's GEMMs (layers and the all-rows lm_head) on the
     # split kernels (h3, the default, or x6) and on the fp32 MFMAs: losses
     # and probabilities agree to fp32 rounding.  dim 64, 2 x 40 rows, vocab
-    # 300.
+    # 300, and 301 (an odd lm_head width: ragged last column tile, unpaired
+    # epilogue stores).
     M = pkg.hip.Model
-    cfg = pkg.ModelConfig.new(300, 64, 4, 2, 40)
+    cfg = pkg.ModelConfig.new(vocab, 64, 4, 2, 40)
     w = pkg.synthetic_weights(cfg, seed=64)
     B, S = 2, 40
-    toks = np.stack([ora.rand_tokens(S, 300, 300 + b) for b in range(B)])
-    tgts = np.stack([ora.rand_tokens(S, 300, 400 + b) for b in range(B)])
+    toks = np.stack([ora.rand_tokens(S, vocab, 300 + b) for b in range(B)])
+    tgts = np.stack([ora.rand_tokens(S, vocab, 400 + b) for b in range(B)])
     model = pkg.hip.Model(backend, cfg)
     model.upload(w)
     model.set_prefill_split(M.SPLIT_H3 if kind == "h3" else M.SPLIT_X6)
