@@ -116,6 +116,75 @@ __device__ __forceinline__ void epi_pair_gemm(const GemmParams& p, int M,
   }
 }
 
+// The epilogue of one 32-row MFMA tile pair as a lane holds it: rows
+// mbase + acc_row(r, h), r = 0..15, columns n and n + 1 (n even).  Every load
+// the epilogue needs (the residual of GEMM_ADD, the RoPE table and row map of
+// GEMM_QKV) is issued for all 16 rows before the first store: stores may
+// alias those loads as far as the compiler knows, so pair by pair each load
+// would wait out the previous store and its own latency in turn.
+template <int EPI>
+__device__ __forceinline__ void epi_tile(const GemmParams& p, int M, int N, int mbase, int n,
+                                         const float (&v0)[16], const float (&v1)[16]) {
+  const int h = (threadIdx.x & 63) >> 5;
+  if (EPI == GEMM_ADD && (N & 1) == 0 && n < N) {
+    float2 old[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = mbase + acc_row(r, h);
+      old[r] = m < M ? *reinterpret_cast<const float2*>(p.c + (size_t)m * N + n)
+                     : make_float2(0.f, 0.f);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = mbase + acc_row(r, h);
+      if (m < M)
+        *reinterpret_cast<float2*>(p.c + (size_t)m * N + n) =
+            make_float2(old[r].x + v0[r], old[r].y + v1[r]);
+    }
+    return;
+  }
+  if (EPI == GEMM_QKV && n < N) {
+    const int dim = p.dim, region = n / dim, c = n - region * dim;
+    const int i = (c % p.head_dim) >> 1, half_hd = p.head_dim >> 1;
+    int seq[16], t[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = min(mbase + acc_row(r, h), M - 1);
+      if (p.rowmap) {
+        const int2 st = p.rowmap[m];
+        seq[r] = st.x;
+        t[r] = st.y;
+      } else {
+        div_rows(m, p.S, seq[r], t[r]);
+      }
+    }
+    float2 cs[16];
+    if (region < 2) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) cs[r] = p.rope[(size_t)t[r] * half_hd + i];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = mbase + acc_row(r, h);
+      if (m >= M) continue;
+      float a = v0[r], b = v1[r];
+      if (region < 2) rope_pair(a, b, cs[r].x, cs[r].y);
+      float* dst;
+      if (region == 0)
+        dst = p.q_out + (size_t)m * dim + c;
+      else if (p.kv_packed)
+        dst = (region == 1 ? p.kcache : p.vcache) + (size_t)m * dim + c;
+      else
+        dst = (region == 1 ? p.kcache : p.vcache) + (size_t)seq[r] * p.seq_stride +
+              (size_t)t[r] * dim + c;
+      *reinterpret_cast<float2*>(dst) = make_float2(a, b);
+    }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) epi_pair_gemm<EPI>(p, M, N, mbase + acc_row(r, h), n, v0[r], v1[r]);
+}
+
 // C[M,N] = A[M,K] B[K,N], 128x128 block tile, BK = 16, 4 waves in 2x2,
 // each wave a 64x64 sub-tile as 2x2 MFMA 32x32 tiles.  A is staged
 // transposed in LDS so MFMA A-operand reads are contiguous; within a wave's
@@ -224,12 +293,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   }
 
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < 2; ++a) {
+    float v0[16], v1[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * 64 + a * 32 + acc_row(r, h);
-      const int n = n0 + wn * 64 + 2 * j;
-      epi_pair_gemm<EPI>(p, M, N, m, n, acc[a][0][r], acc[a][1][r]);
+      v0[r] = acc[a][0][r];
+      v1[r] = acc[a][1][r];
+    }
+    epi_tile<EPI>(p, M, N, m0 + wm * 64 + a * 32, n0 + wn * 64 + 2 * j, v0, v1);
     }
 }
 
@@ -660,12 +731,14 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
   if (kt < nk) stepk(kt, 0);
 
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < 4; ++a) {
+    float v0[16], v1[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * 128 + a * 32 + acc_row(r, h);
-      const int n = n0 + wn * 64 + 2 * j;
-      epi_pair_gemm<EPI>(p, M, N, m, n, acc[a][0][r], acc[a][1][r]);
+      v0[r] = acc[a][0][r];
+      v1[r] = acc[a][1][r];
+    }
+    epi_tile<EPI>(p, M, N, m0 + wm * 128 + a * 32, n0 + wn * 64 + 2 * j, v0, v1);
     }
 }
 
@@ -944,12 +1017,14 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_x6(GemmParams p) {
   if (kt < nk) step(0);  // odd step count: the last step sits in buffer 0
 
 #pragma unroll
-  for (int a = 0; a < TA; ++a)
+  for (int a = 0; a < TA; ++a) {
+    float v0[16], v1[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * (32 * TA) + a * 32 + acc_row(r, h);
-      const int n = n0 + wn * 64 + 2 * j;
-      epi_pair_gemm<EPI>(p, M, N, m, n, acc[a][0][r], acc[a][1][r]);
+      v0[r] = acc[a][0][r];
+      v1[r] = acc[a][1][r];
+    }
+    epi_tile<EPI>(p, M, N, m0 + wm * (32 * TA) + a * 32, n0 + wn * 64 + 2 * j, v0, v1);
     }
 }
 
@@ -1117,15 +1192,15 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void k_gemm_h3(GemmParams p) {
 
   bool finite = true;
 #pragma unroll
-  for (int a = 0; a < TA; ++a)
+  for (int a = 0; a < TA; ++a) {
+    float v0[16], v1[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = m0 + wm * (32 * TA) + a * 32 + acc_row(r, h);
-      const int n = n0 + wn * 64 + 2 * j;
-      const float v0 = acc[a][0][r] + cor[a][0][r] * 0x1p-11f;
-      const float v1 = acc[a][1][r] + cor[a][1][r] * 0x1p-11f;
-      finite = finite && __builtin_isfinite(v0) && __builtin_isfinite(v1);
-      epi_pair_gemm<EPI>(p, M, N, m, n, v0, v1);
+      v0[r] = acc[a][0][r] + cor[a][0][r] * 0x1p-11f;
+      v1[r] = acc[a][1][r] + cor[a][1][r] * 0x1p-11f;
+      finite = finite && __builtin_isfinite(v0[r]) && __builtin_isfinite(v1[r]);
+    }
+    epi_tile<EPI>(p, M, N, m0 + wm * (32 * TA) + a * 32, n0 + wn * 64 + 2 * j, v0, v1);
     }
   if (!finite) *p.range_flag = 1;
 }
