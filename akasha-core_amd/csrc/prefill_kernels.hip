@@ -20,40 +20,47 @@ __global__ void k_embedding_rows(const uint32_t* tokens, const float* table,
 }
 
 // RMSNorm of every row (cpu.rs:205-222), one 256-thread block per row.
-// Rows of up to 4096 floats (a multiple of 4) stay in registers between the
-// sum of squares and the scaling, read and written 16 bytes at a time, and
-// each thread's gain loads are issued before its stores; other sizes go
-// element by element.
+// Rows of up to 4096 floats (a multiple of 4): one wave per row, four rows
+// per block, the row held in registers between the sum of squares (a wave
+// butterfly, no LDS or barrier) and the scaling, read and written 16 bytes
+// at a time.  Other sizes: one block per row, element by element.
+template <int QL>  // float4 per lane: size <= 256 QL
 __global__ __launch_bounds__(256) void k_rows_rmsnorm(const float* __restrict__ x,
                                                       const float* __restrict__ w,
-                                                      float* __restrict__ out, int size,
-                                                      float eps) {
-  __shared__ float red4[4];
-  const float* xr = x + (size_t)blockIdx.x * size;
-  float* o = out + (size_t)blockIdx.x * size;
-  float ss = 0.f;
-  if ((size & 3) == 0 && size <= 4096) {
+                                                      float* __restrict__ out, int rows,
+                                                      int size, float eps) {
+  if (QL > 0) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * size);
+    float4* o = reinterpret_cast<float4*>(out + (size_t)row * size);
+    const float4* g4 = reinterpret_cast<const float4*>(w);
     const int nq = size >> 2;
-    float4 v[4], g[4];
+    float4 v[QL > 0 ? QL : 1], g[QL > 0 ? QL : 1];
+    float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = threadIdx.x + 256 * i;
-      v[i] = q < nq ? reinterpret_cast<const float4*>(xr)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-      g[i] = q < nq ? reinterpret_cast<const float4*>(w)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < QL; ++i) {
+      const int q = lane + 64 * i;
+      v[i] = q < nq ? xr[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      g[i] = q < nq ? g4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
       ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
     }
-    ss = block_sum256(ss, red4);
+    ss = wave_sum(ss);
     const float rs = 1.0f / sqrtf(ss / (float)size + eps);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = threadIdx.x + 256 * i;
+    for (int i = 0; i < QL; ++i) {
+      const int q = lane + 64 * i;
       if (q < nq)
-        reinterpret_cast<float4*>(o)[q] = make_float4(
+        o[q] = make_float4(
             __fmul_rn(__fmul_rn(v[i].x, rs), g[i].x), __fmul_rn(__fmul_rn(v[i].y, rs), g[i].y),
             __fmul_rn(__fmul_rn(v[i].z, rs), g[i].z), __fmul_rn(__fmul_rn(v[i].w, rs), g[i].w));
     }
     return;
   }
+  __shared__ float red4[4];
+  const float* xr = x + (size_t)blockIdx.x * size;
+  float* o = out + (size_t)blockIdx.x * size;
+  float ss = 0.f;
   for (int c = threadIdx.x; c < size; c += 256) ss += xr[c] * xr[c];
   ss = block_sum256(ss, red4);
   const float rs = 1.0f / sqrtf(ss / (float)size + eps);
@@ -2295,8 +2302,15 @@ hipError_t launch_flash_bf16(const FlashParams& p, int batch, int max_rows, hipS
 
 hipError_t launch_rows_rmsnorm(const float* x, const float* w, float* out,
                                int rows, int size, float eps, hipStream_t s) {
-  hipLaunchKernelGGL(k_rows_rmsnorm, dim3(rows), dim3(256), 0, s, x, w, out,
-                     size, eps);
+  const dim3 g((rows + 3) / 4);
+  if (size % 4 != 0 || size > 4096)
+    hipLaunchKernelGGL(k_rows_rmsnorm<0>, dim3(rows), dim3(256), 0, s, x, w, out, rows, size, eps);
+  else if (size <= 1024)
+    hipLaunchKernelGGL(k_rows_rmsnorm<4>, g, dim3(256), 0, s, x, w, out, rows, size, eps);
+  else if (size <= 2048)
+    hipLaunchKernelGGL(k_rows_rmsnorm<8>, g, dim3(256), 0, s, x, w, out, rows, size, eps);
+  else
+    hipLaunchKernelGGL(k_rows_rmsnorm<16>, g, dim3(256), 0, s, x, w, out, rows, size, eps);
   return hipGetLastError();
 }
 
