@@ -114,9 +114,10 @@ __device__ __forceinline__ uint32_t cvt_pk_f16(float lo, float hi) {
 // Eight floats as two fp16 octets with x = hi + 2^-11 lo to within 2^-22 |x|
 // (the scaled-residual split of Ootomo and Yokota, IJHPCA 2022): hi rounds x
 // to 11 significant bits, the remainder x - hi is exact and at most 2^-11 |x|,
-// and lo rounds it scaled by 2^11.  Below fp16's normal range hi is
-// subnormal, which the fp16 MFMAs take exactly (checked on gfx950), and lo
-// still carries the remainder; |x| >= 65520 gives an infinite hi.
+// and lo rounds it scaled by 2^11.  Below fp16's normal range (|x| < 2^-14)
+// hi is subnormal, which the fp16 MFMAs take exactly (checked on gfx950), and
+// lo still carries the remainder, so the error stays below 2^-36 there;
+// |x| >= 65520 gives an infinite hi.
 __device__ __forceinline__ void split2_f16(float4 x0, float4 x1, uint4& hi, uint4& lo) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
