@@ -1245,7 +1245,8 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void k_gemm_h3(GemmParams p) {
 // into LDS per key block); P^T feeds O^T += V^T P^T from the accumulator
 // registers: MFMA 0 of a 32-key block takes accumulator entries 0..7 of each
 // lane (keys acc_row(0..7, h)), MFMA 1 entries 8..15, and the V^T fragment
-// reads the same keys, two runs of four.  Softmax statistics are fp32; the
+// reads the same keys, one 16-byte run (V^T keys are stored with bits 2 and
+// 3 of their index swapped).  Softmax statistics are fp32; the
 // output is bfloat16.
 template <int HD>
 __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
@@ -1315,20 +1316,23 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
     for (int i = 0; i < KPT; ++i)
       *reinterpret_cast<uint2*>(&Ks[sk + i][sc]) =
           make_uint2(pack_bf16x2(kr[i].x, kr[i].y), pack_bf16x2(kr[i].z, kr[i].w));
+    // V^T keys at their permuted positions (bits 2 and 3 of the key swapped,
+    // so the eight keys an MFMA lane takes are one 16-byte run).
+    const int vk = (sk & ~12) | ((sk >> 1) & 4) | ((sk << 1) & 8);
     if constexpr (KPT == 4) {
-      *reinterpret_cast<uint2*>(&Vt[sc][sk]) =
+      *reinterpret_cast<uint2*>(&Vt[sc][vk]) =
           make_uint2(pack_bf16x2(vr[0].x, vr[1].x), pack_bf16x2(vr[2].x, vr[3].x));
-      *reinterpret_cast<uint2*>(&Vt[sc + 1][sk]) =
+      *reinterpret_cast<uint2*>(&Vt[sc + 1][vk]) =
           make_uint2(pack_bf16x2(vr[0].y, vr[1].y), pack_bf16x2(vr[2].y, vr[3].y));
-      *reinterpret_cast<uint2*>(&Vt[sc + 2][sk]) =
+      *reinterpret_cast<uint2*>(&Vt[sc + 2][vk]) =
           make_uint2(pack_bf16x2(vr[0].z, vr[1].z), pack_bf16x2(vr[2].z, vr[3].z));
-      *reinterpret_cast<uint2*>(&Vt[sc + 3][sk]) =
+      *reinterpret_cast<uint2*>(&Vt[sc + 3][vk]) =
           make_uint2(pack_bf16x2(vr[0].w, vr[1].w), pack_bf16x2(vr[2].w, vr[3].w));
     } else {
-      *reinterpret_cast<uint32_t*>(&Vt[sc][sk]) = pack_bf16x2(vr[0].x, vr[1].x);
-      *reinterpret_cast<uint32_t*>(&Vt[sc + 1][sk]) = pack_bf16x2(vr[0].y, vr[1].y);
-      *reinterpret_cast<uint32_t*>(&Vt[sc + 2][sk]) = pack_bf16x2(vr[0].z, vr[1].z);
-      *reinterpret_cast<uint32_t*>(&Vt[sc + 3][sk]) = pack_bf16x2(vr[0].w, vr[1].w);
+      *reinterpret_cast<uint32_t*>(&Vt[sc][vk]) = pack_bf16x2(vr[0].x, vr[1].x);
+      *reinterpret_cast<uint32_t*>(&Vt[sc + 1][vk]) = pack_bf16x2(vr[0].y, vr[1].y);
+      *reinterpret_cast<uint32_t*>(&Vt[sc + 2][vk]) = pack_bf16x2(vr[0].z, vr[1].z);
+      *reinterpret_cast<uint32_t*>(&Vt[sc + 3][vk]) = pack_bf16x2(vr[0].w, vr[1].w);
     }
     __syncthreads();
     load_kv(kb + 1);  // rows past S read row 0: harmless, never used
@@ -1380,12 +1384,8 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const uint16_t* vrow = Vt[32 * t + j];
-      const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
-      const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
-      const uint2 a2 = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * h);
-      const uint2 a3 = *reinterpret_cast<const uint2*>(vrow + 24 + 4 * h);
-      o[t] = mfma_bf16(bf16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y)), p0, o[t]);
-      o[t] = mfma_bf16(bf16x8_of(make_uint4(a2.x, a2.y, a3.x, a3.y)), p1, o[t]);
+      o[t] = mfma_bf16(bf16x8_of(*reinterpret_cast<const uint4*>(vrow + 8 * h)), p0, o[t]);
+      o[t] = mfma_bf16(bf16x8_of(*reinterpret_cast<const uint4*>(vrow + 16 + 8 * h)), p1, o[t]);
     }
   }
 
@@ -1507,7 +1507,10 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
       for (int pl = 0; pl < 3; ++pl)
         *reinterpret_cast<uint2*>(&Ks(pl)[sk + i][sc]) = make_uint2(lo[pl], hi[pl]);
     }
-    // V^T: dim row sc + c, keys sk .. sk + KPT - 1.
+    // V^T: dim row sc + c, keys sk .. sk + KPT - 1 at their permuted
+    // positions (bits 2 and 3 of the key swapped, so the eight keys an MFMA
+    // lane takes, acc_row(8 half .. 8 half + 7, h), are one 16-byte run).
+    const int vk = (sk & ~12) | ((sk >> 1) & 4) | ((sk << 1) & 8);
     const float vc[4][4] = {
 #define AKH_VCOL(f) {vr[0].f, vr[1].f, KPT == 4 ? vr[KPT - 2].f : 0.f, KPT == 4 ? vr[KPT - 1].f : 0.f}
         AKH_VCOL(x), AKH_VCOL(y), AKH_VCOL(z), AKH_VCOL(w)
@@ -1521,11 +1524,11 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
         split_pair(vc[c][2], vc[c][3], t23);
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl)
-          *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][sk]) = make_uint2(t01[pl], t23[pl]);
+          *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][vk]) = make_uint2(t01[pl], t23[pl]);
       } else {
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl)
-          *reinterpret_cast<uint32_t*>(&Vt(pl)[sc + c][sk]) = t01[pl];
+          *reinterpret_cast<uint32_t*>(&Vt(pl)[sc + c][vk]) = t01[pl];
       }
     }
     __syncthreads();
@@ -1594,15 +1597,12 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        // V^T rows of the same keys: two runs of four.
+        // V^T rows of the same keys: one 16-byte run at their permuted positions.
         bf16x8 vf[3];
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) {
-          const uint16_t* vrow = Vt(pl)[32 * t + j] + 16 * half;
-          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
-          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
-          vf[pl] = bf16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
-        }
+        for (int pl = 0; pl < 3; ++pl)
+          vf[pl] = bf16x8_of(
+              *reinterpret_cast<const uint4*>(Vt(pl)[32 * t + j] + 16 * half + 8 * h));
         o[t] = mfma_bf16(vf[2], bf16x8_of(pf[half][0]), o[t]);
         o[t] = mfma_bf16(vf[1], bf16x8_of(pf[half][1]), o[t]);
         o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][2]), o[t]);
@@ -1742,7 +1742,10 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
       for (int pl = 0; pl < 2; ++pl)
         *reinterpret_cast<uint2*>(&Ks(pl)[sk + i][sc]) = make_uint2(lo[pl], hi[pl]);
     }
-    // V^T: dim row sc + c, keys sk .. sk + KPT - 1.
+    // V^T: dim row sc + c, keys sk .. sk + KPT - 1 at their permuted
+    // positions (bits 2 and 3 of the key swapped, so the eight keys an MFMA
+    // lane takes, acc_row(8 half .. 8 half + 7, h), are one 16-byte run).
+    const int vk = (sk & ~12) | ((sk >> 1) & 4) | ((sk << 1) & 8);
     const float vc[4][4] = {
 #define AKH_VCOL(f) {vr[0].f, vr[1].f, KPT == 4 ? vr[KPT - 2].f : 0.f, KPT == 4 ? vr[KPT - 1].f : 0.f}
         AKH_VCOL(x), AKH_VCOL(y), AKH_VCOL(z), AKH_VCOL(w)
@@ -1756,11 +1759,11 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
         split_v(vc[c][2], vc[c][3], t23);
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl)
-          *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][sk]) = make_uint2(t01[pl], t23[pl]);
+          *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][vk]) = make_uint2(t01[pl], t23[pl]);
       } else {
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl)
-          *reinterpret_cast<uint32_t*>(&Vt(pl)[sc + c][sk]) = t01[pl];
+          *reinterpret_cast<uint32_t*>(&Vt(pl)[sc + c][vk]) = t01[pl];
       }
     }
     __syncthreads();
@@ -1828,14 +1831,12 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        // V^T rows of the same keys: two runs of four.
+        // V^T rows of the same keys: one 16-byte run at their permuted positions.
         f16x8 vf[3];
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl) {
-          const uint16_t* vrow = Vt(pl)[32 * t + j] + 16 * half;
-          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
-          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
-          vf[pl] = f16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
+          vf[pl] = f16x8_of(
+              *reinterpret_cast<const uint4*>(Vt(pl)[32 * t + j] + 16 * half + 8 * h));
         }
         // Smallest terms first: p1 (2^-11 v0), p0 v1, then p0 v0.
         o[t] = mfma_f16(vf[2], f16x8_of(pf[half][1]), o[t]);
@@ -1978,10 +1979,14 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
         const float x1 = c == 0 ? e.x : c == 1 ? e.y : c == 2 ? e.z : e.w;
         split_pair(x0, x1, t[g]);
       }
+      // Keys sk .. sk + 7 at their permuted positions (bits 2 and 3 of the
+      // key swapped; see k_flash_x6): two runs of four.
 #pragma unroll
-      for (int pl = 0; pl < 3; ++pl)
-        *reinterpret_cast<uint4*>(&Vt(pl)[sc + c][sk]) =
-            make_uint4(t[0][pl], t[1][pl], t[2][pl], t[3][pl]);
+      for (int pl = 0; pl < 3; ++pl) {
+        const int k0 = (sk & ~12) | ((sk >> 1) & 4) | ((sk << 1) & 8), k1 = k0 + 8;
+        *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][k0]) = make_uint2(t[0][pl], t[1][pl]);
+        *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][k1]) = make_uint2(t[2][pl], t[3][pl]);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the writes have landed
     __builtin_amdgcn_wave_barrier();
@@ -2048,12 +2053,9 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
       for (int half = 0; half < 2; ++half) {
         bf16x8 vf[3];
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) {
-          const uint16_t* vrow = Vt(pl)[32 * t + j] + 16 * half;
-          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
-          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
-          vf[pl] = bf16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
-        }
+        for (int pl = 0; pl < 3; ++pl)
+          vf[pl] = bf16x8_of(
+              *reinterpret_cast<const uint4*>(Vt(pl)[32 * t + j] + 16 * half + 8 * h));
         o[t] = mfma_bf16(vf[2], bf16x8_of(pf[half][0]), o[t]);
         o[t] = mfma_bf16(vf[1], bf16x8_of(pf[half][1]), o[t]);
         o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][2]), o[t]);
