@@ -1979,14 +1979,10 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
         const float x1 = c == 0 ? e.x : c == 1 ? e.y : c == 2 ? e.z : e.w;
         split_pair(x0, x1, t[g]);
       }
-      // Keys sk .. sk + 7 at their permuted positions (bits 2 and 3 of the
-      // key swapped; see k_flash_x6): two runs of four.
 #pragma unroll
-      for (int pl = 0; pl < 3; ++pl) {
-        const int k0 = (sk & ~12) | ((sk >> 1) & 4) | ((sk << 1) & 8), k1 = k0 + 8;
-        *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][k0]) = make_uint2(t[0][pl], t[1][pl]);
-        *reinterpret_cast<uint2*>(&Vt(pl)[sc + c][k1]) = make_uint2(t[2][pl], t[3][pl]);
-      }
+      for (int pl = 0; pl < 3; ++pl)
+        *reinterpret_cast<uint4*>(&Vt(pl)[sc + c][sk]) =
+            make_uint4(t[0][pl], t[1][pl], t[2][pl], t[3][pl]);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the writes have landed
     __builtin_amdgcn_wave_barrier();
@@ -2051,11 +2047,17 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
+        // V^T rows of the same keys: two runs of four (the staging writes
+        // eight consecutive keys per lane; k_flash_x6's permuted layout,
+        // which would split them, measured slower here).
         bf16x8 vf[3];
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
-          vf[pl] = bf16x8_of(
-              *reinterpret_cast<const uint4*>(Vt(pl)[32 * t + j] + 16 * half + 8 * h));
+        for (int pl = 0; pl < 3; ++pl) {
+          const uint16_t* vrow = Vt(pl)[32 * t + j] + 16 * half;
+          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
+          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
+          vf[pl] = bf16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
+        }
         o[t] = mfma_bf16(vf[2], bf16x8_of(pf[half][0]), o[t]);
         o[t] = mfma_bf16(vf[1], bf16x8_of(pf[half][1]), o[t]);
         o[t] = mfma_bf16(vf[0], bf16x8_of(pf[half][2]), o[t]);
