@@ -136,15 +136,17 @@ def test_forward_errors(backend, pkg):
     f.close()
 
 
-@pytest.mark.parametrize("kind,vocab", [("h3", 300), ("h3", 301), ("x6", 300)])
-def test_forward_split_matches_fp32_mfma(backend, pkg, ora, kind, vocab):
+@pytest.mark.parametrize("kind,vocab,dim", [("h3", 300, 64), ("h3", 301, 64), ("x6", 300, 64),
+                                            ("h3", 300, 72), ("x6", 300, 72)])
+def test_forward_split_matches_fp32_mfma(backend, pkg, ora, kind, vocab, dim):
     # The trainer forward's GEMMs (layers and the all-rows lm_head) on the
     # split kernels (h3, the default, or x6) and on the fp32 MFMAs: losses
-    # and probabilities agree to fp32 rounding.  dim 64, 2 x 40 rows, vocab
+    # and probabilities agree to fp32 rounding.  2 x 40 rows; dim 64, vocab
     # 300, and 301 (an odd lm_head width: ragged last column tile, unpaired
-    # epilogue stores).
+    # epilogue stores); dim 72 (4 heads of 18): every GEMM's K = 72 or 288
+    # ends on a partial 32-k step of the split kernels.
     M = pkg.hip.Model
-    cfg = pkg.ModelConfig.new(vocab, 64, 4, 2, 40)
+    cfg = pkg.ModelConfig.new(vocab, dim, 4, 2, 40)
     w = pkg.synthetic_weights(cfg, seed=64)
     B, S = 2, 40
     toks = np.stack([ora.rand_tokens(S, vocab, 300 + b) for b in range(B)])
