@@ -132,6 +132,9 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
 #ifndef AKH_GEMM_NT
 #define AKH_GEMM_NT 1
 #endif
+#ifndef AKH_DEC_PIPE
+#define AKH_DEC_PIPE 1
+#endif
 #ifndef AKH_LM_GEMM_NT
 #define AKH_LM_GEMM_NT 0
 #endif
@@ -166,6 +169,81 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   f32x16 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
+  if constexpr (PRO == PRO_NONE && MT == 1 && AKH_DEC_PIPE) {
+    // Plain A, one row tile: the loads of pass i + 1 are issued before the
+    // MFMAs of pass i, so a block waits on one memory round trip, not one per
+    // pass.  Loads past K read the block's last valid quad (clamped, always
+    // issued, so the wait counts are static) and are zeroed where they are
+    // used.  Measured on MI355X: config 4's qkv 5.5 -> 4.9 us, ffn_up 5.7 ->
+    // 5.3 us, its step 0.641 -> 0.632 ms.  With two row tiles the second
+    // register set costs occupancy: config 5's qkv went 13.7 -> 15.4 us and
+    // its lm_head 82 -> 97 us, so two-tile blocks keep the loop below.
+    constexpr bool kNT = AKH_GEMM_NT && (AKH_LM_GEMM_NT || EPI != DEC_LOGITS);
+    using WRaw = typename std::conditional<BF, uint4, float4>::type;
+    constexpr int NW = BF ? HQ / 2 : HQ;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int kqe = (ke >> 2) - 1;  // last valid k-quad
+    WRaw wc[2][NW];
+    float4 a[2][MT][HQ];
+    auto load_pass = [&](int k0, int set) {
+      const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const int kq = min(kq0 + (BF ? 2 * i : i), BF ? (kqe & ~1) : kqe);
+        const f4* src = reinterpret_cast<const f4*>(
+            BF ? static_cast<const void*>(wh + (size_t)kq * 128)
+               : static_cast<const void*>(wt + (size_t)kq * 128));
+        wc[set][i] = __builtin_bit_cast(WRaw, kNT ? __builtin_nontemporal_load(src) : *src);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q = 0; q < HQ; ++q) {
+          const int kq = min(kq0 + q, kqe);
+          a[set][mt][q] = *reinterpret_cast<const float4*>(
+              p.xt + (size_t)mt * 32 * K + ((size_t)kq * 32 + j) * 4);
+        }
+    };
+    auto mma_pass = [&](int k0, int set) {
+      const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (BF) {
+#pragma unroll
+          for (int q = 0; q < HQ; q += 2) {
+            const bool in = 4 * (kq0 + q) < ke, in1 = 4 * (kq0 + q + 1) < ke;
+            const bf16x8 w8 = bf16x8_of(in ? wc[set][q / 2] : make_uint4(0u, 0u, 0u, 0u));
+            uint4 hi, mid, lo;
+            split3_bf16(in ? a[set][mt][q] : z, in1 ? a[set][mt][q + 1] : z, hi, mid, lo);
+            acc[mt] = mfma_bf16(bf16x8_of(hi), w8, acc[mt]);
+            acc[mt] = mfma_bf16(bf16x8_of(mid), w8, acc[mt]);
+            acc[mt] = mfma_bf16(bf16x8_of(lo), w8, acc[mt]);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < HQ; ++q) {
+            const bool in = 4 * (kq0 + q) < ke;
+            const float4 x = in ? a[set][mt][q] : z, w = in ? wc[set][q] : z;
+            acc[mt] = mfma32(x.x, w.x, acc[mt]);
+            acc[mt] = mfma32(x.y, w.y, acc[mt]);
+            acc[mt] = mfma32(x.z, w.z, acc[mt]);
+            acc[mt] = mfma32(x.w, w.w, acc[mt]);
+          }
+        }
+      }
+    };
+    const int np = (ke - kb + KC - 1) / KC;  // passes of this block
+    load_pass(kb, 0);
+    int i = 0;
+    for (; i + 2 <= np; i += 2) {
+      load_pass(kb + (i + 1) * KC, 1);
+      mma_pass(kb + i * KC, 0);
+      if (i + 2 < np) load_pass(kb + (i + 2) * KC, 0);
+      mma_pass(kb + (i + 1) * KC, 1);
+    }
+    if (i < np) mma_pass(kb + i * KC, 0);
+  } else
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;  // first k-quad of this half
     // PRO_NORM: the RMSNorm scale of every row from the residual's
