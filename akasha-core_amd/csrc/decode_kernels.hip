@@ -138,7 +138,7 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
 #ifndef AKH_LM_GEMM_NT
 #define AKH_LM_GEMM_NT 0
 #endif
-template <int W, int HL, int EPI, int PRO, bool BF, int MT>
+template <int W, int HL, int EPI, int PRO, bool BF, int MT, int NT = 1>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   constexpr int KC = 2 * W * HL;
   constexpr int HQ = HL / 4;
@@ -148,6 +148,9 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16, "W must be a power of 2 <= 16");
   static_assert(MT == 1 || MT == 2, "one or two row tiles");
   static_assert(EPI != DEC_RESID || W > 1, "the residual epilogue reduces across waves");
+  static_assert(NT == 1 || NT == 2, "one or two column tiles");
+  static_assert(NT == 1 || (EPI != DEC_RESID && PRO != PRO_NORM),
+                "the residual epilogue and the norm prologue work per column tile");
   __shared__ float red[W][32][33];
   // PRO_NORM: per-row sums of four column tiles, and the rows' scales.
   __shared__ float nsum[PRO == PRO_NORM ? R : 1][33];
@@ -157,19 +160,23 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   const int M = p.M, N = p.N, K = p.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, h = lane >> 5;
-  const int tile = blockIdx.x, col = tile * 32 + j;
-  const bool cok = col < N;
+  // The block's column tiles: tile, tile + 1, ... tile + NT - 1.
+  const int ntiles = (N + 31) / 32;
+  const int tile = blockIdx.x * NT;
   const int rows = p.kpass * KC;  // whole passes per block
   const int kb = blockIdx.y * rows;
   if (kb >= K) return;
   const int ke = min(K, kb + rows);
   const float* wt = p.w + (size_t)tile * p.Kp * 32 + j * 4;
   const uint16_t* wh = reinterpret_cast<const uint16_t*>(p.w) + (size_t)tile * p.Kp * 32 + j * 8;
+  // Offset of column tile tile + nt's weights from wt / wh (elements); a
+  // tile past the last reads the last one's and stores nothing.
+  auto wofs = [&](int nt) { return (size_t)(min(tile + nt, ntiles - 1) - tile) * p.Kp * 32; };
 
-  f32x16 acc[MT];
+  f32x16 acc[MT * NT];  // [row tile][column tile]
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
-  if constexpr (PRO == PRO_NONE && MT == 1 && AKH_DEC_PIPE) {
+  for (int i = 0; i < MT * NT; ++i) acc[i] = zero16();
+  if constexpr (PRO == PRO_NONE && MT == 1 && NT == 1 && AKH_DEC_PIPE) {
     // Plain A, one row tile: the loads of pass i + 1 are issued before the
     // MFMAs of pass i, so a block waits on one memory round trip, not one per
     // pass.  Loads past K read the block's last valid quad (clamped, always
@@ -272,15 +279,18 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
     using WRaw = typename std::conditional<BF, uint4, float4>::type;
     constexpr int NW = BF ? HQ / 2 : HQ;
     typedef float f4 __attribute__((ext_vector_type(4)));
-    WRaw wc[NW];
+    WRaw wc[NT][NW];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
       const int kq = kq0 + (BF ? 2 * i : i);  // BF: even, HL is a multiple of 8
-      const f4* src = reinterpret_cast<const f4*>(BF ? static_cast<const void*>(wh + (size_t)kq * 128)
-                                                     : static_cast<const void*>(wt + (size_t)kq * 128));
+      const size_t wo = wofs(nt) + (size_t)kq * 128;
+      const f4* src = reinterpret_cast<const f4*>(BF ? static_cast<const void*>(wh + wo)
+                                                     : static_cast<const void*>(wt + wo));
       const f4 t = 4 * kq < ke ? (kNT ? __builtin_nontemporal_load(src) : *src)
                                : f4{0.f, 0.f, 0.f, 0.f};
-      wc[i] = __builtin_bit_cast(WRaw, t);
+      wc[nt][i] = __builtin_bit_cast(WRaw, t);
     }
     float4 g[HQ];  // PRO_NORM: the gain of the pass's k
     if constexpr (PRO == PRO_NORM) {
@@ -371,26 +381,34 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
         }
       }
     }
+    // Each split of A feeds the MFMAs of all NT column tiles.
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       if constexpr (BF) {
 #pragma unroll
         for (int q = 0; q < HQ; q += 2) {
-          const bf16x8 w8 = bf16x8_of(wc[q / 2]);
           uint4 hi, mid, lo;
           split3_bf16(a[mt][q], a[mt][q + 1], hi, mid, lo);
-          acc[mt] = mfma_bf16(bf16x8_of(hi), w8, acc[mt]);
-          acc[mt] = mfma_bf16(bf16x8_of(mid), w8, acc[mt]);
-          acc[mt] = mfma_bf16(bf16x8_of(lo), w8, acc[mt]);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            f32x16& c = acc[mt * NT + nt];
+            const bf16x8 w8 = bf16x8_of(wc[nt][q / 2]);
+            c = mfma_bf16(bf16x8_of(hi), w8, c);
+            c = mfma_bf16(bf16x8_of(mid), w8, c);
+            c = mfma_bf16(bf16x8_of(lo), w8, c);
+          }
         }
       } else {
 #pragma unroll
-        for (int q = 0; q < HQ; ++q) {
-          acc[mt] = mfma32(a[mt][q].x, wc[q].x, acc[mt]);
-          acc[mt] = mfma32(a[mt][q].y, wc[q].y, acc[mt]);
-          acc[mt] = mfma32(a[mt][q].z, wc[q].z, acc[mt]);
-          acc[mt] = mfma32(a[mt][q].w, wc[q].w, acc[mt]);
-        }
+        for (int q = 0; q < HQ; ++q)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            f32x16& c = acc[mt * NT + nt];
+            c = mfma32(a[mt][q].x, wc[nt][q].x, c);
+            c = mfma32(a[mt][q].y, wc[nt][q].y, c);
+            c = mfma32(a[mt][q].z, wc[nt][q].z, c);
+            c = mfma32(a[mt][q].w, wc[nt][q].w, c);
+          }
       }
     }
   }
@@ -399,16 +417,18 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
     // Partial tiles: every wave's 32x32 tile goes to LDS behind one barrier,
     // then wave w sums rows [w * 32 / W, (w + 1) * 32 / W) over the waves in
     // index order and stores them (lane: column j, rows h, h + 2, ...).
-    // Row tile by row tile, one barrier before each tile's reads and one
-    // before the next tile overwrites the LDS.
+    // Tile by tile (row tiles, then column tiles within each), one barrier
+    // before each tile's reads and one before the next tile overwrites the
+    // LDS.
     constexpr int RW = 32 / W;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (mt > 0) __syncthreads();
+    for (int pi = 0; pi < MT * NT; ++pi) {
+      const int mt = pi / NT, ct = tile + pi % NT, cl = ct * 32 + j;
+      if (pi > 0) __syncthreads();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[wave][acc_row(r, h)][j] = acc[mt][r];
+      for (int r = 0; r < 16; ++r) red[wave][acc_row(r, h)][j] = acc[pi][r];
       __syncthreads();
-      if (cok) {
+      if (cl < N) {
 #pragma unroll
         for (int i = 0; i < RW / 2; ++i) {
           const int ml = wave * RW + h + 2 * i, m = mt * 32 + ml;
@@ -419,24 +439,24 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
             // One split: the block holds whole sums.  Residual add, and the
             // row's sum of squares over the tile's 32 columns (a butterfly
             // over the half-wave; lane 0's result is stored).
-            float* rp = p.res + (size_t)mt * 32 * N + kq_index(ml, col);
+            float* rp = p.res + (size_t)mt * 32 * N + kq_index(ml, cl);
             const float r = *rp + v;
             *rp = r;
             float q2 = r * r;
 #pragma unroll
             for (int o = 16; o > 0; o >>= 1) q2 += __shfl_xor(q2, o, 64);
-            if (j == 0) p.ssq_out[(size_t)m * (N >> 5) + tile] = q2;
+            if (j == 0) p.ssq_out[(size_t)m * (N >> 5) + ct] = q2;
           } else if (EPI == DEC_PART)
-            p.y[((size_t)blockIdx.y * R + m) * N + col] = v;
+            p.y[((size_t)blockIdx.y * R + m) * N + cl] = v;
           else if (EPI == DEC_PART_T)
-            p.y[((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, col)] = v;
+            p.y[((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, cl)] = v;
           else if (EPI == DEC_RESID)
             // Written through to device scope (a relaxed agent-scope atomic
             // store): no cache write-back is needed before the count below.
-            __hip_atomic_store(p.y + ((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, col),
+            __hip_atomic_store(p.y + ((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, cl),
                                v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           else
-            p.y[(size_t)mt * 32 * N + kq_index(ml, col)] = silu(v);
+            p.y[(size_t)mt * 32 * N + kq_index(ml, cl)] = silu(v);
         }
       }
     }
@@ -505,39 +525,41 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
     return;
   }
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+  for (int pi = 0; pi < MT * NT; ++pi) {
+    const int mt = pi / NT, ct = tile + pi % NT, cl = ct * 32 + j;
+    const bool ck = cl < N;
     if (W > 1) {
       for (int half = W / 2; half >= 1; half >>= 1) {
         __syncthreads();
         if (wave >= half && wave < 2 * half)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) red[wave - half][acc_row(r, h)][j] = acc[mt][r];
+          for (int r = 0; r < 16; ++r) red[wave - half][acc_row(r, h)][j] = acc[pi][r];
         __syncthreads();
         if (wave < half)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[mt][r] += red[wave][acc_row(r, h)][j];
+          for (int r = 0; r < 16; ++r) acc[pi][r] += red[wave][acc_row(r, h)][j];
       }
     }
     if (wave != 0) continue;
 
     float bv = -INFINITY;
-    uint32_t bi = (uint32_t)col;
+    uint32_t bi = (uint32_t)cl;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int ml = acc_row(r, h), m = mt * 32 + ml;
       if (EPI == DEC_PART) {
-        if (cok) p.y[((size_t)blockIdx.y * R + m) * N + col] = acc[mt][r];
+        if (ck) p.y[((size_t)blockIdx.y * R + m) * N + cl] = acc[pi][r];
       } else if (EPI == DEC_PART_T) {
-        if (cok) p.y[((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, col)] = acc[mt][r];
+        if (ck) p.y[((size_t)blockIdx.y * R + mt * 32) * N + kq_index(ml, cl)] = acc[pi][r];
       } else if (EPI == DEC_SILU_T) {
-        if (cok) p.y[(size_t)mt * 32 * N + kq_index(ml, col)] = silu(acc[mt][r]);
+        if (ck) p.y[(size_t)mt * 32 * N + kq_index(ml, cl)] = silu(acc[pi][r]);
       } else if (EPI == DEC_LOGITS) {
         // Logits, and the first maximum of the row over this tile's columns.
         bv = -INFINITY;
-        bi = (uint32_t)col;
-        if (m < M && cok) {
-          p.y[(size_t)m * N + col] = acc[mt][r];
-          bv = acc[mt][r];
+        bi = (uint32_t)cl;
+        if (m < M && ck) {
+          p.y[(size_t)m * N + cl] = acc[pi][r];
+          bv = acc[pi][r];
         }
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) {
@@ -545,8 +567,8 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
           const uint32_t oi = __shfl_xor(bi, o, 64);
           amax_merge(bv, bi, ov, oi);
         }
-        if (j == 0 && m < M)
-          p.amax[(size_t)m * gridDim.x + tile] = make_uint2(__float_as_uint(bv), bi);
+        if (j == 0 && m < M && ct < ntiles)
+          p.amax[(size_t)m * ntiles + ct] = make_uint2(__float_as_uint(bv), bi);
       }
     }
   }
@@ -1134,6 +1156,9 @@ bool role_bf16(int K, int N) {
                           : S::HL % 8 == 0 || S::W % 2 == 0;
 }
 
+#ifndef AKH_DEC_NT2
+#define AKH_DEC_NT2 2
+#endif
 template <int ROLE, bool LARGE, int EPI, int PRO>
 hipError_t dec_go_shape(DecGemmParams p, hipStream_t s) {
   using S = RoleShape<ROLE, LARGE>;
@@ -1144,7 +1169,8 @@ hipError_t dec_go_shape(DecGemmParams p, hipStream_t s) {
   static_assert(kOct || S::W % 2 == 0, "no k-octet shape with the same pass length");
   constexpr int WB = kOct ? S::W : S::W / 2, HLB = kOct ? S::HL : 2 * S::HL;
   p.kpass = role_kpass<ROLE, LARGE>(p.K, p.N);
-  const dim3 g((p.N + 31) / 32, role_splits<ROLE, LARGE>(p.K, p.N));
+  const int ntiles = (p.N + 31) / 32, splits = role_splits<ROLE, LARGE>(p.K, p.N);
+  const dim3 g(ntiles, splits);
 #define AKH_DEC_GO(MT)                                                                        \
   if (p.wbf16)                                                                                \
     hipLaunchKernelGGL((k_dec_gemm<WB, HLB, EPI, PRO, true, MT>), g, dim3(64 * WB), 0, s, p); \
@@ -1154,6 +1180,22 @@ hipError_t dec_go_shape(DecGemmParams p, hipStream_t s) {
   if (p.mt == 1) {
     AKH_DEC_GO(1)
   } else if (p.mt == 2) {
+    // Two row tiles of bfloat16 weights: each block of the K-split roles
+    // (qkv, out, down) takes two column tiles, so every A operand it loads
+    // (4x the bytes of a tile's weights per pass) and every split of it
+    // feeds twice the MFMAs.  Config 5, A/B on one box: out 13.7 -> 11.0 us,
+    // down 15.1 -> 14.0 us, qkv 13.7 -> 13.4 us.  ffn_up (one K split, 128
+    // blocks left) went 15.9 -> 19.9 us and the lm_head 82 -> 111 us, so
+    // they keep one column tile.
+    constexpr bool kNT2 =
+        ROLE == DEC_CFG_QKV || ROLE == DEC_CFG_OUT || ROLE == DEC_CFG_DOWN;
+    if constexpr (AKH_DEC_NT2 == 2 && kNT2 && EPI != DEC_RESID && PRO != PRO_NORM) {
+      if (p.wbf16) {
+        hipLaunchKernelGGL((k_dec_gemm<WB, HLB, EPI, PRO, true, 2, 2>),
+                           dim3((ntiles + 1) / 2, splits), dim3(64 * WB), 0, s, p);
+        return hipGetLastError();
+      }
+    }
     AKH_DEC_GO(2)
   } else {
     return hipErrorInvalidValue;
