@@ -63,3 +63,37 @@ def test_random_session_matches_oracle(backend, pkg, ora, seed):
         o.close()
     s.close()
     model.close()
+
+
+@pytest.mark.parametrize("dim,heads,batch", [(96, 3, 33), (160, 5, 40), (224, 2, 40)])
+def test_odd_column_tile_counts_on_two_row_tiles(backend, pkg, ora, dim, heads, batch):
+    """Sessions of 33..64 rows with bfloat16 weight tiles run their K-split
+    decode GEMMs (qkv, out, down) two column tiles per block; widths of an odd
+    number of 32-column tiles (3, 5, 7 for out and down; 9, 15, 21 for qkv)
+    end the grid on a block whose second tile does not exist.  Prefill and
+    greedy decode against the oracle, sequences at both row tiles."""
+    layers, ctx, steps = 2, 40, 4
+    case = f"dim {dim} heads {heads} batch {batch}"
+    print(case, flush=True)
+    cfg = dataclasses.replace(pkg.ModelConfig.new(211, dim, heads, layers, ctx), ffn_hidden=3 * dim)
+    w = pkg.synthetic_weights(cfg, seed=dim, bf16=True)
+    r = np.random.default_rng(dim)
+    lens = [int(x) for x in r.integers(1, ctx - steps, size=batch)]
+    prompts = [r.integers(0, cfg.vocab_size, size=n).astype(np.uint32) for n in lens]
+    model = pkg.hip.Model(backend, cfg)
+    model.upload(w)
+    assert model.set_bf16_tiles(True) == 4 * layers, case  # every layer matrix
+    s = pkg.hip.Session(model, ctx, batch)
+    logits, nxt = s.prefill(prompts)
+    got = [(logits, nxt)] + [s.decode_step(None) for _ in range(steps)]
+    for b in (0, 31, 32, batch - 1):
+        o = ora.OracleSession(cfg, w, ctx)
+        ref = o.prefill(prompts[b])
+        for i in range(steps + 1):
+            if i:
+                ref = o.decode_step(ora.argmax(ref))
+            assert np.abs(got[i][0][b] - ref).max() < TOL, f"{case}, sequence {b} step {i}"
+            assert int(got[i][1][b]) == ora.argmax(ref), f"{case}, sequence {b} step {i}"
+        o.close()
+    s.close()
+    model.close()
