@@ -941,9 +941,13 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
 #ifndef AKH_NORM_NB1
 #define AKH_NORM_NB1 24
 #endif
-template <int QPT>
-__global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
-  __shared__ float red4[4];
+#ifndef AKH_NORM_WIDE
+#define AKH_NORM_WIDE 1
+#endif
+template <int QPT, int NTH>
+__global__ __launch_bounds__(NTH) void k_rows_norm(RowsNormParams p) {
+  static_assert(NTH == 256 || NTH == 512, "256 or 512 threads per row");
+  __shared__ float redw[NTH / 64];
   const int m = blockIdx.x, d = p.d, nq = d / 4;
   const size_t tile_off = (size_t)(m >> 5) * 32 * d;  // row m's 32-row k-quad tile
   // The gain does not depend on the row: request it first, so its memory
@@ -951,7 +955,7 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
   float4 g[QPT];
 #pragma unroll
   for (int i = 0; i < QPT; ++i) {
-    const int q = threadIdx.x + 256 * i;
+    const int q = threadIdx.x + NTH * i;
     g[i] = q < nq ? *reinterpret_cast<const float4*>(p.gain + 4 * q)
                   : make_float4(0.f, 0.f, 0.f, 0.f);
   }
@@ -967,7 +971,7 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < QPT; ++i) {
-    const int q = threadIdx.x + 256 * i;
+    const int q = threadIdx.x + NTH * i;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (q < nq) {
       float* xq = p.xt + tile_off + ((size_t)q * 32 + (m & 31)) * 4;
@@ -996,12 +1000,18 @@ __global__ __launch_bounds__(256) void k_rows_norm(RowsNormParams p) {
       ss += ((v.x + v.y) + v.z) + v.w;
     }
   } else {
-    ss = block_sum256(ss, red4);
+    // The waves' sums, added in wave order.
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) redw[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = redw[0];
+#pragma unroll
+    for (int w = 1; w < NTH / 64; ++w) ss += redw[w];
   }
   const float rs = 1.0f / sqrtf(ss / (float)d + p.eps);
 #pragma unroll
   for (int i = 0; i < QPT; ++i) {
-    const int q = threadIdx.x + 256 * i;
+    const int q = threadIdx.x + NTH * i;
     if (q < nq) {
       const float4 v = x[i];
       *reinterpret_cast<float4*>(p.xnt + tile_off + ((size_t)q * 32 + (m & 31)) * 4) = make_float4(
@@ -1481,11 +1491,13 @@ hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, ui
 hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s) {
   const int nq = p.d / 4;
   if (nq <= 256)
-    hipLaunchKernelGGL(k_rows_norm<1>, dim3(M), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((k_rows_norm<1, 256>), dim3(M), dim3(256), 0, s, p);
   else if (nq <= 512)
-    hipLaunchKernelGGL(k_rows_norm<2>, dim3(M), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((k_rows_norm<AKH_NORM_WIDE ? 1 : 2, AKH_NORM_WIDE ? 512 : 256>), dim3(M),
+                       dim3(AKH_NORM_WIDE ? 512 : 256), 0, s, p);
   else if (nq <= 1024)
-    hipLaunchKernelGGL(k_rows_norm<4>, dim3(M), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((k_rows_norm<AKH_NORM_WIDE ? 2 : 4, AKH_NORM_WIDE ? 512 : 256>), dim3(M),
+                       dim3(AKH_NORM_WIDE ? 512 : 256), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
