@@ -149,6 +149,67 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// x of the lane that DPP control CTRL selects within the lane's 16-lane row
+// (a VALU operand modifier: no LDS crossbar traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// x[lane] + x[lane ^ O] and max(x[lane], x[lane ^ O]) for O = 16 or 32, on
+// gfx950's permlane swaps (VALU, no LDS crossbar).  Swapping x with itself
+// leaves, across the two results, x of the lane and of its partner in an
+// order that depends on the lane: v_permlane16_swap exchanges the odd
+// 16-lane rows of its first operand with the even rows of its second,
+// v_permlane32_swap the upper 32 lanes of the first with the lower 32 of
+// the second.  The sum and max of the pair are commutative, so both
+// partners get the same value.
+template <int O>
+__device__ __forceinline__ void xor_pair(float x, float& a, float& b) {
+  static_assert(O == 16 || O == 32, "permlane swaps pair lanes 16 or 32 apart");
+  const uint32_t u = __float_as_uint(x);
+  if constexpr (O == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  }
+}
+template <int O>
+__device__ __forceinline__ float xor_sum(float x) {
+  float a, b;
+  xor_pair<O>(x, a, b);
+  return a + b;
+}
+template <int O>
+__device__ __forceinline__ float xor_max(float x) {
+  float a, b;
+  xor_pair<O>(x, a, b);
+  return fmaxf(a, b);
+}
+
+// Sum over aligned groups of N lanes (N a power of two <= 64); every lane of
+// a group receives the same total.  Within a 16-lane row the partners come
+// from DPP: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (lane 7 - i of each 8, pairing the two quads) and
+// row_mirror (lane 15 - i, pairing the two halves); each step adds two
+// partial sums that already agree across the lanes being paired.  Wider
+// groups add lane ^ 16 and lane ^ 32 by permlane swaps.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N is a power of two <= 64");
+  if constexpr (N >= 2) v += dpp_f32<0xB1>(v);
+  if constexpr (N >= 4) v += dpp_f32<0x4E>(v);
+  if constexpr (N >= 8) v += dpp_f32<0x141>(v);
+  if constexpr (N >= 16) v += dpp_f32<0x140>(v);
+  if constexpr (N >= 32) v = xor_sum<16>(v);
+  if constexpr (N >= 64) v = xor_sum<32>(v);
+  return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

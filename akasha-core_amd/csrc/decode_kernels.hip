@@ -747,6 +747,51 @@ __global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
 // KV16: the cache holds bfloat16 rows (a lane loads 8 bytes per row and
 // widens them); the new row is rounded to bfloat16 before it is used and
 // appended, so every step sees the cache's values.
+// A row's score: the sum of its LPR lanes' partial dot products.
+#ifndef AKH_ATTN_DPP
+#define AKH_ATTN_DPP 1
+#endif
+template <int LPR>
+__device__ __forceinline__ float row_dot_sum(float s) {
+  if constexpr (AKH_ATTN_DPP) {
+    return group_sum<LPR>(s);
+  } else {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    return s;
+  }
+}
+
+// Sum and max over a wave's row slots: lanes LPR, 2 LPR, ... apart (each
+// lane pairs with the lane of the same column in the other slot; slots
+// under 16 lanes apart by bpermute).
+template <int LPR>
+__device__ __forceinline__ float slots_sum(float v) {
+  if constexpr (AKH_ATTN_DPP) {
+#pragma unroll
+    for (int o = LPR; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+    if constexpr (LPR <= 16) v = xor_sum<16>(v);
+    if constexpr (LPR <= 32) v = xor_sum<32>(v);
+  } else {
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  }
+  return v;
+}
+template <int LPR>
+__device__ __forceinline__ float slots_max(float v) {
+  if constexpr (AKH_ATTN_DPP) {
+#pragma unroll
+    for (int o = LPR; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if constexpr (LPR <= 16) v = xor_max<16>(v);
+    if constexpr (LPR <= 32) v = xor_max<32>(v);
+  } else {
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  }
+  return v;
+}
+
 template <int HD, int AW, int RB, int SP, bool KV16>
 __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
   constexpr int LPR = HD / 4;    // lanes per row
@@ -854,8 +899,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     // The new row; every lane of a row group holds its full score, and only
     // row slot 0 adds it so the slot sum below counts it once.
     float s = q4.x * kn.x + q4.y * kn.y + q4.z * kn.z + q4.w * kn.w;
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = row_dot_sum<LPR>(s);
     m = s * p.scale;
     l = rl == 0 ? 1.f : 0.f;
     acc = rl == 0 ? vn : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -867,15 +911,13 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     for (int i = 0; i < RB; ++i) {
       const float4 kk = wide(kv[i]);
       float s = q4.x * kk.x + q4.y * kk.y + q4.z * kk.z + q4.w * kk.w;
-#pragma unroll
-      for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+      s = row_dot_sum<LPR>(s);
       t[i] = ok[i] ? s * p.scale : -INFINITY;
     }
     float bm = t[0];
 #pragma unroll
     for (int i = 1; i < RB; ++i) bm = fmaxf(bm, t[i]);
-#pragma unroll
-    for (int o = LPR; o < 64; o <<= 1) bm = fmaxf(bm, __shfl_xor(bm, o, 64));
+    bm = slots_max<LPR>(bm);
     const float mn = fmaxf(m, bm);
     const float corr = m == -INFINITY ? 0.f : expf(m - mn);
     float ps = 0.f;
@@ -898,14 +940,9 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     m = mn;
   }
   // Sum the wave's row slots (they share the running max m).
-#pragma unroll
-  for (int o = LPR; o < 64; o <<= 1) {
-    l += __shfl_xor(l, o, 64);
-    acc.x += __shfl_xor(acc.x, o, 64);
-    acc.y += __shfl_xor(acc.y, o, 64);
-    acc.z += __shfl_xor(acc.z, o, 64);
-    acc.w += __shfl_xor(acc.w, o, 64);
-  }
+  l = slots_sum<LPR>(l);
+  acc = make_float4(slots_sum<LPR>(acc.x), slots_sum<LPR>(acc.y), slots_sum<LPR>(acc.z),
+                    slots_sum<LPR>(acc.w));
   if (rl == 0) wo_s[wave][g] = acc;
   if (lane == 0) {
     wm_s[wave] = m;
