@@ -138,6 +138,23 @@ __device__ __forceinline__ float4 bf16x4(uint32_t lo, uint32_t hi) {
 #ifndef AKH_LM_GEMM_NT
 #define AKH_LM_GEMM_NT 0
 #endif
+// The attention's softmax runs in the log2 domain: scores scaled by
+// scale * log2(e), weights from the hardware 2^x (one v_exp_f32 against
+// about 35 instructions for expf).  The split states (max, sum) it hands to
+// out_proj's merge are in the same units.
+#ifndef AKH_ATTN_EXP2
+#define AKH_ATTN_EXP2 1
+#endif
+__device__ __forceinline__ float attn_exp(float x) {
+  if constexpr (AKH_ATTN_EXP2)
+    return __builtin_amdgcn_exp2f(x);
+  else
+    return expf(x);
+}
+__device__ __forceinline__ float attn_score_scale(float scale) {
+  return AKH_ATTN_EXP2 ? scale * 1.44269504088896341f : scale;
+}
+
 template <int W, int HL, int EPI, int PRO, bool BF, int MT, int NT = 1>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   constexpr int KC = 2 * W * HL;
@@ -317,7 +334,8 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
         } else if (PRO == PRO_ATTN_MERGE) {
           // Softmax states (max, sum, unnormalised o) of the attention
           // splits of row 32 mt + j, head (4 kq) / hd:
-          // o = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(max_s - max).
+          // o = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(max_s - max)
+          // (2^(max_s - max): the attention keeps its maxima in log2 units).
           const int H = K / p.hd, hq = (4 * kq) / p.hd;
           float2 ml[kMaxAttnSplits];
           float4 o[kMaxAttnSplits];
@@ -335,7 +353,7 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
           float L = 0.f;
 #pragma unroll
           for (int sp = 0; sp < kMaxAttnSplits; ++sp) {
-            const float w = ml[sp].x == -INFINITY ? 0.f : expf(ml[sp].x - mx);
+            const float w = ml[sp].x == -INFINITY ? 0.f : attn_exp(ml[sp].x - mx);
             L += w * ml[sp].y;
             t.x += w * o[sp].x;
             t.y += w * o[sp].y;
@@ -893,6 +911,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     *reinterpret_cast<float4*>(static_cast<float*>(p.vc) + hoff + (size_t)pos * d) = vn;
   }
 
+  const float qs = attn_score_scale(p.scale);
   float m = -INFINITY, l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (last && wave == 0) {
@@ -900,7 +919,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     // row slot 0 adds it so the slot sum below counts it once.
     float s = q4.x * kn.x + q4.y * kn.y + q4.z * kn.z + q4.w * kn.w;
     s = row_dot_sum<LPR>(s);
-    m = s * p.scale;
+    m = s * qs;
     l = rl == 0 ? 1.f : 0.f;
     acc = rl == 0 ? vn : make_float4(0.f, 0.f, 0.f, 0.f);
   }
@@ -912,19 +931,19 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
       const float4 kk = wide(kv[i]);
       float s = q4.x * kk.x + q4.y * kk.y + q4.z * kk.z + q4.w * kk.w;
       s = row_dot_sum<LPR>(s);
-      t[i] = ok[i] ? s * p.scale : -INFINITY;
+      t[i] = ok[i] ? s * qs : -INFINITY;
     }
     float bm = t[0];
 #pragma unroll
     for (int i = 1; i < RB; ++i) bm = fmaxf(bm, t[i]);
     bm = slots_max<LPR>(bm);
     const float mn = fmaxf(m, bm);
-    const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+    const float corr = m == -INFINITY ? 0.f : attn_exp(m - mn);
     float ps = 0.f;
     float4 pv = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
-      const float e = ok[i] ? expf(t[i] - mn) : 0.f;
+      const float e = ok[i] ? attn_exp(t[i] - mn) : 0.f;
       const float4 vw = wide(vv[i]);
       ps += e;
       pv.x += e * vw.x;
@@ -956,7 +975,7 @@ __global__ __launch_bounds__(64 * AW) void k_dec_attn(DecAttnParams p) {
     float L = 0.f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int w = 0; w < AW; ++w) {
-      const float wg = wm_s[w] == -INFINITY ? 0.f : expf(wm_s[w] - M);
+      const float wg = wm_s[w] == -INFINITY ? 0.f : attn_exp(wm_s[w] - M);
       L += wg * wl_s[w];
       o.x += wg * wo_s[w][t].x;
       o.y += wg * wo_s[w][t].y;
