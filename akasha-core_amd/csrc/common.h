@@ -143,11 +143,6 @@ __device__ __forceinline__ int acc_row(int r, int h) {
   return (r >> 2) * 8 + h * 4 + (r & 3);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 
 // x of the lane that DPP control CTRL selects within the lane's 16-lane row
 // (a VALU operand modifier: no LDS crossbar traffic).
@@ -210,11 +205,36 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Maximum over aligned groups of N lanes, the partners of group_sum.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N is a power of two <= 64");
+  if constexpr (N >= 2) v = fmaxf(v, dpp_f32<0xB1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp_f32<0x4E>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp_f32<0x141>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp_f32<0x140>(v));
+  if constexpr (N >= 32) v = xor_max<16>(v);
+  if constexpr (N >= 64) v = xor_max<32>(v);
+  return v;
+}
+
+// Sum and maximum over the wave; every lane receives the result.
+#ifndef AKH_WAVE_DPP
+#define AKH_WAVE_DPP 1
+#endif
+__device__ __forceinline__ float wave_sum(float v) {
+  if constexpr (AKH_WAVE_DPP) return group_sum<64>(v);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
 __device__ __forceinline__ float wave_max(float v) {
+  if constexpr (AKH_WAVE_DPP) return group_max<64>(v);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+
 
 // Reductions over a 256-thread block; every thread gets the result.  The
 // order is fixed (butterfly in waves, then waves 0..3), so results are
