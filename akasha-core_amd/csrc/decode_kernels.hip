@@ -63,6 +63,33 @@ __global__ __launch_bounds__(256) void k_pack_tiles(const float* __restrict__ w,
   *reinterpret_cast<float4*>(out + (((size_t)t * (Kp / 4) + q) * 32 + j) * 4) = v;
 }
 
+// Split-fp16 lm_head tiles (launch_pack_lm_h3): one thread per (k-octet,
+// column), 32 bytes out (hi octet, then lo octet).
+__global__ __launch_bounds__(256) void k_pack_lm_h3(const float* __restrict__ w, int K, int N,
+                                                    int Kp, uint16_t* __restrict__ out,
+                                                    int* __restrict__ flag) {
+  const int j = threadIdx.x & 31;
+  const int o = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int t = blockIdx.y;
+  if (8 * o >= Kp) return;
+  const int n = t * 32 + j;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int k = 8 * o + e;
+    x[e] = n < N && k < K ? w[(size_t)k * N + n] : 0.f;
+  }
+  uint4 hi, lo;
+  split2_f16(make_float4(x[0], x[1], x[2], x[3]), make_float4(x[4], x[5], x[6], x[7]), hi, lo);
+  bool ok = true;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ok = ok && fabsf(x[e]) < 65504.f;
+  if (!ok) *flag = 1;
+  uint4* dst = reinterpret_cast<uint4*>(out + (((size_t)t * (Kp / 8) + o) * 32 + j) * 16);
+  dst[0] = hi;
+  dst[1] = lo;
+}
+
 // The same tiles with bfloat16 elements in k-octets: element (k, n) of tile
 // t = n / 32 at ((k / 8) * 32 + n % 32) * 8 + k % 8, so a lane's 16-byte load
 // holds eight consecutive k of its column.  Used only for matrices whose
@@ -746,6 +773,142 @@ __global__ __launch_bounds__(64 * W) void k_dec_lm(DecGemmParams p) {
   }
 }
 
+// k_dec_lm on split-fp16 tiles (k_pack_lm_h3): the same persistent grid,
+// prefetch and epilogue, with each 16-k step of a row tile three
+// v_mfma_f32_32x32x16_f16 products (hi.hi into acc, hi.lo and lo.hi into
+// cor; the result is acc + 2^-11 cor, error ~2^-22 relative) instead of
+// sixteen fp32 MFMAs of twice the cycles.  The weights take the same 4
+// bytes per element.  A is split once: the block scales it by 2^-S, S the
+// smallest shift that brings max |A| under 2^15 (0 for any ordinary row),
+// so its fp16 terms cannot overflow, and scales the results back by 2^S
+// (both exact).  Half h of a wave's lanes covers k [2 HL w + HL h, + HL) as
+// in k_dec_lm, eight k per step.
+template <int W, int HL, int MT>
+__global__ __launch_bounds__(64 * W) void k_dec_lm_h3(DecGemmParams p) {
+  constexpr int RW = 32 / W;
+  constexpr int LPR = 64 / RW;
+  constexpr int NS = HL / 8;  // 16-k MFMA steps per tile
+  static_assert(W * RW == 32 && LPR <= 64, "W must divide 32");
+  static_assert(HL % 8 == 0, "HL must cover whole k-octets");
+  static_assert(MT == 1 || MT == 2, "one or two row tiles");
+  __shared__ float red[2][W][32][33];
+  __shared__ float amx[W];
+  const int N = p.N, K = p.K, Kp = p.Kp;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  const int ntiles = (N + 31) / 32;
+  const int G = gridDim.x;
+  const int k0 = wave * 2 * HL + h * HL;  // first k of this half
+  // Lane offset within a tile: octet k0 / 8 + s, column j, 32 bytes each.
+  const uint32_t voff = (uint32_t)((k0 / 8) * 32 + j) * 32u;
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.w), (short)0, ntiles * Kp * 128, 0x00020000);
+
+  float4 af[MT][2 * NS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int q = 0; q < 2 * NS; ++q) {
+      const int kq = k0 / 4 + q;
+      af[mt][q] = 4 * kq < K ? *reinterpret_cast<const float4*>(
+                                   p.xt + (size_t)mt * 32 * K + ((size_t)kq * 32 + j) * 4)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  // Block scale: max |A| over the block (every block holds all of A).
+  float mx = 0.f;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int q = 0; q < 2 * NS; ++q)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(af[mt][q].x), fabsf(af[mt][q].y)),
+                           fmaxf(fabsf(af[mt][q].z), fabsf(af[mt][q].w))));
+  mx = wave_max(mx);
+  if (lane == 0) amx[wave] = mx;
+  __syncthreads();
+  mx = amx[0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) mx = fmaxf(mx, amx[w]);
+  float down = 1.f, up = 1.f;
+  if (mx >= 32768.f && mx <= 3.0e38f) {
+    int e;
+    frexpf(mx, &e);  // mx < 2^e
+    down = ldexpf(1.f, 15 - e);
+    up = ldexpf(1.f, e - 15);
+  }
+  uint4 ah[MT][NS], al[MT][NS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float4 x0 = af[mt][2 * s], x1 = af[mt][2 * s + 1];
+      split2_f16(make_float4(x0.x * down, x0.y * down, x0.z * down, x0.w * down),
+                 make_float4(x1.x * down, x1.y * down, x1.z * down, x1.w * down), ah[mt][s],
+                 al[mt][s]);
+    }
+
+  float bv[MT];
+  uint32_t bi[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    bv[mt] = -INFINITY;
+    bi[mt] = 0xFFFFFFFFu;
+  }
+  auto load_b = [&](uint4 (&bb)[2 * NS], int tile) {
+    const uint32_t vo = tile < ntiles ? voff : 0x80000000u;
+    const int so = tile * Kp * 128;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      bb[2 * s] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, (int)vo, so + s * 1024, AKH_LM_CPOL));
+      bb[2 * s + 1] = __builtin_bit_cast(
+          uint4,
+          __builtin_amdgcn_raw_buffer_load_b128(wres, (int)vo, so + s * 1024 + 16, AKH_LM_CPOL));
+    }
+  };
+  uint4 cur[2 * NS], nxt[2 * NS];
+  load_b(cur, blockIdx.x);
+  int par = 0;
+#pragma unroll 1
+  for (int tile = blockIdx.x; tile < ntiles; tile += G) {
+    load_b(nxt, tile + G);
+    asm volatile("" ::: "memory");  // keep the prefetch issued here
+    f32x16 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x16 c = zero16(), cor = zero16();
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const f16x8 bh = f16x8_of(cur[2 * s]), bl = f16x8_of(cur[2 * s + 1]);
+        const f16x8 xh = f16x8_of(ah[mt][s]), xl = f16x8_of(al[mt][s]);
+        cor = mfma_f16(xl, bh, cor);
+        cor = mfma_f16(xh, bl, cor);
+        c = mfma_f16(xh, bh, c);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][r] = (c[r] + cor[r] * 0x1p-11f) * up;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      lm_finish<W>(acc[mt], red[par], tile, 32 * mt, p, bv[mt], bi[mt]);
+      par ^= 1;
+    }
+#pragma unroll
+    for (int q = 0; q < 2 * NS; ++q) cur[q] = nxt[q];
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv[mt], o, 64);
+      const uint32_t oi = __shfl_xor(bi[mt], o, 64);
+      amax_merge(bv[mt], bi[mt], ov, oi);
+    }
+    const int m = 32 * mt + wave * RW + lane / LPR;
+    if (lane % LPR == 0 && m < p.M)
+      p.amax[(size_t)m * G + blockIdx.x] = make_uint2(__float_as_uint(bv[mt]), bi[mt]);
+  }
+}
+
 // Single-query attention over the KV cache, one (sequence, head, split) per
 // block, with the fused head of the layer's attention:
 //   q, k, v of the new token = the sum of the QKV GEMM's partial tiles, with
@@ -1299,6 +1462,17 @@ hipError_t launch_pack_tiles(const float* w, int K, int N, int Kp, float* out, b
   return hipGetLastError();
 }
 
+hipError_t launch_pack_lm_h3(const float* w, int K, int N, int Kp, uint16_t* out, int* flag,
+                             hipStream_t s) {
+  if (K <= 0 || N <= 0 || Kp < K || Kp % 8 != 0 || !flag) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pack_lm_h3, dim3((Kp / 8 + 7) / 8, (N + 31) / 32), dim3(256), 0, s, w, K,
+                     N, Kp, out, flag);
+  return hipGetLastError();
+}
+
+// Sessions of one and two row tiles both run the persistent kernel (K <= 768).
+bool dec_lm_h3_capable(int K, int N) { return lm_persistent(N, K, 2); }
+
 hipError_t launch_check_bf16(const float* w, size_t n, int* flag, hipStream_t s) {
   const size_t blocks = std::min<size_t>(2048, (n + 255) / 256);
   hipLaunchKernelGGL(k_check_bf16, dim3((unsigned)std::max<size_t>(1, blocks)), dim3(256), 0,
@@ -1345,9 +1519,27 @@ int dec_lm_parts(int N, int K, int num_cus, int mt) {
 
 hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s) {
   if (p.mt != 1 && p.mt != 2) return hipErrorInvalidValue;
-  if (!lm_persistent(p.N, p.K, p.mt)) return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
+  if (!lm_persistent(p.N, p.K, p.mt)) {
+    if (p.wh3) return hipErrorInvalidValue;  // split tiles serve the persistent kernel only
+    return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
+  }
   if (p.Kp != lm_rows(p.K)) return hipErrorInvalidValue;
   const dim3 g(dec_lm_parts(p.N, p.K, num_cus, p.mt));
+  if (p.wh3) {
+    if (p.Kp != 256 && p.Kp != 768) return hipErrorInvalidValue;
+#define AKH_LM_H3_GO(MT)                                                    \
+  if (p.Kp == 256)                                                          \
+    hipLaunchKernelGGL((k_dec_lm_h3<8, 16, MT>), g, dim3(512), 0, s, p);    \
+  else                                                                      \
+    hipLaunchKernelGGL((k_dec_lm_h3<8, 48, MT>), g, dim3(512), 0, s, p);
+    if (p.mt == 1) {
+      AKH_LM_H3_GO(1)
+    } else {
+      AKH_LM_H3_GO(2)
+    }
+#undef AKH_LM_H3_GO
+    return hipGetLastError();
+  }
 #define AKH_LM_GO(MT)                                           \
   if (p.Kp == 256)                                              \
     hipLaunchKernelGGL((k_dec_lm<8, 16, MT>), g, dim3(512), 0, s, p); \

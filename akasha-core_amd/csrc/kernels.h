@@ -215,6 +215,7 @@ struct DecGemmParams {
   int nparts;
   const float* w;   // weights packed by launch_pack_tiles (Kp rows per tile)
   int wbf16;        // w holds bfloat16 k-octet tiles
+  int wh3;          // lm_head only: w holds fp16 hi/lo k-octet tiles (launch_pack_lm_h3)
   int M, N, K, Kp;
   float* y;         // partial tiles or logits
   uint2* amax;      // DEC_LOGITS: [32, parts] (value bits, index)
@@ -249,6 +250,16 @@ hipError_t launch_pack_tiles(const float* w, int K, int N, int Kp, float* out, b
                              hipStream_t s);
 // *flag |= 1 if any of w[0..n) is not a bfloat16 value (low 16 bits set).
 hipError_t launch_check_bf16(const float* w, size_t n, int* flag, hipStream_t s);
+// The persistent lm_head's split-fp16 tiles: element (k, n) of tile
+// t = n / 32 as two fp16 terms (w = hi + 2^-11 lo to within 2^-22 |w|) at
+// (((k / 8) * 32 + n % 32) * 2 + plane) * 8 + k % 8, the same 4 bytes per
+// element as the float tiles (Kp a multiple of 8).  *flag = 1 if a weight is
+// beyond fp16's range (|w| >= 65520: the tiles are then unusable).
+hipError_t launch_pack_lm_h3(const float* w, int K, int N, int Kp, uint16_t* out, int* flag,
+                             hipStream_t s);
+// Whether the lm_head of a (K, N) matrix runs the persistent kernel for
+// sessions of one and two row tiles (its tiles may then be split-fp16).
+bool dec_lm_h3_capable(int K, int N);
 // Rows Kp of a role's packed tiles (K rounded up to 8, or more for
 // lm_head's padding).
 int dec_packed_rows(int role, int K);

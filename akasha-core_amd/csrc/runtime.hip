@@ -553,6 +553,7 @@ struct PackedMatrix {
   float* w = nullptr;
   int K = 0, N = 0, rows = 0, role = 0;
   bool bf16 = false;  // tiles hold bfloat16 (every value of the matrix is one)
+  bool h3 = false;    // lm_head tiles hold fp16 hi/lo terms (launch_pack_lm_h3)
 };
 
 struct akh_model {
@@ -749,6 +750,9 @@ extern "C" akh_status akh_model_param(akh_model* m, uint32_t index,
 
 namespace {
 
+#ifndef AKH_LM_H3
+#define AKH_LM_H3 1
+#endif
 // Rebuilds the packed decode copy of parameter `index` from its rows: in
 // bfloat16 when the role's kernel supports it and every value is a
 // bfloat16, else in float.
@@ -765,13 +769,26 @@ akh_status repack(akh_model* m, uint32_t index) {
     HIP_TRY(hipStreamSynchronize(st));
     bf16 = flag == 0;
   }
-  HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, bf16, st));
+  // The persistent lm_head reads split-fp16 tiles (the same bytes as float
+  // ones, a fifth of the MFMA cycles) unless a weight is beyond fp16's range.
+  bool h3 = false;
+  if (AKH_LM_H3 && pm.role == DEC_CFG_LM && !bf16 && dec_lm_h3_capable(pm.K, pm.N)) {
+    int flag = 0;
+    HIP_TRY(hipMemcpyAsync(m->bf16_flag, &flag, sizeof(int), hipMemcpyHostToDevice, st));
+    HIP_TRY(launch_pack_lm_h3(m->params[index], pm.K, pm.N, pm.rows,
+                              reinterpret_cast<uint16_t*>(pm.w), m->bf16_flag, st));
+    HIP_TRY(hipMemcpyAsync(&flag, m->bf16_flag, sizeof(int), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    h3 = flag == 0;
+  }
+  if (!h3) HIP_TRY(launch_pack_tiles(m->params[index], pm.K, pm.N, pm.rows, pm.w, bf16, st));
   if (index < m->wt16.size() && m->wt16[index])
     HIP_TRY(launch_transpose_bf16(m->params[index], pm.K, pm.N, m->wt16[index], st));
   if (index < m->wsplit.size() && m->wsplit[index]) HIP_TRY(fill_split(m, index, st));
   HIP_TRY(hipStreamSynchronize(st));
-  if (bf16 != pm.bf16) {
+  if (bf16 != pm.bf16 || h3 != pm.h3) {
     pm.bf16 = bf16;
+    pm.h3 = h3;
     ++m->layout_gen;  // captured decode graphs chose kernels by element type
   }
   return AKH_OK;
@@ -1123,6 +1140,7 @@ void use_packed(DecGemmParams& p, const PackedMatrix& pm) {
   p.w = pm.w;
   p.Kp = pm.rows;
   p.wbf16 = pm.bf16 ? 1 : 0;
+  p.wh3 = pm.h3 ? 1 : 0;
 }
 
 RowsNormParams norm_base(akh_session* s, const float* gain) {

@@ -647,6 +647,42 @@ def test_prefill_h3_out_of_fp16_range_reruns_in_fp32(backend, pkg, where):
     f.close()
 
 
+@pytest.mark.parametrize("case", ["plain", "scaled_rows", "weight_beyond_fp16", "two_row_tiles"])
+def test_lm_head_split_tiles_match_oracle(backend, pkg, ora, case):
+    # The persistent lm_head reads its weights as two fp16 terms (three
+    # fp16 products per multiply-add).  "scaled_rows": final-norm gains of
+    # 4e4 put the normed rows beyond 2^15, so the kernel scales them by a
+    # power of two and back; "weight_beyond_fp16": one lm_head weight of 1e5
+    # keeps that matrix on float tiles; "two_row_tiles": 40 sequences.
+    # Prefill and greedy decode against the oracle, logits within 1e-3 plus
+    # 2e-6 of their magnitude, tokens identical.
+    cfg = pkg.ModelConfig.new(300, 128, 2, 2, 24)
+    L = cfg.num_layers
+    w = pkg.synthetic_weights(cfg, seed=71)
+    if case == "scaled_rows":
+        w[1 + 6 * L] = w[1 + 6 * L] * np.float32(4e4)
+    elif case == "weight_beyond_fp16":
+        lm = w[2 + 6 * L].copy()
+        lm.flat[777] = 1e5
+        w[2 + 6 * L] = lm
+    B, P, steps = (40 if case == "two_row_tiles" else 3), 8, 3
+    toks = pkg.synthetic_tokens(B * P, cfg.vocab_size, seed=72).reshape(B, P)
+    model, s = _session(pkg, backend, cfg, w, 24, B)
+    got = [s.prefill(toks)] + [s.decode_step(None) for _ in range(steps)]
+    for b in sorted({0, B - 1}):
+        o = ora.OracleSession(cfg, w, 24)
+        ref = o.prefill(toks[b])
+        for i in range(steps + 1):
+            if i:
+                ref = o.decode_step(ora.argmax(ref))
+            tol = 1e-3 + 2e-6 * float(np.abs(ref).max())
+            assert np.abs(got[i][0][b] - ref).max() < tol, f"{case}: sequence {b} step {i}"
+            assert int(got[i][1][b]) == ora.argmax(ref), f"{case}: sequence {b} step {i}"
+        o.close()
+    if case == "scaled_rows":
+        assert np.abs(got[0][0]).max() > 100.0  # the rows really were large
+
+
 def test_decode_kernel_timers(backend, pkg):
     # akh_session_time_decode_attn (events carried by the dispatches) and
     # the back-to-back timer measure the same kernel: both positive and
