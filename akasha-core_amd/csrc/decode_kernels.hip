@@ -1285,14 +1285,18 @@ namespace {
 // 1024, out 1024, up 256 -- one K split, so ffn_up applies SiLU itself and
 // the separate SiLU kernel goes -- and down 512 measured best per role,
 // 6.52 -> 6.13 ms per bf16-KV step); hall-1.0's grids stay below every cap.
+// hall-1.0's shapes, re-swept with the pipelined passes and the attention
+// and norm changes: qkv 16,8 (three K splits) and up 16,24 (one K split, so
+// ffn_up applies SiLU and ffn_down reads plain rows) took the step from
+// 0.593 to 0.588 ms; out 4,12 and down 16,12 stayed best.
 #ifndef AKH_SHAPE_QKV
-#define AKH_SHAPE_QKV 16, 12
+#define AKH_SHAPE_QKV 16, 8
 #endif
 #ifndef AKH_SHAPE_OUT
 #define AKH_SHAPE_OUT 4, 12
 #endif
 #ifndef AKH_SHAPE_UP
-#define AKH_SHAPE_UP 8, 24
+#define AKH_SHAPE_UP 16, 24
 #endif
 #ifndef AKH_SHAPE_DOWN
 #define AKH_SHAPE_DOWN 16, 12
