@@ -647,16 +647,19 @@ def test_prefill_h3_out_of_fp16_range_reruns_in_fp32(backend, pkg, where):
     f.close()
 
 
-@pytest.mark.parametrize("case", ["plain", "scaled_rows", "weight_beyond_fp16", "two_row_tiles"])
+@pytest.mark.parametrize("case", ["plain", "scaled_rows", "weight_beyond_fp16", "two_row_tiles",
+                                  "two_row_tiles_dim384"])
 def test_lm_head_split_tiles_match_oracle(backend, pkg, ora, case):
     # The persistent lm_head reads its weights as two fp16 terms (three
     # fp16 products per multiply-add).  "scaled_rows": final-norm gains of
     # 4e4 put the normed rows beyond 2^15, so the kernel scales them by a
     # power of two and back; "weight_beyond_fp16": one lm_head weight of 1e5
-    # keeps that matrix on float tiles; "two_row_tiles": 40 sequences.
+    # keeps that matrix on float tiles; "two_row_tiles": 40 sequences, also at
+    # dim 384 (tiles of 768 k, the kernel's other size).
     # Prefill and greedy decode against the oracle, logits within 1e-3 plus
     # 2e-6 of their magnitude, tokens identical.
-    cfg = pkg.ModelConfig.new(300, 128, 2, 2, 24)
+    dim, heads = (384, 3) if case == "two_row_tiles_dim384" else (128, 2)
+    cfg = pkg.ModelConfig.new(300, dim, heads, 2, 24)
     L = cfg.num_layers
     w = pkg.synthetic_weights(cfg, seed=71)
     if case == "scaled_rows":
@@ -665,7 +668,7 @@ def test_lm_head_split_tiles_match_oracle(backend, pkg, ora, case):
         lm = w[2 + 6 * L].copy()
         lm.flat[777] = 1e5
         w[2 + 6 * L] = lm
-    B, P, steps = (40 if case == "two_row_tiles" else 3), 8, 3
+    B, P, steps = (40 if case.startswith("two_row_tiles") else 3), 8, 3
     toks = pkg.synthetic_tokens(B * P, cfg.vocab_size, seed=72).reshape(B, P)
     model, s = _session(pkg, backend, cfg, w, 24, B)
     got = [s.prefill(toks)] + [s.decode_step(None) for _ in range(steps)]
