@@ -192,7 +192,8 @@ __device__ __forceinline__ float xor_max(float x) {
 // row_half_mirror (lane 7 - i of each 8, pairing the two quads) and
 // row_mirror (lane 15 - i, pairing the two halves); each step adds two
 // partial sums that already agree across the lanes being paired.  Wider
-// groups add lane ^ 16 and lane ^ 32 by permlane swaps.
+// groups add lane ^ 16 and lane ^ 32 by permlane swaps.  Every lane of the
+// wave must be active (the callers reduce in uniform control flow).
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
   static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N is a power of two <= 64");
