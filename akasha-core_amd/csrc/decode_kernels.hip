@@ -1512,11 +1512,14 @@ int dec_gemm_splits(int role, int K, int N) {
 }
 
 #ifndef AKH_LM_BLOCKS_PER_CU
-#define AKH_LM_BLOCKS_PER_CU 2  // 2 beat 1 and 3 (config 4: 34.7 us vs 39.6)
+#define AKH_LM_BLOCKS_PER_CU 2  // float tiles: 2 beat 1 and 3 (config 4: 34.7 us vs 39.6)
 #endif
-int dec_lm_parts(int N, int K, int num_cus, int mt) {
+#ifndef AKH_LM_H3_BLOCKS_PER_CU
+#define AKH_LM_H3_BLOCKS_PER_CU 1  // split tiles (one block fits per CU): 27.4 us vs 30.0 for 2
+#endif
+int dec_lm_parts(int N, int K, int num_cus, int mt, bool h3) {
   // Two row tiles hold twice the A registers: one block per CU fits.
-  const int per_cu = mt == 1 ? AKH_LM_BLOCKS_PER_CU : 1;
+  const int per_cu = mt == 1 ? (h3 ? AKH_LM_H3_BLOCKS_PER_CU : AKH_LM_BLOCKS_PER_CU) : 1;
   if (lm_persistent(N, K, mt)) return std::max(1, std::min((N + 31) / 32, per_cu * num_cus));
   return (N + 31) / 32;
 }
@@ -1528,7 +1531,7 @@ hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s) {
     return dec_go<DEC_CFG_LM, DEC_LOGITS, PRO_NONE>(p, s);
   }
   if (p.Kp != lm_rows(p.K)) return hipErrorInvalidValue;
-  const dim3 g(dec_lm_parts(p.N, p.K, num_cus, p.mt));
+  const dim3 g(dec_lm_parts(p.N, p.K, num_cus, p.mt, p.wh3 != 0));
   if (p.wh3) {
     if (p.Kp != 256 && p.Kp != 768) return hipErrorInvalidValue;
 #define AKH_LM_H3_GO(MT)                                                    \

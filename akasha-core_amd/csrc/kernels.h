@@ -275,9 +275,10 @@ bool dec_norm_fusable(int K);
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s);
 
 // lm_head: logits y[M, N] = xt . w and argmax partials amax[M, parts], where
-// parts = dec_lm_parts(N, K, num_cus, mt) (each the first maximum of the row
-// over a subset of the columns).
-int dec_lm_parts(int N, int K, int num_cus, int mt);
+// parts = dec_lm_parts(N, K, num_cus, mt, h3) (each the first maximum of the
+// row over a subset of the columns; h3: the tiles are split-fp16).  The
+// float tiles' count is the larger: size buffers with h3 = false.
+int dec_lm_parts(int N, int K, int num_cus, int mt, bool h3);
 hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s);
 
 struct DecAttnParams {

@@ -1072,8 +1072,15 @@ struct akh_session {
 
 namespace {
 
+// The lm_head's argmax partials per row for the model's current tiles, and
+// the most any tiles need (the size of amax).
 int lm_parts(const akh_session* s) {
-  return dec_lm_parts((int)s->m->cfg.vocab_size, (int)s->m->cfg.dim, s->be->num_cus, s->mt);
+  return dec_lm_parts((int)s->m->cfg.vocab_size, (int)s->m->cfg.dim, s->be->num_cus, s->mt,
+                      s->m->packed_lm_head().h3);
+}
+int lm_parts_max(const akh_session* s) {
+  return dec_lm_parts((int)s->m->cfg.vocab_size, (int)s->m->cfg.dim, s->be->num_cus, s->mt,
+                      false);
 }
 
 void free_prefill(akh_session* s) {
@@ -1560,7 +1567,7 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
     alloc((void**)&s->rcount, (d / 32) * sizeof(int));  // zeroed by alloc
   }
   alloc((void**)&s->logits, R * V * 4);
-  alloc((void**)&s->amax, R * (size_t)lm_parts(s) * sizeof(uint2));
+  alloc((void**)&s->amax, R * (size_t)lm_parts_max(s) * sizeof(uint2));
   alloc((void**)&s->tok, RB * 4);
   alloc((void**)&s->pos, RB * 4);
   alloc((void**)&s->hist, (size_t)batch * (max_context_len + 1) * 4);
