@@ -1743,6 +1743,46 @@ hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, ui
   return hipGetLastError();
 }
 
+// Synthetic KV rows for timing decode over a filled cache: rows [0, len) of
+// every (layer, K/V, sequence) plane get N(0, 1) values from a counter-based
+// hash of (seed, plane, row, column) (splitmix64 finaliser, then Box-Muller
+// on two 24-bit uniforms).  Planes are max_ctx * d apart; kv16 stores
+// bfloat16 rounded to nearest even.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void k_fill_kv_synthetic(void* kv, bool kv16, size_t planes,
+                                                           int len, int d, long max_ctx,
+                                                           uint64_t seed) {
+  const size_t n = planes * (size_t)len * d;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t c = i % d, r = (i / d) % len, pl = i / ((size_t)d * len);
+    const size_t dst = (pl * max_ctx + r) * d + c;
+    const uint64_t h = mix64(seed * 0x9E3779B97F4A7C15ull + dst);
+    const float u1 = ((float)(h >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+    const float u2 = (float)((h >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    const float v = sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958648f * u2);
+    if (kv16)
+      static_cast<uint16_t*>(kv)[dst] = (uint16_t)bf16_bits(v);
+    else
+      static_cast<float*>(kv)[dst] = v;
+  }
+}
+
+hipError_t launch_fill_kv_synthetic(void* kv, bool kv16, size_t planes, int len, int d,
+                                    long max_ctx, uint64_t seed, hipStream_t s) {
+  const size_t n = planes * (size_t)len * d;
+  if (n == 0) return hipSuccess;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(k_fill_kv_synthetic, dim3((unsigned)blocks), dim3(256), 0, s, kv, kv16,
+                     planes, len, d, max_ctx, seed);
+  return hipGetLastError();
+}
+
 hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s) {
   const int nq = p.d / 4;
   if (nq <= 256)

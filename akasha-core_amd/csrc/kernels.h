@@ -316,6 +316,10 @@ int dec_attn_max_splits();
 hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
                                 size_t rows, int S, int d, long seq_stride,
                                 const int2* rowmap, hipStream_t s);
+// N(0, 1) values (hash of seed and element offset) in rows [0, len) of
+// `planes` KV planes of [max_ctx][d] (f32, or bfloat16 when kv16).
+hipError_t launch_fill_kv_synthetic(void* kv, bool kv16, size_t planes, int len, int d,
+                                    long max_ctx, uint64_t seed, hipStream_t s);
 // With t0 and t1 set, the dispatch records them at its own start and end.
 hipError_t launch_dec_attn(const DecAttnParams& p, int batch, int hd,
                            hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);

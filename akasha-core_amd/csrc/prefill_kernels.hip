@@ -13,6 +13,11 @@ __global__ void k_embedding_rows(const uint32_t* tokens, const float* table,
                                  float* out, int d, uint32_t vocab) {
   const int t = blockIdx.x;
   const uint32_t id = tokens[t];
+  if (d % 4 != 0) {  // rows without 16-byte alignment: element by element
+    for (int c = threadIdx.x; c < d; c += blockDim.x)
+      out[(size_t)t * d + c] = id < vocab ? table[(size_t)id * d + c] : 0.f;
+    return;
+  }
   const float4* src = reinterpret_cast<const float4*>(table + (size_t)id * d);
   float4* dst = reinterpret_cast<float4*>(out + (size_t)t * d);
   for (int c = threadIdx.x; c < d / 4; c += blockDim.x)
@@ -1451,9 +1456,15 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   const float* qp = p.q + fs.q + hh * hd;
   const float* kp = p.k + fs.kv + hh * hd;
   const float* vp = p.v + fs.kv + hh * hd;
-  // Columns past the head size (hd a multiple of 4 below HD) read as zero.
+  // Columns past the head size read as zero.  A head size that is not a
+  // multiple of 4 leaves head rows without 16-byte alignment (and a last
+  // quad that reaches into the next head): such heads load element by
+  // element (hd is uniform, so the branch is too).
   auto col4 = [hd](const float* src, int c) {
-    return c < hd ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if ((hd & 3) == 0)
+      return c < hd ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+    return make_float4(c < hd ? src[0] : 0.f, c + 1 < hd ? src[1] : 0.f,
+                       c + 2 < hd ? src[2] : 0.f, c + 3 < hd ? src[3] : 0.f);
   };
 
   const int qi = q0 + wave * 32 + j;
@@ -2137,10 +2148,9 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
   if (p.hd <= 0 || p.d % p.hd != 0) return hipErrorInvalidValue;
   const int H = p.d / p.hd;
   if (p.hd > 32 && p.hd < 128 && p.hd != 64) {
-    // A head size between the MFMA kernels' (a multiple of 4): the split-bf16
-    // kernel of the next larger size, columns past hd zero (fp32-accurate,
-    // whatever p.x6 asks).
-    if (p.hd % 4 != 0) return hipErrorInvalidValue;
+    // A head size between the MFMA kernels': the split-bf16 kernel of the
+    // next larger size, columns past hd zero (fp32-accurate, whatever p.x6
+    // asks); heads that are not a multiple of 4 load element by element.
     const dim3 g(H, batch, (max_rows + 127) / 128);
     if (p.hd < 64)
       hipLaunchKernelGGL(k_flash_x6<64>, g, dim3(256), 0, s, p);

@@ -44,13 +44,11 @@ akh_status fail(akh_status st, const std::string& msg) {
     if (!(cond)) return fail(AKH_E_INVALID, std::string(msg)); \
   } while (0)
 
-// Head sizes the flash kernels take (the reference's FLASH_ATTENTION takes
-// any head_dim <= 128 dividing dim, emit.rs:564-572): up to 32 any (the
-// scalar kernel of the next power of two), beyond that a multiple of 4 up
-// to 128 (the MFMA kernel of 64 or 128 columns, the rest zero).
-bool supported_head_dim(uint32_t hd) {
-  return hd >= 1 && (hd <= 32 || (hd <= 128 && hd % 4 == 0));
-}
+// Head sizes the flash kernels take: any head_dim up to 128 dividing dim,
+// as the reference's FLASH_ATTENTION (emit.rs:564-572).  Up to 32 the
+// scalar kernel of the next power of two; beyond that the MFMA kernel of 64
+// or 128 columns, the columns past the head size zero.
+bool supported_head_dim(uint32_t hd) { return hd >= 1 && hd <= 128; }
 
 }  // namespace
 
@@ -346,8 +344,6 @@ extern "C" akh_status akh_flash_attention(akh_backend* be, const float* q,
             "flash_attention: head_dim must be <= 128");
   CHECK_ARG(shape.dim % shape.head_dim == 0,
             "flash_attention: dim must be divisible by head_dim");
-  CHECK_ARG(supported_head_dim(shape.head_dim),
-            "flash_attention: head_dim above 32 must be a multiple of 4");
   HIP_TRY(shader_flash_attention(q, k, v, out, l_cache, shape, meta, 1, be->stream));
   return AKH_OK;
 }
@@ -363,8 +359,6 @@ extern "C" akh_status akh_flash_attention_batched(akh_backend* be, const float* 
             "flash_attention: head_dim must be <= 128");
   CHECK_ARG(shape.dim % shape.head_dim == 0,
             "flash_attention: dim must be divisible by head_dim");
-  CHECK_ARG(supported_head_dim(shape.head_dim),
-            "flash_attention: head_dim above 32 must be a multiple of 4");
   HIP_TRY(shader_flash_attention(q, k, v, out, l_cache, shape, meta, batch, be->stream));
   return AKH_OK;
 }
@@ -571,8 +565,9 @@ struct akh_model {
   // SPLIT_X6 three bfloat16 terms per operand (k_gemm_x6, on transposed fp32
   // [N, K] copies), SPLIT_H3 two fp16 terms (k_gemm_h3, on fp16 planes), the
   // default where dim and ffn_hidden are multiples of 8.  wsplit holds the
-  // copies per parameter (layer matrices and lm_head); flash attention runs
-  // split-bfloat16 under either split.
+  // copies per parameter (layer matrices and lm_head).  Flash attention
+  // follows the split: split-fp16 (k_flash_h3, flagged and rerun like the
+  // GEMMs) under SPLIT_H3, split-bfloat16 (k_flash_x6) under SPLIT_X6.
   int prefill_split = AKH_SPLIT_NONE;
   std::vector<void*> wsplit;
   int* range_flag = nullptr;  // set by k_gemm_h3 on a non-finite result
@@ -1631,6 +1626,20 @@ extern "C" akh_status akh_session_set_len(akh_session* s, uint32_t len) {
   return upload_positions(s);
 }
 
+extern "C" akh_status akh_session_fill_cache_synthetic(akh_session* s, uint32_t len,
+                                                       uint64_t seed) {
+  CHECK_ARG(s && len <= s->max_ctx, "akh_session_fill_cache_synthetic: bad argument");
+  CHECK_ARG(!s->be->capturing, "akh_session_fill_cache_synthetic: graph capture in progress");
+  akh_status nc = need_caches(s);
+  if (nc != AKH_OK) return nc;
+  HIP_TRY(hipSetDevice(s->be->device));
+  const akh_model_config& c = s->m->cfg;
+  HIP_TRY(launch_fill_kv_synthetic(s->kv, s->kv16, (size_t)c.num_layers * 2 * s->B, (int)len,
+                                   (int)c.dim, (long)s->max_ctx, seed, s->be->stream));
+  std::fill(s->cur_len.begin(), s->cur_len.end(), len);
+  return upload_positions(s);
+}
+
 extern "C" akh_status akh_session_truncate(akh_session* s, uint32_t len) {
   CHECK_ARG(s, "akh_session_truncate: NULL session");
   for (uint32_t b = 0; b < s->B; ++b)
@@ -1953,33 +1962,40 @@ akh_status prefill_impl(akh_session* s, const uint32_t* tokens, const uint32_t* 
   pr.S = S;
   pr.ragged = ragged;
   const bool h3 = h3_prefill(s->m);
-  if (h3) HIP_TRY(clear_range_flag(s->m, st));
-  HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
-                                (int)d, c.vocab_size, st));
-  HIP_TRY(s->m->prefill_bf16 ? prefill_layers_bf16(s, pr) : prefill_layers_f32(s, pr, false));
-  bool redo = false;
-  if (h3) HIP_TRY(range_flag_set(s->m, st, &redo));
-  if (redo) {
-    // An operand beyond fp16's range: the same layers on the fp32 kernels
-    // (they rewrite every row and cache entry the first pass wrote).
-    HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
-                                  (int)d, c.vocab_size, st));
-    HIP_TRY(prefill_layers_f32(s, pr, true));
-  }
   // Last row of every sequence -> final RMSNorm -> lm_head -> greedy token
   // (inference.rs:120-168).
-  {
+  auto tail = [&]() -> hipError_t {
     RowsNormParams r = norm_base(s, s->m->final_norm());
     r.src = s->px;
     r.row0 = (long)S - 1;
     r.row_stride = (long)S;
     r.src_rows = ragged ? s->p_last : nullptr;
-    HIP_TRY(launch_rows_norm(r, (int)s->B, st));
+    hipError_t e = launch_rows_norm(r, (int)s->B, st);
+    if (e == hipSuccess) e = enqueue_lm_head(s);
+    if (e == hipSuccess)
+      e = launch_argmax_final(s->amax, lm_parts(s), (int)s->B, s->tok, nullptr, s->hist,
+                              (int)s->max_ctx + 1, (int)S, st, ragged ? s->p_len : nullptr);
+    return e;
+  };
+  if (h3) HIP_TRY(clear_range_flag(s->m, st));
+  HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
+                                (int)d, c.vocab_size, st));
+  HIP_TRY(s->m->prefill_bf16 ? prefill_layers_bf16(s, pr) : prefill_layers_f32(s, pr, false));
+  // The tail is queued before the range flag is read, so the stream does not
+  // wait for the host in the middle of the prefill; the flag is almost never
+  // set.
+  HIP_TRY(tail());
+  bool redo = false;
+  if (h3) HIP_TRY(range_flag_set(s->m, st, &redo));
+  if (redo) {
+    // An operand beyond fp16's range: the same layers on the fp32 kernels
+    // (they rewrite every row and cache entry the first pass wrote), then
+    // the tail again.
+    HIP_TRY(launch_embedding_rows(s->ptok, s->m->embedding(), s->px, (int)rows,
+                                  (int)d, c.vocab_size, st));
+    HIP_TRY(prefill_layers_f32(s, pr, true));
+    HIP_TRY(tail());
   }
-  HIP_TRY(enqueue_lm_head(s));
-  HIP_TRY(launch_argmax_final(s->amax, lm_parts(s),
-                              (int)s->B, s->tok, nullptr, s->hist,
-                              (int)s->max_ctx + 1, (int)S, st, ragged ? s->p_len : nullptr));
   for (uint32_t b = 0; b < s->B; ++b) s->cur_len[b] = lens[b];
   akh_status ps = upload_positions(s);
   if (ps != AKH_OK) return ps;
@@ -2546,7 +2562,10 @@ extern "C" akh_status akh_forward_loss(akh_forward* f, const uint32_t* tokens,
   PrefillRows pr;
   pr.rows = rows;
   pr.S = S;
-  const bool h3 = h3_prefill(f->m);
+  // The range flag needs a check whenever a GEMM may run k_gemm_h3: the
+  // layers under the split-fp16 prefill, and the lm_head whenever the model
+  // keeps its split-fp16 copy, also under the bf16-MFMA layers.
+  const bool h3 = f->m->prefill_split == AKH_SPLIT_H3;
   // The layers, final_norm and lm_head on every row (train.rs:154-177).
   auto forward = [&](bool exact) -> hipError_t {
     hipError_t e = launch_embedding_rows(s->ptok, f->m->embedding(), s->px, (int)rows, (int)d,
@@ -2566,15 +2585,22 @@ extern "C" akh_status akh_forward_loss(akh_forward* f, const uint32_t* tokens,
     if (e == hipSuccess) e = prefill_gemm(f->m, g, 2 + 6 * c.num_layers, GEMM_STORE, st, exact);
     return e;
   };
+  // The forward and the loss, whose copy to the host is queued before the
+  // range flag is read (one wait for both).
+  std::vector<float> l(rows);
+  auto forward_loss = [&](bool exact) -> hipError_t {
+    hipError_t e = forward(exact);
+    if (e == hipSuccess)
+      e = launch_cross_entropy(f->logits, f->targets, f->losses, (uint32_t)rows, f->ce, st);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(l.data(), f->losses, rows * 4, hipMemcpyDeviceToHost, st);
+    return e;
+  };
   if (h3) HIP_TRY(clear_range_flag(f->m, st));
-  HIP_TRY(forward(false));
+  HIP_TRY(forward_loss(false));
   bool redo = false;
   if (h3) HIP_TRY(range_flag_set(f->m, st, &redo));
-  if (redo) HIP_TRY(forward(true));  // an operand beyond fp16's range
-  // The loss.
-  HIP_TRY(launch_cross_entropy(f->logits, f->targets, f->losses, (uint32_t)rows, f->ce, st));
-  std::vector<float> l(rows);
-  HIP_TRY(hipMemcpyAsync(l.data(), f->losses, rows * 4, hipMemcpyDeviceToHost, st));
+  if (redo) HIP_TRY(forward_loss(true));  // an operand beyond fp16's range
   HIP_TRY(hipStreamSynchronize(st));
   // CrossEntropy::loss (layers.rs:512-515): sequential f32 sum over rows.
   float sum = 0.f;

@@ -224,6 +224,7 @@ _SIGS = {
     "akh_session_prefill_ragged": (ST, [P, P, P, P, P]),
     "akh_session_truncate": (ST, [P, U32]),
     "akh_session_set_len": (ST, [P, U32]),
+    "akh_session_fill_cache_synthetic": (ST, [P, U32, C.c_uint64]),
     "akh_session_set_kv_bf16": (ST, [P, C.c_int]),
     "akh_session_take_cache": (ST, [P, U32, P, P, C.POINTER(U32), C.POINTER(C.c_int)]),
     "akh_session_replace_cache": (ST, [P, U32, P, P, U32]),
@@ -747,6 +748,12 @@ class Session:
     def set_len(self, length: int):
         """Cache::cur_len = length for every sequence (rows untouched)."""
         _check(_lib.akh_session_set_len(self.handle, length), "set_len")
+
+    def fill_cache_synthetic(self, length: int, seed: int):
+        """Rows [0, length) of every K/V cache filled with N(0, 1) values
+        (hash of seed), then cur_len = length (measurement only)."""
+        _check(_lib.akh_session_fill_cache_synthetic(self.handle, length, seed),
+               "fill_cache_synthetic")
 
     def set_kv_bf16(self, enable: bool):
         """bfloat16 KV cache (the optional bf16 path); caches must be empty."""

@@ -85,20 +85,36 @@ def prefill_flop_parts(cfg, B, S, lm_rows=None):
 
 
 def prefill_rates(ms, gemm, attn, lm, h3_flop, x6_flop):
-    """Rates of a prefill that took `ms`: useful fp32 TFLOP/s; their fraction
-    of the fp32 MFMA peak (the roofline of fp32 arithmetic on this part);
-    and the MFMA pipes' busy fraction, the executed MFMA work at the peak rate
-    of the instructions that ran it: the split-fp16 GEMMs (`h3_flop` of the
-    useful flops) execute three fp16 products per multiply-add, the
-    split-bfloat16 ones (`x6_flop`) six bf16 products, both at the 16-bit
-    peak; everything else runs on fp32 MFMAs."""
+    """Rates of a prefill that took `ms`.
+
+    - `tflops`: useful fp32 work per second (2 x multiply-adds of the GEMMs,
+      the causal attention pairs and the lm_head rows).
+    - `fp32_equiv_over_fp32_peak`: that rate over the fp32 MFMA peak.  It is
+      not a fraction of any ceiling when the work runs on 16-bit MFMAs (it
+      can exceed 1): it says how the kernels compare with fp32 arithmetic.
+    - `roofline`: the MFMA work the kernels execute against the peak of the
+      instructions that execute it.  The split-fp16 kernels (`h3_flop` of the
+      useful flops) run three fp16 products per fp32 multiply-add, the
+      split-bfloat16 ones (`x6_flop`) six bf16 products, both on 16-bit MFMAs
+      (2516.6 TFLOP/s dense); the rest runs on fp32 MFMAs (157.3).  `frac`
+      = the time those pipes need at their peaks / the elapsed time."""
     t = ms / 1e3
     useful = gemm + attn + lm
-    busy = ((3 * h3_flop + 6 * x6_flop) / (BF16_MFMA_PEAK_TFLOPS * 1e12)
-            + (useful - h3_flop - x6_flop) / (FP32_MFMA_PEAK_TFLOPS * 1e12))
+    exec16 = 3 * h3_flop + 6 * x6_flop
+    exec32 = useful - h3_flop - x6_flop
+    busy = exec16 / (BF16_MFMA_PEAK_TFLOPS * 1e12) + exec32 / (FP32_MFMA_PEAK_TFLOPS * 1e12)
+    if exec16:
+        instr = ("v_mfma_f32_32x32x16_f16, 3 products per fp32 multiply-add" if h3_flop
+                 else "v_mfma_f32_32x32x16_bf16, 6 products per fp32 multiply-add")
+        roof = {"bound": "mfma", "instr": instr, "achieved": round(exec16 / t / 1e12, 2),
+                "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(busy / t, 4)}
+    else:
+        roof = {"bound": "mfma", "instr": "v_mfma_f32_32x32x2_f32",
+                "achieved": round(exec32 / t / 1e12, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(busy / t, 4)}
     return {"tflops": round(useful / t / 1e12, 2),
-            "fp32_roofline_frac": round(useful / t / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
-            "mfma_busy_frac": round(busy / t, 4)}
+            "fp32_equiv_over_fp32_peak": round(useful / t / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "roofline": roof}
 
 
 def scaled_decode(hip, be, model, cfg, T, steps):
@@ -113,13 +129,14 @@ def scaled_decode(hip, be, model, cfg, T, steps):
     kv = sum(2 * L * B * (T - steps + i + 1) * d * 4 for i in range(steps))
     s = hip.Session(model, T, B)
     out = {"decode_workload": f"{B} sequences in one session, {steps} steps to KV length "
-                              f"{T} over a zero KV prefix (set_len)",
+                              f"{T}, KV rows before them filled with N(0, 1) values "
+                              f"(akh_session_fill_cache_synthetic, seed 6)",
            "decode_launches_per_step": s.decode_launches()}
     for kv16 in (False, True):
         if kv16:
             s.set_len(0)
             s.set_kv_bf16(True)
-        s.set_len(T - steps)
+        s.fill_cache_synthetic(T - steps, 6)
         s.decode_greedy(1, want_tokens=False)  # capture + warm
         s.set_len(T - steps)
         be.synchronize()
@@ -168,7 +185,7 @@ def kernel_legs_only(pkg, hip, be, model, cfg, reps, scaled):
     """The per-kernel decode legs without any graph replay (for counter
     runs): config 4 at T = 481 after a 32 x 448 prefill with the KV length
     then set to 480, and with `scaled` config 5's 64-row session at
-    T = 2048 over a zero KV prefix."""
+    T = 2048 over KV rows filled with N(0, 1) values."""
     B, P, CTX = 32, 448, 512
     sess = hip.Session(model, CTX, B)
     prompt = pkg.synthetic_tokens(B * P, cfg.vocab_size, seed=4).reshape(B, P)
@@ -177,8 +194,17 @@ def kernel_legs_only(pkg, hip, be, model, cfg, reps, scaled):
     sess.set_len(480)
     log(f"bench: config 4 decode kernels, {reps} launches each")
     k4, a4 = decode_kernel_legs(sess, cfg, B, 481, reps)
+    # The same legs with the fused norm (akh_session_set_fused_norm): out_proj
+    # and ffn_down add their sums to the residual themselves, qkv_proj and
+    # ffn_up scale their A operand by the RMSNorm, and the norm kernel that
+    # remains is the final norm before the lm_head.
+    log(f"bench: config 4 decode kernels with the fused norm, {reps} launches each")
+    sess.set_fused_norm(True)
+    k4f, _ = decode_kernel_legs(sess, cfg, B, 481, reps)
+    sess.set_fused_norm(False)
     sess.close()
-    out = {"config4": {"T": 481, "kernels": k4, "attn_dispatch_ms": round(a4, 5)}}
+    out = {"config4": {"T": 481, "kernels": k4, "attn_dispatch_ms": round(a4, 5)},
+           "config4_fused_norm": {"T": 481, "kernels": k4f}}
     if scaled:
         c5 = pkg.ModelConfig.scaled()
         log("bench: scaled config weights (seed 5, bf16 values)")
@@ -187,7 +213,7 @@ def kernel_legs_only(pkg, hip, be, model, cfg, reps, scaled):
         m5.upload(w5)
         del w5
         s5 = hip.Session(m5, 2048, 64)
-        s5.set_len(2047)
+        s5.fill_cache_synthetic(2047, 6)
         log(f"bench: config 5 decode kernels, {reps} launches each")
         k5, a5 = decode_kernel_legs(s5, c5, 64, 2048, reps, wbytes=2)
         s5.close()
@@ -196,18 +222,15 @@ def kernel_legs_only(pkg, hip, be, model, cfg, reps, scaled):
     return out
 
 
-def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=True):
+def scaled_measurement(pkg, hip, be, w, steps=8, with_prefill=True, with_decode=True):
     """Config 5: the scaled architecture (dim 2048, 24 layers, 16 x 128, FFN
-    8192, vocab 50257) with bf16-valued weights (seed 5).  Decode: 64
+    8192, vocab 50257) with bf16-valued weights `w` (seed 5).  Decode: 64
     sequences (one session) for `steps` steps ending at KV length
-    2048, over a zero KV prefix declared with set_len (the cost of a step does
-    not depend on the cached values).  Prefill: 8 x 2048 (seed 7)."""
+    2048, over KV rows filled with N(0, 1) values.  Prefill: 8 x 2048
+    (seed 7)."""
     cfg = pkg.ModelConfig.scaled()
-    log("bench: scaled config weights (seed 5, bf16 values)")
-    w = pkg.synthetic_weights(cfg, seed=5, bf16=True)
     model = hip.Model(be, cfg)
     model.upload(w)
-    del w
     T, V = 2048, cfg.vocab_size
     out = {"workload": "config 5: scaled architecture, bf16-valued weights (seed 5)"}
     if with_decode:
@@ -230,8 +253,8 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
                                        "products; fp32-accurate, default)",
                     "prefill_ms": round(pms, 2), "prefill_tok_s": round(Bp * Sp / (pms / 1e3), 1),
                     "prefill_tflops": r["tflops"],
-                    "prefill_fp32_roofline_frac": r["fp32_roofline_frac"],
-                    "prefill_mfma_busy_frac": r["mfma_busy_frac"]})
+                    "prefill_fp32_equiv_over_fp32_peak": r["fp32_equiv_over_fp32_peak"],
+                    "prefill_roofline": r["roofline"]})
         # The same prefill with the layer GEMMs and flash on the fp32 MFMAs.
         log("bench: scaled config prefill 8 x 2048, fp32 MFMAs")
         split = model.prefill_split()
@@ -246,7 +269,7 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
         model.set_prefill_split(split)
         out.update({"prefill_fp32_mfma_ms": round(fms, 2),
                     "prefill_fp32_mfma_tok_s": round(Bp * Sp / (fms / 1e3), 1),
-                    "prefill_fp32_mfma_frac": round(fl / (fms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)})
+                    "prefill_fp32_mfma_roofline": prefill_rates(fms, g, a, lm, 0, 0)["roofline"]})
         # The optional bf16-MFMA prefill (logits within 2e-2 of f32).
         log("bench: scaled config prefill 8 x 2048, bf16 MFMA")
         model.set_prefill_bf16(True)
@@ -261,7 +284,11 @@ def scaled_measurement(pkg, hip, be, steps=8, with_prefill=True, with_decode=Tru
         out.update({"prefill_bf16_ms": round(bms, 2),
                     "prefill_bf16_tok_s": round(Bp * Sp / (bms / 1e3), 1),
                     "prefill_bf16_tflops": round(fl / (bms / 1e3) / 1e12, 2),
-                    "prefill_bf16_mfma_frac_bf16": round(fl / (bms / 1e3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)})
+                    "prefill_bf16_roofline": {
+                        "bound": "mfma", "instr": "v_mfma_f32_32x32x16_bf16, 1 product",
+                        "achieved": round(fl / (bms / 1e3) / 1e12, 2),
+                        "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(fl / (bms / 1e3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}})
         ps.close()
     model.close()
     return out
@@ -313,7 +340,8 @@ def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
     model.set_prefill_split(split)
     prefill["fp32_mfma"] = {"ms": round(p32, 3), "tok_s": round(Bp * Sp / (p32 / 1e3), 1),
                             "tflops": round(fl / (p32 / 1e3) / 1e12, 2),
-                            "mfma_frac": round(fl / (p32 / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
+                            **{k: v for k, v in prefill_rates(p32, g, a, lm, 0, 0).items()
+                               if k == "roofline"}}
     ps.close()
     # Trainer::forward + CrossEntropy on the same 16 x 512 rows: the
     # lm_head runs on every row (+2 rows d V flop) and the loss follows.
@@ -336,6 +364,55 @@ def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
         "mean_loss": round(mean_loss, 4), "flop": ffl}
     fw.close()
     return prefill
+
+
+def config2_measurement(hip, be, reps=10):
+    """Config 2: the flash-attention op, 8 sequences x 12 heads x 512 x 64,
+    N(0,1) from seed 2, scale 1/8.  As the reference issues it: one
+    FLASH_ATTENTION node per sequence at row_offset b * 512
+    (layers.rs:410-421; each node runs the key-split kernel), and the same
+    nodes as one launch (akh_flash_attention_batched).  Both run the
+    split-bfloat16 kernels (six bf16 products per fp32 multiply-add)."""
+    B2, S2, H2, hd2 = 8, 512, 12, 64
+    d2 = H2 * hd2
+    rng2 = np.random.default_rng(2)
+    q2, k2, v2 = (be.tensor(rng2.standard_normal(B2 * S2 * d2, dtype=np.float32))
+                  for _ in range(3))
+    o2, l2 = be.zeros(B2 * S2 * d2), be.zeros(S2 * H2)
+    metas = [hip.FlashAttnMeta(S2, d2, hd2, 0.125, b * S2) for b in range(B2)]
+    metas = [(m, be.meta(m)) for m in metas]
+
+    def flash_all():
+        for shape, meta in metas:
+            be.flash_attention(q2, k2, v2, o2, l2, shape, meta)
+    flash_all()
+    be.synchronize()
+    be.timer_start()
+    for _ in range(reps):
+        flash_all()
+    c2_ms = be.timer_stop() / reps
+    c2_flop = 2 * hd2 * S2 * (S2 + 1) * B2 * H2
+    rn = prefill_rates(c2_ms, 0, c2_flop, 0, 0, c2_flop)
+    bshape = hip.FlashAttnMeta(S2, d2, hd2, 0.125, 0)
+    bmeta = be.meta(bshape)
+    l2b = be.zeros(B2 * S2 * H2)
+    be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
+    be.synchronize()
+    be.timer_start()
+    for _ in range(reps):
+        be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
+    c2b_ms = be.timer_stop() / reps
+    rb = prefill_rates(c2b_ms, 0, c2_flop, 0, 0, c2_flop)
+    return {"workload": "config 2: flash attention 8 x 12 x 512 x 64 (seed 2)",
+            "kernel": "split-bf16 flash (fp32-accurate)", "flop": c2_flop,
+            "per_node_ms": round(c2_ms, 4),
+            "per_node_tflops": rn["tflops"],
+            "per_node_fp32_equiv_over_fp32_peak": rn["fp32_equiv_over_fp32_peak"],
+            "per_node_roofline": rn["roofline"],
+            "batched_ms": round(c2b_ms, 4),
+            "batched_tflops": rb["tflops"],
+            "batched_fp32_equiv_over_fp32_peak": rb["fp32_equiv_over_fp32_peak"],
+            "batched_roofline": rb["roofline"]}
 
 
 def cpu_baseline(cfg, weights, prompt_len, budget_s=10.0, max_steps=None, threads=1):
@@ -417,6 +494,56 @@ def cpu_prefill_baseline(cfg, weights, tokens, threads):
     return len(tokens) / dt, dt
 
 
+def cpu_config1(pkg, cfg, weights, threads):
+    """Config 1 in full on the oracle: prefill of the 64-token prompt
+    (seed 1), then 64 greedy decode steps, each token the first maximum of
+    the previous logits (InferenceSession::generate's greedy loop,
+    inference.rs:264-326).  Returns the figures and the 65 greedy tokens."""
+    ora = entry.load_oracle()
+    ora.set_threads(threads)
+    s = ora.OracleSession(cfg, weights, 128)
+    prompt = pkg.synthetic_tokens(64, cfg.vocab_size, seed=1)
+    t0 = time.perf_counter()
+    logits = s.prefill(prompt)
+    tp = time.perf_counter() - t0
+    toks = [ora.argmax(logits)]
+    t1 = time.perf_counter()
+    for _ in range(64):
+        toks.append(ora.argmax(s.decode_step(toks[-1])))
+    td = time.perf_counter() - t1
+    s.close()
+    ora.set_threads(1)
+    return {"value": round(64 / td, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "ms_per_token": round(td / 64 * 1e3, 3), "prefill_s": round(tp, 3),
+            "total_s": round(tp + td, 3),
+            "sample": "config 1 in full: oracle prefill of the 64-token prompt (seed 1), then "
+                      "64 greedy decode steps (value = decode tokens / decode time)"}, toks
+
+
+def cpu_config5(cfg, weights, threads, T=2048, budget_s=10.0, max_steps=16):
+    """A labelled config-5 slice on the oracle: one sequence of the scaled
+    architecture decoding at KV length up to T, over a zero KV prefix (the
+    cost of a step does not depend on the cached values), until `budget_s`
+    seconds or `max_steps` steps have run."""
+    ora = entry.load_oracle()
+    ora.set_threads(threads)
+    s = ora.OracleSession(cfg, weights, T)
+    s.set_len(T - max_steps)
+    tok, n = 1, 0
+    t0 = time.perf_counter()
+    while n < max_steps and time.perf_counter() - t0 < budget_s:
+        tok = ora.argmax(s.decode_step(tok))
+        n += 1
+    dt = time.perf_counter() - t0
+    s.close()
+    ora.set_threads(1)
+    return {"value": round(n / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "steps": n, "seconds": round(dt, 2),
+            "sample": f"config 5 slice: oracle decode of 1 sequence of the scaled architecture "
+                      f"(bf16-valued weights, seed 5), {n} steps at KV length "
+                      f"{T - max_steps + 1}..{T - max_steps + n}, zero KV prefix"}
+
+
 def host_cpu():
     """(model name, logical CPUs) of the host."""
     name = "unknown"
@@ -471,6 +598,9 @@ def main():
     ap.add_argument("--scaled-prefill-only", action="store_true",
                     help="measure only config 5's prefill legs and print them (for profiling: "
                          "no graph replays)")
+    ap.add_argument("--config2-only", action="store_true",
+                    help="measure only config 2's flash legs (8 per-node launches, then the "
+                         "batched launch, 10 timed rounds each) and print them (for profiling)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the per-kernel decode legs, no graph replay (for counter "
                          "runs); config 5's too unless --no-scaled")
@@ -485,7 +615,9 @@ def main():
     hip = pkg.hip
     if args.scaled_prefill_only:
         be = hip.Backend(0)
-        print(json.dumps({"scaled": scaled_measurement(pkg, hip, be, with_decode=False)}),
+        log("bench: scaled config weights (seed 5, bf16 values)")
+        w5 = pkg.synthetic_weights(pkg.ModelConfig.scaled(), seed=5, bf16=True)
+        print(json.dumps({"scaled": scaled_measurement(pkg, hip, be, w5, with_decode=False)}),
               flush=True)
         be.close()
         return
@@ -499,6 +631,11 @@ def main():
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=2)}),
               flush=True)
+        model.close()
+        be.close()
+        return
+    if args.config2_only:
+        print(json.dumps({"config2": config2_measurement(hip, be)}), flush=True)
         model.close()
         be.close()
         return
@@ -570,63 +707,30 @@ def main():
     # Config 1: batch-1 greedy latency (64-token prompt, seed 1; 64 steps).
     s1 = hip.Session(model, 128, 1)
     p1 = pkg.synthetic_tokens(64, cfg.vocab_size, seed=1).reshape(1, 64)
-    s1.prefill(p1, want_logits=False)
+    _, first = s1.prefill(p1, want_logits=False)
     s1.decode_greedy(8, want_tokens=False)  # capture + warm
     s1.truncate(64)
     be.synchronize()
     be.timer_start()
     s1.decode_greedy(64, want_tokens=False)
     c1_ms = be.timer_stop()
+    # The same 64 steps again for their tokens (compared with the CPU leg's).
+    s1.truncate(64)
+    config1_tokens = [int(first[0])] + [int(t) for t in s1.decode_greedy(64)[:, 0]]
     s1.close()
     c1_bytes = decode_step_bytes(cfg, 1, 64 + 32)
     config1 = {"workload": "config 1: hall-1.0 batch 1, 64-token prompt (seed 1), 64 greedy steps",
                "ms_per_token": round(c1_ms / 64, 4), "tok_s": round(64 / (c1_ms / 1e3), 1),
                "hbm_frac": round(c1_bytes / (c1_ms / 64 / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
 
-    # Config 2: the flash-attention op, 8 sequences x 12 heads x 512 x 64,
-    # N(0,1) from seed 2, scale 1/8, one launch per sequence at row_offset
-    # b * 512 as the reference's batched attention issues it.
-    B2, S2, H2, hd2 = 8, 512, 12, 64
-    d2 = H2 * hd2
-    rng2 = np.random.default_rng(2)
-    q2, k2, v2 = (be.tensor(rng2.standard_normal(B2 * S2 * d2, dtype=np.float32)) for _ in range(3))
-    o2, l2 = be.zeros(B2 * S2 * d2), be.zeros(S2 * H2)
-    metas = [(hip.FlashAttnMeta(S2, d2, hd2, 0.125, b * S2),) for b in range(B2)]
-    metas = [(m[0], be.meta(m[0])) for m in metas]
+    config2 = config2_measurement(hip, be)
 
-    def flash_all():
-        for shape, meta in metas:
-            be.flash_attention(q2, k2, v2, o2, l2, shape, meta)
-    flash_all()
-    be.synchronize()
-    be.timer_start()
-    for _ in range(10):
-        flash_all()
-    c2_ms = be.timer_stop() / 10
-    c2_flop = 2 * hd2 * S2 * (S2 + 1) * B2 * H2
-    # The same nodes as one launch (akh_flash_attention_batched).
-    bshape = hip.FlashAttnMeta(S2, d2, hd2, 0.125, 0)
-    bmeta = be.meta(bshape)
-    l2b = be.zeros(B2 * S2 * H2)
-    be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
-    be.synchronize()
-    be.timer_start()
-    for _ in range(10):
-        be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
-    c2b_ms = be.timer_stop() / 10
-    rb = prefill_rates(c2b_ms, 0, c2_flop, 0, 0, c2_flop)
-    config2 = {"workload": "config 2: flash attention 8 x 12 x 512 x 64 (seed 2)",
-               "kernel": "split-bf16 flash (fp32-accurate)",
-               "per_node_ms": round(c2_ms, 4),
-               "per_node_tflops": round(c2_flop / (c2_ms / 1e3) / 1e12, 2),
-               "batched_ms": round(c2b_ms, 4),
-               "batched_tflops": rb["tflops"],
-               "batched_fp32_roofline_frac": rb["fp32_roofline_frac"],
-               "batched_mfma_busy_frac": rb["mfma_busy_frac"]}
-
-    scaled = None
+    scaled, w5, c5 = None, None, pkg.ModelConfig.scaled()
+    if not args.no_scaled or not args.no_cpu:
+        log("bench: scaled config weights (seed 5, bf16 values)")
+        w5 = pkg.synthetic_weights(c5, seed=5, bf16=True)
     if not args.no_scaled:
-        scaled = scaled_measurement(pkg, hip, be, with_prefill=not args.no_prefill,
+        scaled = scaled_measurement(pkg, hip, be, w5, with_prefill=not args.no_prefill,
                                     with_decode=not args.no_scaled_decode)
 
     cpu = None
@@ -661,6 +765,36 @@ def main():
         cpu_omp["prefill"] = {"value": round(vp, 2), "unit": "tok/s", "cores": nt,
                               "sample": f"oracle prefill of config 3's sequence 0 (512 "
                                         f"tokens), column-split OpenMP ({tp:.1f} s)"}
+        # The same prefill on one thread, over the first 64 of those tokens.
+        log("bench: CPU baseline (oracle prefill of 64 tokens, 1 thread)")
+        vp1, tp1 = cpu_prefill_baseline(cfg, w, ptok[:64], 1)
+        cpu["prefill"] = {"value": round(vp1, 2), "unit": "tok/s", "cores": 1,
+                          "sample": f"oracle prefill of the first 64 tokens of config 3's "
+                                    f"sequence 0, one thread ({tp1:.1f} s)"}
+        # Config 1 in full (prompt + 64 greedy steps), one thread and all.
+        log("bench: CPU config 1 (64-token prefill + 64 greedy steps), 1 thread")
+        c1cpu, c1toks = cpu_config1(pkg, cfg, w, 1)
+        log(f"bench: CPU config 1, {nt} threads")
+        c1omp, _ = cpu_config1(pkg, cfg, w, nt)
+        c1cpu["tokens_match_gpu"] = c1toks == config1_tokens
+        config1["cpu_baseline"] = c1cpu
+        config1["cpu_baseline_omp"] = c1omp
+        # A config-5 slice: one sequence of the scaled architecture at KV ~2048.
+        log("bench: CPU config 5 slice (1 sequence at KV 2048), 1 thread")
+        c5cpu = cpu_config5(c5, w5, 1)
+        log(f"bench: CPU config 5 slice, {nt} threads")
+        c5omp = cpu_config5(c5, w5, nt, budget_s=4.0, max_steps=8)
+        log(f"bench: CPU config 5 prefill slice (64 tokens), {nt} threads")
+        p5 = pkg.synthetic_tokens(8 * 2048, c5.vocab_size, seed=7)[:64]
+        vp5, tp5 = cpu_prefill_baseline(c5, w5, p5, nt)
+        c5omp["prefill"] = {"value": round(vp5, 3), "unit": "tok/s", "cores": nt,
+                            "sample": f"oracle prefill of the first 64 tokens of config 5's "
+                                      f"prefill sequence 0 (seed 7), column-split OpenMP "
+                                      f"({tp5:.1f} s)"}
+        if scaled is None:
+            scaled = {}
+        scaled["cpu_baseline"] = c5cpu
+        scaled["cpu_baseline_omp"] = c5omp
     else:
         cpu_omp = None
 

@@ -307,9 +307,13 @@ akh_status akh_model_set_prefill_bf16(akh_model* m, int enable);
  *   AKH_SPLIT_NONE: the fp32 MFMAs (v_mfma_f32_32x32x2_f32).
  * Either split keeps a copy of every layer matrix and of lm_head (4 bytes an
  * element: fp16 planes, or transposed fp32), refreshed by
- * akh_model_upload_param, and runs flash attention (head_dim 64 / 128) on
- * split-bfloat16 MFMAs.  The bf16-MFMA prefill (akh_model_set_prefill_bf16),
- * when on, takes precedence. */
+ * akh_model_upload_param.  Flash attention (head_dim 64 / 128) follows the
+ * split: AKH_SPLIT_H3 runs it on split-fp16 MFMAs (two terms, three
+ * products), flagged and rerun in fp32 like the GEMMs when an operand is
+ * out of fp16's range; AKH_SPLIT_X6, and the per-shader FLASH_ATTENTION
+ * launchers whatever the split, run it on split-bfloat16 MFMAs.  The
+ * bf16-MFMA prefill (akh_model_set_prefill_bf16), when on, takes
+ * precedence. */
 #define AKH_SPLIT_NONE 0
 #define AKH_SPLIT_X6 1
 #define AKH_SPLIT_H3 2
@@ -435,6 +439,12 @@ akh_status akh_session_generate_ragged(akh_session* s, const uint32_t* tokens,
  * (inference_graphs.rs:515); rows below `len` keep whatever they hold.  Used
  * to time decode at a given context length. */
 akh_status akh_session_set_len(akh_session* s, uint32_t len);
+/* No reference counterpart (measurement only): fill rows [0, len) of every
+ * sequence's K and V caches, all layers, with N(0, 1) values from a hash of
+ * `seed` and the element's offset (bfloat16-rounded in a bf16 cache), then
+ * set every cur_len to `len` as akh_session_set_len does.  Decode over a
+ * long context can then be timed without prefilling it. */
+akh_status akh_session_fill_cache_synthetic(akh_session* s, uint32_t len, uint64_t seed);
 /* No reference counterpart (the reference's Cache is f32): with enable = 1
  * the session's KV cache holds bfloat16 rows (rounded to nearest even),
  * half the bytes decode attention streams; decode still computes in f32.

@@ -647,6 +647,35 @@ def test_prefill_h3_out_of_fp16_range_reruns_in_fp32(backend, pkg, where):
     f.close()
 
 
+def test_forward_bf16_layers_lm_head_out_of_fp16_range_reruns(backend, pkg):
+    # Under the bf16-MFMA layers the trainer forward's lm_head still runs the
+    # split-fp16 GEMM on the model's fp16 copy.  One lm_head weight of 1e5
+    # (beyond fp16's range) must flag and rerun it in fp32: the losses are
+    # finite and equal, bit for bit, to the forward whose lm_head runs on the
+    # fp32 MFMAs from the start (SPLIT_NONE; the bf16 layers are the same).
+    M = pkg.hip.Model
+    cfg = pkg.ModelConfig.new(300, 256, 4, 2, 80)
+    L = cfg.num_layers
+    w = pkg.synthetic_weights(cfg, seed=65)
+    lm = w[2 + 6 * L].copy()
+    lm.flat[4321] = 1e5
+    w[2 + 6 * L] = lm
+    model = M(backend, cfg)
+    model.upload(w)
+    assert model.prefill_split() == M.SPLIT_H3
+    model.set_prefill_bf16(True)
+    toks = pkg.synthetic_tokens(2 * 40, cfg.vocab_size, seed=66).reshape(2, 40)
+    tg = np.roll(toks, -1, axis=1)
+    f = pkg.hip.Forward(model, 2, 40)
+    mh, lsh = f.loss(toks, tg)
+    assert np.isfinite(lsh).all()
+    model.set_prefill_split(M.SPLIT_NONE)
+    mf, lsf = f.loss(toks, tg)
+    assert np.array_equal(lsh, lsf) and mh == mf
+    f.close()
+    model.close()
+
+
 @pytest.mark.parametrize("case", ["plain", "scaled_rows", "weight_beyond_fp16", "two_row_tiles",
                                   "two_row_tiles_dim384"])
 def test_lm_head_split_tiles_match_oracle(backend, pkg, ora, case):

@@ -3,8 +3,10 @@
 
 Two calls in a row, the second smaller, each compared token for token with
 akh_sample_rows on the same inputs (integer outputs: bit-exact), in greedy
-and sampling modes; and the workspace limit (rows * n <= 2^21) is enforced
-before anything runs.
+and sampling modes; inside a captured graph on a fresh backend, where the
+allocating akh_sample_rows is refused (its scratch cannot grow during
+capture), replayed and compared with akh_sample_rows run outside capture;
+and the workspace limit (rows * n <= 2^21) is enforced before anything runs.
 """
 
 import numpy as np
@@ -58,6 +60,44 @@ def test_noalloc_sampler_matches_sample_rows(backend, pkg):
     for t, k, p, pen in ((1.0, 0, 1.0, 1.0), (0.5, 5, 1.0, 2.0), (0.0, 0, 1.0, 1.0)):
         got, want = _both(backend, dev2, stride2, rows2, n2, t, k, p, pen)
         assert np.array_equal(got, want), (t, k, p, pen)
+
+
+def test_noalloc_sampler_inside_graph_capture(pkg):
+    # The callers this entry point is for cannot allocate: here, code under
+    # graph capture on a backend that has never grown its scratch.  Inputs
+    # are allocated before the capture; the capture records the no-alloc
+    # sampler, while akh_sample_rows is refused (its scratch would have to
+    # grow).  Each replay, with eager work and a synchronisation between
+    # replays, is checked against akh_sample_rows run outside capture.
+    hip = pkg.hip
+    be = hip.Backend(0)
+    try:
+        rng = np.random.default_rng(79)
+        rows, n = 16, 50257
+        dev, stride = _inputs(pkg, be, rng, rows, n, ties=True)
+        params = (0.8, 40, 0.95, 1.15)
+        args = (dev["logits"], rows, n, dev["out"], *params, dev["seen"], stride,
+                dev["lens"], dev["u"])
+        be.graph_begin()
+        try:
+            be.sample_rows_noalloc(*args)
+            with pytest.raises(hip.InvalidArgument):
+                be.sample_rows(*args)
+        finally:
+            g = be.graph_end()
+        be.sample_rows(*args)  # eager, outside capture: grows the scratch
+        want = dev["out"].download(np.uint32, rows).copy()
+        for rep in range(3):
+            dev["out"].upload(np.full(rows, 0xFFFFFFFF, np.uint32))
+            g.execute()
+            be.synchronize()
+            got = dev["out"].download(np.uint32, rows).copy()
+            assert np.array_equal(got, want), rep
+            be.sample_rows(*args)  # eager work between the replays
+            be.synchronize()
+        g.close()
+    finally:
+        be.close()
 
 
 def test_noalloc_sampler_rejects_oversized_input(backend, pkg):
