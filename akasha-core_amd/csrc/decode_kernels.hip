@@ -1565,6 +1565,13 @@ hipError_t launch_dec_lm(const DecGemmParams& p, int num_cus, hipStream_t s) {
 
 bool dec_norm_fusable(int K) { return K % 128 == 0 && K <= 4096; }
 
+// The shapes the batched decode kernels take: lanes read head rows four
+// columns at a time (k_dec_attn), activations are whole 32-column k-quad
+// tiles of at most 4096 columns (k_rows_norm, k_dec_gemm).
+bool dec_fast_shape(int d, int hd, int F) {
+  return hd >= 4 && hd <= 128 && hd % 4 == 0 && d % 32 == 0 && d <= 4096 && F % 32 == 0;
+}
+
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s) {
   // PRO_NORM reads [rows][K / 32] sums of squares four tiles at a time;
   // DEC_RESID writes them for N / 32 column tiles.
@@ -1732,10 +1739,39 @@ __global__ void k_kv_store_bf16(const float* __restrict__ k, const float* __rest
   }
 }
 
+// The same store element by element, for a dim that is not a multiple of 4.
+__global__ void k_kv_store_bf16_1(const float* __restrict__ k, const float* __restrict__ v,
+                                  uint16_t* kc, uint16_t* vc, int S, int d, long seq_stride,
+                                  const int2* __restrict__ rowmap, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t row = i / d, c = i % d;
+    size_t b, t;
+    if (rowmap) {
+      const int2 st = rowmap[row];
+      b = (size_t)st.x;
+      t = (size_t)st.y;
+    } else {
+      b = row / S;
+      t = row % S;
+    }
+    const size_t dst = b * seq_stride + t * d + c;
+    kc[dst] = (uint16_t)bf16_bits(k[row * d + c]);
+    vc[dst] = (uint16_t)bf16_bits(v[row * d + c]);
+  }
+}
+
 hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
                                 size_t rows, int S, int d, long seq_stride,
                                 const int2* rowmap, hipStream_t s) {
-  if (d % 4 != 0 || (!rowmap && S <= 0)) return hipErrorInvalidValue;
+  if (d <= 0 || (!rowmap && S <= 0)) return hipErrorInvalidValue;
+  if (d % 4 != 0) {
+    const size_t n = rows * d;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 65535u * 16u);
+    hipLaunchKernelGGL(k_kv_store_bf16_1, dim3((unsigned)std::max<size_t>(1, blocks)), dim3(256),
+                       0, s, k, v, kc, vc, S, d, seq_stride, rowmap, n);
+    return hipGetLastError();
+  }
   const size_t n4 = rows * (d / 4);
   const size_t blocks = std::min<size_t>((n4 + 255) / 256, 65535u * 16u);
   hipLaunchKernelGGL(k_kv_store_bf16, dim3((unsigned)std::max<size_t>(1, blocks)), dim3(256), 0,

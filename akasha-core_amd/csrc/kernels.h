@@ -272,6 +272,9 @@ int dec_gemm_splits(int role, int K, int N);
 // Whether the RMSNorm folds into the decode GEMMs (PRO_NORM / DEC_RESID)
 // for a residual width of K: a multiple of 128, at most 4096.
 bool dec_norm_fusable(int K);
+// Whether a model of dim d, head size hd and ffn_hidden F decodes on the
+// batched kernels (else on decode_generic.hip's).
+bool dec_fast_shape(int d, int hd, int F);
 hipError_t launch_dec_gemm(const DecGemmParams& p, int role, hipStream_t s);
 
 // lm_head: logits y[M, N] = xt . w and argmax partials amax[M, parts], where
@@ -316,6 +319,29 @@ int dec_attn_max_splits();
 hipError_t launch_kv_store_bf16(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
                                 size_t rows, int S, int d, long seq_stride,
                                 const int2* rowmap, hipStream_t s);
+// Decode for shapes the batched decode kernels do not take
+// (decode_generic.hip): activations in row-major rows [B, *].
+struct GenAttnParams {
+  const float* qkv;     // [B, 3d]: q, k, v of the step's token
+  const float2* rope;   // [max_ctx, hd / 2] (cos, sin)
+  void* kc;             // layer's K cache: sequence b at b * seq_stride (f32 or bf16)
+  void* vc;
+  long seq_stride;      // elements
+  const int* pos;       // per-sequence position of the token
+  const int* active;    // optional: rows with 0 are skipped
+  float* out;           // [B, d]
+  int d, hd;
+  float scale;
+  int kv16;
+};
+hipError_t launch_gen_attn(const GenAttnParams& p, int batch, hipStream_t s);
+// The first-max partial (value bits, index) of each of `rows` rows of n logits.
+hipError_t launch_gen_argmax_part(const float* logits, int rows, int n, uint2* part,
+                                  hipStream_t s);
+// dst row m = src row (src_rows ? src_rows[m] : row0 + m * row_stride), d floats.
+hipError_t launch_gen_gather_rows(const float* src, float* dst, int rows, int d, long row0,
+                                  long row_stride, const int* src_rows, hipStream_t s);
+
 // N(0, 1) values (hash of seed and element offset) in rows [0, len) of
 // `planes` KV planes of [max_ctx][d] (f32, or bfloat16 when kv16).
 hipError_t launch_fill_kv_synthetic(void* kv, bool kv16, size_t planes, int len, int d,

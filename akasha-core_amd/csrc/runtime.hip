@@ -1013,6 +1013,12 @@ struct akh_session {
   uint32_t* hist = nullptr; // [B, max_ctx + 1] token at each position
 
   int ks_qkv = 1, ks_out = 1, ks_up = 1, ks_down = 1;
+  // A shape the batched decode kernels do not take (dec_fast_shape): the
+  // step runs on decode_generic.hip's kernels over row-major activations
+  // (residual, normed rows, qkv, attention output, ffn), and the lm_head
+  // leaves one argmax partial per row.
+  bool generic = false;
+  float *gx = nullptr, *gxn = nullptr, *gqkv = nullptr, *gattn = nullptr, *gffn = nullptr;
   // 32-row tiles of the decode rows (B <= 32 * mt): activations are
   // [mt][K/4][32][4], partial tiles [splits][32 * mt][N].
   int mt = 1;
@@ -1077,6 +1083,8 @@ int lm_parts_max(const akh_session* s) {
   return dec_lm_parts((int)s->m->cfg.vocab_size, (int)s->m->cfg.dim, s->be->num_cus, s->mt,
                       false);
 }
+// The argmax partials per row the step's lm_head leaves.
+int argmax_parts(const akh_session* s) { return s->generic ? 1 : lm_parts(s); }
 
 void free_prefill(akh_session* s) {
   for (float* p : {s->px, s->pxn, s->pq, s->pattn, s->pffn, s->pk, s->pv})
@@ -1308,7 +1316,10 @@ hipError_t enqueue_lm_head(akh_session* s) {
 // out GEMM, residual + norm_2, up GEMM, down GEMM, residual + next norm;
 // lm_head, greedy argmax + position advance.  Reads tok/pos from the
 // device, so it can be replayed step after step with no host work.
+hipError_t enqueue_decode_generic(akh_session* s);
+
 hipError_t enqueue_decode_body(akh_session* s) {
+  if (s->generic) return enqueue_decode_generic(s);
   const akh_model_config& c = s->m->cfg;
   hipStream_t st = s->be->stream;
   RowsNormParams emb = norm_base(s, s->m->layer(0, W_NORM1));
@@ -1335,10 +1346,81 @@ hipError_t enqueue_decode_body(akh_session* s) {
   return e;
 }
 
+// A GEMM of the generic step: y (epi) a[B, K] w[K, N], on the fp32-MFMA
+// prefill GEMM (any M, N, K).
+hipError_t gen_gemm(akh_session* s, const float* a, const float* w, float* y, uint32_t N,
+                    uint32_t K, int epi) {
+  GemmParams g{};
+  g.a = a;
+  g.b = w;
+  g.c = y;
+  g.M = (int)s->B;
+  g.N = (int)N;
+  g.K = (int)K;
+  return launch_gemm(g, epi, s->be->stream);
+}
+
+// The final RMSNorm of the rows in gx, the lm_head and each row's first-max
+// partial (the generic step's and the generic prefill's tail).
+hipError_t gen_lm_tail(akh_session* s) {
+  const akh_model_config& c = s->m->cfg;
+  hipStream_t st = s->be->stream;
+  hipError_t e = launch_rows_rmsnorm(s->gx, s->m->final_norm(), s->gxn, (int)s->B,
+                                     (int)c.dim, c.norm_eps, st);
+  if (e == hipSuccess)
+    e = gen_gemm(s, s->gxn, s->m->lm_head(), s->logits, c.vocab_size, c.dim, GEMM_STORE);
+  if (e == hipSuccess)
+    e = launch_gen_argmax_part(s->logits, (int)s->B, (int)c.vocab_size, s->amax, st);
+  return e;
+}
+
+// build_decode_layer's step (inference_graphs.rs:339-509) on the generic
+// kernels, every sequence at its own position (pos on the device).
+hipError_t enqueue_decode_generic(akh_session* s) {
+  const akh_model_config& c = s->m->cfg;
+  hipStream_t st = s->be->stream;
+  const int B = (int)s->B, d = (int)c.dim;
+  const uint32_t hd = c.dim / c.num_heads;
+  hipError_t e = launch_embedding_rows(s->tok, s->m->embedding(), s->gx, B, d, c.vocab_size, st);
+  if (e == hipSuccess)
+    e = launch_rows_rmsnorm(s->gx, s->m->layer(0, W_NORM1), s->gxn, B, d, c.norm_eps, st);
+  for (uint32_t l = 0; l < c.num_layers && e == hipSuccess; ++l) {
+    e = gen_gemm(s, s->gxn, s->m->layer(l, W_QKV), s->gqkv, 3 * c.dim, c.dim, GEMM_STORE);
+    if (e == hipSuccess) {
+      GenAttnParams a{};
+      a.qkv = s->gqkv;
+      a.rope = s->rope;
+      a.kc = s->kv_at(l, 0);
+      a.vc = s->kv_at(l, 1);
+      a.seq_stride = s->seq_stride();
+      a.pos = s->pos;
+      a.active = s->active;
+      a.out = s->gattn;
+      a.d = d;
+      a.hd = (int)hd;
+      a.scale = 1.0f / sqrtf((float)hd);
+      a.kv16 = s->kv16 ? 1 : 0;
+      e = launch_gen_attn(a, B, st);
+    }
+    if (e == hipSuccess)
+      e = gen_gemm(s, s->gattn, s->m->layer(l, W_OUT), s->gx, c.dim, c.dim, GEMM_ADD);
+    if (e == hipSuccess)
+      e = launch_rows_rmsnorm(s->gx, s->m->layer(l, W_NORM2), s->gxn, B, d, c.norm_eps, st);
+    if (e == hipSuccess)
+      e = gen_gemm(s, s->gxn, s->m->layer(l, W_UP), s->gffn, c.ffn_hidden, c.dim, GEMM_SILU);
+    if (e == hipSuccess)
+      e = gen_gemm(s, s->gffn, s->m->layer(l, W_DOWN), s->gx, c.dim, c.ffn_hidden, GEMM_ADD);
+    if (e == hipSuccess && l + 1 < c.num_layers)
+      e = launch_rows_rmsnorm(s->gx, s->m->layer(l + 1, W_NORM1), s->gxn, B, d, c.norm_eps, st);
+  }
+  if (e == hipSuccess) e = gen_lm_tail(s);
+  return e;
+}
+
 hipError_t enqueue_decode(akh_session* s) {
   hipError_t e = enqueue_decode_body(s);
   if (e == hipSuccess)
-    e = launch_argmax_final(s->amax, lm_parts(s), (int)s->B, s->tok, s->pos, s->hist,
+    e = launch_argmax_final(s->amax, argmax_parts(s), (int)s->B, s->tok, s->pos, s->hist,
                             (int)s->max_ctx + 1, 0, s->be->stream);
   return e;
 }
@@ -1483,7 +1565,8 @@ extern "C" void akh_session_free(akh_session* s) {
                   s->p_qkv,  s->p_out,  s->p_up,   s->up_act, s->p_down,
                   s->logits, s->amax,   s->ssq,    s->rcount,
                   s->tok,    s->pos,    s->hist,   s->active, s->done,   s->gstart,
-                  s->gcount, s->ggen,   s->guni,   s->gwbuf};
+                  s->gcount, s->ggen,   s->guni,   s->gwbuf,  s->gx,     s->gxn,
+                  s->gqkv,   s->gattn,  s->gffn};
   for (void* p : bufs)
     if (p) hipFree(p);
   delete s;
@@ -1514,27 +1597,26 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
             "akh_session_new: batch must be in 1..64");
   CHECK_ARG(max_context_len >= 1, "akh_session_new: max_context_len is 0");
   const uint32_t hd = c.dim / c.num_heads;
-  // RoPE rotates pairs inside a head (cpu.rs:84-109): an even head size; the
-  // decode attention reads rows four columns per lane.
-  CHECK_ARG(supported_head_dim(hd) && hd % 2 == 0 && (!decode || (hd >= 4 && hd % 4 == 0)),
-            "akh_session_new: head_dim must be even and at most 128, a multiple of 4 "
-            "for decoding");
-  CHECK_ARG(!decode || (c.dim % 32 == 0 && c.dim <= 4096),
-            "akh_session_new: dim must be a multiple of 32, at most 4096");
-  CHECK_ARG(!decode || c.ffn_hidden % 32 == 0,
-            "akh_session_new: ffn_hidden must be a multiple of 32");
+  // RoPE rotates pairs inside a head (cpu.rs:84-109): an even head size, at
+  // most 128 (FLASH_ATTENTION's limit, emit.rs:564-567).
+  CHECK_ARG(supported_head_dim(hd) && hd % 2 == 0,
+            "akh_session_new: head_dim must be even and at most 128");
 
   akh_session* s = new akh_session();
+  // Shapes outside the batched decode kernels decode on the generic ones.
+  s->generic = decode && !dec_fast_shape(c.dim, hd, c.ffn_hidden);
   s->m = m;
   s->be = m->be;
   s->max_ctx = max_context_len;
   s->B = batch;
   s->cur_len.assign(batch, 0);
   s->has_cache.assign(batch, 1);
-  s->ks_qkv = dec_gemm_splits(DEC_CFG_QKV, c.dim, 3 * c.dim);
-  s->ks_out = dec_gemm_splits(DEC_CFG_OUT, c.dim, c.dim);
-  s->ks_up = dec_gemm_splits(DEC_CFG_UP, c.dim, c.ffn_hidden);
-  s->ks_down = dec_gemm_splits(DEC_CFG_DOWN, c.ffn_hidden, c.dim);
+  if (!s->generic) {
+    s->ks_qkv = dec_gemm_splits(DEC_CFG_QKV, c.dim, 3 * c.dim);
+    s->ks_out = dec_gemm_splits(DEC_CFG_OUT, c.dim, c.dim);
+    s->ks_up = dec_gemm_splits(DEC_CFG_UP, c.dim, c.ffn_hidden);
+    s->ks_down = dec_gemm_splits(DEC_CFG_DOWN, c.ffn_hidden, c.dim);
+  }
 
   s->mt = batch > 32 ? 2 : 1;
   // Activation and partial tiles hold R rows; the per-row step state holds
@@ -1547,7 +1629,15 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
   };
   alloc((void**)&s->kv, (size_t)c.num_layers * 2 * batch * max_context_len * d * 4);
   alloc((void**)&s->rope, (size_t)max_context_len * (hd / 2) * sizeof(float2));
-  if (decode) {
+  if (decode && s->generic) {
+    const size_t Bs = batch;
+    alloc((void**)&s->gx, Bs * d * 4);
+    alloc((void**)&s->gxn, Bs * d * 4);
+    alloc((void**)&s->gqkv, Bs * 3 * d * 4);
+    alloc((void**)&s->gattn, Bs * d * 4);
+    alloc((void**)&s->gffn, Bs * F * 4);
+  }
+  if (decode && !s->generic) {
   alloc((void**)&s->xt, R * d * 4);
   alloc((void**)&s->xnt, R * d * 4);
   alloc((void**)&s->attn_t, (size_t)dec_attn_max_splits() * R * d * 4);
@@ -1561,8 +1651,10 @@ akh_status session_create(akh_model* m, uint32_t max_context_len, uint32_t batch
     alloc((void**)&s->ssq, R * (d / 32) * 4);
     alloc((void**)&s->rcount, (d / 32) * sizeof(int));  // zeroed by alloc
   }
+  }
+  if (decode) {
   alloc((void**)&s->logits, R * V * 4);
-  alloc((void**)&s->amax, R * (size_t)lm_parts_max(s) * sizeof(uint2));
+  alloc((void**)&s->amax, R * (size_t)(s->generic ? 1 : lm_parts_max(s)) * sizeof(uint2));
   alloc((void**)&s->tok, RB * 4);
   alloc((void**)&s->pos, RB * 4);
   alloc((void**)&s->hist, (size_t)batch * (max_context_len + 1) * 4);
@@ -1965,6 +2057,15 @@ akh_status prefill_impl(akh_session* s, const uint32_t* tokens, const uint32_t* 
   // Last row of every sequence -> final RMSNorm -> lm_head -> greedy token
   // (inference.rs:120-168).
   auto tail = [&]() -> hipError_t {
+    if (s->generic) {
+      hipError_t e = launch_gen_gather_rows(s->px, s->gx, (int)s->B, (int)d, (long)S - 1,
+                                            (long)S, ragged ? s->p_last : nullptr, st);
+      if (e == hipSuccess) e = gen_lm_tail(s);
+      if (e == hipSuccess)
+        e = launch_argmax_final(s->amax, 1, (int)s->B, s->tok, nullptr, s->hist,
+                                (int)s->max_ctx + 1, (int)S, st, ragged ? s->p_len : nullptr);
+      return e;
+    }
     RowsNormParams r = norm_base(s, s->m->final_norm());
     r.src = s->px;
     r.row0 = (long)S - 1;
@@ -2395,6 +2496,8 @@ extern "C" akh_status akh_session_time_decode_kernel(akh_session* s,
                                                      float* avg_ms) {
   CHECK_ARG(s && avg_ms && reps > 0, "akh_session_time_decode_kernel: bad argument");
   CHECK_ARG(kernel >= 0 && kernel <= 6, "akh_session_time_decode_kernel: bad kernel");
+  CHECK_ARG(!s->generic, "akh_session_time_decode_kernel: times the batched decode kernels, "
+                         "which this session's shape does not run");
   for (uint32_t b = 0; b < s->B; ++b)
     CHECK_ARG(s->cur_len[b] >= 1 && s->cur_len[b] < s->max_ctx,
               "akh_session_time_decode_kernel: needs 1 <= cur_len < max_ctx");
@@ -2432,6 +2535,8 @@ extern "C" akh_status akh_session_time_decode_attn(akh_session* s, uint32_t reps
                                                    float* avg_ms) {
   CHECK_ARG(s && avg_ms && reps > 0 && reps <= 4096,
             "akh_session_time_decode_attn: bad argument");
+  CHECK_ARG(!s->generic, "akh_session_time_decode_attn: times the batched decode kernels, "
+                         "which this session's shape does not run");
   for (uint32_t b = 0; b < s->B; ++b)
     CHECK_ARG(s->cur_len[b] >= 1 && s->cur_len[b] < s->max_ctx,
               "akh_session_time_decode_attn: needs 1 <= cur_len < max_ctx");
@@ -2480,7 +2585,8 @@ extern "C" akh_status akh_session_set_fused_norm(akh_session* s, int enable) {
   CHECK_ARG(s, "akh_session_set_fused_norm: NULL session");
   CHECK_ARG(!s->be->capturing, "akh_session_set_fused_norm: graph capture in progress");
   CHECK_ARG(!enable || s->ssq,
-            "akh_session_set_fused_norm: needs a decode session whose dim is a multiple of "
+            "akh_session_set_fused_norm: needs a decode session on the batched kernels "
+            "whose dim is a multiple of "
             "128, at most 4096");
   if (s->fuse_out != (enable != 0)) {
     HIP_TRY(hipSetDevice(s->be->device));

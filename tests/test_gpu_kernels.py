@@ -143,7 +143,12 @@ def _flash(backend, h, q, k, v, seq, dim, hd, row_offset=0, total_rows=None):
                                           # head sizes that are not powers of two (emit.rs:
                                           # 564-572 takes any head_dim <= 128)
                                           (40, 2, 6), (33, 3, 12), (50, 4, 24), (77, 2, 48),
-                                          (200, 2, 80), (130, 3, 96), (150, 1, 100)])
+                                          (200, 2, 80), (130, 3, 96), (150, 1, 100),
+                                          # head sizes that are not multiples of 4: rows
+                                          # without 16-byte alignment, loaded element by
+                                          # element
+                                          (70, 2, 34), (90, 3, 50), (140, 2, 126), (60, 3, 33),
+                                          (45, 1, 65)])
 def test_flash_attention(backend, pkg, ora, seq, heads, hd):
     # flash_attention_matches_cpu_reference (emit.rs:1001-1098), tol 1e-3.
     h = pkg.hip
