@@ -1890,20 +1890,26 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
 
 // k_flash_x6 for grids too small to fill the part (a single sequence's
 // FLASH_ATTENTION node): one 32-query tile per block, its key blocks dealt
-// round-robin to the 4 waves.  Each wave stages its own K and V^T planes in
-// a private LDS region (no block barrier in the key loop) and keeps its own
-// softmax state; at the end the four partial states merge through LDS:
-// M = max m_w, O = sum O_w 2^(m_w - M) / sum l_w 2^(m_w - M).  The heaviest
-// tile walks a quarter of the key blocks on its critical path.  Scores,
+// round-robin to the block's NW waves.  Each wave stages its own key block
+// in a private LDS region and keeps its own softmax state, so the key loop
+// has no block barrier; at the end the partial states merge through LDS:
+// M = max m_w, O = sum O_w 2^(m_w - M) / sum l_w 2^(m_w - M).  A wave stages
+// K's three planes, takes the scores, then stages V^T's three planes in the
+// same region for the output products, so a region holds one of the two
+// (HD 64: 15 KB, eight waves in 123 KB; HD 128: 31 KB, four waves).  The
+// next key block's K rows are loaded while the wave works on this one's
+// scores and its V rows while it takes this one's output.  The heaviest
+// tile walks 1 / NW of the key blocks on its critical path.  Scores,
 // products and statistics are those of k_flash_x6.
-template <int HD>
-__global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
-  constexpr int KB = 32, NW = 4, NT = HD / 32, NQ = HD / 16;
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void k_flash_x6w(FlashParams p) {
+  constexpr int KB = 32, NT = HD / 32, NQ = HD / 16;
   constexpr int KP = HD + 8, VP = KB + 8, CPR = HD / 4;
   constexpr int KPT = KB * CPR / 64;  // consecutive keys staged per lane
-  static_assert(KPT == 8, "a wave stages 32 keys as 4 groups of 8");
+  static_assert(KPT == 8 || KPT == 16, "a wave stages 32 keys in runs of 8 or 16");
   constexpr int K_PLANE = KB * KP, V_PLANE = HD * VP;  // bf16 elements
-  constexpr int W_BYTES = 3 * (K_PLANE + V_PLANE) * 2;
+  constexpr int K_BYTES = 3 * K_PLANE * 2, V_BYTES = 3 * V_PLANE * 2;
+  constexpr int W_BYTES = K_BYTES > V_BYTES ? K_BYTES : V_BYTES;
   constexpr int OS = 33;                                // merge row stride
   constexpr int M_BYTES = NW * (HD * OS + 64) * 4;
   __shared__ __align__(16) unsigned char lds[NW * W_BYTES > M_BYTES ? NW * W_BYTES : M_BYTES];
@@ -1921,9 +1927,7 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
   const int j = lane & 31, h = lane >> 5;
   unsigned char* wl = lds + wave * W_BYTES;
   auto Ks = [&](int pl) { return reinterpret_cast<uint16_t (*)[KP]>(wl) + pl * KB; };
-  auto Vt = [&](int pl) {
-    return reinterpret_cast<uint16_t (*)[VP]>(wl + 3 * K_PLANE * 2) + pl * HD;
-  };
+  auto Vt = [&](int pl) { return reinterpret_cast<uint16_t (*)[VP]>(wl) + pl * HD; };
 
   const float* qp = p.q + fs.q + hh * HD;
   const float* kp = p.k + fs.kv + hh * HD;
@@ -1947,16 +1951,15 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
   const int kend = min(S, q0 + 32);
   const int nkb = (kend + KB - 1) / KB;
 
-  // Staging: lane l takes dims 4 (l % CPR) .. + 3 of keys 8 (l / CPR) .. + 7.
+  // Staging: lane l takes dims 4 (l % CPR) .. + 3 of keys KPT (l / CPR) ..
+  // + KPT - 1.
   const int sc = (lane % CPR) * 4, sk = (lane / CPR) * KPT;
   float4 kr[KPT], vr[KPT];
-  auto load_kv = [&](int kb) {
+  auto load_rows = [&](const float* src, int kb, float4 (&r)[KPT]) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int key = kb * KB + sk + i;
-      const size_t off = (size_t)(key < S ? key : 0) * d + sc;
-      kr[i] = *reinterpret_cast<const float4*>(kp + off);
-      vr[i] = *reinterpret_cast<const float4*>(vp + off);
+      r[i] = *reinterpret_cast<const float4*>(src + (size_t)(key < S ? key : 0) * d + sc);
     }
   };
   auto split_pair = [](float a, float c, uint32_t (&t)[3]) {
@@ -1965,9 +1968,13 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
     t[1] = cvt_pk_bf16(ra, rc);
     t[2] = cvt_pk_bf16(ra - __uint_as_float(t[1] << 16), rc - __uint_as_float(t[1] & 0xFFFF0000u));
   };
-  if (wave < nkb) load_kv(wave);
+  if (wave < nkb) {
+    load_rows(kp, wave, kr);
+    load_rows(vp, wave, vr);
+  }
   for (int kb = wave; kb < nkb; kb += NW) {
-    // The wave's own region: its reads of the previous key block were
+    const bool more = kb + NW < nkb;
+    // The wave's own region: its reads of the previous key block's V^T were
     // issued before these writes, and one wave's LDS operations complete in
     // order; the wave barrier keeps the compiler from moving them across.
     __builtin_amdgcn_wave_barrier();
@@ -1980,24 +1987,9 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
       for (int pl = 0; pl < 3; ++pl)
         *reinterpret_cast<uint2*>(&Ks(pl)[sk + i][sc]) = make_uint2(lo[pl], hi[pl]);
     }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint32_t t[4][3];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 a = vr[2 * g], e = vr[2 * g + 1];
-        const float x0 = c == 0 ? a.x : c == 1 ? a.y : c == 2 ? a.z : a.w;
-        const float x1 = c == 0 ? e.x : c == 1 ? e.y : c == 2 ? e.z : e.w;
-        split_pair(x0, x1, t[g]);
-      }
-#pragma unroll
-      for (int pl = 0; pl < 3; ++pl)
-        *reinterpret_cast<uint4*>(&Vt(pl)[sc + c][sk]) =
-            make_uint4(t[0][pl], t[1][pl], t[2][pl], t[3][pl]);
-    }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the writes have landed
     __builtin_amdgcn_wave_barrier();
-    if (kb + NW < nkb) load_kv(kb + NW);
+    if (more) load_rows(kp, kb + NW, kr);
     const int j0 = kb * KB;
 
     f32x16 st = zero16();
@@ -2014,6 +2006,28 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
       st = mfma_bf16(kf[0], bf16x8_of(qf[1][s]), st);
       st = mfma_bf16(kf[0], bf16x8_of(qf[0][s]), st);
     }
+    // The score MFMAs consumed every K fragment read, so those reads have
+    // completed: V^T may overwrite the region.
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int run = 0; run < KPT / 8; ++run) {
+        uint32_t t[4][3];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 a = vr[8 * run + 2 * g], e = vr[8 * run + 2 * g + 1];
+          const float x0 = c == 0 ? a.x : c == 1 ? a.y : c == 2 ? a.z : a.w;
+          const float x1 = c == 0 ? e.x : c == 1 ? e.y : c == 2 ? e.z : e.w;
+          split_pair(x0, x1, t[g]);
+        }
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint4*>(&Vt(pl)[sc + c][sk + 8 * run]) =
+              make_uint4(t[0][pl], t[1][pl], t[2][pl], t[3][pl]);
+      }
+    }
+    if (more) load_rows(vp, kb + NW, vr);
     const bool masked = j0 + KB - 1 > q0 || j0 + KB > S;
     float pm = -INFINITY;
 #pragma unroll
@@ -2054,12 +2068,14 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
                  make_float4(st[8 * half + 4], st[8 * half + 5], st[8 * half + 6],
                              st[8 * half + 7]),
                  pf[half][0], pf[half][1], pf[half][2]);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V^T writes have landed
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         // V^T rows of the same keys: two runs of four (the staging writes
-        // eight consecutive keys per lane; k_flash_x6's permuted layout,
+        // eight consecutive keys per store; k_flash_x6's permuted layout,
         // which would split them, measured slower here).
         bf16x8 vf[3];
 #pragma unroll
@@ -2091,7 +2107,7 @@ __global__ __launch_bounds__(256) void k_flash_x6w(FlashParams p) {
   if (h == 0) ML[wave * 32 + j] = make_float2(mrow, lrow);
   __syncthreads();
   float* op = p.o + fs.o + hh * HD;
-  for (int e = tid; e < 32 * HD; e += 256) {
+  for (int e = tid; e < 32 * HD; e += 64 * NW) {
     const int qr = e / HD, dim = e % HD, qrow = q0 + qr;
     if (qrow >= S) continue;
     float2 ml[NW];
@@ -2163,11 +2179,14 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
     // causal block is dispatched before any shorter one, so the grid ends on
     // short blocks (longest-first scheduling).
     const dim3 g(H, batch, (max_rows + 127) / 128);
-    if (p.x6 && p.hd == 64 && (long)g.x * g.y * g.z < flash_small_grid()) {
+    if (p.x6 && (long)g.x * g.y * g.z < flash_small_grid()) {
       // Fewer 128-query blocks than CUs: 32-query tiles, keys split over
       // the block's waves (k_flash_x6w).
-      hipLaunchKernelGGL(k_flash_x6w<64>, dim3(H, batch, (max_rows + 31) / 32), dim3(256), 0,
-                         s, p);
+      const dim3 gw(H, batch, (max_rows + 31) / 32);
+      if (p.hd == 64)
+        hipLaunchKernelGGL((k_flash_x6w<64, 8>), gw, dim3(512), 0, s, p);
+      else
+        hipLaunchKernelGGL((k_flash_x6w<128, 4>), gw, dim3(256), 0, s, p);
     } else if (p.x6 == FLASH_H3) {
       if (p.hd == 64)
         hipLaunchKernelGGL(k_flash_h3<64>, g, dim3(256), 0, s, p);

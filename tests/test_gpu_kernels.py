@@ -182,7 +182,7 @@ def test_flash_attention_live_meta_bounds_work(backend, pkg, ora, hd):
     # The grid is sized from the recorded shape (200 rows); the meta read
     # when the kernel runs says 150: rows 0..149 are attention over the first
     # 150 tokens, rows past them stay untouched, and l_cache covers 150 rows.
-    # hd 64 runs the key-split kernel (a small grid), hd 128 the 128-query one.
+    # Both head sizes run the key-split kernel (a small grid).
     h = pkg.hip
     heads, S, live = 2, 200, 150
     dim = heads * hd
