@@ -77,6 +77,35 @@ def test_generic_shape_session_matches_oracle(backend, pkg, ora, dim, heads, ffn
     model.close()
 
 
+@pytest.mark.parametrize("kv16", [False, True])
+def test_generic_shape_long_context(backend, pkg, ora, kv16):
+    # The generic attention holds 1024 scores per pass over the keys: a
+    # 1500-token prompt and decode steps past it take two passes, the
+    # running maximum and sum rescaled between them.  Against the oracle
+    # (logits within 1e-3, or 2e-2 with the bfloat16 cache).
+    cfg, w, model = _model(pkg, backend, 100, 2, 2, 400, seed=17)
+    r = np.random.default_rng(18)
+    prompt = r.integers(0, cfg.vocab_size, size=(2, 1500)).astype(np.uint32)
+    s = pkg.hip.Session(model, 1600, 2)
+    if kv16:
+        s.set_kv_bf16(True)
+    logits, nxt = s.prefill(prompt)
+    got = [(logits, nxt)] + [s.decode_step(None) for _ in range(3)]
+    tol = 2e-2 if kv16 else TOL
+    for b in range(2):
+        o = ora.OracleSession(cfg, w, 1600)
+        ref = o.prefill(prompt[b])
+        for i in range(4):
+            if i:
+                ref = o.decode_step(int(got[i - 1][1][b]))
+            assert np.abs(got[i][0][b] - ref).max() < tol, f"sequence {b} step {i}"
+            if not kv16:
+                assert int(got[i][1][b]) == ora.argmax(ref), f"sequence {b} step {i}"
+        o.close()
+    s.close()
+    model.close()
+
+
 @pytest.mark.parametrize("dim,heads,ffn", [(100, 2, 400), (102, 3, 408)])
 def test_generic_shape_bf16_kv_cache(backend, pkg, ora, dim, heads, ffn):
     # The bfloat16 KV cache on the generic kernels: logits within 2e-2 of
