@@ -17,6 +17,7 @@ library is missing, ``load()`` raises.
 
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
 import weakref
@@ -332,6 +333,21 @@ def _p(x):
     return x
 
 
+# Backends still open when the interpreter exits are closed (children
+# first) before the HIP runtime's own teardown, which would otherwise run
+# before the garbage collector frees them in arbitrary order.
+_LIVE_BACKENDS = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_backends():
+    for be in list(_LIVE_BACKENDS):
+        try:
+            be.close()
+        except Exception:
+            pass
+
+
 class Backend:
     """HipBackend: one device, one stream (default priority)."""
 
@@ -342,6 +358,7 @@ class Backend:
         self.handle = h
         # Sessions, models and tensors must be released before the backend.
         self._children = weakref.WeakSet()
+        _LIVE_BACKENDS.add(self)
 
     def _adopt(self, obj):
         self._children.add(obj)
