@@ -1242,7 +1242,7 @@ __global__ __launch_bounds__(NTH) void k_rows_norm(RowsNormParams p) {
 
 __global__ __launch_bounds__(256) void k_argmax_final(
     const uint2* part, int ntiles, uint32_t* tok, int* pos, uint32_t* hist,
-    int hist_stride, int next_pos, const int* at) {
+    int hist_stride, int next_pos, const int* at, const float* logits, long lstride) {
   const int m = blockIdx.x;
   float bv = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
@@ -1252,7 +1252,10 @@ __global__ __launch_bounds__(256) void k_argmax_final(
   }
   block_amax256(bv, bi);
   if (threadIdx.x == 0) {
-    const uint32_t id = bi == 0xFFFFFFFFu ? 0u : bi;
+    // The reference's scan (sampling.rs:83-91) starts from index 0; a NaN
+    // logit there never loses a comparison, so it stays the answer.
+    const bool nan0 = logits && __builtin_isnan(logits[(size_t)m * lstride]);
+    const uint32_t id = bi == 0xFFFFFFFFu || nan0 ? 0u : bi;
     uint32_t* hrow = hist ? hist + (size_t)m * hist_stride : nullptr;
     if (pos) {
       const int p0 = pos[m];
@@ -1836,9 +1839,10 @@ hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s) {
 
 hipError_t launch_argmax_final(const uint2* part, int ntiles, int M,
                                uint32_t* tok, int* pos, uint32_t* hist,
-                               int hist_stride, int next_pos, hipStream_t s, const int* at) {
+                               int hist_stride, int next_pos, hipStream_t s, const int* at,
+                               const float* logits, long lstride) {
   hipLaunchKernelGGL(k_argmax_final, dim3(M), dim3(256), 0, s, part, ntiles,
-                     tok, pos, hist, hist_stride, next_pos, at);
+                     tok, pos, hist, hist_stride, next_pos, at, logits, lstride);
   return hipGetLastError();
 }
 

@@ -377,7 +377,9 @@ struct RowsNormParams {
 
 hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s);
 
-// Greedy token per row from the lm_head partials.  With `pos`, also the
+// Greedy token per row from the lm_head partials; with `logits` (row m at
+// m * lstride), a row whose first logit is NaN takes token 0, as the
+// reference's scan from index 0 does.  With `pos`, also the
 // decode step's bookkeeping on the device: hist[m, pos] = consumed token,
 // hist[m, pos + 1] = chosen token, pos[m] += 1.  Without it (prefill) the
 // chosen token is recorded at hist[m, next_pos], or at hist[m, at[m]] when
@@ -385,7 +387,8 @@ hipError_t launch_rows_norm(const RowsNormParams& p, int M, hipStream_t s);
 hipError_t launch_argmax_final(const uint2* part, int ntiles, int M,
                                uint32_t* tok, int* pos, uint32_t* hist,
                                int hist_stride, int next_pos, hipStream_t s,
-                               const int* at = nullptr);
+                               const int* at = nullptr, const float* logits = nullptr,
+                               long lstride = 0);
 
 // ---------------------------------------------------------------------------
 // Token sampling (sample_kernels.hip): sample_token of sampling.rs:3-81 per

@@ -1421,7 +1421,8 @@ hipError_t enqueue_decode(akh_session* s) {
   hipError_t e = enqueue_decode_body(s);
   if (e == hipSuccess)
     e = launch_argmax_final(s->amax, argmax_parts(s), (int)s->B, s->tok, s->pos, s->hist,
-                            (int)s->max_ctx + 1, 0, s->be->stream);
+                            (int)s->max_ctx + 1, 0, s->be->stream, nullptr, s->logits,
+                            (long)s->m->cfg.vocab_size);
   return e;
 }
 
@@ -2063,7 +2064,8 @@ akh_status prefill_impl(akh_session* s, const uint32_t* tokens, const uint32_t* 
       if (e == hipSuccess) e = gen_lm_tail(s);
       if (e == hipSuccess)
         e = launch_argmax_final(s->amax, 1, (int)s->B, s->tok, nullptr, s->hist,
-                                (int)s->max_ctx + 1, (int)S, st, ragged ? s->p_len : nullptr);
+                                (int)s->max_ctx + 1, (int)S, st, ragged ? s->p_len : nullptr,
+                                s->logits, (long)c.vocab_size);
       return e;
     }
     RowsNormParams r = norm_base(s, s->m->final_norm());
@@ -2075,7 +2077,8 @@ akh_status prefill_impl(akh_session* s, const uint32_t* tokens, const uint32_t* 
     if (e == hipSuccess) e = enqueue_lm_head(s);
     if (e == hipSuccess)
       e = launch_argmax_final(s->amax, lm_parts(s), (int)s->B, s->tok, nullptr, s->hist,
-                              (int)s->max_ctx + 1, (int)S, st, ragged ? s->p_len : nullptr);
+                              (int)s->max_ctx + 1, (int)S, st, ragged ? s->p_len : nullptr,
+                              s->logits, (long)c.vocab_size);
     return e;
   };
   if (h3) HIP_TRY(clear_range_flag(s->m, st));

@@ -233,7 +233,9 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
     for (int i = threadIdx.x; i < n; i += NT) amax_merge(bv, bi, pen_logit(row, i, bm, a.penalty), (uint32_t)i);
     const float mx = block_max_f(bv, sh);
     pick = block_min_u(bv == mx ? bi : 0xFFFFFFFFu, sh);
-    if (pick == 0xFFFFFFFFu) pick = 0;
+    // The reference's scan starts from index 0 and a NaN there never loses
+    // a comparison: it stays the answer.
+    if (pick == 0xFFFFFFFFu || __builtin_isnan(pen_logit(row, 0, bm, a.penalty))) pick = 0;
   } else {
     float mxv = -INFINITY;
     for (int i = threadIdx.x; i < n; i += NT) mxv = fmaxf(mxv, pen_logit(row, i, bm, a.penalty));

@@ -254,7 +254,9 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const float* logits,
   uint32_t bi = 0xFFFFFFFFu;
   for (uint32_t i = threadIdx.x; i < n; i += 256) amax_merge(bv, bi, row[i], i);
   block_amax256(bv, bi);
-  if (threadIdx.x == 0) out[blockIdx.x] = bi == 0xFFFFFFFFu ? 0u : bi;
+  // The reference's scan (sampling.rs:83-91) starts from index 0; a NaN
+  // there never loses a comparison, so it stays the answer.
+  if (threadIdx.x == 0) out[blockIdx.x] = bi == 0xFFFFFFFFu || __builtin_isnan(row[0]) ? 0u : bi;
 }
 
 // ---------------------------------------------------------------------------

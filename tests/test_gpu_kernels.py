@@ -283,6 +283,13 @@ def test_argmax_rows(backend, pkg, ora):
     o2 = backend.zeros(4, np.uint32)
     backend.argmax_rows(backend.tensor(big), 4, 50257, o2)
     assert list(o2.download(np.uint32)) == [ora.argmax(r) for r in big]
+    # NaN logits (sampling.rs:83-91 scans from index 0 with `>`): a NaN at
+    # index 0 never loses, so the answer is 0; a NaN elsewhere never wins.
+    nan = np.array([[np.nan, 4, 2, 8, 3], [1, np.nan, 9, 8, 3], [np.nan] * 5,
+                    [-np.inf, np.nan, -np.inf, 2, 2]], np.float32)
+    o3 = backend.zeros(4, np.uint32)
+    backend.argmax_rows(backend.tensor(nan), 4, 5, o3)
+    assert list(o3.download(np.uint32)) == [ora.argmax(r) for r in nan] == [0, 2, 0, 3]
 
 
 def test_shader_decode_graph_replays_with_live_metas(backend, pkg, ora):

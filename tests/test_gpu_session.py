@@ -706,6 +706,35 @@ def test_prefill_h3_out_of_fp16_range_reruns_in_fp32(backend, pkg, where):
     f.close()
 
 
+def test_greedy_tokens_with_nan_first_logit(backend, pkg, ora):
+    # lm_head column 0 set to NaN makes every row's logit 0 NaN.  The
+    # reference's argmax (sampling.rs:83-91) starts from index 0 and a NaN
+    # there never loses a comparison, so prefill, decode steps, greedy
+    # replays and temperature-0 generate all pick token 0, as the oracle does.
+    cfg = pkg.ModelConfig.new(300, 128, 2, 2, 40)
+    L = cfg.num_layers
+    w = pkg.synthetic_weights(cfg, seed=67)
+    lm = w[2 + 6 * L].copy()
+    lm[:, 0] = np.nan
+    w[2 + 6 * L] = lm
+    model, s = _session(pkg, backend, cfg, w, 40, 3)
+    toks = pkg.synthetic_tokens(3 * 10, cfg.vocab_size, seed=68).reshape(3, 10)
+    logits, nxt = s.prefill(toks)
+    assert np.isnan(logits[:, 0]).all() and np.isfinite(logits[:, 1:]).all()
+    o = ora.OracleSession(cfg, w, 40)
+    assert ora.argmax(o.prefill(toks[0])) == 0
+    o.close()
+    assert list(nxt) == [0, 0, 0]
+    _, nxt = s.decode_step(None)
+    assert list(nxt) == [0, 0, 0]
+    assert (s.decode_greedy(2) == 0).all()
+    s.reset()
+    outs = s.generate(toks, 3)
+    assert all(list(x) == [0, 0, 0] for x in outs)
+    s.close()
+    model.close()
+
+
 def test_forward_bf16_layers_lm_head_out_of_fp16_range_reruns(backend, pkg):
     # Under the bf16-MFMA layers the trainer forward's lm_head still runs the
     # split-fp16 GEMM on the model's fp16 copy.  One lm_head weight of 1e5

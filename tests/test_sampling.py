@@ -104,6 +104,12 @@ def test_device_reference_tests(backend, pkg):
     got = _device_sample(pkg, backend, ll, 100.0, 0, 1.0, 1.0, [[]] * 500, rng.random(500))
     assert set(got) == {0, 1, 2, 3, 4}
     assert list(_device_sample(pkg, backend, l[:1], 0.0, 0, 1.0, 100.0, [[3]], u[:1])) == [1]
+    # Greedy over NaN logits follows the reference's scan from index 0: a NaN
+    # at index 0 stays the answer, a NaN elsewhere never wins.
+    nanl = np.tile(LOGITS, (2, 1))
+    nanl[0, 0] = np.nan
+    nanl[1, 2] = np.nan
+    assert list(_device_sample(pkg, backend, nanl, 0.0, 0, 1.0, 1.0, [[]] * 2, u[:2])) == [0, 3]
 
 
 @pytest.mark.gpu
