@@ -112,6 +112,9 @@ struct GemmParams {
   // GEMM_QKV: K and V rows go to kcache / vcache at row m (rows packed like
   // the prompt's) instead of sequence * seq_stride + position.
   int kv_packed;
+  // launch_gemm_bf16 with an fp32 A: round A to bfloat16 (one product)
+  // instead of splitting it into hi + lo (two).
+  int a_hi_only;
 };
 
 enum { FLASH_X6 = 1, FLASH_H3 = 2 };  // FlashParams::x6

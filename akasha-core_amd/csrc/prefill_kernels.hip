@@ -637,13 +637,16 @@ __global__ __launch_bounds__(256) void k_transpose_bf16(const float* __restrict_
 // column 2j + t: each lane ends up with adjacent column pairs, as the
 // paired epilogues (RoPE) need.
 //
-// A32: A is fp32 (p.a) and enters as two bfloat16 parts, hi = bf16(a) and
-// lo = bf16(a - hi), each multiplied by B (two MFMAs): with bfloat16-exact
-// weights the products then carry a's first 16 significant bits.
-template <int EPI, bool A32>
+// AM (A's form): 0, A is bfloat16 (p.a16); 1, A is fp32 (p.a) and enters as
+// two bfloat16 parts, hi = bf16(a) and lo = bf16(a - hi), each multiplied by
+// B (two MFMAs): with bfloat16-exact weights the products then carry a's
+// first 16 significant bits; 2, A is fp32 rounded to bfloat16 as it is
+// staged (one MFMA).
+template <int EPI, int AM>
 __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
   constexpr int BM = 256, BN = 256, BK = 32, LD = BK + 8;
-  constexpr int NA = A32 ? 2 : 1;
+  constexpr bool A32 = AM != 0;
+  constexpr int NA = AM == 1 ? 2 : 1;
   __shared__ __align__(16) uint16_t As[NA][2][BM][LD];
   __shared__ __align__(16) uint16_t Bs[2][BN][LD];
 
@@ -713,11 +716,13 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(GemmParams p) {
         const int f = tid + 512 * i, r = f >> 3, k = 4 * (f & 7);
         const float4 x = fa[set][i];
         const uint2 hi = make_uint2(cvt_pk_bf16(x.x, x.y), cvt_pk_bf16(x.z, x.w));
-        const uint2 lo = make_uint2(
-            cvt_pk_bf16(x.x - __uint_as_float(hi.x << 16), x.y - __uint_as_float(hi.x & 0xFFFF0000u)),
-            cvt_pk_bf16(x.z - __uint_as_float(hi.y << 16), x.w - __uint_as_float(hi.y & 0xFFFF0000u)));
         *reinterpret_cast<uint2*>(&As[0][buf][r][k]) = hi;
-        *reinterpret_cast<uint2*>(&As[NA - 1][buf][r][k]) = lo;
+        if constexpr (NA == 2) {
+          const uint2 lo = make_uint2(
+              cvt_pk_bf16(x.x - __uint_as_float(hi.x << 16), x.y - __uint_as_float(hi.x & 0xFFFF0000u)),
+              cvt_pk_bf16(x.z - __uint_as_float(hi.y << 16), x.w - __uint_as_float(hi.y & 0xFFFF0000u)));
+          *reinterpret_cast<uint2*>(&As[NA - 1][buf][r][k]) = lo;
+        }
       }
     }
   };
@@ -2228,10 +2233,12 @@ hipError_t launch_gemm_bf16(const GemmParams& p, int epi, hipStream_t s) {
   if (!p.a == !p.a16) return hipErrorInvalidValue;
   dim3 g((p.N + 255) / 256, (p.M + 255) / 256), b(512);
 #define AKH_GO(E)                                                 \
-  if (p.a)                                                        \
-    hipLaunchKernelGGL((k_gemm_bf16<E, true>), g, b, 0, s, p);    \
+  if (p.a && p.a_hi_only)                                         \
+    hipLaunchKernelGGL((k_gemm_bf16<E, 2>), g, b, 0, s, p);       \
+  else if (p.a)                                                   \
+    hipLaunchKernelGGL((k_gemm_bf16<E, 1>), g, b, 0, s, p);       \
   else                                                            \
-    hipLaunchKernelGGL((k_gemm_bf16<E, false>), g, b, 0, s, p);
+    hipLaunchKernelGGL((k_gemm_bf16<E, 0>), g, b, 0, s, p);
   switch (epi) {
     case GEMM_ADD: AKH_GO(GEMM_ADD) break;
     case GEMM_SILU: AKH_GO(GEMM_SILU) break;

@@ -285,7 +285,9 @@ def scaled_measurement(pkg, hip, be, w, steps=8, with_prefill=True, with_decode=
                     "prefill_bf16_tok_s": round(Bp * Sp / (bms / 1e3), 1),
                     "prefill_bf16_tflops": round(fl / (bms / 1e3) / 1e12, 2),
                     "prefill_bf16_roofline": {
-                        "bound": "mfma", "instr": "v_mfma_f32_32x32x16_bf16, 1 product",
+                        "bound": "mfma",
+                        "instr": "v_mfma_f32_32x32x16_bf16; useful flops counted once (ffn_up and "
+                                 "ffn_down run two products, hi + lo of their fp32 input)",
                         "achieved": round(fl / (bms / 1e3) / 1e12, 2),
                         "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(fl / (bms / 1e3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4)}})
