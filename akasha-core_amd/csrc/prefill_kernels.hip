@@ -1427,8 +1427,11 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
 // contractions accumulate the six products down to 2^-16 of each full
 // product (as k_gemm_x6), so scores and outputs carry fp32-level error.
 // Softmax statistics, the output and lse are fp32, as in k_flash_mfma,
-// whose per-shader meta handling (row_offset) this follows.
-template <int HD>
+// whose per-shader meta handling (row_offset) this follows.  UA: the head
+// size is not a multiple of 4, so head rows lack 16-byte alignment and are
+// loaded element by element (a separate instantiation: the aligned kernels
+// keep their code).
+template <int HD, bool UA = false>
 __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   constexpr int QB = 128, KB = 32, NT = HD / 32, NQ = HD / 16;
   constexpr int KP = HD + 8;   // K row stride (bf16)
@@ -1462,11 +1465,10 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   const float* kp = p.k + fs.kv + hh * hd;
   const float* vp = p.v + fs.kv + hh * hd;
   // Columns past the head size read as zero.  A head size that is not a
-  // multiple of 4 leaves head rows without 16-byte alignment (and a last
-  // quad that reaches into the next head): such heads load element by
-  // element (hd is uniform, so the branch is too).
+  // multiple of 4 (UA) leaves head rows without 16-byte alignment, and its
+  // last quad reaches into the next head: element by element.
   auto col4 = [hd](const float* src, int c) {
-    if ((hd & 3) == 0)
+    if constexpr (!UA)
       return c < hd ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
     return make_float4(c < hd ? src[0] : 0.f, c + 1 < hd ? src[1] : 0.f,
                        c + 2 < hd ? src[2] : 0.f, c + 3 < hd ? src[3] : 0.f);
@@ -2173,10 +2175,17 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
     // next larger size, columns past hd zero (fp32-accurate, whatever p.x6
     // asks); heads that are not a multiple of 4 load element by element.
     const dim3 g(H, batch, (max_rows + 127) / 128);
-    if (p.hd < 64)
-      hipLaunchKernelGGL(k_flash_x6<64>, g, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL(k_flash_x6<128>, g, dim3(256), 0, s, p);
+    const bool ua = p.hd % 4 != 0;
+    if (p.hd < 64) {
+      if (ua)
+        hipLaunchKernelGGL((k_flash_x6<64, true>), g, dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL((k_flash_x6<64, false>), g, dim3(256), 0, s, p);
+    } else if (ua) {
+      hipLaunchKernelGGL((k_flash_x6<128, true>), g, dim3(256), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((k_flash_x6<128, false>), g, dim3(256), 0, s, p);
+    }
     return hipGetLastError();
   }
   if (p.hd == 64 || p.hd == 128) {
