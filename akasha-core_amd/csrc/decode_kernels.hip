@@ -182,7 +182,16 @@ __device__ __forceinline__ float attn_score_scale(float scale) {
   return AKH_ATTN_EXP2 ? scale * 1.44269504088896341f : scale;
 }
 
-template <int W, int HL, int EPI, int PRO, bool BF, int MT, int NT = 1>
+//
+// VB > 0: at most VB live rows (small batches), on the VALU instead of the
+// MFMAs.  A 32-row MFMA tile spends the same matrix-pipe time on one live
+// row as on 32, and that time sits on the decode step's critical path
+// (ffn_up's 96 blocks: ~2.6 us of fp32 MFMAs per CU); the VALU computes only
+// the live rows.  Lane (j, h) takes the dot products of rows 0..VB-1 with
+// its column over its k-quads, the two halves are added, and the sums enter
+// the MFMA accumulator layout (row h*4 + r in entry r) so the epilogues are
+// unchanged.
+template <int W, int HL, int EPI, int PRO, bool BF, int MT, int NT = 1, int VB = 0>
 __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   constexpr int KC = 2 * W * HL;
   constexpr int HQ = HL / 4;
@@ -220,7 +229,89 @@ __global__ __launch_bounds__(64 * W) void k_dec_gemm(DecGemmParams p) {
   f32x16 acc[MT * NT];  // [row tile][column tile]
 #pragma unroll
   for (int i = 0; i < MT * NT; ++i) acc[i] = zero16();
-  if constexpr (PRO == PRO_NONE && MT == 1 && NT == 1 && AKH_DEC_PIPE) {
+  if constexpr (VB > 0) {
+    static_assert(VB <= 8 && MT == 1 && NT == 1 && !BF && PRO != PRO_NORM,
+                  "the VALU rows serve one tile of float weights");
+    constexpr bool kNT = AKH_GEMM_NT && EPI != DEC_LOGITS;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    // A's four k of row `row` at k-quad kq (in range).
+    auto a_quad = [&](int kq, int row) -> float4 {
+      const size_t off = ((size_t)kq * 32 + row) * 4;
+      float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (PRO == PRO_SILU_SUM) {
+        t = sum_parts4<4>(t, p.xt + off, (size_t)R * K, p.nparts);
+        t = make_float4(silu_fast(t.x), silu_fast(t.y), silu_fast(t.z), silu_fast(t.w));
+      } else if constexpr (PRO == PRO_ATTN_MERGE) {
+        // The attention splits' softmax states of (row, head (4 kq) / hd),
+        // merged as in the MFMA path.
+        const int H = K / p.hd, hq = (4 * kq) / p.hd;
+        float mx = -INFINITY;
+        float2 ml[kMaxAttnSplits];
+#pragma unroll
+        for (int sp = 0; sp < kMaxAttnSplits; ++sp) {
+          ml[sp] = sp < p.nparts ? p.ml[((size_t)sp * H + hq) * R + row]
+                                 : make_float2(-INFINITY, 0.f);
+          mx = fmaxf(mx, ml[sp].x);
+        }
+        float L = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < kMaxAttnSplits; ++sp) {
+          if (sp >= p.nparts) continue;
+          const float4 o = *reinterpret_cast<const float4*>(p.xt + (size_t)sp * R * K + off);
+          const float w = ml[sp].x == -INFINITY ? 0.f : attn_exp(ml[sp].x - mx);
+          L += w * ml[sp].y;
+          t.x += w * o.x;
+          t.y += w * o.y;
+          t.z += w * o.z;
+          t.w += w * o.w;
+        }
+        const float inv = L > 0.f ? 1.0f / L : 0.f;
+        t = make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
+      } else {
+        t = *reinterpret_cast<const float4*>(p.xt + off);
+      }
+      return t;
+    };
+    float sum[VB];
+#pragma unroll
+    for (int b = 0; b < VB; ++b) sum[b] = 0.f;
+    for (int k0 = kb; k0 < ke; k0 += KC) {
+      const int kq0 = (k0 + wave * 2 * HL + h * HL) >> 2;
+      float4 wq[HQ], aq[VB][HQ];
+#pragma unroll
+      for (int q = 0; q < HQ; ++q) {
+        const int kq = kq0 + q;
+        const f4* src = reinterpret_cast<const f4*>(wt + (size_t)kq * 128);
+        const f4 t = 4 * kq < ke ? (kNT ? __builtin_nontemporal_load(src) : *src)
+                                 : f4{0.f, 0.f, 0.f, 0.f};
+        wq[q] = make_float4(t.x, t.y, t.z, t.w);
+      }
+#pragma unroll
+      for (int q = 0; q < HQ; ++q)
+#pragma unroll
+        for (int b = 0; b < VB; ++b)
+          aq[b][q] = 4 * (kq0 + q) < ke ? a_quad(kq0 + q, b) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int q = 0; q < HQ; ++q)
+#pragma unroll
+        for (int b = 0; b < VB; ++b) {
+          sum[b] = fmaf(aq[b][q].x, wq[q].x, sum[b]);
+          sum[b] = fmaf(aq[b][q].y, wq[q].y, sum[b]);
+          sum[b] = fmaf(aq[b][q].z, wq[q].z, sum[b]);
+          sum[b] = fmaf(aq[b][q].w, wq[q].w, sum[b]);
+        }
+    }
+    // The two halves of the wave took different k: add them, then lane
+    // (j, h) holds rows h*4 .. h*4 + 3 in accumulator entries 0..3.
+#pragma unroll
+    for (int b = 0; b < VB; ++b) sum[b] += __shfl_xor(sum[b], 32, 64);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v0 = r < VB ? sum[r < VB ? r : 0] : 0.f;
+      const float v1 = 4 + r < VB ? sum[4 + r < VB ? 4 + r : 0] : 0.f;
+      acc[0][r] = h == 0 ? v0 : v1;
+    }
+  } else if constexpr (PRO == PRO_NONE && MT == 1 && NT == 1 && AKH_DEC_PIPE) {
     // Plain A, one row tile: the loads of pass i + 1 are issued before the
     // MFMAs of pass i, so a block waits on one memory round trip, not one per
     // pass.  Loads past K read the block's last valid quad (clamped, always
@@ -1395,6 +1486,9 @@ bool role_bf16(int K, int N) {
 #ifndef AKH_DEC_NT2
 #define AKH_DEC_NT2 2
 #endif
+#ifndef AKH_DEC_VALU
+#define AKH_DEC_VALU 1
+#endif
 template <int ROLE, bool LARGE, int EPI, int PRO>
 hipError_t dec_go_shape(DecGemmParams p, hipStream_t s) {
   using S = RoleShape<ROLE, LARGE>;
@@ -1414,6 +1508,21 @@ hipError_t dec_go_shape(DecGemmParams p, hipStream_t s) {
     hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, false, MT>), g, dim3(64 * S::W), 0, \
                        s, p);
   if (p.mt == 1) {
+    // A single sequence of float tiles on the VALU.  Measured on MI355X at
+    // hall-1.0: one live row, qkv 4.08 -> 3.71 us, ffn_up 6.75 -> 5.11 us,
+    // ffn_down 4.86 -> 4.00 us, config 1 0.406 -> 0.376 ms per token; four
+    // live rows lost (out_proj 4.1 -> 7.0 us, ffn_up 6.8 -> 9.4 us: every
+    // lane loads, and for out_proj merges, each row's A), so those keep the
+    // MFMAs.
+    constexpr bool kValu = AKH_DEC_VALU && EPI != DEC_RESID && EPI != DEC_LOGITS &&
+                           PRO != PRO_NORM;
+    if constexpr (kValu) {
+      if (!p.wbf16 && p.M == 1) {
+        hipLaunchKernelGGL((k_dec_gemm<S::W, S::HL, EPI, PRO, false, 1, 1, 1>), g,
+                           dim3(64 * S::W), 0, s, p);
+        return hipGetLastError();
+      }
+    }
     AKH_DEC_GO(1)
   } else if (p.mt == 2) {
     // Two row tiles of bfloat16 weights: each block of the K-split roles
