@@ -117,7 +117,7 @@ struct GemmParams {
   int a_hi_only;
 };
 
-enum { FLASH_X6 = 1, FLASH_H3 = 2 };  // FlashParams::x6
+enum { FLASH_X6 = 1, FLASH_H3 = 2, FLASH_FP32 = 3 };  // FlashParams::x6
 
 struct FlashParams {
   const float* q;
@@ -135,7 +135,11 @@ struct FlashParams {
   int x6;         // launch_flash, head_dim 64 / 128: split-bfloat16 MFMAs
                   // (fp32 accuracy) instead of fp32 MFMAs; FLASH_H3: split
                   // fp16 MFMAs (fp32 accuracy), setting *range_flag when an
-                  // operand is beyond fp16's range
+                  // operand is beyond fp16's range (grids of fewer blocks
+                  // than CUs recompute such tiles themselves); FLASH_FP32:
+                  // fp32 accuracy without a flag (split-fp16 tiles that
+                  // recompute themselves on split-bfloat16; split-bfloat16
+                  // throughout for head size 128 on large grids)
   int* range_flag;
   // Ragged prompts packed back to back: sequence b's rows of q, o (and lse)
   // are [rows_at[b], rows_at[b + 1]) and its length is their count (S is

@@ -1431,8 +1431,17 @@ __global__ __launch_bounds__(256, 2) void k_flash_bf16(FlashParams p) {
 // size is not a multiple of 4, so head rows lack 16-byte alignment and are
 // loaded element by element (a separate instantiation: the aligned kernels
 // keep their code).
-template <int HD, bool UA = false>
-__global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
+// LDS of a 128-query tile: K's KPLANES planes and V^T's three, or the four
+// waves' 32 x 33 output transposes.
+template <int HD, int KPLANES>
+constexpr int flash_q128_lds() {
+  constexpr int KB = 32, KV_BYTES = (KPLANES * KB * (HD + 8) + 3 * HD * (KB + 8)) * 2;
+  constexpr int O_BYTES = 4 * 32 * 33 * 4;
+  return KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES;
+}
+
+template <int HD, bool UA>
+__device__ __forceinline__ void flash_x6_tile(const FlashParams& p, unsigned char* lds) {
   constexpr int QB = 128, KB = 32, NT = HD / 32, NQ = HD / 16;
   constexpr int KP = HD + 8;   // K row stride (bf16)
   constexpr int VP = KB + 8;   // V^T row stride (bf16)
@@ -1440,9 +1449,6 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
   constexpr int KPT = KB * CPR / 256;  // consecutive keys staged per thread
   static_assert(KPT == 2 || KPT == 4, "staging covers 2 or 4 keys per thread");
   constexpr int K_PLANE = KB * KP, V_PLANE = HD * VP;  // bf16 elements
-  constexpr int KV_BYTES = 3 * (K_PLANE + V_PLANE) * 2;
-  constexpr int O_BYTES = 4 * 32 * 33 * 4;
-  __shared__ __align__(16) unsigned char lds[KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES];
   auto Ks = [&](int pl) { return reinterpret_cast<uint16_t (*)[KP]>(lds) + pl * KB; };
   auto Vt = [&](int pl) {
     return reinterpret_cast<uint16_t (*)[VP]>(lds + 3 * K_PLANE * 2) + pl * HD;
@@ -1652,6 +1658,12 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
         mrow * 0.69314718055994531f + logf(lrow);
 }
 
+template <int HD, bool UA = false>
+__global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
+  __shared__ __align__(16) unsigned char lds[flash_q128_lds<HD, 3>()];
+  flash_x6_tile<HD, UA>(p, lds);
+}
+
 // Causal flash attention in fp32 accuracy on fp16 MFMAs, the structure of
 // k_flash_x6 with two-term fp16 splits (split2_f16: x = hi + 2^-11 lo) and
 // three products per contraction instead of six.  Scores: Q and K split,
@@ -1662,8 +1674,11 @@ __global__ __launch_bounds__(256, 2) void k_flash_x6(FlashParams p) {
 // subnormal, but each loses at most 2^-25 absolute, weighted by the
 // probabilities (sum 1).  Output, lse and softmax statistics stay fp32.  A
 // non-finite output (an operand beyond fp16's range) sets *p.range_flag.
-template <int HD>
-__global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
+// FALLBACK: a tile with a non-finite output stores nothing and returns false
+// (the caller recomputes it); otherwise it sets *p.range_flag, if given, and
+// stores.
+template <int HD, bool FALLBACK>
+__device__ __forceinline__ bool flash_h3_tile(const FlashParams& p, unsigned char* lds) {
   constexpr int QB = 128, KB = 32, NT = HD / 32, NQ = HD / 16;
   constexpr int KP = HD + 8;   // K row stride (fp16)
   constexpr int VP = KB + 8;   // V^T row stride (fp16)
@@ -1671,9 +1686,6 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
   constexpr int KPT = KB * CPR / 256;  // consecutive keys staged per thread
   static_assert(KPT == 2 || KPT == 4, "staging covers 2 or 4 keys per thread");
   constexpr int K_PLANE = KB * KP, V_PLANE = HD * VP;  // fp16 elements
-  constexpr int KV_BYTES = (2 * K_PLANE + 3 * V_PLANE) * 2;
-  constexpr int O_BYTES = 4 * 32 * 33 * 4;
-  __shared__ __align__(16) unsigned char lds[KV_BYTES > O_BYTES ? KV_BYTES : O_BYTES];
   auto Ks = [&](int pl) { return reinterpret_cast<uint16_t (*)[KP]>(lds) + pl * KB; };
   auto Vt = [&](int pl) {
     return reinterpret_cast<uint16_t (*)[VP]>(lds + 2 * K_PLANE * 2) + pl * HD;
@@ -1681,14 +1693,14 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
 
   const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   FlashSeq fs;
-  if (!flash_seq<HD>(p, hh, b, fs)) return;
+  if (!flash_seq<HD>(p, hh, b, fs)) return true;
   const int S = fs.S, d = fs.d, hd = p.hd;  // head size hd <= HD
   const float scale = fs.scale;
   const int H = d / hd;
   // Scores in the log2 domain: exp(scale x - m) = exp2(scale log2(e) x - m').
   const float qscale = scale * 1.44269504088896341f;
   const int q0 = qblk * QB;
-  if (q0 >= S) return;
+  if (q0 >= S) return true;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
 
@@ -1867,14 +1879,19 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
   // O^T (rows = dims) -> LDS, one 32-dim tile at a time -> coalesced rows.
   const float inv = 1.0f / lrow;
   // An operand beyond fp16's range (|x| >= 65520) makes the output or the
-  // softmax state non-finite: flag it for the caller's fp32 rerun.
+  // softmax state non-finite: give the tile back to the caller (FALLBACK),
+  // or flag it for the caller's fp32 rerun.
   {
     bool finite = __builtin_isfinite(inv);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) finite = finite && __builtin_isfinite(o[t][r]);
-    if (!finite && p.range_flag) *p.range_flag = 1;
+    if constexpr (FALLBACK) {
+      if (__syncthreads_or(!finite)) return false;
+    } else if (!finite && p.range_flag) {
+      *p.range_flag = 1;
+    }
   }
   float (*Os)[33] = reinterpret_cast<float (*)[33]>(lds + wave * 32 * 33 * 4);
   float* op = p.o + fs.o + hh * hd;
@@ -1893,6 +1910,28 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
   if (p.lse && h == 0 && qi < S)  // max + ln(sum), back in natural units
     p.lse[fs.l + (size_t)qi * H + hh] =
         mrow * 0.69314718055994531f + logf(lrow);
+  return true;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
+  __shared__ __align__(16) unsigned char lds[flash_q128_lds<HD, 2>()];
+  flash_h3_tile<HD, false>(p, lds);
+}
+
+// The 128-query tile on split-fp16 products, recomputed on split-bf16
+// products when an operand is beyond fp16's range (a non-finite output):
+// fp32 accuracy for any finite input, with no flag for the caller to read.
+// Head size 64 only: at 128 the two paths in one kernel spill registers.
+template <int HD>
+__global__ __launch_bounds__(256, 2) void k_flash_h3x(FlashParams p) {
+  static_assert(HD == 64, "k_flash_x6 serves head size 128");
+  constexpr int L2 = flash_q128_lds<HD, 2>(), L3 = flash_q128_lds<HD, 3>();
+  __shared__ __align__(16) unsigned char lds[L2 > L3 ? L2 : L3];
+  if (!flash_h3_tile<HD, true>(p, lds)) {
+    __syncthreads();
+    flash_x6_tile<HD, false>(p, lds);
+  }
 }
 
 // k_flash_x6 for grids too small to fill the part (a single sequence's
@@ -1908,8 +1947,19 @@ __global__ __launch_bounds__(256, 2) void k_flash_h3(FlashParams p) {
 // scores and its V rows while it takes this one's output.  The heaviest
 // tile walks 1 / NW of the key blocks on its critical path.  Scores,
 // products and statistics are those of k_flash_x6.
+//
+// LDS of a key-split tile: NW per-wave regions holding K's KPLANES planes or
+// V^T's three (whichever is larger), or the merge's NW partial states.
+template <int HD, int NW, int KPLANES>
+constexpr int flash_w_lds() {
+  constexpr int KB = 32, K_BYTES = KPLANES * KB * (HD + 8) * 2, V_BYTES = 3 * HD * (KB + 8) * 2;
+  constexpr int W_BYTES = K_BYTES > V_BYTES ? K_BYTES : V_BYTES;
+  constexpr int M_BYTES = NW * (HD * 33 + 64) * 4;
+  return NW * W_BYTES > M_BYTES ? NW * W_BYTES : M_BYTES;
+}
+
 template <int HD, int NW>
-__global__ __launch_bounds__(64 * NW) void k_flash_x6w(FlashParams p) {
+__device__ __forceinline__ void flash_x6w_tile(const FlashParams& p, unsigned char* lds) {
   constexpr int KB = 32, NT = HD / 32, NQ = HD / 16;
   constexpr int KP = HD + 8, VP = KB + 8, CPR = HD / 4;
   constexpr int KPT = KB * CPR / 64;  // consecutive keys staged per lane
@@ -1918,8 +1968,6 @@ __global__ __launch_bounds__(64 * NW) void k_flash_x6w(FlashParams p) {
   constexpr int K_BYTES = 3 * K_PLANE * 2, V_BYTES = 3 * V_PLANE * 2;
   constexpr int W_BYTES = K_BYTES > V_BYTES ? K_BYTES : V_BYTES;
   constexpr int OS = 33;                                // merge row stride
-  constexpr int M_BYTES = NW * (HD * OS + 64) * 4;
-  __shared__ __align__(16) unsigned char lds[NW * W_BYTES > M_BYTES ? NW * W_BYTES : M_BYTES];
 
   const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
   FlashSeq fs;
@@ -1941,20 +1989,6 @@ __global__ __launch_bounds__(64 * NW) void k_flash_x6w(FlashParams p) {
   const float* vp = p.v + fs.kv + hh * HD;
 
   const int qi = q0 + j;
-  uint4 qf[3][NQ];
-  {
-    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 8 * h;
-#pragma unroll
-    for (int s = 0; s < NQ; ++s)
-      split3_rne(*reinterpret_cast<const float4*>(qr + 16 * s),
-                 *reinterpret_cast<const float4*>(qr + 16 * s + 4), qf[0][s], qf[1][s],
-                 qf[2][s]);
-  }
-  f32x16 o[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) o[t] = zero16();
-  float mrow = -INFINITY, lrow = 0.f;
-
   const int kend = min(S, q0 + 32);
   const int nkb = (kend + KB - 1) / KB;
 
@@ -1975,10 +2009,29 @@ __global__ __launch_bounds__(64 * NW) void k_flash_x6w(FlashParams p) {
     t[1] = cvt_pk_bf16(ra, rc);
     t[2] = cvt_pk_bf16(ra - __uint_as_float(t[1] << 16), rc - __uint_as_float(t[1] & 0xFFFF0000u));
   };
+  // The query rows, then the first key block's K and V rows, all in flight
+  // before the wave waits on any of them.
+  float4 qr4[2 * NQ];
+  {
+    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 8 * h;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      qr4[2 * s] = *reinterpret_cast<const float4*>(qr + 16 * s);
+      qr4[2 * s + 1] = *reinterpret_cast<const float4*>(qr + 16 * s + 4);
+    }
+  }
   if (wave < nkb) {
     load_rows(kp, wave, kr);
     load_rows(vp, wave, vr);
   }
+  uint4 qf[3][NQ];
+#pragma unroll
+  for (int s = 0; s < NQ; ++s)
+    split3_rne(qr4[2 * s], qr4[2 * s + 1], qf[0][s], qf[1][s], qf[2][s]);
+  f32x16 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = zero16();
+  float mrow = -INFINITY, lrow = 0.f;
   for (int kb = wave; kb < nkb; kb += NW) {
     const bool more = kb + NW < nkb;
     // The wave's own region: its reads of the previous key block's V^T were
@@ -2137,6 +2190,289 @@ __global__ __launch_bounds__(64 * NW) void k_flash_x6w(FlashParams p) {
   }
 }
 
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void k_flash_x6w(FlashParams p) {
+  __shared__ __align__(16) unsigned char lds[flash_w_lds<HD, NW, 3>()];
+  flash_x6w_tile<HD, NW>(p, lds);
+}
+
+// The key-split tile on split-fp16 products (k_flash_h3's arithmetic: Q and
+// K as two fp16 terms, three products per score contraction; P as two terms
+// and V^T as hi, remainder and hi 2^-11, three products per output), with
+// k_flash_x6w's layout: K's two planes or V^T's three in a wave's region,
+// partial states merged through LDS.  Fewer planes and half the MFMAs of the
+// split-bf16 tile.  An operand beyond fp16's range makes some output of the
+// tile NaN (its infinite hi meets the opposite infinity of its remainder in
+// every sum it enters), so the merge computes the tile's outputs, and stores
+// them only if all are finite; otherwise it returns false having stored
+// nothing, and the caller recomputes the tile on split-bf16 products.
+template <int HD, int NW>
+__device__ __forceinline__ bool flash_h3w_tile(const FlashParams& p, unsigned char* lds) {
+  constexpr int KB = 32, NT = HD / 32, NQ = HD / 16;
+  constexpr int KP = HD + 8, VP = KB + 8, CPR = HD / 4;
+  constexpr int KPT = KB * CPR / 64;  // consecutive keys staged per lane
+  static_assert(KPT == 8 || KPT == 16, "a wave stages 32 keys in runs of 8 or 16");
+  constexpr int K_PLANE = KB * KP, V_PLANE = HD * VP;  // fp16 elements
+  constexpr int K_BYTES = 2 * K_PLANE * 2, V_BYTES = 3 * V_PLANE * 2;
+  constexpr int W_BYTES = K_BYTES > V_BYTES ? K_BYTES : V_BYTES;
+  constexpr int OS = 33;                          // merge row stride
+  constexpr int PER = 32 * HD / (64 * NW);        // merged outputs per lane
+  static_assert(PER * 64 * NW == 32 * HD, "the merge deals whole rounds");
+
+  const int qblk = gridDim.z - 1 - blockIdx.z, hh = blockIdx.x, b = blockIdx.y;
+  FlashSeq fs;
+  if (!flash_seq<HD>(p, hh, b, fs)) return true;
+  const int S = fs.S, d = fs.d;
+  const float scale = fs.scale;
+  const int H = d / HD;
+  const float qscale = scale * 1.44269504088896341f;
+  const int q0 = qblk * 32;
+  if (q0 >= S) return true;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+  unsigned char* wl = lds + wave * W_BYTES;
+  auto Ks = [&](int pl) { return reinterpret_cast<uint16_t (*)[KP]>(wl) + pl * KB; };
+  auto Vt = [&](int pl) { return reinterpret_cast<uint16_t (*)[VP]>(wl) + pl * HD; };
+
+  const float* qp = p.q + fs.q + hh * HD;
+  const float* kp = p.k + fs.kv + hh * HD;
+  const float* vp = p.v + fs.kv + hh * HD;
+
+  const int qi = q0 + j;
+  const int kend = min(S, q0 + 32);
+  const int nkb = (kend + KB - 1) / KB;
+
+  // Staging: lane l takes dims 4 (l % CPR) .. + 3 of keys KPT (l / CPR) ..
+  // + KPT - 1.
+  const int sc = (lane % CPR) * 4, sk = (lane / CPR) * KPT;
+  float4 kr[KPT], vr[KPT];
+  auto load_rows = [&](const float* src, int kb, float4 (&r)[KPT]) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int key = kb * KB + sk + i;
+      r[i] = *reinterpret_cast<const float4*>(src + (size_t)(key < S ? key : 0) * d + sc);
+    }
+  };
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  // K: hi and scaled lo (x = hi + 2^-11 lo), packed as pairs.
+  auto split_k = [](float a, float c, uint32_t (&t)[2]) {
+    t[0] = cvt_pk_f16(a, c);
+    const h2 hv = __builtin_bit_cast(h2, t[0]);
+    t[1] = cvt_pk_f16((a - (float)hv[0]) * 2048.f, (c - (float)hv[1]) * 2048.f);
+  };
+  // V: hi, the unscaled remainder, and hi 2^-11, so that with P split as
+  // p0 + 2^-11 p1 one accumulator takes p0 v0 + p0 v1 + p1 (2^-11 v0).
+  auto split_v = [](float a, float c, uint32_t (&t)[3]) {
+    t[0] = cvt_pk_f16(a, c);
+    const h2 hv = __builtin_bit_cast(h2, t[0]);
+    const float ha = (float)hv[0], hc = (float)hv[1];
+    t[1] = cvt_pk_f16(a - ha, c - hc);
+    t[2] = cvt_pk_f16(ha * 0x1p-11f, hc * 0x1p-11f);
+  };
+  // The query rows, then the first key block's K and V rows, all in flight
+  // before the wave waits on any of them.
+  float4 qr4[2 * NQ];
+  {
+    const float* qr = qp + (size_t)(qi < S ? qi : 0) * d + 8 * h;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      qr4[2 * s] = *reinterpret_cast<const float4*>(qr + 16 * s);
+      qr4[2 * s + 1] = *reinterpret_cast<const float4*>(qr + 16 * s + 4);
+    }
+  }
+  if (wave < nkb) {
+    load_rows(kp, wave, kr);
+    load_rows(vp, wave, vr);
+  }
+  uint4 qf[2][NQ];
+#pragma unroll
+  for (int s = 0; s < NQ; ++s) split2_f16(qr4[2 * s], qr4[2 * s + 1], qf[0][s], qf[1][s]);
+  f32x16 o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = zero16();
+  float mrow = -INFINITY, lrow = 0.f;
+  for (int kb = wave; kb < nkb; kb += NW) {
+    const bool more = kb + NW < nkb;
+    // The wave's own region: its reads of the previous key block's V^T were
+    // issued before these writes, and one wave's LDS operations complete in
+    // order; the wave barrier keeps the compiler from moving them across.
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      uint32_t lo[2], hi[2];
+      split_k(kr[i].x, kr[i].y, lo);
+      split_k(kr[i].z, kr[i].w, hi);
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl)
+        *reinterpret_cast<uint2*>(&Ks(pl)[sk + i][sc]) = make_uint2(lo[pl], hi[pl]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the writes have landed
+    __builtin_amdgcn_wave_barrier();
+    if (more) load_rows(kp, kb + NW, kr);
+    const int j0 = kb * KB;
+
+    // Scores: hi.hi in st, the cross terms in scr, st + 2^-11 scr.
+    f32x16 st = zero16(), scr = zero16();
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      f16x8 kf[2];
+#pragma unroll
+      for (int pl = 0; pl < 2; ++pl)
+        kf[pl] = f16x8_of(*reinterpret_cast<const uint4*>(&Ks(pl)[j][16 * s + 8 * h]));
+      scr = mfma_f16(kf[1], f16x8_of(qf[0][s]), scr);
+      scr = mfma_f16(kf[0], f16x8_of(qf[1][s]), scr);
+      st = mfma_f16(kf[0], f16x8_of(qf[0][s]), st);
+    }
+    // The score MFMAs consumed every K fragment read, so those reads have
+    // completed: V^T may overwrite the region.
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int run = 0; run < KPT / 8; ++run) {
+        uint32_t t[4][3];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 a = vr[8 * run + 2 * g], e = vr[8 * run + 2 * g + 1];
+          const float x0 = c == 0 ? a.x : c == 1 ? a.y : c == 2 ? a.z : a.w;
+          const float x1 = c == 0 ? e.x : c == 1 ? e.y : c == 2 ? e.z : e.w;
+          split_v(x0, x1, t[g]);
+        }
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+          *reinterpret_cast<uint4*>(&Vt(pl)[sc + c][sk + 8 * run]) =
+              make_uint4(t[0][pl], t[1][pl], t[2][pl], t[3][pl]);
+      }
+    }
+    if (more) load_rows(vp, kb + NW, vr);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[r] += scr[r] * 0x1p-11f;
+    const bool masked = j0 + KB - 1 > q0 || j0 + KB > S;
+    float pm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = st[r] * qscale;
+      if (masked) {
+        const int key = j0 + acc_row(r, h);
+        if (key > qi || key >= S) v = -INFINITY;
+      }
+      st[r] = v;
+      pm = fmaxf(pm, v);
+    }
+    pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+    // Every block this wave takes has a key at or below each query of the
+    // tile except on the diagonal, where key j0 <= q0 <= qi: pm is finite
+    // unless a score is +inf.
+    const float mnew = fmaxf(mrow, pm);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = __builtin_amdgcn_exp2f(st[r] - mnew);
+      st[r] = e;
+      ps += e;
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    const float corr = __builtin_amdgcn_exp2f(mrow - mnew);
+    lrow = lrow * corr + ps;
+    if (__any(mnew != mrow)) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] *= corr;
+    }
+    mrow = mnew;
+    uint4 pf[2][2];
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+      split2_f16(make_float4(st[8 * half], st[8 * half + 1], st[8 * half + 2], st[8 * half + 3]),
+                 make_float4(st[8 * half + 4], st[8 * half + 5], st[8 * half + 6],
+                             st[8 * half + 7]),
+                 pf[half][0], pf[half][1]);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V^T writes have landed
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        // V^T rows of the same keys: two runs of four (acc_row(8 half ..
+        // 8 half + 7, h)).
+        f16x8 vf[3];
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+          const uint16_t* vrow = Vt(pl)[32 * t + j] + 16 * half;
+          const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 4 * h);
+          const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 8 + 4 * h);
+          vf[pl] = f16x8_of(make_uint4(a0.x, a0.y, a1.x, a1.y));
+        }
+        // Smallest terms first: p1 (2^-11 v0), p0 v1, then p0 v0.
+        o[t] = mfma_f16(vf[2], f16x8_of(pf[half][1]), o[t]);
+        o[t] = mfma_f16(vf[1], f16x8_of(pf[half][0]), o[t]);
+        o[t] = mfma_f16(vf[0], f16x8_of(pf[half][0]), o[t]);
+      }
+    }
+  }
+
+  // Merge as in flash_x6w_tile, into registers first.
+  __syncthreads();
+  float* Om = reinterpret_cast<float*>(lds);
+  float2* ML = reinterpret_cast<float2*>(lds + NW * HD * OS * 4);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Om[(wave * HD + 32 * t + acc_row(r, h)) * OS + j] = o[t][r];
+  if (h == 0) ML[wave * 32 + j] = make_float2(mrow, lrow);
+  __syncthreads();
+  float res[PER], lse[PER];
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = tid + i * 64 * NW;
+    const int qr = e / HD, dim = e % HD;
+    float2 ml[NW];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      ml[w] = ML[w * 32 + qr];
+      mx = fmaxf(mx, ml[w].x);
+    }
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = __builtin_amdgcn_exp2f(ml[w].x - mx);
+      num += Om[(w * HD + dim) * OS + qr] * f;
+      den += ml[w].y * f;
+    }
+    res[i] = num / den;
+    lse[i] = mx * 0.69314718055994531f + logf(den);
+    // Rows past S hold no keys' weights: not stored, not checked.
+    if (q0 + qr < S) finite = finite && __builtin_isfinite(res[i]) && __builtin_isfinite(lse[i]);
+  }
+  if (__syncthreads_or(!finite)) return false;
+  float* op = p.o + fs.o + hh * HD;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = tid + i * 64 * NW;
+    const int qr = e / HD, dim = e % HD, qrow = q0 + qr;
+    if (qrow >= S) continue;
+    op[(size_t)qrow * d + dim] = res[i];
+    if (p.lse && dim == 0) p.lse[fs.l + (size_t)qrow * H + hh] = lse[i];
+  }
+  return true;
+}
+
+// The key-split tile on split-fp16 products, recomputed on split-bf16
+// products when an operand is beyond fp16's range: fp32 accuracy for any
+// finite input, with no flag for the caller to read.
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void k_flash_h3w(FlashParams p) {
+  constexpr int L2 = flash_w_lds<HD, NW, 2>(), L3 = flash_w_lds<HD, NW, 3>();
+  __shared__ __align__(16) unsigned char lds[L2 > L3 ? L2 : L3];
+  if (!flash_h3w_tile<HD, NW>(p, lds)) {
+    __syncthreads();
+    flash_x6w_tile<HD, NW>(p, lds);
+  }
+}
+
 // ---------------------------------------------------------------------------
 
 hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
@@ -2195,17 +2531,27 @@ hipError_t launch_flash(const FlashParams& p, int batch, int max_rows,
     const dim3 g(H, batch, (max_rows + 127) / 128);
     if (p.x6 && (long)g.x * g.y * g.z < flash_small_grid()) {
       // Fewer 128-query blocks than CUs: 32-query tiles, keys split over
-      // the block's waves (k_flash_x6w).
+      // the block's waves; split-fp16 tiles that recompute themselves on
+      // split-bf16 when an operand is out of fp16's range (k_flash_h3w),
+      // or split-bf16 throughout for FLASH_X6.
       const dim3 gw(H, batch, (max_rows + 31) / 32);
-      if (p.hd == 64)
-        hipLaunchKernelGGL((k_flash_x6w<64, 8>), gw, dim3(512), 0, s, p);
-      else
-        hipLaunchKernelGGL((k_flash_x6w<128, 4>), gw, dim3(256), 0, s, p);
+      if (p.x6 == FLASH_X6) {
+        if (p.hd == 64)
+          hipLaunchKernelGGL((k_flash_x6w<64, 8>), gw, dim3(512), 0, s, p);
+        else
+          hipLaunchKernelGGL((k_flash_x6w<128, 4>), gw, dim3(256), 0, s, p);
+      } else if (p.hd == 64) {
+        hipLaunchKernelGGL((k_flash_h3w<64, 8>), gw, dim3(512), 0, s, p);
+      } else {
+        hipLaunchKernelGGL((k_flash_h3w<128, 4>), gw, dim3(256), 0, s, p);
+      }
     } else if (p.x6 == FLASH_H3) {
       if (p.hd == 64)
         hipLaunchKernelGGL(k_flash_h3<64>, g, dim3(256), 0, s, p);
       else
         hipLaunchKernelGGL(k_flash_h3<128>, g, dim3(256), 0, s, p);
+    } else if (p.x6 == FLASH_FP32 && p.hd == 64) {
+      hipLaunchKernelGGL(k_flash_h3x<64>, g, dim3(256), 0, s, p);
     } else if (p.x6) {
       if (p.hd == 64)
         hipLaunchKernelGGL(k_flash_x6<64>, g, dim3(256), 0, s, p);

@@ -346,7 +346,8 @@ hipError_t shader_flash_attention(const float* q, const float* k,
   // Sequence b is the node at row_offset + b * seq_len.
   p.q_bs = p.kv_bs = p.o_bs = (long)shape.seq_len * shape.dim;
   p.lse_bs = (long)shape.seq_len * (shape.dim / shape.head_dim);
-  p.x6 = 1;  // head_dim 64 / 128: split-bfloat16 MFMAs, fp32 accuracy
+  // head_dim 64 / 128: fp32 accuracy on split MFMAs, no flag to read back.
+  p.x6 = FLASH_FP32;
   return launch_flash(p, (int)batch, shape.seq_len, s);
 }
 

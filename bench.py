@@ -297,8 +297,9 @@ def scaled_measurement(pkg, hip, be, w, steps=8, with_prefill=True, with_decode=
 
 
 def prefill_measurement(pkg, hip, be, model, cfg, CTX, reps=3):
-    """Config 3 (16 x 512 prefill, seed 3) on the default split-bf16 kernels
-    and on the fp32 MFMAs, then the trainer forward on the same rows."""
+    """Config 3 (16 x 512 prefill, seed 3) on the default split-fp16 kernels,
+    on the split-bf16 ones and on the fp32 MFMAs, then the trainer forward on
+    the same rows."""
     Bp, Sp = 16, 512
     ps = hip.Session(model, CTX, Bp)
     ptoks = pkg.synthetic_tokens(Bp * Sp, cfg.vocab_size, seed=3).reshape(Bp, Sp)
@@ -373,8 +374,10 @@ def config2_measurement(hip, be, reps=10):
     N(0,1) from seed 2, scale 1/8.  As the reference issues it: one
     FLASH_ATTENTION node per sequence at row_offset b * 512
     (layers.rs:410-421; each node runs the key-split kernel), and the same
-    nodes as one launch (akh_flash_attention_batched).  Both run the
-    split-bfloat16 kernels (six bf16 products per fp32 multiply-add)."""
+    nodes as one launch (akh_flash_attention_batched).  Both run split-fp16
+    tiles (three fp16 products per fp32 multiply-add); a tile with an operand
+    beyond fp16's range recomputes itself on split-bfloat16 products (none
+    does on these inputs)."""
     B2, S2, H2, hd2 = 8, 512, 12, 64
     d2 = H2 * hd2
     rng2 = np.random.default_rng(2)
@@ -394,7 +397,7 @@ def config2_measurement(hip, be, reps=10):
         flash_all()
     c2_ms = be.timer_stop() / reps
     c2_flop = 2 * hd2 * S2 * (S2 + 1) * B2 * H2
-    rn = prefill_rates(c2_ms, 0, c2_flop, 0, 0, c2_flop)
+    rn = prefill_rates(c2_ms, 0, c2_flop, 0, c2_flop, 0)
     bshape = hip.FlashAttnMeta(S2, d2, hd2, 0.125, 0)
     bmeta = be.meta(bshape)
     l2b = be.zeros(B2 * S2 * H2)
@@ -404,9 +407,10 @@ def config2_measurement(hip, be, reps=10):
     for _ in range(reps):
         be.flash_attention_batched(q2, k2, v2, o2, l2b, bshape, bmeta, B2)
     c2b_ms = be.timer_stop() / reps
-    rb = prefill_rates(c2b_ms, 0, c2_flop, 0, 0, c2_flop)
+    rb = prefill_rates(c2b_ms, 0, c2_flop, 0, c2_flop, 0)
     return {"workload": "config 2: flash attention 8 x 12 x 512 x 64 (seed 2)",
-            "kernel": "split-bf16 flash (fp32-accurate)", "flop": c2_flop,
+            "kernel": "split-fp16 flash (fp32-accurate; split-bf16 recompute of any tile "
+                      "with an operand beyond fp16's range)", "flop": c2_flop,
             "per_node_ms": round(c2_ms, 4),
             "per_node_tflops": rn["tflops"],
             "per_node_fp32_equiv_over_fp32_peak": rn["fp32_equiv_over_fp32_peak"],

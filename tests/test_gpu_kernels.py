@@ -178,6 +178,73 @@ def test_flash_attention(backend, pkg, ora, seq, heads, hd):
 
 
 @pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("where", ["none", "q", "k", "v"])
+def test_flash_attention_beyond_fp16_range(backend, pkg, ora, hd, where):
+    # A small grid runs split-fp16 tiles; a tile with an operand beyond
+    # fp16's range (|x| >= 65520) recomputes itself on split-bf16 products,
+    # so every tile matches a float64 reference to fp32 level.  The large
+    # entry's partner dims are scaled down so the scores stay moderate (an
+    # fp32 score of 1e4 would already move the weights by ~1e-3).
+    h = pkg.hip
+    heads, S = 2, 160
+    dim = heads * hd
+    q, k, v = (ora.rand_vec(S * dim, 60 + i).reshape(S, dim) for i in range(3))
+    if where == "q":
+        q[100, 5] = 1.0e5
+        k[:, 5] *= 1e-4
+    elif where == "k":
+        k[37, hd + 3] = -7.0e4
+        q[:, hd + 3] *= 1e-4
+    elif where == "v":
+        v[50, 7] = 9.0e4
+    got, lse = _flash(backend, h, q.ravel(), k.ravel(), v.ravel(), S, dim, hd)
+    got = got.reshape(S, dim)
+    Q, K, V = (x.astype(np.float64) for x in (q, k, v))
+    for hh in range(heads):
+        sl = slice(hh * hd, (hh + 1) * hd)
+        s = Q[:, sl] @ K[:, sl].T / np.sqrt(hd)
+        s[np.triu_indices(S, 1)] = -np.inf
+        w = np.exp(s - s.max(1, keepdims=True))
+        ref = (w / w.sum(1, keepdims=True)) @ V[:, sl]
+        tol = 1e-5 * (1.0 + np.abs(V[:, sl]).max(0))
+        assert np.all(np.abs(got[:, sl] - ref) <= tol), (where, hh)
+        ref_l = np.log(w.sum(1)) + s.max(1)
+        assert np.abs(lse.reshape(S, heads)[:, hh] - ref_l).max() < 1e-5
+
+
+def test_flash_attention_batched_beyond_fp16_range(backend, pkg):
+    # A grid of 128-query tiles as large as the part (8 x 8 x 4 = 256 blocks)
+    # runs split-fp16 tiles that recompute themselves on split-bf16 products
+    # when an operand is beyond fp16's range: sequence 3 holds such a K entry
+    # and sequence 6 such a V entry; sequence 0 has none.  Each matches a
+    # float64 reference to fp32 level.
+    h = pkg.hip
+    B, S, H, hd = 8, 512, 8, 64
+    d = H * hd
+    rng = np.random.default_rng(70)
+    q, k, v = (rng.standard_normal((B, S, d), dtype=np.float32) for _ in range(3))
+    k[3, 100, 5] = 7.0e4
+    q[3, :, 5] *= 1e-4
+    v[6, 200, hd + 6] = -9.0e4
+    out, lse = backend.zeros(B * S * d), backend.zeros(B * S * H)
+    shape = h.FlashAttnMeta(S, d, hd, 0.125, 0)
+    backend.flash_attention_batched(backend.tensor(q.ravel()), backend.tensor(k.ravel()),
+                                    backend.tensor(v.ravel()), out, lse, shape,
+                                    _meta(backend, shape), B)
+    got = out.download().reshape(B, S, d)
+    for b in (0, 3, 6):
+        Q, K, V = (x[b].astype(np.float64) for x in (q, k, v))
+        for hh in (0, 1):
+            sl = slice(hh * hd, (hh + 1) * hd)
+            s = Q[:, sl] @ K[:, sl].T * 0.125
+            s[np.triu_indices(S, 1)] = -np.inf
+            w = np.exp(s - s.max(1, keepdims=True))
+            ref = (w / w.sum(1, keepdims=True)) @ V[:, sl]
+            tol = 1e-5 * (1.0 + np.abs(V[:, sl]).max(0))
+            assert np.all(np.abs(got[b][:, sl] - ref) <= tol), (b, hh)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
 def test_flash_attention_live_meta_bounds_work(backend, pkg, ora, hd):
     # The grid is sized from the recorded shape (200 rows); the meta read
     # when the kernel runs says 150: rows 0..149 are attention over the first
