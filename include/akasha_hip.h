@@ -310,10 +310,12 @@ akh_status akh_model_set_prefill_bf16(akh_model* m, int enable);
  * akh_model_upload_param.  Flash attention (head_dim 64 / 128) follows the
  * split: AKH_SPLIT_H3 runs it on split-fp16 MFMAs (two terms, three
  * products), flagged and rerun in fp32 like the GEMMs when an operand is
- * out of fp16's range; AKH_SPLIT_X6, and the per-shader FLASH_ATTENTION
- * launchers whatever the split, run it on split-bfloat16 MFMAs.  The
- * bf16-MFMA prefill (akh_model_set_prefill_bf16), when on, takes
- * precedence. */
+ * out of fp16's range; AKH_SPLIT_X6 runs it on split-bfloat16 MFMAs.  The
+ * per-shader FLASH_ATTENTION launchers, whatever the split, run split-fp16
+ * tiles that recompute themselves on split-bfloat16 MFMAs when an operand is
+ * out of fp16's range (split-bfloat16 throughout at head_dim 128 on grids
+ * that fill the part).  The bf16-MFMA prefill (akh_model_set_prefill_bf16),
+ * when on, takes precedence. */
 #define AKH_SPLIT_NONE 0
 #define AKH_SPLIT_X6 1
 #define AKH_SPLIT_H3 2
