@@ -3,9 +3,10 @@
 The compute lives in libakasha_hip.so (hand-written HIP kernels + C++
 runtime behind the C ABI in include/akasha_hip.h).  This package holds the
 ctypes bindings (``hip``), the model profiles and synthetic-input generators
-(``model``), V3 checkpoint files (``checkpoint``) and the build recipe
-(``build``).
+(``model``), V3 checkpoint files (``checkpoint``), the reference's per-shader
+inference graphs driven through the launchers (``shader_graph``) and the
+build recipe (``build``).
 """
 
-from . import checkpoint, hip, model  # noqa: F401
+from . import checkpoint, hip, model, shader_graph  # noqa: F401
 from .model import ModelConfig, synthetic_tokens, synthetic_weights  # noqa: F401

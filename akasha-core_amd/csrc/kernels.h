@@ -27,9 +27,13 @@ hipError_t shader_rmsnorm(const float* x, const float* w, float* out,
                           akh_norm_meta shape, const akh_norm_meta* meta,
                           hipStream_t s);
 // MATMUL / GEMV (accumulate = 0) and MATMUL_ADD / GEMV_ADD (accumulate = 1).
+// `ws` (kGemvWsFloats floats) and `cnt` (kGemvSlabs counters, zero between
+// launches) serve the K-split small-m path; null: one split.
+constexpr size_t kGemvWsFloats = (size_t)4 << 20;
+constexpr int kGemvSlabs = 1 << 16;
 hipError_t shader_matmul(const float* a, const float* b, float* c,
                          akh_matmul_meta shape, const akh_matmul_meta* meta,
-                         int accumulate, hipStream_t s);
+                         int accumulate, float* ws, int* cnt, hipStream_t s);
 hipError_t shader_head_gather(const float* src, float* dst,
                               akh_head_move_meta shape,
                               const akh_head_move_meta* meta, hipStream_t s);

@@ -65,6 +65,10 @@ struct akh_backend {
   void* scratch = nullptr;  // launcher scratch, grown on demand outside capture
   size_t scratch_bytes = 0;
   double* noalloc_scratch = nullptr;  // the device's fixed sampler workspace
+  // The small-m MATMUL launchers' K-split partials and per-slab counters
+  // (allocated with the backend, so graph capture never has to).
+  float* gemv_ws = nullptr;
+  int* gemv_cnt = nullptr;
 };
 
 namespace {
@@ -114,6 +118,9 @@ extern "C" akh_status akh_backend_new(int device, akh_backend** out) {
   // The device's copy of the allocation-free sampler's workspace (device
   // current above).
   if (e == hipSuccess) e = sample_noalloc_scratch(device, &be->noalloc_scratch);
+  if (e == hipSuccess) e = hipMalloc(&be->gemv_ws, kGemvWsFloats * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&be->gemv_cnt, kGemvSlabs * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(be->gemv_cnt, 0, kGemvSlabs * sizeof(int));
   if (e != hipSuccess) {
     akh_backend_free(be);
     return fail(AKH_E_HIP, std::string("akh_backend_new: ") + hipGetErrorString(e));
@@ -129,6 +136,8 @@ extern "C" void akh_backend_free(akh_backend* be) {
   if (be->t0) hipEventDestroy(be->t0);
   if (be->t1) hipEventDestroy(be->t1);
   if (be->scratch) hipFree(be->scratch);
+  if (be->gemv_ws) hipFree(be->gemv_ws);
+  if (be->gemv_cnt) hipFree(be->gemv_cnt);
   if (be->stream) hipStreamDestroy(be->stream);
   delete be;
 }
@@ -273,7 +282,7 @@ extern "C" akh_status akh_matmul(akh_backend* be, const float* a,
                                  const akh_matmul_meta* meta) {
   BE_CHECK(be);
   CHECK_ARG(a && b && c && meta, "akh_matmul: NULL buffer");
-  HIP_TRY(shader_matmul(a, b, c, shape, meta, 0, be->stream));
+  HIP_TRY(shader_matmul(a, b, c, shape, meta, 0, be->gemv_ws, be->gemv_cnt, be->stream));
   return AKH_OK;
 }
 
@@ -283,7 +292,7 @@ extern "C" akh_status akh_matmul_add(akh_backend* be, const float* a,
                                      const akh_matmul_meta* meta) {
   BE_CHECK(be);
   CHECK_ARG(a && b && c && meta, "akh_matmul_add: NULL buffer");
-  HIP_TRY(shader_matmul(a, b, c, shape, meta, 1, be->stream));
+  HIP_TRY(shader_matmul(a, b, c, shape, meta, 1, be->gemv_ws, be->gemv_cnt, be->stream));
   return AKH_OK;
 }
 

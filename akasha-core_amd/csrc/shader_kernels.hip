@@ -6,6 +6,8 @@
 // (ARCHITECTURE.md "live metas").
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -55,87 +57,147 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x,
 // MATMUL / GEMV and MATMUL_ADD / GEMV_ADD for m <= 32 (the reference routes
 // m == 1 to GEMV, emit.rs:31-33): C[m, n] (+)= A[m, k] B[k, n].
 //
-// One 256-thread block per 32-column tile of C, whole K.  Row-major A is
-// staged through LDS 256 k at a time in the k-quad layout, so every MFMA
-// A operand is one conflict-free LDS read per four k; the four waves split
-// each staged piece and their partial tiles are reduced in LDS.
-__global__ __launch_bounds__(256) void k_shader_skinny(
-    const float* a, const float* b, float* c, const akh_matmul_meta* meta,
-    int accumulate) {
-  constexpr int KP = 256;  // k per staged piece
-  __shared__ float4 xs[KP / 4][32];
-  __shared__ float red[2][32][33];
-  const int M = (int)meta->m, N = (int)meta->n, K = (int)meta->k;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int j = lane & 31, h = lane >> 5;
-  const int n0 = blockIdx.x * 32;
-  if (n0 >= N || M <= 0) return;
-  const int ncol = n0 + j;
-  const bool col_ok = ncol < N;
-  const bool a_vec = (K & 3) == 0;
-  f32x16 acc = zero16();
+// B streams once over the whole part.  A block takes a slab of 32 columns
+// and one of `splits` ranges of `kchunk` rows of B.  Thread t reads row
+// t / 8 of each 32-row round and columns 4 (t % 8) .. + 3 of it (one 16-byte
+// load where B and N allow, so a wave's load is 1 KB of eight rows), with
+// GR rounds in flight; it keeps the sums of up to MR rows of A.  The 32 row
+// lanes of each column meet through lane exchanges and LDS.  With one split
+// the block writes C.  Otherwise it writes its partial sums to the
+// workspace (through to device scope), waits for them to complete and counts
+// itself; the last block of the slab adds the partials in split order (the
+// same sums whichever block arrives last) and writes C.  Few splits per slab
+// (their counts meet at one address), many slabs.  The grid and the splits
+// come from the recorded shape; M, N and K from the meta (at most the
+// recorded ones).
+struct GemvParams {
+  const float* a;
+  const float* b;
+  float* c;
+  const akh_matmul_meta* meta;
+  int accumulate;
+  int mrec, nrec;  // the recorded shape: the workspace's layout
+  int splits, kchunk;
+  float* ws;
+  int* cnt;
+  int vec;  // B 16-byte aligned and the recorded N a multiple of 4
+};
 
-  for (int kp0 = 0; kp0 < K; kp0 += KP) {
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < 32 * (KP / 4); idx += 256) {
-      const int m = idx / (KP / 4), q = idx % (KP / 4);
-      const int k = kp0 + 4 * q;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (m < M) {
-        const float* ar = a + (size_t)m * K;
-        if (a_vec && k + 3 < K) {
-          v = *reinterpret_cast<const float4*>(ar + k);
-        } else {
-          if (k < K) v.x = ar[k];
-          if (k + 1 < K) v.y = ar[k + 1];
-          if (k + 2 < K) v.z = ar[k + 2];
-          if (k + 3 < K) v.w = ar[k + 3];
+template <int MR>
+__global__ __launch_bounds__(256) void k_shader_gemv(GemvParams g) {
+#ifndef AKH_GEMV_GR
+#define AKH_GEMV_GR 4
+#endif
+  constexpr int GR = MR > 4 ? 2 : AKH_GEMV_GR;  // 32-row rounds in flight
+  __shared__ float red[4][MR][32];
+  __shared__ int last_block;
+  const int M = min((int)g.meta->m, min(g.mrec, MR)), N = min((int)g.meta->n, g.nrec);
+  const int K = (int)g.meta->k;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n0 = blockIdx.x * 32;
+  if (n0 >= N || M <= 0) return;  // the whole slab: no block of it counts
+  const int rl = tid >> 3, nc = n0 + 4 * (tid & 7);
+  const int k0 = min(K, blockIdx.y * g.kchunk), k1 = min(K, k0 + g.kchunk);
+  const bool vec = g.vec && N % 4 == 0;
+  float acc[MR][4];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[m][c] = 0.f;
+  for (int kg = k0 + rl; kg < k1; kg += 32 * GR) {
+    float w[GR][4];
+#pragma unroll
+    for (int u = 0; u < GR; ++u) {
+      const int k = kg + 32 * u;
+      const bool ok = k < k1 && nc < N;
+      const float* src = g.b + (size_t)(ok ? k : 0) * N + (ok ? nc : 0);
+      if (vec) {
+        const float4 t = ok ? *reinterpret_cast<const float4*>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+        w[u][0] = t.x;
+        w[u][1] = t.y;
+        w[u][2] = t.z;
+        w[u][3] = t.w;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) w[u][c] = ok && nc + c < N ? src[c] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m >= M) continue;
+      const float* ar = g.a + (size_t)m * K;
+#pragma unroll
+      for (int u = 0; u < GR; ++u) {
+        const int k = kg + 32 * u;
+        const float x = k < k1 ? ar[k] : 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(x, w[u][c], acc[m][c]);
+      }
+    }
+  }
+  // Rows: the wave's eight row lanes of each column (lane bits 3..5), then
+  // the four waves through LDS.  Thread t < 32 then holds column n0 + t.
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float v = acc[m][c];
+      v += __shfl_xor(v, 8, 64);
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      acc[m][c] = v;
+    }
+  if (lane < 8)
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[wave][m][4 * lane + c] = acc[m][c];
+  __syncthreads();
+  const int n = n0 + tid;
+  const bool col = tid < 32 && n < N;
+  float tot[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const int t = tid & 31;
+    tot[m] = ((red[0][m][t] + red[1][m][t]) + red[2][m][t]) + red[3][m][t];
+  }
+  if (g.splits == 1) {
+    if (col)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) {
+          float* y = g.c + (size_t)m * N + n;
+          *y = g.accumulate ? *y + tot[m] : tot[m];
         }
-      }
-      xs[q][m] = v;
-    }
-    __syncthreads();
-    // Wave w takes k-quads [16w, 16w + 16) of the piece; half h the first
-    // or second 8 of them.
-    const int qb = wave * 16 + h * 8;
-#pragma unroll
-    for (int g = 0; g < 8; g += 2) {
-      float wv[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int k = kp0 + 4 * (qb + g) + u;
-        wv[u] = (k < K && col_ok) ? b[(size_t)k * N + ncol] : 0.f;
-      }
-      const float4 x0 = xs[qb + g][j], x1 = xs[qb + g + 1][j];
-      acc = mfma32(x0.x, wv[0], acc);
-      acc = mfma32(x0.y, wv[1], acc);
-      acc = mfma32(x0.z, wv[2], acc);
-      acc = mfma32(x0.w, wv[3], acc);
-      acc = mfma32(x1.x, wv[4], acc);
-      acc = mfma32(x1.y, wv[5], acc);
-      acc = mfma32(x1.z, wv[6], acc);
-      acc = mfma32(x1.w, wv[7], acc);
-    }
+    return;
   }
-  // Tree reduction of the four waves' tiles: (2,3) -> (0,1), then 1 -> 0.
-  for (int half = 2; half >= 1; half >>= 1) {
-    __syncthreads();
-    if (wave >= half && wave < 2 * half)
+  const size_t plane = (size_t)g.mrec * g.nrec;
+  if (col)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[wave - half][acc_row(r, h)][j] = acc[r];
-    __syncthreads();
-    if (wave < half)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] += red[wave][acc_row(r, h)][j];
+    for (int m = 0; m < MR; ++m)
+      if (m < M)
+        __hip_atomic_store(g.ws + blockIdx.y * plane + (size_t)m * g.nrec + n, tot[m],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const int done =
+        __hip_atomic_fetch_add(g.cnt + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_block = done == g.splits - 1;
+    if (last_block)  // zero for the next launch
+      __hip_atomic_store(g.cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (wave != 0 || !col_ok) return;
+  __syncthreads();
+  if (!last_block || !col) return;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int m = acc_row(r, h);
-    if (m < M) {
-      float* y = c + (size_t)m * N + ncol;
-      *y = accumulate ? *y + acc[r] : acc[r];
-    }
+  for (int m = 0; m < MR; ++m) {
+    if (m >= M) continue;
+    const float* q = g.ws + (size_t)m * g.nrec + n;
+    float sum = 0.f;
+    for (int sp = 0; sp < g.splits; ++sp)
+      sum += __hip_atomic_load(q + sp * plane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float* y = g.c + (size_t)m * N + n;
+    *y = g.accumulate ? *y + sum : sum;
   }
 }
 
@@ -281,11 +343,37 @@ hipError_t shader_rmsnorm(const float* x, const float* w, float* out,
 
 hipError_t shader_matmul(const float* a, const float* b, float* c,
                          akh_matmul_meta shape, const akh_matmul_meta* meta,
-                         int accumulate, hipStream_t s) {
+                         int accumulate, float* ws, int* cnt, hipStream_t s) {
   if (shape.m == 0 || shape.n == 0) return hipSuccess;
-  if (shape.m <= 32u) {  // one 32-row MFMA tile
-    hipLaunchKernelGGL(k_shader_skinny, dim3((shape.n + 31) / 32), dim3(256),
-                       0, s, a, b, c, meta, accumulate);
+  if (shape.m <= 32u) {
+    // 32-column slabs over at most 8 ranges of K (at least 128 rows each),
+    // about 256 blocks where the slabs are fewer.
+#ifndef AKH_GEMV_TARGET
+#define AKH_GEMV_TARGET 256
+#endif
+#ifndef AKH_GEMV_SMAX
+#define AKH_GEMV_SMAX 8
+#endif
+#ifndef AKH_GEMV_KMIN
+#define AKH_GEMV_KMIN 128
+#endif
+    GemvParams g{a, b, c, meta, accumulate, (int)shape.m, (int)shape.n, 1, 1, ws, cnt, 0};
+    g.vec = shape.n % 4 == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0;
+    const int slabs = (int)((shape.n + 31) / 32), K = (int)shape.k;
+    int splits = std::min(AKH_GEMV_SMAX, std::max(1, (AKH_GEMV_TARGET + slabs - 1) / slabs));
+    splits = std::min(splits, std::max(1, K / AKH_GEMV_KMIN));
+    if (!ws || !cnt || slabs > kGemvSlabs) splits = 1;
+    const size_t plane = (size_t)shape.m * shape.n;
+    if ((size_t)splits * plane > kGemvWsFloats) splits = (int)std::max<size_t>(1, kGemvWsFloats / plane);
+    g.kchunk = std::max(1, (K + splits - 1) / splits);
+    g.splits = std::max(1, (K + g.kchunk - 1) / g.kchunk);
+    const dim3 grid(slabs, g.splits);
+    if (shape.m == 1)
+      hipLaunchKernelGGL(k_shader_gemv<1>, grid, dim3(256), 0, s, g);
+    else if (shape.m <= 4)
+      hipLaunchKernelGGL(k_shader_gemv<4>, grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL(k_shader_gemv<32>, grid, dim3(256), 0, s, g);
     return hipGetLastError();
   }
   GemmParams p{};

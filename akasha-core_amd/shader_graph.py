@@ -86,6 +86,16 @@ class ShaderDecoder:
                   hip.MatMulMeta(1, V, d), self.lm_meta)
         self.graph = be.graph_end()
 
+    def close(self):
+        """Release the graph and every device buffer this decoder holds."""
+        if self.graph is not None:
+            self.graph.close()
+            self.graph = None
+        for v in list(vars(self).values()):
+            for t in v if isinstance(v, list) else [v]:
+                if isinstance(t, self.hip.DeviceTensor):
+                    t.free()
+
     def decode_step(self, token):
         hip, be, c = self.hip, self.be, self.cfg
         pos = self.cur_len

@@ -500,6 +500,48 @@ def cpu_prefill_baseline(cfg, weights, tokens, threads):
     return len(tokens) / dt, dt
 
 
+def shader_graph_measurement(pkg, hip, be, cfg, weights, session_tokens):
+    """Config 1 through the reference's per-shader decode graph: ShaderDecoder
+    rebuilds build_decode_layer node for node from the C-ABI launchers (one
+    launcher per shader, inference_graphs.rs:339-509), captures it once and
+    replays it every step after rewriting the four dynamic metas, and reads
+    the logits back, as InferenceSession::decode_step does
+    (inference.rs:178-262).  The 64-token prompt goes in as decode steps,
+    then 64 greedy steps with the argmax on the host, as the reference's
+    loop takes it.  This is what the reference's own emitter gets from the
+    launchers, beside the session API's fused step."""
+    import time
+    dec = pkg.shader_graph.ShaderDecoder(hip, be, cfg, weights, 128)
+    prompt = pkg.synthetic_tokens(64, cfg.vocab_size, seed=1)
+    t0 = time.perf_counter()
+    for t in prompt:
+        logits = dec.decode_step(int(t))
+    t1 = time.perf_counter()
+    toks = [int(np.argmax(logits))]
+    t2 = time.perf_counter()
+    for _ in range(64):
+        logits = dec.decode_step(toks[-1])
+        toks.append(int(np.argmax(logits)))
+    t3 = time.perf_counter()
+    be.synchronize()
+    be.timer_start()
+    for _ in range(16):
+        dec.graph.execute()
+    replay_ms = be.timer_stop() / 16
+    L = cfg.num_layers
+    out = {"workload": "config 1 through the per-shader decode graph (the reference's "
+                       "build_decode_layer from the C-ABI launchers, replayed as a hipGraph "
+                       "with live metas; logits read back and argmax on the host each step)",
+           "launches_per_step": 16 * L + 3,
+           "prompt_ms_per_token": round((t1 - t0) / 64 * 1e3, 3),
+           "ms_per_token": round((t3 - t2) / 64 * 1e3, 3),
+           "tok_s": round(64 / (t3 - t2), 1),
+           "graph_replay_ms": round(replay_ms, 3),
+           "tokens_match_session": toks == session_tokens}
+    dec.close()
+    return out
+
+
 def cpu_config1(pkg, cfg, weights, threads):
     """Config 1 in full on the oracle: prefill of the 64-token prompt
     (seed 1), then 64 greedy decode steps, each token the first maximum of
@@ -728,6 +770,8 @@ def main():
     config1 = {"workload": "config 1: hall-1.0 batch 1, 64-token prompt (seed 1), 64 greedy steps",
                "ms_per_token": round(c1_ms / 64, 4), "tok_s": round(64 / (c1_ms / 1e3), 1),
                "hbm_frac": round(c1_bytes / (c1_ms / 64 / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+    log("bench: config 1 through the per-shader decode graph")
+    config1["shader_graph"] = shader_graph_measurement(pkg, hip, be, cfg, w, config1_tokens)
 
     config2 = config2_measurement(hip, be)
 

@@ -56,7 +56,10 @@ def test_gemv_routing(backend, pkg, ora):
 
 
 @pytest.mark.parametrize("m,n,k", [(37, 301, 19), (2, 50257, 768), (32, 768, 3072),
-                                   (128, 128, 64), (200, 2304, 768), (513, 130, 37)])
+                                   (128, 128, 64), (200, 2304, 768), (513, 130, 37),
+                                   # small m: K split over the part (decode's GEMVs)
+                                   (1, 768, 3072), (1, 2304, 768), (5, 3072, 768), (1, 3, 5),
+                                   (1, 1000, 1), (17, 768, 768)])
 def test_matmul_and_add(backend, pkg, ora, m, n, k):
     h = pkg.hip
     a, b = ora.rand_vec(m * k, 1), ora.rand_vec(k * n, 2)
@@ -88,6 +91,40 @@ def test_matmul_live_meta_bounds_work(backend, pkg, ora):
         ref = ora.matmul(a[: m * K], b[: K * n], m, n, K)
         assert np.abs(got[: m * n] - ref).max() < 1e-4
         assert np.all(got[m * n:] == 7.0)
+
+
+def test_small_m_matmul_k_split_live_meta(backend, pkg, ora):
+    # Small-m MATMUL splits K over blocks whose partial sums the last block
+    # of each column slab adds.  The grid and splits follow the recorded
+    # shape; live metas shrink m, n and k, so some splits get no rows and
+    # some slabs no columns (they must neither count nor store).  Every call
+    # after the first reuses the workspace and its counters; the same call
+    # twice gives the same bits.
+    h = pkg.hip
+    M, N, K = 4, 2304, 768
+    a, b = ora.rand_vec(M * K, 11), ora.rand_vec(K * N, 12)
+    c0 = ora.rand_vec(M * N, 13)
+    rec = h.MatMulMeta(M, N, K)
+    for m, n, k in ((4, 2304, 768), (1, 2304, 768), (3, 1000, 300), (2, 257, 7), (4, 2304, 768)):
+        tb = backend.tensor(b[: k * n].copy())
+        am = a.reshape(M, K)[:m, :k].copy().ravel()
+        tam = backend.tensor(am)
+        meta = _meta(backend, h.MatMulMeta(m, n, k))
+        outs = []
+        for _ in range(2):
+            c = backend.tensor(np.full(M * N, 7.0, np.float32))
+            backend.matmul(tam, tb, c, rec, meta)
+            outs.append(c.download())
+        cadd = backend.tensor(c0)
+        backend.matmul_add(tam, tb, cadd, rec, meta)
+        ref = ora.matmul(am, b[: k * n], m, n, k)
+        tol = 1e-4 * max(1.0, np.sqrt(k / 19.0))
+        assert np.abs(outs[0][: m * n] - ref).max() < tol, (m, n, k)
+        assert np.all(outs[0][m * n:] == 7.0)
+        assert np.array_equal(outs[0], outs[1])
+        got = cadd.download()
+        assert np.abs(got[: m * n] - ora.matmul_add(am, b[: k * n], c0[: m * n], m, n, k)).max() < tol
+        assert np.array_equal(got[m * n:], c0[m * n:])
 
 
 @pytest.mark.parametrize("seq,dim", [(8, 4), (37, 12), (65, 48)])
@@ -363,7 +400,7 @@ def test_shader_decode_graph_replays_with_live_metas(backend, pkg, ora):
     # build_decode_layer + decode_step through the per-shader ABI, captured
     # once into a hipGraph and replayed every step after the dynamic metas
     # are rewritten (inference.rs:178-262).
-    from shader_graph import ShaderDecoder
+    from akasha_core_amd.shader_graph import ShaderDecoder
     cfg = pkg.ModelConfig.new(97, 64, 4, 2, 16)
     w = pkg.synthetic_weights(cfg, seed=42)
     dec = ShaderDecoder(pkg.hip, backend, cfg, w, 16)
@@ -377,7 +414,7 @@ def test_shader_decode_graph_replays_with_live_metas(backend, pkg, ora):
 
 
 def test_shader_prefill_graph(backend, pkg, ora):
-    from shader_graph import shader_prefill
+    from akasha_core_amd.shader_graph import shader_prefill
     cfg = pkg.ModelConfig.new(97, 128, 2, 2, 48)  # head_dim 64 -> MFMA flash
     w = pkg.synthetic_weights(cfg, seed=8)
     toks = ora.rand_tokens(37, 97, 4)
