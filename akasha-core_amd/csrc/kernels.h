@@ -119,6 +119,12 @@ struct GemmParams {
   // launch_gemm_bf16 with an fp32 A: round A to bfloat16 (one product)
   // instead of splitting it into hi + lo (two).
   int a_hi_only;
+  // launch_gemm with a workspace (kGemvWsFloats floats, kGemvSlabs counters
+  // at zero): grids too small for the part split K over several blocks per
+  // tile.  Null: no split.
+  float* split_ws;
+  int* split_cnt;
+  int split_kc;  // set by launch_gemm: rows of K per split
 };
 
 enum { FLASH_X6 = 1, FLASH_H3 = 2, FLASH_FP32 = 3 };  // FlashParams::x6

@@ -3,6 +3,8 @@
 // the embedding gather.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -235,6 +237,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   constexpr int APAD = 4;
   __shared__ float As[BK][BM + APAD];
   __shared__ float Bs[BK][BN];
+  __shared__ int last_split;
 
   int M = p.M, N = p.N, K = p.K;
   if (p.meta) {
@@ -247,7 +250,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   const int per_xcd = (int)(gridDim.x * gridDim.y) / 8;
   if (id < per_xcd * 8) id = (id % 8) * per_xcd + id / 8;
   const int m0 = (id / gridDim.x) * BM, n0 = (id % gridDim.x) * BN;
-  if (m0 >= M || n0 >= N) return;
+  if (m0 >= M || n0 >= N) return;  // every split of the tile returns here
+  // This block's rows of K: all of them, or split blockIdx.z's p.split_kc.
+  const int kbeg = p.split_ws ? min(K, (int)blockIdx.z * p.split_kc) : 0;
+  const int kend = p.split_ws ? min(K, kbeg + p.split_kc) : K;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
@@ -267,27 +273,27 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int gk = k0 + a_k + 4 * q;
-      if (gm < M && a_vec && gk + 3 < K) {
+      if (gm < M && a_vec && gk + 3 < kend) {
         const float4 t = *reinterpret_cast<const float4*>(ap + gk);
         ra[4 * q] = t.x; ra[4 * q + 1] = t.y; ra[4 * q + 2] = t.z; ra[4 * q + 3] = t.w;
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          ra[4 * q + e] = (gm < M && gk + e < K) ? ap[gk + e] : 0.f;
+          ra[4 * q + e] = (gm < M && gk + e < kend) ? ap[gk + e] : 0.f;
       }
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int gk = k0 + b_row + 8 * q;
       const int gn = n0 + b_col;
-      const float* bp = p.b + (size_t)(gk < K ? gk : 0) * N + gn;
-      if (gk < K && b_vec && gn + 3 < N) {
+      const float* bp = p.b + (size_t)(gk < kend ? gk : 0) * N + gn;
+      if (gk < kend && b_vec && gn + 3 < N) {
         const float4 t = *reinterpret_cast<const float4*>(bp);
         rb[4 * q] = t.x; rb[4 * q + 1] = t.y; rb[4 * q + 2] = t.z; rb[4 * q + 3] = t.w;
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          rb[4 * q + e] = (gk < K && gn + e < N) ? bp[e] : 0.f;
+          rb[4 * q + e] = (gk < kend && gn + e < N) ? bp[e] : 0.f;
       }
     }
   };
@@ -306,12 +312,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) acc[a][t] = zero16();
 
-  const int nk = (K + BK - 1) / BK;
-  load_tile(0);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+  load_tile(kbeg);
   store_tile();
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) load_tile((kt + 1) * BK);
+    if (kt + 1 < nk) load_tile(kbeg + (kt + 1) * BK);
 #pragma unroll
     for (int s = 0; s < BK / 2; ++s) {
       const int kk = 2 * s + h;
@@ -330,6 +336,62 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     }
   }
 
+  if (p.split_ws && gridDim.z > 1) {
+    // A split tile: each block stores its sums (written through to device
+    // scope, lane-major), waits until they have completed and counts
+    // itself; the last of the tile's blocks adds every split's sums in split
+    // order (the same float sums whichever block is last) and runs the
+    // epilogue.
+    constexpr int TILE = BM * BN;
+    const int tile = blockIdx.x + gridDim.x * blockIdx.y;
+    const int tiles = gridDim.x * gridDim.y;
+    auto at = [&](int a, int t, int r) { return (((wave * 2 + a) * 2 + t) * 16 + r) * 64 + lane; };
+    float* mine = p.split_ws + ((size_t)blockIdx.z * tiles + tile) * TILE;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          __hip_atomic_store(mine + at(a, t, r), acc[a][t][r], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const int done =
+          __hip_atomic_fetch_add(p.split_cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_split = done == (int)gridDim.z - 1;
+      if (last_split)  // zero for the next launch
+        __hip_atomic_store(p.split_cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last_split) return;
+    // Split by split, each split's 64 values per lane all in flight at once.
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][t][r] = 0.f;
+    for (int sp = 0; sp < (int)gridDim.z; ++sp) {
+      const float* part = p.split_ws + ((size_t)sp * tiles + tile) * TILE;
+      float v[2][2][16];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            v[a][t][r] = __hip_atomic_load(part + at(a, t, r), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[a][t][r] += v[a][t][r];
+    }
+  }
 #pragma unroll
   for (int a = 0; a < 2; ++a) {
     float v0[16], v1[16];
@@ -2477,11 +2539,28 @@ __global__ __launch_bounds__(64 * NW) void k_flash_h3w(FlashParams p) {
 
 hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
   dim3 g((p.N + 127) / 128, (p.M + 127) / 128), b(256);
+  GemmParams q = p;
+  q.split_kc = p.K;
+  if (p.split_ws && p.split_cnt) {
+    // Fewer tiles than the part has CUs: K split over up to 16 blocks per
+    // tile (at least 64 rows each), about 256 blocks in all, within the
+    // workspace (one 128 x 128 partial per tile and split).
+    const long tiles = (long)g.x * g.y, ws_tiles = (long)(kGemvWsFloats / (128 * 128));
+    int splits = 1;
+    if (tiles < 256 && tiles <= kGemvSlabs)
+      splits = (int)std::min<long>({16, (256 + tiles - 1) / tiles, std::max(1, p.K / 64),
+                                    ws_tiles / tiles});
+    if (splits > 1) {
+      q.split_kc = ((p.K + splits - 1) / splits + 15) / 16 * 16;
+      g.z = (p.K + q.split_kc - 1) / q.split_kc;
+    }
+    if (g.z <= 1) q.split_ws = nullptr;
+  }
   switch (epi) {
-    case GEMM_STORE: hipLaunchKernelGGL(k_gemm<GEMM_STORE>, g, b, 0, s, p); break;
-    case GEMM_ADD: hipLaunchKernelGGL(k_gemm<GEMM_ADD>, g, b, 0, s, p); break;
-    case GEMM_SILU: hipLaunchKernelGGL(k_gemm<GEMM_SILU>, g, b, 0, s, p); break;
-    case GEMM_QKV: hipLaunchKernelGGL(k_gemm<GEMM_QKV>, g, b, 0, s, p); break;
+    case GEMM_STORE: hipLaunchKernelGGL(k_gemm<GEMM_STORE>, g, b, 0, s, q); break;
+    case GEMM_ADD: hipLaunchKernelGGL(k_gemm<GEMM_ADD>, g, b, 0, s, q); break;
+    case GEMM_SILU: hipLaunchKernelGGL(k_gemm<GEMM_SILU>, g, b, 0, s, q); break;
+    case GEMM_QKV: hipLaunchKernelGGL(k_gemm<GEMM_QKV>, g, b, 0, s, q); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -70,6 +70,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x,
 // (their counts meet at one address), many slabs.  The grid and the splits
 // come from the recorded shape; M, N and K from the meta (at most the
 // recorded ones).
+constexpr int kGemvMaxSplits = 8;
+
 struct GemvParams {
   const float* a;
   const float* b;
@@ -189,13 +191,20 @@ __global__ __launch_bounds__(256) void k_shader_gemv(GemvParams g) {
   }
   __syncthreads();
   if (!last_block || !col) return;
+  // At most kGemvMaxSplits partials per value, all loads in flight at once.
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     if (m >= M) continue;
     const float* q = g.ws + (size_t)m * g.nrec + n;
+    float t[kGemvMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kGemvMaxSplits; ++sp)
+      t[sp] = sp < g.splits ? __hip_atomic_load(q + sp * plane, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0.f;
     float sum = 0.f;
-    for (int sp = 0; sp < g.splits; ++sp)
-      sum += __hip_atomic_load(q + sp * plane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int sp = 0; sp < kGemvMaxSplits; ++sp) sum += t[sp];
     float* y = g.c + (size_t)m * N + n;
     *y = g.accumulate ? *y + sum : sum;
   }
@@ -352,7 +361,7 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
 #define AKH_GEMV_TARGET 256
 #endif
 #ifndef AKH_GEMV_SMAX
-#define AKH_GEMV_SMAX 8
+#define AKH_GEMV_SMAX kGemvMaxSplits
 #endif
 #ifndef AKH_GEMV_KMIN
 #define AKH_GEMV_KMIN 128
@@ -384,6 +393,8 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
   p.N = shape.n;
   p.K = shape.k;
   p.meta = meta;
+  p.split_ws = ws;  // prompt-sized m: K split where the tiles are few
+  p.split_cnt = cnt;
   return launch_gemm(p, accumulate ? GEMM_ADD : GEMM_STORE, s);
 }
 

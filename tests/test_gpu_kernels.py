@@ -59,7 +59,9 @@ def test_gemv_routing(backend, pkg, ora):
                                    (128, 128, 64), (200, 2304, 768), (513, 130, 37),
                                    # small m: K split over the part (decode's GEMVs)
                                    (1, 768, 3072), (1, 2304, 768), (5, 3072, 768), (1, 3, 5),
-                                   (1, 1000, 1), (17, 768, 768)])
+                                   (1, 1000, 1), (17, 768, 768),
+                                   # prompt-sized m: K split where the tiles are few
+                                   (64, 768, 3072), (64, 2304, 768), (512, 768, 3072)])
 def test_matmul_and_add(backend, pkg, ora, m, n, k):
     h = pkg.hip
     a, b = ora.rand_vec(m * k, 1), ora.rand_vec(k * n, 2)
@@ -109,6 +111,38 @@ def test_small_m_matmul_k_split_live_meta(backend, pkg, ora):
         tb = backend.tensor(b[: k * n].copy())
         am = a.reshape(M, K)[:m, :k].copy().ravel()
         tam = backend.tensor(am)
+        meta = _meta(backend, h.MatMulMeta(m, n, k))
+        outs = []
+        for _ in range(2):
+            c = backend.tensor(np.full(M * N, 7.0, np.float32))
+            backend.matmul(tam, tb, c, rec, meta)
+            outs.append(c.download())
+        cadd = backend.tensor(c0)
+        backend.matmul_add(tam, tb, cadd, rec, meta)
+        ref = ora.matmul(am, b[: k * n], m, n, k)
+        tol = 1e-4 * max(1.0, np.sqrt(k / 19.0))
+        assert np.abs(outs[0][: m * n] - ref).max() < tol, (m, n, k)
+        assert np.all(outs[0][m * n:] == 7.0)
+        assert np.array_equal(outs[0], outs[1])
+        got = cadd.download()
+        assert np.abs(got[: m * n] - ora.matmul_add(am, b[: k * n], c0[: m * n], m, n, k)).max() < tol
+        assert np.array_equal(got[m * n:], c0[m * n:])
+
+
+def test_prompt_m_matmul_k_split_live_meta(backend, pkg, ora):
+    # m > 32 on a grid of fewer tiles than CUs splits K over several blocks
+    # per tile, whose partial sums the tile's last block adds.  Live metas
+    # shrink m, n and k under the recorded shape's grid and splits, so some
+    # splits get no rows and some tiles no rows or columns; repeated calls
+    # reuse the workspace and counters and give the same bits.
+    h = pkg.hip
+    M, N, K = 100, 768, 3072
+    a, b = ora.rand_vec(M * K, 21), ora.rand_vec(K * N, 22)
+    c0 = ora.rand_vec(M * N, 23)
+    rec = h.MatMulMeta(M, N, K)
+    for m, n, k in ((100, 768, 3072), (70, 500, 1000), (33, 129, 40), (100, 768, 3072)):
+        am = a.reshape(M, K)[:m, :k].copy().ravel()
+        tam, tb = backend.tensor(am), backend.tensor(b[: k * n].copy())
         meta = _meta(backend, h.MatMulMeta(m, n, k))
         outs = []
         for _ in range(2):
