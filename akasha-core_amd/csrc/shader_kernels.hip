@@ -37,21 +37,45 @@ __global__ void k_embedding(const uint32_t* tokens, const float* table,
 }
 
 // RMSNORM (src/shaders/cpu.rs:205-222), one 256-thread block per row:
-// y = x * (1 / sqrt(sum(x^2) / size + eps)) * w.
+// y = x * (1 / sqrt(sum(x^2) / size + eps)) * w.  Rows of up to 1024 are held
+// in registers, their x and w loaded together; each thread sums its columns
+// c, c + 256, ... in that order either way.
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* x,
                                                  const float* w, float* out,
                                                  const akh_norm_meta* meta) {
+  constexpr uint32_t U = 4;
   __shared__ float red4[4];
   const uint32_t r = blockIdx.x;
   if (r >= meta->seq_len) return;
   const uint32_t size = meta->size;
   const float* xr = x + (size_t)r * size;
+  float* yr = out + (size_t)r * size;
+  if (size <= 256 * U) {
+    float xv[U], wv[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t c = threadIdx.x + 256 * u;
+      xv[u] = c < size ? xr[c] : 0.f;
+      wv[u] = c < size ? w[c] : 0.f;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) ss += xv[u] * xv[u];
+    ss = block_sum256(ss, red4);
+    const float rs = 1.0f / sqrtf(ss / (float)size + meta->eps);
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t c = threadIdx.x + 256 * u;
+      if (c < size) yr[c] = __fmul_rn(__fmul_rn(xv[u], rs), wv[u]);
+    }
+    return;
+  }
   float ss = 0.f;
   for (uint32_t c = threadIdx.x; c < size; c += 256) ss += xr[c] * xr[c];
   ss = block_sum256(ss, red4);
   const float rs = 1.0f / sqrtf(ss / (float)size + meta->eps);
   for (uint32_t c = threadIdx.x; c < size; c += 256)
-    out[(size_t)r * size + c] = __fmul_rn(__fmul_rn(xr[c], rs), w[c]);
+    yr[c] = __fmul_rn(__fmul_rn(xr[c], rs), w[c]);
 }
 
 // MATMUL / GEMV and MATMUL_ADD / GEMV_ADD for m <= 32 (the reference routes
@@ -258,29 +282,77 @@ __global__ void k_cache_write(const float* src, float* dst,
     dst[(size_t)off * width + i] = src[i];
 }
 
-// ATTN_QK_CACHED (src/shaders/cpu.rs:144-162): one thread per (row, head).
-__global__ void k_attn_qk_cached(const float* q, const float* kc,
-                                 float* scores,
-                                 const akh_attn_cached_meta* meta) {
+// ATTN_QK_CACHED (src/shaders/cpu.rs:144-162): scores[h][j] = q_h . K[j]_h
+// for j < attn_len.  Sixteen lanes per (row, head): lane l takes columns
+// l, l + 16, ... of the head, up to eight of them loaded before any is
+// summed (one memory round trip per 128 columns), and the sixteen partial
+// sums meet by lane exchanges.  A block of 256 threads takes 16 rows.
+__global__ __launch_bounds__(256) void k_attn_qk_cached(const float* q, const float* kc,
+                                                        float* scores,
+                                                        const akh_attn_cached_meta* meta) {
   const uint32_t len = meta->attn_len, dim = meta->dim, hd = meta->head_dim;
-  const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x, h = blockIdx.y;
-  if (j >= len || h >= dim / hd) return;
+  const uint32_t sub = threadIdx.x & 15;
+  const uint32_t j = blockIdx.x * 16 + (threadIdx.x >> 4), h = blockIdx.y;
+  if (blockIdx.x * 16 >= len || h >= dim / hd) return;  // whole block
+  const bool live = j < len;
   const float* qh = q + h * hd;
-  const float* kr = kc + (size_t)j * dim + h * hd;
+  const float* kr = kc + (size_t)(live ? j : 0) * dim + h * hd;
   float s = 0.f;
-  for (uint32_t c = 0; c < hd; ++c) s += qh[c] * kr[c];
-  scores[(size_t)h * len + j] = s;
+  for (uint32_t c0 = 0; c0 < hd; c0 += 128) {
+    float kv[8], qv[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+      const uint32_t c = c0 + sub + 16 * u;
+      const bool ok = live && c < hd;
+      kv[u] = ok ? kr[c] : 0.f;
+      qv[u] = ok ? qh[c] : 0.f;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) s = fmaf(qv[u], kv[u], s);
+  }
+  s += __shfl_xor(s, 8, 64);
+  s += __shfl_xor(s, 4, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 1, 64);
+  if (live && sub == 0) scores[(size_t)h * len + j] = s;
 }
 
-// SOFTMAX_RECT (src/shaders/cpu.rs:180-203), one block per row.
+// SOFTMAX_RECT (src/shaders/cpu.rs:180-203), one block per row; rows of up
+// to 1024 stay in registers between the passes.
 __global__ __launch_bounds__(256) void k_softmax_rect(
     float* x, const akh_softmax_rect_meta* meta) {
+  constexpr uint32_t U = 4;
   __shared__ float red4[4];
   const uint32_t r = blockIdx.x;
   if (r >= meta->num_rows) return;
   const uint32_t width = meta->width;
   const float scale = meta->scale;
   float* row = x + (size_t)r * width;
+  if (width <= 256 * U) {
+    float v[U];
+    float mx = -INFINITY;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = threadIdx.x + 256 * u;
+      v[u] = i < width ? row[i] * scale : -INFINITY;
+      mx = fmaxf(mx, v[u]);
+    }
+    mx = block_max256(mx, red4);
+    float sum = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = threadIdx.x + 256 * u;
+      v[u] = i < width ? expf(v[u] - mx) : 0.f;
+      sum += v[u];
+    }
+    sum = block_sum256(sum, red4);
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = threadIdx.x + 256 * u;
+      if (i < width) row[i] = v[u] / sum;
+    }
+    return;
+  }
   float mx = -INFINITY;
   for (uint32_t i = threadIdx.x; i < width; i += 256)
     mx = fmaxf(mx, row[i] * scale);
@@ -295,16 +367,42 @@ __global__ __launch_bounds__(256) void k_softmax_rect(
   for (uint32_t i = threadIdx.x; i < width; i += 256) row[i] = row[i] / sum;
 }
 
-// ATTN_AV_CACHED (src/shaders/cpu.rs:164-178): one thread per channel.
-__global__ void k_attn_av_cached(const float* p, const float* vc, float* out,
-                                 const akh_attn_cached_meta* meta) {
+// ATTN_AV_CACHED (src/shaders/cpu.rs:164-178): out[d] = sum_j p[h(d)][j] V[j][d].
+// A block of 512 threads takes 64 channels: wave w sums rows w, w + 8, ...
+// with 16 rows' loads in flight per lane (one memory round trip per 128
+// rows), and the eight waves' sums meet in LDS in wave order.
+__global__ __launch_bounds__(512) void k_attn_av_cached(const float* p, const float* vc,
+                                                        float* out,
+                                                        const akh_attn_cached_meta* meta) {
+  constexpr uint32_t W = 8, U = 16;
+  __shared__ float part[W][64];
   const uint32_t len = meta->attn_len, dim = meta->dim, hd = meta->head_dim;
-  const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
-  if (d >= dim) return;
-  const float* ph = p + (size_t)(d / hd) * len;
+  const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t d = blockIdx.x * 64 + lane;
+  const bool live = d < dim;
+  const float* ph = p + (size_t)(live ? d / hd : 0) * len;
+  const float* vd = vc + (live ? d : 0);
   float s = 0.f;
-  for (uint32_t j = 0; j < len; ++j) s += ph[j] * vc[(size_t)j * dim + d];
-  out[d] = s;
+  for (uint32_t j0 = w; j0 < len; j0 += W * U) {
+    float pv[U], vv[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t j = j0 + W * u;
+      const bool ok = live && j < len;
+      pv[u] = ok ? ph[j] : 0.f;
+      vv[u] = ok ? vd[(size_t)j * dim] : 0.f;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) s = fmaf(pv[u], vv[u], s);
+  }
+  part[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && live) {
+    float t = part[0][lane];
+#pragma unroll
+    for (uint32_t i = 1; i < W; ++i) t += part[i][lane];
+    out[d] = t;
+  }
 }
 
 // SILU (src/shaders/cpu.rs:63-69).
@@ -455,8 +553,9 @@ hipError_t shader_attn_qk_cached(const float* q, const float* kc,
                                  uint32_t max_attn_len,
                                  const akh_attn_cached_meta* meta,
                                  hipStream_t s) {
+  if (max_attn_len == 0 || num_heads == 0) return hipSuccess;
   hipLaunchKernelGGL(k_attn_qk_cached,
-                     dim3((max_attn_len + 255) / 256, num_heads), dim3(256), 0,
+                     dim3((max_attn_len + 15) / 16, num_heads), dim3(256), 0,
                      s, q, kc, scores, meta);
   return hipGetLastError();
 }
@@ -474,7 +573,8 @@ hipError_t shader_attn_av_cached(const float* scores, const float* vc,
                                  float* out, uint32_t dim,
                                  const akh_attn_cached_meta* meta,
                                  hipStream_t s) {
-  hipLaunchKernelGGL(k_attn_av_cached, dim3((dim + 255) / 256), dim3(256), 0,
+  if (dim == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_attn_av_cached, dim3((dim + 63) / 64), dim3(512), 0,
                      s, scores, vc, out, meta);
   return hipGetLastError();
 }
