@@ -81,12 +81,14 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x,
 // MATMUL / GEMV and MATMUL_ADD / GEMV_ADD for m <= 32 (the reference routes
 // m == 1 to GEMV, emit.rs:31-33): C[m, n] (+)= A[m, k] B[k, n].
 //
-// B streams once over the whole part.  A block takes a slab of 32 columns
-// and one of `splits` ranges of `kchunk` rows of B.  Thread t reads row
-// t / 8 of each 32-row round and columns 4 (t % 8) .. + 3 of it (one 16-byte
-// load where B and N allow, so a wave's load is 1 KB of eight rows), with
-// GR rounds in flight; it keeps the sums of up to MR rows of A.  The 32 row
-// lanes of each column meet through lane exchanges and LDS.  With one split
+// B streams once over the whole part.  A block takes a slab of 4 CG columns
+// and one of `splits` ranges of `kchunk` rows of B.  With 16-byte rows
+// (CG = 8), thread t reads row t / 8 of each 32-row round and columns
+// 4 (t % 8) .. + 3 of it with one 16-byte load, so a wave's load is 1 KB of
+// eight rows; other rows take lane-adjacent columns (LC: t % CG + CG c), so
+// a load instruction reads whole runs of a row.  GR rounds are in flight;
+// a thread keeps the sums of up to MR rows of A.  The row lanes of each
+// column meet through lane exchanges and LDS.  With one split
 // the block writes C.  Otherwise it writes its partial sums to the
 // workspace (through to device scope), waits for them to complete and counts
 // itself; the last block of the slab adds the partials in split order (the
@@ -109,32 +111,38 @@ struct GemvParams {
   int vec;  // B 16-byte aligned and the recorded N a multiple of 4
 };
 
-template <int MR>
+template <int MR, int CG, bool LC>
 __global__ __launch_bounds__(256) void k_shader_gemv(GemvParams g) {
 #ifndef AKH_GEMV_GR
 #define AKH_GEMV_GR 4
 #endif
-  constexpr int GR = MR > 4 ? 2 : AKH_GEMV_GR;  // 32-row rounds in flight
-  __shared__ float red[4][MR][32];
+  constexpr int SW = 4 * CG;    // slab columns
+  constexpr int RL = 256 / CG;  // row lanes of the block
+  constexpr int GR = MR > 4 ? 2 : AKH_GEMV_GR;  // rounds of RL rows in flight
+  __shared__ float red[4][MR][SW];
   __shared__ int last_block;
   const int M = min((int)g.meta->m, min(g.mrec, MR)), N = min((int)g.meta->n, g.nrec);
   const int K = (int)g.meta->k;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int n0 = blockIdx.x * 32;
+  const int n0 = blockIdx.x * SW;
   if (n0 >= N || M <= 0) return;  // the whole slab: no block of it counts
-  const int rl = tid >> 3, nc = n0 + 4 * (tid & 7);
+  // Thread columns: four adjacent ones (one 16-byte load), or with LC the
+  // columns n0 + t % CG + CG c, so a load instruction's lanes read adjacent
+  // words of a row (rows whose 16-byte pieces straddle cache lines).
+  const int rl = tid / CG, nc = LC ? n0 + tid % CG : n0 + 4 * (tid % CG);
+  constexpr int CS = LC ? CG : 1;  // column step between a thread's columns
   const int k0 = min(K, blockIdx.y * g.kchunk), k1 = min(K, k0 + g.kchunk);
-  const bool vec = g.vec && N % 4 == 0;
+  const bool vec = !LC && g.vec && N % 4 == 0;
   float acc[MR][4];
 #pragma unroll
   for (int m = 0; m < MR; ++m)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[m][c] = 0.f;
-  for (int kg = k0 + rl; kg < k1; kg += 32 * GR) {
+  for (int kg = k0 + rl; kg < k1; kg += RL * GR) {
     float w[GR][4];
 #pragma unroll
     for (int u = 0; u < GR; ++u) {
-      const int k = kg + 32 * u;
+      const int k = kg + RL * u;
       const bool ok = k < k1 && nc < N;
       const float* src = g.b + (size_t)(ok ? k : 0) * N + (ok ? nc : 0);
       if (vec) {
@@ -145,7 +153,7 @@ __global__ __launch_bounds__(256) void k_shader_gemv(GemvParams g) {
         w[u][3] = t.w;
       } else {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) w[u][c] = ok && nc + c < N ? src[c] : 0.f;
+        for (int c = 0; c < 4; ++c) w[u][c] = ok && nc + CS * c < N ? src[CS * c] : 0.f;
       }
     }
 #pragma unroll
@@ -154,37 +162,36 @@ __global__ __launch_bounds__(256) void k_shader_gemv(GemvParams g) {
       const float* ar = g.a + (size_t)m * K;
 #pragma unroll
       for (int u = 0; u < GR; ++u) {
-        const int k = kg + 32 * u;
+        const int k = kg + RL * u;
         const float x = k < k1 ? ar[k] : 0.f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[m][c] = fmaf(x, w[u][c], acc[m][c]);
       }
     }
   }
-  // Rows: the wave's eight row lanes of each column (lane bits 3..5), then
-  // the four waves through LDS.  Thread t < 32 then holds column n0 + t.
+  // Rows: the wave's row lanes of each column (lanes CG, 2 CG, ... apart),
+  // then the four waves through LDS.  Thread t < SW then holds column n0 + t.
 #pragma unroll
   for (int m = 0; m < MR; ++m)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float v = acc[m][c];
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
+#pragma unroll
+      for (int o = CG; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
       acc[m][c] = v;
     }
-  if (lane < 8)
+  if (lane < CG)
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) red[wave][m][4 * lane + c] = acc[m][c];
+      for (int c = 0; c < 4; ++c) red[wave][m][LC ? lane + CG * c : 4 * lane + c] = acc[m][c];
   __syncthreads();
   const int n = n0 + tid;
-  const bool col = tid < 32 && n < N;
+  const bool col = tid < SW && n < N;
   float tot[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    const int t = tid & 31;
+    const int t = tid % SW;
     tot[m] = ((red[0][m][t] + red[1][m][t]) + red[2][m][t]) + red[3][m][t];
   }
   if (g.splits == 1) {
@@ -453,7 +460,7 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
                          int accumulate, float* ws, int* cnt, hipStream_t s) {
   if (shape.m == 0 || shape.n == 0) return hipSuccess;
   if (shape.m <= 32u) {
-    // 32-column slabs over at most 8 ranges of K (at least 128 rows each),
+    // Column slabs over at most 8 ranges of K (at least 128 rows each),
     // about 256 blocks where the slabs are fewer.
 #ifndef AKH_GEMV_TARGET
 #define AKH_GEMV_TARGET 256
@@ -466,7 +473,17 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
 #endif
     GemvParams g{a, b, c, meta, accumulate, (int)shape.m, (int)shape.n, 1, 1, ws, cnt, 0};
     g.vec = shape.n % 4 == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0;
-    const int slabs = (int)((shape.n + 31) / 32), K = (int)shape.k;
+    // Rows that are not whole 16-byte pieces take lane-adjacent columns, for
+    // m <= 4 in the widest slabs (up to 256 columns) that still number 128:
+    // measured at m = 1, K = 768, N = 50257 took 47.7 us on 32-column slabs
+    // of four adjacent columns per lane and 29.1 us on 256-column ones, and
+    // N = 771 9.4 us at 256 columns, 5.8 us at 64.
+    int cg = 8;
+    if (!g.vec && shape.m <= 4u) {
+      cg = 64;
+      while (cg > 16 && (shape.n + 4 * cg - 1) / (4 * cg) < 128) cg /= 2;
+    }
+    const int slabs = (int)((shape.n + 4 * cg - 1) / (4 * cg)), K = (int)shape.k;
     int splits = std::min(AKH_GEMV_SMAX, std::max(1, (AKH_GEMV_TARGET + slabs - 1) / slabs));
     splits = std::min(splits, std::max(1, K / AKH_GEMV_KMIN));
     if (!ws || !cnt || slabs > kGemvSlabs) splits = 1;
@@ -475,12 +492,24 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
     g.kchunk = std::max(1, (K + splits - 1) / splits);
     g.splits = std::max(1, (K + g.kchunk - 1) / g.kchunk);
     const dim3 grid(slabs, g.splits);
-    if (shape.m == 1)
-      hipLaunchKernelGGL(k_shader_gemv<1>, grid, dim3(256), 0, s, g);
-    else if (shape.m <= 4)
-      hipLaunchKernelGGL(k_shader_gemv<4>, grid, dim3(256), 0, s, g);
-    else
-      hipLaunchKernelGGL(k_shader_gemv<32>, grid, dim3(256), 0, s, g);
+#define AKH_GEMV_GO(MR, CG, LC) \
+  hipLaunchKernelGGL((k_shader_gemv<MR, CG, LC>), grid, dim3(256), 0, s, g)
+    if (g.vec) {
+      if (shape.m == 1) AKH_GEMV_GO(1, 8, false);
+      else if (shape.m <= 4) AKH_GEMV_GO(4, 8, false);
+      else AKH_GEMV_GO(32, 8, false);
+    } else if (shape.m > 4) {
+      AKH_GEMV_GO(32, 8, true);
+    } else if (cg == 8) {
+      if (shape.m == 1) AKH_GEMV_GO(1, 8, true); else AKH_GEMV_GO(4, 8, true);
+    } else if (cg == 16) {
+      if (shape.m == 1) AKH_GEMV_GO(1, 16, true); else AKH_GEMV_GO(4, 16, true);
+    } else if (cg == 32) {
+      if (shape.m == 1) AKH_GEMV_GO(1, 32, true); else AKH_GEMV_GO(4, 32, true);
+    } else {
+      if (shape.m == 1) AKH_GEMV_GO(1, 64, true); else AKH_GEMV_GO(4, 64, true);
+    }
+#undef AKH_GEMV_GO
     return hipGetLastError();
   }
   GemmParams p{};

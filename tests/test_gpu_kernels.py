@@ -60,6 +60,8 @@ def test_gemv_routing(backend, pkg, ora):
                                    # small m: K split over the part (decode's GEMVs)
                                    (1, 768, 3072), (1, 2304, 768), (5, 3072, 768), (1, 3, 5),
                                    (1, 1000, 1), (17, 768, 768),
+                                   # rows not whole 16-byte pieces: lane-adjacent columns
+                                   (1, 50257, 768), (4, 1001, 513),
                                    # prompt-sized m: K split where the tiles are few
                                    (64, 768, 3072), (64, 2304, 768), (512, 768, 3072)])
 def test_matmul_and_add(backend, pkg, ora, m, n, k):
