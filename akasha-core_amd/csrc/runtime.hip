@@ -12,8 +12,10 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <string>
 #include <cstring>
+#include <unordered_map>
 #include <vector>
 
 #include "akasha_hip.h"
@@ -69,6 +71,22 @@ struct akh_backend {
   // (allocated with the backend, so graph capture never has to).
   float* gemv_ws = nullptr;
   int* gemv_cnt = nullptr;
+  // Tensor memory.  Every use of a tensor is on the backend's one stream, so
+  // allocation, upload and free are ordered on it instead of waiting for it:
+  // a freed block is kept (up to kPoolCap bytes) and handed out again zeroed
+  // by a fill queued behind the work that used it before; an upload of up to
+  // kStageSlot bytes is copied into a pinned slot and queued, the slot reused
+  // once its copy has run.
+  static constexpr size_t kPoolCap = (size_t)8 << 30;
+  static constexpr int kStageSlots = 64;
+  static constexpr size_t kStageSlot = 64 << 10;
+  std::multimap<size_t, void*> pool;        // capacity -> free block
+  std::unordered_map<void*, size_t> owned;  // block handed out -> capacity
+  size_t pool_bytes = 0;
+  char* stage = nullptr;
+  hipEvent_t stage_done[kStageSlots] = {};
+  bool stage_busy[kStageSlots] = {};
+  int stage_next = 0;
 };
 
 namespace {
@@ -86,6 +104,18 @@ akh_status backend_scratch(akh_backend* be, size_t bytes, void** out) {
   }
   *out = be->scratch;
   return AKH_OK;
+}
+
+// Returns the pooled blocks to HIP (after the stream has drained).
+hipError_t pool_release(akh_backend* be) {
+  hipError_t e = hipStreamSynchronize(be->stream);
+  for (auto& kv : be->pool) {
+    hipError_t f = hipFree(kv.second);
+    if (e == hipSuccess) e = f;
+  }
+  be->pool.clear();
+  be->pool_bytes = 0;
+  return e;
 }
 
 }  // namespace
@@ -121,6 +151,11 @@ extern "C" akh_status akh_backend_new(int device, akh_backend** out) {
   if (e == hipSuccess) e = hipMalloc(&be->gemv_ws, kGemvWsFloats * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&be->gemv_cnt, kGemvSlabs * sizeof(int));
   if (e == hipSuccess) e = hipMemset(be->gemv_cnt, 0, kGemvSlabs * sizeof(int));
+  if (e == hipSuccess)
+    e = hipHostMalloc(reinterpret_cast<void**>(&be->stage),
+                      akh_backend::kStageSlots * akh_backend::kStageSlot, hipHostMallocDefault);
+  for (int i = 0; e == hipSuccess && i < akh_backend::kStageSlots; ++i)
+    e = hipEventCreateWithFlags(&be->stage_done[i], hipEventDisableTiming);
   if (e != hipSuccess) {
     akh_backend_free(be);
     return fail(AKH_E_HIP, std::string("akh_backend_new: ") + hipGetErrorString(e));
@@ -138,6 +173,10 @@ extern "C" void akh_backend_free(akh_backend* be) {
   if (be->scratch) hipFree(be->scratch);
   if (be->gemv_ws) hipFree(be->gemv_ws);
   if (be->gemv_cnt) hipFree(be->gemv_cnt);
+  if (be->stream) pool_release(be);
+  for (hipEvent_t ev : be->stage_done)
+    if (ev) hipEventDestroy(ev);
+  if (be->stage) hipHostFree(be->stage);
   if (be->stream) hipStreamDestroy(be->stream);
   delete be;
 }
@@ -154,14 +193,31 @@ extern "C" akh_status akh_tensor_alloc(akh_backend* be, size_t bytes,
   CHECK_ARG(be && dev, "akh_tensor_alloc: NULL argument");
   CHECK_ARG(!be->capturing, "akh_tensor_alloc: graph capture in progress");
   *dev = nullptr;
+  const size_t want = bytes ? bytes : 4;
   void* p = nullptr;
-  HIP_TRY(hipMalloc(&p, bytes ? bytes : 4));
-  hipError_t e = hipMemsetAsync(p, 0, bytes ? bytes : 4, be->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
+  size_t cap = want;
+  // A pooled block of at least `want` bytes and at most twice that.
+  auto it = be->pool.lower_bound(want);
+  if (it != be->pool.end() && it->first <= 2 * want) {
+    cap = it->first;
+    p = it->second;
+    be->pool_bytes -= cap;
+    be->pool.erase(it);
+  } else {
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess && !be->pool.empty()) {  // give the pool back, retry
+      (void)hipGetLastError();
+      HIP_TRY(pool_release(be));
+      e = hipMalloc(&p, want);
+    }
+    if (e != hipSuccess) return fail(AKH_E_HIP, std::string("akh_tensor_alloc: ") + hipGetErrorString(e));
+  }
+  hipError_t e = hipMemsetAsync(p, 0, want, be->stream);
   if (e != hipSuccess) {
     hipFree(p);
     return fail(AKH_E_HIP, std::string("akh_tensor_alloc: ") + hipGetErrorString(e));
   }
+  be->owned[p] = cap;
   *dev = p;
   return AKH_OK;
 }
@@ -170,6 +226,14 @@ extern "C" akh_status akh_tensor_free(akh_backend* be, void* dev) {
   CHECK_ARG(be, "akh_tensor_free: backend is NULL");
   CHECK_ARG(!be->capturing, "akh_tensor_free: graph capture in progress");
   if (!dev) return AKH_OK;
+  auto it = be->owned.find(dev);
+  if (it != be->owned.end() && be->pool_bytes + it->second <= akh_backend::kPoolCap) {
+    be->pool.emplace(it->second, dev);
+    be->pool_bytes += it->second;
+    be->owned.erase(it);
+    return AKH_OK;
+  }
+  if (it != be->owned.end()) be->owned.erase(it);
   HIP_TRY(hipStreamSynchronize(be->stream));
   HIP_TRY(hipFree(dev));
   return AKH_OK;
@@ -181,6 +245,17 @@ extern "C" akh_status akh_tensor_upload(akh_backend* be, void* dev,
             "akh_tensor_upload: NULL argument");
   CHECK_ARG(!be->capturing, "akh_tensor_upload: graph capture in progress");
   if (!bytes) return AKH_OK;
+  if (bytes <= akh_backend::kStageSlot) {
+    const int i = be->stage_next;
+    be->stage_next = (i + 1) % akh_backend::kStageSlots;
+    if (be->stage_busy[i]) HIP_TRY(hipEventSynchronize(be->stage_done[i]));
+    char* slot = be->stage + (size_t)i * akh_backend::kStageSlot;
+    memcpy(slot, host, bytes);
+    HIP_TRY(hipMemcpyAsync(dev, slot, bytes, hipMemcpyHostToDevice, be->stream));
+    HIP_TRY(hipEventRecord(be->stage_done[i], be->stream));
+    be->stage_busy[i] = true;
+    return AKH_OK;
+  }
   HIP_TRY(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, be->stream));
   HIP_TRY(hipStreamSynchronize(be->stream));
   return AKH_OK;

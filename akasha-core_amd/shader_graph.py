@@ -5,10 +5,10 @@ A restatement of what akasha-core's emitters do when the backend is HIP:
 InferenceSession::decode_step (src/nn/inference_graphs.rs:13-196, 339-509;
 src/nn/inference.rs:178-262): the graph is captured once, with constant and
 dynamic metas in device memory, and replayed every step after the four
-dynamic metas are rewritten.  ``shader_prefill`` mirrors build_prefill_layer
-(inference_graphs.rs:198-337) + InferenceSession::prefill
-(inference.rs:61-176).  Every node is one launcher of include/akasha_hip.h
-with buffers in binding-slot order.
+dynamic metas are rewritten.  ``shader_prefill`` and ``ShaderDecoder.prefill``
+mirror build_prefill_layer (inference_graphs.rs:198-337) +
+InferenceSession::prefill (inference.rs:61-176).  Every node is one launcher
+of include/akasha_hip.h with buffers in binding-slot order.
 """
 
 import numpy as np
@@ -96,6 +96,23 @@ class ShaderDecoder:
                 if isinstance(t, self.hip.DeviceTensor):
                     t.free()
 
+    def prefill(self, tokens):
+        """InferenceSession::prefill into this decoder's caches (inference.rs:
+        61-176, which generate runs on an empty cache, inference.rs:288-289):
+        the prompt's rows through the per-shader prefill graph; returns the
+        last row's logits, and decode steps continue at position len(tokens)."""
+        assert self.cur_len == 0 and 0 < len(tokens) <= self.max_ctx
+        logits = _prefill_nodes(self.hip, self.be, self.cfg, self.w, tokens,
+                                self.k_cache, self.v_cache)
+        out = logits.download()
+        self.cur_len = len(tokens)
+        return out
+
+    def reset(self):
+        """An empty cache again (cur_len = 0): the next prefill rewrites its
+        rows."""
+        self.cur_len = 0
+
     def decode_step(self, token):
         hip, be, c = self.hip, self.be, self.cfg
         pos = self.cur_len
@@ -115,58 +132,78 @@ class ShaderDecoder:
         return self.logits.download()
 
 
-def shader_prefill(hip, be, cfg, weights, tokens, max_ctx):
-    """One sequence through the per-shader prefill graph; returns last-row
-    logits and the per-layer K caches."""
+def _prefill_nodes(hip, be, cfg, w, tokens, kc, vc):
+    """The nodes of InferenceSession::prefill (inference.rs:61-176): the
+    embedding, build_prefill_layer per layer (inference_graphs.rs:198-337)
+    writing rows 0..S-1 of the caches kc / vc, then the last row's head
+    gather, final norm and lm_head.  Every intermediate tensor and meta is
+    allocated as the graph is built, as the reference's builder does; the
+    nodes run as they are issued (the reference executes its prefill graph
+    once).  The graph's tensors live until every node is queued (freeing
+    one waits for the stream).  Returns the logits tensor."""
     d, hd, F, V, L = cfg.dim, cfg.head_dim, cfg.ffn_hidden, cfg.vocab_size, cfg.num_layers
     S = len(tokens)
-    w = [be.tensor(np.ascontiguousarray(a, np.float32)) for a in weights]
-    tok = be.tensor(np.asarray(tokens, np.uint32))
-    hidden = be.zeros(S * d)
-    kc = [be.zeros(max_ctx * d) for _ in range(L)]
-    vc = [be.zeros(max_ctx * d) for _ in range(L)]
+    held = []
+
+    def keep(t):
+        held.append(t)
+        return t
+
+    tok = keep(be.tensor(np.asarray(tokens, np.uint32)))
+    hidden = keep(be.zeros(S * d))
     emb = hip.EmbeddingMeta(V, d, S)
-    be.embedding(tok, w[0], hidden, emb, be.meta(emb))
+    be.embedding(tok, w[0], hidden, emb, keep(be.meta(emb)))
     ns = hip.NormMeta(S, d, cfg.norm_eps)
     for l in range(L):
         n1, qkv, wo, n2, up, down = (w[1 + 6 * l + j] for j in range(6))
-        norm1 = be.zeros(S * d)
-        be.rmsnorm(hidden, n1, norm1, ns, be.meta(ns))
-        qkv_out = be.zeros(S * 3 * d)
+        norm1 = keep(be.zeros(S * d))
+        be.rmsnorm(hidden, n1, norm1, ns, keep(be.meta(ns)))
+        qkv_out = keep(be.zeros(S * 3 * d))
         mm = hip.MatMulMeta(S, 3 * d, d)
-        be.matmul(norm1, qkv, qkv_out, mm, be.meta(mm))
-        q, k, v = be.zeros(S * d), be.zeros(S * d), be.zeros(S * d)
+        be.matmul(norm1, qkv, qkv_out, mm, keep(be.meta(mm)))
+        q, k, v = keep(be.zeros(S * d)), keep(be.zeros(S * d)), keep(be.zeros(S * d))
         for buf, off in ((q, 0), (k, d), (v, 2 * d)):
             hm = hip.HeadMoveMeta(S, 3 * d, d, off)
-            be.head_gather(qkv_out, buf, hm, be.meta(hm))
+            be.head_gather(qkv_out, buf, hm, keep(be.meta(hm)))
         rm = hip.RopeMeta(S, d, hd, 0)
-        be.rope(q, rm, be.meta(rm))
-        be.rope(k, rm, be.meta(rm))
+        be.rope(q, rm, keep(be.meta(rm)))
+        be.rope(k, rm, keep(be.meta(rm)))
         cw = hip.CacheWriteMeta(S, d, 0)
-        be.cache_write(k, kc[l], cw, be.meta(cw))
-        be.cache_write(v, vc[l], cw, be.meta(cw))
-        attn = be.zeros(S * d)
-        lse = be.zeros(S * cfg.num_heads)
+        be.cache_write(k, kc[l], cw, keep(be.meta(cw)))
+        be.cache_write(v, vc[l], cw, keep(be.meta(cw)))
+        attn = keep(be.zeros(S * d))
+        lse = keep(be.zeros(S * cfg.num_heads))
         fm = hip.FlashAttnMeta(S, d, hd, np.float32(1.0) / np.sqrt(np.float32(hd)), 0)
-        be.flash_attention(q, k, v, attn, lse, fm, be.meta(fm))
+        be.flash_attention(q, k, v, attn, lse, fm, keep(be.meta(fm)))
         mo = hip.MatMulMeta(S, d, d)
-        be.matmul_add(attn, wo, hidden, mo, be.meta(mo))
-        norm2 = be.zeros(S * d)
-        be.rmsnorm(hidden, n2, norm2, ns, be.meta(ns))
-        ffn = be.zeros(S * F)
+        be.matmul_add(attn, wo, hidden, mo, keep(be.meta(mo)))
+        norm2 = keep(be.zeros(S * d))
+        be.rmsnorm(hidden, n2, norm2, ns, keep(be.meta(ns)))
+        ffn = keep(be.zeros(S * F))
         mu = hip.MatMulMeta(S, F, d)
-        be.matmul(norm2, up, ffn, mu, be.meta(mu))
+        be.matmul(norm2, up, ffn, mu, keep(be.meta(mu)))
         be.silu(ffn, S * F)
         md = hip.MatMulMeta(S, d, F)
-        be.matmul_add(ffn, down, hidden, md, be.meta(md))
-    last = be.zeros(d)
+        be.matmul_add(ffn, down, hidden, md, keep(be.meta(md)))
+    last = keep(be.zeros(d))
     hm = hip.HeadMoveMeta(1, d, d, (S - 1) * d)
-    be.head_gather(hidden, last, hm, be.meta(hm))
-    fo = be.zeros(d)
+    be.head_gather(hidden, last, hm, keep(be.meta(hm)))
+    fo = keep(be.zeros(d))
     n1m = hip.NormMeta(1, d, cfg.norm_eps)
-    be.rmsnorm(last, w[1 + 6 * L], fo, n1m, be.meta(n1m))
-    logits = be.zeros(V)
+    be.rmsnorm(last, w[1 + 6 * L], fo, n1m, keep(be.meta(n1m)))
+    logits = keep(be.zeros(V))
     lm = hip.MatMulMeta(1, V, d)
-    be.matmul(fo, w[2 + 6 * L], logits, lm, be.meta(lm))
+    be.matmul(fo, w[2 + 6 * L], logits, lm, keep(be.meta(lm)))
+    return logits
+
+
+def shader_prefill(hip, be, cfg, weights, tokens, max_ctx):
+    """One sequence through the per-shader prefill graph; returns last-row
+    logits and the per-layer K caches."""
+    d, L = cfg.dim, cfg.num_layers
+    w = [be.tensor(np.ascontiguousarray(a, np.float32)) for a in weights]
+    kc = [be.zeros(max_ctx * d) for _ in range(L)]
+    vc = [be.zeros(max_ctx * d) for _ in range(L)]
+    logits = _prefill_nodes(hip, be, cfg, w, tokens, kc, vc)
     be.synchronize()
     return logits.download(), [t.download().reshape(max_ctx, d) for t in kc]

@@ -86,7 +86,13 @@ const char* akh_last_error(void);
 int akh_abi_version(void);
 
 /* Tensor::init_from_cpu / copy_from_cpu / to_cpu (inference.rs:83,189,261).
- * akh_tensor_alloc returns zeroed device memory. */
+ * akh_tensor_alloc returns zeroed device memory.  Alloc, free and upload are
+ * ordered on the backend's stream and do not wait for it: the zeroing and
+ * the copy are queued behind the work already issued, a freed block (kept by
+ * the backend, up to 8 GB) is reused only by a later alloc, and an upload of
+ * up to 64 KB copies the host bytes out before it returns (larger ones wait
+ * for their copy).  Download waits for the stream.  So a tensor is used on
+ * the backend that made it, or after akh_synchronize. */
 akh_status akh_tensor_alloc(akh_backend* be, size_t bytes, void** dev);
 akh_status akh_tensor_free(akh_backend* be, void* dev);
 akh_status akh_tensor_upload(akh_backend* be, void* dev, const void* host,

@@ -27,6 +27,47 @@ def test_embedding(backend, pkg, ora):
     assert np.array_equal(got, ora.embedding(toks, table, vocab, dim, len(toks)))
 
 
+def test_tensor_reuse_is_ordered_on_the_stream(backend):
+    # A freed tensor's block is handed out again without waiting for the
+    # stream: the new tensor's zeroing is queued behind the kernels still
+    # writing the old one.
+    n = 1 << 24
+    old = backend.tensor(np.full(n, 2.0, np.float32))
+    addr = old.ptr.value
+    for _ in range(20):
+        backend.silu(old, n)
+    old.free()
+    new = backend.zeros(n)
+    assert new.ptr.value == addr
+    assert not new.download().any()
+    new.free()
+
+
+def test_uploads_are_staged_and_ordered(backend):
+    # Uploads return before the copy runs: the host array is copied out at
+    # once (changing it afterwards changes nothing), a kernel queued after an
+    # upload sees the data, and more uploads than staging slots all land.
+    a = np.linspace(-4, 4, 5000, dtype=np.float32)
+    t = backend.zeros(a.size)
+    host = a.copy()
+    t.upload(host)
+    host[:] = 7.0
+    backend.silu(t, a.size)
+    exp = a / (np.float32(1) + np.exp(-a))
+    np.testing.assert_allclose(t.download(), exp, rtol=2e-6, atol=1e-7)
+    rng = np.random.default_rng(3)
+    datas = [rng.standard_normal(1000 + 37 * i).astype(np.float32) for i in range(150)]
+    ts = [backend.zeros(d.size) for d in datas]
+    for x, d in zip(ts, datas):
+        x.upload(d)
+    for x, d in zip(ts, datas):
+        assert np.array_equal(x.download(), d)
+    big = rng.standard_normal(1 << 20).astype(np.float32)  # past one staging slot
+    tb = backend.zeros(big.size)
+    tb.upload(big)
+    assert np.array_equal(tb.download(), big)
+
+
 @pytest.mark.parametrize("rows,size", [(5, 96), (3, 768), (1, 32)])
 def test_rmsnorm(backend, pkg, ora, rows, size):
     h = pkg.hip
@@ -447,6 +488,28 @@ def test_shader_decode_graph_replays_with_live_metas(backend, pkg, ora):
         exp = ref.decode_step(t)
         assert np.abs(got - exp).max() < 1e-3
         assert int(np.argmax(got)) == ora.argmax(exp)
+
+
+@pytest.mark.parametrize("plen", [5, 37])
+def test_shader_generate_prefill_then_decode(backend, pkg, ora, plen):
+    # generate on an empty cache (inference.rs:264-326): the prompt through
+    # the per-shader prefill graph into the decoder's caches, then greedy
+    # decode steps through the captured decode graph from position plen.
+    # 5 rows run the small-m GEMV, 37 the MFMA GEMM with its K split.
+    from akasha_core_amd.shader_graph import ShaderDecoder
+    cfg = pkg.ModelConfig.new(97, 128, 2, 2, 48)
+    w = pkg.synthetic_weights(cfg, seed=9)
+    toks = [int(t) for t in ora.rand_tokens(plen, 97, 5)]
+    dec = ShaderDecoder(pkg.hip, backend, cfg, w, 48)
+    ref = ora.OracleSession(cfg, w, 48)
+    got, exp = dec.prefill(toks), ref.prefill(toks)
+    assert np.abs(got - exp).max() < 1e-3
+    for _ in range(6):
+        t = ora.argmax(exp)
+        assert int(np.argmax(got)) == t
+        got, exp = dec.decode_step(t), ref.decode_step(t)
+        assert np.abs(got - exp).max() < 1e-3
+    dec.close()
 
 
 def test_shader_prefill_graph(backend, pkg, ora):
