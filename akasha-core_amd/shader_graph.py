@@ -15,8 +15,13 @@ import numpy as np
 
 
 class ShaderDecoder:
-    def __init__(self, hip, backend, cfg, weights, max_ctx):
+    """With capture=False every decode step issues the same launchers
+    eagerly instead of replaying the captured graph (for tools that cannot
+    follow graph launches, such as kernel tracers)."""
+
+    def __init__(self, hip, backend, cfg, weights, max_ctx, capture=True):
         self.hip, self.be, self.cfg, self.max_ctx = hip, backend, cfg, max_ctx
+        self.capture = capture
         be, d, hd, H, F, V = backend, cfg.dim, cfg.head_dim, cfg.num_heads, cfg.ffn_hidden, cfg.vocab_size
         self.w = [be.tensor(np.ascontiguousarray(a, np.float32)) for a in weights]
         z = lambda n: be.zeros(n)  # noqa: E731
@@ -51,9 +56,13 @@ class ShaderDecoder:
         return self.w[i]
 
     def _build(self):
+        self.be.graph_begin()
+        self._nodes()
+        self.graph = self.be.graph_end()
+
+    def _nodes(self):
         hip, be, c = self.hip, self.be, self.cfg
         d, hd, H, F, V = c.dim, c.head_dim, c.num_heads, c.ffn_hidden, c.vocab_size
-        be.graph_begin()
         be.embedding(self.token, self._param(0), self.hidden, self.emb_shape, self.emb_meta)
         for l in range(c.num_layers):
             n1, qkv, wo, n2, up, down = (self._param(1 + 6 * l + j) for j in range(6))
@@ -84,7 +93,6 @@ class ShaderDecoder:
                    self.norm_meta)
         be.matmul(self.final_norm_out, self._param(2 + 6 * L), self.logits,
                   hip.MatMulMeta(1, V, d), self.lm_meta)
-        self.graph = be.graph_end()
 
     def close(self):
         """Release the graph and every device buffer this decoder holds."""
@@ -125,9 +133,12 @@ class ShaderDecoder:
         be.write_meta(self.attn_meta, hip.AttnCachedMeta(pos + 1, c.dim, hd))
         be.write_meta(self.sm_meta, hip.SoftmaxRectMeta(c.num_heads, pos + 1,
                                                         np.float32(1.0) / np.sqrt(np.float32(hd))))
-        if self.graph is None:
-            self._build()
-        self.graph.execute()
+        if not self.capture:
+            self._nodes()
+        else:
+            if self.graph is None:
+                self._build()
+            self.graph.execute()
         self.cur_len = pos + 1
         return self.logits.download()
 

@@ -500,7 +500,7 @@ def cpu_prefill_baseline(cfg, weights, tokens, threads):
     return len(tokens) / dt, dt
 
 
-def shader_graph_measurement(pkg, hip, be, cfg, weights, session_tokens):
+def shader_graph_measurement(pkg, hip, be, cfg, weights, session_tokens, capture=True):
     """Config 1 through the reference's per-shader decode graph: ShaderDecoder
     rebuilds build_decode_layer node for node from the C-ABI launchers (one
     launcher per shader, inference_graphs.rs:339-509), captures it once and
@@ -515,7 +515,7 @@ def shader_graph_measurement(pkg, hip, be, cfg, weights, session_tokens):
     This is what the reference's own emitter gets from the launchers, beside
     the session API's fused step."""
     import time
-    dec = pkg.shader_graph.ShaderDecoder(hip, be, cfg, weights, 128)
+    dec = pkg.shader_graph.ShaderDecoder(hip, be, cfg, weights, 128, capture=capture)
     prompt = [int(t) for t in pkg.synthetic_tokens(64, cfg.vocab_size, seed=1)]
     for _ in range(2):  # warm: first launches, and the backend's tensor pool
         dec.prefill(prompt)
@@ -534,22 +534,25 @@ def shader_graph_measurement(pkg, hip, be, cfg, weights, session_tokens):
         logits = dec.decode_step(toks[-1])
         toks.append(int(np.argmax(logits)))
     t3 = time.perf_counter()
-    be.synchronize()
-    be.timer_start()
-    for _ in range(16):
-        dec.graph.execute()
-    replay_ms = be.timer_stop() / 16
+    replay_ms = None
+    if capture:
+        be.synchronize()
+        be.timer_start()
+        for _ in range(16):
+            dec.graph.execute()
+        replay_ms = be.timer_stop() / 16
     L = cfg.num_layers
     out = {"workload": "config 1 through the per-shader graphs from the C-ABI launchers: the "
                        "64-token prompt through build_prefill_layer's nodes (allocated as "
                        "built, run once; median of 3 on a warm backend), then "
                        "build_decode_layer replayed as a hipGraph with live metas; logits "
                        "read back and argmax on the host each step",
-           "launches_per_step": 16 * L + 3,
+           "launches_per_step": 17 * L + 3,
            "prompt_prefill_ms": round(float(np.median(pre)) * 1e3, 3),
            "ms_per_token": round((t3 - t2) / 64 * 1e3, 3),
            "tok_s": round(64 / (t3 - t2), 1),
-           "graph_replay_ms": round(replay_ms, 3),
+           "graph_replay_ms": round(replay_ms, 3) if capture else None,
+           "decode": "graph replays" if capture else "eager launches (no capture)",
            "tokens_match_session": toks == session_tokens}
     dec.close()
     return out
@@ -662,6 +665,11 @@ def main():
     ap.add_argument("--config2-only", action="store_true",
                     help="measure only config 2's flash legs (8 per-node launches, then the "
                          "batched launch, 10 timed rounds each) and print them (for profiling)")
+    ap.add_argument("--shader-graph-only", action="store_true",
+                    help="run only config 1 through the per-shader graphs and print it")
+    ap.add_argument("--eager-shader", action="store_true",
+                    help="with --shader-graph-only: decode steps launch eagerly instead of "
+                         "replaying the captured graph (for kernel tracers)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the per-kernel decode legs, no graph replay (for counter "
                          "runs); config 5's too unless --no-scaled")
@@ -687,6 +695,12 @@ def main():
     log("bench: generating hall-1.0 weights (seed 0)")
     w = pkg.synthetic_weights(cfg, seed=0)
     be = hip.Backend(0)
+    if args.shader_graph_only:
+        out = shader_graph_measurement(pkg, hip, be, cfg, w, [], capture=not args.eager_shader)
+        out.pop("tokens_match_session")
+        print(json.dumps({"config1": {"shader_graph": out}}), flush=True)
+        be.close()
+        return
     model = hip.Model(be, cfg)
     model.upload(w)
     if args.prefill_only:

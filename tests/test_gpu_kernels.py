@@ -490,6 +490,20 @@ def test_shader_decode_graph_replays_with_live_metas(backend, pkg, ora):
         assert int(np.argmax(got)) == ora.argmax(exp)
 
 
+def test_shader_decode_eager_matches_graph(backend, pkg):
+    # The same launchers issued eagerly every step (capture=False) give the
+    # graph replay's logits bit for bit.
+    from akasha_core_amd.shader_graph import ShaderDecoder
+    cfg = pkg.ModelConfig.new(97, 64, 4, 2, 16)
+    w = pkg.synthetic_weights(cfg, seed=43)
+    g = ShaderDecoder(pkg.hip, backend, cfg, w, 16)
+    e = ShaderDecoder(pkg.hip, backend, cfg, w, 16, capture=False)
+    for t in [5, 9, 60, 2, 2]:
+        assert np.array_equal(g.decode_step(t), e.decode_step(t))
+    g.close()
+    e.close()
+
+
 @pytest.mark.parametrize("plen", [5, 37])
 def test_shader_generate_prefill_then_decode(backend, pkg, ora, plen):
     # generate on an empty cache (inference.rs:264-326): the prompt through
