@@ -428,6 +428,10 @@ struct SampleArgs {
   const double* uniform;     // [rows] draws in [0, 1)
   double* wbuf;              // scratch, sample_scratch_bytes(rows, n)
   uint32_t* out;             // [rows]
+  // Per-row arrival counters, zero between launches (kSampleCounters of
+  // them), or nullptr: with them a row sampled with 0 < top_k <= 256 may be
+  // split over several blocks whose last one merges the parts.
+  int* cnt;
 
   // Session mode (tok != nullptr), one round of InferenceSession::generate
   // (inference.rs:303-323) per launch.  A row with done[m] set is skipped
@@ -452,6 +456,7 @@ struct SampleArgs {
 };
 
 size_t sample_scratch_bytes(int rows, int n);
+constexpr int kSampleCounters = 4096;
 
 // The allocation-free sampler's workspace: a device array of
 // kNoAllocSampleElems doubles (rows * n at most), one copy per GPU.

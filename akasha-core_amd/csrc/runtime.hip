@@ -71,6 +71,8 @@ struct akh_backend {
   // (allocated with the backend, so graph capture never has to).
   float* gemv_ws = nullptr;
   int* gemv_cnt = nullptr;
+  // The sampler's per-row arrival counters (zero between launches).
+  int* sample_cnt = nullptr;
   // Tensor memory.  Every use of a tensor is on the backend's one stream, so
   // allocation, upload and free are ordered on it instead of waiting for it:
   // a freed block is kept (up to kPoolCap bytes) and handed out again zeroed
@@ -151,6 +153,8 @@ extern "C" akh_status akh_backend_new(int device, akh_backend** out) {
   if (e == hipSuccess) e = hipMalloc(&be->gemv_ws, kGemvWsFloats * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&be->gemv_cnt, kGemvSlabs * sizeof(int));
   if (e == hipSuccess) e = hipMemset(be->gemv_cnt, 0, kGemvSlabs * sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&be->sample_cnt, kSampleCounters * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(be->sample_cnt, 0, kSampleCounters * sizeof(int));
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&be->stage),
                       akh_backend::kStageSlots * akh_backend::kStageSlot, hipHostMallocDefault);
@@ -173,6 +177,7 @@ extern "C" void akh_backend_free(akh_backend* be) {
   if (be->scratch) hipFree(be->scratch);
   if (be->gemv_ws) hipFree(be->gemv_ws);
   if (be->gemv_cnt) hipFree(be->gemv_cnt);
+  if (be->sample_cnt) hipFree(be->sample_cnt);
   if (be->stream) pool_release(be);
   for (hipEvent_t ev : be->stage_done)
     if (ev) hipEventDestroy(ev);
@@ -555,7 +560,7 @@ namespace {
 akh_status sample_rows_into(akh_backend* be, const float* logits, uint32_t rows, uint32_t n,
                             akh_sampling params, const uint32_t* seen, uint32_t seen_stride,
                             const uint32_t* seen_len, const double* uniforms, uint32_t* out,
-                            double* wbuf);
+                            double* wbuf, int* cnt);
 }  // namespace
 
 extern "C" akh_status akh_sample_rows(akh_backend* be, const float* logits, uint32_t rows,
@@ -571,7 +576,7 @@ extern "C" akh_status akh_sample_rows(akh_backend* be, const float* logits, uint
   akh_status st = backend_scratch(be, sample_scratch_bytes((int)rows, (int)n), &wb);
   if (st != AKH_OK) return st;
   return sample_rows_into(be, logits, rows, n, params, seen, seen_stride, seen_len, uniforms,
-                          out, static_cast<double*>(wb));
+                          out, static_cast<double*>(wb), be->sample_cnt);
 }
 
 extern "C" akh_status akh_sample_rows_noalloc(akh_backend* be, const float* logits,
@@ -589,7 +594,7 @@ extern "C" akh_status akh_sample_rows_noalloc(akh_backend* be, const float* logi
             "akh_sample_rows_noalloc: seen needs seen_len");
   CHECK_ARG(be->noalloc_scratch, "akh_sample_rows_noalloc: no workspace on this device");
   return sample_rows_into(be, logits, rows, n, params, seen, seen_stride, seen_len, uniforms,
-                          out, be->noalloc_scratch);
+                          out, be->noalloc_scratch, nullptr);
 }
 
 namespace {
@@ -599,7 +604,7 @@ namespace {
 akh_status sample_rows_into(akh_backend* be, const float* logits, uint32_t rows, uint32_t n,
                             akh_sampling params, const uint32_t* seen, uint32_t seen_stride,
                             const uint32_t* seen_len, const double* uniforms, uint32_t* out,
-                            double* wbuf) {
+                            double* wbuf, int* cnt) {
   SampleArgs a{};
   a.logits = logits;
   a.n = (int)n;
@@ -614,6 +619,7 @@ akh_status sample_rows_into(akh_backend* be, const float* logits, uint32_t rows,
   a.uniform = uniforms;
   a.wbuf = wbuf;
   a.out = out;
+  a.cnt = cnt;
   HIP_TRY(launch_sample_rows(a, (int)rows, be->stream));
   return AKH_OK;
 }
@@ -1526,6 +1532,7 @@ hipError_t enqueue_generate_round(akh_session* s) {
   a.penalty = s->gparams.repetition_penalty;
   a.uniform = s->gparams.temperature > 0.0f ? s->guni : nullptr;
   a.wbuf = s->gwbuf;
+  a.cnt = s->be->sample_cnt;
   a.tok = s->tok;
   a.pos = s->pos;
   a.hist = s->hist;

@@ -18,8 +18,18 @@
 // is this implementation's choice).  The per-element weights live in a
 // scratch row; the repetition penalty is applied on the fly through a bitmap
 // of the seen ids in LDS.
+//
+// With 0 < top_k <= 1024 (run_chat's 40) only the top_k elements matter:
+// a cut on d = max - l admitting between top_k and 2048 elements is found
+// by counting against 16 thresholds per pass (powers of four, then 16-way
+// refinements), those elements are gathered to LDS and bitonic-sorted by
+// (logit descending, index ascending), and one thread takes the first top_k
+// through the reference's own sequence: f64 probabilities summed in order,
+// the top_p prefix, the walk r -= p.  NaN or infinite maxima, fewer than
+// top_k finite elements and ties too wide for the cut take the radix path.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "common.h"
@@ -182,43 +192,324 @@ __device__ uint32_t select_desc(int n, KeyFn key_of, const double* weights, doub
   return (uint32_t)n;
 }
 
+constexpr int KCAP = 1024;  // largest top_k of the candidate path
+constexpr int CCAP = 2048;  // candidates gathered for the sort
+constexpr int NTH = 16;     // thresholds counted per pass
+
+struct TopKShared {
+  unsigned long long comp[CCAP];  // key << 32 | ~index: descending = the order
+  unsigned long long top[KCAP];   // the first entries of that order
+  double prob[KCAP];
+  double norm;
+  int keep;
+  uint32_t wcnt[NW][NTH];
+  uint32_t cnt[NTH];
+  uint32_t n_cand;
+  uint32_t pick;
+};
+
+// The float whose order_key is k.
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// tk.top[0 .. min(nc, K)) = the first entries of tk.comp[0 .. nc) in
+// descending order (nc <= CCAP, K <= KCAP).  The entries are distinct (each
+// holds its element's index), so an entry's place is the number of entries
+// above it: every thread counts for its own entries, reading the others as
+// LDS broadcasts, with no barrier in between.
+__device__ int rank_top(int nc, int K, TopKShared& tk) {
+  for (int e = threadIdx.x; e < nc; e += NT) {
+    const unsigned long long x = tk.comp[e];
+    int above = 0;
+#pragma unroll 8
+    for (int f = 0; f < nc; ++f) above += tk.comp[f] > x ? 1 : 0;
+    if (above < K) tk.top[above] = x;
+  }
+  __syncthreads();
+  return min(nc, K);
+}
+
+// sampling.rs:45-80 over tk.top[0 .. top_k) in the reference's order: f64
+// probabilities, their sum folded in order (one thread), each divided by it,
+// the top_p prefix by the in-order running sum, its sum folded in order and
+// divided out, and the walk r -= p.  The divisions, independent per element,
+// run in parallel; the folds and the walk, whose order fixes the bits, on one
+// thread.
+__device__ uint32_t tail_topk(uint32_t top_k, float temperature, float top_p, double r,
+                              TopKShared& tk) {
+  const int K = (int)top_k;
+  const double mxd = (double)key_value((uint32_t)(tk.top[0] >> 32));
+  for (int t = threadIdx.x; t < K; t += NT)
+    tk.prob[t] = exp(((double)key_value((uint32_t)(tk.top[t] >> 32)) - mxd) / (double)temperature);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double sum = 0.0;
+    for (int t = 0; t < K; ++t) sum += tk.prob[t];
+    tk.norm = sum;
+  }
+  __syncthreads();
+  const double sum = tk.norm;
+  for (int t = threadIdx.x; t < K; t += NT) tk.prob[t] /= sum;
+  __syncthreads();
+  int len = K;
+  if (top_p < 1.0f) {
+    if (threadIdx.x == 0) {
+      double cum = 0.0;
+      int keep = K;
+      for (int t = 0; t < K; ++t) {
+        cum += tk.prob[t];
+        if (cum >= (double)top_p) {
+          keep = t + 1;
+          break;
+        }
+      }
+      double s2 = 0.0;
+      for (int t = 0; t < keep; ++t) s2 += tk.prob[t];
+      tk.keep = keep;
+      tk.norm = s2;
+    }
+    __syncthreads();
+    len = tk.keep;
+    const double s2 = tk.norm;
+    for (int t = threadIdx.x; t < len; t += NT) tk.prob[t] /= s2;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    auto idx_of = [&](int t) { return 0xFFFFFFFFu - (uint32_t)(tk.top[t] & 0xFFFFFFFFull); };
+    uint32_t pk = idx_of(len - 1);
+    double rr = r;
+    for (int t = 0; t < len; ++t) {
+      if (rr < tk.prob[t]) {
+        pk = idx_of(t);
+        break;
+      }
+      rr -= tk.prob[t];
+    }
+    tk.pick = pk;
+  }
+  __syncthreads();
+  return tk.pick;
+}
+
+// Calls f(l, i, live) for every index of the row in chunks of U elements per
+// thread, the chunk's loads issued before any is used; every thread makes
+// the same number of calls (live = i < n), so f may use wave-wide votes.
+constexpr int U = 8;
+template <typename LFn, typename F>
+__device__ __forceinline__ void for_row(int n, LFn l_of, F f) {
+  for (int c0 = 0; c0 < n; c0 += NT * U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = c0 + u * NT + (int)threadIdx.x;
+      v[u] = i < n ? l_of(i) : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = c0 + u * NT + (int)threadIdx.x;
+      f(v[u], i, i < n);
+    }
+  }
+}
+
+// Block sums of per-thread counts c[j] (plus base) -> tk.cnt.
+__device__ void reduce_counts(const uint32_t (&c)[NTH], uint32_t base, TopKShared& tk) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < NTH; ++j) {
+    uint32_t x = c[j];
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    if (lane == 0) tk.wcnt[w][j] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < NTH) {
+    uint32_t t = base;
+    for (int k = 0; k < NW; ++k) t += tk.wcnt[k][threadIdx.x];
+    tk.cnt[threadIdx.x] = t;
+  }
+  __syncthreads();
+}
+
+// The top_k elements of l_of(0 .. n) (0 < top_k <= KCAP) in order in
+// tk.top (index idx0 + i), from at most CCAP candidates gathered to tk.comp:
+// returns how many (top_k, or fewer with all_finite), or -1 where the radix path must decide instead
+// (NaN, an infinite maximum, fewer than top_k finite elements near the
+// maximum, ties too wide to cut).  With all_finite, fewer than top_k finite
+// elements near the maximum gathers every finite element instead (a part
+// of a row, which may hold fewer than top_k).  Every thread of the block
+// calls it; the outcome is the same for all.  The first count bins d =
+// max - l by its binary exponent (d < 2^(2j - 12) exactly when its
+// exponent is below 2j - 12), four packed 8-bit counters per chunk;
+// refinements compare only the elements inside the narrowed interval.
+template <typename LFn>
+__device__ int topk_candidates(int n, LFn l_of, uint32_t idx0, uint32_t top_k, bool all_finite,
+                               SampleShared& sh, TopKShared& tk) {
+  float mxv = -INFINITY;
+  uint32_t nan = 0;
+  for_row(n, l_of, [&](float l, int, bool) {
+    if (l != l) nan = 1;
+    else mxv = fmaxf(mxv, l);
+  });
+  const float mx = block_max_f(mxv, sh);
+  if (block_sum_u(nan, sh) != 0) return -1;
+  if (mx == -INFINITY && all_finite) return 0;  // a part with no finite element
+  if (!isfinite(mx)) return -1;
+
+  // Threshold t: 2^(2t - 12) in the first count, then (lo, hi] cut in NTH.
+  bool linear = false;
+  float lo = 0.0f, hi = 0.0f;
+  auto thr = [&](int t) {
+    return !linear ? ldexpf(1.0f, 2 * t - 12)
+                   : (t == NTH - 1 ? hi : lo + (hi - lo) * (float)(t + 1) / NTH);
+  };
+  {
+    uint32_t c[NTH];
+#pragma unroll
+    for (int j = 0; j < NTH; ++j) c[j] = 0u;
+    uint32_t h[4] = {0u, 0u, 0u, 0u};  // this chunk's bins (at most U per field)
+    int k = 0;
+    for_row(n, l_of, [&](float l, int, bool) {
+      const float d = mx - l;
+      int j0 = 0;
+      if (!(d < ldexpf(1.0f, -12))) j0 = ((int)((__float_as_uint(d) >> 23) & 255u) - 127 + 12) / 2 + 1;
+      if (j0 < NTH) {
+        const uint32_t inc = 1u << ((j0 & 3) * 8);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h[q] += (j0 >> 2) == q ? inc : 0u;
+      }
+      if (++k == U) {  // fold the chunk's bins into the cumulative counts
+        uint32_t run = 0;
+#pragma unroll
+        for (int j = 0; j < NTH; ++j) {
+          run += (h[j >> 2] >> ((j & 3) * 8)) & 255u;
+          c[j] += run;
+        }
+        h[0] = h[1] = h[2] = h[3] = 0u;
+        k = 0;
+      }
+    });
+    reduce_counts(c, 0u, tk);
+  }
+  float cut = 0.0f;
+  for (int round = 0; round < 4; ++round) {
+    int j = 0;
+    while (j < NTH && tk.cnt[j] < top_k) ++j;
+    if (j == NTH) {  // fewer than top_k finite elements near the max
+      if (!all_finite) return -1;
+      cut = INFINITY;
+      break;
+    }
+    if (tk.cnt[j] <= (uint32_t)(round == 0 ? CCAP / 4 : CCAP)) {
+      cut = thr(j);
+      break;
+    }
+    if (round == 3) return -1;  // ties too wide to cut
+    const uint32_t base = j > 0 ? tk.cnt[j - 1] : 0u;
+    const float nlo = j > 0 ? thr(j - 1) : lo, nhi = thr(j);
+    lo = nlo;
+    hi = nhi;
+    linear = true;
+    float tv[NTH];
+#pragma unroll
+    for (int t = 0; t < NTH; ++t) tv[t] = thr(t);
+    uint32_t c[NTH];
+#pragma unroll
+    for (int t = 0; t < NTH; ++t) c[t] = 0u;
+    for_row(n, l_of, [&](float l, int, bool) {
+      const float d = mx - l;
+      if (!(d < lo) && d < hi) {
+#pragma unroll
+        for (int t = 0; t < NTH; ++t) c[t] += d < tv[t] ? 1u : 0u;
+      }
+    });
+    __syncthreads();  // every thread has read cnt
+    reduce_counts(c, base, tk);
+  }
+
+  // Gather the elements under the cut.
+  if (threadIdx.x == 0) tk.n_cand = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  for_row(n, l_of, [&](float l, int i, bool live) {
+    const bool take = live && mx - l < cut;
+    const unsigned long long mask = __ballot(take);
+    if (mask) {
+      const int lead = __ffsll((long long)mask) - 1;
+      uint32_t base = 0;
+      if (lane == lead) base = atomicAdd(&tk.n_cand, (uint32_t)__popcll(mask));
+      base = __shfl(base, lead, 64);
+      const uint32_t slot = base + __popcll(mask & ((1ull << lane) - 1ull));
+      if (take && slot < (uint32_t)CCAP)
+        tk.comp[slot] = ((unsigned long long)order_key(l) << 32) | (0xFFFFFFFFu - (idx0 + (uint32_t)i));
+    }
+  });
+  __syncthreads();
+  const int nc = (int)tk.n_cand;
+  if (nc > CCAP || (!all_finite && nc < (int)top_k)) return -1;
+  return rank_top(nc, (int)top_k, tk);
+}
+
 __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
   extern __shared__ uint32_t bitmap[];
   __shared__ SampleShared sh;
+  __shared__ TopKShared tk;
   const int m = blockIdx.x, n = a.n;
   const float* row = a.logits + (size_t)m * a.row_stride;
   double* w = a.wbuf + (size_t)m * n;
 
-  // This row's seen ids and draw.
-  const uint32_t* sr = nullptr;
-  uint32_t cnt = 0;
+  // This row's seen ids (positions [s_lo, s_hi) of ids, a row of id_len
+  // entries) and draw, their loads issued together.
+  const uint32_t* ids = nullptr;
+  long id_len = 0;
+  int s_lo = 0, s_hi = 0;
   double r = 0.0;
   if (a.tok) {
-    if (a.done[m]) {
+    const int dn = a.done[m], st = a.start[m], p = a.pos[m];
+    const uint32_t c = a.count[m];
+    if (dn) {
       if (threadIdx.x == 0) a.active[m] = 0;
       return;
     }
-    const int st = a.start[m], p = a.pos[m];
-    sr = a.hist + (size_t)m * a.hist_stride + st;
-    cnt = p > st ? (uint32_t)(p - st) : 0u;
-    if (a.uniform) r = a.uniform[(size_t)a.count[m] * gridDim.x + m];
+    ids = a.hist + (size_t)m * a.hist_stride;
+    id_len = a.hist_stride;
+    s_lo = st;
+    s_hi = p > st ? p : st;
+    if (a.uniform) r = a.uniform[(size_t)c * gridDim.x + m];
   } else {
     if (a.seen) {
-      sr = a.seen + (size_t)m * a.seen_stride;
-      cnt = a.seen_len ? min(a.seen_len[m], (uint32_t)a.seen_stride) : 0u;
+      ids = a.seen + (size_t)m * a.seen_stride;
+      id_len = a.seen_stride;
+      s_hi = a.seen_len ? (int)min(a.seen_len[m], (uint32_t)a.seen_stride) : 0;
     }
     if (a.uniform) r = a.uniform[m];
   }
 
   // Bitmap of this row's seen ids (only if the penalty changes anything).
+  // The ids are read from their whole row (its extent is known) while the
+  // range is still being loaded.
   const uint32_t* bm = nullptr;
-  if (a.penalty != 1.0f && sr) {
+  if (a.penalty != 1.0f && ids) {
     const int words = (n + 31) / 32;
-    for (int k = threadIdx.x; k < words; k += NT) bitmap[k] = 0;
-    __syncthreads();
-    for (uint32_t s = threadIdx.x; s < cnt; s += NT) {
-      const uint32_t id = sr[s];
-      if (id < (uint32_t)n) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    for (long s0 = 0; s0 < id_len; s0 += 4 * NT) {
+      uint32_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const long q = s0 + u * NT + threadIdx.x;
+        v[u] = q < id_len ? ids[q] : 0u;
+      }
+      if (s0 == 0) {
+        for (int k = threadIdx.x; k < words; k += NT) bitmap[k] = 0;
+        __syncthreads();
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const long q = s0 + u * NT + threadIdx.x;
+        if (q >= s_lo && q < s_hi && v[u] < (uint32_t)n) atomicOr(&bitmap[v[u] >> 5], 1u << (v[u] & 31));
+      }
+    }
+    if (id_len <= 0) {
+      for (int k = threadIdx.x; k < words; k += NT) bitmap[k] = 0;
     }
     __syncthreads();
     bm = bitmap;
@@ -226,7 +517,73 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
   auto key_of = [&](int i) { return order_key(pen_logit(row, i, bm, a.penalty)); };
 
   uint32_t pick;
-  if (a.temperature <= 0.0f) {
+  bool picked = false;
+  const bool topk = a.temperature > 0.0f && a.top_k > 0 && a.top_k < n && a.top_k <= KCAP;
+  auto l_at = [&](int i) { return pen_logit(row, i, bm, a.penalty); };
+  const int S = gridDim.y;
+  int nc = 0;
+  if (topk) {
+    // With S > 1 (the host splits only rows with topk, a.cnt, and
+    // S * (top_k + 1) <= n) this block takes part blockIdx.y of the row.
+    const int per = (n + S - 1) / S;
+    const int lo = min(n, (int)blockIdx.y * per), hi = min(n, lo + per);
+    if (lo < hi)
+      nc = topk_candidates(hi - lo, [&](int i) { return l_at(lo + i); }, (uint32_t)lo,
+                           (uint32_t)a.top_k, S > 1, sh, tk);
+  }
+  if (S > 1) {
+    // Its top_k (at most) to the row's workspace, then the row's last part
+    // to arrive merges them.
+    const int part = blockIdx.y;
+    const int L = nc;
+    unsigned long long* cand = reinterpret_cast<unsigned long long*>(w);
+    int* status = reinterpret_cast<int*>(cand + (size_t)S * a.top_k);
+    for (int t = threadIdx.x; t < L; t += NT)
+      __hip_atomic_store(cand + (size_t)part * a.top_k + t, tk.top[t], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0)
+      __hip_atomic_store(status + part, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int done = __hip_atomic_fetch_add(a.cnt + m, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sh.bcast_u[1] = done == S - 1;
+      if (done == S - 1)  // zero for the next launch
+        __hip_atomic_store(a.cnt + m, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!sh.bcast_u[1]) return;
+    auto part_len = [&](int q) {
+      return __hip_atomic_load(status + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    int total = 0;
+    bool fail = false;
+    for (int q = 0; q < S; ++q) {
+      const int Lq = part_len(q);
+      fail = fail || Lq < 0;
+      total += Lq > 0 ? Lq : 0;
+    }
+    if (!fail && total >= a.top_k && total <= CCAP) {
+      int off = 0;
+      for (int q = 0; q < S; ++q) {
+        const int Lq = part_len(q);
+        for (int t = threadIdx.x; t < Lq; t += NT)
+          tk.comp[off + t] = __hip_atomic_load(cand + (size_t)q * a.top_k + t, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        off += Lq;
+      }
+      __syncthreads();
+      rank_top(total, a.top_k, tk);
+      pick = tail_topk((uint32_t)a.top_k, a.temperature, a.top_p, r, tk);
+      picked = true;
+    }
+    // Otherwise this block takes the whole row on the radix path below.
+  } else if (topk && nc >= 0) {
+    pick = tail_topk((uint32_t)a.top_k, a.temperature, a.top_p, r, tk);
+    picked = true;
+  }
+  if (picked) {
+  } else if (a.temperature <= 0.0f) {
     // sampling.rs:30-32, 83-91: first index of the maximum.
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
@@ -371,7 +728,16 @@ hipError_t launch_sample_rows(const SampleArgs& a, int rows, hipStream_t s) {
                 a.max_new <= 0))
     return hipErrorInvalidValue;
   const size_t lds = a.penalty != 1.0f && (a.seen || a.tok) ? (size_t)(a.n + 31) / 32 * 4 : 0;
-  hipLaunchKernelGGL(k_sample_rows, dim3(rows), dim3(NT), lds, s, a);
+  // Rows sampled with 0 < top_k <= 256 over parts of the vocabulary: about
+  // 256 blocks in all, at most 16 parts, each part's top_k and status within
+  // the row's workspace of n doubles.
+  int parts = 1;
+  if (a.cnt && rows <= kSampleCounters && a.temperature > 0.0f && a.top_k > 0 &&
+      a.top_k <= 256 && a.top_k < a.n) {
+    parts = std::min(16, std::max(1, 256 / rows));
+    while (parts > 1 && (long)parts * (a.top_k + 1) > a.n) --parts;
+  }
+  hipLaunchKernelGGL(k_sample_rows, dim3(rows, parts), dim3(NT), lds, s, a);
   return hipGetLastError();
 }
 

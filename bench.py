@@ -500,6 +500,44 @@ def cpu_prefill_baseline(cfg, weights, tokens, threads):
     return len(tokens) / dt, dt
 
 
+def sampled_generate_measurement(hip, be, model, prompt, ctx, steps=64, reps=3):
+    """run_chat's own loop (main.rs:162): generate(prompt, steps, 0.8, 40,
+    0.95, 1.15) on every sequence from empty caches (inference.rs:264-326):
+    the prefill, then `steps` rounds of sample_token over each sequence's
+    history (its prompt and the tokens so far) and a decode step, all on the
+    device (draws from seeded uniforms).  Per round: the generate's time less
+    the same prefill timed alone (medians of `reps`)."""
+    import time
+    B = prompt.shape[0]
+    uni = np.random.default_rng(11).random((steps, B))
+    sess = hip.Session(model, ctx, B)
+    args = (steps, 0.8, 40, 0.95, 1.15)
+    sess.generate(prompt, *args, uniforms=uni)  # warm: captures
+    gen, pre, counts = [], [], 0
+    for _ in range(reps):
+        sess.truncate(0)
+        be.synchronize()
+        t0 = time.perf_counter()
+        toks = sess.generate(prompt, *args, uniforms=uni)
+        gen.append(time.perf_counter() - t0)
+        counts = sum(len(t) for t in toks)
+        sess.truncate(0)
+        be.synchronize()
+        t0 = time.perf_counter()
+        sess.prefill(prompt, want_logits=False)
+        be.synchronize()
+        pre.append(time.perf_counter() - t0)
+    sess.close()
+    g, p = float(np.median(gen)), float(np.median(pre))
+    per = (g - p) / steps
+    return {"workload": f"config 4's prompts ({B} x {prompt.shape[1]}, seed 4) through "
+                        f"generate(..., {steps}, 0.8, 40, 0.95, 1.15) as run_chat calls it: "
+                        f"prefill, then {steps} rounds of device sampling + decode step",
+            "generate_ms": round(g * 1e3, 3), "prefill_ms": round(p * 1e3, 3),
+            "ms_per_round": round(per * 1e3, 4), "tokens": int(counts),
+            "tok_s": round(counts / (g - p), 1)}
+
+
 def shader_graph_measurement(pkg, hip, be, cfg, weights, session_tokens, capture=True):
     """Config 1 through the reference's per-shader decode graph: ShaderDecoder
     rebuilds build_decode_layer node for node from the C-ABI launchers (one
@@ -767,6 +805,9 @@ def main():
                   "step_frac": round(total_bytes / (fused_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
     sess.set_fused_norm(False)
 
+    log("bench: sampled generate (run_chat's parameters)")
+    sampled = sampled_generate_measurement(hip, be, model, prompt, CTX, steps=window)
+
     # Dominant kernel: decode attention at T = 481 (pos 480), launches cycled
     # over the 12 layers so each reads its KV rows from HBM as in a step.
     sess.truncate(P)
@@ -910,6 +951,7 @@ def main():
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                           "bytes_per_step_mean": int(total_bytes / steps)},
         "decode_fused_norm": fused_norm,
+        "decode_sampled": sampled,
         "kernels": kernels,
         "prefill": prefill,
         "config1": config1,
