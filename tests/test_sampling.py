@@ -133,3 +133,25 @@ def test_device_sampler_matches_oracle(backend, pkg, ora, t, k, p, pen, ties):
     got = _device_sample(pkg, backend, l, t, k, p, pen, seen_rows, u)
     want = [ora.sample_token(l[i], t, k, p, seen_rows[i], pen, u[i]) for i in range(rows)]
     assert list(got) == want
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows", [4, 64])
+def test_device_sampler_split_rows_edge_cases(backend, pkg, ora, rows):
+    # run_chat's parameters with rows split over parts of the vocabulary (16
+    # parts at 4 rows, 4 at 64): a quarter of the vocabulary at -inf (parts
+    # with no finite element), only 10 finite logits (fewer than top_k: the
+    # radix path), integer logits (ties across parts, lower index first),
+    # and plain rows; every row against the oracle.
+    rng = np.random.default_rng(77 + rows)
+    n = 50257
+    l = (rng.standard_normal((rows, n)) * 2.5).astype(np.float32)
+    l[0, : n // 4] = -np.inf
+    l[1, :] = -np.inf
+    l[1, rng.choice(n, 10, replace=False)] = rng.standard_normal(10).astype(np.float32)
+    l[2] = np.round(l[2]).astype(np.float32)
+    seen_rows = [rng.integers(0, n, int(rng.integers(0, 64))).astype(np.uint32) for _ in range(rows)]
+    u = rng.random(rows)
+    got = _device_sample(pkg, backend, l, 0.8, 40, 0.95, 1.15, seen_rows, u)
+    want = [ora.sample_token(l[i], 0.8, 40, 0.95, seen_rows[i], 1.15, u[i]) for i in range(rows)]
+    assert list(got) == want
