@@ -538,6 +538,38 @@ def sampled_generate_measurement(hip, be, model, prompt, ctx, steps=64, reps=3):
             "tok_s": round(counts / (g - p), 1)}
 
 
+def sampler_measurement(hip, be, reps=20):
+    """akh_sample_rows on config 4's shape (32 rows x vocabulary 50257, logits
+    N(0, 2^2), seed 0; 480 seen ids per row, as at KV 480) for run_chat's
+    parameters and each feature alone, eager launches timed with events (the
+    kernel alone: sample_token, sampling.rs:18-81, per row)."""
+    rows, n, H = 32, 50257, 480
+    rng = np.random.default_rng(0)
+    logits = be.tensor((rng.standard_normal(rows * n) * 2).astype(np.float32))
+    seen = be.tensor(rng.integers(0, n, rows * H, dtype=np.uint32))
+    seen_len = be.tensor(np.full(rows, H, np.uint32))
+    uni = be.tensor(rng.random(rows))
+    out = be.zeros(rows, np.uint32)
+    res = {"workload": f"{rows} rows x {n} logits, {H} seen ids per row, one launch per call"}
+    for name, kw in (("run_chat", dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.15)),
+                     ("top_k_40", dict(temperature=0.8, top_k=40)),
+                     ("top_p_0.95", dict(temperature=0.8, top_p=0.95)),
+                     ("temperature", dict(temperature=0.8)),
+                     ("greedy", dict(temperature=0.0))):
+        call = lambda: be.sample_rows(logits, rows, n, out, seen=seen, seen_stride=H,  # noqa: E731
+                                      seen_len=seen_len, uniforms=uni, **kw)
+        for _ in range(3):
+            call()
+        be.synchronize()
+        be.timer_start()
+        for _ in range(reps):
+            call()
+        res[name + "_us"] = round(be.timer_stop() / reps * 1e3, 2)
+    for t in (logits, seen, seen_len, uni, out):
+        t.free()
+    return res
+
+
 def shader_graph_measurement(pkg, hip, be, cfg, weights, session_tokens, capture=True):
     """Config 1 through the reference's per-shader decode graph: ShaderDecoder
     rebuilds build_decode_layer node for node from the C-ABI launchers (one
@@ -708,6 +740,8 @@ def main():
     ap.add_argument("--eager-shader", action="store_true",
                     help="with --shader-graph-only: decode steps launch eagerly instead of "
                          "replaying the captured graph (for kernel tracers)")
+    ap.add_argument("--sampler-only", action="store_true",
+                    help="time only the device sampler on config 4's shape and print it")
     ap.add_argument("--kernels-only", action="store_true",
                     help="run only the per-kernel decode legs, no graph replay (for counter "
                          "runs); config 5's too unless --no-scaled")
@@ -720,6 +754,11 @@ def main():
 
     pkg = entry.load_package()
     hip = pkg.hip
+    if args.sampler_only:
+        be = hip.Backend(0)
+        print(json.dumps({"sampler": sampler_measurement(hip, be)}), flush=True)
+        be.close()
+        return
     if args.scaled_prefill_only:
         be = hip.Backend(0)
         log("bench: scaled config weights (seed 5, bf16 values)")
@@ -807,6 +846,7 @@ def main():
 
     log("bench: sampled generate (run_chat's parameters)")
     sampled = sampled_generate_measurement(hip, be, model, prompt, CTX, steps=window)
+    sampled["sampler"] = sampler_measurement(hip, be)
 
     # Dominant kernel: decode attention at T = 481 (pos 480), launches cycled
     # over the 12 layers so each reads its KV rows from HBM as in a step.
