@@ -111,15 +111,16 @@ struct GemvParams {
   int vec;  // B 16-byte aligned and the recorded N a multiple of 4
 };
 
-template <int MR, int CG, bool LC>
-__global__ __launch_bounds__(256) void k_shader_gemv(GemvParams g) {
+template <int MR, int CG, bool LC, int NTB = 256>
+__global__ __launch_bounds__(NTB) void k_shader_gemv(GemvParams g) {
 #ifndef AKH_GEMV_GR
 #define AKH_GEMV_GR 4
 #endif
-  constexpr int SW = 4 * CG;    // slab columns
-  constexpr int RL = 256 / CG;  // row lanes of the block
-  constexpr int GR = MR > 4 ? 2 : AKH_GEMV_GR;  // rounds of RL rows in flight
-  __shared__ float red[4][MR][SW];
+  constexpr int NWB = NTB / 64;  // waves of the block
+  constexpr int SW = 4 * CG;     // slab columns
+  constexpr int RL = NTB / CG;   // row lanes of the block
+  constexpr int GR = NTB > 256 ? 6 : MR > 4 ? 2 : AKH_GEMV_GR;  // rounds of RL rows in flight
+  __shared__ float red[NWB][MR][SW];
   __shared__ int last_block;
   const int M = min((int)g.meta->m, min(g.mrec, MR)), N = min((int)g.meta->n, g.nrec);
   const int K = (int)g.meta->k;
@@ -192,7 +193,10 @@ __global__ __launch_bounds__(256) void k_shader_gemv(GemvParams g) {
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     const int t = tid % SW;
-    tot[m] = ((red[0][m][t] + red[1][m][t]) + red[2][m][t]) + red[3][m][t];
+    float v = red[0][m][t];
+#pragma unroll
+    for (int q = 1; q < NWB; ++q) v += red[q][m][t];
+    tot[m] = v;
   }
   if (g.splits == 1) {
     if (col)
@@ -494,7 +498,19 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
     const dim3 grid(slabs, g.splits);
 #define AKH_GEMV_GO(MR, CG, LC) \
   hipLaunchKernelGGL((k_shader_gemv<MR, CG, LC>), grid, dim3(256), 0, s, g)
-    if (g.vec) {
+#ifndef AKH_GEMV_WIDE_K
+#define AKH_GEMV_WIDE_K 768
+#endif
+    if (g.vec && shape.m == 1 && (int)shape.k <= AKH_GEMV_WIDE_K) {
+      // One 1024-thread block per slab over all of K (K <= 768: a single
+      // round of 6 x 128 rows in flight), so no partial sums and no handoff
+      // between blocks.  Measured at m = 1 against K split over 256-thread
+      // blocks: N = 2304 7.1 -> 5.1 us, 768 5.2 -> 4.3, 3072 7.2 -> 5.2; at
+      // K = 3072 (4 rounds) 9.5 -> 11.0, so larger K keeps the split.
+      g.splits = 1;
+      g.kchunk = (int)shape.k;
+      hipLaunchKernelGGL((k_shader_gemv<1, 8, false, 1024>), dim3(slabs, 1), dim3(1024), 0, s, g);
+    } else if (g.vec) {
       if (shape.m == 1) AKH_GEMV_GO(1, 8, false);
       else if (shape.m <= 4) AKH_GEMV_GO(4, 8, false);
       else AKH_GEMV_GO(32, 8, false);

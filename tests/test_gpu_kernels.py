@@ -138,19 +138,23 @@ def test_matmul_live_meta_bounds_work(backend, pkg, ora):
         assert np.all(got[m * n:] == 7.0)
 
 
-def test_small_m_matmul_k_split_live_meta(backend, pkg, ora):
+@pytest.mark.parametrize("M", [4, 1])
+def test_small_m_matmul_k_split_live_meta(backend, pkg, ora, M):
     # Small-m MATMUL splits K over blocks whose partial sums the last block
     # of each column slab adds.  The grid and splits follow the recorded
     # shape; live metas shrink m, n and k, so some splits get no rows and
     # some slabs no columns (they must neither count nor store).  Every call
     # after the first reuses the workspace and its counters; the same call
     # twice gives the same bits.
+    # With M = 1 the recorded shape runs one 1024-thread block per slab
+    # over all of K (no split).
     h = pkg.hip
-    M, N, K = 4, 2304, 768
+    N, K = 2304, 768
     a, b = ora.rand_vec(M * K, 11), ora.rand_vec(K * N, 12)
     c0 = ora.rand_vec(M * N, 13)
     rec = h.MatMulMeta(M, N, K)
-    for m, n, k in ((4, 2304, 768), (1, 2304, 768), (3, 1000, 300), (2, 257, 7), (4, 2304, 768)):
+    live = ((4, 2304, 768), (1, 2304, 768), (3, 1000, 300), (2, 257, 7), (4, 2304, 768))
+    for m, n, k in ((min(m, M), n, k) for m, n, k in live):
         tb = backend.tensor(b[: k * n].copy())
         am = a.reshape(M, K)[:m, :k].copy().ravel()
         tam = backend.tensor(am)
