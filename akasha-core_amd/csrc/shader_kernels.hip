@@ -498,18 +498,19 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
     const dim3 grid(slabs, g.splits);
 #define AKH_GEMV_GO(MR, CG, LC) \
   hipLaunchKernelGGL((k_shader_gemv<MR, CG, LC>), grid, dim3(256), 0, s, g)
-#ifndef AKH_GEMV_WIDE_K
-#define AKH_GEMV_WIDE_K 768
-#endif
-    if (g.vec && shape.m == 1 && (int)shape.k <= AKH_GEMV_WIDE_K) {
-      // One 1024-thread block per slab over all of K (K <= 768: a single
-      // round of 6 x 128 rows in flight), so no partial sums and no handoff
-      // between blocks.  Measured at m = 1 against K split over 256-thread
-      // blocks: N = 2304 7.1 -> 5.1 us, 768 5.2 -> 4.3, 3072 7.2 -> 5.2; at
-      // K = 3072 (4 rounds) 9.5 -> 11.0, so larger K keeps the split.
-      g.splits = 1;
-      g.kchunk = (int)shape.k;
-      hipLaunchKernelGGL((k_shader_gemv<1, 8, false, 1024>), dim3(slabs, 1), dim3(1024), 0, s, g);
+    // m = 1 on 16-byte rows: 1024-thread blocks, each over one range of at
+    // most 768 rows of K (a single round of 6 x 128 rows in flight); one range
+    // needs no partial sums, more are added by the slab's last block.
+    // Measured at m = 1 against 256-thread blocks over up to 8 ranges:
+    // K = 768: N = 2304 7.1 -> 5.1 us, 768 5.2 -> 4.3, 3072 7.2 -> 5.2;
+    // K = 3072, N = 768 (four ranges) 9.5 -> 6.9 us.
+    const int wranges = ((int)shape.k + 767) / 768;
+    if (g.vec && shape.m == 1 && shape.k > 0 &&
+        (wranges == 1 || (ws && cnt && slabs <= kGemvSlabs && wranges <= kGemvMaxSplits &&
+                          (size_t)wranges * shape.n <= kGemvWsFloats))) {
+      g.splits = wranges;
+      g.kchunk = wranges == 1 ? (int)shape.k : 768;
+      hipLaunchKernelGGL((k_shader_gemv<1, 8, false, 1024>), dim3(slabs, wranges), dim3(1024), 0, s, g);
     } else if (g.vec) {
       if (shape.m == 1) AKH_GEMV_GO(1, 8, false);
       else if (shape.m <= 4) AKH_GEMV_GO(4, 8, false);

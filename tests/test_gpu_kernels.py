@@ -138,18 +138,18 @@ def test_matmul_live_meta_bounds_work(backend, pkg, ora):
         assert np.all(got[m * n:] == 7.0)
 
 
-@pytest.mark.parametrize("M", [4, 1])
-def test_small_m_matmul_k_split_live_meta(backend, pkg, ora, M):
+@pytest.mark.parametrize("M,K", [(4, 768), (1, 768), (1, 3072)])
+def test_small_m_matmul_k_split_live_meta(backend, pkg, ora, M, K):
     # Small-m MATMUL splits K over blocks whose partial sums the last block
     # of each column slab adds.  The grid and splits follow the recorded
     # shape; live metas shrink m, n and k, so some splits get no rows and
     # some slabs no columns (they must neither count nor store).  Every call
     # after the first reuses the workspace and its counters; the same call
     # twice gives the same bits.
-    # With M = 1 the recorded shape runs one 1024-thread block per slab
-    # over all of K (no split).
+    # With M = 1 the recorded shape runs 1024-thread blocks over ranges of
+    # 768 rows of K: one range (K = 768, no partial sums) or four.
     h = pkg.hip
-    N, K = 2304, 768
+    N = 2304
     a, b = ora.rand_vec(M * K, 11), ora.rand_vec(K * N, 12)
     c0 = ora.rand_vec(M * N, 13)
     rec = h.MatMulMeta(M, N, K)
