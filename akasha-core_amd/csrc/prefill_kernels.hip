@@ -231,13 +231,15 @@ __device__ __forceinline__ void epi_tile(const GemmParams& p, int M, int N, int 
 // 64 columns, lane j of N tile t owns column 2j + t so each lane holds
 // adjacent column pairs (float2 B reads, paired epilogue for RoPE).  The
 // next K tile is fetched into registers while the current one is consumed.
-template <int EPI>
+// SPLIT: the grid's z splits K over p.split_kc rows per block, the tile's
+// last block adding the splits (a separate instantiation: the split code
+// made the unsplit kernel 30 % slower on config 3's fp32-MFMA prefill).
+template <int EPI, bool SPLIT = false>
 __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   constexpr int BM = 128, BN = 128, BK = 16;
   constexpr int APAD = 4;
   __shared__ float As[BK][BM + APAD];
   __shared__ float Bs[BK][BN];
-  __shared__ int last_split;
 
   int M = p.M, N = p.N, K = p.K;
   if (p.meta) {
@@ -252,8 +254,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   const int m0 = (id / gridDim.x) * BM, n0 = (id % gridDim.x) * BN;
   if (m0 >= M || n0 >= N) return;  // every split of the tile returns here
   // This block's rows of K: all of them, or split blockIdx.z's p.split_kc.
-  const int kbeg = p.split_ws ? min(K, (int)blockIdx.z * p.split_kc) : 0;
-  const int kend = p.split_ws ? min(K, kbeg + p.split_kc) : K;
+  const int kbeg = SPLIT ? min(K, (int)blockIdx.z * p.split_kc) : 0;
+  const int kend = SPLIT ? min(K, kbeg + p.split_kc) : K;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
@@ -336,7 +338,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     }
   }
 
-  if (p.split_ws && gridDim.z > 1) {
+  if constexpr (SPLIT) {
+    __shared__ int last_split;
     // A split tile: each block stores its sums (written through to device
     // scope, lane-major), waits until they have completed and counts
     // itself; the last of the tile's blocks adds every split's sums in split
@@ -2541,7 +2544,7 @@ hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
   dim3 g((p.N + 127) / 128, (p.M + 127) / 128), b(256);
   GemmParams q = p;
   q.split_kc = p.K;
-  if (p.split_ws && p.split_cnt) {
+  if (p.split_ws && p.split_cnt && (epi == GEMM_STORE || epi == GEMM_ADD)) {
     // Fewer tiles than the part has CUs: K split over up to 16 blocks per
     // tile (at least 64 rows each), about 256 blocks in all, within the
     // workspace (one 128 x 128 partial per tile and split).
@@ -2554,11 +2557,17 @@ hipError_t launch_gemm(const GemmParams& p, int epi, hipStream_t s) {
       q.split_kc = ((p.K + splits - 1) / splits + 15) / 16 * 16;
       g.z = (p.K + q.split_kc - 1) / q.split_kc;
     }
-    if (g.z <= 1) q.split_ws = nullptr;
   }
+  if (g.z <= 1) q.split_ws = nullptr;
   switch (epi) {
-    case GEMM_STORE: hipLaunchKernelGGL(k_gemm<GEMM_STORE>, g, b, 0, s, q); break;
-    case GEMM_ADD: hipLaunchKernelGGL(k_gemm<GEMM_ADD>, g, b, 0, s, q); break;
+    case GEMM_STORE:
+      if (q.split_ws) hipLaunchKernelGGL((k_gemm<GEMM_STORE, true>), g, b, 0, s, q);
+      else hipLaunchKernelGGL((k_gemm<GEMM_STORE>), g, b, 0, s, q);
+      break;
+    case GEMM_ADD:
+      if (q.split_ws) hipLaunchKernelGGL((k_gemm<GEMM_ADD, true>), g, b, 0, s, q);
+      else hipLaunchKernelGGL((k_gemm<GEMM_ADD>), g, b, 0, s, q);
+      break;
     case GEMM_SILU: hipLaunchKernelGGL(k_gemm<GEMM_SILU>, g, b, 0, s, q); break;
     case GEMM_QKV: hipLaunchKernelGGL(k_gemm<GEMM_QKV>, g, b, 0, s, q); break;
     default: return hipErrorInvalidValue;
