@@ -39,7 +39,13 @@ namespace akh {
 
 namespace {
 
-constexpr int NT = 1024;        // threads per row
+#ifndef AKH_SAMPLE_NT
+#define AKH_SAMPLE_NT 1024
+#endif
+#ifndef AKH_SAMPLE_BLOCKS
+#define AKH_SAMPLE_BLOCKS 256
+#endif
+constexpr int NT = AKH_SAMPLE_NT;  // threads per row (per part of a split row)
 constexpr int NW = NT / 64;     // waves per block
 
 struct SampleShared {
@@ -734,7 +740,7 @@ hipError_t launch_sample_rows(const SampleArgs& a, int rows, hipStream_t s) {
   int parts = 1;
   if (a.cnt && rows <= kSampleCounters && a.temperature > 0.0f && a.top_k > 0 &&
       a.top_k <= 256 && a.top_k < a.n) {
-    parts = std::min(16, std::max(1, 256 / rows));
+    parts = std::min(AKH_SAMPLE_BLOCKS / 16, std::max(1, AKH_SAMPLE_BLOCKS / rows));
     while (parts > 1 && (long)parts * (a.top_k + 1) > a.n) --parts;
   }
   hipLaunchKernelGGL(k_sample_rows, dim3(rows, parts), dim3(NT), lds, s, a);
