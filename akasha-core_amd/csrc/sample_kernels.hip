@@ -736,12 +736,13 @@ hipError_t launch_sample_rows(const SampleArgs& a, int rows, hipStream_t s) {
   const size_t lds = a.penalty != 1.0f && (a.seen || a.tok) ? (size_t)(a.n + 31) / 32 * 4 : 0;
   // Rows sampled with 0 < top_k <= 256 over parts of the vocabulary: about
   // 256 blocks in all, at most 16 parts, each part's top_k and status within
-  // the row's workspace of n doubles.
+  // the row's workspace of n doubles, and all parts' top_k within CCAP.
   int parts = 1;
   if (a.cnt && rows <= kSampleCounters && a.temperature > 0.0f && a.top_k > 0 &&
       a.top_k <= 256 && a.top_k < a.n) {
     parts = std::min(AKH_SAMPLE_BLOCKS / 16, std::max(1, AKH_SAMPLE_BLOCKS / rows));
-    while (parts > 1 && (long)parts * (a.top_k + 1) > a.n) --parts;
+    // The last block merges parts * top_k entries in its CCAP-entry buffer.
+    while (parts > 1 && ((long)parts * (a.top_k + 1) > a.n || (long)parts * a.top_k > CCAP)) --parts;
   }
   hipLaunchKernelGGL(k_sample_rows, dim3(rows, parts), dim3(NT), lds, s, a);
   return hipGetLastError();

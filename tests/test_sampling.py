@@ -136,10 +136,11 @@ def test_device_sampler_matches_oracle(backend, pkg, ora, t, k, p, pen, ties):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows", [4, 64])
-def test_device_sampler_split_rows_edge_cases(backend, pkg, ora, rows):
+@pytest.mark.parametrize("rows,k", [(4, 40), (64, 40), (3, 200)])
+def test_device_sampler_split_rows_edge_cases(backend, pkg, ora, rows, k):
     # run_chat's parameters with rows split over parts of the vocabulary (16
-    # parts at 4 rows, 4 at 64): a quarter of the vocabulary at -inf (parts
+    # parts at 4 rows, 4 at 64; top_k 200 at 3 rows: 10 parts, so that all
+    # parts' top_k fit the merge): a quarter of the vocabulary at -inf (parts
     # with no finite element), only 10 finite logits (fewer than top_k: the
     # radix path), integer logits (ties across parts, lower index first),
     # and plain rows; every row against the oracle.
@@ -152,6 +153,6 @@ def test_device_sampler_split_rows_edge_cases(backend, pkg, ora, rows):
     l[2] = np.round(l[2]).astype(np.float32)
     seen_rows = [rng.integers(0, n, int(rng.integers(0, 64))).astype(np.uint32) for _ in range(rows)]
     u = rng.random(rows)
-    got = _device_sample(pkg, backend, l, 0.8, 40, 0.95, 1.15, seen_rows, u)
-    want = [ora.sample_token(l[i], 0.8, 40, 0.95, seen_rows[i], 1.15, u[i]) for i in range(rows)]
+    got = _device_sample(pkg, backend, l, 0.8, k, 0.95, 1.15, seen_rows, u)
+    want = [ora.sample_token(l[i], 0.8, k, 0.95, seen_rows[i], 1.15, u[i]) for i in range(rows)]
     assert list(got) == want
