@@ -238,7 +238,12 @@ extern "C" akh_status akh_tensor_free(akh_backend* be, void* dev) {
     be->owned.erase(it);
     return AKH_OK;
   }
-  if (it != be->owned.end()) be->owned.erase(it);
+  if (it != be->owned.end()) {
+    be->owned.erase(it);
+  } else {
+    for (const auto& kv : be->pool)
+      CHECK_ARG(kv.second != dev, "akh_tensor_free: tensor already freed");
+  }
   HIP_TRY(hipStreamSynchronize(be->stream));
   HIP_TRY(hipFree(dev));
   return AKH_OK;

@@ -92,7 +92,8 @@ int akh_abi_version(void);
  * the backend, up to 8 GB) is reused only by a later alloc, and an upload of
  * up to 64 KB copies the host bytes out before it returns (larger ones wait
  * for their copy).  Download waits for the stream.  So a tensor is used on
- * the backend that made it, or after akh_synchronize. */
+ * the backend that made it, or after akh_synchronize.  Freeing a tensor
+ * twice returns AKH_E_INVALID. */
 akh_status akh_tensor_alloc(akh_backend* be, size_t bytes, void** dev);
 akh_status akh_tensor_free(akh_backend* be, void* dev);
 akh_status akh_tensor_upload(akh_backend* be, void* dev, const void* host,

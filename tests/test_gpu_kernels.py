@@ -43,6 +43,20 @@ def test_tensor_reuse_is_ordered_on_the_stream(backend):
     new.free()
 
 
+def test_tensor_double_free_is_refused(backend, pkg):
+    # A freed block waits in the backend's pool: freeing it again is an
+    # error, not a second hipFree of memory a later alloc may hand out.
+    h = pkg.hip
+    t = backend.zeros(1000)
+    p = t.ptr
+    t.free()
+    assert h._lib.akh_tensor_free(backend.handle, p) == h.InvalidArgument.code
+    assert b"already freed" in h._lib.akh_last_error()
+    again = backend.zeros(1000)
+    assert again.ptr.value == p.value and not again.download().any()
+    again.free()
+
+
 def test_uploads_are_staged_and_ordered(backend):
     # Uploads return before the copy runs: the host array is copied out at
     # once (changing it afterwards changes nothing), a kernel queued after an
