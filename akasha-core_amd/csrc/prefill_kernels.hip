@@ -350,14 +350,17 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     const int tiles = gridDim.x * gridDim.y;
     auto at = [&](int a, int t, int r) { return (((wave * 2 + a) * 2 + t) * 16 + r) * 64 + lane; };
     float* mine = p.split_ws + ((size_t)blockIdx.z * tiles + tile) * TILE;
+    // A wave whose 64 rows all lie past M neither stores nor reads partials.
+    const bool live = m0 + wm * 64 < M;
+    if (live)
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          __hip_atomic_store(mine + at(a, t, r), acc[a][t][r], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+          for (int r = 0; r < 16; ++r)
+            __hip_atomic_store(mine + at(a, t, r), acc[a][t][r], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -376,7 +379,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[a][t][r] = 0.f;
-    for (int sp = 0; sp < (int)gridDim.z; ++sp) {
+    for (int sp = 0; live && sp < (int)gridDim.z; ++sp) {
       const float* part = p.split_ws + ((size_t)sp * tiles + tile) * TILE;
       float v[2][2][16];
 #pragma unroll
