@@ -559,24 +559,43 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
     }
     __syncthreads();
     if (!sh.bcast_u[1]) return;
-    auto part_len = [&](int q) {
-      return __hip_atomic_load(status + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
+    // Every part's status in one batch of loads (at most 16 parts).
+    int Lp[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      Lp[q] = q < S ? __hip_atomic_load(status + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
     int total = 0;
     bool fail = false;
-    for (int q = 0; q < S; ++q) {
-      const int Lq = part_len(q);
-      fail = fail || Lq < 0;
-      total += Lq > 0 ? Lq : 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      fail = fail || Lp[q] < 0;
+      total += Lp[q] > 0 ? Lp[q] : 0;
     }
     if (!fail && total >= a.top_k && total <= CCAP) {
-      int off = 0;
-      for (int q = 0; q < S; ++q) {
-        const int Lq = part_len(q);
-        for (int t = threadIdx.x; t < Lq; t += NT)
-          tk.comp[off + t] = __hip_atomic_load(cand + (size_t)q * a.top_k + t, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        off += Lq;
+      // Entry e of the merged list: part q (the one whose prefix covers e),
+      // position e - prefix; a thread's entries (at most two) load at once.
+      unsigned long long got[CCAP / NT];
+#pragma unroll
+      for (int u = 0; u < CCAP / NT; ++u) {
+        const int e = threadIdx.x + u * NT;
+        int q = -1, base = 0, run = 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int len = Lp[k] > 0 ? Lp[k] : 0;
+          if (q < 0 && e < run + len) {
+            q = k;
+            base = run;
+          }
+          run += len;
+        }
+        got[u] = q >= 0 ? __hip_atomic_load(cand + (size_t)q * a.top_k + (e - base),
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < CCAP / NT; ++u) {
+        const int e = threadIdx.x + u * NT;
+        if (e < total) tk.comp[e] = got[u];
       }
       __syncthreads();
       rank_top(total, a.top_k, tk);
