@@ -152,8 +152,8 @@ def test_matmul_live_meta_bounds_work(backend, pkg, ora):
         assert np.all(got[m * n:] == 7.0)
 
 
-@pytest.mark.parametrize("M,K", [(4, 768), (1, 768), (1, 3072)])
-def test_small_m_matmul_k_split_live_meta(backend, pkg, ora, M, K):
+@pytest.mark.parametrize("M,K,N", [(4, 768, 2304), (1, 768, 2304), (1, 3072, 2304), (1, 768, 2305)])
+def test_small_m_matmul_k_split_live_meta(backend, pkg, ora, M, K, N):
     # Small-m MATMUL splits K over blocks whose partial sums the last block
     # of each column slab adds.  The grid and splits follow the recorded
     # shape; live metas shrink m, n and k, so some splits get no rows and
@@ -161,9 +161,9 @@ def test_small_m_matmul_k_split_live_meta(backend, pkg, ora, M, K):
     # after the first reuses the workspace and its counters; the same call
     # twice gives the same bits.
     # With M = 1 the recorded shape runs 1024-thread blocks over ranges of
-    # 768 rows of K: one range (K = 768, no partial sums) or four.
+    # 768 rows of K: one range (K = 768, no partial sums) or four; N = 2305
+    # (rows not whole 16-byte pieces) takes lane-adjacent columns.
     h = pkg.hip
-    N = 2304
     a, b = ora.rand_vec(M * K, 11), ora.rand_vec(K * N, 12)
     c0 = ora.rand_vec(M * N, 13)
     rec = h.MatMulMeta(M, N, K)
