@@ -1,5 +1,5 @@
 // Device-side token choice: sample_token of src/nn/sampling.rs:3-81 for a
-// batch of rows, one 1024-thread block per row.
+// batch of rows, one 1024-thread block per row (or per part of a row, below).
 //
 // The reference copies the logits, applies the repetition penalty to every
 // distinct seen id, and then either takes the argmax (temperature <= 0) or
@@ -8,9 +8,10 @@
 // cumulative probability reaches top_p (renormalised), and walks the prefix
 // with r = rand::random() until r < p.
 //
-// Here nothing is sorted.  Every cut the reference makes along the sorted
-// order -- the k-th element, the top_p crossing, the element where the walk
-// stops -- is found by a radix select over 32-bit order-preserving keys of
+// On the general path nothing is sorted.  Every cut the reference makes
+// along the sorted order -- the k-th element, the top_p crossing, the
+// element where the walk stops -- is found by a radix select over 32-bit
+// order-preserving keys of
 // the penalised logits: four 8-bit histogram passes narrow the key, counting
 // elements (top_k) or summing their f64 weights (top_p, the walk), and the
 // elements that share the final key are resolved in index order (the
@@ -22,11 +23,14 @@
 // With 0 < top_k <= 1024 (run_chat's 40) only the top_k elements matter:
 // a cut on d = max - l admitting between top_k and 2048 elements is found
 // by counting against 16 thresholds per pass (powers of four, then 16-way
-// refinements), those elements are gathered to LDS and bitonic-sorted by
-// (logit descending, index ascending), and one thread takes the first top_k
-// through the reference's own sequence: f64 probabilities summed in order,
-// the top_p prefix, the walk r -= p.  NaN or infinite maxima, fewer than
-// top_k finite elements and ties too wide for the cut take the radix path.
+// refinements), those elements are gathered to LDS and each takes its place
+// in the order (logit descending, index ascending) by counting the entries
+// above it; the first top_k then go through the reference's own sequence:
+// f64 probabilities summed in order, the top_p prefix, the walk r -= p.
+// With top_k <= 256 a row is split over several blocks (parts of the
+// vocabulary), whose top_k the row's last block merges.  NaN or infinite
+// maxima, fewer than top_k finite elements and ties too wide for the cut
+// take the radix path.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
