@@ -11,9 +11,9 @@
 // On the general path nothing is sorted.  Every cut the reference makes
 // along the sorted order -- the k-th element, the top_p crossing, the
 // element where the walk stops -- is found by a radix select over 32-bit
-// order-preserving keys of
-// the penalised logits: four 8-bit histogram passes narrow the key, counting
-// elements (top_k) or summing their f64 weights (top_p, the walk), and the
+// order-preserving keys of the penalised logits: four 8-bit histogram
+// passes narrow the key, counting elements (top_k) or summing their f64
+// weights (top_p, the walk), and the
 // elements that share the final key are resolved in index order (the
 // reference's unstable sort leaves that order unspecified; lower index first
 // is this implementation's choice).  The per-element weights live in a
