@@ -57,6 +57,39 @@ def test_tensor_double_free_is_refused(backend, pkg):
     again.free()
 
 
+def test_tensor_pool_random_reuse(backend):
+    # Seeded random allocations, uploads, frees and queued kernels on one
+    # backend: every new tensor reads zero, every live tensor keeps what was
+    # last written to it, whichever pooled block it landed on.
+    rng = np.random.default_rng(5)
+    live = []
+    for _ in range(300):
+        op = rng.random()
+        if op < 0.45 or not live:
+            n = int(rng.choice([1, 7, 1000, 4096, 65537, 300000]))
+            t = backend.zeros(n)
+            assert not t.download()[:n].any()
+            v = rng.standard_normal(n).astype(np.float32)
+            if rng.random() < 0.5:
+                t.upload(v)
+            else:
+                v = np.zeros(n, np.float32)
+            live.append((t, v))
+        elif op < 0.8:
+            t, v = live.pop(int(rng.integers(len(live))))
+            assert np.array_equal(t.download()[: v.size], v)
+            t.free()
+        else:
+            t, v = live[int(rng.integers(len(live)))]
+            backend.silu(t, v.size)  # queued work on a live tensor
+            v[:] = v / (np.float32(1) + np.exp(-v))
+            np.testing.assert_allclose(t.download()[: v.size], v, rtol=2e-6, atol=1e-7)
+            live[[x[0] for x in live].index(t)] = (t, t.download()[: v.size].copy())
+    for t, v in live:
+        assert np.array_equal(t.download()[: v.size], v)
+        t.free()
+
+
 def test_uploads_are_staged_and_ordered(backend):
     # Uploads return before the copy runs: the host array is copied out at
     # once (changing it afterwards changes nothing), a kernel queued after an
