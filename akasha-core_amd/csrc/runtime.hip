@@ -193,6 +193,34 @@ extern "C" akh_status akh_synchronize(akh_backend* be) {
   return AKH_OK;
 }
 
+namespace {
+
+// A device block of `want` bytes from the backend's pool (one of at least
+// `want` and at most twice that) or from HIP, its capacity in *cap.
+akh_status tensor_block(akh_backend* be, size_t want, void** out, size_t* cap) {
+  auto it = be->pool.lower_bound(want);
+  if (it != be->pool.end() && it->first <= 2 * want) {
+    *cap = it->first;
+    *out = it->second;
+    be->pool_bytes -= it->first;
+    be->pool.erase(it);
+    return AKH_OK;
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, want);
+  if (e != hipSuccess && !be->pool.empty()) {  // give the pool back, retry
+    (void)hipGetLastError();
+    HIP_TRY(pool_release(be));
+    e = hipMalloc(&p, want);
+  }
+  if (e != hipSuccess) return fail(AKH_E_HIP, std::string("tensor allocation: ") + hipGetErrorString(e));
+  *cap = want;
+  *out = p;
+  return AKH_OK;
+}
+
+}  // namespace
+
 extern "C" akh_status akh_tensor_alloc(akh_backend* be, size_t bytes,
                                        void** dev) {
   CHECK_ARG(be && dev, "akh_tensor_alloc: NULL argument");
@@ -200,29 +228,35 @@ extern "C" akh_status akh_tensor_alloc(akh_backend* be, size_t bytes,
   *dev = nullptr;
   const size_t want = bytes ? bytes : 4;
   void* p = nullptr;
-  size_t cap = want;
-  // A pooled block of at least `want` bytes and at most twice that.
-  auto it = be->pool.lower_bound(want);
-  if (it != be->pool.end() && it->first <= 2 * want) {
-    cap = it->first;
-    p = it->second;
-    be->pool_bytes -= cap;
-    be->pool.erase(it);
-  } else {
-    hipError_t e = hipMalloc(&p, want);
-    if (e != hipSuccess && !be->pool.empty()) {  // give the pool back, retry
-      (void)hipGetLastError();
-      HIP_TRY(pool_release(be));
-      e = hipMalloc(&p, want);
-    }
-    if (e != hipSuccess) return fail(AKH_E_HIP, std::string("akh_tensor_alloc: ") + hipGetErrorString(e));
-  }
+  size_t cap = 0;
+  akh_status st = tensor_block(be, want, &p, &cap);
+  if (st != AKH_OK) return st;
   hipError_t e = hipMemsetAsync(p, 0, want, be->stream);
   if (e != hipSuccess) {
     hipFree(p);
     return fail(AKH_E_HIP, std::string("akh_tensor_alloc: ") + hipGetErrorString(e));
   }
   be->owned[p] = cap;
+  *dev = p;
+  return AKH_OK;
+}
+
+extern "C" akh_status akh_tensor_from_host(akh_backend* be, const void* host, size_t bytes,
+                                           void** dev) {
+  CHECK_ARG(be && dev && (host || !bytes), "akh_tensor_from_host: NULL argument");
+  CHECK_ARG(!be->capturing, "akh_tensor_from_host: graph capture in progress");
+  if (!bytes) return akh_tensor_alloc(be, 0, dev);
+  *dev = nullptr;
+  void* p = nullptr;
+  size_t cap = 0;
+  akh_status st = tensor_block(be, bytes, &p, &cap);
+  if (st != AKH_OK) return st;
+  be->owned[p] = cap;
+  st = akh_tensor_upload(be, p, host, bytes);  // every byte written: no zero fill
+  if (st != AKH_OK) {
+    akh_tensor_free(be, p);
+    return st;
+  }
   *dev = p;
   return AKH_OK;
 }

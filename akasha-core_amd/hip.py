@@ -167,6 +167,7 @@ _SIGS = {
     "akh_tensor_alloc": (ST, [P, C.c_size_t, C.POINTER(P)]),
     "akh_tensor_free": (ST, [P, P]),
     "akh_tensor_upload": (ST, [P, P, P, C.c_size_t]),
+    "akh_tensor_from_host": (ST, [P, P, C.c_size_t, C.POINTER(P)]),
     "akh_tensor_download": (ST, [P, P, P, C.c_size_t]),
     "akh_graph_begin": (ST, [P]),
     "akh_graph_end": (ST, [P, C.POINTER(P)]),
@@ -288,11 +289,17 @@ def _ptr(a: np.ndarray):
 class DeviceTensor:
     """A device allocation (Tensor<HipBackend>): raw pointer + byte size."""
 
-    def __init__(self, backend: "Backend", nbytes: int):
+    def __init__(self, backend: "Backend", nbytes: int, host=None):
+        """Zeroed device memory, or (host: a buffer of nbytes) a copy of host
+        (akh_tensor_from_host, Tensor::init_from_cpu)."""
         self.backend = backend
         self.nbytes = nbytes
         out = C.c_void_p()
-        _check(_lib.akh_tensor_alloc(backend.handle, nbytes, C.byref(out)), "alloc")
+        if host is None:
+            _check(_lib.akh_tensor_alloc(backend.handle, nbytes, C.byref(out)), "alloc")
+        else:
+            _check(_lib.akh_tensor_from_host(backend.handle, host, nbytes, C.byref(out)),
+                   "from_host")
         self.ptr = out
         backend._adopt(self)
 
@@ -384,16 +391,16 @@ class Backend:
     def tensor(self, data: np.ndarray) -> DeviceTensor:
         """Tensor::init_from_cpu."""
         data = np.ascontiguousarray(data)
-        return DeviceTensor(self, max(data.nbytes, 4)).upload(data)
+        if data.nbytes == 0:
+            return DeviceTensor(self, 4)
+        return DeviceTensor(self, data.nbytes, _ptr(data))
 
     def zeros(self, n: int, dtype=np.float32) -> DeviceTensor:
         return DeviceTensor(self, max(n * np.dtype(dtype).itemsize, 4))
 
     def meta(self, m: C.Structure) -> DeviceTensor:
         """KernelMeta::upload (src/nn/ops/meta.rs:4-11)."""
-        t = DeviceTensor(self, C.sizeof(m))
-        _check(_lib.akh_tensor_upload(self.handle, t.ptr, C.byref(m), C.sizeof(m)), "meta")
-        return t
+        return DeviceTensor(self, C.sizeof(m), C.cast(C.pointer(m), C.c_void_p))
 
     def write_meta(self, t: DeviceTensor, m: C.Structure):
         """KernelMeta::write_to (src/nn/ops/meta.rs:12-15)."""

@@ -98,6 +98,11 @@ akh_status akh_tensor_alloc(akh_backend* be, size_t bytes, void** dev);
 akh_status akh_tensor_free(akh_backend* be, void* dev);
 akh_status akh_tensor_upload(akh_backend* be, void* dev, const void* host,
                              size_t bytes);
+/* Tensor::init_from_cpu (inference.rs:83) in one call: a device tensor of
+ * `bytes` holding a copy of host[0 .. bytes), ordered on the stream as
+ * akh_tensor_alloc followed by akh_tensor_upload, without the zeroing that
+ * the upload would overwrite. */
+akh_status akh_tensor_from_host(akh_backend* be, const void* host, size_t bytes, void** dev);
 akh_status akh_tensor_download(akh_backend* be, void* host, const void* dev,
                                size_t bytes);
 

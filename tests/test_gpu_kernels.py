@@ -90,6 +90,23 @@ def test_tensor_pool_random_reuse(backend):
         t.free()
 
 
+def test_tensor_from_host(backend, pkg):
+    # Tensor::init_from_cpu in one call (no zero fill): the copy is taken
+    # before the call returns, small (staged) and large alike.
+    h = pkg.hip
+    for n in (1, 3, 1000, 16384, 300000):
+        a = np.arange(n, dtype=np.float32) - 7.5
+        host = a.copy()
+        t = backend.tensor(host)
+        host[:] = 3.0
+        assert np.array_equal(t.download()[:n], a)
+        t.free()
+    m = h.MatMulMeta(5, 6, 7)
+    t = backend.meta(m)
+    assert list(t.download(np.uint32, 3)) == [5, 6, 7]
+    t.free()
+
+
 def test_uploads_are_staged_and_ordered(backend):
     # Uploads return before the copy runs: the host array is copied out at
     # once (changing it afterwards changes nothing), a kernel queued after an
