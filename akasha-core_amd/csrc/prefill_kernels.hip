@@ -243,9 +243,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 
   int M = p.M, N = p.N, K = p.K;
   if (p.meta) {
-    M = (int)p.meta->m;
-    N = (int)p.meta->n;
-    K = (int)p.meta->k;
+    // The live shape, at most the recorded one (the grid, the split ranges
+    // and the caller's buffers are sized by the recorded shape).
+    M = min((int)p.meta->m, p.M);
+    N = min((int)p.meta->n, p.N);
+    K = min((int)p.meta->k, p.K);
   }
   // Each XCD takes a contiguous run of tiles (see k_gemm_bf16).
   int id = blockIdx.x + gridDim.x * blockIdx.y;

@@ -105,6 +105,7 @@ struct GemvParams {
   const akh_matmul_meta* meta;
   int accumulate;
   int mrec, nrec;  // the recorded shape: the workspace's layout
+  int krec;        // the recorded K: a live K is clamped to it
   int splits, kchunk;
   float* ws;
   int* cnt;
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(NTB) void k_shader_gemv(GemvParams g) {
   __shared__ float red[NWB][MR][SW];
   __shared__ int last_block;
   const int M = min((int)g.meta->m, min(g.mrec, MR)), N = min((int)g.meta->n, g.nrec);
-  const int K = (int)g.meta->k;
+  const int K = min((int)g.meta->k, g.krec);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n0 = blockIdx.x * SW;
   if (n0 >= N || M <= 0) return;  // the whole slab: no block of it counts
@@ -475,7 +476,8 @@ hipError_t shader_matmul(const float* a, const float* b, float* c,
 #ifndef AKH_GEMV_KMIN
 #define AKH_GEMV_KMIN 128
 #endif
-    GemvParams g{a, b, c, meta, accumulate, (int)shape.m, (int)shape.n, 1, 1, ws, cnt, 0};
+    GemvParams g{a, b, c, meta, accumulate, (int)shape.m, (int)shape.n, (int)shape.k,
+                 1, 1, ws, cnt, 0};
     g.vec = shape.n % 4 == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0;
     // Rows that are not whole 16-byte pieces take lane-adjacent columns, for
     // m <= 4 in the widest slabs (up to 256 columns) that still number 128:

@@ -156,9 +156,13 @@ akh_status akh_cache_write(akh_backend* be, const float* src, float* cache,
 /* FLASH_ATTENTION, ops::flash_attention (emit.rs:556-597): causal
  * softmax(scale Q K^T) V for one sequence of rows [row_offset,
  * row_offset+seq_len) of [*, dim] buffers; l_cache[row*H + h] receives
- * max + ln(sum).  head_dim <= 128 (emit.rs:564-567).  head_dim 64 and
- * 128 run on bf16 MFMAs with every fp32 operand split exactly into three
- * bfloat16 terms (six products per contraction, fp32-level error). */
+ * max + ln(sum).  head_dim <= 128 (emit.rs:564-567).  Every head size
+ * keeps fp32-level error.  head_dim 64 (and 128 on grids of fewer 128-row
+ * blocks than CUs) runs split-fp16 MFMA tiles: two fp16 terms per operand,
+ * three products, and a tile whose operands leave fp16's range recomputes
+ * itself on split-bfloat16.  head_dim 128 on larger grids and 33..127
+ * otherwise run split-bfloat16 MFMAs throughout: three bfloat16 terms per
+ * operand, six products.  head_dim <= 32 runs a scalar fp32 kernel. */
 akh_status akh_flash_attention(akh_backend* be, const float* q,
                                const float* k, const float* v, float* out,
                                float* l_cache, akh_flash_attn_meta shape,

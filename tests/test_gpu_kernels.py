@@ -272,6 +272,37 @@ def test_prompt_m_matmul_k_split_live_meta(backend, pkg, ora):
         assert np.array_equal(got[m * n:], c0[m * n:])
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 768, 2304), (1, 3072, 768), (4, 768, 2304),
+                                   (1, 768, 2305), (100, 3072, 768), (2048, 64, 2048)])
+def test_matmul_live_meta_beyond_recorded_is_clamped(backend, pkg, ora, M, K, N):
+    # A live meta larger than the recorded shape in m, n and k computes the
+    # recorded product and writes nothing past it.  The operands carry extra
+    # data after the recorded extent (so a read past it would change the
+    # sums, not leave the buffers); C's tail keeps its sentinel.  Shapes: the
+    # m = 1 GEMV over one range of K and over four, the m = 4 GEMV, the
+    # lane-adjacent-column GEMV, the K-split MFMA GEMM and the unsplit one
+    # (256 tiles).
+    h = pkg.hip
+    pad = 4096
+    a, b = ora.rand_vec(M * K + pad, 31), ora.rand_vec(K * N + pad, 32)
+    c0 = ora.rand_vec(M * N + pad, 33)
+    rec = h.MatMulMeta(M, N, K)
+    meta = _meta(backend, h.MatMulMeta(M + 3, N + 5, K + 7))
+    ta, tb = backend.tensor(a), backend.tensor(b)
+    c = backend.tensor(np.full(M * N + pad, 7.0, np.float32))
+    backend.matmul(ta, tb, c, rec, meta)
+    cadd = backend.tensor(c0)
+    backend.matmul_add(ta, tb, cadd, rec, meta)
+    tol = 1e-4 * max(1.0, np.sqrt(K / 19.0))
+    got = c.download()
+    assert np.abs(got[: M * N] - ora.matmul(a[: M * K], b[: K * N], M, N, K)).max() < tol
+    assert np.all(got[M * N:] == 7.0)
+    got = cadd.download()
+    ref = ora.matmul_add(a[: M * K], b[: K * N], c0[: M * N], M, N, K)
+    assert np.abs(got[: M * N] - ref).max() < tol
+    assert np.array_equal(got[M * N:], c0[M * N:])
+
+
 @pytest.mark.parametrize("seq,dim", [(8, 4), (37, 12), (65, 48)])
 def test_head_gather_qkv_slices(backend, pkg, ora, seq, dim):
     # qkv_split_matches_three_head_gathers shapes (emit.rs:1227-1231).
