@@ -119,20 +119,22 @@ __device__ float block_max_f(float v, SampleShared& sh) {
   return t;
 }
 
-// Inclusive prefix sum over the block in thread order.
+// Exclusive prefix sum over the block in thread order (0 for thread 0).
 template <typename T>
-__device__ T block_scan(T v, T* wave_tot) {
+__device__ T block_scan_excl(T v, T* wave_tot) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int o = 1; o < 64; o <<= 1) {
     const T u = __shfl_up(v, o, 64);
     if (lane >= o) v += u;
   }
+  T ex = __shfl_up(v, 1, 64);
+  if (lane == 0) ex = 0;
   __syncthreads();
   if (lane == 63) wave_tot[w] = v;
   __syncthreads();
   T off = 0;
   for (int k = 0; k < w; ++k) off += wave_tot[k];
-  return v + off;
+  return ex + off;
 }
 
 // The element of the descending order at which a cumulative quantity
@@ -186,20 +188,30 @@ __device__ uint32_t select_desc(int n, KeyFn key_of, const double* weights, doub
     target = sh.bcast_d[0];
     __syncthreads();
   }
-  // Elements with the final key, in index order.
-  double base = 0.0;
-  for (int c = 0; c < n; c += NT) {
-    const int i = c + threadIdx.x;
-    double v = 0.0;
-    if (i < n && key_of(i) == prefix) v = weights ? weights[i] : 1.0;
-    const double incl = block_scan<double>(v, sh.wave_d) + base;
-    const bool hit = v != 0.0 && (weights ? (inclusive ? incl >= target : incl > target)
-                                          : incl >= target);
-    const uint32_t first = block_min_u(hit ? (uint32_t)i : 0xFFFFFFFFu, sh);
-    if (first != 0xFFFFFFFFu) return first;
-    base = block_sum_d(v, sh) + base;
+  // Elements with the final key, in index order: each thread sums its
+  // members over a contiguous run of the row, one block scan gives every run
+  // the total before it, and each thread walks its run again from there
+  // (two barriers, where 1024-element chunks of the row took three block
+  // reductions each).
+  const int run = (n + NT - 1) / NT;
+  const int i0 = min(n, (int)threadIdx.x * run), i1 = min(n, i0 + run);
+  double own = 0.0;
+  for (int i = i0; i < i1; ++i)
+    if (key_of(i) == prefix) own += weights ? weights[i] : 1.0;
+  double incl = block_scan_excl<double>(own, sh.wave_d);
+  uint32_t first = 0xFFFFFFFFu;
+  for (int i = i0; i < i1; ++i) {
+    if (key_of(i) != prefix) continue;
+    const double v = weights ? weights[i] : 1.0;
+    if (v == 0.0) continue;
+    incl += v;
+    if (weights ? (inclusive ? incl >= target : incl > target) : incl >= target) {
+      first = (uint32_t)i;
+      break;
+    }
   }
-  return (uint32_t)n;
+  first = block_min_u(first, sh);
+  return first == 0xFFFFFFFFu ? (uint32_t)n : first;
 }
 
 constexpr int KCAP = 1024;  // largest top_k of the candidate path
