@@ -11,10 +11,10 @@
 // On the general path nothing is sorted.  Every cut the reference makes
 // along the sorted order -- the k-th element, the top_p crossing, the
 // element where the walk stops -- is found by a radix select over 32-bit
-// order-preserving keys of the penalised logits: four 8-bit histogram
-// passes narrow the key, counting elements (top_k) or summing their f64
-// weights (top_p, the walk), and the
-// elements that share the final key are resolved in index order (the
+// order-preserving keys of the penalised logits: three histogram passes
+// (11, 11 and 10 bits) narrow the key, counting elements (top_k) or summing
+// their f64 weights (top_p, the walk), and the elements that share the
+// final key are resolved in index order (the
 // reference's unstable sort leaves that order unspecified; lower index first
 // is this implementation's choice).  The per-element weights live in a
 // scratch row; the repetition penalty is applied on the fly through a bitmap
@@ -52,9 +52,14 @@ namespace {
 constexpr int NT = AKH_SAMPLE_NT;  // threads per row (per part of a split row)
 constexpr int NW = NT / 64;     // waves per block
 
+// Radix digits of the order keys: 11, 11 and 10 bits (three passes).
+constexpr int kBins = 2048;
 struct SampleShared {
-  uint32_t hist_n[256];
-  double hist_w[256];
+  // One radix pass's bins: counts or f64 weight sums (a select uses one).
+  union {
+    uint32_t hist_n[kBins];
+    double hist_w[kBins];
+  };
   double wave_d[NW];
   uint32_t wave_u[NW];
   float wave_f[NW];
@@ -75,7 +80,7 @@ __device__ __forceinline__ float pen_logit(const float* row, int i, const uint32
   return l;
 }
 
-__device__ double block_sum_d(double v, SampleShared& sh) {
+__device__ __forceinline__ double block_sum_d(double v, SampleShared& sh) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   const int w = threadIdx.x >> 6;
   __syncthreads();
@@ -86,7 +91,7 @@ __device__ double block_sum_d(double v, SampleShared& sh) {
   return t;
 }
 
-__device__ uint32_t block_sum_u(uint32_t v, SampleShared& sh) {
+__device__ __forceinline__ uint32_t block_sum_u(uint32_t v, SampleShared& sh) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   const int w = threadIdx.x >> 6;
   __syncthreads();
@@ -97,7 +102,7 @@ __device__ uint32_t block_sum_u(uint32_t v, SampleShared& sh) {
   return t;
 }
 
-__device__ uint32_t block_min_u(uint32_t v, SampleShared& sh) {
+__device__ __forceinline__ uint32_t block_min_u(uint32_t v, SampleShared& sh) {
   for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor(v, o, 64));
   const int w = threadIdx.x >> 6;
   __syncthreads();
@@ -108,7 +113,7 @@ __device__ uint32_t block_min_u(uint32_t v, SampleShared& sh) {
   return t;
 }
 
-__device__ float block_max_f(float v, SampleShared& sh) {
+__device__ __forceinline__ float block_max_f(float v, SampleShared& sh) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   const int w = threadIdx.x >> 6;
   __syncthreads();
@@ -143,19 +148,22 @@ __device__ T block_scan_excl(T v, T* wave_tot) {
 // inclusive, > target otherwise).  Returns the index, or n if the total
 // never crosses.  `key_of(i)` gives element i's order key.
 template <typename KeyFn>
-__device__ uint32_t select_desc(int n, KeyFn key_of, const double* weights, double target,
-                                bool inclusive, SampleShared& sh) {
+__device__ __forceinline__ uint32_t select_desc(int n, KeyFn key_of, const double* weights,
+                                                double target, bool inclusive,
+                                                SampleShared& sh) {
   uint32_t prefix = 0, mask = 0;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = threadIdx.x; b < 256; b += NT) {
-      sh.hist_n[b] = 0;
-      sh.hist_w[b] = 0.0;
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : pass == 1 ? 10 : 0;
+    const int nb = pass < 2 ? kBins : kBins / 2;
+    for (int b = threadIdx.x; b < kBins; b += NT) {
+      if (weights) sh.hist_w[b] = 0.0;
+      else sh.hist_n[b] = 0u;
     }
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += NT) {
       const uint32_t k = key_of(i);
       if ((k & mask) == prefix) {
-        const int bin = (k >> shift) & 255;
+        const int bin = (k >> shift) & (nb - 1);
         if (weights) {
           const double w = weights[i];
           if (w != 0.0) atomicAdd(&sh.hist_w[bin], w);
@@ -165,26 +173,29 @@ __device__ uint32_t select_desc(int n, KeyFn key_of, const double* weights, doub
       }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      double acc = 0.0;
-      int sel = -1;
-      for (int b = 255; b >= 0; --b) {
-        const double v = weights ? sh.hist_w[b] : (double)sh.hist_n[b];
-        const double nxt = acc + v;
-        if (weights ? (inclusive ? nxt >= target : nxt > target) : nxt >= target) {
-          sel = b;
-          break;
-        }
-        acc = nxt;
-      }
-      sh.bcast_u[0] = (uint32_t)sel;
-      sh.bcast_d[0] = target - acc;
+    // The first bin in descending order whose cumulative total crosses
+    // target: thread t holds bins nb - 1 - 2t and nb - 2 - 2t, one block scan
+    // gives the total before them, and the lowest crossing thread wins.
+    const int t = threadIdx.x, b1 = nb - 1 - 2 * t, b0 = b1 - 1;
+    auto val = [&](int b) {
+      return b < 0 ? 0.0 : weights ? sh.hist_w[b] : (double)sh.hist_n[b];
+    };
+    const double v1 = val(b1), v0 = val(b0);
+    const double before = block_scan_excl<double>(v1 + v0, sh.wave_d);
+    auto crosses = [&](double nxt) {
+      return weights ? (inclusive ? nxt >= target : nxt > target) : nxt >= target;
+    };
+    const double n1 = before + v1;
+    const int mine = b1 < 0 ? -1 : crosses(n1) ? b1 : (b0 >= 0 && crosses(n1 + v0)) ? b0 : -1;
+    const uint32_t win = block_min_u(mine >= 0 ? (uint32_t)t : 0xFFFFFFFFu, sh);
+    if (win == 0xFFFFFFFFu) return (uint32_t)n;
+    if ((uint32_t)t == win) {
+      sh.bcast_u[0] = (uint32_t)mine;
+      sh.bcast_d[0] = target - (mine == b1 ? before : n1);
     }
     __syncthreads();
-    const int sel = (int)sh.bcast_u[0];
-    if (sel < 0) return (uint32_t)n;
-    prefix |= (uint32_t)sel << shift;
-    mask |= 0xFFu << shift;
+    prefix |= sh.bcast_u[0] << shift;
+    mask |= (uint32_t)(nb - 1) << shift;
     target = sh.bcast_d[0];
     __syncthreads();
   }
@@ -240,7 +251,7 @@ __device__ __forceinline__ float key_value(uint32_t k) {
 // holds its element's index), so an entry's place is the number of entries
 // above it: every thread counts for its own entries, reading the others as
 // LDS broadcasts, with no barrier in between.
-__device__ int rank_top(int nc, int K, TopKShared& tk) {
+__device__ __forceinline__ int rank_top(int nc, int K, TopKShared& tk) {
   for (int e = threadIdx.x; e < nc; e += NT) {
     const unsigned long long x = tk.comp[e];
     int above = 0;
@@ -258,8 +269,8 @@ __device__ int rank_top(int nc, int K, TopKShared& tk) {
 // divided out, and the walk r -= p.  The divisions, independent per element,
 // run in parallel; the folds and the walk, whose order fixes the bits, on one
 // thread.
-__device__ uint32_t tail_topk(uint32_t top_k, float temperature, float top_p, double r,
-                              TopKShared& tk) {
+__device__ __forceinline__ uint32_t tail_topk(uint32_t top_k, float temperature, float top_p,
+                                              double r, TopKShared& tk) {
   const int K = (int)top_k;
   const double mxd = (double)key_value((uint32_t)(tk.top[0] >> 32));
   for (int t = threadIdx.x; t < K; t += NT)
@@ -365,8 +376,8 @@ __device__ void reduce_counts(const uint32_t (&c)[NTH], uint32_t base, TopKShare
 // exponent is below 2j - 12), four packed 8-bit counters per chunk;
 // refinements compare only the elements inside the narrowed interval.
 template <typename LFn>
-__device__ int topk_candidates(int n, LFn l_of, uint32_t idx0, uint32_t top_k, bool all_finite,
-                               SampleShared& sh, TopKShared& tk) {
+__device__ __forceinline__ int topk_candidates(int n, LFn l_of, uint32_t idx0, uint32_t top_k,
+                                              bool all_finite, SampleShared& sh, TopKShared& tk) {
   float mxv = -INFINITY;
   uint32_t nan = 0;
   for_row(n, l_of, [&](float l, int, bool) {
