@@ -60,6 +60,9 @@ struct SampleShared {
     uint32_t hist_n[kBins];
     double hist_w[kBins];
   };
+  // The last pass's bins (kBins / 2): members of nonzero weight, lowest index.
+  uint32_t last_n[kBins / 2];
+  uint32_t last_i[kBins / 2];
   double wave_d[NW];
   uint32_t wave_u[NW];
   float wave_f[NW];
@@ -158,17 +161,25 @@ __device__ __forceinline__ uint32_t select_desc(int n, KeyFn key_of, const doubl
     for (int b = threadIdx.x; b < kBins; b += NT) {
       if (weights) sh.hist_w[b] = 0.0;
       else sh.hist_n[b] = 0u;
+      if (pass == 2 && b < kBins / 2) {
+        sh.last_n[b] = 0u;
+        sh.last_i[b] = 0xFFFFFFFFu;
+      }
     }
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += NT) {
       const uint32_t k = key_of(i);
       if ((k & mask) == prefix) {
         const int bin = (k >> shift) & (nb - 1);
+        const double w = weights ? weights[i] : 1.0;
         if (weights) {
-          const double w = weights[i];
           if (w != 0.0) atomicAdd(&sh.hist_w[bin], w);
         } else {
           atomicAdd(&sh.hist_n[bin], 1u);
+        }
+        if (pass == 2 && w != 0.0) {
+          atomicAdd(&sh.last_n[bin], 1u);
+          atomicMin(&sh.last_i[bin], (uint32_t)i);
         }
       }
     }
@@ -194,10 +205,16 @@ __device__ __forceinline__ uint32_t select_desc(int n, KeyFn key_of, const doubl
       sh.bcast_d[0] = target - (mine == b1 ? before : n1);
     }
     __syncthreads();
-    prefix |= sh.bcast_u[0] << shift;
+    const uint32_t sel = sh.bcast_u[0];
+    prefix |= sel << shift;
     mask |= (uint32_t)(nb - 1) << shift;
     target = sh.bcast_d[0];
+    // One member of nonzero weight with the final key (distinct logits):
+    // the crossing is in its bin, so it is the answer.
+    const bool only = pass == 2 && sh.last_n[sel] == 1u;
+    const uint32_t at = only ? sh.last_i[sel] : 0u;
     __syncthreads();
+    if (only) return at;
   }
   // Elements with the final key, in index order: each thread sums its
   // members over a contiguous run of the row, one block scan gives every run
