@@ -686,15 +686,19 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
       w[i] = e;
       part += e;
     }
+    // The reference divides every weight by their sum (sampling.rs:50-52),
+    // and by the kept sum after the top_p cut, before comparing cumulative
+    // sums with top_p and r.  The weights stay unnormalised here and those
+    // targets are scaled by the sums instead: the same comparisons up to
+    // rounding, without a pass over the row for each division.
     const double sum = block_sum_d(part, sh);
-    for (int i = threadIdx.x; i < n; i += NT) w[i] = w[i] / sum;
-    __syncthreads();
+    double total = sum;
 
     // top_p (sampling.rs:55-70): the smallest prefix reaching top_p, renormalised.
     uint32_t last = kth < (uint32_t)n ? kth : (uint32_t)n;  // last kept element, n = unknown
     if (a.top_p < 1.0f) {
       // No crossing keeps every element (and still renormalises).
-      const uint32_t cut = select_desc(n, key_of, w, (double)a.top_p, true, sh);
+      const uint32_t cut = select_desc(n, key_of, w, (double)a.top_p * sum, true, sh);
       const uint32_t ckey = cut < (uint32_t)n ? key_of((int)cut) : 0u;
       double kept = 0.0;
       for (int i = threadIdx.x; i < n; i += NT) {
@@ -704,15 +708,13 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
         }
         kept += w[i];
       }
-      const double s = block_sum_d(kept, sh);
-      for (int i = threadIdx.x; i < n; i += NT) w[i] = w[i] / s;
-      __syncthreads();
+      total = block_sum_d(kept, sh);
       if (cut < (uint32_t)n) last = cut;
     }
 
     // The walk (sampling.rs:72-80): first element whose cumulative
     // probability exceeds r; the last kept element if none does.
-    pick = select_desc(n, key_of, w, r, false, sh);
+    pick = select_desc(n, key_of, w, r * total, false, sh);
     if (pick >= (uint32_t)n) {
       if (last >= (uint32_t)n) {
         // Every element is kept: the last of the descending order is the
