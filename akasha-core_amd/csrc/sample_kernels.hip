@@ -656,7 +656,9 @@ __global__ __launch_bounds__(NT) void k_sample_rows(SampleArgs a) {
     // sampling.rs:30-32, 83-91: first index of the maximum.
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    for (int i = threadIdx.x; i < n; i += NT) amax_merge(bv, bi, pen_logit(row, i, bm, a.penalty), (uint32_t)i);
+    for_row(n, l_at, [&](float l, int i, bool live) {
+      if (live) amax_merge(bv, bi, l, (uint32_t)i);
+    });
     const float mx = block_max_f(bv, sh);
     pick = block_min_u(bv == mx ? bi : 0xFFFFFFFFu, sh);
     // The reference's scan starts from index 0 and a NaN there never loses
